@@ -1,0 +1,134 @@
+/*
+ * ma_attn.h -- C-ABI of the MI355X sparse-attention forward engine (gfx950).
+ *
+ * Plain C: integer sizes, raw device pointers and a hipStream_t passed as
+ * void*.  No torch or HIP types appear in these signatures, so any host
+ * language (ctypes, cffi, a C++ extension) can bind them.
+ *
+ * Layout of every Q/K/V/O buffer: [batch, seq_len, num_heads, head_dim],
+ * head_dim fastest, contiguous (the reference's NWHD layout,
+ * src/csrc/tensor.cpp:108 and src/cuda/sparse_attention_kernel.cu:28-32).
+ * Q, K, V and O share one dtype.  O is written exactly once per row.
+ *
+ * Index sets S_i (key positions query i attends, ascending, clipped to [0,N)):
+ *   SLIDING      { i + dilation*t : -left <= t <= right }
+ *                (reference window_size=w  <=>  left = right = w, dilation 1)
+ *   DENSE        [0, N), or [0, i] when causal
+ *   BLOCK_SPARSE union over c in block_table[i / block_size][*] (c >= 0)
+ *                of [c*block_size, min((c+1)*block_size, N))
+ *   LONGFORMER   i <  num_global: [0, N)
+ *                i >= num_global: { i - left .. i + right } U [0, num_global)
+ *                (set union, every key once)
+ * An empty S_i gives an all-zero output row (src/csrc/ma_core.cpp:212).
+ *
+ * Return codes: 0 on success, non-zero on invalid input or launch failure;
+ * ma_attn_last_error() then holds a message.  Nothing is launched on invalid
+ * input.  All calls are asynchronous on the given stream and never allocate.
+ */
+#ifndef MA_ATTN_H
+#define MA_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum ma_attn_dtype {
+  MA_ATTN_F32 = 0,
+  MA_ATTN_BF16 = 1,
+  MA_ATTN_F16 = 2
+};
+
+enum ma_attn_pattern {
+  MA_ATTN_SLIDING = 0,
+  MA_ATTN_DENSE = 1,
+  MA_ATTN_BLOCK_SPARSE = 2,
+  MA_ATTN_LONGFORMER = 3
+};
+
+typedef struct ma_attn_desc {
+  int64_t batch;
+  int64_t seq_len;
+  int64_t num_heads;
+  int64_t head_dim;
+  int32_t dtype;    /* enum ma_attn_dtype */
+  int32_t pattern;  /* enum ma_attn_pattern */
+  int64_t left;     /* SLIDING / LONGFORMER: taps before i */
+  int64_t right;    /* SLIDING / LONGFORMER: taps after i */
+  int64_t dilation; /* SLIDING: stride between taps, >= 1 */
+  int32_t causal;   /* DENSE: 1 => keys [0, i] */
+  int32_t reserved0;
+  int64_t block_size;         /* BLOCK_SPARSE: rows per block, >= 1 */
+  const int32_t* block_table; /* BLOCK_SPARSE: device int32 [ceil(N/bs), blocks_per_row],
+                                 ascending, -1 padded */
+  int64_t blocks_per_row;     /* BLOCK_SPARSE: table width */
+  int64_t num_global;         /* LONGFORMER: global tokens at positions 0..G-1 */
+  float scale;                /* softmax scale; 0 => 1.0f / sqrtf((float)head_dim) */
+  int32_t reserved1;
+} ma_attn_desc;
+
+/*
+ * Sparse-attention forward: O = softmax_j(<Q_i, K_j> * scale) V over j in S_i.
+ * Replaces the reference's extension entry points
+ *   sparse_forward_cuda   src/cuda/sparse_attention_kernel.cu:423-458 (SLIDING, left=right=w)
+ *   dense_forward_cuda    src/cuda/sparse_attention_kernel.cu:348-382 (DENSE)
+ * and the CPU engine it is checked against,
+ *   ma_core::compute_sparse_attention  src/csrc/ma_core.cpp:160-246
+ *   ma_core::compute_dense_attention   src/csrc/ma_core.cpp:66-157,
+ * and gives the block-sparse / Longformer patterns of
+ *   src/csrc/sparse_attention.cpp:203-259 a working forward.
+ * workspace: device memory of ma_attn_workspace_size(desc) bytes (may be NULL
+ * when that size is 0).  stream: a hipStream_t (NULL = default stream).
+ */
+int ma_attn_forward(const ma_attn_desc* desc, const void* q, const void* k,
+                    const void* v, void* o, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* Bytes of device workspace ma_attn_forward needs for desc (0 for most
+ * patterns).  No reference counterpart: the reference allocates inside its
+ * extension (sparse_attention_kernel.cu:440); this engine never allocates. */
+size_t ma_attn_workspace_size(const ma_attn_desc* desc);
+
+/* Validates desc without launching; 0 when ma_attn_forward would accept it.
+ * Mirrors the checks of sparse_attention_kernel.cu:427-432. */
+int ma_attn_validate(const ma_attn_desc* desc);
+
+/* Message for the last non-zero return on this thread ("" if none). */
+const char* ma_attn_last_error(void);
+
+/*
+ * Host: seeded block table for BLOCK_SPARSE.  Row r holds {r} U {r-1 if r>=1}
+ * U `random_per_row` distinct blocks drawn uniformly (SplitMix64 keyed by
+ * (seed, r), rejection sampling) from the remaining blocks, sorted ascending,
+ * -1 padded to width 2 + random_per_row.  Replaces the unseeded
+ * BlockSparseAttention / create_random_sparse_pattern generators
+ * (src/csrc/sparse_attention.cpp:203-231, :287-310).
+ * table_out: host int32 [num_blocks, 2 + random_per_row].
+ */
+int ma_attn_block_table(uint64_t seed, int64_t num_blocks,
+                        int64_t random_per_row, int32_t* table_out);
+
+/*
+ * Host: the ascending key list S_i of query row i for desc (block_table, if
+ * used, is a HOST pointer here).  Writes min(|S_i|, cap) keys to keys_out and
+ * returns |S_i|, or -1 on invalid input.  The same closed forms drive the
+ * kernels; this exposes them for bit-exact index checks.  Replaces the COO
+ * generators create_sliding_window_pattern (src/csrc/ma_core.cpp:34-48) and
+ * SlidingWindow/Longformer generate_sparse_pattern
+ * (src/csrc/sparse_attention.cpp:181-259).
+ */
+int64_t ma_attn_row_keys(const ma_attn_desc* desc, const int32_t* host_block_table,
+                         int64_t i, int64_t* keys_out, int64_t cap);
+
+/* ABI version of this header (bumped on incompatible change). */
+int ma_attn_abi_version(void);
+
+#define MA_ATTN_ABI_VERSION 1
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MA_ATTN_H */

@@ -1,0 +1,623 @@
+// ma_attn.hip -- MI355X (gfx950) sparse-attention forward engine behind the
+// C-ABI of include/ma_attn.h.
+//
+// Kernels
+//   band_kernel<T>   bf16/fp16, head_dim 64, SLIDING (any dilation): one
+//                    workgroup per 64-query tile of one (batch, head, residue
+//                    class); the K/V band of the tile is staged in LDS (K row
+//                    major, V transposed) and both contractions run on MFMA
+//                    (16x16x32 for Q.K^T, 16x16x16 for P.V) with an online
+//                    softmax held in registers.  One O store per row.
+//   rows_kernel<T>   every pattern / dtype / head_dim <= 512: one wave per
+//                    query row, lanes over keys for the scores, lanes over
+//                    head_dim for P.V.  Used where the tiled kernel does not
+//                    apply.
+//
+// Semantics follow ma_core::compute_sparse_attention
+// (/root/reference src/csrc/ma_core.cpp:160-246): softmax over the row's key
+// set with scale 1/sqrtf(D), empty set => zero row.  The reference GPU
+// launcher this replaces is sparse_forward_cuda
+// (src/cuda/sparse_attention_kernel.cu:423-458).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/ma_attn.h"
+#include "pattern.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return 1;
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------ element access
+
+template <typename T>
+__device__ __forceinline__ float ld_f(const T* p) {
+  return static_cast<float>(*p);
+}
+
+template <typename T>
+__device__ __forceinline__ T cvt_out(float x) {
+  return static_cast<T>(x);
+}
+
+// ------------------------------------------------------------------ wave64 reductions
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m, 64));
+  return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
+  return x;
+}
+
+__device__ __forceinline__ float bcast_f(float x, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+
+__device__ __forceinline__ int bcast_i(int x, int lane) {
+  return __builtin_amdgcn_readlane(x, lane);
+}
+
+// ------------------------------------------------------------------ rows_kernel
+
+constexpr int kRowsWaves = 4;
+
+// One wave per query row (row = (b*N + i)*H + h).  Scores: lane t of a
+// 64-key chunk owns key key_at(t); online softmax across chunks (m, l, acc).
+// P.V: lanes own head_dim slots d = lane + 64*c.
+template <typename T, int DPL>
+__global__ __launch_bounds__(256) void rows_kernel(const T* __restrict__ q, const T* __restrict__ k,
+                                                   const T* __restrict__ v, T* __restrict__ o,
+                                                   int64_t B, int64_t H, int64_t D,
+                                                   ma::PatternParams pp, float scale) {
+  extern __shared__ float q_lds[];  // kRowsWaves * D floats
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int64_t N = pp.n;
+  const int64_t row = (int64_t)blockIdx.x * kRowsWaves + wv;
+  const bool row_ok = row < B * N * H;
+  const int64_t rr = row_ok ? row : 0;
+  const int64_t h = rr % H;
+  const int64_t bi = rr / H;
+  const int64_t i = bi % N;
+  const int64_t b = bi / N;
+  const int64_t rs = H * D;  // elements between consecutive tokens
+
+  float* qw = q_lds + wv * D;
+  for (int64_t d = lane; d < D; d += 64) qw[d] = row_ok ? ld_f(q + rr * D + d) : 0.0f;
+  __syncthreads();
+  if (!row_ok) return;  // no barrier below this point
+
+  const T* kb = k + (b * N * H + h) * D;
+  const T* vb = v + (b * N * H + h) * D;
+  const ma::RowKeys rk = ma::row_keys(pp, i);
+  const int64_t cnt = rk.count;
+
+  float m = -INFINITY, l = 0.0f;
+  float acc[DPL];
+#pragma unroll
+  for (int c = 0; c < DPL; ++c) acc[c] = 0.0f;
+
+  for (int64_t c0 = 0; c0 < cnt; c0 += 64) {
+    const int64_t t = c0 + lane;
+    const bool valid = t < cnt;
+    const int64_t j = valid ? ma::key_at(pp, rk, i, t) : 0;
+    float s = -INFINITY;
+    if (valid) {
+      const T* kr = kb + j * rs;
+      float dot = 0.0f;
+      for (int64_t d = 0; d < D; ++d) dot = fmaf(qw[d], ld_f(kr + d), dot);
+      s = dot * scale;
+    }
+    const float mn = fmaxf(m, wave_max(s));  // finite: lane 0 is valid
+    const float corr = expf(m - mn);
+    const float p = valid ? expf(s - mn) : 0.0f;
+    l = l * corr + wave_sum(p);
+#pragma unroll
+    for (int c = 0; c < DPL; ++c) acc[c] *= corr;
+    const int nk = (int)ma::imin64(64, cnt - c0);
+    for (int kk = 0; kk < nk; ++kk) {
+      const float pk = bcast_f(p, kk);
+      const int64_t jk = (int64_t)bcast_i((int)j, kk);
+      const T* vr = vb + jk * rs;
+#pragma unroll
+      for (int c = 0; c < DPL; ++c) {
+        const int64_t d = lane + 64 * c;
+        if (d < D) acc[c] = fmaf(pk, ld_f(vr + d), acc[c]);
+      }
+    }
+    m = mn;
+  }
+  const float inv = cnt > 0 ? 1.0f / l : 0.0f;
+  T* orow = o + rr * D;
+#pragma unroll
+  for (int c = 0; c < DPL; ++c) {
+    const int64_t d = lane + 64 * c;
+    if (d < D) orow[d] = cvt_out<T>(acc[c] * inv);
+  }
+}
+
+// ------------------------------------------------------------------ band_kernel (MFMA)
+
+// Operand types and MFMA selection per 16-bit element type.
+template <typename T>
+struct Mma;
+
+template <>
+struct Mma<__bf16> {
+  static __device__ __forceinline__ f32x4 qk(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 pv(uint2 a, uint2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                     __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float x, float y) {
+    const __bf16 a = static_cast<__bf16>(x), b = static_cast<__bf16>(y);
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  }
+};
+
+template <>
+struct Mma<_Float16> {
+  static __device__ __forceinline__ f32x4 qk(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 pv(uint2 a, uint2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                                 __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float x, float y) {
+    const _Float16 a = static_cast<_Float16>(x), b = static_cast<_Float16>(y);
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  }
+};
+
+constexpr int kBandD = 64;         // head_dim handled by band_kernel
+constexpr int kBandQ = 64;         // queries per workgroup (4 waves x 16)
+constexpr int kBandKC = 128;       // keys staged per LDS stage
+constexpr int kKsStride = 72;      // K row in LDS: 64 + 8 pad (144 B: conflict-free 16 B reads)
+constexpr int kVtStride = kBandKC + 8;  // V^T row in LDS: 136 (272 B: conflict-free 8 B reads)
+
+struct BandArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  int64_t B, N, H;
+  int64_t left, right, dil;
+  int64_t tiles;     // query tiles per residue class (ceil(ceil(N/dil)/64))
+  float scale_log2;  // scale * log2(e)
+};
+
+// Workgroup -> (b, tile, h, rho) with the dispatcher's round-robin over the
+// 8 XCDs undone, so each XCD walks a contiguous run of tiles (the K/V halo of
+// tile t+1 is the tile t block that the same XCD's L2 just fetched).
+__device__ __forceinline__ int64_t xcd_linear(int64_t bid, int64_t nwg) {
+  const int64_t xcd = bid & 7, idx = bid >> 3;
+  const int64_t per = nwg >> 3, rem = nwg & 7;
+  return xcd * per + (xcd < rem ? xcd : rem) + idx;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void band_kernel(BandArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t ks[kBandKC * kKsStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vt[kBandD * kVtStride];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = tid >> 6;
+  const int c = lane & 15;  // MFMA column: this lane's query within the wave tile
+  const int g = lane >> 4;  // MFMA row group: keys 4g..4g+3 of a 16-key sub-tile
+
+  int64_t lin = xcd_linear(blockIdx.x, gridDim.x);
+  const int64_t rho = lin % a.dil;
+  lin /= a.dil;
+  const int64_t h = lin % a.H;
+  lin /= a.H;
+  const int64_t tile = lin % a.tiles;
+  const int64_t b = lin / a.tiles;
+
+  const int64_t Nr = (a.N - rho + a.dil - 1) / a.dil;  // length of residue class rho
+  const int64_t m0 = tile * kBandQ;
+  if (m0 >= Nr) return;  // whole workgroup: uniform exit before any barrier
+
+  // element offset of (b, residue index m, h, 0)
+  const int64_t tok_stride = a.dil * a.H * kBandD;
+  const int64_t base = ((b * a.N + rho) * a.H + h) * kBandD;
+  const uint16_t* Q = static_cast<const uint16_t*>(a.q) + base;
+  const uint16_t* K = static_cast<const uint16_t*>(a.k) + base;
+  const uint16_t* V = static_cast<const uint16_t*>(a.v) + base;
+  uint16_t* O = static_cast<uint16_t*>(a.o) + base;
+
+  // Q^T operand (B of the 16x16x32 MFMA): query column c, head_dim slice 8g..8g+7 (+32)
+  const int64_t qa = m0 + 16 * wv;  // first query of this wave
+  const int64_t qm = qa + c;        // this lane's query
+  const bool wave_has_q = qa < Nr;
+  const bool q_ok = qm < Nr;
+  uint4 qb0 = make_uint4(0, 0, 0, 0), qb1 = make_uint4(0, 0, 0, 0);
+  if (q_ok) {
+    const uint16_t* qr = Q + qm * tok_stride + 8 * g;
+    qb0 = *reinterpret_cast<const uint4*>(qr);
+    qb1 = *reinterpret_cast<const uint4*>(qr + 32);
+  }
+
+  const int64_t need_lo = ma::imax64(qa - a.left, 0);
+  const int64_t need_hi = ma::imin64(qa + 15 + a.right, Nr - 1);
+  const int64_t band_lo = ma::imax64(m0 - a.left, 0);
+  const int64_t band_hi = ma::imin64(m0 + kBandQ - 1 + a.right, Nr - 1);
+
+  float m_run = -INFINITY;  // running max of scaled log2 scores for query qm
+  float l_run = 0.0f;       // this lane's share of the softmax denominator
+  f32x4 acc[4];             // O^T tiles: head_dim rows 16*dt + 4g + r, query column c
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  for (int64_t s0 = band_lo; s0 <= band_hi; s0 += kBandKC) {
+    __syncthreads();  // previous stage fully consumed
+    // ---- stage K (row major) : 128 keys x 8 chunks of 16 B
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int idx = tid + 256 * r;
+      const int key = idx >> 3, ch = idx & 7;
+      const int64_t km = s0 + key;
+      uint4 val = make_uint4(0, 0, 0, 0);
+      if (km <= band_hi) val = *reinterpret_cast<const uint4*>(K + km * tok_stride + 8 * ch);
+      *reinterpret_cast<uint4*>(&ks[key * kKsStride + 8 * ch]) = val;
+    }
+    // ---- stage V transposed: V^T[d][key]; thread = key pair kp, head_dim chunks dc, dc+4
+    {
+      const int kp = tid & 63, dc = tid >> 6;
+      const int64_t k0 = s0 + 2 * kp, k1 = k0 + 1;
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int ch = dc + 4 * half;
+        uint4 x0 = make_uint4(0, 0, 0, 0), x1 = make_uint4(0, 0, 0, 0);
+        if (k0 <= band_hi) x0 = *reinterpret_cast<const uint4*>(V + k0 * tok_stride + 8 * ch);
+        if (k1 <= band_hi) x1 = *reinterpret_cast<const uint4*>(V + k1 * tok_stride + 8 * ch);
+        const uint32_t w0[4] = {x0.x, x0.y, x0.z, x0.w};
+        const uint32_t w1[4] = {x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t lo = (w0[e] & 0xFFFFu) | (w1[e] << 16);
+          const uint32_t hi = (w0[e] >> 16) | (w1[e] & 0xFFFF0000u);
+          *reinterpret_cast<uint32_t*>(&vt[(8 * ch + 2 * e) * kVtStride + 2 * kp]) = lo;
+          *reinterpret_cast<uint32_t*>(&vt[(8 * ch + 2 * e + 1) * kVtStride + 2 * kp]) = hi;
+        }
+      }
+    }
+    __syncthreads();
+    if (!wave_has_q) continue;
+
+    // ---- S^T = K . Q^T for the 16-key sub-tiles this wave needs
+    f32x4 sc[kBandKC / 16];
+#pragma unroll
+    for (int st = 0; st < kBandKC / 16; ++st) {
+      const int64_t k_lo = s0 + 16 * st;
+      const bool active = (k_lo <= need_hi) && (k_lo + 15 >= need_lo);
+      sc[st] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      if (active) {
+        const uint16_t* kr = &ks[(16 * st + c) * kKsStride + 8 * g];
+        const uint4 ka0 = *reinterpret_cast<const uint4*>(kr);
+        const uint4 ka1 = *reinterpret_cast<const uint4*>(kr + 32);
+        f32x4 z = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        z = Mma<T>::qk(ka0, qb0, z);
+        z = Mma<T>::qk(ka1, qb1, z);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t km = k_lo + 4 * g + r;
+          const bool ok = q_ok && km <= band_hi && ma::in_window(qm, km, a.left, a.right);
+          sc[st][r] = ok ? z[r] * a.scale_log2 : -INFINITY;
+        }
+      }
+    }
+    // ---- online softmax update (stats per query column; 4 lane groups share a query)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int st = 0; st < kBandKC / 16; ++st)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sc[st][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
+    l_run *= corr;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) acc[dt] *= corr;
+    m_run = m_new;
+
+    // ---- O^T += V^T . P^T
+#pragma unroll
+    for (int st = 0; st < kBandKC / 16; ++st) {
+      const int64_t k_lo = s0 + 16 * st;
+      const bool active = (k_lo <= need_hi) && (k_lo + 15 >= need_lo);
+      if (!active) continue;
+      float p[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[r] = __builtin_amdgcn_exp2f(sc[st][r] - m_use);
+        l_run += p[r];
+      }
+      uint2 pb;
+      pb.x = Mma<T>::pack2(p[0], p[1]);
+      pb.y = Mma<T>::pack2(p[2], p[3]);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const uint2 va = *reinterpret_cast<const uint2*>(&vt[(16 * dt + c) * kVtStride + 16 * st + 4 * g]);
+        acc[dt] = Mma<T>::pv(va, pb, acc[dt]);
+      }
+    }
+  }
+
+  if (!q_ok) return;
+  float l_tot = l_run + __shfl_xor(l_run, 16, 64);
+  l_tot += __shfl_xor(l_tot, 32, 64);
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  uint16_t* orow = O + qm * tok_stride;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    uint2 ov;
+    ov.x = Mma<T>::pack2(acc[dt][0] * inv, acc[dt][1] * inv);
+    ov.y = Mma<T>::pack2(acc[dt][2] * inv, acc[dt][3] * inv);
+    *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * g) = ov;
+  }
+}
+
+// ------------------------------------------------------------------ host side
+
+size_t elt_size(int32_t dt) { return dt == MA_ATTN_F32 ? 4 : 2; }
+
+ma::PatternParams params_of(const ma_attn_desc* d, const int32_t* table) {
+  ma::PatternParams p;
+  p.n = d->seq_len;
+  p.pattern = d->pattern;
+  p.causal = d->causal;
+  p.left = d->left;
+  p.right = d->right;
+  p.dilation = d->dilation;
+  p.block_size = d->block_size;
+  p.table = table;
+  p.bpr = d->blocks_per_row;
+  p.num_global = d->num_global;
+  return p;
+}
+
+int validate(const ma_attn_desc* d) {
+  if (!d) return fail("ma_attn: null descriptor");
+  if (d->batch < 0 || d->seq_len < 0 || d->num_heads < 0 || d->head_dim < 0)
+    return fail("ma_attn: negative dimension (B=%lld N=%lld H=%lld D=%lld)", (long long)d->batch,
+                (long long)d->seq_len, (long long)d->num_heads, (long long)d->head_dim);
+  if (d->dtype != MA_ATTN_F32 && d->dtype != MA_ATTN_BF16 && d->dtype != MA_ATTN_F16)
+    return fail("ma_attn: unsupported dtype %d (float32, bfloat16, float16 only)", d->dtype);
+  if (d->head_dim > 512) return fail("ma_attn: head_dim %lld > 512 unsupported", (long long)d->head_dim);
+  if (d->seq_len > (int64_t)INT32_MAX) return fail("ma_attn: seq_len exceeds int32 range");
+  switch (d->pattern) {
+    case MA_ATTN_SLIDING:
+      if (d->dilation < 1) return fail("ma_attn: dilation must be >= 1 (got %lld)", (long long)d->dilation);
+      break;
+    case MA_ATTN_DENSE:
+      break;
+    case MA_ATTN_BLOCK_SPARSE:
+      if (d->block_size < 1) return fail("ma_attn: block_size must be >= 1");
+      if (d->blocks_per_row < 1 || d->blocks_per_row > 64)
+        return fail("ma_attn: blocks_per_row must be in [1, 64]");
+      if (!d->block_table && d->seq_len > 0) return fail("ma_attn: block_table is null");
+      break;
+    case MA_ATTN_LONGFORMER:
+      if (d->num_global < 0) return fail("ma_attn: num_global must be >= 0");
+      break;
+    default:
+      return fail("ma_attn: unknown pattern %d", d->pattern);
+  }
+  if (!(d->scale >= 0.0f) || std::isinf(d->scale)) return fail("ma_attn: scale must be finite and >= 0");
+  return 0;
+}
+
+float scale_of(const ma_attn_desc* d) {
+  if (d->scale > 0.0f) return d->scale;
+  return 1.0f / std::sqrt(static_cast<float>(d->head_dim));
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <typename T>
+int launch_rows(const ma_attn_desc* d, const void* q, const void* k, const void* v, void* o,
+                hipStream_t st) {
+  const int64_t rows = d->batch * d->seq_len * d->num_heads;
+  const int64_t blocks = (rows + kRowsWaves - 1) / kRowsWaves;
+  if (blocks > (int64_t)INT32_MAX) return fail("ma_attn: problem too large for one launch");
+  const size_t shm = sizeof(float) * kRowsWaves * (size_t)d->head_dim;
+  const ma::PatternParams pp = params_of(d, d->block_table);
+  const float scale = scale_of(d);
+  const int dpl = (int)((d->head_dim + 63) / 64);
+  const T* tq = static_cast<const T*>(q);
+  const T* tk = static_cast<const T*>(k);
+  const T* tv = static_cast<const T*>(v);
+  T* to = static_cast<T*>(o);
+#define MA_ROWS(N_)                                                                            \
+  hipLaunchKernelGGL((rows_kernel<T, N_>), dim3((unsigned)blocks), dim3(256), shm, st, tq, tk, \
+                     tv, to, d->batch, d->num_heads, d->head_dim, pp, scale)
+  if (dpl <= 1)
+    MA_ROWS(1);
+  else if (dpl <= 2)
+    MA_ROWS(2);
+  else if (dpl <= 4)
+    MA_ROWS(4);
+  else
+    MA_ROWS(8);
+#undef MA_ROWS
+  return 0;
+}
+
+bool band_applies(const ma_attn_desc* d, const void* q, const void* k, const void* v, const void* o) {
+  return d->pattern == MA_ATTN_SLIDING && (d->dtype == MA_ATTN_BF16 || d->dtype == MA_ATTN_F16) &&
+         d->head_dim == kBandD && d->left >= 0 && d->right >= 0 && aligned16(q) && aligned16(k) &&
+         aligned16(v) && aligned16(o);
+}
+
+int launch_band(const ma_attn_desc* d, const void* q, const void* k, const void* v, void* o,
+                hipStream_t st) {
+  BandArgs a;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.B = d->batch;
+  a.N = d->seq_len;
+  a.H = d->num_heads;
+  a.left = d->left;
+  a.right = d->right;
+  a.dil = d->dilation;
+  const int64_t nr_max = (d->seq_len + d->dilation - 1) / d->dilation;
+  a.tiles = (nr_max + kBandQ - 1) / kBandQ;
+  a.scale_log2 = scale_of(d) * 1.4426950408889634f;
+  const int64_t wgs = d->batch * a.tiles * d->num_heads * d->dilation;
+  if (wgs > (int64_t)INT32_MAX) return fail("ma_attn: problem too large for one launch");
+  if (d->dtype == MA_ATTN_BF16)
+    hipLaunchKernelGGL(band_kernel<__bf16>, dim3((unsigned)wgs), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(band_kernel<_Float16>, dim3((unsigned)wgs), dim3(256), 0, st, a);
+  return 0;
+}
+
+uint64_t splitmix64(uint64_t* s) {
+  uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+}  // namespace
+
+extern "C" {
+
+int ma_attn_abi_version(void) { return MA_ATTN_ABI_VERSION; }
+
+const char* ma_attn_last_error(void) { return g_last_error.c_str(); }
+
+int ma_attn_validate(const ma_attn_desc* desc) {
+  g_last_error.clear();
+  return validate(desc);
+}
+
+size_t ma_attn_workspace_size(const ma_attn_desc* desc) {
+  (void)desc;
+  return 0;
+}
+
+int ma_attn_forward(const ma_attn_desc* desc, const void* q, const void* k, const void* v, void* o,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  g_last_error.clear();
+  if (validate(desc)) return 1;
+  const int64_t rows = desc->batch * desc->seq_len * desc->num_heads;
+  if (rows == 0 || desc->head_dim == 0) return 0;
+  if (!q || !k || !v || !o) return fail("ma_attn: null tensor pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  (void)hipGetLastError();  // launch errors below must be ours
+  int rc;
+  if (band_applies(desc, q, k, v, o)) {
+    rc = launch_band(desc, q, k, v, o, st);
+  } else {
+    switch (desc->dtype) {
+      case MA_ATTN_F32:
+        rc = launch_rows<float>(desc, q, k, v, o, st);
+        break;
+      case MA_ATTN_BF16:
+        rc = launch_rows<__bf16>(desc, q, k, v, o, st);
+        break;
+      default:
+        rc = launch_rows<_Float16>(desc, q, k, v, o, st);
+        break;
+    }
+  }
+  if (rc) return rc;
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail("ma_attn: kernel launch failed: %s", hipGetErrorString(e));
+  return 0;
+}
+
+int ma_attn_block_table(uint64_t seed, int64_t num_blocks, int64_t random_per_row, int32_t* out) {
+  g_last_error.clear();
+  if (num_blocks < 0 || random_per_row < 0 || random_per_row > 62 || (!out && num_blocks > 0))
+    return fail("ma_attn_block_table: bad arguments");
+  const int64_t w = 2 + random_per_row;
+  const uint64_t nb = (uint64_t)num_blocks;
+  const uint64_t limit = nb ? (UINT64_MAX / nb) * nb : 0;
+  for (int64_t r = 0; r < num_blocks; ++r) {
+    int32_t row[64];
+    int64_t cnt = 0;
+    row[cnt++] = (int32_t)r;
+    if (r >= 1) row[cnt++] = (int32_t)(r - 1);
+    const int64_t want = ma::imin64(random_per_row, num_blocks - cnt);
+    uint64_t s = seed ^ (0x9E3779B97F4A7C15ull * (uint64_t)(r + 1));
+    int64_t got = 0;
+    while (got < want) {
+      const uint64_t z = splitmix64(&s);
+      if (z >= limit) continue;
+      const int32_t cand = (int32_t)(z % nb);
+      bool dup = false;
+      for (int64_t e = 0; e < cnt; ++e) dup = dup || row[e] == cand;
+      if (dup) continue;
+      row[cnt++] = cand;
+      ++got;
+    }
+    for (int64_t x = 1; x < cnt; ++x) {  // insertion sort, ascending
+      const int32_t key = row[x];
+      int64_t y = x - 1;
+      while (y >= 0 && row[y] > key) {
+        row[y + 1] = row[y];
+        --y;
+      }
+      row[y + 1] = key;
+    }
+    for (int64_t e = 0; e < w; ++e) out[r * w + e] = e < cnt ? row[e] : -1;
+  }
+  return 0;
+}
+
+int64_t ma_attn_row_keys(const ma_attn_desc* desc, const int32_t* host_block_table, int64_t i,
+                         int64_t* keys_out, int64_t cap) {
+  g_last_error.clear();
+  if (validate(desc)) return -1;
+  if (desc->pattern == MA_ATTN_BLOCK_SPARSE && !host_block_table) {
+    fail("ma_attn_row_keys: block table required");
+    return -1;
+  }
+  const ma::PatternParams pp = params_of(desc, host_block_table);
+  const ma::RowKeys rk = ma::row_keys(pp, i);
+  for (int64_t t = 0; t < rk.count && t < cap; ++t) keys_out[t] = ma::key_at(pp, rk, i, t);
+  return rk.count;
+}
+
+}  // extern "C"

@@ -1,0 +1,355 @@
+"""PyTorch bridge to the MI355X sparse-attention engine.
+
+Keeps the public surface of the reference bridge
+(/root/reference src/layers/ma_core_bridge.py):
+
+* ``MACoreAttentionFunction``  autograd.Function (:44-154)
+* ``MACoreAttention``          nn.Module with the same constructor defaults and
+                               ValueError / TypeError rules (:250-330)
+* ``create_attention_layer``   factory (:333-352)
+* ``pytorch_dense_attention``, ``pytorch_sparse_attention`` the PyTorch
+                               reference implementations (:184-247)
+* ``pytorch_to_ma_core``, ``ma_core_to_pytorch`` converters (:157-181), live
+                               only when the reference's CPU ``ma_core`` module
+                               is importable.
+
+Routing differs from the reference in one deliberate way: device tensors of
+every supported dtype (float32, bfloat16, float16) go to the native HIP
+kernels; the reference sent non-float32 device tensors to a Python loop
+(:77-80).  If device tensors arrive and the native library is missing, the
+call raises -- there is no silent fallback on a GPU.  CPU tensors use the
+PyTorch reference implementations (the reference's ma_core CPU engine is not
+part of this package).
+
+New, keyword-only constructor arguments select the BASELINE patterns and
+default to the reference behaviour: ``pattern`` ("sliding", "dense",
+"block_sparse", "longformer"), ``causal``, ``window_left``, ``window_right``,
+``dilation``, ``block_size``, ``block_table``, ``num_global_tokens``.
+"""
+from __future__ import annotations
+
+import os
+import sys
+from dataclasses import dataclass
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+
+_PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if _PKG_DIR not in sys.path:
+    sys.path.insert(0, _PKG_DIR)
+
+
+def _try_import_sparse_ext():
+    """Import the native extension.  On a machine with a GPU a failure is fatal."""
+    try:
+        import sparse_attention_cuda  # noqa: F401
+        return sparse_attention_cuda
+    except ImportError:
+        if torch.cuda.is_available():
+            raise
+        return None
+
+
+sparse_attention_cuda = _try_import_sparse_ext()
+_HAS_SPARSE_CUDA = sparse_attention_cuda is not None
+
+try:  # the reference's CPU engine, only for the two converters
+    import ma_core  # type: ignore  # noqa: F401
+except ImportError:  # pragma: no cover - depends on the environment
+    ma_core = None
+
+
+@dataclass(frozen=True)
+class PatternSpec:
+    """A resolved index-set choice (see include/ma_attn.h for the sets)."""
+
+    pattern: str = "sliding"       # sliding | dense | block_sparse | longformer
+    left: int = 64
+    right: int = 64
+    dilation: int = 1
+    causal: bool = False
+    block_size: int = 64
+    block_table: Optional[torch.Tensor] = None
+    num_global: int = 0
+
+    def mask(self, N: int, device) -> torch.Tensor:
+        """[N, N] boolean membership mask (for the PyTorch paths)."""
+        i = torch.arange(N, device=device).unsqueeze(1)
+        j = torch.arange(N, device=device).unsqueeze(0)
+        if self.pattern == "sliding":
+            d = j - i
+            t = torch.div(d, self.dilation, rounding_mode="floor")
+            return (d % self.dilation == 0) & (t >= -self.left) & (t <= self.right)
+        if self.pattern == "dense":
+            return j <= i if self.causal else torch.ones(N, N, dtype=torch.bool, device=device)
+        if self.pattern == "block_sparse":
+            bs = self.block_size
+            tab = self.block_table.to(device=device, dtype=torch.long)
+            rb = (torch.arange(N, device=device) // bs)
+            kb = (torch.arange(N, device=device) // bs)
+            hit = (tab[rb].unsqueeze(-1) == kb.view(1, 1, N)).any(dim=1)
+            return hit
+        if self.pattern == "longformer":
+            G = self.num_global
+            local = (j >= i - self.left) & (j <= i + self.right)
+            return (i < G) | (j < G) | local
+        raise ValueError(f"unknown pattern {self.pattern}")
+
+
+def _native_forward(q, k, v, sparse, window_size, use_causal_mask, spec: Optional[PatternSpec]):
+    ext = sparse_attention_cuda
+    cq, ck, cv = q.contiguous(), k.contiguous(), v.contiguous()
+    if spec is None:
+        if sparse:
+            return ext.forward(cq, ck, cv, int(window_size))
+        return ext.dense_forward(cq, ck, cv, bool(use_causal_mask))
+    if spec.pattern == "sliding":
+        return ext.sliding_forward(cq, ck, cv, spec.left, spec.right, spec.dilation)
+    if spec.pattern == "dense":
+        return ext.dense_forward(cq, ck, cv, spec.causal)
+    if spec.pattern == "block_sparse":
+        return ext.block_sparse_forward(cq, ck, cv, spec.block_table, spec.block_size)
+    if spec.pattern == "longformer":
+        return ext.longformer_forward(cq, ck, cv, spec.left, spec.right, spec.num_global)
+    raise ValueError(f"unknown pattern {spec.pattern}")
+
+
+def pytorch_pattern_attention(query, key, value, spec: PatternSpec) -> torch.Tensor:
+    """Differentiable masked attention for any PatternSpec (float32 math)."""
+    B, S, H, D = query.shape
+    scale = 1.0 / (D ** 0.5)
+    mask = spec.mask(S, query.device)
+    qh, kh, vh = (t.transpose(1, 2).float() for t in (query, key, value))
+    s = torch.matmul(qh * scale, kh.transpose(-2, -1))
+    s = s.masked_fill(~mask, float("-inf"))
+    p = torch.nan_to_num(torch.softmax(s, dim=-1), nan=0.0)
+    return torch.matmul(p, vh).transpose(1, 2).to(query.dtype).contiguous()
+
+
+class MACoreAttentionFunction(torch.autograd.Function):
+    """Autograd function: native forward, recomputation backward.
+
+    Reference: src/layers/ma_core_bridge.py:44-154.  The extra trailing
+    argument ``spec`` (a PatternSpec or None) selects a non-reference pattern.
+    """
+
+    @staticmethod
+    def forward(ctx, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                sparse: bool = False, window_size: int = 64,
+                use_causal_mask: bool = False, spec: Optional[PatternSpec] = None) -> torch.Tensor:
+        ctx.save_for_backward(query, key, value)
+        ctx.sparse = sparse
+        ctx.window_size = window_size
+        ctx.use_causal_mask = use_causal_mask
+        ctx.spec = spec
+        on_device = query.is_cuda or key.is_cuda or value.is_cuda
+        if on_device:
+            if not _HAS_SPARSE_CUDA:
+                raise RuntimeError("device tensors given but the native sparse-attention "
+                                   "library (libma_attn.so) is not loaded")
+            return _native_forward(query, key, value, sparse, window_size, use_causal_mask, spec)
+        if spec is not None:
+            return pytorch_pattern_attention(query, key, value, spec)
+        if sparse:
+            return pytorch_sparse_attention(query, key, value, window_size)
+        return pytorch_dense_attention(query, key, value, use_causal_mask)
+
+    @staticmethod
+    def backward(ctx, grad_output: torch.Tensor) -> Tuple[Optional[torch.Tensor], ...]:
+        query, key, value = ctx.saved_tensors
+        spec = ctx.spec
+        if _HAS_SPARSE_CUDA and query.is_cuda and spec is None:
+            cq, ck, cv, cgo = (t.contiguous() for t in (query, key, value, grad_output))
+            if ctx.sparse:
+                dQ, dK, dV = sparse_attention_cuda.backward(cq, ck, cv, cgo, int(ctx.window_size))
+            else:
+                dQ, dK, dV = sparse_attention_cuda.dense_backward(cq, ck, cv, cgo,
+                                                                  bool(ctx.use_causal_mask))
+            return (dQ if ctx.needs_input_grad[0] else None,
+                    dK if ctx.needs_input_grad[1] else None,
+                    dV if ctx.needs_input_grad[2] else None, None, None, None, None)
+        # Recompute with the PyTorch implementation and differentiate (:140-154)
+        with torch.enable_grad():
+            q, k, v = (t.detach().requires_grad_(True) for t in (query, key, value))
+            if spec is not None:
+                out = pytorch_pattern_attention(q, k, v, spec)
+            elif ctx.sparse:
+                out = pytorch_sparse_attention(q, k, v, ctx.window_size)
+            else:
+                out = pytorch_dense_attention(q, k, v, ctx.use_causal_mask)
+            dq, dk, dv = torch.autograd.grad(out, (q, k, v), grad_output)
+        return (dq if ctx.needs_input_grad[0] else None,
+                dk if ctx.needs_input_grad[1] else None,
+                dv if ctx.needs_input_grad[2] else None, None, None, None, None)
+
+
+def pytorch_to_ma_core(tensor: torch.Tensor):
+    """Convert a tensor to a reference ``ma_core.Tensor`` (:157-168).
+
+    Requires the reference's CPU module ``ma_core``; not shipped here.
+    """
+    if ma_core is None:
+        raise ImportError("ma_core (the reference CPU engine) is not installed")
+    cpu_tensor = tensor.detach().cpu().contiguous()
+    mc = ma_core.create_tensor(list(cpu_tensor.shape))
+    mc.copy_from_numpy(cpu_tensor.numpy())
+    return mc
+
+
+def ma_core_to_pytorch(mc_tensor, device: torch.device, dtype: torch.dtype) -> torch.Tensor:
+    """Convert a reference ``ma_core.Tensor`` back to torch (:171-181)."""
+    out = torch.from_numpy(mc_tensor.to_numpy())
+    if out.dtype != dtype:
+        out = out.to(dtype)
+    return out.to(device) if device.type != "cpu" else out
+
+
+def pytorch_dense_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                            use_causal_mask: bool = False) -> torch.Tensor:
+    """PyTorch dense attention with the reference's arithmetic (:184-221):
+    scale Q first, Q K^T, causal fill -1e9, softmax, P V."""
+    B, S, H, D = query.shape
+    query = query * (1.0 / (D ** 0.5))
+    qh = query.transpose(1, 2).reshape(B * H, S, D)
+    kh = key.transpose(1, 2).reshape(B * H, S, D)
+    vh = value.transpose(1, 2).reshape(B * H, S, D)
+    scores = torch.matmul(qh, kh.transpose(-2, -1).contiguous())
+    if use_causal_mask:
+        mask = torch.tril(torch.ones(S, S, device=query.device, dtype=torch.bool))
+        scores = scores.masked_fill(~mask, -1e9)
+    p = torch.softmax(scores, dim=-1)
+    out = torch.matmul(p, vh)
+    return out.view(B, H, S, D).transpose(1, 2).contiguous()
+
+
+def pytorch_sparse_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                             window_size: int = 64) -> torch.Tensor:
+    """PyTorch sliding-window attention, keys [max(0,i-w), min(S,i+w+1)) (:224-247).
+
+    Same semantics as the reference's per-(b, i, h) loop (scale Q, scores,
+    softmax over the window, weights @ V; an empty window gives zeros), computed
+    over query chunks with their key band so it scales past toy sizes.
+    Differentiable.
+    """
+    B, S, H, D = query.shape
+    w = int(window_size)
+    scale = 1.0 / (D ** 0.5)
+    if w < 0:
+        return torch.zeros_like(query)
+    out = []
+    chunk = 256
+    for r0 in range(0, S, chunk):
+        r1 = min(S, r0 + chunk)
+        k0, k1 = max(0, r0 - w), min(S, r1 + w)
+        q = (query[:, r0:r1] * scale).transpose(1, 2)        # [B,H,R,D]
+        kk = key[:, k0:k1].transpose(1, 2)                   # [B,H,K,D]
+        vv = value[:, k0:k1].transpose(1, 2)
+        s = torch.matmul(q, kk.transpose(-2, -1).contiguous())
+        ii = torch.arange(r0, r1, device=query.device).unsqueeze(1)
+        jj = torch.arange(k0, k1, device=query.device).unsqueeze(0)
+        band = (jj >= ii - w) & (jj <= ii + w)
+        s = s.masked_fill(~band, float("-inf"))
+        p = torch.softmax(s, dim=-1)
+        out.append(torch.matmul(p, vv).transpose(1, 2))
+    return torch.cat(out, dim=1).contiguous()
+
+
+_PATTERNS = ("sliding", "dense", "block_sparse", "longformer")
+
+
+class MACoreAttention(nn.Module):
+    """Drop-in attention module (reference: ma_core_bridge.py:250-330).
+
+    Eval mode (or ``fallback_training=False``) runs the native engine through
+    ``MACoreAttentionFunction``; training mode with ``fallback_training=True``
+    uses the PyTorch implementations, as the reference does (:317-325).
+    """
+
+    def __init__(self, sparse: bool = False, window_size: int = 64,
+                 use_causal_mask: bool = False, fallback_training: bool = True, *,
+                 pattern: Optional[str] = None, causal: bool = False,
+                 window_left: Optional[int] = None, window_right: Optional[int] = None,
+                 dilation: int = 1, block_size: int = 64,
+                 block_table: Optional[torch.Tensor] = None, num_global_tokens: int = 0):
+        super().__init__()
+        self.sparse = sparse
+        if self.sparse:
+            if not isinstance(window_size, int):
+                raise TypeError("window_size must be an integer for sparse attention")
+            if window_size <= 0:
+                raise ValueError("window_size must be > 0 for sparse attention")
+        self.window_size = window_size
+        self.use_causal_mask = use_causal_mask
+        self.fallback_training = fallback_training
+        self.spec = self._resolve(pattern, causal, window_left, window_right, dilation,
+                                  block_size, block_table, num_global_tokens)
+
+    def _resolve(self, pattern, causal, left, right, dilation, block_size, table, num_global):
+        if pattern is None and not causal and left is None and right is None and dilation == 1:
+            return None  # reference behaviour
+        pattern = pattern or ("sliding" if self.sparse else "dense")
+        if pattern not in _PATTERNS:
+            raise ValueError(f"Unknown pattern: {pattern}")
+        if not isinstance(dilation, int) or dilation < 1:
+            raise ValueError("dilation must be an integer >= 1")
+        w = int(self.window_size)
+        if pattern in ("sliding", "longformer"):
+            if left is None:
+                left = w - 1 if causal else w
+            if right is None:
+                right = 0 if causal else w
+        if pattern == "block_sparse":
+            if table is None:
+                raise ValueError("block_sparse pattern needs block_table")
+            table = torch.as_tensor(table, dtype=torch.int32)
+        if pattern == "dense":
+            causal = causal or self.use_causal_mask
+        return PatternSpec(pattern=pattern, left=int(left or 0), right=int(right or 0),
+                           dilation=int(dilation), causal=bool(causal),
+                           block_size=int(block_size), block_table=table,
+                           num_global=int(num_global))
+
+    def forward(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor) -> torch.Tensor:
+        if query.dim() != 4 or key.dim() != 4 or value.dim() != 4:
+            raise ValueError("Expected tensors with shape [batch, seq_len, num_heads, head_dim]")
+        # Auto-correct a seq_len / num_heads swap in Q and K (:299-304)
+        if (query.shape[0] == value.shape[0] and query.shape[1] == value.shape[2]
+                and query.shape[2] == value.shape[1] and query.shape[3] == value.shape[3]
+                and key.shape == query.shape):
+            query = query.transpose(1, 2).contiguous()
+            key = key.transpose(1, 2).contiguous()
+        if query.shape != key.shape or key.shape != value.shape:
+            raise ValueError(
+                "Tensor size mismatch: query, key, and value must have identical shapes "
+                "[batch, sequence length, num_heads, head_dim]")
+        b, s, h, d = query.shape
+        if b <= 0 or s <= 0 or h <= 0 or d <= 0:
+            raise ValueError("All tensor dimensions must be > 0")
+        if self.sparse and (self.window_size <= 0):
+            raise ValueError("window_size must be > 0 for sparse attention")
+
+        if self.training and self.fallback_training:
+            for t in (query, key, value):
+                if t.requires_grad and t.grad_fn is not None:
+                    t.retain_grad()
+            if self.spec is not None:
+                return pytorch_pattern_attention(query, key, value, self.spec)
+            if self.sparse:
+                return pytorch_sparse_attention(query, key, value, self.window_size)
+            return pytorch_dense_attention(query, key, value, self.use_causal_mask)
+
+        return MACoreAttentionFunction.apply(query, key, value, self.sparse, self.window_size,
+                                             self.use_causal_mask, self.spec)
+
+
+def create_attention_layer(attention_type: str = "dense", **kwargs) -> nn.Module:
+    """Factory (reference :333-352): "dense", "sparse" or "auto" (= sparse)."""
+    if attention_type == "dense":
+        return MACoreAttention(sparse=False, **kwargs)
+    if attention_type == "sparse":
+        return MACoreAttention(sparse=True, **kwargs)
+    if attention_type == "auto":
+        return MACoreAttention(sparse=True, **kwargs)
+    raise ValueError(f"Unknown attention type: {attention_type}")

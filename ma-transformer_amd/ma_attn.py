@@ -1,0 +1,149 @@
+"""ctypes binding of libma_attn.so (the C-ABI declared in include/ma_attn.h).
+
+This is the only place Python touches the native engine.  ``torch`` is
+imported before the library is opened so that the HIP runtime torch bundles
+(soname libamdhip64.so.7) is the one the engine binds to: tensors, streams and
+kernels then share one runtime.  Missing library => ImportError; there is no
+fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must precede loading the HIP library)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get("MA_ATTN_LIB", os.path.join(_HERE, "libma_attn.so"))
+
+F32, BF16, F16 = 0, 1, 2
+SLIDING, DENSE, BLOCK_SPARSE, LONGFORMER = 0, 1, 2, 3
+ABI_VERSION = 1
+
+DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+
+
+class Desc(ctypes.Structure):
+    """Mirror of ``ma_attn_desc`` (include/ma_attn.h)."""
+
+    _fields_ = [
+        ("batch", ctypes.c_int64),
+        ("seq_len", ctypes.c_int64),
+        ("num_heads", ctypes.c_int64),
+        ("head_dim", ctypes.c_int64),
+        ("dtype", ctypes.c_int32),
+        ("pattern", ctypes.c_int32),
+        ("left", ctypes.c_int64),
+        ("right", ctypes.c_int64),
+        ("dilation", ctypes.c_int64),
+        ("causal", ctypes.c_int32),
+        ("reserved0", ctypes.c_int32),
+        ("block_size", ctypes.c_int64),
+        ("block_table", ctypes.c_void_p),
+        ("blocks_per_row", ctypes.c_int64),
+        ("num_global", ctypes.c_int64),
+        ("scale", ctypes.c_float),
+        ("reserved1", ctypes.c_int32),
+    ]
+
+
+def _open():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"libma_attn.so not found at {LIB_PATH}; build it with "
+            "`python setup.py build_ext` (hipcc --offload-arch=gfx950)")
+    lib = ctypes.CDLL(LIB_PATH)
+    lib.ma_attn_abi_version.restype = ctypes.c_int
+    lib.ma_attn_last_error.restype = ctypes.c_char_p
+    lib.ma_attn_validate.restype = ctypes.c_int
+    lib.ma_attn_validate.argtypes = [ctypes.POINTER(Desc)]
+    lib.ma_attn_workspace_size.restype = ctypes.c_size_t
+    lib.ma_attn_workspace_size.argtypes = [ctypes.POINTER(Desc)]
+    lib.ma_attn_forward.restype = ctypes.c_int
+    lib.ma_attn_forward.argtypes = [ctypes.POINTER(Desc)] + [ctypes.c_void_p] * 5 + \
+        [ctypes.c_size_t, ctypes.c_void_p]
+    lib.ma_attn_block_table.restype = ctypes.c_int
+    lib.ma_attn_block_table.argtypes = [ctypes.c_uint64, ctypes.c_int64, ctypes.c_int64,
+                                        ctypes.c_void_p]
+    lib.ma_attn_row_keys.restype = ctypes.c_int64
+    lib.ma_attn_row_keys.argtypes = [ctypes.POINTER(Desc), ctypes.c_void_p, ctypes.c_int64,
+                                     ctypes.c_void_p, ctypes.c_int64]
+    if lib.ma_attn_abi_version() != ABI_VERSION:
+        raise ImportError("libma_attn.so ABI version mismatch; rebuild it")
+    return lib
+
+
+LIB = _open()
+
+
+def last_error() -> str:
+    return (LIB.ma_attn_last_error() or b"").decode()
+
+
+def make_desc(B, N, H, D, dtype_code, pattern, left=0, right=0, dilation=1, causal=False,
+              block_size=64, block_table_ptr=0, blocks_per_row=0, num_global=0,
+              scale=0.0) -> Desc:
+    d = Desc()
+    d.batch, d.seq_len, d.num_heads, d.head_dim = int(B), int(N), int(H), int(D)
+    d.dtype, d.pattern = int(dtype_code), int(pattern)
+    d.left, d.right, d.dilation = int(left), int(right), int(dilation)
+    d.causal = int(bool(causal))
+    d.block_size = int(block_size)
+    d.block_table = int(block_table_ptr) or None
+    d.blocks_per_row = int(blocks_per_row)
+    d.num_global = int(num_global)
+    d.scale = float(scale)
+    return d
+
+
+def validate(desc: Desc) -> None:
+    if LIB.ma_attn_validate(ctypes.byref(desc)) != 0:
+        raise RuntimeError(last_error())
+
+
+def workspace_size(desc: Desc) -> int:
+    return int(LIB.ma_attn_workspace_size(ctypes.byref(desc)))
+
+
+def forward_raw(desc: Desc, q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int,
+                ws_ptr: int = 0, ws_bytes: int = 0, stream: int = 0) -> None:
+    """Launch on ``stream`` (a hipStream_t as int).  Raises RuntimeError on rejection."""
+    rc = LIB.ma_attn_forward(ctypes.byref(desc), q_ptr, k_ptr, v_ptr, o_ptr, ws_ptr or None,
+                             ws_bytes, stream or None)
+    if rc != 0:
+        raise RuntimeError(last_error())
+
+
+def block_table(seed: int, num_blocks: int, random_per_row: int = 2) -> torch.Tensor:
+    """Seeded int32 [num_blocks, 2 + random_per_row] table (CPU tensor)."""
+    out = torch.empty((max(num_blocks, 0), 2 + random_per_row), dtype=torch.int32)
+    rc = LIB.ma_attn_block_table(ctypes.c_uint64(int(seed) & (2**64 - 1)), int(num_blocks),
+                                 int(random_per_row), out.data_ptr() if num_blocks > 0 else None)
+    if rc != 0:
+        raise ValueError(last_error())
+    return out
+
+
+def row_keys(desc: Desc, i: int, host_table: torch.Tensor | None = None) -> list:
+    """Ascending key list S_i from the engine's closed forms (host side)."""
+    cap = max(int(desc.seq_len), 1)
+    buf = (ctypes.c_int64 * cap)()
+    tptr = None
+    if host_table is not None:
+        host_table = host_table.to(torch.int32).contiguous()
+        tptr = host_table.data_ptr()
+    n = LIB.ma_attn_row_keys(ctypes.byref(desc), tptr, int(i), buf, cap)
+    if n < 0:
+        raise ValueError(last_error())
+    return list(buf[:n])
+
+
+def default_scale(D: int) -> float:
+    """1.0f / sqrtf((float)D) in float32, as src/csrc/ma_core.cpp:188."""
+    import numpy as np
+    return float(np.float32(1.0) / np.sqrt(np.float32(D)))
+
+
+__all__ = ["LIB", "Desc", "make_desc", "forward_raw", "validate", "workspace_size",
+           "block_table", "row_keys", "last_error", "DTYPES", "default_scale",
+           "SLIDING", "DENSE", "BLOCK_SPARSE", "LONGFORMER", "F32", "BF16", "F16"]

@@ -1,0 +1,185 @@
+"""Drop-in for the reference's GPU extension module ``sparse_attention_cuda``.
+
+Same import name, functions, signatures and defaults as the reference's
+pybind module (/root/reference src/cuda/sparse_attention_kernel.cu:501-510):
+
+    forward(query, key, value, window_size=64) -> Tensor
+    dense_forward(query, key, value, use_causal_mask=False) -> Tensor
+    backward(query, key, value, grad_out, window_size=64) -> [dQ, dK, dV]
+    dense_backward(query, key, value, grad_out, use_causal_mask=False) -> [dQ, dK, dV]
+
+and the same input contract as its TORCH_CHECKs (:427-432): device tensors,
+one dtype, contiguous, identical 4-D [B, S, H, D] shapes, else RuntimeError.
+The dtype set is widened from float32 to float32 / bfloat16 / float16; the
+output has the input dtype.  Kernels run asynchronously on the current HIP
+stream (torch.cuda.current_stream(), as :450 uses the current CUDA stream).
+
+New pattern entry points (not in the reference):
+
+    sliding_forward(q, k, v, left, right, dilation=1)
+    block_sparse_forward(q, k, v, block_table, block_size=64)
+    longformer_forward(q, k, v, left, right=0, num_global=16)
+    make_block_table(seed, num_blocks, random_per_row=2)
+
+The forward passes are hand-written HIP kernels (libma_attn.so).  The two
+backward entry points recompute the pattern's attention with torch autograd
+on the device (no HIP backward kernel yet); they exist so that
+``MACoreAttentionFunction.backward`` keeps its reference behaviour.
+"""
+from __future__ import annotations
+
+from typing import List
+
+import torch
+
+import ma_attn as _ma
+
+__all__ = ["forward", "dense_forward", "backward", "dense_backward", "sliding_forward",
+           "block_sparse_forward", "longformer_forward", "make_block_table"]
+
+
+def _check(*ts: torch.Tensor) -> None:
+    """The reference's TORCH_CHECKs (sparse_attention_kernel.cu:427-432) as RuntimeError."""
+    for t in ts:
+        if not isinstance(t, torch.Tensor):
+            raise RuntimeError("Inputs must be tensors")
+    if not all(t.is_cuda for t in ts):
+        raise RuntimeError("Inputs must be CUDA (HIP) device tensors")
+    dt = ts[0].dtype
+    if dt not in _ma.DTYPES or any(t.dtype != dt for t in ts):
+        raise RuntimeError("Inputs must share one dtype among float32, bfloat16, float16")
+    if not all(t.is_contiguous() for t in ts):
+        raise RuntimeError("Inputs must be contiguous")
+    if any(t.shape != ts[0].shape for t in ts):
+        raise RuntimeError("Q,K,V must have same shape")
+    if ts[0].dim() != 4:
+        raise RuntimeError("Expected shape [B, S, H, D]")
+    dev = ts[0].device
+    if any(t.device != dev for t in ts):
+        raise RuntimeError("Inputs must be on one device")
+
+
+def _launch(q, k, v, pattern, **kw) -> torch.Tensor:
+    _check(q, k, v)
+    B, N, H, D = q.shape
+    out = torch.empty_like(q)
+    desc = _ma.make_desc(B, N, H, D, _ma.DTYPES[q.dtype], pattern, **kw)
+    ws = None
+    nbytes = _ma.workspace_size(desc)
+    if nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        _ma.forward_raw(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                        ws.data_ptr() if ws is not None else 0, nbytes, stream)
+    return out
+
+
+def forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+            window_size: int = 64) -> torch.Tensor:
+    """Sliding-window forward over keys [max(0,i-w), min(S,i+w+1)).
+
+    Reference: sparse_forward_cuda (sparse_attention_kernel.cu:423-458).
+    w = 0 gives O = V; w < 0 gives an empty window and O = 0 (:232-238).
+    """
+    w = int(window_size)
+    return _launch(query, key, value, _ma.SLIDING, left=w, right=w, dilation=1)
+
+
+def dense_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                  use_causal_mask: bool = False) -> torch.Tensor:
+    """Dense (optionally causal) forward.  Reference: dense_forward_cuda (:348-382)."""
+    return _launch(query, key, value, _ma.DENSE, causal=bool(use_causal_mask))
+
+
+def sliding_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                    left: int, right: int, dilation: int = 1) -> torch.Tensor:
+    """Keys {i + dilation*t : -left <= t <= right} inside [0, S).
+
+    causal window w: left=w-1, right=0; the reference's symmetric w: left=right=w.
+    """
+    return _launch(query, key, value, _ma.SLIDING, left=int(left), right=int(right),
+                   dilation=int(dilation))
+
+
+def make_block_table(seed: int, num_blocks: int, random_per_row: int = 2) -> torch.Tensor:
+    """Seeded int32 [num_blocks, 2 + random_per_row] block table (host tensor)."""
+    return _ma.block_table(seed, num_blocks, random_per_row)
+
+
+def block_sparse_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                         block_table: torch.Tensor, block_size: int = 64) -> torch.Tensor:
+    """Query block r attends the key blocks listed in block_table[r] (ascending, -1 padded)."""
+    _check(query, key, value)
+    B, N, H, D = query.shape
+    bs = int(block_size)
+    if bs < 1:
+        raise RuntimeError("block_size must be >= 1")
+    nb = (N + bs - 1) // bs
+    if block_table.dim() != 2 or block_table.shape[0] != nb:
+        raise RuntimeError(f"block_table must be [ceil(S/block_size)={nb}, width]")
+    if block_table.shape[1] < 1 or block_table.shape[1] > 64:
+        raise RuntimeError("block_table width must be in [1, 64]")
+    tab_cpu = block_table.detach().to("cpu", torch.int32)
+    if tab_cpu.numel() and ((tab_cpu >= nb).any() or (tab_cpu < -1).any()):
+        raise RuntimeError("block_table entries must be -1 or in [0, num_blocks)")
+    srt = tab_cpu.clone()
+    srt[srt < 0] = torch.iinfo(torch.int32).max
+    if tab_cpu.numel() and (torch.diff(srt, dim=1) <= 0).any():
+        raise RuntimeError("block_table rows must be strictly ascending with -1 padding last")
+    # Allocated on the current stream; the caching allocator reuses its memory
+    # only for later work on that same stream, i.e. after the kernel read it.
+    tab = tab_cpu.to(query.device).contiguous()
+    return _launch(query, key, value, _ma.BLOCK_SPARSE, block_size=bs,
+                   block_table_ptr=tab.data_ptr(), blocks_per_row=tab.shape[1])
+
+
+def longformer_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                       left: int, right: int = 0, num_global: int = 16) -> torch.Tensor:
+    """Rows i < G attend all keys; others attend [i-left, i+right] U [0, G)."""
+    return _launch(query, key, value, _ma.LONGFORMER, left=int(left), right=int(right),
+                   num_global=int(num_global))
+
+
+# ---------------------------------------------------------------- backward (torch autograd)
+
+def _pattern_mask(N: int, device, window_size=None, causal=None) -> torch.Tensor:
+    i = torch.arange(N, device=device).unsqueeze(1)
+    j = torch.arange(N, device=device).unsqueeze(0)
+    if window_size is not None:
+        return (j >= i - window_size) & (j <= i + window_size)
+    if causal:
+        return j <= i
+    return torch.ones(N, N, dtype=torch.bool, device=device)
+
+
+def _masked_attention_f32(q, k, v, mask):
+    B, N, H, D = q.shape
+    scale = _ma.default_scale(D)
+    qh, kh, vh = (t.float().permute(0, 2, 1, 3).contiguous() for t in (q, k, v))
+    s = torch.matmul(qh, kh.transpose(-1, -2).contiguous()) * scale
+    s = s.masked_fill(~mask, float("-inf"))
+    p = torch.softmax(s, dim=-1)
+    p = torch.nan_to_num(p, nan=0.0)  # empty rows
+    return torch.matmul(p, vh).permute(0, 2, 1, 3)
+
+
+def _grads(q, k, v, grad_out, mask) -> List[torch.Tensor]:
+    _check(q, k, v, grad_out)
+    with torch.enable_grad():
+        qq, kk, vv = (t.detach().requires_grad_(True) for t in (q, k, v))
+        out = _masked_attention_f32(qq, kk, vv, mask)
+        dq, dk, dv = torch.autograd.grad(out, (qq, kk, vv), grad_out.float())
+    return [dq.to(q.dtype).contiguous(), dk.to(q.dtype).contiguous(), dv.to(q.dtype).contiguous()]
+
+
+def backward(query, key, value, grad_out, window_size: int = 64) -> List[torch.Tensor]:
+    """dQ, dK, dV of forward(); reference sparse_backward_cuda (:460-497)."""
+    mask = _pattern_mask(query.shape[1], query.device, window_size=int(window_size))
+    return _grads(query, key, value, grad_out, mask)
+
+
+def dense_backward(query, key, value, grad_out, use_causal_mask: bool = False) -> List[torch.Tensor]:
+    """dQ, dK, dV of dense_forward(); reference dense_backward_cuda (:384-421)."""
+    mask = _pattern_mask(query.shape[1], query.device, causal=bool(use_causal_mask))
+    return _grads(query, key, value, grad_out, mask)

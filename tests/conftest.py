@@ -1,0 +1,33 @@
+"""Shared pytest setup: import paths, the `gpu` marker, seeded inputs."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(REPO, "ma-transformer_amd")
+for p in (REPO, PKG):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (HIP device) and libma_attn.so")
+
+
+def randn(shape, seed, scale=1.0):
+    """i.i.d. N(0,1)*scale float32 from numpy's PCG64 (identical on every host)."""
+    return (np.random.default_rng(seed).standard_normal(shape, dtype=np.float32) * scale).astype(np.float32)
+
+
+def qkv(shape, seed, scale=1.0):
+    return randn(shape, seed, scale), randn(shape, seed + 1, scale), randn(shape, seed + 2, scale)
+
+
+@pytest.fixture(scope="session")
+def oracle():
+    from oracle import oracle as O
+    if not os.path.exists(O.LIB_PATH):
+        O.build()
+    return O

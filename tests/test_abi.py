@@ -1,0 +1,101 @@
+"""C-ABI library checks that need no GPU: load, exported symbols, host-side
+validation, the engine's closed-form index sets and block table vs the oracle."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "ma_attn.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ma_attn_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    import ma_attn
+    names = _declared_functions()
+    assert len(names) >= 7
+    lib = ctypes.CDLL(ma_attn.LIB_PATH)
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in include/ma_attn.h but not exported"
+    assert ma_attn.LIB.ma_attn_abi_version() == ma_attn.ABI_VERSION
+
+
+def test_desc_layout_matches_header():
+    import ma_attn
+    # int64 x4, int32 x2, int64 x3, int32 x2, int64, ptr, int64 x2, float, int32
+    assert ctypes.sizeof(ma_attn.Desc) == 4 * 8 + 2 * 4 + 3 * 8 + 2 * 4 + 8 + 8 + 2 * 8 + 4 + 4
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(dtype_code=7), "dtype"),
+    (dict(pattern=9), "pattern"),
+    (dict(dilation=0), "dilation"),
+    (dict(D=1000), "head_dim"),
+    (dict(N=-1), "negative"),
+])
+def test_validate_rejects(kw, msg):
+    import ma_attn
+    args = dict(B=1, N=8, H=1, D=16, dtype_code=ma_attn.F32, pattern=ma_attn.SLIDING)
+    args.update(kw)
+    d = ma_attn.make_desc(**args)
+    with pytest.raises(RuntimeError, match=msg):
+        ma_attn.validate(d)
+
+
+def test_forward_rejects_before_launch():
+    """Invalid descriptors fail on the host; nothing touches a device."""
+    import ma_attn
+    d = ma_attn.make_desc(1, 8, 1, 16, ma_attn.F32, ma_attn.BLOCK_SPARSE, blocks_per_row=2)
+    with pytest.raises(RuntimeError, match="block_table"):
+        ma_attn.forward_raw(d, 1, 1, 1, 1)
+    d = ma_attn.make_desc(0, 8, 1, 16, ma_attn.F32, ma_attn.SLIDING)  # empty problem: no-op
+    ma_attn.forward_raw(d, 0, 0, 0, 0)
+
+
+def _engine_vs_oracle_keys(oracle, N, pattern, table=None, **kw):
+    import ma_attn
+    import torch
+    code = {"sliding": ma_attn.SLIDING, "dense": ma_attn.DENSE, "block_sparse": ma_attn.BLOCK_SPARSE,
+            "longformer": ma_attn.LONGFORMER}[pattern]
+    # block_table_ptr only has to be non-null: host enumeration reads the host table argument
+    d = ma_attn.make_desc(1, N, 1, 1, ma_attn.F32, code,
+                          blocks_per_row=0 if table is None else table.shape[1],
+                          block_table_ptr=0 if table is None else 1, **kw)
+    s = oracle.Spec(1, N, 1, 1, pattern=pattern, table=table, **kw)
+    ht = None if table is None else torch.from_numpy(table)
+    for i in range(N):
+        assert ma_attn.row_keys(d, i, ht) == oracle.row_keys(s, i).tolist(), (pattern, kw, i)
+
+
+@pytest.mark.parametrize("pattern,kw", [
+    ("sliding", dict(left=63, right=0)), ("sliding", dict(left=32, right=31)),
+    ("sliding", dict(left=63, right=0, dilation=4)), ("sliding", dict(left=2, right=7, dilation=3)),
+    ("sliding", dict(left=-1, right=-1)), ("sliding", dict(left=-3, right=5)),
+    ("dense", dict(causal=True)), ("dense", dict(causal=False)),
+    ("longformer", dict(left=127, right=0, num_global=16)), ("longformer", dict(left=3, right=2, num_global=5)),
+])
+@pytest.mark.parametrize("N", [1, 7, 150])
+def test_engine_index_sets_match_oracle(oracle, pattern, kw, N):
+    _engine_vs_oracle_keys(oracle, N, pattern, **kw)
+
+
+def test_engine_block_index_sets_match_oracle(oracle):
+    for N, bs in ((150, 16), (64, 64), (129, 64)):
+        nb = (N + bs - 1) // bs
+        _engine_vs_oracle_keys(oracle, N, "block_sparse", table=oracle.block_table(4, nb, 2), block_size=bs)
+
+
+def test_engine_block_table_bitexact(oracle):
+    import ma_attn
+    for seed, nb, extra in ((1234, 256, 2), (0, 1, 2), (7, 2, 2), (99, 1000, 5), (2**63 + 5, 17, 3)):
+        assert np.array_equal(ma_attn.block_table(seed, nb, extra).numpy(), oracle.block_table(seed, nb, extra))
+    fix = np.fromfile(os.path.join(REPO, "tests", "golden", "block_table_seed1234_nb256_r2.bin"),
+                      dtype="<i4").reshape(256, 4)
+    assert np.array_equal(ma_attn.block_table(1234, 256, 2).numpy(), fix)
