@@ -392,6 +392,262 @@ __global__ __launch_bounds__(256) void band_kernel(BandArgs a) {
   }
 }
 
+// ------------------------------------------------------------------ stream_kernel (MFMA, K/V ring)
+//
+// Sliding windows (bf16/fp16, head_dim 64).  One workgroup streams a chunk of
+// consecutive 64-query tiles of one (batch, head, residue class).  K/V live
+// in an LDS ring of 64-key blocks (K row major, V transposed); tile t needs
+// blocks floor((64t-left)/64) .. floor((64t+63+right)/64), so moving to tile
+// t+1 needs exactly one new block.  While tile t computes, the next tile's Q
+// rows and its new K/V block are already in flight into registers; after the
+// tile, the block is written over the ring slot that no tile needs any more.
+// Every Q/K/V/O row crosses HBM once, except the ring warm-up at chunk start.
+//
+// Per wave: 16 queries (one MFMA column each) against the 16-key sub-tiles
+// that intersect their windows.  Index math is 32-bit (seq_len < 2^31 is
+// validated on the host); sub-tiles lying wholly inside every query's window
+// skip the per-element mask.
+
+constexpr int kBlk = 64;                        // keys per ring block
+constexpr int kSlotK = kBlk * kKsStride;        // K rows of a block (64 x 72)
+constexpr int kVtStrideBlk = kBlk + 8;          // V^T row of a block: 72 (144 B)
+constexpr int kSlotElems = kSlotK + kBandD * kVtStrideBlk;  // 9216 uint16 = 18 KB
+
+struct StreamArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  int64_t N, H;
+  int32_t left, right, dil;
+  int32_t tiles;   // query tiles of the longest residue class
+  int32_t chunk;   // tiles per workgroup
+  int32_t chunks;  // ceil(tiles / chunk)
+  float scale_log2;
+};
+
+// One 64-key block in flight: K as 2 x 16 B per thread, V as 2 keys x 16 B.
+struct BlockRegs {
+  uint4 k0, k1, v0, v1;
+};
+
+__device__ __forceinline__ uint4 ld16(const uint16_t* p, bool ok) {
+  return ok ? *reinterpret_cast<const uint4*>(p) : make_uint4(0, 0, 0, 0);
+}
+
+// K: thread -> keys (tid>>3) and (tid>>3)+32, 16 B column tid&7 (a wave
+// instruction reads 8 whole 128 B rows).  V: key pair tid&31, column tid>>5.
+__device__ __forceinline__ void load_block(BlockRegs& r, const uint16_t* K, const uint16_t* V,
+                                           int64_t tok_stride, int blk, int Nr, int tid) {
+  const int key0 = blk * kBlk;
+  const int ka = key0 + (tid >> 3), kb = ka + 32;
+  const int chk = tid & 7;
+  r.k0 = ld16(K + (int64_t)ka * tok_stride + 8 * chk, ka < Nr);
+  r.k1 = ld16(K + (int64_t)kb * tok_stride + 8 * chk, kb < Nr);
+  const int kp = tid & 31, chv = tid >> 5;
+  const int v0 = key0 + 2 * kp, v1 = v0 + 1;
+  r.v0 = ld16(V + (int64_t)v0 * tok_stride + 8 * chv, v0 < Nr);
+  r.v1 = ld16(V + (int64_t)v1 * tok_stride + 8 * chv, v1 < Nr);
+}
+
+// V^T words: (key 2kp, key 2kp+1) pairs for one head_dim row, built with v_perm.
+__device__ __forceinline__ void store_block(const BlockRegs& r, uint16_t* slot, int tid) {
+  uint16_t* ks = slot;
+  uint16_t* vt = slot + kSlotK;
+  const int chk = tid & 7;
+  *reinterpret_cast<uint4*>(&ks[(tid >> 3) * kKsStride + 8 * chk]) = r.k0;
+  *reinterpret_cast<uint4*>(&ks[((tid >> 3) + 32) * kKsStride + 8 * chk]) = r.k1;
+  const int kp = tid & 31, chv = tid >> 5;
+  const uint32_t w0[4] = {r.v0.x, r.v0.y, r.v0.z, r.v0.w};
+  const uint32_t w1[4] = {r.v1.x, r.v1.y, r.v1.z, r.v1.w};
+  uint32_t* col = reinterpret_cast<uint32_t*>(&vt[(8 * chv) * kVtStrideBlk + 2 * kp]);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    col[(2 * e) * (kVtStrideBlk / 2)] = __builtin_amdgcn_perm(w1[e], w0[e], 0x05040100u);
+    col[(2 * e + 1) * (kVtStrideBlk / 2)] = __builtin_amdgcn_perm(w1[e], w0[e], 0x07060302u);
+  }
+}
+
+__device__ __forceinline__ int floordiv32(int a, int d) {
+  const int q = a / d;
+  return (a % d != 0 && a < 0) ? q - 1 : q;
+}
+
+template <typename T, int NSLOT, int SG>
+__global__ __launch_bounds__(256, 4) void stream_kernel(StreamArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t ring[];  // NSLOT * kSlotElems
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = tid >> 6;
+  const int c = lane & 15;
+  const int g = lane >> 4;
+
+  int lin = blockIdx.x;
+  const int chunk_id = lin % a.chunks;
+  lin /= a.chunks;
+  const int rho = lin % a.dil;
+  lin /= a.dil;
+  const int h = lin % (int)a.H;
+  const int b = lin / (int)a.H;
+
+  const int Nr = (int)((a.N - rho + a.dil - 1) / a.dil);
+  const int tiles_r = (Nr + 63) >> 6;
+  const int t0 = chunk_id * a.chunk;
+  const int t1 = min(t0 + a.chunk, tiles_r);
+  if (t0 >= t1) return;  // uniform per workgroup, before any barrier
+  const int nblk = tiles_r;  // 64-key blocks of this residue class
+  const int L = a.left, R = a.right;
+
+  const int64_t tok_stride = (int64_t)a.dil * a.H * kBandD;
+  const int64_t base = (((int64_t)b * a.N + rho) * a.H + h) * kBandD;
+  const uint16_t* Q = static_cast<const uint16_t*>(a.q) + base;
+  const uint16_t* K = static_cast<const uint16_t*>(a.k) + base;
+  const uint16_t* V = static_cast<const uint16_t*>(a.v) + base;
+  uint16_t* O = static_cast<uint16_t*>(a.o) + base;
+
+  // ---- ring warm-up: blocks of tile t0
+  {
+    const int blo = max(floordiv32(t0 * kBlk - L, kBlk), 0);
+    const int bhi = min(floordiv32(t0 * kBlk + 63 + R, kBlk), nblk - 1);
+    BlockRegs pre[NSLOT];
+#pragma unroll
+    for (int s = 0; s < NSLOT; ++s)
+      if (blo + s <= bhi) load_block(pre[s], K, V, tok_stride, blo + s, Nr, tid);
+#pragma unroll
+    for (int s = 0; s < NSLOT; ++s)
+      if (blo + s <= bhi) store_block(pre[s], ring + ((blo + s) % NSLOT) * kSlotElems, tid);
+  }
+  uint4 qb0, qb1;
+  {
+    const int qm = t0 * 64 + 16 * wv + c;
+    const uint16_t* qr = Q + (int64_t)qm * tok_stride + 8 * g;
+    qb0 = ld16(qr, qm < Nr);
+    qb1 = ld16(qr + 32, qm < Nr);
+  }
+  __syncthreads();
+
+  // LDS byte offsets of this lane's operand reads inside a slot
+  const uint16_t* k_lane = ring + c * kKsStride + 8 * g;
+  const uint16_t* v_lane = ring + kSlotK + c * kVtStrideBlk + 4 * g;
+
+  for (int t = t0; t < t1; ++t) {
+    // ---- prefetch tile t+1: its new K/V block and its Q rows
+    const bool has_next = t + 1 < t1;
+    const int nb = floordiv32((t + 1) * kBlk + 63 + R, kBlk);
+    const bool load_nb = has_next && nb < nblk;
+    BlockRegs pf;
+    if (load_nb) load_block(pf, K, V, tok_stride, nb, Nr, tid);
+    uint4 qn0 = make_uint4(0, 0, 0, 0), qn1 = make_uint4(0, 0, 0, 0);
+    if (has_next) {
+      const int qm = (t + 1) * 64 + 16 * wv + c;
+      const uint16_t* qr = Q + (int64_t)qm * tok_stride + 8 * g;
+      qn0 = ld16(qr, qm < Nr);
+      qn1 = ld16(qr + 32, qm < Nr);
+    }
+
+    // ---- tile t: this wave's 16 queries qa..qa+15
+    const int qa = t * 64 + 16 * wv;
+    if (qa < Nr) {
+      const int qm = qa + c;
+      const bool rows_full = qa + 15 < Nr;
+      const int sub_lo = max(floordiv32(qa - L, 16), 0);
+      const int sub_hi = min(floordiv32(qa + 15 + R, 16), (Nr - 1) >> 4);
+      // key - query offset of accumulator element r of sub-tile s: 16s + r + d_lane
+      const int d_lane = 4 * g - c - qa;
+      const uint32_t span = (uint32_t)(L + R);
+      float m_run = -INFINITY, l_run = 0.0f;
+      f32x4 acc[4];
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int s0 = sub_lo; s0 <= sub_hi; s0 += SG) {
+        f32x4 sc[SG];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < SG; ++j) {
+          const int s = s0 + j;
+          sc[j] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+          if (s <= sub_hi) {
+            const int soff = ((s >> 2) % NSLOT) * kSlotElems + (s & 3) * 16 * kKsStride;
+            const uint4 ka0 = *reinterpret_cast<const uint4*>(k_lane + soff);
+            const uint4 ka1 = *reinterpret_cast<const uint4*>(k_lane + soff + 32);
+            f32x4 z = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            z = Mma<T>::qk(ka0, qb0, z);
+            z = Mma<T>::qk(ka1, qb1, z);
+            // wave-uniform: every (key, query) pair of the sub-tile inside the window?
+            const int dmin = 16 * s - qa - 15, dmax = 16 * s + 15 - qa;
+            const bool full = rows_full && dmin >= -L && dmax <= R && 16 * s + 15 < Nr;
+            if (!full) {
+              const int d0 = 16 * s + d_lane;
+              const bool q_ok = qm < Nr;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const bool ok = q_ok && (uint32_t)(d0 + r + L) <= span && 16 * s + 4 * g + r < Nr;
+                z[r] = ok ? z[r] : -INFINITY;
+              }
+            }
+            sc[j] = z;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, z[r]);
+          }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run, mx);
+        // scores are raw dot products; the softmax scale is folded into exp2's argument
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new * a.scale_log2;
+        if (m_run != m_new) {
+          const float corr = __builtin_amdgcn_exp2f(m_run * a.scale_log2 - m_use);
+          l_run *= corr;
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) acc[dt] *= corr;
+        }
+        m_run = m_new;
+#pragma unroll
+        for (int j = 0; j < SG; ++j) {
+          const int s = s0 + j;
+          if (s > sub_hi) continue;
+          float p[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            p[r] = __builtin_amdgcn_exp2f(fmaf(sc[j][r], a.scale_log2, -m_use));
+            l_run += p[r];
+          }
+          uint2 pb;
+          pb.x = Mma<T>::pack2(p[0], p[1]);
+          pb.y = Mma<T>::pack2(p[2], p[3]);
+          const int voff = ((s >> 2) % NSLOT) * kSlotElems + (s & 3) * 16;
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) {
+            const uint2 va = *reinterpret_cast<const uint2*>(v_lane + voff + 16 * dt * kVtStrideBlk);
+            acc[dt] = Mma<T>::pv(va, pb, acc[dt]);
+          }
+        }
+      }
+      float l_tot = l_run + __shfl_xor(l_run, 16, 64);
+      l_tot += __shfl_xor(l_tot, 32, 64);
+      const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+      if (qm < Nr) {
+        uint16_t* orow = O + (int64_t)qm * tok_stride + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          uint2 ov;
+          ov.x = Mma<T>::pack2(acc[dt][0] * inv, acc[dt][1] * inv);
+          ov.y = Mma<T>::pack2(acc[dt][2] * inv, acc[dt][3] * inv);
+          *reinterpret_cast<uint2*>(orow + 16 * dt) = ov;
+        }
+      }
+    }
+
+    // ---- rotate: the new block replaces the slot no later tile reads
+    __syncthreads();
+    if (load_nb) store_block(pf, ring + (nb % NSLOT) * kSlotElems, tid);
+    __syncthreads();
+    qb0 = qn0;
+    qb1 = qn1;
+  }
+}
+
 // ------------------------------------------------------------------ host side
 
 size_t elt_size(int32_t dt) { return dt == MA_ATTN_F32 ? 4 : 2; }
@@ -509,6 +765,84 @@ int launch_band(const ma_attn_desc* d, const void* q, const void* k, const void*
   return 0;
 }
 
+// Ring blocks a tile touches: floor((63+R)/64) - floor(-L/64) + 1.
+int64_t stream_slots(const ma_attn_desc* d) {
+  return ma::floordiv64(63 + d->right, kBlk) - ma::floordiv64(-d->left, kBlk) + 1;
+}
+
+constexpr int kMaxSlots = 6;  // 108 KB of LDS
+constexpr int kStreamSG = 5;  // sub-tiles per softmax group (a causal-64 wave tile needs 5)
+
+bool stream_applies(const ma_attn_desc* d, const void* q, const void* k, const void* v, const void* o) {
+  if (!band_applies(d, q, k, v, o)) return false;
+  if (d->left > (1 << 28) || d->right > (1 << 28)) return false;
+  const int64_t slots = stream_slots(d);
+  return slots >= 1 && slots <= kMaxSlots;
+}
+
+const char* kernel_override() {
+  const char* s = getenv("MA_ATTN_KERNEL");  // "stream" | "band" | "rows" (testing / A-B timing)
+  return s ? s : "";
+}
+
+template <typename T, int NSLOT>
+int launch_stream_t(const StreamArgs& a, int64_t wgs, hipStream_t st) {
+  const size_t shm = (size_t)NSLOT * kSlotElems * sizeof(uint16_t);
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&stream_kernel<T, NSLOT, kStreamSG>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess)
+      return fail("ma_attn: cannot reserve %zu B of LDS for the stream kernel", shm);
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((stream_kernel<T, NSLOT, kStreamSG>), dim3((unsigned)wgs), dim3(256), shm, st, a);
+  return 0;
+}
+
+template <typename T>
+int launch_stream_slots(const StreamArgs& a, int64_t slots, int64_t wgs, hipStream_t st) {
+  switch (slots) {
+    case 1: return launch_stream_t<T, 1>(a, wgs, st);
+    case 2: return launch_stream_t<T, 2>(a, wgs, st);
+    case 3: return launch_stream_t<T, 3>(a, wgs, st);
+    case 4: return launch_stream_t<T, 4>(a, wgs, st);
+    case 5: return launch_stream_t<T, 5>(a, wgs, st);
+    default: return launch_stream_t<T, 6>(a, wgs, st);
+  }
+}
+
+int launch_stream(const ma_attn_desc* d, const void* q, const void* k, const void* v, void* o,
+                  hipStream_t st) {
+  const int64_t slots = stream_slots(d);
+  const int64_t nr_max = (d->seq_len + d->dilation - 1) / d->dilation;
+  const int64_t tiles = (nr_max + 63) / 64;
+  const int64_t streams = d->batch * d->num_heads * d->dilation;
+  // Enough chunks to fill every CU with as many resident workgroups as LDS allows.
+  const int64_t per_cu = ma::imax64(1, ma::imin64(4, (160 * 1024) / (slots * kSlotElems * 2)));
+  const int64_t target = 256 * per_cu;
+  int64_t chunk = ma::imax64(1, (streams * tiles + target - 1) / target);
+  if (const char* e = getenv("MA_ATTN_STREAM_CHUNK")) chunk = ma::imax64(1, atoll(e));
+  const int64_t chunks = (tiles + chunk - 1) / chunk;
+  const int64_t wgs = streams * chunks;
+  if (wgs > (int64_t)INT32_MAX || tiles > (1 << 24)) return fail("ma_attn: problem too large for one launch");
+  StreamArgs a;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.N = d->seq_len;
+  a.H = d->num_heads;
+  a.left = (int32_t)d->left;
+  a.right = (int32_t)d->right;
+  a.dil = (int32_t)d->dilation;
+  a.tiles = (int32_t)tiles;
+  a.chunk = (int32_t)chunk;
+  a.chunks = (int32_t)chunks;
+  a.scale_log2 = scale_of(d) * 1.4426950408889634f;
+  if (d->dtype == MA_ATTN_BF16) return launch_stream_slots<__bf16>(a, slots, wgs, st);
+  return launch_stream_slots<_Float16>(a, slots, wgs, st);
+}
+
 uint64_t splitmix64(uint64_t* s) {
   uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
   z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -546,7 +880,12 @@ int ma_attn_forward(const ma_attn_desc* desc, const void* q, const void* k, cons
   hipStream_t st = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();  // launch errors below must be ours
   int rc;
-  if (band_applies(desc, q, k, v, o)) {
+  const char* force = kernel_override();
+  const bool want_rows = strcmp(force, "rows") == 0;
+  const bool want_band = strcmp(force, "band") == 0;
+  if (!want_rows && !want_band && stream_applies(desc, q, k, v, o)) {
+    rc = launch_stream(desc, q, k, v, o, st);
+  } else if (!want_rows && band_applies(desc, q, k, v, o)) {
     rc = launch_band(desc, q, k, v, o, st);
   } else {
     switch (desc->dtype) {
