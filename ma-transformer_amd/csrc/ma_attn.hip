@@ -403,15 +403,19 @@ __global__ __launch_bounds__(256) void band_kernel(BandArgs a) {
 // tile, the block is written over the ring slot that no tile needs any more.
 // Every Q/K/V/O row crosses HBM once, except the ring warm-up at chunk start.
 //
-// Per wave: 16 queries (one MFMA column each) against the 16-key sub-tiles
-// that intersect their windows.  Index math is 32-bit (seq_len < 2^31 is
-// validated on the host); sub-tiles lying wholly inside every query's window
-// skip the per-element mask.
+// All global traffic uses buffer instructions on a per-workgroup resource
+// whose range ends at the residue class's last row: rows past the end read as
+// zero and their stores are dropped by the hardware range check, so loads and
+// stores are issued unconditionally (exact memory counters, no exec-masked
+// branches) and the ragged last tile needs no separate path.  Per wave: 16
+// queries (one MFMA column each) against the 16-key sub-tiles that intersect
+// their windows; all control is wave-uniform (scalar).
 
 constexpr int kBlk = 64;                        // keys per ring block
 constexpr int kSlotK = kBlk * kKsStride;        // K rows of a block (64 x 72)
 constexpr int kVtStrideBlk = kBlk + 8;          // V^T row of a block: 72 (144 B)
 constexpr int kSlotElems = kSlotK + kBandD * kVtStrideBlk;  // 9216 uint16 = 18 KB
+constexpr uint32_t kRsrcWord3 = 0x00020000u;    // raw buffer, 32-bit dwords (gfx9 family)
 
 struct StreamArgs {
   const void* q;
@@ -420,34 +424,69 @@ struct StreamArgs {
   void* o;
   int64_t N, H;
   int32_t left, right, dil;
-  int32_t tiles;   // query tiles of the longest residue class
-  int32_t chunk;   // tiles per workgroup
-  int32_t chunks;  // ceil(tiles / chunk)
+  int32_t tiles;      // query tiles of the longest residue class
+  int32_t chunk;      // tiles per workgroup
+  int32_t chunks;     // ceil(tiles / chunk)
+  int32_t tok_bytes;  // bytes between consecutive rows of a residue class (dil * H * 128)
   float scale_log2;
 };
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, (int)kRsrcWord3);
+}
+
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+// Base offset for a load that must be issued (to keep the memory counters
+// exact) but whose data is not needed: every lane offset added to it stays
+// in [2^31, 2^32), past any buffer range, so the hardware returns zeros
+// without a memory access.
+constexpr uint32_t kOob = 0x80000000u;
+
+__device__ __forceinline__ void bstore8(__amdgpu_buffer_rsrc_t r, int off, uint2 x) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, x), r, off, 0, 0);
+}
+
+// Reductions over the 4 lanes {l, l^16, l^32, l^48} (the lane groups that
+// share one MFMA column) with the gfx950 row/half swaps: each swap returns a
+// lane's own value and its partner's, so op(pair) is the xor-exchange result.
+__device__ __forceinline__ float col_max(float x) {
+  const i32x2 p = __builtin_amdgcn_permlane16_swap(__float_as_int(x), __float_as_int(x), false, false);
+  x = fmaxf(__int_as_float(p[0]), __int_as_float(p[1]));
+  const i32x2 q = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return fmaxf(__int_as_float(q[0]), __int_as_float(q[1]));
+}
+
+__device__ __forceinline__ float col_sum(float x) {
+  const i32x2 p = __builtin_amdgcn_permlane16_swap(__float_as_int(x), __float_as_int(x), false, false);
+  x = __int_as_float(p[0]) + __int_as_float(p[1]);
+  const i32x2 q = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return __int_as_float(q[0]) + __int_as_float(q[1]);
+}
 
 // One 64-key block in flight: K as 2 x 16 B per thread, V as 2 keys x 16 B.
 struct BlockRegs {
   uint4 k0, k1, v0, v1;
 };
 
-__device__ __forceinline__ uint4 ld16(const uint16_t* p, bool ok) {
-  return ok ? *reinterpret_cast<const uint4*>(p) : make_uint4(0, 0, 0, 0);
-}
-
+// Per-lane byte offsets of the block loads, relative to the block's first row.
 // K: thread -> keys (tid>>3) and (tid>>3)+32, 16 B column tid&7 (a wave
 // instruction reads 8 whole 128 B rows).  V: key pair tid&31, column tid>>5.
-__device__ __forceinline__ void load_block(BlockRegs& r, const uint16_t* K, const uint16_t* V,
-                                           int64_t tok_stride, int blk, int Nr, int tid) {
-  const int key0 = blk * kBlk;
-  const int ka = key0 + (tid >> 3), kb = ka + 32;
-  const int chk = tid & 7;
-  r.k0 = ld16(K + (int64_t)ka * tok_stride + 8 * chk, ka < Nr);
-  r.k1 = ld16(K + (int64_t)kb * tok_stride + 8 * chk, kb < Nr);
-  const int kp = tid & 31, chv = tid >> 5;
-  const int v0 = key0 + 2 * kp, v1 = v0 + 1;
-  r.v0 = ld16(V + (int64_t)v0 * tok_stride + 8 * chv, v0 < Nr);
-  r.v1 = ld16(V + (int64_t)v1 * tok_stride + 8 * chv, v1 < Nr);
+struct BlockLane {
+  uint32_t k, v;
+};
+
+__device__ __forceinline__ void load_block(BlockRegs& r, __amdgpu_buffer_rsrc_t K, __amdgpu_buffer_rsrc_t V,
+                                           const BlockLane& bl, uint32_t row_off, int tok_bytes) {
+  r.k0 = bload16(K, bl.k + row_off);
+  r.k1 = bload16(K, bl.k + row_off + 32 * (uint32_t)tok_bytes);
+  r.v0 = bload16(V, bl.v + row_off);
+  r.v1 = bload16(V, bl.v + row_off + (uint32_t)tok_bytes);
 }
 
 // V^T words: (key 2kp, key 2kp+1) pairs for one head_dim row, built with v_perm.
@@ -473,13 +512,192 @@ __device__ __forceinline__ int floordiv32(int a, int d) {
   return (a % d != 0 && a < 0) ? q - 1 : q;
 }
 
+// Accumulator layout shared by both tile routines.  The P.V MFMA produces
+// O^T tiles dt = 0..3 of 16 head_dim rows; tile row m of tile dt is head_dim
+//   d(dt, m) = 32*(dt>>1) + 8*(m>>2) + 4*(dt&1) + (m&3),
+// so lane (query c, group g) ends up holding O[c][8g..8g+7] in acc[0..1] and
+// O[c][32+8g..32+8g+7] in acc[2..3]: two 16 B stores per lane.  The
+// permutation is applied by which V^T row each lane reads (v_row_of_lane).
+__device__ __forceinline__ int v_row_of_lane(int c) { return 8 * (c >> 2) + (c & 3); }
+__device__ __forceinline__ constexpr int v_row_of_tile(int dt) { return 32 * (dt >> 1) + 4 * (dt & 1); }
+
+// Normalise and store one wave's 16 O rows (rows past the end are dropped by
+// the buffer range check).
+template <typename T>
+__device__ __forceinline__ void store_o(const f32x4 (&acc)[4], float l_run, __amdgpu_buffer_rsrc_t Orsrc,
+                                        int o_off) {
+  const float l_tot = col_sum(l_run);
+  const float inv = l_tot > 0.0f ? __builtin_amdgcn_rcpf(l_tot) : 0.0f;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    const f32x4 a0 = acc[2 * half], a1 = acc[2 * half + 1];
+    uint4 ov;
+    ov.x = Mma<T>::pack2(a0[0] * inv, a0[1] * inv);
+    ov.y = Mma<T>::pack2(a0[2] * inv, a0[3] * inv);
+    ov.z = Mma<T>::pack2(a1[0] * inv, a1[1] * inv);
+    ov.w = Mma<T>::pack2(a1[2] * inv, a1[3] * inv);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, ov), Orsrc, o_off + 64 * half, 0, 0);
+  }
+}
+
+// One wave's 16 queries qa..qa+15 (qa wave-uniform) against the K/V ring,
+// any window (runtime left/right): scores on MFMA, softmax in registers
+// (online across groups of SG sub-tiles), P.V on MFMA, one O store per row.
+// Used for tiles at the sequence edges and for windows without a fixed-shape
+// instantiation.  Rows >= Nr compute on zero Q rows and their stores fall
+// outside the buffer range.
 template <typename T, int NSLOT, int SG>
+__device__ __forceinline__ void stream_tile(const uint16_t* k_lane, const uint16_t* v_lane, uint4 qb0,
+                                            uint4 qb1, int qa, int Nr, int L, int R, float sl2,
+                                            __amdgpu_buffer_rsrc_t Orsrc, int o_off, int g, int dl) {
+  const int sub_lo = max(floordiv32(qa - L, 16), 0);
+  const int sub_hi = min(floordiv32(qa + 15 + R, 16), (Nr - 1) >> 4);
+  const uint32_t span = (uint32_t)(L + R);
+  float m_run = -INFINITY, l_run = 0.0f;
+  f32x4 acc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = sub_lo; s0 <= sub_hi; s0 += SG) {
+    f32x4 sc[SG];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < SG; ++j) {
+      const int s = s0 + j;
+      if (s > sub_hi) break;
+      const int soff = ((s >> 2) % NSLOT) * kSlotElems + (s & 3) * 16 * kKsStride;
+      const uint4 ka0 = *reinterpret_cast<const uint4*>(k_lane + soff);
+      const uint4 ka1 = *reinterpret_cast<const uint4*>(k_lane + soff + 32);
+      f32x4 z = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      z = Mma<T>::qk(ka0, qb0, z);
+      z = Mma<T>::qk(ka1, qb1, z);
+      // key - query offsets of this sub-tile span [16s-qa-15, 16s-qa+15]
+      const int rel = 16 * s - qa;
+      if (rel - 15 < -L || rel + 15 > R) {
+        // element r: key - query + L = dl + rel + r, inside the window iff in [0, L+R]
+        const int x = dl + rel;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) z[r] = (uint32_t)(x + r) <= span ? z[r] : -INFINITY;
+      }
+      if (16 * s + 15 >= Nr) {
+        const int km = 16 * s + 4 * g;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) z[r] = km + r < Nr ? z[r] : -INFINITY;
+      }
+      sc[j] = z;
+      mx = fmaxf(mx, fmaxf(fmaxf(z[0], z[1]), fmaxf(z[2], z[3])));
+    }
+    const float m_new = fmaxf(m_run, col_max(mx));
+    // scores are raw dot products; the softmax scale is folded into exp2's argument
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new * sl2;
+    if (s0 != sub_lo) {  // rescale what earlier groups accumulated
+      const float corr = __builtin_amdgcn_exp2f(m_run * sl2 - m_use);
+      l_run *= corr;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) acc[dt] *= corr;
+    }
+    m_run = m_new;
+#pragma unroll
+    for (int j = 0; j < SG; ++j) {
+      const int s = s0 + j;
+      if (s > sub_hi) break;
+      float p[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[r] = __builtin_amdgcn_exp2f(fmaf(sc[j][r], sl2, -m_use));
+        l_run += p[r];
+      }
+      uint2 pb;
+      pb.x = Mma<T>::pack2(p[0], p[1]);
+      pb.y = Mma<T>::pack2(p[2], p[3]);
+      const int voff = ((s >> 2) % NSLOT) * kSlotElems + (s & 3) * 16;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const uint2 va = *reinterpret_cast<const uint2*>(v_lane + voff + v_row_of_tile(dt) * kVtStrideBlk);
+        acc[dt] = Mma<T>::pv(va, pb, acc[dt]);
+      }
+    }
+  }
+  store_o<T>(acc, l_run, Orsrc, o_off);
+}
+
+// Compile-time geometry of a fixed window [i-L, i+R] (dilation handled by
+// the residue-class split): a wave's 16 queries at qa = 16*(4t + wv) read
+// sub-tiles s = 4t + wv - CL + j, j < NSUB, whose key - query offsets
+// 16*(j-CL) + [-15, 15] are the same for every interior tile.
+template <int L, int R>
+struct WinGeom {
+  static constexpr int CL = (L + 15) / 16;
+  static constexpr int NSUB = (15 + R) / 16 + CL + 1;
+  static constexpr int NSLOT = (63 + R) / 64 + (L + 63) / 64 + 1;
+};
+
+// Interior tile of a fixed window: every sub-tile exists and lies before the
+// sequence end, so the whole tile is straight-line code (no branches): the
+// sub-tile count and which sub-tiles need a mask are compile-time, the
+// per-lane mask compares are loop-invariant, and the softmax is two-pass.
+template <typename T, int L, int R>
+__device__ __forceinline__ void window_tile(const uint16_t* k_lane, const uint16_t* v_lane, uint4 qb0,
+                                            uint4 qb1, int t, int wv, float sl2,
+                                            __amdgpu_buffer_rsrc_t Orsrc, int o_off, int dl) {
+  using G = WinGeom<L, R>;
+  f32x4 sc[G::NSUB];
+  int voff[G::NSUB];
+#pragma unroll
+  for (int j = 0; j < G::NSUB; ++j) {
+    const int u = wv + 3 * G::CL + j;  // s = 4(t - CL) + u, u >= 0
+    const int slot = (t - G::CL + (u >> 2)) % G::NSLOT;
+    const int soff = slot * kSlotElems + (u & 3) * 16 * kKsStride;
+    voff[j] = slot * kSlotElems + (u & 3) * 16;
+    const uint4 ka0 = *reinterpret_cast<const uint4*>(k_lane + soff);
+    const uint4 ka1 = *reinterpret_cast<const uint4*>(k_lane + soff + 32);
+    f32x4 z = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    z = Mma<T>::qk(ka0, qb0, z);
+    z = Mma<T>::qk(ka1, qb1, z);
+    const int rel = 16 * (j - G::CL);
+    if (rel - 15 < -L || rel + 15 > R) {  // resolved at compile time
+#pragma unroll
+      for (int r = 0; r < 4; ++r) z[r] = (uint32_t)(dl + rel + r) <= (uint32_t)(L + R) ? z[r] : -INFINITY;
+    }
+    sc[j] = z;
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < G::NSUB; ++j) mx = fmaxf(mx, fmaxf(fmaxf(sc[j][0], sc[j][1]), fmaxf(sc[j][2], sc[j][3])));
+  const float m_use = col_max(mx) * sl2;  // finite: every query sees its own key
+  float l_run = 0.0f;
+  f32x4 acc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < G::NSUB; ++j) {
+    float p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[r] = __builtin_amdgcn_exp2f(fmaf(sc[j][r], sl2, -m_use));
+      l_run += p[r];
+    }
+    uint2 pb;
+    pb.x = Mma<T>::pack2(p[0], p[1]);
+    pb.y = Mma<T>::pack2(p[2], p[3]);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const uint2 va = *reinterpret_cast<const uint2*>(v_lane + voff[j] + v_row_of_tile(dt) * kVtStrideBlk);
+      acc[dt] = Mma<T>::pv(va, pb, acc[dt]);
+    }
+  }
+  store_o<T>(acc, l_run, Orsrc, o_off);
+}
+
+// FL/FR >= 0: the kernel is specialised for window [i-FL, i+FR] (interior
+// tiles take window_tile); FL < 0: any window, every tile takes stream_tile.
+template <typename T, int NSLOT, int SG, int FL, int FR>
 __global__ __launch_bounds__(256, 4) void stream_kernel(StreamArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t ring[];  // NSLOT * kSlotElems
+  constexpr bool kFixed = FL >= 0;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wv = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, kept in an SGPR
   const int c = lane & 15;
   const int g = lane >> 4;
 
@@ -497,154 +715,92 @@ __global__ __launch_bounds__(256, 4) void stream_kernel(StreamArgs a) {
   const int t1 = min(t0 + a.chunk, tiles_r);
   if (t0 >= t1) return;  // uniform per workgroup, before any barrier
   const int nblk = tiles_r;  // 64-key blocks of this residue class
-  const int L = a.left, R = a.right;
+  const int L = kFixed ? FL : a.left;
+  const int R = kFixed ? FR : a.right;
+  const int tb = a.tok_bytes;
 
-  const int64_t tok_stride = (int64_t)a.dil * a.H * kBandD;
-  const int64_t base = (((int64_t)b * a.N + rho) * a.H + h) * kBandD;
-  const uint16_t* Q = static_cast<const uint16_t*>(a.q) + base;
-  const uint16_t* K = static_cast<const uint16_t*>(a.k) + base;
-  const uint16_t* V = static_cast<const uint16_t*>(a.v) + base;
-  uint16_t* O = static_cast<uint16_t*>(a.o) + base;
+  // Buffer resources start at the first row this workgroup reads; their
+  // range ends with the residue class's last row.  Offsets below are bytes
+  // relative to base_row (the host checks they stay below 2^31).
+  const int blo0 = max(floordiv32(t0 * kBlk - L, kBlk), 0);
+  const int base_row = blo0 * kBlk;
+  const int64_t base = (((int64_t)b * a.N + rho) * a.H + h) * kBandD + (int64_t)base_row * (tb / 2);
+  const int64_t range = (int64_t)(Nr - 1 - base_row) * tb + 2 * kBandD;
+  const uint32_t nrec = (uint32_t)(range < 0x7FFFFFFF ? range : 0x7FFFFFFF);
+  const __amdgpu_buffer_rsrc_t Qr = make_rsrc(static_cast<const uint16_t*>(a.q) + base, nrec);
+  const __amdgpu_buffer_rsrc_t Kr = make_rsrc(static_cast<const uint16_t*>(a.k) + base, nrec);
+  const __amdgpu_buffer_rsrc_t Vr = make_rsrc(static_cast<const uint16_t*>(a.v) + base, nrec);
+  const __amdgpu_buffer_rsrc_t Or = make_rsrc(static_cast<const uint16_t*>(a.o) + base, nrec);
 
-  // ---- ring warm-up: blocks of tile t0
+  BlockLane bl;
+  bl.k = (tid >> 3) * tb + (tid & 7) * 16;
+  bl.v = 2 * (tid & 31) * tb + (tid >> 5) * 16;
+  const uint32_t q_lane = (16 * wv + c) * tb + 16 * g;  // Q^T operand: query c, head_dim 8g..8g+7 (+32)
+  const int o_lane = (16 * wv + c) * tb + 16 * g;  // O row c, head_dim 8g..8g+7 (+32)
+  const int dl = 4 * g - c + L;                    // key - query + L of accumulator element 0
+  // first tile whose sub-tiles all start at key >= 0, and the number of
+  // tiles whose sub-tiles all end before the residue class does
+  constexpr int kCL = kFixed ? WinGeom<(FL < 0 ? 0 : FL), (FR < 0 ? 0 : FR)>::CL : 0;
+  constexpr int kNSUB = kFixed ? WinGeom<(FL < 0 ? 0 : FL), (FR < 0 ? 0 : FR)>::NSUB : 0;
+  const int t_int_lo = (kCL + 3) >> 2;
+  // wave 3's last sub-tile 4t + 2 - CL + NSUB must end before Nr
+  const int t_int_hi = floordiv32(floordiv32(Nr - 16, 16) + kCL - 2 - kNSUB, 4) + 1;
+
+  // ---- prologue: Q rows of tile t0, the ring blocks tile t0 reads, and
+  // tile t0+1's new block
+  const uint32_t q0 = (t0 * kBlk - base_row) * tb + q_lane;
+  uint4 qc0 = bload16(Qr, q0);
+  uint4 qc1 = bload16(Qr, q0 + 64);
+  BlockRegs X, Y;
   {
-    const int blo = max(floordiv32(t0 * kBlk - L, kBlk), 0);
     const int bhi = min(floordiv32(t0 * kBlk + 63 + R, kBlk), nblk - 1);
     BlockRegs pre[NSLOT];
 #pragma unroll
     for (int s = 0; s < NSLOT; ++s)
-      if (blo + s <= bhi) load_block(pre[s], K, V, tok_stride, blo + s, Nr, tid);
+      load_block(pre[s], Kr, Vr, bl, blo0 + s <= bhi ? (uint32_t)(s * kBlk * tb) : kOob, tb);
+    const int nb1 = floordiv32((t0 + 1) * kBlk + 63 + R, kBlk);
+    load_block(X, Kr, Vr, bl, t0 + 1 < t1 && nb1 < nblk ? (uint32_t)((nb1 * kBlk - base_row) * tb) : kOob, tb);
 #pragma unroll
     for (int s = 0; s < NSLOT; ++s)
-      if (blo + s <= bhi) store_block(pre[s], ring + ((blo + s) % NSLOT) * kSlotElems, tid);
-  }
-  uint4 qb0, qb1;
-  {
-    const int qm = t0 * 64 + 16 * wv + c;
-    const uint16_t* qr = Q + (int64_t)qm * tok_stride + 8 * g;
-    qb0 = ld16(qr, qm < Nr);
-    qb1 = ld16(qr + 32, qm < Nr);
+      if (blo0 + s <= bhi) store_block(pre[s], ring + ((blo0 + s) % NSLOT) * kSlotElems, tid);
   }
   __syncthreads();
 
-  // LDS byte offsets of this lane's operand reads inside a slot
+  // LDS operand addresses of this lane inside a slot
   const uint16_t* k_lane = ring + c * kKsStride + 8 * g;
-  const uint16_t* v_lane = ring + kSlotK + c * kVtStrideBlk + 4 * g;
+  const uint16_t* v_lane = ring + kSlotK + v_row_of_lane(c) * kVtStrideBlk + 4 * g;
 
-  for (int t = t0; t < t1; ++t) {
-    // ---- prefetch tile t+1: its new K/V block and its Q rows
-    const bool has_next = t + 1 < t1;
+  // One pipeline step: tile t computes while tile t+1's Q rows and tile
+  // t+2's new K/V block (into `next`) are in flight; tile t+1's block
+  // (`cur`, loaded one step earlier) then replaces the ring slot tile t
+  // was the last to read.
+  auto step = [&](int t, BlockRegs& cur, BlockRegs& next) {
+    const uint32_t qn = (t + 1 < t1 ? (uint32_t)(((t + 1) * kBlk - base_row) * tb) : kOob) + q_lane;
+    const uint4 qn0 = bload16(Qr, qn);
+    const uint4 qn1 = bload16(Qr, qn + 64);
+    const int nb2 = floordiv32((t + 2) * kBlk + 63 + R, kBlk);
+    load_block(next, Kr, Vr, bl, t + 2 < t1 && nb2 < nblk ? (uint32_t)((nb2 * kBlk - base_row) * tb) : kOob, tb);
+
+    const int o_off = (t * kBlk - base_row) * tb + o_lane;
+    if (kFixed && t >= t_int_lo && t < t_int_hi)
+      window_tile<T, (FL < 0 ? 0 : FL), (FR < 0 ? 0 : FR)>(k_lane, v_lane, qc0, qc1, t, wv, a.scale_log2,
+                                                          Or, o_off, dl);
+    else
+      stream_tile<T, NSLOT, SG>(k_lane, v_lane, qc0, qc1, t * kBlk + 16 * wv, Nr, L, R, a.scale_log2, Or,
+                                o_off, g, dl);
+
     const int nb = floordiv32((t + 1) * kBlk + 63 + R, kBlk);
-    const bool load_nb = has_next && nb < nblk;
-    BlockRegs pf;
-    if (load_nb) load_block(pf, K, V, tok_stride, nb, Nr, tid);
-    uint4 qn0 = make_uint4(0, 0, 0, 0), qn1 = make_uint4(0, 0, 0, 0);
-    if (has_next) {
-      const int qm = (t + 1) * 64 + 16 * wv + c;
-      const uint16_t* qr = Q + (int64_t)qm * tok_stride + 8 * g;
-      qn0 = ld16(qr, qm < Nr);
-      qn1 = ld16(qr + 32, qm < Nr);
-    }
-
-    // ---- tile t: this wave's 16 queries qa..qa+15
-    const int qa = t * 64 + 16 * wv;
-    if (qa < Nr) {
-      const int qm = qa + c;
-      const bool rows_full = qa + 15 < Nr;
-      const int sub_lo = max(floordiv32(qa - L, 16), 0);
-      const int sub_hi = min(floordiv32(qa + 15 + R, 16), (Nr - 1) >> 4);
-      // key - query offset of accumulator element r of sub-tile s: 16s + r + d_lane
-      const int d_lane = 4 * g - c - qa;
-      const uint32_t span = (uint32_t)(L + R);
-      float m_run = -INFINITY, l_run = 0.0f;
-      f32x4 acc[4];
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      for (int s0 = sub_lo; s0 <= sub_hi; s0 += SG) {
-        f32x4 sc[SG];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int j = 0; j < SG; ++j) {
-          const int s = s0 + j;
-          sc[j] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-          if (s <= sub_hi) {
-            const int soff = ((s >> 2) % NSLOT) * kSlotElems + (s & 3) * 16 * kKsStride;
-            const uint4 ka0 = *reinterpret_cast<const uint4*>(k_lane + soff);
-            const uint4 ka1 = *reinterpret_cast<const uint4*>(k_lane + soff + 32);
-            f32x4 z = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            z = Mma<T>::qk(ka0, qb0, z);
-            z = Mma<T>::qk(ka1, qb1, z);
-            // wave-uniform: every (key, query) pair of the sub-tile inside the window?
-            const int dmin = 16 * s - qa - 15, dmax = 16 * s + 15 - qa;
-            const bool full = rows_full && dmin >= -L && dmax <= R && 16 * s + 15 < Nr;
-            if (!full) {
-              const int d0 = 16 * s + d_lane;
-              const bool q_ok = qm < Nr;
-#pragma unroll
-              for (int r = 0; r < 4; ++r) {
-                const bool ok = q_ok && (uint32_t)(d0 + r + L) <= span && 16 * s + 4 * g + r < Nr;
-                z[r] = ok ? z[r] : -INFINITY;
-              }
-            }
-            sc[j] = z;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, z[r]);
-          }
-        }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m_run, mx);
-        // scores are raw dot products; the softmax scale is folded into exp2's argument
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new * a.scale_log2;
-        if (m_run != m_new) {
-          const float corr = __builtin_amdgcn_exp2f(m_run * a.scale_log2 - m_use);
-          l_run *= corr;
-#pragma unroll
-          for (int dt = 0; dt < 4; ++dt) acc[dt] *= corr;
-        }
-        m_run = m_new;
-#pragma unroll
-        for (int j = 0; j < SG; ++j) {
-          const int s = s0 + j;
-          if (s > sub_hi) continue;
-          float p[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            p[r] = __builtin_amdgcn_exp2f(fmaf(sc[j][r], a.scale_log2, -m_use));
-            l_run += p[r];
-          }
-          uint2 pb;
-          pb.x = Mma<T>::pack2(p[0], p[1]);
-          pb.y = Mma<T>::pack2(p[2], p[3]);
-          const int voff = ((s >> 2) % NSLOT) * kSlotElems + (s & 3) * 16;
-#pragma unroll
-          for (int dt = 0; dt < 4; ++dt) {
-            const uint2 va = *reinterpret_cast<const uint2*>(v_lane + voff + 16 * dt * kVtStrideBlk);
-            acc[dt] = Mma<T>::pv(va, pb, acc[dt]);
-          }
-        }
-      }
-      float l_tot = l_run + __shfl_xor(l_run, 16, 64);
-      l_tot += __shfl_xor(l_tot, 32, 64);
-      const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-      if (qm < Nr) {
-        uint16_t* orow = O + (int64_t)qm * tok_stride + 4 * g;
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-          uint2 ov;
-          ov.x = Mma<T>::pack2(acc[dt][0] * inv, acc[dt][1] * inv);
-          ov.y = Mma<T>::pack2(acc[dt][2] * inv, acc[dt][3] * inv);
-          *reinterpret_cast<uint2*>(orow + 16 * dt) = ov;
-        }
-      }
-    }
-
-    // ---- rotate: the new block replaces the slot no later tile reads
     __syncthreads();
-    if (load_nb) store_block(pf, ring + (nb % NSLOT) * kSlotElems, tid);
+    if (t + 1 < t1 && nb < nblk) store_block(cur, ring + (nb % NSLOT) * kSlotElems, tid);
     __syncthreads();
-    qb0 = qn0;
-    qb1 = qn1;
+    qc0 = qn0;
+    qc1 = qn1;
+  };
+
+  for (int t = t0; t < t1; t += 2) {
+    step(t, X, Y);
+    if (t + 1 >= t1) break;
+    step(t + 1, Y, X);
   }
 }
 
@@ -773,11 +929,38 @@ int64_t stream_slots(const ma_attn_desc* d) {
 constexpr int kMaxSlots = 6;  // 108 KB of LDS
 constexpr int kStreamSG = 5;  // sub-tiles per softmax group (a causal-64 wave tile needs 5)
 
+// Work split of the stream kernel: `chunk` consecutive tiles per workgroup,
+// enough workgroups to give every CU as many as its LDS holds.
+struct StreamPlan {
+  int64_t slots, tiles, chunk, chunks, wgs, tok_bytes;
+};
+
+StreamPlan stream_plan(const ma_attn_desc* d) {
+  StreamPlan p;
+  p.slots = stream_slots(d);
+  const int64_t nr_max = (d->seq_len + d->dilation - 1) / d->dilation;
+  p.tiles = (nr_max + 63) / 64;
+  const int64_t streams = d->batch * d->num_heads * d->dilation;
+  const int64_t per_cu = ma::imax64(1, ma::imin64(4, (160 * 1024) / (p.slots * kSlotElems * 2)));
+  const int64_t target = 256 * per_cu;
+  p.chunk = ma::imax64(1, (streams * p.tiles + target - 1) / target);
+  if (const char* e = getenv("MA_ATTN_STREAM_CHUNK")) p.chunk = ma::imax64(1, atoll(e));
+  p.chunks = (p.tiles + p.chunk - 1) / p.chunk;
+  p.wgs = streams * p.chunks;
+  p.tok_bytes = d->dilation * d->num_heads * kBandD * 2;
+  return p;
+}
+
 bool stream_applies(const ma_attn_desc* d, const void* q, const void* k, const void* v, const void* o) {
   if (!band_applies(d, q, k, v, o)) return false;
-  if (d->left > (1 << 28) || d->right > (1 << 28)) return false;
-  const int64_t slots = stream_slots(d);
-  return slots >= 1 && slots <= kMaxSlots;
+  if (d->left > (1 << 20) || d->right > (1 << 20)) return false;
+  const StreamPlan p = stream_plan(d);
+  if (p.slots < 1 || p.slots > kMaxSlots) return false;
+  if (p.wgs > (int64_t)INT32_MAX || p.tiles > (1 << 24)) return false;
+  // Every buffer offset a workgroup forms is below
+  // (chunk*64 + left + right + 256 + 64*slots) rows past its first row.
+  const int64_t rows = p.chunk * 64 + d->left + d->right + 256 + 64 * p.slots;
+  return p.tok_bytes < (1LL << 24) && rows * p.tok_bytes + 256 < (1LL << 31);
 }
 
 const char* kernel_override() {
@@ -785,46 +968,41 @@ const char* kernel_override() {
   return s ? s : "";
 }
 
-template <typename T, int NSLOT>
+template <typename T, int NSLOT, int FL, int FR>
 int launch_stream_t(const StreamArgs& a, int64_t wgs, hipStream_t st) {
   const size_t shm = (size_t)NSLOT * kSlotElems * sizeof(uint16_t);
+  auto kern = &stream_kernel<T, NSLOT, kStreamSG, FL, FR>;
   static bool attr_set = false;
   if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&stream_kernel<T, NSLOT, kStreamSG>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess)
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)shm) != hipSuccess)
       return fail("ma_attn: cannot reserve %zu B of LDS for the stream kernel", shm);
     attr_set = true;
   }
-  hipLaunchKernelGGL((stream_kernel<T, NSLOT, kStreamSG>), dim3((unsigned)wgs), dim3(256), shm, st, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)wgs), dim3(256), shm, st, a);
   return 0;
 }
 
+// Fixed-window instantiations (the BASELINE windows); others run generic.
 template <typename T>
-int launch_stream_slots(const StreamArgs& a, int64_t slots, int64_t wgs, hipStream_t st) {
+int launch_stream_any(const StreamArgs& a, int64_t slots, int64_t wgs, hipStream_t st) {
+  if (!getenv("MA_ATTN_NO_FIXED")) {
+    if (a.left == 63 && a.right == 0) return launch_stream_t<T, WinGeom<63, 0>::NSLOT, 63, 0>(a, wgs, st);
+    if (a.left == 32 && a.right == 31) return launch_stream_t<T, WinGeom<32, 31>::NSLOT, 32, 31>(a, wgs, st);
+  }
   switch (slots) {
-    case 1: return launch_stream_t<T, 1>(a, wgs, st);
-    case 2: return launch_stream_t<T, 2>(a, wgs, st);
-    case 3: return launch_stream_t<T, 3>(a, wgs, st);
-    case 4: return launch_stream_t<T, 4>(a, wgs, st);
-    case 5: return launch_stream_t<T, 5>(a, wgs, st);
-    default: return launch_stream_t<T, 6>(a, wgs, st);
+    case 1: return launch_stream_t<T, 1, -1, -1>(a, wgs, st);
+    case 2: return launch_stream_t<T, 2, -1, -1>(a, wgs, st);
+    case 3: return launch_stream_t<T, 3, -1, -1>(a, wgs, st);
+    case 4: return launch_stream_t<T, 4, -1, -1>(a, wgs, st);
+    case 5: return launch_stream_t<T, 5, -1, -1>(a, wgs, st);
+    default: return launch_stream_t<T, 6, -1, -1>(a, wgs, st);
   }
 }
 
 int launch_stream(const ma_attn_desc* d, const void* q, const void* k, const void* v, void* o,
                   hipStream_t st) {
-  const int64_t slots = stream_slots(d);
-  const int64_t nr_max = (d->seq_len + d->dilation - 1) / d->dilation;
-  const int64_t tiles = (nr_max + 63) / 64;
-  const int64_t streams = d->batch * d->num_heads * d->dilation;
-  // Enough chunks to fill every CU with as many resident workgroups as LDS allows.
-  const int64_t per_cu = ma::imax64(1, ma::imin64(4, (160 * 1024) / (slots * kSlotElems * 2)));
-  const int64_t target = 256 * per_cu;
-  int64_t chunk = ma::imax64(1, (streams * tiles + target - 1) / target);
-  if (const char* e = getenv("MA_ATTN_STREAM_CHUNK")) chunk = ma::imax64(1, atoll(e));
-  const int64_t chunks = (tiles + chunk - 1) / chunk;
-  const int64_t wgs = streams * chunks;
-  if (wgs > (int64_t)INT32_MAX || tiles > (1 << 24)) return fail("ma_attn: problem too large for one launch");
+  const StreamPlan p = stream_plan(d);
   StreamArgs a;
   a.q = q;
   a.k = k;
@@ -835,12 +1013,13 @@ int launch_stream(const ma_attn_desc* d, const void* q, const void* k, const voi
   a.left = (int32_t)d->left;
   a.right = (int32_t)d->right;
   a.dil = (int32_t)d->dilation;
-  a.tiles = (int32_t)tiles;
-  a.chunk = (int32_t)chunk;
-  a.chunks = (int32_t)chunks;
+  a.tiles = (int32_t)p.tiles;
+  a.chunk = (int32_t)p.chunk;
+  a.chunks = (int32_t)p.chunks;
+  a.tok_bytes = (int32_t)p.tok_bytes;
   a.scale_log2 = scale_of(d) * 1.4426950408889634f;
-  if (d->dtype == MA_ATTN_BF16) return launch_stream_slots<__bf16>(a, slots, wgs, st);
-  return launch_stream_slots<_Float16>(a, slots, wgs, st);
+  if (d->dtype == MA_ATTN_BF16) return launch_stream_any<__bf16>(a, p.slots, p.wgs, st);
+  return launch_stream_any<_Float16>(a, p.slots, p.wgs, st);
 }
 
 uint64_t splitmix64(uint64_t* s) {
