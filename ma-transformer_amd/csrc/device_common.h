@@ -1,0 +1,113 @@
+// device_common.h -- gfx950 device helpers shared by the attention kernels:
+// vector types, MFMA selection per element type, buffer-resource loads and
+// stores with hardware range checking, and the cross-lane reductions that
+// combine the four lane groups sharing one MFMA column.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace ma_dev {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+// MFMA operand handling per 16-bit element type.
+//   qk : 16x16x32 (8 elements of the contraction per lane)
+//   pv : 16x16x16 (4 elements per lane)
+template <typename T>
+struct Mma;
+
+template <>
+struct Mma<__bf16> {
+  static __device__ __forceinline__ f32x4 qk(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                   c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 pv(uint2 a, uint2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b),
+                                                     c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float x, float y) {
+    const __bf16 a = static_cast<__bf16>(x), b = static_cast<__bf16>(y);
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  }
+};
+
+template <>
+struct Mma<_Float16> {
+  static __device__ __forceinline__ f32x4 qk(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                  0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 pv(uint2 a, uint2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0,
+                                                 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float x, float y) {
+    const _Float16 a = static_cast<_Float16>(x), b = static_cast<_Float16>(y);
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  }
+};
+
+// fp32 MFMA: 16x16x4, one contraction element per lane.
+__device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------- buffer resources
+//
+// A raw buffer resource (stride 0) covers [base, base + bytes).  Loads past
+// the range return zero and stores past it are dropped, by the hardware range
+// check, so both can be issued unconditionally.
+constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit dwords (gfx9 family)
+
+// Base offset for a load that must be issued (to keep the memory counters
+// exact) but whose data is not needed: every lane offset added to it stays in
+// [2^31, 2^32), past any buffer range, so the hardware returns zeros without
+// a memory access.
+constexpr uint32_t kOob = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, (int)kRsrcWord3);
+}
+
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+__device__ __forceinline__ void bstore16(__amdgpu_buffer_rsrc_t r, uint32_t off, uint4 x) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, x), r, (int)off, 0, 0);
+}
+
+// ---------------------------------------------------------------- reductions
+//
+// Over the 4 lanes {l, l^16, l^32, l^48} (the lane groups that share one MFMA
+// column) with the gfx950 row/half swaps: each swap returns a lane's own value
+// and its partner's, so op(pair) is the xor-exchange result.
+__device__ __forceinline__ float col_max(float x) {
+  const i32x2 p = __builtin_amdgcn_permlane16_swap(__float_as_int(x), __float_as_int(x), false, false);
+  x = fmaxf(__int_as_float(p[0]), __int_as_float(p[1]));
+  const i32x2 q = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return fmaxf(__int_as_float(q[0]), __int_as_float(q[1]));
+}
+
+__device__ __forceinline__ float col_sum(float x) {
+  const i32x2 p = __builtin_amdgcn_permlane16_swap(__float_as_int(x), __float_as_int(x), false, false);
+  x = __int_as_float(p[0]) + __int_as_float(p[1]);
+  const i32x2 q = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return __int_as_float(q[0]) + __int_as_float(q[1]);
+}
+
+__device__ __forceinline__ int floordiv32(int a, int d) {
+  const int q = a / d;
+  return (a % d != 0 && a < 0) ? q - 1 : q;
+}
+
+}  // namespace ma_dev

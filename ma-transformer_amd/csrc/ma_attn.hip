@@ -28,7 +28,9 @@
 #include <string>
 
 #include "../../include/ma_attn.h"
+#include "device_common.h"
 #include "pattern.h"
+#include "stream_kernel.h"
 
 namespace {
 
@@ -44,11 +46,7 @@ int fail(const char* fmt, ...) {
   return 1;
 }
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+using namespace ma_dev;
 
 // ------------------------------------------------------------------ element access
 
@@ -164,42 +162,6 @@ __global__ __launch_bounds__(256) void rows_kernel(const T* __restrict__ q, cons
 }
 
 // ------------------------------------------------------------------ band_kernel (MFMA)
-
-// Operand types and MFMA selection per 16-bit element type.
-template <typename T>
-struct Mma;
-
-template <>
-struct Mma<__bf16> {
-  static __device__ __forceinline__ f32x4 qk(uint4 a, uint4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ f32x4 pv(uint2 a, uint2 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
-                                                     __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ uint32_t pack2(float x, float y) {
-    const __bf16 a = static_cast<__bf16>(x), b = static_cast<__bf16>(y);
-    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
-  }
-};
-
-template <>
-struct Mma<_Float16> {
-  static __device__ __forceinline__ f32x4 qk(uint4 a, uint4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ f32x4 pv(uint2 a, uint2 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
-                                                 __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ uint32_t pack2(float x, float y) {
-    const _Float16 a = static_cast<_Float16>(x), b = static_cast<_Float16>(y);
-    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
-  }
-};
 
 constexpr int kBandD = 64;         // head_dim handled by band_kernel
 constexpr int kBandQ = 64;         // queries per workgroup (4 waves x 16)
@@ -392,418 +354,6 @@ __global__ __launch_bounds__(256) void band_kernel(BandArgs a) {
   }
 }
 
-// ------------------------------------------------------------------ stream_kernel (MFMA, K/V ring)
-//
-// Sliding windows (bf16/fp16, head_dim 64).  One workgroup streams a chunk of
-// consecutive 64-query tiles of one (batch, head, residue class).  K/V live
-// in an LDS ring of 64-key blocks (K row major, V transposed); tile t needs
-// blocks floor((64t-left)/64) .. floor((64t+63+right)/64), so moving to tile
-// t+1 needs exactly one new block.  While tile t computes, the next tile's Q
-// rows and its new K/V block are already in flight into registers; after the
-// tile, the block is written over the ring slot that no tile needs any more.
-// Every Q/K/V/O row crosses HBM once, except the ring warm-up at chunk start.
-//
-// All global traffic uses buffer instructions on a per-workgroup resource
-// whose range ends at the residue class's last row: rows past the end read as
-// zero and their stores are dropped by the hardware range check, so loads and
-// stores are issued unconditionally (exact memory counters, no exec-masked
-// branches) and the ragged last tile needs no separate path.  Per wave: 16
-// queries (one MFMA column each) against the 16-key sub-tiles that intersect
-// their windows; all control is wave-uniform (scalar).
-
-constexpr int kBlk = 64;                        // keys per ring block
-constexpr int kSlotK = kBlk * kKsStride;        // K rows of a block (64 x 72)
-constexpr int kVtStrideBlk = kBlk + 8;          // V^T row of a block: 72 (144 B)
-constexpr int kSlotElems = kSlotK + kBandD * kVtStrideBlk;  // 9216 uint16 = 18 KB
-constexpr uint32_t kRsrcWord3 = 0x00020000u;    // raw buffer, 32-bit dwords (gfx9 family)
-
-struct StreamArgs {
-  const void* q;
-  const void* k;
-  const void* v;
-  void* o;
-  int64_t N, H;
-  int32_t left, right, dil;
-  int32_t tiles;      // query tiles of the longest residue class
-  int32_t chunk;      // tiles per workgroup
-  int32_t chunks;     // ceil(tiles / chunk)
-  int32_t tok_bytes;  // bytes between consecutive rows of a residue class (dil * H * 128)
-  float scale_log2;
-};
-
-typedef int i32x4 __attribute__((ext_vector_type(4)));
-typedef int i32x2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, (int)kRsrcWord3);
-}
-
-__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
-}
-
-// Base offset for a load that must be issued (to keep the memory counters
-// exact) but whose data is not needed: every lane offset added to it stays
-// in [2^31, 2^32), past any buffer range, so the hardware returns zeros
-// without a memory access.
-constexpr uint32_t kOob = 0x80000000u;
-
-__device__ __forceinline__ void bstore8(__amdgpu_buffer_rsrc_t r, int off, uint2 x) {
-  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, x), r, off, 0, 0);
-}
-
-// Reductions over the 4 lanes {l, l^16, l^32, l^48} (the lane groups that
-// share one MFMA column) with the gfx950 row/half swaps: each swap returns a
-// lane's own value and its partner's, so op(pair) is the xor-exchange result.
-__device__ __forceinline__ float col_max(float x) {
-  const i32x2 p = __builtin_amdgcn_permlane16_swap(__float_as_int(x), __float_as_int(x), false, false);
-  x = fmaxf(__int_as_float(p[0]), __int_as_float(p[1]));
-  const i32x2 q = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
-  return fmaxf(__int_as_float(q[0]), __int_as_float(q[1]));
-}
-
-__device__ __forceinline__ float col_sum(float x) {
-  const i32x2 p = __builtin_amdgcn_permlane16_swap(__float_as_int(x), __float_as_int(x), false, false);
-  x = __int_as_float(p[0]) + __int_as_float(p[1]);
-  const i32x2 q = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
-  return __int_as_float(q[0]) + __int_as_float(q[1]);
-}
-
-// One 64-key block in flight: K as 2 x 16 B per thread, V as 2 keys x 16 B.
-struct BlockRegs {
-  uint4 k0, k1, v0, v1;
-};
-
-// Per-lane byte offsets of the block loads, relative to the block's first row.
-// K: thread -> keys (tid>>3) and (tid>>3)+32, 16 B column tid&7 (a wave
-// instruction reads 8 whole 128 B rows).  V: key pair tid&31, column tid>>5.
-struct BlockLane {
-  uint32_t k, v;
-};
-
-__device__ __forceinline__ void load_block(BlockRegs& r, __amdgpu_buffer_rsrc_t K, __amdgpu_buffer_rsrc_t V,
-                                           const BlockLane& bl, uint32_t row_off, int tok_bytes) {
-  r.k0 = bload16(K, bl.k + row_off);
-  r.k1 = bload16(K, bl.k + row_off + 32 * (uint32_t)tok_bytes);
-  r.v0 = bload16(V, bl.v + row_off);
-  r.v1 = bload16(V, bl.v + row_off + (uint32_t)tok_bytes);
-}
-
-// V^T words: (key 2kp, key 2kp+1) pairs for one head_dim row, built with v_perm.
-__device__ __forceinline__ void store_block(const BlockRegs& r, uint16_t* slot, int tid) {
-  uint16_t* ks = slot;
-  uint16_t* vt = slot + kSlotK;
-  const int chk = tid & 7;
-  *reinterpret_cast<uint4*>(&ks[(tid >> 3) * kKsStride + 8 * chk]) = r.k0;
-  *reinterpret_cast<uint4*>(&ks[((tid >> 3) + 32) * kKsStride + 8 * chk]) = r.k1;
-  const int kp = tid & 31, chv = tid >> 5;
-  const uint32_t w0[4] = {r.v0.x, r.v0.y, r.v0.z, r.v0.w};
-  const uint32_t w1[4] = {r.v1.x, r.v1.y, r.v1.z, r.v1.w};
-  uint32_t* col = reinterpret_cast<uint32_t*>(&vt[(8 * chv) * kVtStrideBlk + 2 * kp]);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    col[(2 * e) * (kVtStrideBlk / 2)] = __builtin_amdgcn_perm(w1[e], w0[e], 0x05040100u);
-    col[(2 * e + 1) * (kVtStrideBlk / 2)] = __builtin_amdgcn_perm(w1[e], w0[e], 0x07060302u);
-  }
-}
-
-__device__ __forceinline__ int floordiv32(int a, int d) {
-  const int q = a / d;
-  return (a % d != 0 && a < 0) ? q - 1 : q;
-}
-
-// Accumulator layout shared by both tile routines.  The P.V MFMA produces
-// O^T tiles dt = 0..3 of 16 head_dim rows; tile row m of tile dt is head_dim
-//   d(dt, m) = 32*(dt>>1) + 8*(m>>2) + 4*(dt&1) + (m&3),
-// so lane (query c, group g) ends up holding O[c][8g..8g+7] in acc[0..1] and
-// O[c][32+8g..32+8g+7] in acc[2..3]: two 16 B stores per lane.  The
-// permutation is applied by which V^T row each lane reads (v_row_of_lane).
-__device__ __forceinline__ int v_row_of_lane(int c) { return 8 * (c >> 2) + (c & 3); }
-__device__ __forceinline__ constexpr int v_row_of_tile(int dt) { return 32 * (dt >> 1) + 4 * (dt & 1); }
-
-// Normalise and store one wave's 16 O rows (rows past the end are dropped by
-// the buffer range check).
-template <typename T>
-__device__ __forceinline__ void store_o(const f32x4 (&acc)[4], float l_run, __amdgpu_buffer_rsrc_t Orsrc,
-                                        int o_off) {
-  const float l_tot = col_sum(l_run);
-  const float inv = l_tot > 0.0f ? __builtin_amdgcn_rcpf(l_tot) : 0.0f;
-#pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    const f32x4 a0 = acc[2 * half], a1 = acc[2 * half + 1];
-    uint4 ov;
-    ov.x = Mma<T>::pack2(a0[0] * inv, a0[1] * inv);
-    ov.y = Mma<T>::pack2(a0[2] * inv, a0[3] * inv);
-    ov.z = Mma<T>::pack2(a1[0] * inv, a1[1] * inv);
-    ov.w = Mma<T>::pack2(a1[2] * inv, a1[3] * inv);
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, ov), Orsrc, o_off + 64 * half, 0, 0);
-  }
-}
-
-// One wave's 16 queries qa..qa+15 (qa wave-uniform) against the K/V ring,
-// any window (runtime left/right): scores on MFMA, softmax in registers
-// (online across groups of SG sub-tiles), P.V on MFMA, one O store per row.
-// Used for tiles at the sequence edges and for windows without a fixed-shape
-// instantiation.  Rows >= Nr compute on zero Q rows and their stores fall
-// outside the buffer range.
-template <typename T, int NSLOT, int SG>
-__device__ __forceinline__ void stream_tile(const uint16_t* k_lane, const uint16_t* v_lane, uint4 qb0,
-                                            uint4 qb1, int qa, int Nr, int L, int R, float sl2,
-                                            __amdgpu_buffer_rsrc_t Orsrc, int o_off, int g, int dl) {
-  const int sub_lo = max(floordiv32(qa - L, 16), 0);
-  const int sub_hi = min(floordiv32(qa + 15 + R, 16), (Nr - 1) >> 4);
-  const uint32_t span = (uint32_t)(L + R);
-  float m_run = -INFINITY, l_run = 0.0f;
-  f32x4 acc[4];
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  for (int s0 = sub_lo; s0 <= sub_hi; s0 += SG) {
-    f32x4 sc[SG];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < SG; ++j) {
-      const int s = s0 + j;
-      if (s > sub_hi) break;
-      const int soff = ((s >> 2) % NSLOT) * kSlotElems + (s & 3) * 16 * kKsStride;
-      const uint4 ka0 = *reinterpret_cast<const uint4*>(k_lane + soff);
-      const uint4 ka1 = *reinterpret_cast<const uint4*>(k_lane + soff + 32);
-      f32x4 z = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      z = Mma<T>::qk(ka0, qb0, z);
-      z = Mma<T>::qk(ka1, qb1, z);
-      // key - query offsets of this sub-tile span [16s-qa-15, 16s-qa+15]
-      const int rel = 16 * s - qa;
-      if (rel - 15 < -L || rel + 15 > R) {
-        // element r: key - query + L = dl + rel + r, inside the window iff in [0, L+R]
-        const int x = dl + rel;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) z[r] = (uint32_t)(x + r) <= span ? z[r] : -INFINITY;
-      }
-      if (16 * s + 15 >= Nr) {
-        const int km = 16 * s + 4 * g;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) z[r] = km + r < Nr ? z[r] : -INFINITY;
-      }
-      sc[j] = z;
-      mx = fmaxf(mx, fmaxf(fmaxf(z[0], z[1]), fmaxf(z[2], z[3])));
-    }
-    const float m_new = fmaxf(m_run, col_max(mx));
-    // scores are raw dot products; the softmax scale is folded into exp2's argument
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new * sl2;
-    if (s0 != sub_lo) {  // rescale what earlier groups accumulated
-      const float corr = __builtin_amdgcn_exp2f(m_run * sl2 - m_use);
-      l_run *= corr;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) acc[dt] *= corr;
-    }
-    m_run = m_new;
-#pragma unroll
-    for (int j = 0; j < SG; ++j) {
-      const int s = s0 + j;
-      if (s > sub_hi) break;
-      float p[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        p[r] = __builtin_amdgcn_exp2f(fmaf(sc[j][r], sl2, -m_use));
-        l_run += p[r];
-      }
-      uint2 pb;
-      pb.x = Mma<T>::pack2(p[0], p[1]);
-      pb.y = Mma<T>::pack2(p[2], p[3]);
-      const int voff = ((s >> 2) % NSLOT) * kSlotElems + (s & 3) * 16;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const uint2 va = *reinterpret_cast<const uint2*>(v_lane + voff + v_row_of_tile(dt) * kVtStrideBlk);
-        acc[dt] = Mma<T>::pv(va, pb, acc[dt]);
-      }
-    }
-  }
-  store_o<T>(acc, l_run, Orsrc, o_off);
-}
-
-// Compile-time geometry of a fixed window [i-L, i+R] (dilation handled by
-// the residue-class split): a wave's 16 queries at qa = 16*(4t + wv) read
-// sub-tiles s = 4t + wv - CL + j, j < NSUB, whose key - query offsets
-// 16*(j-CL) + [-15, 15] are the same for every interior tile.
-template <int L, int R>
-struct WinGeom {
-  static constexpr int CL = (L + 15) / 16;
-  static constexpr int NSUB = (15 + R) / 16 + CL + 1;
-  static constexpr int NSLOT = (63 + R) / 64 + (L + 63) / 64 + 1;
-};
-
-// Interior tile of a fixed window: every sub-tile exists and lies before the
-// sequence end, so the whole tile is straight-line code (no branches): the
-// sub-tile count and which sub-tiles need a mask are compile-time, the
-// per-lane mask compares are loop-invariant, and the softmax is two-pass.
-template <typename T, int L, int R>
-__device__ __forceinline__ void window_tile(const uint16_t* k_lane, const uint16_t* v_lane, uint4 qb0,
-                                            uint4 qb1, int t, int wv, float sl2,
-                                            __amdgpu_buffer_rsrc_t Orsrc, int o_off, int dl) {
-  using G = WinGeom<L, R>;
-  f32x4 sc[G::NSUB];
-  int voff[G::NSUB];
-#pragma unroll
-  for (int j = 0; j < G::NSUB; ++j) {
-    const int u = wv + 3 * G::CL + j;  // s = 4(t - CL) + u, u >= 0
-    const int slot = (t - G::CL + (u >> 2)) % G::NSLOT;
-    const int soff = slot * kSlotElems + (u & 3) * 16 * kKsStride;
-    voff[j] = slot * kSlotElems + (u & 3) * 16;
-    const uint4 ka0 = *reinterpret_cast<const uint4*>(k_lane + soff);
-    const uint4 ka1 = *reinterpret_cast<const uint4*>(k_lane + soff + 32);
-    f32x4 z = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    z = Mma<T>::qk(ka0, qb0, z);
-    z = Mma<T>::qk(ka1, qb1, z);
-    const int rel = 16 * (j - G::CL);
-    if (rel - 15 < -L || rel + 15 > R) {  // resolved at compile time
-#pragma unroll
-      for (int r = 0; r < 4; ++r) z[r] = (uint32_t)(dl + rel + r) <= (uint32_t)(L + R) ? z[r] : -INFINITY;
-    }
-    sc[j] = z;
-  }
-  float mx = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < G::NSUB; ++j) mx = fmaxf(mx, fmaxf(fmaxf(sc[j][0], sc[j][1]), fmaxf(sc[j][2], sc[j][3])));
-  const float m_use = col_max(mx) * sl2;  // finite: every query sees its own key
-  float l_run = 0.0f;
-  f32x4 acc[4];
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int j = 0; j < G::NSUB; ++j) {
-    float p[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      p[r] = __builtin_amdgcn_exp2f(fmaf(sc[j][r], sl2, -m_use));
-      l_run += p[r];
-    }
-    uint2 pb;
-    pb.x = Mma<T>::pack2(p[0], p[1]);
-    pb.y = Mma<T>::pack2(p[2], p[3]);
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      const uint2 va = *reinterpret_cast<const uint2*>(v_lane + voff[j] + v_row_of_tile(dt) * kVtStrideBlk);
-      acc[dt] = Mma<T>::pv(va, pb, acc[dt]);
-    }
-  }
-  store_o<T>(acc, l_run, Orsrc, o_off);
-}
-
-// FL/FR >= 0: the kernel is specialised for window [i-FL, i+FR] (interior
-// tiles take window_tile); FL < 0: any window, every tile takes stream_tile.
-template <typename T, int NSLOT, int SG, int FL, int FR>
-__global__ __launch_bounds__(256, 4) void stream_kernel(StreamArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t ring[];  // NSLOT * kSlotElems
-  constexpr bool kFixed = FL >= 0;
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, kept in an SGPR
-  const int c = lane & 15;
-  const int g = lane >> 4;
-
-  int lin = blockIdx.x;
-  const int chunk_id = lin % a.chunks;
-  lin /= a.chunks;
-  const int rho = lin % a.dil;
-  lin /= a.dil;
-  const int h = lin % (int)a.H;
-  const int b = lin / (int)a.H;
-
-  const int Nr = (int)((a.N - rho + a.dil - 1) / a.dil);
-  const int tiles_r = (Nr + 63) >> 6;
-  const int t0 = chunk_id * a.chunk;
-  const int t1 = min(t0 + a.chunk, tiles_r);
-  if (t0 >= t1) return;  // uniform per workgroup, before any barrier
-  const int nblk = tiles_r;  // 64-key blocks of this residue class
-  const int L = kFixed ? FL : a.left;
-  const int R = kFixed ? FR : a.right;
-  const int tb = a.tok_bytes;
-
-  // Buffer resources start at the first row this workgroup reads; their
-  // range ends with the residue class's last row.  Offsets below are bytes
-  // relative to base_row (the host checks they stay below 2^31).
-  const int blo0 = max(floordiv32(t0 * kBlk - L, kBlk), 0);
-  const int base_row = blo0 * kBlk;
-  const int64_t base = (((int64_t)b * a.N + rho) * a.H + h) * kBandD + (int64_t)base_row * (tb / 2);
-  const int64_t range = (int64_t)(Nr - 1 - base_row) * tb + 2 * kBandD;
-  const uint32_t nrec = (uint32_t)(range < 0x7FFFFFFF ? range : 0x7FFFFFFF);
-  const __amdgpu_buffer_rsrc_t Qr = make_rsrc(static_cast<const uint16_t*>(a.q) + base, nrec);
-  const __amdgpu_buffer_rsrc_t Kr = make_rsrc(static_cast<const uint16_t*>(a.k) + base, nrec);
-  const __amdgpu_buffer_rsrc_t Vr = make_rsrc(static_cast<const uint16_t*>(a.v) + base, nrec);
-  const __amdgpu_buffer_rsrc_t Or = make_rsrc(static_cast<const uint16_t*>(a.o) + base, nrec);
-
-  BlockLane bl;
-  bl.k = (tid >> 3) * tb + (tid & 7) * 16;
-  bl.v = 2 * (tid & 31) * tb + (tid >> 5) * 16;
-  const uint32_t q_lane = (16 * wv + c) * tb + 16 * g;  // Q^T operand: query c, head_dim 8g..8g+7 (+32)
-  const int o_lane = (16 * wv + c) * tb + 16 * g;  // O row c, head_dim 8g..8g+7 (+32)
-  const int dl = 4 * g - c + L;                    // key - query + L of accumulator element 0
-  // first tile whose sub-tiles all start at key >= 0, and the number of
-  // tiles whose sub-tiles all end before the residue class does
-  constexpr int kCL = kFixed ? WinGeom<(FL < 0 ? 0 : FL), (FR < 0 ? 0 : FR)>::CL : 0;
-  constexpr int kNSUB = kFixed ? WinGeom<(FL < 0 ? 0 : FL), (FR < 0 ? 0 : FR)>::NSUB : 0;
-  const int t_int_lo = (kCL + 3) >> 2;
-  // wave 3's last sub-tile 4t + 2 - CL + NSUB must end before Nr
-  const int t_int_hi = floordiv32(floordiv32(Nr - 16, 16) + kCL - 2 - kNSUB, 4) + 1;
-
-  // ---- prologue: Q rows of tile t0, the ring blocks tile t0 reads, and
-  // tile t0+1's new block
-  const uint32_t q0 = (t0 * kBlk - base_row) * tb + q_lane;
-  uint4 qc0 = bload16(Qr, q0);
-  uint4 qc1 = bload16(Qr, q0 + 64);
-  BlockRegs X, Y;
-  {
-    const int bhi = min(floordiv32(t0 * kBlk + 63 + R, kBlk), nblk - 1);
-    BlockRegs pre[NSLOT];
-#pragma unroll
-    for (int s = 0; s < NSLOT; ++s)
-      load_block(pre[s], Kr, Vr, bl, blo0 + s <= bhi ? (uint32_t)(s * kBlk * tb) : kOob, tb);
-    const int nb1 = floordiv32((t0 + 1) * kBlk + 63 + R, kBlk);
-    load_block(X, Kr, Vr, bl, t0 + 1 < t1 && nb1 < nblk ? (uint32_t)((nb1 * kBlk - base_row) * tb) : kOob, tb);
-#pragma unroll
-    for (int s = 0; s < NSLOT; ++s)
-      if (blo0 + s <= bhi) store_block(pre[s], ring + ((blo0 + s) % NSLOT) * kSlotElems, tid);
-  }
-  __syncthreads();
-
-  // LDS operand addresses of this lane inside a slot
-  const uint16_t* k_lane = ring + c * kKsStride + 8 * g;
-  const uint16_t* v_lane = ring + kSlotK + v_row_of_lane(c) * kVtStrideBlk + 4 * g;
-
-  // One pipeline step: tile t computes while tile t+1's Q rows and tile
-  // t+2's new K/V block (into `next`) are in flight; tile t+1's block
-  // (`cur`, loaded one step earlier) then replaces the ring slot tile t
-  // was the last to read.
-  auto step = [&](int t, BlockRegs& cur, BlockRegs& next) {
-    const uint32_t qn = (t + 1 < t1 ? (uint32_t)(((t + 1) * kBlk - base_row) * tb) : kOob) + q_lane;
-    const uint4 qn0 = bload16(Qr, qn);
-    const uint4 qn1 = bload16(Qr, qn + 64);
-    const int nb2 = floordiv32((t + 2) * kBlk + 63 + R, kBlk);
-    load_block(next, Kr, Vr, bl, t + 2 < t1 && nb2 < nblk ? (uint32_t)((nb2 * kBlk - base_row) * tb) : kOob, tb);
-
-    const int o_off = (t * kBlk - base_row) * tb + o_lane;
-    if (kFixed && t >= t_int_lo && t < t_int_hi)
-      window_tile<T, (FL < 0 ? 0 : FL), (FR < 0 ? 0 : FR)>(k_lane, v_lane, qc0, qc1, t, wv, a.scale_log2,
-                                                          Or, o_off, dl);
-    else
-      stream_tile<T, NSLOT, SG>(k_lane, v_lane, qc0, qc1, t * kBlk + 16 * wv, Nr, L, R, a.scale_log2, Or,
-                                o_off, g, dl);
-
-    const int nb = floordiv32((t + 1) * kBlk + 63 + R, kBlk);
-    __syncthreads();
-    if (t + 1 < t1 && nb < nblk) store_block(cur, ring + (nb % NSLOT) * kSlotElems, tid);
-    __syncthreads();
-    qc0 = qn0;
-    qc1 = qn1;
-  };
-
-  for (int t = t0; t < t1; t += 2) {
-    step(t, X, Y);
-    if (t + 1 >= t1) break;
-    step(t + 1, Y, X);
-  }
-}
-
 // ------------------------------------------------------------------ host side
 
 size_t elt_size(int32_t dt) { return dt == MA_ATTN_F32 ? 4 : 2; }
@@ -922,44 +472,51 @@ int launch_band(const ma_attn_desc* d, const void* q, const void* k, const void*
 }
 
 // Ring blocks a tile touches: floor((63+R)/64) - floor(-L/64) + 1.
-int64_t stream_slots(const ma_attn_desc* d) {
-  return ma::floordiv64(63 + d->right, kBlk) - ma::floordiv64(-d->left, kBlk) + 1;
+// Ring slots a tile touches for slots of `rows` keys:
+// floor((63+R)/rows) - floor(-L/rows) + 1.
+int64_t stream_slots(const ma_attn_desc* d, int rows) {
+  return ma::floordiv64(63 + d->right, rows) - ma::floordiv64(-d->left, rows) + 1;
 }
 
-constexpr int kMaxSlots = 6;  // 108 KB of LDS
+constexpr int kMaxSlots = 6;  // generic instantiations (16-bit: 108 KB, fp32: 102 KB of LDS)
 constexpr int kStreamSG = 5;  // sub-tiles per softmax group (a causal-64 wave tile needs 5)
 
 // Work split of the stream kernel: `chunk` consecutive tiles per workgroup,
 // enough workgroups to give every CU as many as its LDS holds.
 struct StreamPlan {
-  int64_t slots, tiles, chunk, chunks, wgs, tok_bytes;
+  int64_t rows, slot_bytes, max_per_cu, slots, tiles, chunk, chunks, wgs, tok_bytes;
 };
 
 StreamPlan stream_plan(const ma_attn_desc* d) {
   StreamPlan p;
-  p.slots = stream_slots(d);
+  const bool f32 = d->dtype == MA_ATTN_F32;
+  p.rows = f32 ? F32Path::kRows : HalfPath<__bf16>::kRows;
+  p.slot_bytes = f32 ? F32Path::kSlot : HalfPath<__bf16>::kSlot;
+  p.max_per_cu = f32 ? F32Path::kMinBlocks : HalfPath<__bf16>::kMinBlocks;
+  p.slots = stream_slots(d, (int)p.rows);
   const int64_t nr_max = (d->seq_len + d->dilation - 1) / d->dilation;
   p.tiles = (nr_max + 63) / 64;
   const int64_t streams = d->batch * d->num_heads * d->dilation;
-  const int64_t per_cu = ma::imax64(1, ma::imin64(4, (160 * 1024) / (p.slots * kSlotElems * 2)));
+  const int64_t per_cu = ma::imax64(1, ma::imin64(p.max_per_cu, (160 * 1024) / (p.slots * p.slot_bytes)));
   const int64_t target = 256 * per_cu;
   p.chunk = ma::imax64(1, (streams * p.tiles + target - 1) / target);
   if (const char* e = getenv("MA_ATTN_STREAM_CHUNK")) p.chunk = ma::imax64(1, atoll(e));
   p.chunks = (p.tiles + p.chunk - 1) / p.chunk;
   p.wgs = streams * p.chunks;
-  p.tok_bytes = d->dilation * d->num_heads * kBandD * 2;
+  p.tok_bytes = d->dilation * d->num_heads * kHeadDim * (f32 ? 4 : 2);
   return p;
 }
 
 bool stream_applies(const ma_attn_desc* d, const void* q, const void* k, const void* v, const void* o) {
-  if (!band_applies(d, q, k, v, o)) return false;
+  if (d->pattern != MA_ATTN_SLIDING || d->head_dim != kHeadDim || d->left < 0 || d->right < 0) return false;
+  if (!(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o))) return false;
   if (d->left > (1 << 20) || d->right > (1 << 20)) return false;
   const StreamPlan p = stream_plan(d);
   if (p.slots < 1 || p.slots > kMaxSlots) return false;
   if (p.wgs > (int64_t)INT32_MAX || p.tiles > (1 << 24)) return false;
   // Every buffer offset a workgroup forms is below
-  // (chunk*64 + left + right + 256 + 64*slots) rows past its first row.
-  const int64_t rows = p.chunk * 64 + d->left + d->right + 256 + 64 * p.slots;
+  // (chunk*64 + left + right + 256 + rows*slots) rows past its first row.
+  const int64_t rows = p.chunk * 64 + d->left + d->right + 256 + p.rows * p.slots;
   return p.tok_bytes < (1LL << 24) && rows * p.tok_bytes + 256 < (1LL << 31);
 }
 
@@ -968,10 +525,10 @@ const char* kernel_override() {
   return s ? s : "";
 }
 
-template <typename T, int NSLOT, int FL, int FR>
+template <class P, int NSLOT, int FL, int FR>
 int launch_stream_t(const StreamArgs& a, int64_t wgs, hipStream_t st) {
-  const size_t shm = (size_t)NSLOT * kSlotElems * sizeof(uint16_t);
-  auto kern = &stream_kernel<T, NSLOT, kStreamSG, FL, FR>;
+  const size_t shm = (size_t)NSLOT * P::kSlot;
+  auto kern = &stream_kernel<P, NSLOT, kStreamSG, FL, FR>;
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -983,20 +540,22 @@ int launch_stream_t(const StreamArgs& a, int64_t wgs, hipStream_t st) {
   return 0;
 }
 
-// Fixed-window instantiations (the BASELINE windows); others run generic.
-template <typename T>
+// Fixed-window instantiations (the BASELINE windows); other windows run the
+// generic kernel with `slots` ring slots.
+template <class P>
 int launch_stream_any(const StreamArgs& a, int64_t slots, int64_t wgs, hipStream_t st) {
+  constexpr int RS = P::kRows;
   if (!getenv("MA_ATTN_NO_FIXED")) {
-    if (a.left == 63 && a.right == 0) return launch_stream_t<T, WinGeom<63, 0>::NSLOT, 63, 0>(a, wgs, st);
-    if (a.left == 32 && a.right == 31) return launch_stream_t<T, WinGeom<32, 31>::NSLOT, 32, 31>(a, wgs, st);
+    if (a.left == 63 && a.right == 0) return launch_stream_t<P, WinGeom<63, 0, RS>::NSLOT, 63, 0>(a, wgs, st);
+    if (a.left == 32 && a.right == 31) return launch_stream_t<P, WinGeom<32, 31, RS>::NSLOT, 32, 31>(a, wgs, st);
   }
   switch (slots) {
-    case 1: return launch_stream_t<T, 1, -1, -1>(a, wgs, st);
-    case 2: return launch_stream_t<T, 2, -1, -1>(a, wgs, st);
-    case 3: return launch_stream_t<T, 3, -1, -1>(a, wgs, st);
-    case 4: return launch_stream_t<T, 4, -1, -1>(a, wgs, st);
-    case 5: return launch_stream_t<T, 5, -1, -1>(a, wgs, st);
-    default: return launch_stream_t<T, 6, -1, -1>(a, wgs, st);
+    case 1: return launch_stream_t<P, 1, -1, -1>(a, wgs, st);
+    case 2: return launch_stream_t<P, 2, -1, -1>(a, wgs, st);
+    case 3: return launch_stream_t<P, 3, -1, -1>(a, wgs, st);
+    case 4: return launch_stream_t<P, 4, -1, -1>(a, wgs, st);
+    case 5: return launch_stream_t<P, 5, -1, -1>(a, wgs, st);
+    default: return launch_stream_t<P, 6, -1, -1>(a, wgs, st);
   }
 }
 
@@ -1018,8 +577,11 @@ int launch_stream(const ma_attn_desc* d, const void* q, const void* k, const voi
   a.chunks = (int32_t)p.chunks;
   a.tok_bytes = (int32_t)p.tok_bytes;
   a.scale_log2 = scale_of(d) * 1.4426950408889634f;
-  if (d->dtype == MA_ATTN_BF16) return launch_stream_any<__bf16>(a, p.slots, p.wgs, st);
-  return launch_stream_any<_Float16>(a, p.slots, p.wgs, st);
+  switch (d->dtype) {
+    case MA_ATTN_BF16: return launch_stream_any<HalfPath<__bf16>>(a, p.slots, p.wgs, st);
+    case MA_ATTN_F16: return launch_stream_any<HalfPath<_Float16>>(a, p.slots, p.wgs, st);
+    default: return launch_stream_any<F32Path>(a, p.slots, p.wgs, st);
+  }
 }
 
 uint64_t splitmix64(uint64_t* s) {

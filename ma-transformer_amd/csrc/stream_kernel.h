@@ -1,0 +1,490 @@
+// stream_kernel.h -- the sliding-window forward kernel (head_dim 64, any
+// dilation, any left/right >= 0) for bf16, fp16 and fp32.
+//
+// One workgroup (4 waves) streams a chunk of consecutive 64-query tiles of one
+// (batch, head, residue class).  A residue class rho of a dilated window is
+// the subsequence i = rho + dil*m; on it the window is the contiguous band
+// m-left .. m+right, so every dilation is the same banded problem on strided
+// rows.  K/V live in an LDS ring of slots of P::kRows keys; tile t reads slots
+// floor((64t-left)/rows) .. floor((64t+63+right)/rows), so moving to tile t+1
+// needs exactly 64/rows new slots.  While tile t computes, tile t+1's Q rows
+// and tile t+2's new K/V rows are in flight into registers; after the tile,
+// tile t+1's rows are written over the slots no later tile reads.  Every
+// Q/K/V/O row crosses HBM once, except the ring warm-up at chunk start.
+//
+// All global traffic uses buffer instructions on a per-workgroup resource
+// whose range ends at the residue class's last row: rows past the end read as
+// zero and their stores are dropped by the hardware range check, so loads and
+// stores are issued unconditionally (exact memory counters, no exec-masked
+// branches) and the ragged last tile needs no separate path.
+//
+// Per wave: 16 queries (one MFMA column each) against the 16-key sub-tiles
+// that intersect their windows.  S^T = K Q^T lands as lane (query c, group g)
+// holding keys 4g..4g+3 of a sub-tile, which is exactly the B operand layout
+// P^T of O^T = V^T P^T, so probabilities never leave registers.  All control
+// flow is wave-uniform (scalar).
+#pragma once
+
+#include "device_common.h"
+
+namespace ma_dev {
+
+constexpr int kHeadDim = 64;
+
+struct StreamArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  int64_t N, H;
+  int32_t left, right, dil;
+  int32_t tiles;      // query tiles of the longest residue class
+  int32_t chunk;      // tiles per workgroup
+  int32_t chunks;     // ceil(tiles / chunk)
+  int32_t tok_bytes;  // bytes between consecutive rows of a residue class (dil * H * 64 * elt)
+  float scale_log2;   // softmax scale * log2(e)
+};
+
+// ---------------------------------------------------------------- 16-bit path
+//
+// Q.K^T on 16x16x32 MFMA (K rows row-major in LDS), P.V on 16x16x16 MFMA with
+// V transposed in LDS (V^T rows = head_dim).  V^T rows are read permuted:
+// O^T tile dt row m is head_dim d(dt, m) = 32*(dt>>1) + 8*(m>>2) + 4*(dt&1) +
+// (m&3), so lane (query c, group g) ends with O[c][8g..8g+7] in acc[0..1] and
+// O[c][32+8g..32+8g+7] in acc[2..3]: two 16 B stores per lane.
+__device__ __forceinline__ int v_row_of_lane(int c) { return 8 * (c >> 2) + (c & 3); }
+__device__ __forceinline__ constexpr int v_row_of_tile(int dt) { return 32 * (dt >> 1) + 4 * (dt & 1); }
+
+template <typename T>
+struct HalfPath {
+  using Elt = T;
+  static constexpr int kRows = 64;                         // keys per ring slot
+  static constexpr int kKRow = 144;                        // bytes per K row in LDS (128 + 16 pad)
+  static constexpr int kVRow = 144;                        // bytes per V^T row (64 keys * 2 + 16 pad)
+  static constexpr int kSlotK = kRows * kKRow;             // 9216
+  static constexpr int kSlot = kSlotK + kHeadDim * kVRow;  // 18432
+  static constexpr int kMinBlocks = 4;                     // launch bound (workgroups per CU)
+  struct Q {
+    uint4 r[2];  // query c, head_dim 8g..8g+7 and 32+8g..32+8g+7
+  };
+  struct Slot {
+    uint4 r[4];  // K rows tid>>3 and (tid>>3)+32 at column tid&7; V rows 2(tid&31), +1 at column tid>>5
+  };
+
+  static __device__ __forceinline__ void load_q(Q& q, __amdgpu_buffer_rsrc_t Qr, uint32_t row, int g) {
+    q.r[0] = bload16(Qr, row + 16 * g);
+    q.r[1] = bload16(Qr, row + 16 * g + 64);
+  }
+
+  static __device__ __forceinline__ void load_slot(Slot& s, __amdgpu_buffer_rsrc_t Kr, __amdgpu_buffer_rsrc_t Vr,
+                                                   uint32_t row_off, int tid, uint32_t tb) {
+    const uint32_t k = row_off + (tid >> 3) * tb + (tid & 7) * 16;
+    s.r[0] = bload16(Kr, k);
+    s.r[1] = bload16(Kr, k + 32 * tb);
+    const uint32_t v = row_off + 2 * (tid & 31) * tb + (tid >> 5) * 16;
+    s.r[2] = bload16(Vr, v);
+    s.r[3] = bload16(Vr, v + tb);
+  }
+
+  // V^T words: (key 2kp, key 2kp+1) pairs of one head_dim row, built with v_perm.
+  static __device__ __forceinline__ void store_slot(const Slot& s, uint8_t* slot, int tid) {
+    const int chk = tid & 7;
+    *reinterpret_cast<uint4*>(slot + (tid >> 3) * kKRow + 16 * chk) = s.r[0];
+    *reinterpret_cast<uint4*>(slot + ((tid >> 3) + 32) * kKRow + 16 * chk) = s.r[1];
+    const int kp = tid & 31, chv = tid >> 5;
+    const uint32_t w0[4] = {s.r[2].x, s.r[2].y, s.r[2].z, s.r[2].w};
+    const uint32_t w1[4] = {s.r[3].x, s.r[3].y, s.r[3].z, s.r[3].w};
+    uint8_t* col = slot + kSlotK + (8 * chv) * kVRow + 4 * kp;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      *reinterpret_cast<uint32_t*>(col + (2 * e) * kVRow) = __builtin_amdgcn_perm(w1[e], w0[e], 0x05040100u);
+      *reinterpret_cast<uint32_t*>(col + (2 * e + 1) * kVRow) = __builtin_amdgcn_perm(w1[e], w0[e], 0x07060302u);
+    }
+  }
+
+  // Lane byte offsets inside a slot, and of sub-tile u (16 keys) of a slot.
+  static __device__ __forceinline__ uint32_t k_lane(int c, int g) { return c * kKRow + 16 * g; }
+  static __device__ __forceinline__ uint32_t v_lane(int c, int g) {
+    return kSlotK + v_row_of_lane(c) * kVRow + 8 * g;
+  }
+  static constexpr uint32_t k_sub(int u) { return u * 16 * kKRow; }
+  static constexpr uint32_t v_sub(int u) { return u * 32; }
+
+  // S^T of 16 keys x this wave's 16 queries (raw dot products).
+  static __device__ __forceinline__ f32x4 qk(const uint8_t* kp, const Q& q) {
+    const uint4 a0 = *reinterpret_cast<const uint4*>(kp);
+    const uint4 a1 = *reinterpret_cast<const uint4*>(kp + 64);
+    f32x4 z = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    z = Mma<T>::qk(a0, q.r[0], z);
+    return Mma<T>::qk(a1, q.r[1], z);
+  }
+
+  // O^T += V^T P^T over the 16 keys whose probabilities this lane holds in p.
+  static __device__ __forceinline__ void pv(const uint8_t* vp, const float (&p)[4], f32x4 (&acc)[4]) {
+    uint2 pb;
+    pb.x = Mma<T>::pack2(p[0], p[1]);
+    pb.y = Mma<T>::pack2(p[2], p[3]);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const uint2 va = *reinterpret_cast<const uint2*>(vp + v_row_of_tile(dt) * kVRow);
+      acc[dt] = Mma<T>::pv(va, pb, acc[dt]);
+    }
+  }
+
+  static __device__ __forceinline__ void store_o(const f32x4 (&acc)[4], float inv, __amdgpu_buffer_rsrc_t Or,
+                                                 uint32_t row, int g) {
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const f32x4 a0 = acc[2 * half], a1 = acc[2 * half + 1];
+      uint4 ov;
+      ov.x = Mma<T>::pack2(a0[0] * inv, a0[1] * inv);
+      ov.y = Mma<T>::pack2(a0[2] * inv, a0[3] * inv);
+      ov.z = Mma<T>::pack2(a1[0] * inv, a1[1] * inv);
+      ov.w = Mma<T>::pack2(a1[2] * inv, a1[3] * inv);
+      bstore16(Or, row + 16 * g + 64 * half, ov);
+    }
+  }
+};
+
+// ---------------------------------------------------------------- fp32 path
+//
+// Both contractions on 16x16x4 fp32 MFMA, one contraction element per lane,
+// so neither operand needs a transpose.  Q.K^T: lane (c, g) holds head_dim
+// chunks g, g+4, g+8, g+12 (4 floats each) of key/query c.  P.V: the A operand
+// of MFMA (r, dt) is V[key 4g+r][16dt+c], and V rows are stored in LDS with
+// columns permuted to position 4*(d%16) + d/16 so that one 16 B read gives
+// dt = 0..3.  O^T tile dt row 4g+rr is O[c][16dt+4g+rr]: four 16 B stores.
+// Slots hold 32 keys (17 KB) so that a causal-64 ring is 4 slots = 68 KB.
+struct F32Path {
+  using Elt = float;
+  static constexpr int kRows = 32;
+  static constexpr int kKRow = 272;              // 256 + 16 pad
+  static constexpr int kVRow = 272;
+  static constexpr int kSlotK = kRows * kKRow;   // 8704
+  static constexpr int kSlot = 2 * kSlotK;       // 17408
+  static constexpr int kMinBlocks = 2;
+  struct Q {
+    uint4 r[4];  // query c, head_dim chunk g + 4j (j = 0..3)
+  };
+  struct Slot {
+    uint4 r[4];  // K row tid>>3 chunks tid&7 and (tid&7)+8; V row tid>>3, head_dim 32dp+4cb (+16)
+  };
+
+  static __device__ __forceinline__ void load_q(Q& q, __amdgpu_buffer_rsrc_t Qr, uint32_t row, int g) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) q.r[j] = bload16(Qr, row + 16 * (g + 4 * j));
+  }
+
+  static __device__ __forceinline__ void load_slot(Slot& s, __amdgpu_buffer_rsrc_t Kr, __amdgpu_buffer_rsrc_t Vr,
+                                                   uint32_t row_off, int tid, uint32_t tb) {
+    const uint32_t row = row_off + (tid >> 3) * tb;
+    s.r[0] = bload16(Kr, row + 16 * (tid & 7));
+    s.r[1] = bload16(Kr, row + 16 * (tid & 7) + 128);
+    const int cb = (tid >> 1) & 3, dp = tid & 1;
+    s.r[2] = bload16(Vr, row + 128 * dp + 16 * cb);       // head_dim 32dp + 4cb .. +3
+    s.r[3] = bload16(Vr, row + 128 * dp + 64 + 16 * cb);  // head_dim 32dp + 16 + 4cb .. +3
+  }
+
+  static __device__ __forceinline__ void store_slot(const Slot& s, uint8_t* slot, int tid) {
+    uint8_t* krow = slot + (tid >> 3) * kKRow;
+    *reinterpret_cast<uint4*>(krow + 16 * (tid & 7)) = s.r[0];
+    *reinterpret_cast<uint4*>(krow + 16 * (tid & 7) + 128) = s.r[1];
+    const int cb = (tid >> 1) & 3, dp = tid & 1;
+    uint8_t* vrow = slot + kSlotK + (tid >> 3) * kVRow + 8 * dp;
+    const uint32_t a[4] = {s.r[2].x, s.r[2].y, s.r[2].z, s.r[2].w};
+    const uint32_t b[4] = {s.r[3].x, s.r[3].y, s.r[3].z, s.r[3].w};
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc)
+      *reinterpret_cast<uint2*>(vrow + 16 * (4 * cb + cc)) = make_uint2(a[cc], b[cc]);
+  }
+
+  static __device__ __forceinline__ uint32_t k_lane(int c, int g) { return c * kKRow + 16 * g; }
+  static __device__ __forceinline__ uint32_t v_lane(int c, int g) { return kSlotK + 4 * g * kVRow + 16 * c; }
+  static constexpr uint32_t k_sub(int u) { return u * 16 * kKRow; }
+  static constexpr uint32_t v_sub(int u) { return u * 16 * kVRow; }
+
+  static __device__ __forceinline__ f32x4 qk(const uint8_t* kp, const Q& q) {
+    f32x4 z = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 a = __builtin_bit_cast(f32x4, *reinterpret_cast<const uint4*>(kp + 64 * j));
+      const f32x4 b = __builtin_bit_cast(f32x4, q.r[j]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) z = mfma_f32(a[r], b[r], z);
+    }
+    return z;
+  }
+
+  static __device__ __forceinline__ void pv(const uint8_t* vp, const float (&p)[4], f32x4 (&acc)[4]) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const f32x4 va = __builtin_bit_cast(f32x4, *reinterpret_cast<const uint4*>(vp + r * kVRow));
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) acc[dt] = mfma_f32(va[dt], p[r], acc[dt]);
+    }
+  }
+
+  static __device__ __forceinline__ void store_o(const f32x4 (&acc)[4], float inv, __amdgpu_buffer_rsrc_t Or,
+                                                 uint32_t row, int g) {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) bstore16(Or, row + 16 * g + 64 * dt, __builtin_bit_cast(uint4, acc[dt] * inv));
+  }
+};
+
+// ---------------------------------------------------------------- tiles
+
+// Ring location of sub-tile s (16 keys): slot s / (rows/16), sub-tile within it.
+template <class P, int NSLOT>
+__device__ __forceinline__ uint32_t ring_slot_bytes(int s) {
+  constexpr int kSubs = P::kRows / 16;
+  return (uint32_t)(((s / kSubs) % NSLOT) * P::kSlot);
+}
+
+// One wave's 16 queries qa..qa+15 (qa wave-uniform) against the ring, any
+// window (runtime left/right): scores on MFMA, softmax in registers (online
+// across groups of SG sub-tiles), P.V on MFMA, one store per O row.  Used for
+// tiles at the sequence edges and for windows without a fixed instantiation.
+// Rows >= Nr compute on zero Q rows and their stores fall outside the buffer.
+template <class P, int NSLOT, int SG>
+__device__ __forceinline__ void stream_tile(const uint8_t* ring, uint32_t kl, uint32_t vl, const typename P::Q& q,
+                                            int qa, int Nr, int L, int R, float sl2, __amdgpu_buffer_rsrc_t Or,
+                                            uint32_t orow, int g, int dl) {
+  constexpr int kSubs = P::kRows / 16;
+  const int sub_lo = max(floordiv32(qa - L, 16), 0);
+  const int sub_hi = min(floordiv32(qa + 15 + R, 16), (Nr - 1) >> 4);
+  const uint32_t span = (uint32_t)(L + R);
+  float m_run = -INFINITY, l_run = 0.0f;
+  f32x4 acc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = sub_lo; s0 <= sub_hi; s0 += SG) {
+    f32x4 sc[SG];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < SG; ++j) {
+      const int s = s0 + j;
+      if (s > sub_hi) break;
+      f32x4 z = P::qk(ring + ring_slot_bytes<P, NSLOT>(s) + P::k_sub(s % kSubs) + kl, q);
+      // key - query offsets of this sub-tile span [16s-qa-15, 16s-qa+15]
+      const int rel = 16 * s - qa;
+      if (rel - 15 < -L || rel + 15 > R) {
+        // element r: key - query + L = dl + rel + r, inside the window iff in [0, L+R]
+        const int x = dl + rel;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) z[r] = (uint32_t)(x + r) <= span ? z[r] : -INFINITY;
+      }
+      if (16 * s + 15 >= Nr) {
+        const int km = 16 * s + 4 * g;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) z[r] = km + r < Nr ? z[r] : -INFINITY;
+      }
+      sc[j] = z;
+      mx = fmaxf(mx, fmaxf(fmaxf(z[0], z[1]), fmaxf(z[2], z[3])));
+    }
+    const float m_new = fmaxf(m_run, col_max(mx));
+    // scores are raw dot products; the softmax scale is folded into exp2's argument
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new * sl2;
+    if (s0 != sub_lo) {  // rescale what earlier groups accumulated
+      const float corr = __builtin_amdgcn_exp2f(m_run * sl2 - m_use);
+      l_run *= corr;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) acc[dt] *= corr;
+    }
+    m_run = m_new;
+#pragma unroll
+    for (int j = 0; j < SG; ++j) {
+      const int s = s0 + j;
+      if (s > sub_hi) break;
+      float p[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[r] = __builtin_amdgcn_exp2f(fmaf(sc[j][r], sl2, -m_use));
+        l_run += p[r];
+      }
+      P::pv(ring + ring_slot_bytes<P, NSLOT>(s) + P::v_sub(s % kSubs) + vl, p, acc);
+    }
+  }
+  const float l_tot = col_sum(l_run);
+  P::store_o(acc, l_tot > 0.0f ? __builtin_amdgcn_rcpf(l_tot) : 0.0f, Or, orow, g);
+}
+
+// Compile-time geometry of a fixed window [i-L, i+R]: a wave's 16 queries at
+// qa = 16*(4t + wv) read sub-tiles s = 4t + wv - CL + j, j < NSUB, whose key -
+// query offsets 16*(j-CL) + [-15, 15] are the same for every interior tile.
+template <int L, int R, int RS>
+struct WinGeom {
+  static constexpr int CL = (L + 15) / 16;
+  static constexpr int NSUB = (15 + R) / 16 + CL + 1;
+  static constexpr int NSLOT = (63 + R) / RS + (L + RS - 1) / RS + 1;
+};
+
+// Interior tile of a fixed window: every sub-tile exists and lies before the
+// sequence end, so the whole tile is straight-line code: the sub-tile count,
+// which sub-tiles need a mask and the ring offsets are compile-time (up to the
+// tile's slot rotation), the per-lane mask compares are loop-invariant, and
+// the softmax is two-pass.
+template <class P, int L, int R>
+__device__ __forceinline__ void window_tile(const uint8_t* ring, uint32_t kl, uint32_t vl, const typename P::Q& q,
+                                            int t, int wv, float sl2, __amdgpu_buffer_rsrc_t Or, uint32_t orow,
+                                            int g, int dl) {
+  using G = WinGeom<L, R, P::kRows>;
+  constexpr int kSubs = P::kRows / 16;
+  f32x4 sc[G::NSUB];
+  uint32_t vaddr[G::NSUB];
+#pragma unroll
+  for (int j = 0; j < G::NSUB; ++j) {
+    const int u = wv + 3 * G::CL + j;  // s = 4(t - CL) + u, u >= 0
+    const int slot = ((t - G::CL) * (4 / kSubs) + u / kSubs) % G::NSLOT;
+    const uint32_t sb = (uint32_t)(slot * P::kSlot);
+    vaddr[j] = sb + P::v_sub(u % kSubs) + vl;
+    f32x4 z = P::qk(ring + sb + P::k_sub(u % kSubs) + kl, q);
+    const int rel = 16 * (j - G::CL);
+    if (rel - 15 < -L || rel + 15 > R) {  // resolved at compile time
+#pragma unroll
+      for (int r = 0; r < 4; ++r) z[r] = (uint32_t)(dl + rel + r) <= (uint32_t)(L + R) ? z[r] : -INFINITY;
+    }
+    sc[j] = z;
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < G::NSUB; ++j) mx = fmaxf(mx, fmaxf(fmaxf(sc[j][0], sc[j][1]), fmaxf(sc[j][2], sc[j][3])));
+  const float m_use = col_max(mx) * sl2;  // finite: every query sees its own key
+  float l_run = 0.0f;
+  f32x4 acc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < G::NSUB; ++j) {
+    float p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[r] = __builtin_amdgcn_exp2f(fmaf(sc[j][r], sl2, -m_use));
+      l_run += p[r];
+    }
+    P::pv(ring + vaddr[j], p, acc);
+  }
+  const float l_tot = col_sum(l_run);
+  P::store_o(acc, __builtin_amdgcn_rcpf(l_tot), Or, orow, g);
+}
+
+// ---------------------------------------------------------------- kernel
+//
+// FL/FR >= 0: specialised for window [i-FL, i+FR] (interior tiles take
+// window_tile); FL < 0: any window, every tile takes stream_tile.
+template <class P, int NSLOT, int SG, int FL, int FR>
+__global__ __launch_bounds__(256, P::kMinBlocks) void stream_kernel(StreamArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // NSLOT * P::kSlot bytes
+  using Elt = typename P::Elt;
+  constexpr bool kFixed = FL >= 0;
+  constexpr int FLc = FL < 0 ? 0 : FL, FRc = FR < 0 ? 0 : FR;
+  constexpr int RS = P::kRows;    // keys per slot
+  constexpr int SPS = 64 / RS;    // slots per 64-row step
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, kept in an SGPR
+  const int c = lane & 15;
+  const int g = lane >> 4;
+
+  int lin = blockIdx.x;
+  const int chunk_id = lin % a.chunks;
+  lin /= a.chunks;
+  const int rho = lin % a.dil;
+  lin /= a.dil;
+  const int h = lin % (int)a.H;
+  const int b = lin / (int)a.H;
+
+  const int Nr = (int)((a.N - rho + a.dil - 1) / a.dil);
+  const int tiles_r = (Nr + 63) >> 6;
+  const int t0 = chunk_id * a.chunk;
+  const int t1 = min(t0 + a.chunk, tiles_r);
+  if (t0 >= t1) return;  // uniform per workgroup, before any barrier
+  const int nblk = (Nr + RS - 1) / RS;  // ring slots' worth of keys in this residue class
+  const int L = kFixed ? FL : a.left;
+  const int R = kFixed ? FR : a.right;
+  const uint32_t tb = (uint32_t)a.tok_bytes;
+
+  // Buffer resources start at the first row this workgroup reads; their
+  // range ends with the residue class's last row.  Offsets below are bytes
+  // relative to base_row (the host checks they stay below 2^31).
+  const int blo0 = max(floordiv32(t0 * 64 - L, RS), 0);
+  const int base_row = blo0 * RS;
+  const int64_t base = (((int64_t)b * a.N + rho) * a.H + h) * kHeadDim + (int64_t)base_row * (tb / sizeof(Elt));
+  const int64_t range = (int64_t)(Nr - 1 - base_row) * tb + kHeadDim * sizeof(Elt);
+  const uint32_t nrec = (uint32_t)(range < 0x7FFFFFFF ? range : 0x7FFFFFFF);
+  const __amdgpu_buffer_rsrc_t Qr = make_rsrc(static_cast<const Elt*>(a.q) + base, nrec);
+  const __amdgpu_buffer_rsrc_t Kr = make_rsrc(static_cast<const Elt*>(a.k) + base, nrec);
+  const __amdgpu_buffer_rsrc_t Vr = make_rsrc(static_cast<const Elt*>(a.v) + base, nrec);
+  const __amdgpu_buffer_rsrc_t Or = make_rsrc(static_cast<const Elt*>(a.o) + base, nrec);
+
+  auto row_off = [&](int row) { return (uint32_t)(row - base_row) * tb; };
+  const uint32_t q_lane = (16 * wv + c) * tb;  // this lane's query row within a tile
+  const uint32_t kl = P::k_lane(c, g), vl = P::v_lane(c, g);
+  const int dl = 4 * g - c + L;  // key - query + L of accumulator element 0
+  // Interior tiles: wave 0's first sub-tile 4t - CL >= 0, and wave 3's last
+  // sub-tile 4t + 2 - CL + NSUB ends before Nr.
+  constexpr int kCL = kFixed ? WinGeom<FLc, FRc, RS>::CL : 0;
+  constexpr int kNSUB = kFixed ? WinGeom<FLc, FRc, RS>::NSUB : 0;
+  const int t_int_lo = (kCL + 3) >> 2;
+  const int t_int_hi = floordiv32(floordiv32(Nr - 16, 16) + kCL - 2 - kNSUB, 4) + 1;
+
+  // ---- prologue: Q rows of tile t0, the slots tile t0 reads, and tile
+  // t0+1's new rows
+  typename P::Q qc;
+  P::load_q(qc, Qr, row_off(t0 * 64) + q_lane, g);
+  const int bhi0 = floordiv32(t0 * 64 + 63 + R, RS);
+  const int top0 = min(bhi0, nblk - 1);
+  typename P::Slot X[SPS], Y[SPS];
+  {
+    typename P::Slot pre[NSLOT];
+#pragma unroll
+    for (int s = 0; s < NSLOT; ++s) P::load_slot(pre[s], Kr, Vr, blo0 + s <= top0 ? row_off((blo0 + s) * RS) : kOob, tid, tb);
+#pragma unroll
+    for (int i = 0; i < SPS; ++i) {
+      const int blk = bhi0 + 1 + i;
+      P::load_slot(X[i], Kr, Vr, t0 + 1 < t1 && blk < nblk ? row_off(blk * RS) : kOob, tid, tb);
+    }
+#pragma unroll
+    for (int s = 0; s < NSLOT; ++s)
+      if (blo0 + s <= top0) P::store_slot(pre[s], ring + ((blo0 + s) % NSLOT) * P::kSlot, tid);
+  }
+  __syncthreads();
+
+  // One pipeline step: tile t computes while tile t+1's Q rows and tile t+2's
+  // new K/V rows (into `nxt`) are in flight; tile t+1's rows (`cur`, loaded
+  // one step earlier) then replace the ring slots tile t was the last to read.
+  auto step = [&](int t, typename P::Slot(&cur)[SPS], typename P::Slot(&nxt)[SPS]) {
+    typename P::Q qn;
+    P::load_q(qn, Qr, (t + 1 < t1 ? row_off((t + 1) * 64) : kOob) + q_lane, g);
+    const int bh1 = floordiv32((t + 1) * 64 + 63 + R, RS);  // last slot of tile t+1
+#pragma unroll
+    for (int i = 0; i < SPS; ++i) {
+      const int blk = bh1 + 1 + i;
+      P::load_slot(nxt[i], Kr, Vr, t + 2 < t1 && blk < nblk ? row_off(blk * RS) : kOob, tid, tb);
+    }
+
+    const uint32_t orow = row_off(t * 64) + q_lane;
+    if (kFixed && t >= t_int_lo && t < t_int_hi)
+      window_tile<P, FLc, FRc>(ring, kl, vl, qc, t, wv, a.scale_log2, Or, orow, g, dl);
+    else
+      stream_tile<P, NSLOT, SG>(ring, kl, vl, qc, t * 64 + 16 * wv, Nr, L, R, a.scale_log2, Or, orow, g, dl);
+
+    const int bh0 = floordiv32(t * 64 + 63 + R, RS);  // last slot of tile t
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < SPS; ++i) {
+      const int blk = bh0 + 1 + i;
+      if (t + 1 < t1 && blk < nblk) P::store_slot(cur[i], ring + (blk % NSLOT) * P::kSlot, tid);
+    }
+    __syncthreads();
+    qc = qn;
+  };
+
+  for (int t = t0; t < t1; t += 2) {
+    step(t, X, Y);
+    if (t + 1 >= t1) break;
+    step(t + 1, Y, X);
+  }
+}
+
+}  // namespace ma_dev

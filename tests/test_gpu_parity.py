@@ -104,14 +104,14 @@ def test_forward_shapes_dtypes(ext, oracle, shape, W, dtype):
     assert _max_err(y, oracle.forward(spec, *up)) <= TOL[dtype]
 
 
-# ------------------------------------------------------- MFMA band kernel, random geometry
+# ------------------------------------------------------- streaming kernels, window / length / dilation geometry
 
 @pytest.mark.parametrize("N,left,right,dil", [
     (1, 63, 0, 1), (63, 63, 0, 1), (64, 63, 0, 1), (65, 63, 0, 1), (300, 63, 0, 1),
     (257, 32, 31, 1), (200, 64, 64, 1), (130, 0, 0, 1), (190, 5, 200, 1), (77, 300, 0, 1),
     (1000, 63, 0, 4), (999, 10, 3, 3), (500, 150, 150, 2), (129, 1, 1, 7),
 ])
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_band_kernel_geometry(ext, oracle, N, left, right, dil, dtype):
     shape = (2, N, 3, 64)
     (q, k, v), up = _inputs(shape, N + left + dil, dtype)
