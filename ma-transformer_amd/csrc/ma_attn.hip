@@ -31,6 +31,7 @@
 #include "device_common.h"
 #include "pattern.h"
 #include "stream_kernel.h"
+#include "block_kernel.h"
 
 namespace {
 
@@ -472,51 +473,74 @@ int launch_band(const ma_attn_desc* d, const void* q, const void* k, const void*
 }
 
 // Ring blocks a tile touches: floor((63+R)/64) - floor(-L/64) + 1.
-// Ring slots a tile touches for slots of `rows` keys:
-// floor((63+R)/rows) - floor(-L/rows) + 1.
-int64_t stream_slots(const ma_attn_desc* d, int rows) {
-  return ma::floordiv64(63 + d->right, rows) - ma::floordiv64(-d->left, rows) + 1;
-}
-
 constexpr int kMaxSlots = 6;  // generic instantiations (16-bit: 108 KB, fp32: 102 KB of LDS)
 constexpr int kStreamSG = 5;  // sub-tiles per softmax group (a causal-64 wave tile needs 5)
+
+// The banded problem a descriptor maps to on the stream kernel: window
+// [i-left, i+right] on residue classes of `dil`, plus G global tokens
+// (Longformer, dilation 1).
+struct StreamGeom {
+  int64_t left, right, dil, G;
+};
+
+bool stream_geom(const ma_attn_desc* d, StreamGeom* g) {
+  if (d->pattern == MA_ATTN_SLIDING) {
+    *g = StreamGeom{d->left, d->right, d->dilation, 0};
+    return true;
+  }
+  if (d->pattern == MA_ATTN_LONGFORMER) {
+    *g = StreamGeom{d->left, d->right, 1, ma::imin64(d->num_global, d->seq_len)};
+    return true;
+  }
+  return false;
+}
 
 // Work split of the stream kernel: `chunk` consecutive tiles per workgroup,
 // enough workgroups to give every CU as many as its LDS holds.
 struct StreamPlan {
-  int64_t rows, slot_bytes, max_per_cu, slots, tiles, chunk, chunks, wgs, tok_bytes;
+  StreamGeom geom;
+  int64_t rows, slot_bytes, max_per_cu, slots, lds, tiles, chunk, chunks, wgs, tok_bytes, partial_bytes;
 };
 
 StreamPlan stream_plan(const ma_attn_desc* d) {
   StreamPlan p;
+  stream_geom(d, &p.geom);
   const bool f32 = d->dtype == MA_ATTN_F32;
+  const bool lg = p.geom.G > 0;
   p.rows = f32 ? F32Path::kRows : HalfPath<__bf16>::kRows;
   p.slot_bytes = f32 ? F32Path::kSlot : HalfPath<__bf16>::kSlot;
   p.max_per_cu = f32 ? F32Path::kMinBlocks : HalfPath<__bf16>::kMinBlocks;
-  p.slots = stream_slots(d, (int)p.rows);
-  const int64_t nr_max = (d->seq_len + d->dilation - 1) / d->dilation;
+  p.slots = ma::floordiv64(63 + p.geom.right, p.rows) - ma::floordiv64(-p.geom.left, p.rows) + 1;
+  p.lds = (p.slots + (lg ? 1 : 0)) * p.slot_bytes;
+  const int64_t nr_max = (d->seq_len + p.geom.dil - 1) / p.geom.dil;
   p.tiles = (nr_max + 63) / 64;
-  const int64_t streams = d->batch * d->num_heads * d->dilation;
-  const int64_t per_cu = ma::imax64(1, ma::imin64(p.max_per_cu, (160 * 1024) / (p.slots * p.slot_bytes)));
+  const int64_t streams = d->batch * d->num_heads * p.geom.dil;
+  const int64_t per_cu = ma::imax64(1, ma::imin64(p.max_per_cu, (160 * 1024) / p.lds));
   const int64_t target = 256 * per_cu;
   p.chunk = ma::imax64(1, (streams * p.tiles + target - 1) / target);
   if (const char* e = getenv("MA_ATTN_STREAM_CHUNK")) p.chunk = ma::imax64(1, atoll(e));
   p.chunks = (p.tiles + p.chunk - 1) / p.chunk;
   p.wgs = streams * p.chunks;
-  p.tok_bytes = d->dilation * d->num_heads * kHeadDim * (f32 ? 4 : 2);
+  p.tok_bytes = p.geom.dil * d->num_heads * kHeadDim * (f32 ? 4 : 2);
+  p.partial_bytes = lg ? streams * p.chunks * 4 * 16 * kPartial * (int64_t)sizeof(float) : 0;
   return p;
 }
 
+constexpr int kMaxGlobal = 16;  // Longformer global tokens handled by the stream kernel
+
 bool stream_applies(const ma_attn_desc* d, const void* q, const void* k, const void* v, const void* o) {
-  if (d->pattern != MA_ATTN_SLIDING || d->head_dim != kHeadDim || d->left < 0 || d->right < 0) return false;
+  StreamGeom g;
+  if (!stream_geom(d, &g) || d->head_dim != kHeadDim || g.left < 0 || g.right < 0) return false;
+  if (g.G > 0 && (g.G > kMaxGlobal || d->dtype == MA_ATTN_F32)) return false;
   if (!(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o))) return false;
-  if (d->left > (1 << 20) || d->right > (1 << 20)) return false;
+  if (g.left > (1 << 20) || g.right > (1 << 20)) return false;
   const StreamPlan p = stream_plan(d);
-  if (p.slots < 1 || p.slots > kMaxSlots) return false;
+  if (p.slots < 1 || p.slots > kMaxSlots || p.lds > 160 * 1024) return false;
   if (p.wgs > (int64_t)INT32_MAX || p.tiles > (1 << 24)) return false;
   // Every buffer offset a workgroup forms is below
-  // (chunk*64 + left + right + 256 + rows*slots) rows past its first row.
-  const int64_t rows = p.chunk * 64 + d->left + d->right + 256 + p.rows * p.slots;
+  // (chunk*64 + left + right + 256 + rows*slots) rows past its first row
+  // (Longformer: past row 0).
+  const int64_t rows = (g.G > 0 ? d->seq_len : p.chunk * 64) + g.left + g.right + 256 + p.rows * p.slots;
   return p.tok_bytes < (1LL << 24) && rows * p.tok_bytes + 256 < (1LL << 31);
 }
 
@@ -525,10 +549,10 @@ const char* kernel_override() {
   return s ? s : "";
 }
 
-template <class P, int NSLOT, int FL, int FR>
+template <class P, int NSLOT, int FL, int FR, bool LG>
 int launch_stream_t(const StreamArgs& a, int64_t wgs, hipStream_t st) {
-  const size_t shm = (size_t)NSLOT * P::kSlot;
-  auto kern = &stream_kernel<P, NSLOT, kStreamSG, FL, FR>;
+  const size_t shm = (size_t)(NSLOT + (LG ? 1 : 0)) * P::kSlot;
+  auto kern = &stream_kernel<P, NSLOT, kStreamSG, FL, FR, LG>;
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -542,26 +566,47 @@ int launch_stream_t(const StreamArgs& a, int64_t wgs, hipStream_t st) {
 
 // Fixed-window instantiations (the BASELINE windows); other windows run the
 // generic kernel with `slots` ring slots.
-template <class P>
+template <class P, bool LG>
 int launch_stream_any(const StreamArgs& a, int64_t slots, int64_t wgs, hipStream_t st) {
   constexpr int RS = P::kRows;
   if (!getenv("MA_ATTN_NO_FIXED")) {
-    if (a.left == 63 && a.right == 0) return launch_stream_t<P, WinGeom<63, 0, RS>::NSLOT, 63, 0>(a, wgs, st);
-    if (a.left == 32 && a.right == 31) return launch_stream_t<P, WinGeom<32, 31, RS>::NSLOT, 32, 31>(a, wgs, st);
+    if constexpr (!LG) {
+      if (a.left == 63 && a.right == 0) return launch_stream_t<P, WinGeom<63, 0, RS>::NSLOT, 63, 0, LG>(a, wgs, st);
+      if (a.left == 32 && a.right == 31)
+        return launch_stream_t<P, WinGeom<32, 31, RS>::NSLOT, 32, 31, LG>(a, wgs, st);
+    } else {
+      if (a.left == 127 && a.right == 0)
+        return launch_stream_t<P, WinGeom<127, 0, RS>::NSLOT, 127, 0, LG>(a, wgs, st);
+    }
   }
   switch (slots) {
-    case 1: return launch_stream_t<P, 1, -1, -1>(a, wgs, st);
-    case 2: return launch_stream_t<P, 2, -1, -1>(a, wgs, st);
-    case 3: return launch_stream_t<P, 3, -1, -1>(a, wgs, st);
-    case 4: return launch_stream_t<P, 4, -1, -1>(a, wgs, st);
-    case 5: return launch_stream_t<P, 5, -1, -1>(a, wgs, st);
-    default: return launch_stream_t<P, 6, -1, -1>(a, wgs, st);
+    case 1: return launch_stream_t<P, 1, -1, -1, LG>(a, wgs, st);
+    case 2: return launch_stream_t<P, 2, -1, -1, LG>(a, wgs, st);
+    case 3: return launch_stream_t<P, 3, -1, -1, LG>(a, wgs, st);
+    case 4: return launch_stream_t<P, 4, -1, -1, LG>(a, wgs, st);
+    case 5: return launch_stream_t<P, 5, -1, -1, LG>(a, wgs, st);
+    default: return launch_stream_t<P, 6, -1, -1, LG>(a, wgs, st);
   }
 }
 
-int launch_stream(const ma_attn_desc* d, const void* q, const void* k, const void* v, void* o,
-                  hipStream_t st) {
+template <typename T>
+int launch_stream_half(const ma_attn_desc* d, const StreamArgs& a, const StreamPlan& p, hipStream_t st) {
+  using P = HalfPath<T>;
+  if (p.geom.G == 0) return launch_stream_any<P, false>(a, p.slots, p.wgs, st);
+  const int rc = launch_stream_any<P, true>(a, p.slots, p.wgs, st);
+  if (rc) return rc;
+  hipLaunchKernelGGL(longformer_combine<T>, dim3((unsigned)(d->batch * d->num_heads * p.geom.G)), dim3(64), 0, st,
+                     a.partials, static_cast<T*>(a.o), (int)(p.chunks * 4), (int)p.geom.G, (int)d->num_heads,
+                     d->seq_len);
+  return 0;
+}
+
+int launch_stream(const ma_attn_desc* d, const void* q, const void* k, const void* v, void* o, void* ws,
+                  size_t ws_bytes, hipStream_t st) {
   const StreamPlan p = stream_plan(d);
+  if ((int64_t)ws_bytes < p.partial_bytes || (p.partial_bytes > 0 && !ws))
+    return fail("ma_attn: workspace of %lld bytes required (ma_attn_workspace_size), got %zu",
+                (long long)p.partial_bytes, ws_bytes);
   StreamArgs a;
   a.q = q;
   a.k = k;
@@ -569,19 +614,51 @@ int launch_stream(const ma_attn_desc* d, const void* q, const void* k, const voi
   a.o = o;
   a.N = d->seq_len;
   a.H = d->num_heads;
-  a.left = (int32_t)d->left;
-  a.right = (int32_t)d->right;
-  a.dil = (int32_t)d->dilation;
+  a.left = (int32_t)p.geom.left;
+  a.right = (int32_t)p.geom.right;
+  a.dil = (int32_t)p.geom.dil;
   a.tiles = (int32_t)p.tiles;
   a.chunk = (int32_t)p.chunk;
   a.chunks = (int32_t)p.chunks;
   a.tok_bytes = (int32_t)p.tok_bytes;
   a.scale_log2 = scale_of(d) * 1.4426950408889634f;
+  a.num_global = (int32_t)p.geom.G;
+  a.partials = static_cast<float*>(ws);
   switch (d->dtype) {
-    case MA_ATTN_BF16: return launch_stream_any<HalfPath<__bf16>>(a, p.slots, p.wgs, st);
-    case MA_ATTN_F16: return launch_stream_any<HalfPath<_Float16>>(a, p.slots, p.wgs, st);
-    default: return launch_stream_any<F32Path>(a, p.slots, p.wgs, st);
+    case MA_ATTN_BF16: return launch_stream_half<__bf16>(d, a, p, st);
+    case MA_ATTN_F16: return launch_stream_half<_Float16>(d, a, p, st);
+    default: return launch_stream_any<F32Path, false>(a, p.slots, p.wgs, st);
   }
+}
+
+// Block-sparse on MFMA: block size 64, head_dim 64, 16-bit.
+bool block_applies(const ma_attn_desc* d, const void* q, const void* k, const void* v, const void* o) {
+  if (d->pattern != MA_ATTN_BLOCK_SPARSE || d->block_size != 64 || d->head_dim != kHeadDim) return false;
+  if (d->dtype != MA_ATTN_BF16 && d->dtype != MA_ATTN_F16) return false;
+  if (!(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o))) return false;
+  const int64_t tb = d->num_heads * kHeadDim * 2;
+  const int64_t nbq = (d->seq_len + 63) / 64;
+  return (d->seq_len + 128) * tb < (1LL << 31) && d->batch * d->num_heads * nbq <= (int64_t)INT32_MAX;
+}
+
+int launch_block(const ma_attn_desc* d, const void* q, const void* k, const void* v, void* o, hipStream_t st) {
+  BlockArgs a;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.table = d->block_table;
+  a.N = (int32_t)d->seq_len;
+  a.H = (int32_t)d->num_heads;
+  a.bpr = (int32_t)d->blocks_per_row;
+  a.nbq = (int32_t)((d->seq_len + 63) / 64);
+  a.scale_log2 = scale_of(d) * 1.4426950408889634f;
+  const int64_t wgs = d->batch * d->num_heads * a.nbq;
+  if (d->dtype == MA_ATTN_BF16)
+    hipLaunchKernelGGL(block_kernel<HalfPath<__bf16>>, dim3((unsigned)wgs), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(block_kernel<HalfPath<_Float16>>, dim3((unsigned)wgs), dim3(256), 0, st, a);
+  return 0;
 }
 
 uint64_t splitmix64(uint64_t* s) {
@@ -605,14 +682,19 @@ int ma_attn_validate(const ma_attn_desc* desc) {
 }
 
 size_t ma_attn_workspace_size(const ma_attn_desc* desc) {
-  (void)desc;
-  return 0;
+  g_last_error.clear();
+  if (validate(desc)) return 0;
+  if (desc->pattern != MA_ATTN_LONGFORMER || desc->head_dim != kHeadDim || desc->dtype == MA_ATTN_F32) return 0;
+  if (desc->batch * desc->seq_len * desc->num_heads == 0) return 0;
+  // the size the stream kernel needs whenever it may take this descriptor
+  // (pointer alignment is not known here; 16-byte-aligned tensors are assumed)
+  static const char dummy[16] __attribute__((aligned(16))) = {0};
+  if (!stream_applies(desc, dummy, dummy, dummy, dummy)) return 0;
+  return (size_t)stream_plan(desc).partial_bytes;
 }
 
 int ma_attn_forward(const ma_attn_desc* desc, const void* q, const void* k, const void* v, void* o,
                     void* workspace, size_t workspace_bytes, void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   g_last_error.clear();
   if (validate(desc)) return 1;
   const int64_t rows = desc->batch * desc->seq_len * desc->num_heads;
@@ -625,7 +707,9 @@ int ma_attn_forward(const ma_attn_desc* desc, const void* q, const void* k, cons
   const bool want_rows = strcmp(force, "rows") == 0;
   const bool want_band = strcmp(force, "band") == 0;
   if (!want_rows && !want_band && stream_applies(desc, q, k, v, o)) {
-    rc = launch_stream(desc, q, k, v, o, st);
+    rc = launch_stream(desc, q, k, v, o, workspace, workspace_bytes, st);
+  } else if (!want_rows && block_applies(desc, q, k, v, o)) {
+    rc = launch_block(desc, q, k, v, o, st);
   } else if (!want_rows && band_applies(desc, q, k, v, o)) {
     rc = launch_band(desc, q, k, v, o, st);
   } else {

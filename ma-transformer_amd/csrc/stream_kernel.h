@@ -43,7 +43,13 @@ struct StreamArgs {
   int32_t chunks;     // ceil(tiles / chunk)
   int32_t tok_bytes;  // bytes between consecutive rows of a residue class (dil * H * 64 * elt)
   float scale_log2;   // softmax scale * log2(e)
+  int32_t num_global;  // Longformer: global tokens 0..G-1 (G <= 16)
+  float* partials;     // Longformer: [B*H][chunks*4][16][kPartial] per-wave softmax partials of the global rows
 };
+
+// One partial of a global query row: unnormalised O (64), running max of the
+// log2-scaled scores, and the softmax denominator.
+constexpr int kPartial = kHeadDim + 2;
 
 // ---------------------------------------------------------------- 16-bit path
 //
@@ -128,6 +134,15 @@ struct HalfPath {
     for (int dt = 0; dt < 4; ++dt) {
       const uint2 va = *reinterpret_cast<const uint2*>(vp + v_row_of_tile(dt) * kVRow);
       acc[dt] = Mma<T>::pv(va, pb, acc[dt]);
+    }
+  }
+
+  // Unnormalised accumulators of query c as floats into its 64-float row.
+  static __device__ __forceinline__ void store_acc(const f32x4 (&acc)[4], float* row, int g) {
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      *reinterpret_cast<f32x4*>(row + 32 * half + 8 * g) = acc[2 * half];
+      *reinterpret_cast<f32x4*>(row + 32 * half + 8 * g + 4) = acc[2 * half + 1];
     }
   }
 
@@ -224,6 +239,11 @@ struct F32Path {
     }
   }
 
+  static __device__ __forceinline__ void store_acc(const f32x4 (&acc)[4], float* row, int g) {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) *reinterpret_cast<f32x4*>(row + 16 * dt + 4 * g) = acc[dt];
+  }
+
   static __device__ __forceinline__ void store_o(const f32x4 (&acc)[4], float inv, __amdgpu_buffer_rsrc_t Or,
                                                  uint32_t row, int g) {
 #pragma unroll
@@ -245,18 +265,33 @@ __device__ __forceinline__ uint32_t ring_slot_bytes(int s) {
 // across groups of SG sub-tiles), P.V on MFMA, one store per O row.  Used for
 // tiles at the sequence edges and for windows without a fixed instantiation.
 // Rows >= Nr compute on zero Q rows and their stores fall outside the buffer.
-template <class P, int NSLOT, int SG>
+template <class P, int NSLOT, int SG, bool LG>
 __device__ __forceinline__ void stream_tile(const uint8_t* ring, uint32_t kl, uint32_t vl, const typename P::Q& q,
                                             int qa, int Nr, int L, int R, float sl2, __amdgpu_buffer_rsrc_t Or,
-                                            uint32_t orow, int g, int dl) {
+                                            uint32_t orow, int g, int dl, int G) {
   constexpr int kSubs = P::kRows / 16;
-  const int sub_lo = max(floordiv32(qa - L, 16), 0);
+  int sub_lo = max(floordiv32(qa - L, 16), 0);
   const int sub_hi = min(floordiv32(qa + 15 + R, 16), (Nr - 1) >> 4);
   const uint32_t span = (uint32_t)(L + R);
   float m_run = -INFINITY, l_run = 0.0f;
   f32x4 acc[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (LG) {
+    // Longformer global keys 0..G-1: sub-tile 0 of the slot after the ring
+    f32x4 z = P::qk(ring + NSLOT * P::kSlot + kl, q);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) z[r] = 4 * g + r < G ? z[r] : -INFINITY;
+    m_run = col_max(fmaxf(fmaxf(z[0], z[1]), fmaxf(z[2], z[3])));
+    const float m_use = m_run * sl2;  // finite: G >= 1
+    float p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[r] = __builtin_amdgcn_exp2f(fmaf(z[r], sl2, -m_use));
+      l_run += p[r];
+    }
+    P::pv(ring + NSLOT * P::kSlot + vl, p, acc);
+  }
   for (int s0 = sub_lo; s0 <= sub_hi; s0 += SG) {
     f32x4 sc[SG];
     float mx = -INFINITY;
@@ -278,13 +313,18 @@ __device__ __forceinline__ void stream_tile(const uint8_t* ring, uint32_t kl, ui
 #pragma unroll
         for (int r = 0; r < 4; ++r) z[r] = km + r < Nr ? z[r] : -INFINITY;
       }
+      if (LG && 16 * s < G) {  // window keys below G are already counted as global keys
+        const int km = 16 * s + 4 * g;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) z[r] = km + r >= G ? z[r] : -INFINITY;
+      }
       sc[j] = z;
       mx = fmaxf(mx, fmaxf(fmaxf(z[0], z[1]), fmaxf(z[2], z[3])));
     }
     const float m_new = fmaxf(m_run, col_max(mx));
     // scores are raw dot products; the softmax scale is folded into exp2's argument
     const float m_use = m_new == -INFINITY ? 0.0f : m_new * sl2;
-    if (s0 != sub_lo) {  // rescale what earlier groups accumulated
+    if (LG || s0 != sub_lo) {  // rescale what earlier groups accumulated
       const float corr = __builtin_amdgcn_exp2f(m_run * sl2 - m_use);
       l_run *= corr;
 #pragma unroll
@@ -323,14 +363,22 @@ struct WinGeom {
 // which sub-tiles need a mask and the ring offsets are compile-time (up to the
 // tile's slot rotation), the per-lane mask compares are loop-invariant, and
 // the softmax is two-pass.
-template <class P, int L, int R>
+template <class P, int L, int R, bool LG>
 __device__ __forceinline__ void window_tile(const uint8_t* ring, uint32_t kl, uint32_t vl, const typename P::Q& q,
                                             int t, int wv, float sl2, __amdgpu_buffer_rsrc_t Or, uint32_t orow,
-                                            int g, int dl) {
+                                            int g, int dl, int ng) {
   using G = WinGeom<L, R, P::kRows>;
   constexpr int kSubs = P::kRows / 16;
   f32x4 sc[G::NSUB];
   uint32_t vaddr[G::NSUB];
+  f32x4 zg = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float mx = -INFINITY;
+  if (LG) {  // Longformer global keys 0..ng-1 (interior tiles: no window key is below ng)
+    zg = P::qk(ring + G::NSLOT * P::kSlot + kl, q);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) zg[r] = 4 * g + r < ng ? zg[r] : -INFINITY;
+    mx = fmaxf(fmaxf(zg[0], zg[1]), fmaxf(zg[2], zg[3]));
+  }
 #pragma unroll
   for (int j = 0; j < G::NSUB; ++j) {
     const int u = wv + 3 * G::CL + j;  // s = 4(t - CL) + u, u >= 0
@@ -345,7 +393,6 @@ __device__ __forceinline__ void window_tile(const uint8_t* ring, uint32_t kl, ui
     }
     sc[j] = z;
   }
-  float mx = -INFINITY;
 #pragma unroll
   for (int j = 0; j < G::NSUB; ++j) mx = fmaxf(mx, fmaxf(fmaxf(sc[j][0], sc[j][1]), fmaxf(sc[j][2], sc[j][3])));
   const float m_use = col_max(mx) * sl2;  // finite: every query sees its own key
@@ -353,6 +400,15 @@ __device__ __forceinline__ void window_tile(const uint8_t* ring, uint32_t kl, ui
   f32x4 acc[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (LG) {
+    float p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[r] = __builtin_amdgcn_exp2f(fmaf(zg[r], sl2, -m_use));
+      l_run += p[r];
+    }
+    P::pv(ring + G::NSLOT * P::kSlot + vl, p, acc);
+  }
 #pragma unroll
   for (int j = 0; j < G::NSUB; ++j) {
     float p[4];
@@ -371,9 +427,15 @@ __device__ __forceinline__ void window_tile(const uint8_t* ring, uint32_t kl, ui
 //
 // FL/FR >= 0: specialised for window [i-FL, i+FR] (interior tiles take
 // window_tile); FL < 0: any window, every tile takes stream_tile.
-template <class P, int NSLOT, int SG, int FL, int FR>
-__global__ __launch_bounds__(256, P::kMinBlocks) void stream_kernel(StreamArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // NSLOT * P::kSlot bytes
+//
+// LG: Longformer (dilation 1): every query also attends the global keys
+// 0..G-1 (G <= 16, held in the slot after the ring, window keys below G
+// masked so no key counts twice), and each wave folds one 16-key sub-tile of
+// every tile into an online softmax for the global query rows 0..G-1, written
+// as one partial per wave for longformer_combine.
+template <class P, int NSLOT, int SG, int FL, int FR, bool LG>
+__global__ __launch_bounds__(256, LG ? 2 : P::kMinBlocks) void stream_kernel(StreamArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // (NSLOT + LG) * P::kSlot bytes
   using Elt = typename P::Elt;
   constexpr bool kFixed = FL >= 0;
   constexpr int FLc = FL < 0 ? 0 : FL, FRc = FR < 0 ? 0 : FR;
@@ -408,7 +470,7 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void stream_kernel(StreamArgs a
   // range ends with the residue class's last row.  Offsets below are bytes
   // relative to base_row (the host checks they stay below 2^31).
   const int blo0 = max(floordiv32(t0 * 64 - L, RS), 0);
-  const int base_row = blo0 * RS;
+  const int base_row = LG ? 0 : blo0 * RS;  // Longformer also reads rows 0..G-1
   const int64_t base = (((int64_t)b * a.N + rho) * a.H + h) * kHeadDim + (int64_t)base_row * (tb / sizeof(Elt));
   const int64_t range = (int64_t)(Nr - 1 - base_row) * tb + kHeadDim * sizeof(Elt);
   const uint32_t nrec = (uint32_t)(range < 0x7FFFFFFF ? range : 0x7FFFFFFF);
@@ -425,7 +487,7 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void stream_kernel(StreamArgs a
   // sub-tile 4t + 2 - CL + NSUB ends before Nr.
   constexpr int kCL = kFixed ? WinGeom<FLc, FRc, RS>::CL : 0;
   constexpr int kNSUB = kFixed ? WinGeom<FLc, FRc, RS>::NSUB : 0;
-  const int t_int_lo = (kCL + 3) >> 2;
+  const int t_int_lo = (kCL + (LG ? 4 : 3)) >> 2;  // Longformer: no window sub-tile below key 16
   const int t_int_hi = floordiv32(floordiv32(Nr - 16, 16) + kCL - 2 - kNSUB, 4) + 1;
 
   // ---- prologue: Q rows of tile t0, the slots tile t0 reads, and tile
@@ -448,7 +510,19 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void stream_kernel(StreamArgs a
     for (int s = 0; s < NSLOT; ++s)
       if (blo0 + s <= top0) P::store_slot(pre[s], ring + ((blo0 + s) % NSLOT) * P::kSlot, tid);
   }
+  typename P::Q qg;  // Longformer: Q rows of the global queries (query c of every wave)
+  if (LG) {
+    typename P::Slot gs;
+    P::load_slot(gs, Kr, Vr, row_off(0), tid, tb);
+    P::store_slot(gs, ring + NSLOT * P::kSlot, tid);
+    P::load_q(qg, Qr, row_off(0) + c * tb, g);
+  }
   __syncthreads();
+  const int G = LG ? a.num_global : 0;
+  float mg = -INFINITY, lg = 0.0f;  // Longformer global rows: this wave's softmax partial
+  f32x4 accg[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) accg[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   // One pipeline step: tile t computes while tile t+1's Q rows and tile t+2's
   // new K/V rows (into `nxt`) are in flight; tile t+1's rows (`cur`, loaded
@@ -465,9 +539,33 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void stream_kernel(StreamArgs a
 
     const uint32_t orow = row_off(t * 64) + q_lane;
     if (kFixed && t >= t_int_lo && t < t_int_hi)
-      window_tile<P, FLc, FRc>(ring, kl, vl, qc, t, wv, a.scale_log2, Or, orow, g, dl);
+      window_tile<P, FLc, FRc, LG>(ring, kl, vl, qc, t, wv, a.scale_log2, Or, orow, g, dl, G);
     else
-      stream_tile<P, NSLOT, SG>(ring, kl, vl, qc, t * 64 + 16 * wv, Nr, L, R, a.scale_log2, Or, orow, g, dl);
+      stream_tile<P, NSLOT, SG, LG>(ring, kl, vl, qc, t * 64 + 16 * wv, Nr, L, R, a.scale_log2, Or, orow, g, dl,
+                                    G);
+    if (LG) {  // global query rows against keys 64t + 16wv .. +15 (in the ring at tile t)
+      const int key0 = t * 64 + 16 * wv;
+      constexpr int kSubs = RS / 16;
+      f32x4 z = P::qk(ring + ring_slot_bytes<P, NSLOT>(key0 / 16) + P::k_sub((key0 / 16) % kSubs) + kl, qg);
+      if (key0 + 15 >= Nr) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) z[r] = key0 + 4 * g + r < Nr ? z[r] : -INFINITY;
+      }
+      const float m_new = fmaxf(mg, col_max(fmaxf(fmaxf(z[0], z[1]), fmaxf(z[2], z[3]))));
+      const float m_use = m_new == -INFINITY ? 0.0f : m_new * a.scale_log2;
+      const float corr = __builtin_amdgcn_exp2f(mg * a.scale_log2 - m_use);
+      lg *= corr;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) accg[dt] *= corr;
+      mg = m_new;
+      float p[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[r] = __builtin_amdgcn_exp2f(fmaf(z[r], a.scale_log2, -m_use));
+        lg += p[r];
+      }
+      P::pv(ring + ring_slot_bytes<P, NSLOT>(key0 / 16) + P::v_sub((key0 / 16) % kSubs) + vl, p, accg);
+    }
 
     const int bh0 = floordiv32(t * 64 + 63 + R, RS);  // last slot of tile t
     __syncthreads();
@@ -485,6 +583,41 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void stream_kernel(StreamArgs a
     if (t + 1 >= t1) break;
     step(t + 1, Y, X);
   }
+
+  if (LG) {  // this wave's partial for global query c: [64 unnormalised O][log2-scaled max][denominator]
+    const float l_tot = col_sum(lg);
+    float* dst = a.partials + ((((int64_t)b * a.H + h) * a.chunks + chunk_id) * 4 + wv) * 16 * kPartial + c * kPartial;
+    P::store_acc(accg, dst, g);
+    if (g == 0) {
+      dst[kHeadDim] = mg == -INFINITY ? -INFINITY : mg * a.scale_log2;
+      dst[kHeadDim + 1] = l_tot;
+    }
+  }
+}
+
+// Global query rows of Longformer: merge the per-wave partials of every chunk
+// (log-sum-exp combine) into O rows 0..G-1.  One workgroup of 64 threads
+// (one per head_dim element) per (batch, head, global row).
+template <typename Elt>
+__global__ __launch_bounds__(64) void longformer_combine(const float* __restrict__ partials, Elt* __restrict__ o,
+                                                         int nparts, int G, int H, int64_t N) {
+  const int d = threadIdx.x;
+  const int gq = blockIdx.x % G;
+  const int bh = blockIdx.x / G;  // b * H + h
+  const int h = bh % H;
+  const int b = bh / H;
+  float m = -INFINITY, l = 0.0f, acc = 0.0f;
+  for (int p = 0; p < nparts; ++p) {
+    const float* src = partials + (((int64_t)bh * nparts + p) * 16 + gq) * kPartial;
+    const float mp = src[kHeadDim];
+    if (mp == -INFINITY) continue;
+    const float mn = fmaxf(m, mp);
+    const float ca = __builtin_amdgcn_exp2f(m - mn), cb = __builtin_amdgcn_exp2f(mp - mn);
+    l = l * ca + src[kHeadDim + 1] * cb;
+    acc = acc * ca + src[d] * cb;
+    m = mn;
+  }
+  o[(((int64_t)b * N + gq) * H + h) * kHeadDim + d] = static_cast<Elt>(l > 0.0f ? acc / l : 0.0f);
 }
 
 }  // namespace ma_dev

@@ -123,10 +123,14 @@ def block_sparse_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Te
     tab_cpu = block_table.detach().to("cpu", torch.int32)
     if tab_cpu.numel() and ((tab_cpu >= nb).any() or (tab_cpu < -1).any()):
         raise RuntimeError("block_table entries must be -1 or in [0, num_blocks)")
-    srt = tab_cpu.clone()
-    srt[srt < 0] = torch.iinfo(torch.int32).max
-    if tab_cpu.numel() and (torch.diff(srt, dim=1) <= 0).any():
-        raise RuntimeError("block_table rows must be strictly ascending with -1 padding last")
+    if tab_cpu.numel():
+        valid = tab_cpu >= 0
+        # padding last: once an entry is -1, every later entry of the row is -1
+        if (valid[:, 1:] & ~valid[:, :-1]).any():
+            raise RuntimeError("block_table rows must hold their -1 padding after the valid entries")
+        # strictly ascending among valid entries
+        if ((tab_cpu[:, 1:] <= tab_cpu[:, :-1]) & valid[:, 1:]).any():
+            raise RuntimeError("block_table rows must be strictly ascending")
     # Allocated on the current stream; the caching allocator reuses its memory
     # only for later work on that same stream, i.e. after the kernel read it.
     tab = tab_cpu.to(query.device).contiguous()

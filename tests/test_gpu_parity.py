@@ -120,6 +120,54 @@ def test_band_kernel_geometry(ext, oracle, N, left, right, dil, dtype):
     assert _max_err(y, oracle.forward(spec, *up)) <= TOL[dtype]
 
 
+# ------------------------------------------------------- block-sparse and Longformer kernels
+
+def _random_table(nb, width, seed, rng_extra_pad=True):
+    """Ascending, -1 padded block table with 1..width valid entries per row."""
+    rng = np.random.default_rng(seed)
+    tab = np.full((nb, width), -1, dtype=np.int32)
+    for r in range(nb):
+        n = int(rng.integers(1, width + 1)) if rng_extra_pad else width
+        n = min(n, nb)
+        tab[r, :n] = np.sort(rng.choice(nb, size=n, replace=False))
+    return tab
+
+
+@pytest.mark.parametrize("N", [64, 65, 200, 1000])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_block_sparse_geometry(ext, oracle, N, dtype):
+    shape = (2, N, 3, 64)
+    (q, k, v), up = _inputs(shape, 500 + N, dtype, scale=0.5)
+    nb = (N + 63) // 64
+    for tab in (ext.make_block_table(77 + N, nb, 2).numpy(), _random_table(nb, 5, N)):
+        y = ext.block_sparse_forward(q, k, v, torch.from_numpy(tab), 64)
+        spec = oracle.Spec(*shape, pattern="block_sparse", block_size=64, table=tab)
+        assert _max_err(y, oracle.forward(spec, *up)) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("N,G,left,right", [
+    (16, 16, 127, 0), (17, 16, 127, 0), (100, 5, 127, 0), (300, 16, 127, 0), (1000, 16, 127, 0),
+    (257, 1, 3, 0), (300, 7, 20, 9), (130, 16, 200, 0), (500, 3, 64, 64), (10, 4, 2, 1),
+])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_longformer_geometry(ext, oracle, N, G, left, right, dtype):
+    shape = (2, N, 3, 64)
+    (q, k, v), up = _inputs(shape, 900 + N + G, dtype)
+    y = ext.longformer_forward(q, k, v, left, right, G)
+    spec = oracle.Spec(*shape, pattern="longformer", left=left, right=right, num_global=G)
+    assert _max_err(y, oracle.forward(spec, *up)) <= TOL[dtype]
+
+
+def test_block_table_validation(ext):
+    q = torch.randn(1, 128, 1, 64, device="cuda", dtype=torch.bfloat16)
+    ok = torch.tensor([[0, -1, -1], [0, 1, -1]], dtype=torch.int32)
+    ext.block_sparse_forward(q, q, q, ok, 64)  # multiple -1 pads are fine
+    for bad in ([[1, 0, -1], [0, 1, -1]], [[-1, 0, -1], [0, 1, -1]], [[0, 2, -1], [0, 1, -1]],
+                [[0, 0, -1], [0, 1, -1]]):
+        with pytest.raises(RuntimeError):
+            ext.block_sparse_forward(q, q, q, torch.tensor(bad, dtype=torch.int32), 64)
+
+
 # ------------------------------------------------------- BASELINE configs
 
 def test_cfg1_causal_fp32(ext, oracle):
