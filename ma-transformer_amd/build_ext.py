@@ -14,7 +14,9 @@ import sys
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
 SRC = os.path.join(PKG_DIR, "csrc", "ma_attn.hip")
-HEADERS = [os.path.join(PKG_DIR, "csrc", "pattern.h"), os.path.join(REPO_DIR, "include", "ma_attn.h")]
+HEADERS = [os.path.join(PKG_DIR, "csrc", h) for h in ("pattern.h", "device_common.h", "stream_kernel.h",
+                                                         "block_kernel.h")] + \
+    [os.path.join(REPO_DIR, "include", "ma_attn.h")]
 LIB = os.path.join(PKG_DIR, "libma_attn.so")
 ARCH = os.environ.get("MA_ATTN_ARCH", "gfx950")
 
