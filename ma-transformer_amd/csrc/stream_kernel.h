@@ -437,6 +437,7 @@ __device__ __forceinline__ void window_tile(const uint8_t* ring, uint32_t kl, ui
 }
 
 // ---------------------------------------------------------------- kernel
+
 //
 // FL/FR >= 0: specialised for window [i-FL, i+FR] (interior tiles take
 // window_tile); FL < 0: any window, every tile takes stream_tile.
@@ -461,6 +462,11 @@ __global__ __launch_bounds__(256, LG ? 2 : P::kMinBlocks) void stream_kernel(Str
   const int c = lane & 15;
   const int g = lane >> 4;
 
+  // Workgroup order: chunk fastest.  The dispatcher deals ids to the 8 XCDs
+  // round-robin, so every XCD holds every head and chunks spread over the
+  // whole sequence.  Orders that give an XCD one head, or one contiguous token
+  // range, measured 17-30 % slower on the target (HBM channel locality);
+  // hashed orders measured the same as this one.
   int lin = blockIdx.x;
   const int chunk_id = lin % a.chunks;
   lin /= a.chunks;
