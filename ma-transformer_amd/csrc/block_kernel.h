@@ -1,15 +1,20 @@
 // block_kernel.h -- block-sparse attention forward (block size 64, head_dim
 // 64, bf16/fp16) on MFMA.
 //
-// One workgroup (4 waves) per (batch, head, query block r): its 64 queries
-// attend the key blocks listed in row r of the block table (ascending, -1
-// padded), each a dense 64x64 block product.  Key blocks pass through a
-// two-slot LDS ring (K row major, V transposed, the 16-bit stream layout):
-// block e+1 is in flight into registers while block e computes, and is
-// written into the other slot once block e is done.  Softmax is online
-// across blocks, in registers; one O store per row.  Loads and stores go
-// through range-checked buffer resources over the (batch, head) stream, so
-// a ragged last block reads zero rows (masked) and its stores are dropped.
+// Query block r attends the key blocks listed in row r of the block table
+// (ascending, -1 padded), each a dense 64x64 block product on MFMA.  One
+// workgroup (4 waves, 16 queries each) per (batch, head, query block).  Key
+// blocks pass through a two-slot LDS ring (K row major, V transposed: the
+// 16-bit stream layout): block e+1 is in flight into registers while block e
+// computes.  Softmax is online across a row's blocks, in registers; one O
+// store per row.  Loads and stores go through range-checked buffer resources
+// over the (batch, head) stream, so a ragged last block reads zero rows
+// (masked) and its stores are dropped.
+//
+// Measured alternatives that did not pay on the 4-wide BASELINE table: a
+// workgroup walking a run of consecutive rows with two blocks in flight
+// (the same time at best, slower with more rows per run), because a row's
+// time is not its load latency alone.
 #pragma once
 
 #include "stream_kernel.h"
@@ -21,13 +26,67 @@ struct BlockArgs {
   const void* k;
   const void* v;
   void* o;
-  const int32_t* table;  // [ceil(N/64), bpr]
+  const int32_t* table;  // [nbq, bpr]
   int32_t N, H, bpr, nbq;
   float scale_log2;
 };
 
+// Workgroups are dispatched round-robin over the 8 XCDs, each with its own
+// L2.  Renumbering so that XCD x runs rows [x*G/8, (x+1)*G/8) in order puts
+// row r and row r+1 (which read block r as diagonal and as previous) and a
+// head's random blocks on one L2.  Bijective: the first 8*(G/8) ids are
+// permuted, the rest keep their number.
+__device__ __forceinline__ int xcd_row_order(int bid, int G) {
+  const int per = G >> 3;
+  return bid < (per << 3) ? (bid & 7) * per + (bid >> 3) : bid;
+}
+
+// Online-softmax update of one 64-key block (4 sub-tiles) from an LDS slot.
+// cb < 0: an absent entry, every score masked.
 template <class P>
-__global__ __launch_bounds__(256, P::kMinBlocks) void block_kernel(BlockArgs a) {
+__device__ __forceinline__ void block_update(const uint8_t* slot, uint32_t kl, uint32_t vl, const typename P::Q& q,
+                                             int cb, int N, int g, float sl2, float& m_run, float& l_run,
+                                             f32x4 (&acc)[4]) {
+  const int key0 = 64 * cb;
+  f32x4 sc[4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) sc[u] = P::qk(slot + P::k_sub(u) + kl, q);
+  // One uniform branch after all four products, so they issue back to back.
+  if (cb < 0 || key0 + 63 >= N) {  // absent entry, or keys past the end
+    // key 16u + 4g + rr of the block is valid below lim; the lane term stays
+    // alone on the left (a hoisted table of all 16 lane keys would cost
+    // 16 registers for the whole kernel)
+    const int lim = cb < 0 ? 0 : N - key0;
+    const int lk = 4 * g;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) sc[u][rr] = lk < lim - 16 * u - rr ? sc[u][rr] : -INFINITY;
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) mx = fmaxf(mx, fmaxf(fmaxf(sc[u][0], sc[u][1]), fmaxf(sc[u][2], sc[u][3])));
+  const float m_new = fmaxf(m_run, col_max(mx));
+  const float m_use = m_new == -INFINITY ? 0.0f : m_new * sl2;
+  const float corr = __builtin_amdgcn_exp2f(m_run * sl2 - m_use);  // 0 on a row's first block
+  l_run *= corr;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) acc[dt] *= corr;
+  m_run = m_new;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    float p[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      p[rr] = __builtin_amdgcn_exp2f(fmaf(sc[u][rr], sl2, -m_use));
+      l_run += p[rr];
+    }
+    P::pv(slot + P::v_sub(u) + vl, p, acc);
+  }
+}
+
+template <class P>
+__global__ __launch_bounds__(256, P::kMinBlocks) void block_row_kernel(BlockArgs a) {
   static_assert(P::kRows == 64, "block kernel walks 64-key slots");
   __shared__ __attribute__((aligned(16))) uint8_t ring[2 * P::kSlot];
   using Elt = typename P::Elt;
@@ -38,12 +97,13 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void block_kernel(BlockArgs a) 
   const int c = lane & 15;
   const int g = lane >> 4;
 
-  const int r = blockIdx.x % a.nbq;
-  const int bh = blockIdx.x / a.nbq;  // b * H + h
+  const int wg = xcd_row_order(blockIdx.x, gridDim.x);
+  const int r = wg % a.nbq;
+  const int bh = wg / a.nbq;  // b * H + h
   const int h = bh % a.H;
   const int b = bh / a.H;
   const int N = a.N;
-  const uint32_t tb = (uint32_t)a.H * kHeadDim * sizeof(Elt);  // bytes between tokens
+  const uint32_t tb = (uint32_t)a.H * kHeadDim * sizeof(Elt);
 
   const int64_t base = ((int64_t)b * N * a.H + h) * kHeadDim;
   const uint32_t nrec = (uint32_t)((int64_t)(N - 1) * tb + kHeadDim * sizeof(Elt));
@@ -77,38 +137,7 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void block_kernel(BlockArgs a) 
   for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   for (int e = 0; e < ne; ++e) {
     P::load_slot(nxt, Kr, Vr, blk_off(e + 1), tid, tb);
-    const uint8_t* slot = ring + (e & 1) * P::kSlot;
-    const int key0 = 64 * row[e];
-    f32x4 sc[4];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      f32x4 z = P::qk(slot + P::k_sub(u) + kl, q);
-      if (key0 + 16 * u + 15 >= N) {  // ragged last block: keys past the end
-        const int km = key0 + 16 * u + 4 * g;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) z[rr] = km + rr < N ? z[rr] : -INFINITY;
-      }
-      sc[u] = z;
-      mx = fmaxf(mx, fmaxf(fmaxf(z[0], z[1]), fmaxf(z[2], z[3])));
-    }
-    const float m_new = fmaxf(m_run, col_max(mx));
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new * a.scale_log2;
-    const float corr = __builtin_amdgcn_exp2f(m_run * a.scale_log2 - m_use);  // 0 on the first block
-    l_run *= corr;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) acc[dt] *= corr;
-    m_run = m_new;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      float p[4];
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        p[rr] = __builtin_amdgcn_exp2f(fmaf(sc[u][rr], a.scale_log2, -m_use));
-        l_run += p[rr];
-      }
-      P::pv(slot + P::v_sub(u) + vl, p, acc);
-    }
+    block_update<P>(ring + (e & 1) * P::kSlot, kl, vl, q, row[e], N, g, a.scale_log2, m_run, l_run, acc);
     // block e+1 goes into the slot block e-1 used (all waves passed the
     // barrier that ended iteration e-1)
     if (e + 1 < ne) P::store_slot(nxt, ring + ((e + 1) & 1) * P::kSlot, tid);

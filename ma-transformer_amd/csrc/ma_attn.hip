@@ -641,6 +641,11 @@ bool block_applies(const ma_attn_desc* d, const void* q, const void* k, const vo
   return (d->seq_len + 128) * tb < (1LL << 31) && d->batch * d->num_heads * nbq <= (int64_t)INT32_MAX;
 }
 
+template <class P>
+void launch_block_t(const BlockArgs& a, int64_t bh, hipStream_t st) {
+  hipLaunchKernelGGL(block_row_kernel<P>, dim3((unsigned)(bh * a.nbq)), dim3(256), 0, st, a);
+}
+
 int launch_block(const ma_attn_desc* d, const void* q, const void* k, const void* v, void* o, hipStream_t st) {
   BlockArgs a;
   a.q = q;
@@ -653,11 +658,11 @@ int launch_block(const ma_attn_desc* d, const void* q, const void* k, const void
   a.bpr = (int32_t)d->blocks_per_row;
   a.nbq = (int32_t)((d->seq_len + 63) / 64);
   a.scale_log2 = scale_of(d) * 1.4426950408889634f;
-  const int64_t wgs = d->batch * d->num_heads * a.nbq;
+  const int64_t bh = d->batch * d->num_heads;
   if (d->dtype == MA_ATTN_BF16)
-    hipLaunchKernelGGL(block_kernel<HalfPath<__bf16>>, dim3((unsigned)wgs), dim3(256), 0, st, a);
+    launch_block_t<HalfPath<__bf16>>(a, bh, st);
   else
-    hipLaunchKernelGGL(block_kernel<HalfPath<_Float16>>, dim3((unsigned)wgs), dim3(256), 0, st, a);
+    launch_block_t<HalfPath<_Float16>>(a, bh, st);
   return 0;
 }
 

@@ -18,6 +18,7 @@ New pattern entry points (not in the reference):
 
     sliding_forward(q, k, v, left, right, dilation=1)
     block_sparse_forward(q, k, v, block_table, block_size=64)
+    BlockTable(block_table, seq_len, block_size=64)   (checked once, on the device)
     longformer_forward(q, k, v, left, right=0, num_global=16)
     make_block_table(seed, num_blocks, random_per_row=2)
 
@@ -35,7 +36,7 @@ import torch
 import ma_attn as _ma
 
 __all__ = ["forward", "dense_forward", "backward", "dense_backward", "sliding_forward",
-           "block_sparse_forward", "longformer_forward", "make_block_table"]
+           "block_sparse_forward", "longformer_forward", "make_block_table", "BlockTable"]
 
 
 def _check(*ts: torch.Tensor) -> None:
@@ -107,33 +108,74 @@ def make_block_table(seed: int, num_blocks: int, random_per_row: int = 2) -> tor
     return _ma.block_table(seed, num_blocks, random_per_row)
 
 
+def _validated_table(block_table: torch.Tensor, nb: int) -> torch.Tensor:
+    """Host int32 copy of block_table after the layout checks the kernels rely on."""
+    if not isinstance(block_table, torch.Tensor):
+        raise RuntimeError("block_table must be a tensor")
+    if block_table.dim() != 2 or block_table.shape[0] != nb:
+        raise RuntimeError(f"block_table must be [ceil(S/block_size)={nb}, width]")
+    if block_table.shape[1] < 1 or block_table.shape[1] > 64:
+        raise RuntimeError("block_table width must be in [1, 64]")
+    tab_cpu = block_table.detach().to("cpu", torch.int32)
+    if (tab_cpu >= nb).any() or (tab_cpu < -1).any():
+        raise RuntimeError("block_table entries must be -1 or in [0, num_blocks)")
+    valid = tab_cpu >= 0
+    # padding last: once an entry is -1, every later entry of the row is -1
+    if (valid[:, 1:] & ~valid[:, :-1]).any():
+        raise RuntimeError("block_table rows must hold their -1 padding after the valid entries")
+    # strictly ascending among valid entries
+    if ((tab_cpu[:, 1:] <= tab_cpu[:, :-1]) & valid[:, 1:]).any():
+        raise RuntimeError("block_table rows must be strictly ascending")
+    return tab_cpu.contiguous()
+
+
+class BlockTable:
+    """A block table checked once and kept on the device, for repeated calls.
+
+    block_sparse_forward checks a plain tensor table on the host at every
+    call (a device-to-host copy and a few host reductions); a BlockTable
+    carries the checked device copy, so a call with it only launches.
+    """
+
+    def __init__(self, block_table: torch.Tensor, seq_len: int, block_size: int = 64, device=None):
+        self.seq_len = int(seq_len)
+        self.block_size = int(block_size)
+        if self.block_size < 1:
+            raise RuntimeError("block_size must be >= 1")
+        nb = (self.seq_len + self.block_size - 1) // self.block_size
+        dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self.tensor = _validated_table(block_table, nb).to(dev)
+
+    @property
+    def width(self) -> int:
+        return int(self.tensor.shape[1])
+
+
 def block_sparse_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
-                         block_table: torch.Tensor, block_size: int = 64) -> torch.Tensor:
-    """Query block r attends the key blocks listed in block_table[r] (ascending, -1 padded)."""
+                         block_table, block_size: int = 64) -> torch.Tensor:
+    """Query block r attends the key blocks listed in block_table[r] (ascending, -1 padded).
+
+    block_table: an int tensor [ceil(S/block_size), width] (checked at every
+    call), or a BlockTable made for this sequence length and block size.
+    """
     _check(query, key, value)
     B, N, H, D = query.shape
     bs = int(block_size)
     if bs < 1:
         raise RuntimeError("block_size must be >= 1")
     nb = (N + bs - 1) // bs
-    if block_table.dim() != 2 or block_table.shape[0] != nb:
-        raise RuntimeError(f"block_table must be [ceil(S/block_size)={nb}, width]")
-    if block_table.shape[1] < 1 or block_table.shape[1] > 64:
-        raise RuntimeError("block_table width must be in [1, 64]")
-    tab_cpu = block_table.detach().to("cpu", torch.int32)
-    if tab_cpu.numel() and ((tab_cpu >= nb).any() or (tab_cpu < -1).any()):
-        raise RuntimeError("block_table entries must be -1 or in [0, num_blocks)")
-    if tab_cpu.numel():
-        valid = tab_cpu >= 0
-        # padding last: once an entry is -1, every later entry of the row is -1
-        if (valid[:, 1:] & ~valid[:, :-1]).any():
-            raise RuntimeError("block_table rows must hold their -1 padding after the valid entries")
-        # strictly ascending among valid entries
-        if ((tab_cpu[:, 1:] <= tab_cpu[:, :-1]) & valid[:, 1:]).any():
-            raise RuntimeError("block_table rows must be strictly ascending")
-    # Allocated on the current stream; the caching allocator reuses its memory
-    # only for later work on that same stream, i.e. after the kernel read it.
-    tab = tab_cpu.to(query.device).contiguous()
+    if isinstance(block_table, BlockTable):
+        if block_table.seq_len != N or block_table.block_size != bs:
+            raise RuntimeError(f"BlockTable was made for S={block_table.seq_len}, block_size="
+                               f"{block_table.block_size}; called with S={N}, block_size={bs}")
+        if block_table.tensor.device != query.device:
+            raise RuntimeError("BlockTable is on another device than the inputs")
+        tab = block_table.tensor
+    else:
+        # Allocated on the current stream; the caching allocator reuses its
+        # memory only for later work on that same stream, i.e. after the
+        # kernel read it.
+        tab = _validated_table(block_table, nb).to(query.device)
     return _launch(query, key, value, _ma.BLOCK_SPARSE, block_size=bs,
                    block_table_ptr=tab.data_ptr(), blocks_per_row=tab.shape[1])
 

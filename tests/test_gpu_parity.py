@@ -158,6 +158,22 @@ def test_longformer_geometry(ext, oracle, N, G, left, right, dtype):
     assert _max_err(y, oracle.forward(spec, *up)) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("width,padded", [(2, False), (2, True), (4, False), (4, True), (3, True)])
+def test_block_sparse_many_rows(ext, oracle, width, padded):
+    """4032 (batch, head, block) rows, renumbered over the XCDs, N not a
+    multiple of 64; full and -1 padded tables of several widths."""
+    shape = (4, 4000, 16, 64)
+    (q, k, v), up = _inputs(shape, 4321 + width, torch.bfloat16, scale=0.5)
+    nb = (4000 + 63) // 64
+    tab = _random_table(nb, width, 99 + width, rng_extra_pad=padded)
+    # a checked device-resident table for the padded cases, a plain tensor otherwise
+    arg = ext.BlockTable(torch.from_numpy(tab), 4000, 64) if padded else torch.from_numpy(tab)
+    y = ext.block_sparse_forward(q, k, v, arg, 64)
+    spec = oracle.Spec(*shape, pattern="block_sparse", block_size=64, table=tab)
+    _check_sampled(oracle, spec, up, y, torch.bfloat16, (0, 2), [(0, 4000)])
+    _check_sampled(oracle, spec, up, y, torch.bfloat16, (15, 16), [(0, 4000)])
+
+
 def test_block_table_validation(ext):
     q = torch.randn(1, 128, 1, 64, device="cuda", dtype=torch.bfloat16)
     ok = torch.tensor([[0, -1, -1], [0, 1, -1]], dtype=torch.int32)
@@ -166,6 +182,12 @@ def test_block_table_validation(ext):
                 [[0, 0, -1], [0, 1, -1]]):
         with pytest.raises(RuntimeError):
             ext.block_sparse_forward(q, q, q, torch.tensor(bad, dtype=torch.int32), 64)
+        with pytest.raises(RuntimeError):
+            ext.BlockTable(torch.tensor(bad, dtype=torch.int32), 128, 64)
+    bt = ext.BlockTable(ok, 128, 64)
+    torch.testing.assert_close(ext.block_sparse_forward(q, q, q, bt, 64), ext.block_sparse_forward(q, q, q, ok, 64))
+    with pytest.raises(RuntimeError):  # made for another sequence length
+        ext.block_sparse_forward(q[:, :64].contiguous(), q[:, :64].contiguous(), q[:, :64].contiguous(), bt, 64)
 
 
 # ------------------------------------------------------- BASELINE configs
