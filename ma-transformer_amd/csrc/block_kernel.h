@@ -74,14 +74,15 @@ __device__ __forceinline__ void block_update(const uint8_t* slot, uint32_t kl, u
   for (int dt = 0; dt < 4; ++dt) acc[dt] *= corr;
   m_run = m_new;
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    float p[4];
+  for (int u = 0; u < 4; u += 2) {
+    float p0[4], p1[4];
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-      p[rr] = __builtin_amdgcn_exp2f(fmaf(sc[u][rr], sl2, -m_use));
-      l_run += p[rr];
+      p0[rr] = __builtin_amdgcn_exp2f(fmaf(sc[u][rr], sl2, -m_use));
+      p1[rr] = __builtin_amdgcn_exp2f(fmaf(sc[u + 1][rr], sl2, -m_use));
+      l_run += p0[rr] + p1[rr];
     }
-    P::pv(slot + P::v_sub(u) + vl, p, acc);
+    P::pv2(slot + P::v_sub(u) + vl, slot + P::v_sub(u + 1) + vl, p0, p1, acc);
   }
 }
 

@@ -19,18 +19,18 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 // MFMA operand handling per 16-bit element type.
-//   qk : 16x16x32 (8 elements of the contraction per lane)
-//   pv : 16x16x16 (4 elements per lane)
+//   x32 : 16x16x32 (8 elements of the contraction per lane)
+//   x16 : 16x16x16 (4 elements per lane)
 template <typename T>
 struct Mma;
 
 template <>
 struct Mma<__bf16> {
-  static __device__ __forceinline__ f32x4 qk(uint4 a, uint4 b, f32x4 c) {
+  static __device__ __forceinline__ f32x4 x32(uint4 a, uint4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
                                                    c, 0, 0, 0);
   }
-  static __device__ __forceinline__ f32x4 pv(uint2 a, uint2 b, f32x4 c) {
+  static __device__ __forceinline__ f32x4 x16(uint2 a, uint2 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b),
                                                      c, 0, 0, 0);
   }
@@ -42,11 +42,11 @@ struct Mma<__bf16> {
 
 template <>
 struct Mma<_Float16> {
-  static __device__ __forceinline__ f32x4 qk(uint4 a, uint4 b, f32x4 c) {
+  static __device__ __forceinline__ f32x4 x32(uint4 a, uint4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
                                                   0, 0, 0);
   }
-  static __device__ __forceinline__ f32x4 pv(uint2 a, uint2 b, f32x4 c) {
+  static __device__ __forceinline__ f32x4 x16(uint2 a, uint2 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0,
                                                  0, 0);
   }

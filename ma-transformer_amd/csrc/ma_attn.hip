@@ -292,8 +292,8 @@ __global__ __launch_bounds__(256) void band_kernel(BandArgs a) {
         const uint4 ka0 = *reinterpret_cast<const uint4*>(kr);
         const uint4 ka1 = *reinterpret_cast<const uint4*>(kr + 32);
         f32x4 z = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        z = Mma<T>::qk(ka0, qb0, z);
-        z = Mma<T>::qk(ka1, qb1, z);
+        z = Mma<T>::x32(ka0, qb0, z);
+        z = Mma<T>::x32(ka1, qb1, z);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int64_t km = k_lo + 4 * g + r;
@@ -336,7 +336,7 @@ __global__ __launch_bounds__(256) void band_kernel(BandArgs a) {
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
         const uint2 va = *reinterpret_cast<const uint2*>(&vt[(16 * dt + c) * kVtStride + 16 * st + 4 * g]);
-        acc[dt] = Mma<T>::pv(va, pb, acc[dt]);
+        acc[dt] = Mma<T>::x16(va, pb, acc[dt]);
       }
     }
   }

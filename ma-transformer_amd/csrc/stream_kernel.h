@@ -53,8 +53,10 @@ constexpr int kPartial = kHeadDim + 2;
 
 // ---------------------------------------------------------------- 16-bit path
 //
-// Q.K^T on 16x16x32 MFMA (K rows row-major in LDS), P.V on 16x16x16 MFMA with
-// V transposed in LDS (V^T rows = head_dim).  O^T tile dt row m is head_dim
+// Q.K^T on 16x16x32 MFMA (K rows row-major in LDS), P.V with V transposed in
+// LDS (V^T rows = head_dim): interior tiles pair sub-tiles on 16x16x32 MFMA
+// (pv2), edge tiles take one sub-tile per 16x16x16 MFMA (pv; pairing there
+// spilled registers at the 128-register budget and was measured slower).  O^T tile dt row m is head_dim
 // d(dt, m) = 32*(dt>>1) + 8*(m>>2) + 4*(dt&1) + (m&3), so lane (query c,
 // group g) ends with O[c][8g..8g+7] in acc[0..1] and O[c][32+8g..32+8g+7] in
 // acc[2..3]: two 16 B stores per lane.  The permutation is applied where V^T
@@ -134,8 +136,8 @@ struct HalfPath {
     const uint4 a0 = *reinterpret_cast<const uint4*>(kp);
     const uint4 a1 = *reinterpret_cast<const uint4*>(kp + 64);
     f32x4 z = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    z = Mma<T>::qk(a0, q.r[0], z);
-    return Mma<T>::qk(a1, q.r[1], z);
+    z = Mma<T>::x32(a0, q.r[0], z);
+    return Mma<T>::x32(a1, q.r[1], z);
   }
 
   // O^T += V^T P^T over the 16 keys whose probabilities this lane holds in p.
@@ -146,7 +148,27 @@ struct HalfPath {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
       const uint2 va = *reinterpret_cast<const uint2*>(vp + vt_row_of_tile(dt) * kVRow);
-      acc[dt] = Mma<T>::pv(va, pb, acc[dt]);
+      acc[dt] = Mma<T>::x16(va, pb, acc[dt]);
+    }
+  }
+
+  // The same over two sub-tiles (any two, e.g. from different slots) on one
+  // 16x16x32 MFMA per head_dim tile, twice the keys per instruction of the
+  // 16x16x16 form.  Contraction element 4h + r of lane group g is key 4g + r
+  // of sub-tile h, in both operands: A = the lane's V^T words of the two
+  // sub-tiles side by side, B = p0 then p1.
+  static __device__ __forceinline__ void pv2(const uint8_t* vp0, const uint8_t* vp1, const float (&p0)[4],
+                                             const float (&p1)[4], f32x4 (&acc)[4]) {
+    uint4 pb;
+    pb.x = Mma<T>::pack2(p0[0], p0[1]);
+    pb.y = Mma<T>::pack2(p0[2], p0[3]);
+    pb.z = Mma<T>::pack2(p1[0], p1[1]);
+    pb.w = Mma<T>::pack2(p1[2], p1[3]);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const uint2 a0 = *reinterpret_cast<const uint2*>(vp0 + vt_row_of_tile(dt) * kVRow);
+      const uint2 a1 = *reinterpret_cast<const uint2*>(vp1 + vt_row_of_tile(dt) * kVRow);
+      acc[dt] = Mma<T>::x32(make_uint4(a0.x, a0.y, a1.x, a1.y), pb, acc[dt]);
     }
   }
 
@@ -250,6 +272,13 @@ struct F32Path {
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) acc[dt] = mfma_f32(va[dt], p[r], acc[dt]);
     }
+  }
+
+  // fp32 MFMA has no wider contraction: two sub-tiles are two updates.
+  static __device__ __forceinline__ void pv2(const uint8_t* vp0, const uint8_t* vp1, const float (&p0)[4],
+                                             const float (&p1)[4], f32x4 (&acc)[4]) {
+    pv(vp0, p0, acc);
+    pv(vp1, p1, acc);
   }
 
   static __device__ __forceinline__ void store_acc(const f32x4 (&acc)[4], float* row, int g) {
@@ -413,24 +442,28 @@ __device__ __forceinline__ void window_tile(const uint8_t* ring, uint32_t kl, ui
   f32x4 acc[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  if (LG) {
-    float p[4];
+  // P.V two sub-tiles per MFMA; the Longformer global sub-tile is element 0
+  constexpr int kN = G::NSUB + (LG ? 1 : 0);
+  auto score = [&](int j) -> const f32x4& { return LG ? (j == 0 ? zg : sc[j - 1]) : sc[j]; };
+  auto vaddr_of = [&](int j) { return LG ? (j == 0 ? (uint32_t)(G::NSLOT * P::kSlot) + vl : vaddr[j - 1]) : vaddr[j]; };
+#pragma unroll
+  for (int j = 0; j < kN; j += 2) {
+    float p0[4], p1[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      p[r] = __builtin_amdgcn_exp2f(fmaf(zg[r], sl2, -m_use));
-      l_run += p[r];
+      p0[r] = __builtin_amdgcn_exp2f(fmaf(score(j)[r], sl2, -m_use));
+      l_run += p0[r];
     }
-    P::pv(ring + G::NSLOT * P::kSlot + vl, p, acc);
-  }
+    if (j + 1 < kN) {  // resolved at compile time
 #pragma unroll
-  for (int j = 0; j < G::NSUB; ++j) {
-    float p[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      p[r] = __builtin_amdgcn_exp2f(fmaf(sc[j][r], sl2, -m_use));
-      l_run += p[r];
+      for (int r = 0; r < 4; ++r) {
+        p1[r] = __builtin_amdgcn_exp2f(fmaf(score(j + 1)[r], sl2, -m_use));
+        l_run += p1[r];
+      }
+      P::pv2(ring + vaddr_of(j), ring + vaddr_of(j + 1), p0, p1, acc);
+    } else {
+      P::pv(ring + vaddr_of(j), p0, acc);
     }
-    P::pv(ring + vaddr[j], p, acc);
   }
   const float l_tot = col_sum(l_run);
   P::store_o(acc, __builtin_amdgcn_rcpf(l_tot), Or, orow, g);
