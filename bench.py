@@ -35,6 +35,7 @@ sys.path.insert(0, REPO)
 METRIC = "sparse-attn queries/sec + achieved HBM GB/s (% peak) at N=64K, w=64, 1 GPU"
 HBM_PEAK_GBPS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+MFMA_F32_PEAK_TFLOPS = 157.3
 
 # name: (B, H, N, D, dtype, pattern kwargs, description)
 WORKLOADS = {
@@ -54,6 +55,9 @@ WORKLOADS = {
                   "dilated causal window (i-4k, k<64), fp32, B=1 H=8 N=65536 D=64"),
     "cfg5_bf16": (1, 8, 65536, 64, "bf16", dict(pattern="sliding", left=63, right=0, dilation=4),
                   "dilated causal window (i-4k, k<64), bf16, B=1 H=8 N=65536 D=64"),
+    # not a BASELINE config: the dense_forward(use_causal_mask=True) path at a long sequence
+    "dense_causal_bf16": (1, 8, 16384, 64, "bf16", dict(pattern="dense", causal=True),
+                          "dense causal (keys [0,i]), bf16, B=1 H=8 N=16384 D=64"),
 }
 
 
@@ -73,6 +77,8 @@ def key_count(N: int, pk: dict) -> int:
     if p == "block_sparse":
         nb = (N + pk["block_size"] - 1) // pk["block_size"]
         return (nb * (2 + pk["extra"]) - 1) * pk["block_size"] * pk["block_size"]
+    if p == "dense":
+        return N * (N + 1) // 2 if pk.get("causal") else N * N
     if p == "longformer":
         G, L = pk["num_global"], pk["left"]
         return G * N + sum(i + 1 for i in range(G, G + L)) + (L + 1 + G) * (N - G - L)
@@ -104,7 +110,7 @@ def cpu_baseline(B, H, N, D, dtype, pk, budget_s=12.0):
         table = O.block_table(pk["seed"], nb, pk["extra"])
     spec = O.Spec(B, N, H, D, pattern=pk["pattern"], left=pk.get("left", 0), right=pk.get("right", 0),
                   dilation=pk.get("dilation", 1), block_size=pk.get("block_size", 64), table=table,
-                  num_global=pk.get("num_global", 0))
+                  num_global=pk.get("num_global", 0), causal=pk.get("causal", False))
     # time one head first, then as many whole heads as fit the budget
     t0 = time.perf_counter()
     O.forward(spec, q, k, v, heads=(0, 1))
@@ -169,6 +175,8 @@ def main() -> int:
         # checked and copied to the device once, as a model holding a fixed pattern would
         table = ext.BlockTable(ext.make_block_table(pk["seed"], nb, pk["extra"]), N, pk["block_size"], dev)
         launch = lambda s: ext.block_sparse_forward(s[0], s[1], s[2], table, pk["block_size"])
+    elif pk["pattern"] == "dense":
+        launch = lambda s: ext.dense_forward(s[0], s[1], s[2], pk["causal"])
     else:
         launch = lambda s: ext.longformer_forward(s[0], s[1], s[2], pk["left"], pk["right"], pk["num_global"])
 
@@ -215,6 +223,15 @@ def main() -> int:
     copy_gbps = 2 * (1 << 30) * 10 / (c0.elapsed_time(c1) * 1e-3) / 1e9
     del src, dst
 
+    # the bound is whichever peak the algorithmic work reaches first
+    mfma_peak = MFMA_BF16_PEAK_TFLOPS if dt_name == "bf16" else MFMA_F32_PEAK_TFLOPS
+    tflops = flops / (mean_launch_ms * 1e-3) / 1e12
+    if flops / alg_bytes > mfma_peak * 1e12 / (HBM_PEAK_GBPS * 1e9):
+        roofline = {"bound": "mfma", "achieved": tflops, "peak": mfma_peak, "unit": "TFLOP/s",
+                    "frac": tflops / mfma_peak, "traffic": traffic}
+    else:
+        roofline = {"bound": "hbm", "achieved": achieved_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": achieved_gbps / HBM_PEAK_GBPS, "traffic": traffic}
     out = {
         "metric": METRIC,
         "value": queries / (ms_per_step * 1e-3),
@@ -232,14 +249,7 @@ def main() -> int:
                    **{k_: v_ for k_, v_ in pk.items()}},
         "hbm_gbps": achieved_gbps,
         "hbm_frac_of_peak": achieved_gbps / HBM_PEAK_GBPS,
-        "roofline": {
-            "bound": "hbm",
-            "achieved": achieved_gbps,
-            "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s",
-            "frac": achieved_gbps / HBM_PEAK_GBPS,
-            "traffic": traffic,
-        },
+        "roofline": roofline,
         "kernel_us_mean": mean_launch_ms * 1e3,
         "kernel_us_median": per_launch_ms[len(per_launch_ms) // 2] * 1e3,
         "algorithmic_bytes_per_launch": alg_bytes,

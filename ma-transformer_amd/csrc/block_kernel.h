@@ -26,9 +26,10 @@ struct BlockArgs {
   const void* k;
   const void* v;
   void* o;
-  const int32_t* table;  // [nbq, bpr]
+  const int32_t* table;  // [nbq, bpr]; null: every block (dense), or blocks 0..r (causal)
   int32_t N, H, bpr, nbq;
   float scale_log2;
+  int32_t causal;  // with a null table: keys [0, i]
 };
 
 // Workgroups are dispatched round-robin over the 8 XCDs, each with its own
@@ -42,27 +43,29 @@ __device__ __forceinline__ int xcd_row_order(int bid, int G) {
 }
 
 // Online-softmax update of one 64-key block (4 sub-tiles) from an LDS slot.
-// cb < 0: an absent entry, every score masked.
+// cb < 0: an absent entry, every score masked.  diag: the block is the query
+// block itself under a causal mask, so key k of the block is kept only up to
+// the lane's query ql (0..63 within the block).
 template <class P>
 __device__ __forceinline__ void block_update(const uint8_t* slot, uint32_t kl, uint32_t vl, const typename P::Q& q,
-                                             int cb, int N, int g, float sl2, float& m_run, float& l_run,
-                                             f32x4 (&acc)[4]) {
+                                             int cb, bool diag, int ql, int N, int g, float sl2, float& m_run,
+                                             float& l_run, f32x4 (&acc)[4]) {
   const int key0 = 64 * cb;
   f32x4 sc[4];
   float mx = -INFINITY;
 #pragma unroll
   for (int u = 0; u < 4; ++u) sc[u] = P::qk(slot + P::k_sub(u) + kl, q);
   // One uniform branch after all four products, so they issue back to back.
-  if (cb < 0 || key0 + 63 >= N) {  // absent entry, or keys past the end
-    // key 16u + 4g + rr of the block is valid below lim; the lane term stays
+  if (cb < 0 || diag || key0 + 63 >= N) {  // absent entry, causal diagonal, or keys past the end
+    // key 16u + 4g + rr of the block is kept up to hi; the lane term stays
     // alone on the left (a hoisted table of all 16 lane keys would cost
     // 16 registers for the whole kernel)
-    const int lim = cb < 0 ? 0 : N - key0;
+    const int hi = min(cb < 0 ? -1 : N - key0 - 1, diag ? ql : 63);
     const int lk = 4 * g;
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) sc[u][rr] = lk < lim - 16 * u - rr ? sc[u][rr] : -INFINITY;
+      for (int rr = 0; rr < 4; ++rr) sc[u][rr] = lk <= hi - 16 * u - rr ? sc[u][rr] : -INFINITY;
   }
 #pragma unroll
   for (int u = 0; u < 4; ++u) mx = fmaxf(mx, fmaxf(fmaxf(sc[u][0], sc[u][1]), fmaxf(sc[u][2], sc[u][3])));
@@ -98,8 +101,10 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void block_row_kernel(BlockArgs
   const int c = lane & 15;
   const int g = lane >> 4;
 
+  const bool dense = a.table == nullptr;
   const int wg = xcd_row_order(blockIdx.x, gridDim.x);
-  const int r = wg % a.nbq;
+  // causal rows run longest (last query block) first, so short ones fill the tail
+  const int r = dense && a.causal ? a.nbq - 1 - wg % a.nbq : wg % a.nbq;
   const int bh = wg / a.nbq;  // b * H + h
   const int h = bh % a.H;
   const int b = bh / a.H;
@@ -114,16 +119,18 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void block_row_kernel(BlockArgs
   const __amdgpu_buffer_rsrc_t Or = make_rsrc(static_cast<const Elt*>(a.o) + base, nrec);
 
   // valid entries of this row (the table is -1 padded at the end)
-  const int32_t* row = a.table + (int64_t)r * a.bpr;
-  int ne = 0;
-  for (int e = 0; e < a.bpr; ++e) ne += row[e] >= 0 ? 1 : 0;
+  const int32_t* row = dense ? nullptr : a.table + (int64_t)r * a.bpr;
+  int ne = dense ? (a.causal ? r + 1 : a.nbq) : 0;
+  if (!dense)
+    for (int e = 0; e < a.bpr; ++e) ne += row[e] >= 0 ? 1 : 0;
+  auto block_of = [&](int e) { return e < ne ? (dense ? e : row[min(e, a.bpr - 1)]) : -1; };
 
   const uint32_t qrow = (uint32_t)(64 * r + 16 * wv + c) * tb;
   typename P::Q q;
   P::load_q(q, Qr, qrow, g);
   const uint32_t kl = P::k_lane(c, g), vl = P::v_lane(c, g);
   auto blk_off = [&](int e) {
-    const int cb = e < ne ? row[min(e, a.bpr - 1)] : -1;
+    const int cb = block_of(e);
     return cb >= 0 ? (uint32_t)(64 * cb) * tb : kOob;
   };
 
@@ -138,7 +145,9 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void block_row_kernel(BlockArgs
   for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   for (int e = 0; e < ne; ++e) {
     P::load_slot(nxt, Kr, Vr, blk_off(e + 1), tid, tb);
-    block_update<P>(ring + (e & 1) * P::kSlot, kl, vl, q, row[e], N, g, a.scale_log2, m_run, l_run, acc);
+    const int cb = block_of(e);
+    block_update<P>(ring + (e & 1) * P::kSlot, kl, vl, q, cb, dense && a.causal && cb == r, 16 * wv + c, N, g,
+                    a.scale_log2, m_run, l_run, acc);
     // block e+1 goes into the slot block e-1 used (all waves passed the
     // barrier that ended iteration e-1)
     if (e + 1 < ne) P::store_slot(nxt, ring + ((e + 1) & 1) * P::kSlot, tid);

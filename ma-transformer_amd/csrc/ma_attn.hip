@@ -631,9 +631,11 @@ int launch_stream(const ma_attn_desc* d, const void* q, const void* k, const voi
   }
 }
 
-// Block-sparse on MFMA: block size 64, head_dim 64, 16-bit.
+// Block-sparse on MFMA: block size 64, head_dim 64, 16-bit.  Dense (and
+// causal) attention takes the same kernel with every block (blocks 0..r).
 bool block_applies(const ma_attn_desc* d, const void* q, const void* k, const void* v, const void* o) {
-  if (d->pattern != MA_ATTN_BLOCK_SPARSE || d->block_size != 64 || d->head_dim != kHeadDim) return false;
+  const bool blocks = d->pattern == MA_ATTN_BLOCK_SPARSE && d->block_size == 64;
+  if (!(blocks || d->pattern == MA_ATTN_DENSE) || d->head_dim != kHeadDim) return false;
   if (d->dtype != MA_ATTN_BF16 && d->dtype != MA_ATTN_F16) return false;
   if (!(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o))) return false;
   const int64_t tb = d->num_heads * kHeadDim * 2;
@@ -652,10 +654,12 @@ int launch_block(const ma_attn_desc* d, const void* q, const void* k, const void
   a.k = k;
   a.v = v;
   a.o = o;
-  a.table = d->block_table;
+  const bool dense = d->pattern == MA_ATTN_DENSE;
+  a.table = dense ? nullptr : d->block_table;
+  a.causal = dense && d->causal;
   a.N = (int32_t)d->seq_len;
   a.H = (int32_t)d->num_heads;
-  a.bpr = (int32_t)d->blocks_per_row;
+  a.bpr = dense ? 0 : (int32_t)d->blocks_per_row;
   a.nbq = (int32_t)((d->seq_len + 63) / 64);
   a.scale_log2 = scale_of(d) * 1.4426950408889634f;
   const int64_t bh = d->batch * d->num_heads;

@@ -158,6 +158,27 @@ def test_longformer_geometry(ext, oracle, N, G, left, right, dtype):
     assert _max_err(y, oracle.forward(spec, *up)) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("N", [1, 63, 64, 65, 200, 1000])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_dense_mfma_geometry(ext, oracle, N, causal, dtype):
+    """dense_forward at head_dim 64 in 16-bit (the block kernel with every block)."""
+    shape = (2, N, 3, 64)
+    (q, k, v), up = _inputs(shape, 1300 + N + causal, dtype)
+    y = ext.dense_forward(q, k, v, causal)
+    spec = oracle.Spec(*shape, pattern="dense", causal=causal)
+    assert _max_err(y, oracle.forward(spec, *up)) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_dense_mfma_long(ext, oracle, causal):
+    """B=2 H=4 N=8000: many key blocks per row, causal rows in reverse order."""
+    (q, k, v), up = _inputs((2, 8000, 4, 64), 1400 + causal, torch.bfloat16)
+    y = ext.dense_forward(q, k, v, causal)
+    spec = oracle.Spec(2, 8000, 4, 64, pattern="dense", causal=causal)
+    _check_sampled(oracle, spec, up, y, torch.bfloat16, (0, 4), [(0, 70), (3990, 4100), (7900, 8000)])
+
+
 @pytest.mark.parametrize("width,padded", [(2, False), (2, True), (4, False), (4, True), (3, True)])
 def test_block_sparse_many_rows(ext, oracle, width, padded):
     """4032 (batch, head, block) rows, renumbered over the XCDs, N not a
