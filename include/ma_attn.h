@@ -91,6 +91,28 @@ int ma_attn_forward(const ma_attn_desc* desc, const void* q, const void* k,
  * extension (sparse_attention_kernel.cu:440); this engine never allocates. */
 size_t ma_attn_workspace_size(const ma_attn_desc* desc);
 
+/*
+ * Sparse-attention backward: given dout = dL/dO, writes dq, dk, dv (each
+ * [B,N,H,D] in desc->dtype, every row written) for the SLIDING and DENSE
+ * patterns, recomputing the softmax from q, k, v (no saved forward state),
+ * as the reference's backward entry points do:
+ *   sparse_backward_cuda  src/cuda/sparse_attention_kernel.cu:459-497 (SLIDING, left=right=w;
+ *                         kernel :265-346)
+ *   dense_backward_cuda   src/cuda/sparse_attention_kernel.cu:383-418 (DENSE; kernel :104-175)
+ * generalised to any left/right/dilation and to bf16/fp16 (fp32 arithmetic).
+ * Other patterns return non-zero.  workspace: device memory of
+ * ma_attn_backward_workspace_size(desc) bytes (per-row softmax statistics).
+ */
+int ma_attn_backward(const ma_attn_desc* desc, const void* q, const void* k,
+                     const void* v, const void* dout, void* dq, void* dk,
+                     void* dv, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/* Bytes of device workspace ma_attn_backward needs (8 per (b, i, h) row).
+ * No reference counterpart: the reference keeps no statistics (it recomputes
+ * them per gradient pass, sparse_attention_kernel.cu:285-304). */
+size_t ma_attn_backward_workspace_size(const ma_attn_desc* desc);
+
 /* Validates desc without launching; 0 when ma_attn_forward would accept it.
  * Mirrors the checks of sparse_attention_kernel.cu:427-432. */
 int ma_attn_validate(const ma_attn_desc* desc);
@@ -125,7 +147,7 @@ int64_t ma_attn_row_keys(const ma_attn_desc* desc, const int32_t* host_block_tab
 /* ABI version of this header (bumped on incompatible change). */
 int ma_attn_abi_version(void);
 
-#define MA_ATTN_ABI_VERSION 1
+#define MA_ATTN_ABI_VERSION 2
 
 #ifdef __cplusplus
 }

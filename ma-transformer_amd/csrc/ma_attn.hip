@@ -90,11 +90,20 @@ constexpr int kRowsWaves = 4;
 // One wave per query row (row = (b*N + i)*H + h).  Scores: lane t of a
 // 64-key chunk owns key key_at(t); online softmax across chunks (m, l, acc).
 // P.V: lanes own head_dim slots d = lane + 64*c.
-template <typename T, int DPL>
+// STATS (backward): instead of O, writes the row's softmax statistics
+// stats[row] = {lse, delta}: lse = m + log(l) of the scaled scores, delta =
+// dout . O with O kept in fp32.
+struct RowStat {
+  float lse, delta;
+};
+
+template <typename T, int DPL, bool STATS = false>
 __global__ __launch_bounds__(256) void rows_kernel(const T* __restrict__ q, const T* __restrict__ k,
                                                    const T* __restrict__ v, T* __restrict__ o,
                                                    int64_t B, int64_t H, int64_t D,
-                                                   ma::PatternParams pp, float scale) {
+                                                   ma::PatternParams pp, float scale,
+                                                   const T* __restrict__ dout = nullptr,
+                                                   RowStat* __restrict__ stats = nullptr) {
   extern __shared__ float q_lds[];  // kRowsWaves * D floats
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
@@ -154,11 +163,197 @@ __global__ __launch_bounds__(256) void rows_kernel(const T* __restrict__ q, cons
     m = mn;
   }
   const float inv = cnt > 0 ? 1.0f / l : 0.0f;
-  T* orow = o + rr * D;
+  if constexpr (STATS) {
+    float part = 0.0f;
+#pragma unroll
+    for (int c = 0; c < DPL; ++c) {
+      const int64_t d = lane + 64 * c;
+      if (d < D) part = fmaf(ld_f(dout + rr * D + d), acc[c] * inv, part);
+    }
+    const float delta = wave_sum(part);
+    if (lane == 0) stats[rr] = RowStat{cnt > 0 ? m + logf(l) : 0.0f, delta};
+  } else {
+    T* orow = o + rr * D;
+#pragma unroll
+    for (int c = 0; c < DPL; ++c) {
+      const int64_t d = lane + 64 * c;
+      if (d < D) orow[d] = cvt_out<T>(acc[c] * inv);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ backward row kernels
+//
+// Gradients of O = softmax(S) V, S = Q K^T * scale over each row's key set,
+// as the reference's backward kernels define them
+// (/root/reference src/cuda/sparse_attention_kernel.cu:265-346, dense
+// :104-175): with p_ij = exp(s_ij - lse_i), dp_ij = dout_i . v_j and
+// ds_ij = p_ij (dp_ij - delta_i),
+//   dq_i = scale * sum_{j in S_i} ds_ij k_j
+//   dk_j = scale * sum_{i in T_j} ds_ij q_i,   dv_j = sum_{i in T_j} p_ij dout_i
+// where T_j = {i : j in S_i}, and delta_i = sum_j p_ij dp_ij = dout_i . O_i
+// (the reference's s_dot, :306-316).  Three launches and no atomics: the
+// statistics (rows_kernel<STATS>), dq per query row, dk/dv per key row.  For
+// SLIDING (and DENSE, a window of N-1) T_j is itself a sliding set with left
+// and right swapped, so the key-row kernel walks it with the same closed
+// forms.  Same lane layout as rows_kernel: lanes over the set's entries for
+// the dot products, lanes over head_dim for the accumulations.
+
+// dq: one wave per query row; q_i and dout_i cached in LDS.
+template <typename T, int DPL>
+__global__ __launch_bounds__(256) void bwd_dq_kernel(const T* __restrict__ q, const T* __restrict__ k,
+                                                     const T* __restrict__ v, const T* __restrict__ dout,
+                                                     const RowStat* __restrict__ stats, T* __restrict__ dq,
+                                                     int64_t B, int64_t H, int64_t D, ma::PatternParams pp,
+                                                     float scale) {
+  extern __shared__ float row_lds[];  // kRowsWaves * 2 * D floats
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int64_t N = pp.n;
+  const int64_t row = (int64_t)blockIdx.x * kRowsWaves + wv;
+  const bool row_ok = row < B * N * H;
+  const int64_t rr = row_ok ? row : 0;
+  const int64_t h = rr % H;
+  const int64_t bi = rr / H;
+  const int64_t i = bi % N;
+  const int64_t b = bi / N;
+  const int64_t rs = H * D;
+
+  float* qw = row_lds + wv * 2 * D;
+  float* gw = qw + D;
+  for (int64_t d = lane; d < D; d += 64) {
+    qw[d] = row_ok ? ld_f(q + rr * D + d) : 0.0f;
+    gw[d] = row_ok ? ld_f(dout + rr * D + d) : 0.0f;
+  }
+  __syncthreads();
+  if (!row_ok) return;  // no barrier below this point
+
+  const T* kb = k + (b * N * H + h) * D;
+  const T* vb = v + (b * N * H + h) * D;
+  const ma::RowKeys rk = ma::row_keys(pp, i);
+  const int64_t cnt = rk.count;
+  const RowStat st = stats[rr];
+
+  float acc[DPL];
+#pragma unroll
+  for (int c = 0; c < DPL; ++c) acc[c] = 0.0f;
+  for (int64_t c0 = 0; c0 < cnt; c0 += 64) {
+    const int64_t t = c0 + lane;
+    const bool valid = t < cnt;
+    const int64_t j = valid ? ma::key_at(pp, rk, i, t) : 0;
+    float ds = 0.0f;
+    if (valid) {
+      const T* kr = kb + j * rs;
+      const T* vr = vb + j * rs;
+      float sdot = 0.0f, pdot = 0.0f;
+      for (int64_t d = 0; d < D; ++d) {
+        sdot = fmaf(qw[d], ld_f(kr + d), sdot);
+        pdot = fmaf(gw[d], ld_f(vr + d), pdot);
+      }
+      const float p = expf(sdot * scale - st.lse);
+      ds = p * (pdot - st.delta);
+    }
+    const int nk = (int)ma::imin64(64, cnt - c0);
+    for (int kk = 0; kk < nk; ++kk) {
+      const float dsk = bcast_f(ds, kk);
+      const T* kr = kb + (int64_t)bcast_i((int)j, kk) * rs;
+#pragma unroll
+      for (int c = 0; c < DPL; ++c) {
+        const int64_t d = lane + 64 * c;
+        if (d < D) acc[c] = fmaf(dsk, ld_f(kr + d), acc[c]);
+      }
+    }
+  }
+  T* out = dq + rr * D;
 #pragma unroll
   for (int c = 0; c < DPL; ++c) {
     const int64_t d = lane + 64 * c;
-    if (d < D) orow[d] = cvt_out<T>(acc[c] * inv);
+    if (d < D) out[d] = cvt_out<T>(acc[c] * scale);
+  }
+}
+
+// dk, dv: one wave per key row j over the query set T_j (pt = the transposed
+// pattern); k_j and v_j cached in LDS.
+template <typename T, int DPL>
+__global__ __launch_bounds__(256) void bwd_dkv_kernel(const T* __restrict__ q, const T* __restrict__ k,
+                                                      const T* __restrict__ v, const T* __restrict__ dout,
+                                                      const RowStat* __restrict__ stats, T* __restrict__ dk,
+                                                      T* __restrict__ dv, int64_t B, int64_t H, int64_t D,
+                                                      ma::PatternParams pt, float scale) {
+  extern __shared__ float row_lds[];  // kRowsWaves * 2 * D floats
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int64_t N = pt.n;
+  const int64_t row = (int64_t)blockIdx.x * kRowsWaves + wv;
+  const bool row_ok = row < B * N * H;
+  const int64_t rr = row_ok ? row : 0;
+  const int64_t h = rr % H;
+  const int64_t bj = rr / H;
+  const int64_t j = bj % N;
+  const int64_t b = bj / N;
+  const int64_t rs = H * D;
+
+  float* kw = row_lds + wv * 2 * D;
+  float* vw = kw + D;
+  for (int64_t d = lane; d < D; d += 64) {
+    kw[d] = row_ok ? ld_f(k + rr * D + d) : 0.0f;
+    vw[d] = row_ok ? ld_f(v + rr * D + d) : 0.0f;
+  }
+  __syncthreads();
+  if (!row_ok) return;  // no barrier below this point
+
+  const T* qb = q + (b * N * H + h) * D;
+  const T* gb = dout + (b * N * H + h) * D;
+  const RowStat* sb = stats + b * N * H + h;
+  const ma::RowKeys rq = ma::row_keys(pt, j);
+  const int64_t cnt = rq.count;
+
+  float acc_k[DPL], acc_v[DPL];
+#pragma unroll
+  for (int c = 0; c < DPL; ++c) acc_k[c] = acc_v[c] = 0.0f;
+  for (int64_t c0 = 0; c0 < cnt; c0 += 64) {
+    const int64_t t = c0 + lane;
+    const bool valid = t < cnt;
+    const int64_t i = valid ? ma::key_at(pt, rq, j, t) : 0;
+    float p = 0.0f, ds = 0.0f;
+    if (valid) {
+      const T* qr = qb + i * rs;
+      const T* gr = gb + i * rs;
+      float sdot = 0.0f, pdot = 0.0f;
+      for (int64_t d = 0; d < D; ++d) {
+        sdot = fmaf(ld_f(qr + d), kw[d], sdot);
+        pdot = fmaf(ld_f(gr + d), vw[d], pdot);
+      }
+      const RowStat st = sb[i * H];
+      p = expf(sdot * scale - st.lse);
+      ds = p * (pdot - st.delta);
+    }
+    const int nk = (int)ma::imin64(64, cnt - c0);
+    for (int kk = 0; kk < nk; ++kk) {
+      const float pk = bcast_f(p, kk);
+      const float dsk = bcast_f(ds, kk);
+      const int64_t ik = (int64_t)bcast_i((int)i, kk);
+      const T* qr = qb + ik * rs;
+      const T* gr = gb + ik * rs;
+#pragma unroll
+      for (int c = 0; c < DPL; ++c) {
+        const int64_t d = lane + 64 * c;
+        if (d < D) {
+          acc_v[c] = fmaf(pk, ld_f(gr + d), acc_v[c]);
+          acc_k[c] = fmaf(dsk, ld_f(qr + d), acc_k[c]);
+        }
+      }
+    }
+  }
+  T* ok = dk + rr * D;
+  T* ov = dv + rr * D;
+#pragma unroll
+  for (int c = 0; c < DPL; ++c) {
+    const int64_t d = lane + 64 * c;
+    if (d < D) {
+      ok[d] = cvt_out<T>(acc_k[c] * scale);
+      ov[d] = cvt_out<T>(acc_v[c]);
+    }
   }
 }
 
@@ -670,6 +865,67 @@ int launch_block(const ma_attn_desc* d, const void* q, const void* k, const void
   return 0;
 }
 
+// Backward: SLIDING and DENSE key sets (the reference's backward entry
+// points), any dtype, head_dim <= 512.
+bool backward_supported(const ma_attn_desc* d) {
+  return d->pattern == MA_ATTN_SLIDING || d->pattern == MA_ATTN_DENSE;
+}
+
+// The query sets T_j = {i : j in S_i} as a SLIDING pattern.
+ma::PatternParams transposed_params(const ma_attn_desc* d) {
+  ma::PatternParams p = params_of(d, nullptr);
+  if (d->pattern == MA_ATTN_DENSE) {
+    p.pattern = ma::kSliding;
+    p.dilation = 1;
+    p.left = d->causal ? 0 : d->seq_len - 1;  // i = j + t, t in [-left, right]
+    p.right = d->seq_len - 1;
+  } else {
+    p.left = d->right;
+    p.right = d->left;
+  }
+  p.causal = 0;
+  return p;
+}
+
+template <typename T>
+int launch_backward(const ma_attn_desc* d, const void* q, const void* k, const void* v, const void* dout,
+                    void* dq, void* dk, void* dv, RowStat* stats, hipStream_t st) {
+  const int64_t rows = d->batch * d->seq_len * d->num_heads;
+  const int64_t blocks = (rows + kRowsWaves - 1) / kRowsWaves;
+  if (blocks > (int64_t)INT32_MAX) return fail("ma_attn: problem too large for one launch");
+  const ma::PatternParams pp = params_of(d, nullptr);
+  const ma::PatternParams pt = transposed_params(d);
+  const float scale = scale_of(d);
+  const int dpl = (int)((d->head_dim + 63) / 64);
+  const size_t shm1 = sizeof(float) * kRowsWaves * (size_t)d->head_dim;
+  const size_t shm2 = 2 * shm1;
+  const T* tq = static_cast<const T*>(q);
+  const T* tk = static_cast<const T*>(k);
+  const T* tv = static_cast<const T*>(v);
+  const T* tg = static_cast<const T*>(dout);
+  const dim3 grid((unsigned)blocks), blk(256);
+  const int64_t B = d->batch, H = d->num_heads, D = d->head_dim;
+#define MA_BWD(N_)                                                                                          \
+  do {                                                                                                      \
+    hipLaunchKernelGGL((rows_kernel<T, N_, true>), grid, blk, shm1, st, tq, tk, tv, nullptr, B, H, D, pp,  \
+                       scale, tg, stats);                                                                   \
+    hipLaunchKernelGGL((bwd_dq_kernel<T, N_>), grid, blk, shm2, st, tq, tk, tv, tg, stats,                 \
+                       static_cast<T*>(dq), B, H, D, pp, scale);                                            \
+    hipLaunchKernelGGL((bwd_dkv_kernel<T, N_>), grid, blk, shm2, st, tq, tk, tv, tg, stats,                \
+                       static_cast<T*>(dk), static_cast<T*>(dv), B, H, D, pt, scale);                       \
+  } while (0)
+  if (dpl <= 1)
+    MA_BWD(1);
+  else if (dpl <= 2)
+    MA_BWD(2);
+  else if (dpl <= 4)
+    MA_BWD(4);
+  else
+    MA_BWD(8);
+#undef MA_BWD
+  return 0;
+}
+
 uint64_t splitmix64(uint64_t* s) {
   uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
   z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -737,6 +993,45 @@ int ma_attn_forward(const ma_attn_desc* desc, const void* q, const void* k, cons
   if (rc) return rc;
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail("ma_attn: kernel launch failed: %s", hipGetErrorString(e));
+  return 0;
+}
+
+size_t ma_attn_backward_workspace_size(const ma_attn_desc* desc) {
+  g_last_error.clear();
+  if (validate(desc)) return 0;
+  return (size_t)(desc->batch * desc->seq_len * desc->num_heads) * sizeof(RowStat);
+}
+
+int ma_attn_backward(const ma_attn_desc* desc, const void* q, const void* k, const void* v, const void* dout,
+                     void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes, void* stream) {
+  g_last_error.clear();
+  if (validate(desc)) return 1;
+  if (!backward_supported(desc))
+    return fail("ma_attn_backward: pattern %d has no backward (SLIDING and DENSE only)", desc->pattern);
+  const int64_t rows = desc->batch * desc->seq_len * desc->num_heads;
+  if (rows == 0 || desc->head_dim == 0) return 0;
+  if (!q || !k || !v || !dout || !dq || !dk || !dv) return fail("ma_attn_backward: null tensor pointer");
+  const size_t need = (size_t)rows * sizeof(RowStat);
+  if (!workspace || workspace_bytes < need)
+    return fail("ma_attn_backward: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  (void)hipGetLastError();
+  RowStat* stats = static_cast<RowStat*>(workspace);
+  int rc;
+  switch (desc->dtype) {
+    case MA_ATTN_F32:
+      rc = launch_backward<float>(desc, q, k, v, dout, dq, dk, dv, stats, st);
+      break;
+    case MA_ATTN_BF16:
+      rc = launch_backward<__bf16>(desc, q, k, v, dout, dq, dk, dv, stats, st);
+      break;
+    default:
+      rc = launch_backward<_Float16>(desc, q, k, v, dout, dq, dk, dv, stats, st);
+      break;
+  }
+  if (rc) return rc;
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail("ma_attn_backward: kernel launch failed: %s", hipGetErrorString(e));
   return 0;
 }
 

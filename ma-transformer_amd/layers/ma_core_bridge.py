@@ -129,7 +129,8 @@ def pytorch_pattern_attention(query, key, value, spec: PatternSpec) -> torch.Ten
 
 
 class MACoreAttentionFunction(torch.autograd.Function):
-    """Autograd function: native forward, recomputation backward.
+    """Autograd function: native forward; native backward (HIP kernels that
+    recompute the softmax) for the sliding and dense patterns.
 
     Reference: src/layers/ma_core_bridge.py:44-154.  The extra trailing
     argument ``spec`` (a PatternSpec or None) selects a non-reference pattern.
@@ -160,17 +161,24 @@ class MACoreAttentionFunction(torch.autograd.Function):
     def backward(ctx, grad_output: torch.Tensor) -> Tuple[Optional[torch.Tensor], ...]:
         query, key, value = ctx.saved_tensors
         spec = ctx.spec
-        if _HAS_SPARSE_CUDA and query.is_cuda and spec is None:
+        native = spec is None or spec.pattern in ("sliding", "dense")
+        if _HAS_SPARSE_CUDA and query.is_cuda and native:
+            ext = sparse_attention_cuda
             cq, ck, cv, cgo = (t.contiguous() for t in (query, key, value, grad_output))
-            if ctx.sparse:
-                dQ, dK, dV = sparse_attention_cuda.backward(cq, ck, cv, cgo, int(ctx.window_size))
+            cgo = cgo.to(cq.dtype)
+            if spec is not None and spec.pattern == "sliding":
+                dQ, dK, dV = ext.sliding_backward(cq, ck, cv, cgo, spec.left, spec.right, spec.dilation)
+            elif spec is not None:
+                dQ, dK, dV = ext.dense_backward(cq, ck, cv, cgo, spec.causal)
+            elif ctx.sparse:
+                dQ, dK, dV = ext.backward(cq, ck, cv, cgo, int(ctx.window_size))
             else:
-                dQ, dK, dV = sparse_attention_cuda.dense_backward(cq, ck, cv, cgo,
-                                                                  bool(ctx.use_causal_mask))
+                dQ, dK, dV = ext.dense_backward(cq, ck, cv, cgo, bool(ctx.use_causal_mask))
             return (dQ if ctx.needs_input_grad[0] else None,
                     dK if ctx.needs_input_grad[1] else None,
                     dV if ctx.needs_input_grad[2] else None, None, None, None, None)
-        # Recompute with the PyTorch implementation and differentiate (:140-154)
+        # Block-sparse / Longformer (no native backward) and host tensors:
+        # recompute with the PyTorch implementation and differentiate (:140-154)
         with torch.enable_grad():
             q, k, v = (t.detach().requires_grad_(True) for t in (query, key, value))
             if spec is not None:

@@ -18,7 +18,7 @@ LIB_PATH = os.environ.get("MA_ATTN_LIB", os.path.join(_HERE, "libma_attn.so"))
 
 F32, BF16, F16 = 0, 1, 2
 SLIDING, DENSE, BLOCK_SPARSE, LONGFORMER = 0, 1, 2, 3
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 
@@ -61,6 +61,11 @@ def _open():
     lib.ma_attn_workspace_size.argtypes = [ctypes.POINTER(Desc)]
     lib.ma_attn_forward.restype = ctypes.c_int
     lib.ma_attn_forward.argtypes = [ctypes.POINTER(Desc)] + [ctypes.c_void_p] * 5 + \
+        [ctypes.c_size_t, ctypes.c_void_p]
+    lib.ma_attn_backward_workspace_size.restype = ctypes.c_size_t
+    lib.ma_attn_backward_workspace_size.argtypes = [ctypes.POINTER(Desc)]
+    lib.ma_attn_backward.restype = ctypes.c_int
+    lib.ma_attn_backward.argtypes = [ctypes.POINTER(Desc)] + [ctypes.c_void_p] * 8 + \
         [ctypes.c_size_t, ctypes.c_void_p]
     lib.ma_attn_block_table.restype = ctypes.c_int
     lib.ma_attn_block_table.argtypes = [ctypes.c_uint64, ctypes.c_int64, ctypes.c_int64,
@@ -110,6 +115,19 @@ def forward_raw(desc: Desc, q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int,
     """Launch on ``stream`` (a hipStream_t as int).  Raises RuntimeError on rejection."""
     rc = LIB.ma_attn_forward(ctypes.byref(desc), q_ptr, k_ptr, v_ptr, o_ptr, ws_ptr or None,
                              ws_bytes, stream or None)
+    if rc != 0:
+        raise RuntimeError(last_error())
+
+
+def backward_workspace_size(desc: Desc) -> int:
+    return int(LIB.ma_attn_backward_workspace_size(ctypes.byref(desc)))
+
+
+def backward_raw(desc: Desc, q_ptr: int, k_ptr: int, v_ptr: int, g_ptr: int, dq_ptr: int,
+                 dk_ptr: int, dv_ptr: int, ws_ptr: int, ws_bytes: int, stream: int = 0) -> None:
+    """Launch the backward on ``stream``.  Raises RuntimeError on rejection."""
+    rc = LIB.ma_attn_backward(ctypes.byref(desc), q_ptr, k_ptr, v_ptr, g_ptr, dq_ptr, dk_ptr, dv_ptr,
+                              ws_ptr or None, ws_bytes, stream or None)
     if rc != 0:
         raise RuntimeError(last_error())
 

@@ -22,10 +22,11 @@ New pattern entry points (not in the reference):
     longformer_forward(q, k, v, left, right=0, num_global=16)
     make_block_table(seed, num_blocks, random_per_row=2)
 
-The forward passes are hand-written HIP kernels (libma_attn.so).  The two
-backward entry points recompute the pattern's attention with torch autograd
-on the device (no HIP backward kernel yet); they exist so that
-``MACoreAttentionFunction.backward`` keeps its reference behaviour.
+Forward and backward are hand-written HIP kernels (libma_attn.so).  The
+backward recomputes the softmax from q, k, v as the reference's does, for the
+sliding and dense patterns, in the input dtype:
+
+    sliding_backward(q, k, v, grad_out, left, right, dilation=1) -> [dQ, dK, dV]
 """
 from __future__ import annotations
 
@@ -36,7 +37,8 @@ import torch
 import ma_attn as _ma
 
 __all__ = ["forward", "dense_forward", "backward", "dense_backward", "sliding_forward",
-           "block_sparse_forward", "longformer_forward", "make_block_table", "BlockTable"]
+           "sliding_backward", "block_sparse_forward", "longformer_forward", "make_block_table",
+           "BlockTable"]
 
 
 def _check(*ts: torch.Tensor) -> None:
@@ -187,45 +189,35 @@ def longformer_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tens
                    num_global=int(num_global))
 
 
-# ---------------------------------------------------------------- backward (torch autograd)
+# ---------------------------------------------------------------- backward (HIP kernels)
 
-def _pattern_mask(N: int, device, window_size=None, causal=None) -> torch.Tensor:
-    i = torch.arange(N, device=device).unsqueeze(1)
-    j = torch.arange(N, device=device).unsqueeze(0)
-    if window_size is not None:
-        return (j >= i - window_size) & (j <= i + window_size)
-    if causal:
-        return j <= i
-    return torch.ones(N, N, dtype=torch.bool, device=device)
-
-
-def _masked_attention_f32(q, k, v, mask):
-    B, N, H, D = q.shape
-    scale = _ma.default_scale(D)
-    qh, kh, vh = (t.float().permute(0, 2, 1, 3).contiguous() for t in (q, k, v))
-    s = torch.matmul(qh, kh.transpose(-1, -2).contiguous()) * scale
-    s = s.masked_fill(~mask, float("-inf"))
-    p = torch.softmax(s, dim=-1)
-    p = torch.nan_to_num(p, nan=0.0)  # empty rows
-    return torch.matmul(p, vh).permute(0, 2, 1, 3)
-
-
-def _grads(q, k, v, grad_out, mask) -> List[torch.Tensor]:
+def _backward(q, k, v, grad_out, pattern, **kw) -> List[torch.Tensor]:
     _check(q, k, v, grad_out)
-    with torch.enable_grad():
-        qq, kk, vv = (t.detach().requires_grad_(True) for t in (q, k, v))
-        out = _masked_attention_f32(qq, kk, vv, mask)
-        dq, dk, dv = torch.autograd.grad(out, (qq, kk, vv), grad_out.float())
-    return [dq.to(q.dtype).contiguous(), dk.to(q.dtype).contiguous(), dv.to(q.dtype).contiguous()]
+    B, N, H, D = q.shape
+    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+    desc = _ma.make_desc(B, N, H, D, _ma.DTYPES[q.dtype], pattern, **kw)
+    nbytes = _ma.backward_workspace_size(desc)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        _ma.backward_raw(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), grad_out.data_ptr(),
+                         dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), nbytes, stream)
+    return [dq, dk, dv]
 
 
 def backward(query, key, value, grad_out, window_size: int = 64) -> List[torch.Tensor]:
-    """dQ, dK, dV of forward(); reference sparse_backward_cuda (:460-497)."""
-    mask = _pattern_mask(query.shape[1], query.device, window_size=int(window_size))
-    return _grads(query, key, value, grad_out, mask)
+    """dQ, dK, dV of forward(); reference sparse_backward_cuda (.cu:459-497, kernel :265-346)."""
+    w = int(window_size)
+    return _backward(query, key, value, grad_out, _ma.SLIDING, left=w, right=w, dilation=1)
 
 
 def dense_backward(query, key, value, grad_out, use_causal_mask: bool = False) -> List[torch.Tensor]:
-    """dQ, dK, dV of dense_forward(); reference dense_backward_cuda (:384-421)."""
-    mask = _pattern_mask(query.shape[1], query.device, causal=bool(use_causal_mask))
-    return _grads(query, key, value, grad_out, mask)
+    """dQ, dK, dV of dense_forward(); reference dense_backward_cuda (.cu:383-418, kernel :104-175)."""
+    return _backward(query, key, value, grad_out, _ma.DENSE, causal=bool(use_causal_mask))
+
+
+def sliding_backward(query, key, value, grad_out, left: int, right: int,
+                     dilation: int = 1) -> List[torch.Tensor]:
+    """dQ, dK, dV of sliding_forward() (keys {i + dilation*t : -left <= t <= right})."""
+    return _backward(query, key, value, grad_out, _ma.SLIDING, left=int(left), right=int(right),
+                     dilation=int(dilation))

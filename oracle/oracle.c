@@ -1,5 +1,6 @@
 /*
- * oracle.c -- CPU restatement of the reference sparse-attention forward.
+ * oracle.c -- CPU restatement of the reference sparse-attention forward and
+ * backward.
  *
  * TEST INFRASTRUCTURE ONLY.  This file is the parity checker for the HIP
  * engine and the CPU baseline timed by bench.py.  Only tests/,
@@ -174,6 +175,83 @@ int oracle_forward_f32(const oracle_spec* s, const float* q, const float* k,
   }
   free(keys);
   free(scores);
+  return 0;
+}
+
+/*
+ * fp32 backward: dq, dk, dv (each [B,N,H,D], zero-filled here) for
+ * dout = dL/dO, restating sparse_attention_backward_kernel
+ * (/root/reference src/cuda/sparse_attention_kernel.cu:265-346; the dense
+ * twin :104-175 is the same with keys [0,N) or [0,i]) per query row i:
+ *   1) s_t = (sum_d q[d]*k[j_t][d]) * scale; m = max_t s_t;
+ *      sum = sum_t expf(s_t - m), 1 if 0                      (:285-304)
+ *   2) p_t = expf(s_t - m) / sum; dp_t = sum_d dout[d]*v[j_t][d];
+ *      sdot += dp_t * p_t; dv[j_t] += p_t * dout              (:306-323)
+ *   3) ds_t = (dp_t - sdot) * p_t; dq += ds_t*scale*k[j_t];
+ *      dk[j_t] += ds_t*scale*q                                (:325-345)
+ * over the pattern's ascending key list (oracle_row_keys).  The reference's
+ * atomicAdd order across rows is unspecified; here rows accumulate in
+ * ascending (b, h, i) order.
+ */
+int oracle_backward_f32(const oracle_spec* s, const float* q, const float* k,
+                        const float* v, const float* dout, float* dq, float* dk,
+                        float* dv) {
+  const int64_t N = s->N, H = s->H, D = s->D, B = s->B;
+  if (N < 0 || H < 0 || D <= 0 || B < 0) return -1;
+  const float scale = 1.0f / sqrtf((float)D);
+  const int64_t total = B * N * H * D;
+  for (int64_t x = 0; x < total; ++x) dq[x] = dk[x] = dv[x] = 0.0f;
+  int64_t cap = N > 0 ? N : 1;
+  int64_t* keys = (int64_t*)malloc(sizeof(int64_t) * (size_t)cap);
+  float* sc = (float*)malloc(sizeof(float) * (size_t)cap);
+  float* dp = (float*)malloc(sizeof(float) * (size_t)cap);
+  if (!keys || !sc || !dp) {
+    free(keys);
+    free(sc);
+    free(dp);
+    return -1;
+  }
+  for (int64_t b = 0; b < B; ++b) {
+    for (int64_t h = 0; h < H; ++h) {
+      for (int64_t i = 0; i < N; ++i) {
+        const int64_t ri = ((b * N + i) * H + h) * D;
+        const int64_t n = oracle_row_keys(s, i, keys, cap);
+        if (n <= 0) continue;
+        float m = -INFINITY;
+        for (int64_t t = 0; t < n; ++t) {
+          const float* kj = k + ((b * N + keys[t]) * H + h) * D;
+          float dot = 0.0f;
+          for (int64_t d = 0; d < D; ++d) dot += q[ri + d] * kj[d];
+          sc[t] = dot * scale;
+          if (sc[t] > m) m = sc[t];
+        }
+        float sum = 0.0f;
+        for (int64_t t = 0; t < n; ++t) sum += expf(sc[t] - m);
+        if (sum == 0.0f) sum = 1.0f;
+        float sdot = 0.0f;
+        for (int64_t t = 0; t < n; ++t) {
+          const int64_t rj = ((b * N + keys[t]) * H + h) * D;
+          sc[t] = expf(sc[t] - m) / sum; /* p_t from here on */
+          float acc = 0.0f;
+          for (int64_t d = 0; d < D; ++d) acc += dout[ri + d] * v[rj + d];
+          dp[t] = acc;
+          sdot += acc * sc[t];
+          for (int64_t d = 0; d < D; ++d) dv[rj + d] += sc[t] * dout[ri + d];
+        }
+        for (int64_t t = 0; t < n; ++t) {
+          const int64_t rj = ((b * N + keys[t]) * H + h) * D;
+          const float ds = (dp[t] - sdot) * sc[t];
+          for (int64_t d = 0; d < D; ++d) {
+            dq[ri + d] += ds * scale * k[rj + d];
+            dk[rj + d] += ds * scale * q[ri + d];
+          }
+        }
+      }
+    }
+  }
+  free(keys);
+  free(sc);
+  free(dp);
   return 0;
 }
 

@@ -1,4 +1,4 @@
-"""CPU oracle for the sparse-attention forward -- TEST INFRASTRUCTURE ONLY.
+"""CPU oracle for the sparse-attention forward and backward -- TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline
 leg import this module, and only as the checker / the timed CPU baseline.  The
@@ -15,6 +15,9 @@ Three independent statements of the same semantics live here:
   golden ``pytorch_sparse_attention``, src/layers/ma_core_bridge.py:224-247).
 * ``member`` -- a brute-force membership predicate per pattern, used on tiny
   shapes to pin ``row_keys`` (the closed forms) bit-exactly.
+* ``backward`` -- oracle.c's restatement of the reference's backward kernel
+  (src/cuda/sparse_attention_kernel.cu:265-346) over the same key lists,
+  pinned by float64 autograd and by finite differences of ``forward_f64``.
 
 ``ref_*`` wrap ``_ref/libma_core_ref.so``: the reference's own ma_core.cpp and
 tensor.cpp compiled unchanged (see Makefile).  It exists only where it was
@@ -68,6 +71,8 @@ def _load():
         lib.oracle_forward_f32.restype = ctypes.c_int
         lib.oracle_forward_f32.argtypes = [ctypes.POINTER(_Spec)] + [ctypes.c_void_p] * 4 + \
             [ctypes.c_int64] * 4
+        lib.oracle_backward_f32.restype = ctypes.c_int
+        lib.oracle_backward_f32.argtypes = [ctypes.POINTER(_Spec)] + [ctypes.c_void_p] * 7
         lib.oracle_block_table.restype = ctypes.c_int
         lib.oracle_block_table.argtypes = [ctypes.c_uint64, ctypes.c_int64, ctypes.c_int64,
                                            ctypes.POINTER(ctypes.c_int32)]
@@ -136,6 +141,19 @@ def forward(spec: Spec, q, k, v, heads=None, rows=None) -> np.ndarray:
     if rc != 0:
         raise ValueError("oracle_forward_f32 rejected the spec")
     return o
+
+
+def backward(spec: Spec, q, k, v, dout):
+    """fp32 oracle backward (restated sparse_attention_kernel.cu:265-346) -> (dq, dk, dv)."""
+    lib = _load()
+    q, k, v, dout = (np.ascontiguousarray(x, dtype=np.float32) for x in (q, k, v, dout))
+    dq, dk, dv = (np.empty(q.shape, dtype=np.float32) for _ in range(3))
+    s = spec._c()
+    rc = lib.oracle_backward_f32(ctypes.byref(s), q.ctypes.data, k.ctypes.data, v.ctypes.data,
+                                 dout.ctypes.data, dq.ctypes.data, dk.ctypes.data, dv.ctypes.data)
+    if rc != 0:
+        raise ValueError("oracle_backward_f32 rejected the spec")
+    return dq, dk, dv
 
 
 def block_table(seed: int, num_blocks: int, random_per_row: int) -> np.ndarray:

@@ -1,0 +1,167 @@
+"""GPU parity of the HIP backward (ma_attn_backward through sparse_attention_cuda)
+against the CPU oracle's restatement of the reference backward kernel
+(src/cuda/sparse_attention_kernel.cu:265-346; dense :104-175).
+
+Tolerances: float32 max-abs <= 1e-4 (sums of up to a few hundred products per
+gradient element, in another order than the oracle's); bfloat16 / float16
+max-abs <= 1e-2 * max(1, max|grad|) -- the kernels compute in fp32 on the
+16-bit inputs and round each gradient once to the input dtype (2^-8 relative
+for bf16).  The reference's own tests compare against torch autograd at
+1e-3 / 2e-3 (test_cuda_backward.py:75-101, test_cuda_extensive.py:168-193);
+those checks are repeated here as written.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import qkv, randn
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ext():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    import sparse_attention_cuda
+    return sparse_attention_cuda
+
+
+def _dev(x, dtype):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dtype).to("cuda")
+
+
+def _case(shape, seed, dtype):
+    q, k, v = qkv(shape, seed)
+    g = randn(shape, seed + 1)
+    dev = [_dev(a, dtype) for a in (q, k, v, g)]
+    up = [t.float().cpu().numpy() for t in dev]
+    return dev, up
+
+
+def _check(got, ref, dtype):
+    for name, a, b in zip("qkv", got, ref):
+        a = a.float().cpu().numpy()
+        assert np.isfinite(a).all(), f"d{name}: non-finite"
+        err = float(np.abs(a - b).max()) if a.size else 0.0
+        tol = 1e-4 if dtype == torch.float32 else 1e-2 * max(1.0, float(np.abs(b).max()) if b.size else 1.0)
+        print(f"  d{name}: max|err| = {err:.3e} (tol {tol:.1e})", flush=True)
+        assert err <= tol, (name, err)
+
+
+# ------------------------------------------------------- the reference's own tests
+
+def _torch_dense(q, k, v, causal=False):
+    B, S, H, D = q.shape
+    scale = 1.0 / (D ** 0.5)
+    qh, kh, vh = ((t * scale if i == 0 else t).transpose(1, 2).contiguous() for i, t in enumerate((q, k, v)))
+    s = torch.matmul(qh, kh.transpose(-2, -1).contiguous())
+    if causal:
+        s = s.masked_fill(~torch.tril(torch.ones(S, S, dtype=torch.bool, device=s.device)), -1e9)
+    return torch.matmul(torch.softmax(s, dim=-1), vh).transpose(1, 2).contiguous()
+
+
+def _torch_sparse(q, k, v, window):
+    B, S, H, D = q.shape
+    scale = 1.0 / (D ** 0.5)
+    i = torch.arange(S, device=q.device)
+    mask = (i.view(1, -1) >= i.view(-1, 1) - window) & (i.view(1, -1) <= i.view(-1, 1) + window)
+    qh, kh, vh = (t.transpose(1, 2).contiguous() for t in (q, k, v))
+    s = torch.matmul(qh * scale, kh.transpose(-2, -1).contiguous()).masked_fill(~mask, float("-inf"))
+    return torch.matmul(torch.softmax(s, dim=-1), vh).transpose(1, 2).contiguous()
+
+
+def _ref_grads(fn, q, k, v, loss):
+    q2, k2, v2 = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    loss(fn(q2, k2, v2)).backward()
+    return q2.grad, k2.grad, v2.grad
+
+
+def test_reference_dense_backward(ext):
+    """test_cuda_backward.py:48-73: B=1 S=8 H=2 D=4, atol = rtol = 1e-3."""
+    torch.manual_seed(0)
+    q, k, v = (torch.randn(1, 8, 2, 4, device="cuda") for _ in range(3))
+    dO = torch.ones_like(q)  # d(out.sum())/d(out)
+    got = ext.dense_backward(q, k, v, dO, False)
+    for a, b in zip(got, _ref_grads(_torch_dense, q, k, v, lambda o: o.sum())):
+        assert torch.allclose(a, b, atol=1e-3, rtol=1e-3)
+
+
+def test_reference_sparse_backward(ext):
+    """test_cuda_backward.py:75-101: B=1 S=10 H=2 D=4, window 2, atol = rtol = 1e-3."""
+    torch.manual_seed(0)
+    q, k, v = (torch.randn(1, 10, 2, 4, device="cuda") for _ in range(3))
+    got = ext.backward(q, k, v, torch.ones_like(q), 2)
+    for a, b in zip(got, _ref_grads(lambda a, b, c: _torch_sparse(a, b, c, 2), q, k, v, lambda o: o.sum())):
+        assert torch.allclose(a, b, atol=1e-3, rtol=1e-3)
+
+
+def test_reference_bridge_training_grads(ext):
+    """test_cuda_extensive.py:168-193: MACoreAttention(sparse, W=3, fallback_training=False)."""
+    from layers.ma_core_bridge import MACoreAttention
+    torch.manual_seed(10)
+    q, k, v = (torch.randn(2, 17, 2, 8, device="cuda", requires_grad=True) for _ in range(3))
+    attn = MACoreAttention(sparse=True, window_size=3, fallback_training=False)
+    attn(q, k, v).sin().pow(2).mean().backward()
+    ref = _ref_grads(lambda a, b, c: _torch_sparse(a, b, c, 3), q, k, v, lambda o: o.sin().pow(2).mean())
+    for a, b in zip((q.grad, k.grad, v.grad), ref):
+        assert (a - b).abs().max().item() < 2e-3
+
+
+# ------------------------------------------------------- against the oracle
+
+@pytest.mark.parametrize("N,left,right,dil", [
+    (1, 3, 3, 1), (10, 2, 2, 1), (65, 63, 0, 1), (300, 63, 0, 1), (257, 32, 31, 1),
+    (200, 0, 0, 1), (190, 5, 40, 1), (333, 63, 0, 4), (129, 2, 7, 3), (50, -1, -1, 1),
+])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_sliding_backward_geometry(ext, oracle, N, left, right, dil, dtype):
+    shape = (2, N, 3, 64)
+    (q, k, v, g), up = _case(shape, 700 + N + left + dil, dtype)
+    got = ext.sliding_backward(q, k, v, g, left, right, dil)
+    assert all(t.dtype == dtype and t.shape == q.shape for t in got)
+    spec = oracle.Spec(*shape, pattern="sliding", left=left, right=right, dilation=dil)
+    _check(got, oracle.backward(spec, *up), dtype)
+
+
+@pytest.mark.parametrize("shape", [(1, 7, 2, 16), (2, 33, 2, 40), (1, 20, 1, 130)])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_dense_backward_geometry(ext, oracle, shape, causal, dtype):
+    (q, k, v, g), up = _case(shape, 800 + shape[1] + causal, dtype)
+    got = ext.dense_backward(q, k, v, g, causal)
+    spec = oracle.Spec(*shape, pattern="dense", causal=causal)
+    _check(got, oracle.backward(spec, *up), dtype)
+
+
+def test_backward_target_shape(ext, oracle):
+    """The headline shape in bf16 (B=1 H=8 N=65536 D=64, causal w=64): whole
+    gradients against the oracle."""
+    shape = (1, 65536, 8, 64)
+    (q, k, v, g), up = _case(shape, 900, torch.bfloat16)
+    got = ext.sliding_backward(q, k, v, g, 63, 0, 1)
+    spec = oracle.Spec(*shape, pattern="sliding", left=63, right=0)
+    _check(got, oracle.backward(spec, *up), torch.bfloat16)
+
+
+@pytest.mark.parametrize("left,right,dil", [(63, 0, 1), (32, 31, 1), (63, 0, 4)])
+def test_backward_sum_identities_full_size(ext, left, right, dil):
+    """fp32 at B=1 H=8 N=65536 D=64: rows of P sum to 1 and rows of dS to 0,
+    so per head sum_j dV_j = sum_i dout_i and sum_j dK_j = 0."""
+    shape = (1, 65536, 8, 64)
+    gen = torch.Generator(device="cuda").manual_seed(5 + left + dil)
+    q, k, v, g = (torch.randn(shape, device="cuda", generator=gen) for _ in range(4))
+    dq, dk, dv = ext.sliding_backward(q, k, v, g, left, right, dil)
+    gs = g.double().sum(dim=1)
+    assert (dv.double().sum(dim=1) - gs).abs().max().item() <= 1e-2
+    assert dk.double().sum(dim=1).abs().max().item() <= 1e-2
+
+
+def test_backward_rejects_unsupported(ext):
+    q = torch.randn(1, 64, 1, 64, device="cuda", dtype=torch.bfloat16)
+    from ma_attn import BLOCK_SPARSE, LONGFORMER
+    for pat in (BLOCK_SPARSE, LONGFORMER):
+        with pytest.raises(RuntimeError):
+            ext._backward(q, q, q, q, pat, num_global=4)
+    with pytest.raises(RuntimeError):
+        ext.backward(q, q, q, q.float())  # mixed dtypes

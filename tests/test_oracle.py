@@ -214,3 +214,81 @@ def test_special_cases(oracle):
     assert np.array_equal(a, b)
     # empty window => zero rows
     assert not oracle.forward(_spec(oracle, shape, pattern="sliding", left=-1, right=-1), q, k, v).any()
+
+
+# ----------------------------------------------------------------- backward
+
+def _autograd_f64(q, k, v, dout, mask):
+    """torch float64 autograd of dense-masked softmax(QK^T * scale)V (CPU)."""
+    import torch
+    t = [torch.tensor(x, dtype=torch.float64, requires_grad=True) for x in (q, k, v)]
+    B, N, H, D = q.shape
+    scale = 1.0 / float(np.sqrt(np.float32(D)))
+    qh, kh, vh = (x.permute(0, 2, 1, 3) for x in t)
+    s = torch.matmul(qh, kh.transpose(-1, -2).contiguous()) * scale
+    m = torch.tensor(mask)
+    s = s.masked_fill(~m, float("-inf"))
+    p = torch.nan_to_num(torch.softmax(s, dim=-1), nan=0.0)
+    o = torch.matmul(p, vh).permute(0, 2, 1, 3)
+    o.backward(torch.tensor(dout, dtype=torch.float64))
+    return [x.grad.numpy() for x in t]
+
+
+@pytest.mark.parametrize("pattern,kw", PATTERN_CASES)
+def test_oracle_backward_vs_autograd(oracle, pattern, kw):
+    """Restated .cu:265-346 against float64 autograd of textbook attention."""
+    shape = (2, 40, 2, 16)
+    q, k, v = qkv(shape, 31)
+    dout = randn(shape, 32)
+    s = _spec(oracle, shape, pattern=pattern, **kw)
+    got = oracle.backward(s, q, k, v, dout)
+    ref = _autograd_f64(q, k, v, dout, oracle.mask_dense(s))
+    for g, r in zip(got, ref):
+        assert np.abs(g - r).max() <= 2e-5
+
+
+def test_oracle_backward_block_sparse_vs_autograd(oracle):
+    shape = (1, 70, 2, 8)
+    q, k, v = qkv(shape, 33)
+    dout = randn(shape, 34)
+    s = _spec(oracle, shape, pattern="block_sparse", block_size=8, table=_table(oracle, 70, 8, 2, 3))
+    for g, r in zip(oracle.backward(s, q, k, v, dout), _autograd_f64(q, k, v, dout, oracle.mask_dense(s))):
+        assert np.abs(g - r).max() <= 2e-5
+
+
+@pytest.mark.parametrize("pattern,kw", [("sliding", dict(left=2, right=1)), ("sliding", dict(left=3, right=0, dilation=2)),
+                                        ("dense", dict(causal=True)), ("longformer", dict(left=2, right=0, num_global=2))])
+def test_oracle_backward_finite_differences(oracle, pattern, kw):
+    """Central differences of the float64 forward, L = sum(O * dout): no gradient formula involved."""
+    shape = (1, 7, 1, 3)
+    q, k, v = qkv(shape, 35)
+    dout = randn(shape, 36)
+    s = _spec(oracle, shape, pattern=pattern, **kw)
+    mask = oracle.mask_dense(s)
+    got = oracle.backward(s, q, k, v, dout)
+    x = [a.astype(np.float64) for a in (q, k, v)]
+    eps = 1e-6
+    for which in range(3):
+        fd = np.zeros_like(x[which])
+        for idx in np.ndindex(*shape):
+            for sgn in (1, -1):
+                y = [a.copy() for a in x]
+                y[which][idx] += sgn * eps
+                fd[idx] += sgn * float((oracle.forward_f64(*y, mask) * dout).sum()) / (2 * eps)
+        assert np.abs(got[which] - fd).max() <= 2e-5, which
+
+
+def test_oracle_backward_special_cases(oracle):
+    shape = (2, 30, 2, 8)
+    q, k, v = qkv(shape, 37)
+    dout = randn(shape, 38)
+    # w = 0: O = V, so dV = dout and dQ = dK = 0 exactly
+    dq, dk, dv = oracle.backward(_spec(oracle, shape, pattern="sliding", left=0, right=0), q, k, v, dout)
+    assert np.array_equal(dv, dout) and not dq.any() and not dk.any()
+    # empty window: all zero
+    assert not any(g.any() for g in oracle.backward(_spec(oracle, shape, pattern="sliding", left=-1, right=-1),
+                                                    q, k, v, dout))
+    # rows of P sum to 1 => sum_j dV_j = sum_i dout_i; rows of dS sum to 0 => sum_j dK_j = 0
+    dq, dk, dv = oracle.backward(_spec(oracle, shape, pattern="sliding", left=4, right=2, dilation=2), q, k, v, dout)
+    assert np.abs(dv.sum(axis=1) - dout.sum(axis=1)).max() <= 1e-4
+    assert np.abs(dk.sum(axis=1)).max() <= 1e-4
