@@ -23,7 +23,9 @@ CUDA_AVAILABLE = False     # the reference's legacy ma_transformer_cuda path (:1
 class SparseAttention(nn.Module):
     """Sliding-window attention; priority engine > PyTorch fallback."""
 
-    def __init__(self, window_size=3, use_ma_core=True):
+    def __init__(self, window_size=3, use_ma_core=True, *, fallback_training=True):
+        """fallback_training (keyword-only, not in the reference): False runs
+        the native forward and backward kernels in training mode too."""
         super().__init__()
         if not isinstance(window_size, int):
             raise TypeError("window_size must be an integer for SparseAttention")
@@ -33,7 +35,7 @@ class SparseAttention(nn.Module):
         self.use_ma_core = use_ma_core
         if MA_CORE_AVAILABLE and use_ma_core:
             self.ma_core_attention = MACoreAttention(sparse=True, window_size=window_size,
-                                                     fallback_training=True)
+                                                     fallback_training=fallback_training)
 
     def forward(self, q, k, v):
         """q, k, v: [batch, seq_len, model_dim] -> [batch, seq_len, model_dim]."""
