@@ -45,6 +45,7 @@ struct StreamArgs {
   float scale_log2;   // softmax scale * log2(e)
   int32_t num_global;  // Longformer: global tokens 0..G-1 (G <= 16)
   float* partials;     // Longformer: [B*H][chunks*4][16][kPartial] per-wave softmax partials of the global rows
+  int32_t pairs;       // 1: chunks 2p and 2p+1 share an XCD (grid a multiple of 16, chunks even)
 };
 
 // One partial of a global query row: unnormalised O (64), running max of the
@@ -499,8 +500,15 @@ __global__ __launch_bounds__(256, LG ? 2 : P::kMinBlocks) void stream_kernel(Str
   // round-robin, so every XCD holds every head and chunks spread over the
   // whole sequence.  Orders that give an XCD one head, or one contiguous token
   // range, measured 17-30 % slower on the target (HBM channel locality);
-  // hashed orders measured the same as this one.
+  // hashed orders measured the same as this one.  With `pairs`, chunks 2p and
+  // 2p+1 run on one XCD (pairs still dealt round-robin) and walk towards each
+  // other's boundary, so the halo block they share is fetched once into that
+  // XCD's L2.
   int lin = blockIdx.x;
+  if (a.pairs) {  // ids 8i + x (XCD x): pair 8(i/2) + x, member i&1
+    const int x = lin & 7, i = lin >> 3;
+    lin = 16 * (i >> 1) + 2 * x + (i & 1);
+  }
   const int chunk_id = lin % a.chunks;
   lin /= a.chunks;
   const int rho = lin % a.dil;
@@ -546,10 +554,12 @@ __global__ __launch_bounds__(256, LG ? 2 : P::kMinBlocks) void stream_kernel(Str
   // descend, so two neighbouring chunks read the K/V blocks on their common
   // boundary at the same moment (both at their first tiles or both at their
   // last) and the second read can be served from cache (cfg2 window: 40.5 ->
-  // 38.3 us); causal windows measured faster all ascending (58.5 vs 59.9 us).
+  // 38.3 us); causal windows measured faster all ascending (58.5 vs 59.9 us)
+  // in the plain order.  With pairs and no right halo the even chunk of a
+  // pair descends, so it reads its last block (the odd chunk's halo) first.
   // The ring works either way: a step down needs the 64/rows slots below the
   // current band, and they replace the slots at its top.
-  const int dir = (R > 0 && (chunk_id & 1)) ? -1 : 1;
+  const int dir = R > 0 ? ((chunk_id & 1) ? -1 : 1) : (a.pairs && !(chunk_id & 1) ? -1 : 1);
   const int tfirst = dir > 0 ? t0 : t1 - 1;
   auto blo_of = [&](int t) { return floordiv32(t * 64 - L, RS); };
   auto bhi_of = [&](int t) { return floordiv32(t * 64 + 63 + R, RS); };
