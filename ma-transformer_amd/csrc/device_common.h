@@ -86,6 +86,14 @@ __device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off)
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
 
+__device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+}
+
+__device__ __forceinline__ void bstore8(__amdgpu_buffer_rsrc_t r, uint32_t off, uint2 x) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, x), r, (int)off, 0, 0);
+}
+
 __device__ __forceinline__ void bstore16(__amdgpu_buffer_rsrc_t r, uint32_t off, uint4 x) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, x), r, (int)off, 0, 0);
 }

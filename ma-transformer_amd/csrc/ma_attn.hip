@@ -32,6 +32,7 @@
 #include "pattern.h"
 #include "stream_kernel.h"
 #include "block_kernel.h"
+#include "backward_kernel.h"
 
 namespace {
 
@@ -893,6 +894,76 @@ ma::PatternParams transposed_params(const ma_attn_desc* d) {
   return p;
 }
 
+// MFMA backward: 16-bit, head_dim 64, 16-byte aligned tensors, banded sets
+// whose band holds the query's own key (SLIDING with left, right >= 0;
+// DENSE as the band [i-(N-1), i] or [i-(N-1), i+(N-1)]).
+bool bwd_band(const ma_attn_desc* d, int64_t* left, int64_t* right, int64_t* dil) {
+  if (d->pattern == MA_ATTN_DENSE) {
+    *left = d->seq_len - 1;
+    *right = d->causal ? 0 : d->seq_len - 1;
+    *dil = 1;
+    return true;
+  }
+  if (d->pattern != MA_ATTN_SLIDING || d->left < 0 || d->right < 0) return false;
+  *left = d->left;
+  *right = d->right;
+  *dil = d->dilation;
+  return true;
+}
+
+bool bwd_mfma_applies(const ma_attn_desc* d, const void* const* ptrs) {
+  if ((d->dtype != MA_ATTN_BF16 && d->dtype != MA_ATTN_F16) || d->head_dim != kHeadDim) return false;
+  for (int i = 0; i < 7; ++i)
+    if (!aligned16(ptrs[i])) return false;
+  int64_t L, R, dil;
+  if (!bwd_band(d, &L, &R, &dil)) return false;
+  const int64_t tb = dil * d->num_heads * kHeadDim * 2;
+  const int64_t nr = (d->seq_len + dil - 1) / dil;
+  const int64_t tiles = (nr + 63) / 64;
+  // byte offsets of rows (plus the out-of-range base) fit 32 bits; ids fit the grid
+  return (nr + 128) * tb < (1LL << 31) && nr * dil * d->num_heads * 8 < (1LL << 31) && L + R < (1LL << 30) &&
+         d->batch * d->num_heads * dil * tiles <= (int64_t)INT32_MAX;
+}
+
+template <class P>
+int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* stats, hipStream_t st) {
+  int64_t L, R, dil;
+  bwd_band(d, &L, &R, &dil);
+  BwdArgs a;
+  a.q = ptrs[0];
+  a.k = ptrs[1];
+  a.v = ptrs[2];
+  a.dout = ptrs[3];
+  a.dq = const_cast<void*>(ptrs[4]);
+  a.dk = const_cast<void*>(ptrs[5]);
+  a.dv = const_cast<void*>(ptrs[6]);
+  a.stats = stats;
+  a.N = d->seq_len;
+  a.H = d->num_heads;
+  a.left = (int32_t)L;
+  a.right = (int32_t)R;
+  a.dil = (int32_t)dil;
+  const int64_t nr = (d->seq_len + dil - 1) / dil;
+  a.tiles = (int32_t)((nr + 63) / 64);
+  a.tok_bytes = (int32_t)(dil * d->num_heads * kHeadDim * 2);
+  a.scale = scale_of(d);
+  a.scale_log2 = a.scale * 1.4426950408889634f;
+  const int64_t wgs = d->batch * d->num_heads * dil * a.tiles;
+  const size_t shm_q = 4 * (size_t)P::kSlot, shm_kv = 2 * (2 * (size_t)P::kSlot + 512);
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd_q_kernel<P>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm_q) != hipSuccess ||
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd_kv_kernel<P>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm_kv) != hipSuccess)
+      return fail("ma_attn_backward: cannot reserve LDS for the backward kernels");
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(bwd_q_kernel<P>, dim3((unsigned)wgs), dim3(256), shm_q, st, a);
+  hipLaunchKernelGGL(bwd_kv_kernel<P>, dim3((unsigned)wgs), dim3(256), shm_kv, st, a);
+  return 0;
+}
+
 template <typename T>
 int launch_backward(const ma_attn_desc* d, const void* q, const void* k, const void* v, const void* dout,
                     void* dq, void* dk, void* dv, RowStat* stats, hipStream_t st) {
@@ -1023,7 +1094,17 @@ int ma_attn_backward(const ma_attn_desc* desc, const void* q, const void* k, con
   hipStream_t st = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
   RowStat* stats = static_cast<RowStat*>(workspace);
+  const void* ptrs[7] = {q, k, v, dout, dq, dk, dv};
   int rc;
+  if (strcmp(kernel_override(), "rows") != 0 && bwd_mfma_applies(desc, ptrs)) {
+    rc = desc->dtype == MA_ATTN_BF16
+             ? launch_backward_mfma<HalfPath<__bf16>>(desc, ptrs, reinterpret_cast<float*>(stats), st)
+             : launch_backward_mfma<HalfPath<_Float16>>(desc, ptrs, reinterpret_cast<float*>(stats), st);
+    if (rc) return rc;
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail("ma_attn_backward: kernel launch failed: %s", hipGetErrorString(e));
+    return 0;
+  }
   switch (desc->dtype) {
     case MA_ATTN_F32:
       rc = launch_backward<float>(desc, q, k, v, dout, dq, dk, dv, stats, st);

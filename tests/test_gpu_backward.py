@@ -134,6 +134,29 @@ def test_dense_backward_geometry(ext, oracle, shape, causal, dtype):
     _check(got, oracle.backward(spec, *up), dtype)
 
 
+@pytest.mark.parametrize("N", [1, 64, 65, 300])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_dense_backward_mfma(ext, oracle, N, causal, dtype):
+    """head_dim 64, 16-bit: the MFMA backward with the band [i-(N-1), i(+N-1)]."""
+    shape = (2, N, 3, 64)
+    (q, k, v, g), up = _case(shape, 850 + N + causal, dtype)
+    got = ext.dense_backward(q, k, v, g, causal)
+    _check(got, oracle.backward(oracle.Spec(*shape, pattern="dense", causal=causal), *up), dtype)
+
+
+@pytest.mark.parametrize("N,left,right,dil", [(300, 63, 0, 1), (257, 32, 31, 4), (129, 2, 7, 3)])
+def test_sliding_backward_row_kernels(ext, oracle, monkeypatch, N, left, right, dil):
+    """The VALU row kernels for 16-bit head_dim 64 (the MFMA path's cases),
+    forced with MA_ATTN_KERNEL=rows, stay correct."""
+    monkeypatch.setenv("MA_ATTN_KERNEL", "rows")
+    shape = (2, N, 3, 64)
+    (q, k, v, g), up = _case(shape, 860 + N, torch.bfloat16)
+    got = ext.sliding_backward(q, k, v, g, left, right, dil)
+    spec = oracle.Spec(*shape, pattern="sliding", left=left, right=right, dilation=dil)
+    _check(got, oracle.backward(spec, *up), torch.bfloat16)
+
+
 def test_backward_target_shape(ext, oracle):
     """The headline shape in bf16 (B=1 H=8 N=65536 D=64, causal w=64): whole
     gradients against the oracle."""
