@@ -47,6 +47,7 @@ struct BwdArgs {
   int32_t tiles;             // 64-row tiles of the longest residue class
   int32_t tok_bytes;         // bytes between consecutive rows of a residue class
   float scale, scale_log2;
+  int32_t chunk, chunks;     // stream kernels: tiles per workgroup, workgroups per residue class
 };
 
 // Workgroup -> (b, h, rho, tile) and the residue class's resources.
@@ -86,6 +87,140 @@ __device__ __forceinline__ void bwd_mask(f32x4& z, int x, int span, int idx0, in
     z[r] = (uint32_t)(x + SGN * r) <= (uint32_t)span && idx0 + r < lim ? z[r] : -INFINITY;
 }
 
+// ---------------------------------------------------------------- per-block work
+//
+// One 64-row block of the streamed operand against this wave's 16 rows.
+
+// Scores S^T = K Q^T and dP^T = V dO^T of one key block (sk: (K, K^T) slot,
+// sv: (V, V^T) slot) for this wave's queries q0..q0+15, masked to the band.
+template <class P>
+__device__ __forceinline__ void bwdq_scores(const uint8_t* sk, const uint8_t* sv, uint32_t kl, const typename P::Q& qr,
+                                            const typename P::Q& gr, int key0, int q0, int L, int R, int dl, int g,
+                                            int Nr, f32x4 (&s)[4], f32x4 (&dp)[4]) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    s[u] = P::qk(sk + P::k_sub(u) + kl, qr);
+    dp[u] = P::qk(sv + P::k_sub(u) + kl, gr);
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int rel = key0 + 16 * u - q0;  // key - query offsets span [rel-15, rel+15]
+    if (rel - 15 < -L || rel + 15 > R || key0 + 16 * u + 15 >= Nr)
+      bwd_mask<1>(s[u], dl + rel, L + R, key0 + 16 * u + 4 * g, Nr);
+  }
+}
+
+// Pass 1: online max (m_run, raw scores), sum of e = exp2(s*sl2 - m) and of e*dp.
+__device__ __forceinline__ void bwdq_pass1(const f32x4 (&s)[4], const f32x4 (&dp)[4], float sl2, float& m_run,
+                                           float& l_run, float& a_run) {
+  float mx = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) mx = fmaxf(mx, fmaxf(fmaxf(s[u][0], s[u][1]), fmaxf(s[u][2], s[u][3])));
+  const float m_new = fmaxf(m_run, col_max(mx));
+  const float m_use = m_new == -INFINITY ? 0.0f : m_new * sl2;
+  const float corr = __builtin_amdgcn_exp2f(m_run * sl2 - m_use);
+  l_run *= corr;
+  a_run *= corr;
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float ex = __builtin_amdgcn_exp2f(fmaf(s[u][r], sl2, -m_use));
+      l_run += ex;
+      a_run = fmaf(ex, dp[u][r], a_run);
+    }
+  m_run = m_new;
+}
+
+// lse2 and delta of the wave's queries once pass 1 has seen the whole band
+// (every query sees its own key: left, right >= 0, so the sum is positive).
+__device__ __forceinline__ void bwdq_stats(float m_run, float l_run, float a_run, float sl2, float& lse2,
+                                           float& dlt) {
+  const float l_tot = col_sum(l_run);
+  lse2 = (m_run == -INFINITY ? 0.0f : m_run * sl2) + __log2f(l_tot);
+  dlt = col_sum(a_run) / l_tot;
+}
+
+// Pass 2: dS^T in registers, dQ^T += K^T dS^T (sk's K^T part).
+template <class P>
+__device__ __forceinline__ void bwdq_pass2(const uint8_t* sk, uint32_t vl, const f32x4 (&s)[4], const f32x4 (&dp)[4],
+                                           float sl2, float lse2, float dlt, f32x4 (&acc)[4]) {
+#pragma unroll
+  for (int u = 0; u < 4; u += 2) {
+    float d0[4], d1[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      d0[r] = __builtin_amdgcn_exp2f(fmaf(s[u][r], sl2, -lse2)) * (dp[u][r] - dlt);
+      d1[r] = __builtin_amdgcn_exp2f(fmaf(s[u + 1][r], sl2, -lse2)) * (dp[u + 1][r] - dlt);
+    }
+    P::pv2(sk + P::v_sub(u) + vl, sk + P::v_sub(u + 1) + vl, d0, d1, acc);
+  }
+}
+
+// One query block (sq: (Q, Q^T), sg: (dO, dO^T), st: 64 lse2 then 64 delta)
+// against this wave's keys k0..k0+15 (kr, vr: their K and V rows):
+// dV^T += dO^T P and dK^T += Q^T dS.
+template <class P>
+__device__ __forceinline__ void bwdkv_block(const uint8_t* sq, const uint8_t* sg, const float* st, uint32_t kl,
+                                            uint32_t vl, const typename P::Q& kr, const typename P::Q& vr, int qbase,
+                                            int k0, int L, int R, int dl, int g, int Nr, float sl2,
+                                            f32x4 (&acc_k)[4], f32x4 (&acc_v)[4]) {
+  f32x4 s[4], dp[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    s[u] = P::qk(sq + P::k_sub(u) + kl, kr);   // S[query 16u+4g+r][key c]
+    dp[u] = P::qk(sg + P::k_sub(u) + kl, vr);  // dP[query][key c]
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int rel = k0 - (qbase + 16 * u);  // key - query offsets span [rel-15, rel+15]
+    if (rel - 15 < -L || rel + 15 > R || qbase + 16 * u + 15 >= Nr)
+      bwd_mask<-1>(s[u], dl + rel, L + R, qbase + 16 * u + 4 * g, Nr);
+  }
+#pragma unroll
+  for (int u = 0; u < 4; u += 2) {
+    const f32x4 lse0 = *reinterpret_cast<const f32x4*>(st + 16 * u + 4 * g);
+    const f32x4 dl0 = *reinterpret_cast<const f32x4*>(st + 64 + 16 * u + 4 * g);
+    const f32x4 lse1 = *reinterpret_cast<const f32x4*>(st + 16 * (u + 1) + 4 * g);
+    const f32x4 dl1 = *reinterpret_cast<const f32x4*>(st + 64 + 16 * (u + 1) + 4 * g);
+    float p0[4], p1[4], d0[4], d1[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p0[r] = __builtin_amdgcn_exp2f(fmaf(s[u][r], sl2, -lse0[r]));
+      p1[r] = __builtin_amdgcn_exp2f(fmaf(s[u + 1][r], sl2, -lse1[r]));
+      d0[r] = p0[r] * (dp[u][r] - dl0[r]);
+      d1[r] = p1[r] * (dp[u + 1][r] - dl1[r]);
+    }
+    P::pv2(sg + P::v_sub(u) + vl, sg + P::v_sub(u + 1) + vl, p0, p1, acc_v);  // dV^T += dO^T P
+    P::pv2(sq + P::v_sub(u) + vl, sq + P::v_sub(u + 1) + vl, d0, d1, acc_k);  // dK^T += Q^T dS
+  }
+}
+
+// Query block's statistics staged by threads 0..63 (row tid of the block).
+__device__ __forceinline__ void bwd_stage_stats(uint8_t* st, uint2 xs, int tid) {
+  if (tid < 64) {
+    float* f = reinterpret_cast<float*>(st);
+    f[tid] = __uint_as_float(xs.x);       // lse2
+    f[64 + tid] = __uint_as_float(xs.y);  // delta
+  }
+}
+
+// Statistics of a residue class: row m at float2 index m * dil * H.
+struct BwdStats {
+  __amdgpu_buffer_rsrc_t r;
+  uint32_t stride;
+};
+
+__device__ __forceinline__ BwdStats bwd_stats_rsrc(const BwdArgs& a, int b, int h, int rho, int Nr) {
+  const int64_t sbase = ((int64_t)b * a.N + rho) * a.H + h;
+  BwdStats st;
+  st.stride = (uint32_t)(a.dil * a.H) * 8u;
+  st.r = make_rsrc(a.stats + 2 * sbase, (uint32_t)(Nr - 1) * st.stride + 8u);
+  return st;
+}
+
+// ---------------------------------------------------------------- one tile per workgroup
+
 template <class P>
 __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 buffers x (K slot, V slot)
@@ -119,8 +254,12 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
   const int kb_hi = min(floordiv32(64 * w.t + 63 + R, 64), w.nblk - 1);
   const int nb = kb_hi - kb_lo + 1;
   const int items = 2 * nb;  // pass 1, then pass 2 over the same blocks
+  // A band of at most two blocks stays resident in the two buffers for pass
+  // 2 (block j in buffer j); wider bands stream through them twice.
+  const bool resident = nb <= 2;
   auto blk_of = [&](int e) { return kb_lo + (e < nb ? e : e - nb); };
-  auto off_of = [&](int e) { return e < items ? (uint32_t)(64 * blk_of(e)) * tb : kOob; };
+  auto buf_of = [&](int e) { return resident ? (e < nb ? e : e - nb) : (e & 1); };
+  auto off_of = [&](int e) { return e < (resident ? nb : items) ? (uint32_t)(64 * blk_of(e)) * tb : kOob; };
 
   typename P::Slot xk, xv;
   P::load_slot(xk, Kr, Kr, off_of(0), tid, tb);
@@ -130,7 +269,6 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
   __syncthreads();
 
   const float sl2 = a.scale_log2;
-  const int span = L + R;
   const int dl = 4 * g - c + L;  // key - query + L of element 0, minus the sub-tile base
   float m_run = -INFINITY, l_run = 0.0f, a_run = 0.0f, lse2 = 0.0f, dlt = 0.0f;
   f32x4 acc[4];
@@ -140,60 +278,21 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
   for (int e = 0; e < items; ++e) {
     P::load_slot(xk, Kr, Kr, off_of(e + 1), tid, tb);
     P::load_slot(xv, Vr, Vr, off_of(e + 1), tid, tb);
-    const uint8_t* sk = ring + (e & 1) * kBuf;
-    const uint8_t* sv = sk + P::kSlot;
-    const int key0 = 64 * blk_of(e);
+    const uint8_t* sk = ring + buf_of(e) * kBuf;
     f32x4 s[4], dp[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      s[u] = P::qk(sk + P::k_sub(u) + kl, qr);
-      dp[u] = P::qk(sv + P::k_sub(u) + kl, gr);
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int rel = key0 + 16 * u - q0;  // key - query offsets span [rel-15, rel+15]
-      if (rel - 15 < -L || rel + 15 > R || key0 + 16 * u + 15 >= w.Nr)
-        bwd_mask<1>(s[u], dl + rel, span, key0 + 16 * u + 4 * g, w.Nr);
-    }
-    if (e < nb) {  // pass 1: online max, sum of e and of e * dp
-      float mx = -INFINITY;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) mx = fmaxf(mx, fmaxf(fmaxf(s[u][0], s[u][1]), fmaxf(s[u][2], s[u][3])));
-      const float m_new = fmaxf(m_run, col_max(mx));
-      const float m_use = m_new == -INFINITY ? 0.0f : m_new * sl2;
-      const float corr = __builtin_amdgcn_exp2f(m_run * sl2 - m_use);
-      l_run *= corr;
-      a_run *= corr;
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float ex = __builtin_amdgcn_exp2f(fmaf(s[u][r], sl2, -m_use));
-          l_run += ex;
-          a_run = fmaf(ex, dp[u][r], a_run);
-        }
-      m_run = m_new;
-      if (e == nb - 1) {  // every query sees its own key (left, right >= 0): l_tot > 0
-        const float l_tot = col_sum(l_run);
-        lse2 = m_use + __log2f(l_tot);
-        dlt = col_sum(a_run) / l_tot;
-      }
-    } else {  // pass 2: dS^T in registers, dQ^T += K^T dS^T
-#pragma unroll
-      for (int u = 0; u < 4; u += 2) {
-        float d0[4], d1[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          d0[r] = __builtin_amdgcn_exp2f(fmaf(s[u][r], sl2, -lse2)) * (dp[u][r] - dlt);
-          d1[r] = __builtin_amdgcn_exp2f(fmaf(s[u + 1][r], sl2, -lse2)) * (dp[u + 1][r] - dlt);
-        }
-        P::pv2(sk + P::v_sub(u) + vl, sk + P::v_sub(u + 1) + vl, d0, d1, acc);
-      }
+    bwdq_scores<P>(sk, sk + P::kSlot, kl, qr, gr, 64 * blk_of(e), q0, L, R, dl, g, w.Nr, s, dp);
+    if (e < nb) {  // pass 1
+      bwdq_pass1(s, dp, sl2, m_run, l_run, a_run);
+      if (e == nb - 1) bwdq_stats(m_run, l_run, a_run, sl2, lse2, dlt);
+    } else {  // pass 2
+      bwdq_pass2<P>(sk, vl, s, dp, sl2, lse2, dlt, acc);
     }
     // the next item goes into the buffer item e-1 used (every wave passed the
-    // barrier that ended item e-1)
-    P::store_slot(xk, ring + ((e + 1) & 1) * kBuf, tid);
-    P::store_slot(xv, ring + ((e + 1) & 1) * kBuf + P::kSlot, tid);
+    // barrier that ended item e-1); resident bands load nothing after pass 1
+    if (!resident || e + 1 < nb) {
+      P::store_slot(xk, ring + buf_of(e + 1) * kBuf, tid);
+      P::store_slot(xv, ring + buf_of(e + 1) * kBuf + P::kSlot, tid);
+    }
     __syncthreads();
   }
   P::store_o(acc, a.scale, DQr, qrow, g);
@@ -224,10 +323,7 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdArgs a) {
   const __amdgpu_buffer_rsrc_t Gr = make_rsrc(static_cast<const Elt*>(a.dout) + w.base, w.nrec);
   const __amdgpu_buffer_rsrc_t DKr = make_rsrc(static_cast<Elt*>(a.dk) + w.base, w.nrec);
   const __amdgpu_buffer_rsrc_t DVr = make_rsrc(static_cast<Elt*>(a.dv) + w.base, w.nrec);
-  // statistics of the class: row m at float2 index m * dil * H
-  const int64_t sbase = ((int64_t)w.b * a.N + w.rho) * a.H + w.h;
-  const uint32_t sstride = (uint32_t)(a.dil * a.H) * 8u;
-  const __amdgpu_buffer_rsrc_t Sr = make_rsrc(a.stats + 2 * sbase, (uint32_t)(w.Nr - 1) * sstride + 8u);
+  const BwdStats S = bwd_stats_rsrc(a, w.b, w.h, w.rho, w.Nr);
 
   const int k0 = 64 * w.t + 16 * wv;  // this wave's first key row
   const uint32_t krow = (uint32_t)(k0 + c) * tb;
@@ -242,27 +338,17 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdArgs a) {
   const int nb = qb_hi - qb_lo + 1;
   auto off_of = [&](int e) { return e < nb ? (uint32_t)(64 * (qb_lo + e)) * tb : kOob; };
   // thread tid < 64 carries the statistics of query row tid of the block
-  auto stat_off = [&](int e) { return e < nb && tid < 64 ? (uint32_t)(64 * (qb_lo + e) + tid) * sstride : kOob; };
+  auto stat_off = [&](int e) { return e < nb && tid < 64 ? (uint32_t)(64 * (qb_lo + e) + tid) * S.stride : kOob; };
 
   typename P::Slot xq, xg;
-  uint2 xs;
   P::load_slot(xq, Qr, Qr, off_of(0), tid, tb);
   P::load_slot(xg, Gr, Gr, off_of(0), tid, tb);
-  xs = bload8(Sr, stat_off(0));
-  auto stage = [&](uint8_t* buf) {
-    P::store_slot(xq, buf, tid);
-    P::store_slot(xg, buf + P::kSlot, tid);
-    if (tid < 64) {
-      float* st = reinterpret_cast<float*>(buf + 2 * P::kSlot);
-      st[tid] = __uint_as_float(xs.x);       // lse2
-      st[64 + tid] = __uint_as_float(xs.y);  // delta
-    }
-  };
-  stage(ring);
+  uint2 xs = bload8(S.r, stat_off(0));
+  P::store_slot(xq, ring, tid);
+  P::store_slot(xg, ring + P::kSlot, tid);
+  bwd_stage_stats(ring + 2 * P::kSlot, xs, tid);
   __syncthreads();
 
-  const float sl2 = a.scale_log2;
-  const int span = L + R;
   const int dl = c - 4 * g + L;  // key - query + L of element 0, minus the sub-tile base
   f32x4 acc_k[4], acc_v[4];
 #pragma unroll
@@ -271,45 +357,223 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdArgs a) {
   for (int e = 0; e < nb; ++e) {
     P::load_slot(xq, Qr, Qr, off_of(e + 1), tid, tb);
     P::load_slot(xg, Gr, Gr, off_of(e + 1), tid, tb);
-    xs = bload8(Sr, stat_off(e + 1));
+    xs = bload8(S.r, stat_off(e + 1));
     const uint8_t* sq = ring + (e & 1) * kBuf;
-    const uint8_t* sg = sq + P::kSlot;
-    const float* st = reinterpret_cast<const float*>(sq + 2 * P::kSlot);
-    const int qbase = 64 * (qb_lo + e);
-    f32x4 s[4], dp[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      s[u] = P::qk(sq + P::k_sub(u) + kl, kr);   // S[query 16u+4g+r][key c]
-      dp[u] = P::qk(sg + P::k_sub(u) + kl, vr);  // dP[query][key c]
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int rel = k0 - (qbase + 16 * u);  // key - query offsets span [rel-15, rel+15]
-      if (rel - 15 < -L || rel + 15 > R || qbase + 16 * u + 15 >= w.Nr)
-        bwd_mask<-1>(s[u], dl + rel, span, qbase + 16 * u + 4 * g, w.Nr);
-    }
-#pragma unroll
-    for (int u = 0; u < 4; u += 2) {
-      const f32x4 lse0 = *reinterpret_cast<const f32x4*>(st + 16 * u + 4 * g);
-      const f32x4 dl0 = *reinterpret_cast<const f32x4*>(st + 64 + 16 * u + 4 * g);
-      const f32x4 lse1 = *reinterpret_cast<const f32x4*>(st + 16 * (u + 1) + 4 * g);
-      const f32x4 dl1 = *reinterpret_cast<const f32x4*>(st + 64 + 16 * (u + 1) + 4 * g);
-      float p0[4], p1[4], d0[4], d1[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        p0[r] = __builtin_amdgcn_exp2f(fmaf(s[u][r], sl2, -lse0[r]));
-        p1[r] = __builtin_amdgcn_exp2f(fmaf(s[u + 1][r], sl2, -lse1[r]));
-        d0[r] = p0[r] * (dp[u][r] - dl0[r]);
-        d1[r] = p1[r] * (dp[u + 1][r] - dl1[r]);
-      }
-      P::pv2(sg + P::v_sub(u) + vl, sg + P::v_sub(u + 1) + vl, p0, p1, acc_v);  // dV^T += dO^T P
-      P::pv2(sq + P::v_sub(u) + vl, sq + P::v_sub(u + 1) + vl, d0, d1, acc_k);  // dK^T += Q^T dS
-    }
-    stage(ring + ((e + 1) & 1) * kBuf);
+    bwdkv_block<P>(sq, sq + P::kSlot, reinterpret_cast<const float*>(sq + 2 * P::kSlot), kl, vl, kr, vr,
+                   64 * (qb_lo + e), k0, L, R, dl, g, w.Nr, a.scale_log2, acc_k, acc_v);
+    uint8_t* nx = ring + ((e + 1) & 1) * kBuf;
+    P::store_slot(xq, nx, tid);
+    P::store_slot(xg, nx + P::kSlot, tid);
+    bwd_stage_stats(nx + 2 * P::kSlot, xs, tid);
     __syncthreads();
   }
   P::store_o(acc_v, 1.0f, DVr, krow, g);
   P::store_o(acc_k, a.scale, DKr, krow, g);
+}
+
+// ---------------------------------------------------------------- chunks of tiles per workgroup
+//
+// For bands of at most two 64-row blocks (windows like the BASELINE causal
+// 64): one workgroup streams a chunk of consecutive tiles of a residue class.
+// The band's two blocks sit in two LDS slots (block j in slot j & 1); moving
+// to tile t+1 adds at most one block, prefetched into registers while tile t
+// computes and written over the block tile t+1 no longer reads.  The next
+// tile's register rows are prefetched the same way.  Each block and row
+// crosses HBM once per chunk.
+
+struct BwdChunk {
+  int b, h, rho, t0, t1, Nr, nblk;
+  uint32_t tb;
+  int64_t base;
+  uint32_t nrec;
+};
+
+template <class P>
+__device__ __forceinline__ bool bwd_chunk(const BwdArgs& a, BwdChunk& w) {
+  int lin = blockIdx.x;
+  const int chunk_id = lin % a.chunks;
+  lin /= a.chunks;
+  w.rho = lin % a.dil;
+  lin /= a.dil;
+  w.h = lin % (int)a.H;
+  w.b = lin / (int)a.H;
+  w.Nr = (int)((a.N - w.rho + a.dil - 1) / a.dil);
+  w.nblk = (w.Nr + 63) >> 6;
+  w.t0 = chunk_id * a.chunk;
+  w.t1 = min(w.t0 + a.chunk, w.nblk);
+  w.tb = (uint32_t)a.tok_bytes;
+  w.base = (((int64_t)w.b * a.N + w.rho) * a.H + w.h) * kHeadDim;
+  w.nrec = (uint32_t)((int64_t)(w.Nr - 1) * w.tb + kHeadDim * sizeof(typename P::Elt));
+  return w.t0 < w.t1;
+}
+
+template <class P>
+__global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 slots x (K slot, V slot)
+  using Elt = typename P::Elt;
+  constexpr int kBuf = 2 * P::kSlot;
+  BwdChunk w;
+  if (!bwd_chunk<P>(a, w)) return;  // uniform, before any barrier
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  const int L = a.left, R = a.right;
+  const uint32_t tb = w.tb;
+
+  const __amdgpu_buffer_rsrc_t Qr = make_rsrc(static_cast<const Elt*>(a.q) + w.base, w.nrec);
+  const __amdgpu_buffer_rsrc_t Kr = make_rsrc(static_cast<const Elt*>(a.k) + w.base, w.nrec);
+  const __amdgpu_buffer_rsrc_t Vr = make_rsrc(static_cast<const Elt*>(a.v) + w.base, w.nrec);
+  const __amdgpu_buffer_rsrc_t Gr = make_rsrc(static_cast<const Elt*>(a.dout) + w.base, w.nrec);
+  const __amdgpu_buffer_rsrc_t DQr = make_rsrc(static_cast<Elt*>(a.dq) + w.base, w.nrec);
+
+  auto lo_of = [&](int t) { return max(floordiv32(64 * t - L, 64), 0); };
+  auto hi_of = [&](int t) { return min(floordiv32(64 * t + 63 + R, 64), w.nblk - 1); };
+  const uint32_t lrow = (uint32_t)(16 * wv + c) * tb;  // this lane's row within a tile
+  const uint32_t kl = P::k_lane(c, g), vl = P::v_lane(c, g);
+
+  // prologue: the first tile's rows and band
+  typename P::Q qr, gr, qn, gn;
+  P::load_q(qr, Qr, (uint32_t)(64 * w.t0) * tb + lrow, g);
+  P::load_q(gr, Gr, (uint32_t)(64 * w.t0) * tb + lrow, g);
+  typename P::Slot xk, xv;
+  for (int j = lo_of(w.t0); j <= hi_of(w.t0); ++j) {
+    P::load_slot(xk, Kr, Kr, (uint32_t)(64 * j) * tb, tid, tb);
+    P::load_slot(xv, Vr, Vr, (uint32_t)(64 * j) * tb, tid, tb);
+    P::store_slot(xk, ring + (j & 1) * kBuf, tid);
+    P::store_slot(xv, ring + (j & 1) * kBuf + P::kSlot, tid);
+  }
+  __syncthreads();
+
+  const float sl2 = a.scale_log2;
+  const int dl = 4 * g - c + L;
+  for (int t = w.t0; t < w.t1; ++t) {
+    // prefetch: tile t+1's new block and rows
+    const bool more = t + 1 < w.t1;
+    const int nblk_new = more && hi_of(t + 1) > hi_of(t) ? hi_of(t + 1) : -1;
+    const uint32_t noff = nblk_new >= 0 ? (uint32_t)(64 * nblk_new) * tb : kOob;
+    P::load_slot(xk, Kr, Kr, noff, tid, tb);
+    P::load_slot(xv, Vr, Vr, noff, tid, tb);
+    const uint32_t nrow = more ? (uint32_t)(64 * (t + 1)) * tb + lrow : kOob;
+    P::load_q(qn, Qr, nrow, g);
+    P::load_q(gn, Gr, nrow, g);
+
+    const int q0 = 64 * t + 16 * wv;
+    const int lo = lo_of(t), hi = hi_of(t);
+    float m_run = -INFINITY, l_run = 0.0f, a_run = 0.0f, lse2, dlt;
+    f32x4 s[4], dp[4];
+    for (int j = lo; j <= hi; ++j) {  // pass 1
+      const uint8_t* sk = ring + (j & 1) * kBuf;
+      bwdq_scores<P>(sk, sk + P::kSlot, kl, qr, gr, 64 * j, q0, L, R, dl, g, w.Nr, s, dp);
+      bwdq_pass1(s, dp, sl2, m_run, l_run, a_run);
+    }
+    bwdq_stats(m_run, l_run, a_run, sl2, lse2, dlt);
+    f32x4 acc[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = lo; j <= hi; ++j) {  // pass 2
+      const uint8_t* sk = ring + (j & 1) * kBuf;
+      bwdq_scores<P>(sk, sk + P::kSlot, kl, qr, gr, 64 * j, q0, L, R, dl, g, w.Nr, s, dp);
+      bwdq_pass2<P>(sk, vl, s, dp, sl2, lse2, dlt, acc);
+    }
+    P::store_o(acc, a.scale, DQr, (uint32_t)(64 * t) * tb + lrow, g);
+    const int64_t srow = (((int64_t)w.b * a.N + w.rho + (int64_t)a.dil * (q0 + c)) * a.H + w.h);
+    if (g == 0 && q0 + c < w.Nr) *reinterpret_cast<float2*>(a.stats + 2 * srow) = make_float2(lse2, dlt);
+
+    // the new block replaces block hi(t+1) - 2, which tile t may still read
+    __syncthreads();
+    if (nblk_new >= 0) {
+      P::store_slot(xk, ring + (nblk_new & 1) * kBuf, tid);
+      P::store_slot(xv, ring + (nblk_new & 1) * kBuf + P::kSlot, tid);
+    }
+    __syncthreads();
+    qr = qn;
+    gr = gn;
+  }
+}
+
+template <class P>
+__global__ __launch_bounds__(256, 2) void bwd_kv_stream_kernel(BwdArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 slots x (Q slot, dO slot, stats)
+  using Elt = typename P::Elt;
+  constexpr int kBuf = 2 * P::kSlot + 512;
+  BwdChunk w;
+  if (!bwd_chunk<P>(a, w)) return;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  const int L = a.left, R = a.right;
+  const uint32_t tb = w.tb;
+
+  const __amdgpu_buffer_rsrc_t Qr = make_rsrc(static_cast<const Elt*>(a.q) + w.base, w.nrec);
+  const __amdgpu_buffer_rsrc_t Kr = make_rsrc(static_cast<const Elt*>(a.k) + w.base, w.nrec);
+  const __amdgpu_buffer_rsrc_t Vr = make_rsrc(static_cast<const Elt*>(a.v) + w.base, w.nrec);
+  const __amdgpu_buffer_rsrc_t Gr = make_rsrc(static_cast<const Elt*>(a.dout) + w.base, w.nrec);
+  const __amdgpu_buffer_rsrc_t DKr = make_rsrc(static_cast<Elt*>(a.dk) + w.base, w.nrec);
+  const __amdgpu_buffer_rsrc_t DVr = make_rsrc(static_cast<Elt*>(a.dv) + w.base, w.nrec);
+  const BwdStats S = bwd_stats_rsrc(a, w.b, w.h, w.rho, w.Nr);
+
+  auto lo_of = [&](int t) { return max(floordiv32(64 * t - R, 64), 0); };
+  auto hi_of = [&](int t) { return min(floordiv32(64 * t + 63 + L, 64), w.nblk - 1); };
+  auto stat_off = [&](int j) { return j >= 0 && tid < 64 ? (uint32_t)(64 * j + tid) * S.stride : kOob; };
+  const uint32_t lrow = (uint32_t)(16 * wv + c) * tb;
+  const uint32_t kl = P::k_lane(c, g), vl = P::v_lane(c, g);
+
+  typename P::Q kr, vr, kn, vn;
+  P::load_q(kr, Kr, (uint32_t)(64 * w.t0) * tb + lrow, g);
+  P::load_q(vr, Vr, (uint32_t)(64 * w.t0) * tb + lrow, g);
+  typename P::Slot xq, xg;
+  uint2 xs;
+  for (int j = lo_of(w.t0); j <= hi_of(w.t0); ++j) {
+    P::load_slot(xq, Qr, Qr, (uint32_t)(64 * j) * tb, tid, tb);
+    P::load_slot(xg, Gr, Gr, (uint32_t)(64 * j) * tb, tid, tb);
+    xs = bload8(S.r, stat_off(j));
+    uint8_t* sb = ring + (j & 1) * kBuf;
+    P::store_slot(xq, sb, tid);
+    P::store_slot(xg, sb + P::kSlot, tid);
+    bwd_stage_stats(sb + 2 * P::kSlot, xs, tid);
+  }
+  __syncthreads();
+
+  const int dl = c - 4 * g + L;
+  for (int t = w.t0; t < w.t1; ++t) {
+    const bool more = t + 1 < w.t1;
+    const int nblk_new = more && hi_of(t + 1) > hi_of(t) ? hi_of(t + 1) : -1;
+    const uint32_t noff = nblk_new >= 0 ? (uint32_t)(64 * nblk_new) * tb : kOob;
+    P::load_slot(xq, Qr, Qr, noff, tid, tb);
+    P::load_slot(xg, Gr, Gr, noff, tid, tb);
+    xs = bload8(S.r, stat_off(nblk_new));
+    const uint32_t nrow = more ? (uint32_t)(64 * (t + 1)) * tb + lrow : kOob;
+    P::load_q(kn, Kr, nrow, g);
+    P::load_q(vn, Vr, nrow, g);
+
+    const int k0 = 64 * t + 16 * wv;
+    f32x4 acc_k[4], acc_v[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) acc_k[dt] = acc_v[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = lo_of(t); j <= hi_of(t); ++j) {
+      const uint8_t* sq = ring + (j & 1) * kBuf;
+      bwdkv_block<P>(sq, sq + P::kSlot, reinterpret_cast<const float*>(sq + 2 * P::kSlot), kl, vl, kr, vr, 64 * j,
+                     k0, L, R, dl, g, w.Nr, a.scale_log2, acc_k, acc_v);
+    }
+    const uint32_t orow = (uint32_t)(64 * t) * tb + lrow;
+    P::store_o(acc_v, 1.0f, DVr, orow, g);
+    P::store_o(acc_k, a.scale, DKr, orow, g);
+
+    __syncthreads();
+    if (nblk_new >= 0) {
+      uint8_t* sb = ring + (nblk_new & 1) * kBuf;
+      P::store_slot(xq, sb, tid);
+      P::store_slot(xg, sb + P::kSlot, tid);
+      bwd_stage_stats(sb + 2 * P::kSlot, xs, tid);
+    }
+    __syncthreads();
+    kr = kn;
+    vr = vn;
+  }
 }
 
 }  // namespace ma_dev

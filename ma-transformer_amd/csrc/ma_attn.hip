@@ -948,19 +948,30 @@ int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* 
   a.tok_bytes = (int32_t)(dil * d->num_heads * kHeadDim * 2);
   a.scale = scale_of(d);
   a.scale_log2 = a.scale * 1.4426950408889634f;
-  const int64_t wgs = d->batch * d->num_heads * dil * a.tiles;
+  const int64_t streams = d->batch * d->num_heads * dil;
   const size_t shm_q = 4 * (size_t)P::kSlot, shm_kv = 2 * (2 * (size_t)P::kSlot + 512);
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd_q_kernel<P>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm_q) != hipSuccess ||
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd_kv_kernel<P>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm_kv) != hipSuccess)
+  // Bands of at most two 64-row blocks in both directions stream a chunk of
+  // tiles per workgroup (two workgroups per CU, one wave of workgroups);
+  // wider bands take one workgroup per tile.
+  const bool chunked = ma::floordiv64(63 + R, 64) - ma::floordiv64(-L, 64) + 1 <= 2 &&
+                       ma::floordiv64(63 + L, 64) - ma::floordiv64(-R, 64) + 1 <= 2 &&
+                       !getenv("MA_ATTN_BWD_PER_TILE");
+  auto kq = chunked ? &bwd_q_stream_kernel<P> : &bwd_q_kernel<P>;
+  auto kkv = chunked ? &bwd_kv_stream_kernel<P> : &bwd_kv_kernel<P>;
+  a.chunk = (int32_t)ma::imax64(1, (streams * a.tiles + 511) / 512);
+  a.chunks = (int32_t)((a.tiles + a.chunk - 1) / a.chunk);
+  const int64_t wgs = chunked ? streams * a.chunks : streams * a.tiles;
+  static bool attr_set[2] = {false, false};
+  if (!attr_set[chunked]) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kq), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)shm_q) != hipSuccess ||
+        hipFuncSetAttribute(reinterpret_cast<const void*>(kkv), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)shm_kv) != hipSuccess)
       return fail("ma_attn_backward: cannot reserve LDS for the backward kernels");
-    attr_set = true;
+    attr_set[chunked] = true;
   }
-  hipLaunchKernelGGL(bwd_q_kernel<P>, dim3((unsigned)wgs), dim3(256), shm_q, st, a);
-  hipLaunchKernelGGL(bwd_kv_kernel<P>, dim3((unsigned)wgs), dim3(256), shm_kv, st, a);
+  hipLaunchKernelGGL(kq, dim3((unsigned)wgs), dim3(256), shm_q, st, a);
+  hipLaunchKernelGGL(kkv, dim3((unsigned)wgs), dim3(256), shm_kv, st, a);
   return 0;
 }
 

@@ -157,6 +157,18 @@ def test_sliding_backward_row_kernels(ext, oracle, monkeypatch, N, left, right, 
     _check(got, oracle.backward(spec, *up), torch.bfloat16)
 
 
+@pytest.mark.parametrize("N,H,left,right,dil", [(5000, 16, 63, 0, 1), (4099, 8, 63, 0, 4), (3000, 8, 0, 0, 1),
+                                                 (2500, 8, 10, 0, 3), (3333, 8, 0, 64, 1)])
+def test_backward_chunked(ext, oracle, N, H, left, right, dil):
+    """Bands of at most two blocks stream several tiles per workgroup (the
+    last chunk of each residue class ragged): whole gradients vs the oracle."""
+    shape = (2, N, H, 64)
+    (q, k, v, g), up = _case(shape, 880 + N + dil, torch.bfloat16)
+    got = ext.sliding_backward(q, k, v, g, left, right, dil)
+    spec = oracle.Spec(*shape, pattern="sliding", left=left, right=right, dilation=dil)
+    _check(got, oracle.backward(spec, *up), torch.bfloat16)
+
+
 def test_backward_target_shape(ext, oracle):
     """The headline shape in bf16 (B=1 H=8 N=65536 D=64, causal w=64): whole
     gradients against the oracle."""
