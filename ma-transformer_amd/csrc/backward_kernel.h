@@ -460,23 +460,24 @@ __global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
     P::load_q(gn, Gr, nrow, g);
 
     const int q0 = 64 * t + 16 * wv;
-    const int lo = lo_of(t), hi = hi_of(t);
+    const int lo = lo_of(t), hi = hi_of(t);  // hi - lo is 0 or 1
+    // Both blocks' scores stay in registers from pass 1 to pass 2.
     float m_run = -INFINITY, l_run = 0.0f, a_run = 0.0f, lse2, dlt;
-    f32x4 s[4], dp[4];
-    for (int j = lo; j <= hi; ++j) {  // pass 1
-      const uint8_t* sk = ring + (j & 1) * kBuf;
-      bwdq_scores<P>(sk, sk + P::kSlot, kl, qr, gr, 64 * j, q0, L, R, dl, g, w.Nr, s, dp);
-      bwdq_pass1(s, dp, sl2, m_run, l_run, a_run);
+    const uint8_t* sk0 = ring + (lo & 1) * kBuf;
+    const uint8_t* sk1 = ring + (hi & 1) * kBuf;
+    f32x4 s0[4], dp0[4], s1[4], dp1[4];
+    bwdq_scores<P>(sk0, sk0 + P::kSlot, kl, qr, gr, 64 * lo, q0, L, R, dl, g, w.Nr, s0, dp0);
+    bwdq_pass1(s0, dp0, sl2, m_run, l_run, a_run);
+    if (hi > lo) {
+      bwdq_scores<P>(sk1, sk1 + P::kSlot, kl, qr, gr, 64 * hi, q0, L, R, dl, g, w.Nr, s1, dp1);
+      bwdq_pass1(s1, dp1, sl2, m_run, l_run, a_run);
     }
     bwdq_stats(m_run, l_run, a_run, sl2, lse2, dlt);
     f32x4 acc[4];
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int j = lo; j <= hi; ++j) {  // pass 2
-      const uint8_t* sk = ring + (j & 1) * kBuf;
-      bwdq_scores<P>(sk, sk + P::kSlot, kl, qr, gr, 64 * j, q0, L, R, dl, g, w.Nr, s, dp);
-      bwdq_pass2<P>(sk, vl, s, dp, sl2, lse2, dlt, acc);
-    }
+    bwdq_pass2<P>(sk0, vl, s0, dp0, sl2, lse2, dlt, acc);
+    if (hi > lo) bwdq_pass2<P>(sk1, vl, s1, dp1, sl2, lse2, dlt, acc);
     P::store_o(acc, a.scale, DQr, (uint32_t)(64 * t) * tb + lrow, g);
     const int64_t srow = (((int64_t)w.b * a.N + w.rho + (int64_t)a.dil * (q0 + c)) * a.H + w.h);
     if (g == 0 && q0 + c < w.Nr) *reinterpret_cast<float2*>(a.stats + 2 * srow) = make_float2(lse2, dlt);
