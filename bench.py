@@ -5,11 +5,17 @@ Default workload (BASELINE.json metric): causal sliding-window attention,
 bf16, B=1 H=8 N=65536 D=64, window 64 (keys [i-63, i]).  A "step" is one
 forward pass over that batch.  Prints ONE JSON line:
 
-  value      queries/s (B*H*N query rows per second), whole job, 1 GPU
+  value      queries/s (B*H*N query rows per second), whole job, 1 GPU:
+             K back-to-back launches between two HIP events on the launch
+             stream
   roofline   achieved algorithmic HBM GB/s of the kernel (4*B*N*H*D*elt
-             bytes per launch / mean launch time, HIP events on the launch
-             stream) against the 8 TB/s MI355X peak; traffic = measured HBM
-             bytes per launch from the committed rocprofv3 counter summary
+             bytes per launch / mean kernel duration) against the 8 TB/s
+             MI355X peak (or TFLOP/s against the MFMA peak when the work is
+             above the ridge).  Kernel durations come from HIP events that
+             the library stamps on the kernels' own dispatches
+             (ma_attn_forward_timed, hipExtLaunchKernel) in a second pass of
+             K launches; traffic = measured HBM bytes per launch from the
+             committed rocprofv3 counter summary
   cpu_baseline  the CPU oracle (restatement of ma_core.cpp:160-246) on this
              host, single thread, bounded sample of the same workload
 
@@ -201,10 +207,7 @@ def main() -> int:
     torch.cuda.synchronize()
 
     # Timed region: K back-to-back launches on the launch stream between two
-    # HIP events (an event between launches adds its own completion wait, so
-    # per-launch events are taken in a separate pass below).  The host path
-    # (about 13 us per call) stays ahead of the kernels, so this is the
-    # kernels' throughput; the mean launch duration is total / K.
+    # HIP events; `value` and ms_per_step come from it.
     stream = torch.cuda.current_stream(dev)
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
@@ -216,16 +219,22 @@ def main() -> int:
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
     ms_per_step = total_ms / args.steps
-    mean_launch_ms = ms_per_step
-    # per-launch spread (diagnostic only): an event pair around each launch
-    n_ev = min(args.steps, 50)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_ev)]
-    for i in range(n_ev):
-        ev[i][0].record(stream)
-        launch(sets[i % nsets])
-        ev[i][1].record(stream)
+    # Kernel durations: K more launches, each stamping its kernels' own start
+    # and stop on an event pair (hipExtLaunchKernel through ma_attn_*_timed,
+    # stamped on the dispatch packets).  The stamping slows the launch
+    # sequence, so it stays out of the region above; the roofline uses these
+    # durations.
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for a, b in ev:  # create the events before they are stamped
+        a.record(stream)
+        b.record(stream)
+    torch.cuda.synchronize()
+    for i in range(args.steps):
+        with ext.kernel_events(*ev[i]):
+            launch(sets[i % nsets])
     torch.cuda.synchronize()
     per_launch_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    mean_launch_ms = sum(per_launch_ms) / len(per_launch_ms)
 
     queries = B * H * N
     alg_bytes = tensors * B * N * H * D * elt
@@ -277,7 +286,8 @@ def main() -> int:
         "hbm_frac_of_peak": achieved_gbps / HBM_PEAK_GBPS,
         "roofline": roofline,
         "kernel_us_mean": mean_launch_ms * 1e3,
-        "kernel_us_median_event_pairs": per_launch_ms[len(per_launch_ms) // 2] * 1e3,
+        "kernel_us_median": per_launch_ms[len(per_launch_ms) // 2] * 1e3,
+        "step_us_mean": ms_per_step * 1e3,
         "algorithmic_bytes_per_launch": alg_bytes,
         "flops_per_launch": flops,
         "tflops": flops / (mean_launch_ms * 1e-3) / 1e12,

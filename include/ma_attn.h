@@ -113,6 +113,23 @@ int ma_attn_backward(const ma_attn_desc* desc, const void* q, const void* k,
  * them per gradient pass, sparse_attention_kernel.cu:285-304). */
 size_t ma_attn_backward_workspace_size(const ma_attn_desc* desc);
 
+/*
+ * ma_attn_forward / ma_attn_backward with the call's kernels bracketed by two
+ * caller-created HIP events (hipEvent_t, either may be NULL): start_event
+ * records when the call's first kernel starts and stop_event when its last
+ * kernel ends, stamped on the kernels' own dispatches (hipExtLaunchKernel), so
+ * their difference is the kernels' execution time without the gaps between
+ * launches.  For timing; no counterpart in the reference.
+ */
+int ma_attn_forward_timed(const ma_attn_desc* desc, const void* q, const void* k,
+                          const void* v, void* o, void* workspace,
+                          size_t workspace_bytes, void* stream,
+                          void* start_event, void* stop_event);
+int ma_attn_backward_timed(const ma_attn_desc* desc, const void* q, const void* k,
+                           const void* v, const void* dout, void* dq, void* dk,
+                           void* dv, void* workspace, size_t workspace_bytes,
+                           void* stream, void* start_event, void* stop_event);
+
 /* Validates desc without launching; 0 when ma_attn_forward would accept it.
  * Mirrors the checks of sparse_attention_kernel.cu:427-432. */
 int ma_attn_validate(const ma_attn_desc* desc);
@@ -147,7 +164,7 @@ int64_t ma_attn_row_keys(const ma_attn_desc* desc, const int32_t* host_block_tab
 /* ABI version of this header (bumped on incompatible change). */
 int ma_attn_abi_version(void);
 
-#define MA_ATTN_ABI_VERSION 2
+#define MA_ATTN_ABI_VERSION 3
 
 #ifdef __cplusplus
 }

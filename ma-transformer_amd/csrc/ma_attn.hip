@@ -18,6 +18,7 @@
 // set with scale 1/sqrtf(D), empty set => zero row.  The reference GPU
 // launcher this replaces is sparse_forward_cuda
 // (src/cuda/sparse_attention_kernel.cu:423-458).
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -49,6 +50,27 @@ int fail(const char* fmt, ...) {
 }
 
 using namespace ma_dev;
+
+// ------------------------------------------------------------------ launches
+//
+// Events of the current ma_attn_*_timed call (null otherwise): the call's
+// first kernel takes the start event and its last kernel the stop event, so
+// they bracket the kernels' own execution (hipExtLaunchKernel stamps them on
+// the dispatch packets; no extra queue packets).
+thread_local hipEvent_t g_ev_start = nullptr;
+thread_local hipEvent_t g_ev_stop = nullptr;
+
+template <typename F, typename... Args>
+void launch(bool last, F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t st, Args... args) {
+  hipEvent_t e0 = g_ev_start, e1 = last ? g_ev_stop : nullptr;
+  if (e0 || e1) {
+    g_ev_start = nullptr;
+    if (last) g_ev_stop = nullptr;
+    hipExtLaunchKernelGGL(kernel, grid, block, shm, st, e0, e1, 0u, args...);
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, shm, st, args...);
+  }
+}
 
 // ------------------------------------------------------------------ element access
 
@@ -623,8 +645,8 @@ int launch_rows(const ma_attn_desc* d, const void* q, const void* k, const void*
   const T* tv = static_cast<const T*>(v);
   T* to = static_cast<T*>(o);
 #define MA_ROWS(N_)                                                                            \
-  hipLaunchKernelGGL((rows_kernel<T, N_>), dim3((unsigned)blocks), dim3(256), shm, st, tq, tk, \
-                     tv, to, d->batch, d->num_heads, d->head_dim, pp, scale)
+  launch(true, rows_kernel<T, N_>, dim3((unsigned)blocks), dim3(256), (uint32_t)shm, st, tq, tk, \
+                     tv, to, d->batch, d->num_heads, d->head_dim, pp, scale, (const T*)nullptr, (RowStat*)nullptr)
   if (dpl <= 1)
     MA_ROWS(1);
   else if (dpl <= 2)
@@ -662,9 +684,9 @@ int launch_band(const ma_attn_desc* d, const void* q, const void* k, const void*
   const int64_t wgs = d->batch * a.tiles * d->num_heads * d->dilation;
   if (wgs > (int64_t)INT32_MAX) return fail("ma_attn: problem too large for one launch");
   if (d->dtype == MA_ATTN_BF16)
-    hipLaunchKernelGGL(band_kernel<__bf16>, dim3((unsigned)wgs), dim3(256), 0, st, a);
+    launch(true, band_kernel<__bf16>, dim3((unsigned)wgs), dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL(band_kernel<_Float16>, dim3((unsigned)wgs), dim3(256), 0, st, a);
+    launch(true, band_kernel<_Float16>, dim3((unsigned)wgs), dim3(256), 0, st, a);
   return 0;
 }
 
@@ -756,7 +778,7 @@ int launch_stream_t(const StreamArgs& a, int64_t wgs, hipStream_t st) {
       return fail("ma_attn: cannot reserve %zu B of LDS for the stream kernel", shm);
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)wgs), dim3(256), shm, st, a);
+  launch(!LG, kern, dim3((unsigned)wgs), dim3(256), (uint32_t)shm, st, a);  // Longformer: combine is last
   return 0;
 }
 
@@ -791,7 +813,7 @@ int launch_stream_half(const ma_attn_desc* d, const StreamArgs& a, const StreamP
   if (p.geom.G == 0) return launch_stream_any<P, false>(a, p.slots, p.wgs, st);
   const int rc = launch_stream_any<P, true>(a, p.slots, p.wgs, st);
   if (rc) return rc;
-  hipLaunchKernelGGL(longformer_combine<T>, dim3((unsigned)(d->batch * d->num_heads * p.geom.G)), dim3(64), 0, st,
+  launch(true, longformer_combine<T>, dim3((unsigned)(d->batch * d->num_heads * p.geom.G)), dim3(64), 0, st,
                      a.partials, static_cast<T*>(a.o), (int)(p.chunks * 4), (int)p.geom.G, (int)d->num_heads,
                      d->seq_len);
   return 0;
@@ -847,7 +869,7 @@ bool block_applies(const ma_attn_desc* d, const void* q, const void* k, const vo
 
 template <class P>
 void launch_block_t(const BlockArgs& a, int64_t bh, hipStream_t st) {
-  hipLaunchKernelGGL(block_row_kernel<P>, dim3((unsigned)(bh * a.nbq)), dim3(256), 0, st, a);
+  launch(true, block_row_kernel<P>, dim3((unsigned)(bh * a.nbq)), dim3(256), 0, st, a);
 }
 
 int launch_block(const ma_attn_desc* d, const void* q, const void* k, const void* v, void* o, hipStream_t st) {
@@ -970,8 +992,8 @@ int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* 
       return fail("ma_attn_backward: cannot reserve LDS for the backward kernels");
     attr_set[chunked] = true;
   }
-  hipLaunchKernelGGL(kq, dim3((unsigned)wgs), dim3(256), shm_q, st, a);
-  hipLaunchKernelGGL(kkv, dim3((unsigned)wgs), dim3(256), shm_kv, st, a);
+  launch(false, kq, dim3((unsigned)wgs), dim3(256), (uint32_t)shm_q, st, a);
+  launch(true, kkv, dim3((unsigned)wgs), dim3(256), (uint32_t)shm_kv, st, a);
   return 0;
 }
 
@@ -995,11 +1017,11 @@ int launch_backward(const ma_attn_desc* d, const void* q, const void* k, const v
   const int64_t B = d->batch, H = d->num_heads, D = d->head_dim;
 #define MA_BWD(N_)                                                                                          \
   do {                                                                                                      \
-    hipLaunchKernelGGL((rows_kernel<T, N_, true>), grid, blk, shm1, st, tq, tk, tv, nullptr, B, H, D, pp,  \
+    launch(false, rows_kernel<T, N_, true>, grid, blk, (uint32_t)shm1, st, tq, tk, tv, (T*)nullptr, B, H, D, pp, \
                        scale, tg, stats);                                                                   \
-    hipLaunchKernelGGL((bwd_dq_kernel<T, N_>), grid, blk, shm2, st, tq, tk, tv, tg, stats,                 \
+    launch(false, bwd_dq_kernel<T, N_>, grid, blk, (uint32_t)shm2, st, tq, tk, tv, tg, (const RowStat*)stats,  \
                        static_cast<T*>(dq), B, H, D, pp, scale);                                            \
-    hipLaunchKernelGGL((bwd_dkv_kernel<T, N_>), grid, blk, shm2, st, tq, tk, tv, tg, stats,                \
+    launch(true, bwd_dkv_kernel<T, N_>, grid, blk, (uint32_t)shm2, st, tq, tk, tv, tg, (const RowStat*)stats, \
                        static_cast<T*>(dk), static_cast<T*>(dv), B, H, D, pt, scale);                       \
   } while (0)
   if (dpl <= 1)
@@ -1131,6 +1153,26 @@ int ma_attn_backward(const ma_attn_desc* desc, const void* q, const void* k, con
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail("ma_attn_backward: kernel launch failed: %s", hipGetErrorString(e));
   return 0;
+}
+
+int ma_attn_forward_timed(const ma_attn_desc* desc, const void* q, const void* k, const void* v, void* o,
+                          void* workspace, size_t workspace_bytes, void* stream, void* start_event,
+                          void* stop_event) {
+  g_ev_start = static_cast<hipEvent_t>(start_event);
+  g_ev_stop = static_cast<hipEvent_t>(stop_event);
+  const int rc = ma_attn_forward(desc, q, k, v, o, workspace, workspace_bytes, stream);
+  g_ev_start = g_ev_stop = nullptr;
+  return rc;
+}
+
+int ma_attn_backward_timed(const ma_attn_desc* desc, const void* q, const void* k, const void* v,
+                           const void* dout, void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes,
+                           void* stream, void* start_event, void* stop_event) {
+  g_ev_start = static_cast<hipEvent_t>(start_event);
+  g_ev_stop = static_cast<hipEvent_t>(stop_event);
+  const int rc = ma_attn_backward(desc, q, k, v, dout, dq, dk, dv, workspace, workspace_bytes, stream);
+  g_ev_start = g_ev_stop = nullptr;
+  return rc;
 }
 
 int ma_attn_block_table(uint64_t seed, int64_t num_blocks, int64_t random_per_row, int32_t* out) {

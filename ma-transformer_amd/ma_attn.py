@@ -18,7 +18,7 @@ LIB_PATH = os.environ.get("MA_ATTN_LIB", os.path.join(_HERE, "libma_attn.so"))
 
 F32, BF16, F16 = 0, 1, 2
 SLIDING, DENSE, BLOCK_SPARSE, LONGFORMER = 0, 1, 2, 3
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 
@@ -67,6 +67,12 @@ def _open():
     lib.ma_attn_backward.restype = ctypes.c_int
     lib.ma_attn_backward.argtypes = [ctypes.POINTER(Desc)] + [ctypes.c_void_p] * 8 + \
         [ctypes.c_size_t, ctypes.c_void_p]
+    lib.ma_attn_forward_timed.restype = ctypes.c_int
+    lib.ma_attn_forward_timed.argtypes = [ctypes.POINTER(Desc)] + [ctypes.c_void_p] * 5 + \
+        [ctypes.c_size_t] + [ctypes.c_void_p] * 3
+    lib.ma_attn_backward_timed.restype = ctypes.c_int
+    lib.ma_attn_backward_timed.argtypes = [ctypes.POINTER(Desc)] + [ctypes.c_void_p] * 8 + \
+        [ctypes.c_size_t] + [ctypes.c_void_p] * 3
     lib.ma_attn_block_table.restype = ctypes.c_int
     lib.ma_attn_block_table.argtypes = [ctypes.c_uint64, ctypes.c_int64, ctypes.c_int64,
                                         ctypes.c_void_p]
@@ -111,10 +117,17 @@ def workspace_size(desc: Desc) -> int:
 
 
 def forward_raw(desc: Desc, q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int,
-                ws_ptr: int = 0, ws_bytes: int = 0, stream: int = 0) -> None:
-    """Launch on ``stream`` (a hipStream_t as int).  Raises RuntimeError on rejection."""
-    rc = LIB.ma_attn_forward(ctypes.byref(desc), q_ptr, k_ptr, v_ptr, o_ptr, ws_ptr or None,
-                             ws_bytes, stream or None)
+                ws_ptr: int = 0, ws_bytes: int = 0, stream: int = 0, events=None) -> None:
+    """Launch on ``stream`` (a hipStream_t as int).  Raises RuntimeError on rejection.
+
+    events: optional (start, stop) hipEvent_t handles (ints) stamped on the
+    call's first and last kernel (ma_attn_forward_timed)."""
+    if events:
+        rc = LIB.ma_attn_forward_timed(ctypes.byref(desc), q_ptr, k_ptr, v_ptr, o_ptr, ws_ptr or None,
+                                       ws_bytes, stream or None, events[0] or None, events[1] or None)
+    else:
+        rc = LIB.ma_attn_forward(ctypes.byref(desc), q_ptr, k_ptr, v_ptr, o_ptr, ws_ptr or None,
+                                 ws_bytes, stream or None)
     if rc != 0:
         raise RuntimeError(last_error())
 
@@ -124,10 +137,15 @@ def backward_workspace_size(desc: Desc) -> int:
 
 
 def backward_raw(desc: Desc, q_ptr: int, k_ptr: int, v_ptr: int, g_ptr: int, dq_ptr: int,
-                 dk_ptr: int, dv_ptr: int, ws_ptr: int, ws_bytes: int, stream: int = 0) -> None:
+                 dk_ptr: int, dv_ptr: int, ws_ptr: int, ws_bytes: int, stream: int = 0, events=None) -> None:
     """Launch the backward on ``stream``.  Raises RuntimeError on rejection."""
-    rc = LIB.ma_attn_backward(ctypes.byref(desc), q_ptr, k_ptr, v_ptr, g_ptr, dq_ptr, dk_ptr, dv_ptr,
-                              ws_ptr or None, ws_bytes, stream or None)
+    if events:
+        rc = LIB.ma_attn_backward_timed(ctypes.byref(desc), q_ptr, k_ptr, v_ptr, g_ptr, dq_ptr, dk_ptr, dv_ptr,
+                                        ws_ptr or None, ws_bytes, stream or None, events[0] or None,
+                                        events[1] or None)
+    else:
+        rc = LIB.ma_attn_backward(ctypes.byref(desc), q_ptr, k_ptr, v_ptr, g_ptr, dq_ptr, dk_ptr, dv_ptr,
+                                  ws_ptr or None, ws_bytes, stream or None)
     if rc != 0:
         raise RuntimeError(last_error())
 

@@ -62,6 +62,31 @@ def _check(*ts: torch.Tensor) -> None:
         raise RuntimeError("Inputs must be on one device")
 
 
+# (start, stop) torch.cuda.Event pair for the next launch, set by kernel_events()
+_events = None
+
+
+class kernel_events:
+    """Context manager: the forward / backward calls inside it stamp the
+    kernels' own start and stop on two torch.cuda.Event(enable_timing=True)
+    (already recorded once, so that they exist), without adding commands
+    between launches.  ``start.elapsed_time(stop)`` is then the kernels'
+    execution time of the last call inside the block."""
+
+    def __init__(self, start: torch.cuda.Event, stop: torch.cuda.Event):
+        self.pair = (start.cuda_event, stop.cuda_event)
+
+    def __enter__(self):
+        global _events
+        _events = self.pair
+        return self
+
+    def __exit__(self, *exc):
+        global _events
+        _events = None
+        return False
+
+
 def _launch(q, k, v, pattern, **kw) -> torch.Tensor:
     _check(q, k, v)
     B, N, H, D = q.shape
@@ -74,7 +99,7 @@ def _launch(q, k, v, pattern, **kw) -> torch.Tensor:
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
         _ma.forward_raw(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                        ws.data_ptr() if ws is not None else 0, nbytes, stream)
+                        ws.data_ptr() if ws is not None else 0, nbytes, stream, _events)
     return out
 
 
@@ -201,7 +226,7 @@ def _backward(q, k, v, grad_out, pattern, **kw) -> List[torch.Tensor]:
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
         _ma.backward_raw(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), grad_out.data_ptr(),
-                         dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), nbytes, stream)
+                         dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), nbytes, stream, _events)
     return [dq, dk, dv]
 
 

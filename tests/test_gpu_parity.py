@@ -352,3 +352,29 @@ def test_bridge_backward_on_device(ext):
     pytorch_sparse_attention(q2, k2, v2, 4).sum().backward()
     for a, b in zip(g, (q2.grad, k2.grad, v2.grad)):
         assert (a - b).abs().max().item() <= 1e-4
+
+
+def test_timed_entry_points(ext):
+    """ma_attn_forward_timed / ma_attn_backward_timed: same results as the
+    untimed calls, and the event pair brackets the kernels (positive,
+    shorter than the host-side wall time of the synchronised call)."""
+    import time
+    q, k, v, g = (torch.randn(1, 4096, 4, 64, device="cuda", dtype=torch.bfloat16) for _ in range(4))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    e1.record()
+    torch.cuda.synchronize()
+    ref = ext.sliding_forward(q, k, v, 63, 0)
+    t = time.perf_counter()
+    with ext.kernel_events(e0, e1):
+        out = ext.sliding_forward(q, k, v, 63, 0)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t) * 1e3
+    assert torch.equal(out, ref)
+    assert 0.0 < e0.elapsed_time(e1) <= wall_ms
+    ref_g = ext.sliding_backward(q, k, v, g, 63, 0)
+    with ext.kernel_events(e0, e1):
+        got_g = ext.sliding_backward(q, k, v, g, 63, 0)
+    torch.cuda.synchronize()
+    assert all(torch.equal(a, b) for a, b in zip(got_g, ref_g))
+    assert e0.elapsed_time(e1) > 0.0
