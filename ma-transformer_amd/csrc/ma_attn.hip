@@ -205,6 +205,162 @@ __global__ __launch_bounds__(256) void rows_kernel(const T* __restrict__ q, cons
   }
 }
 
+// ------------------------------------------------------------------ narrow_kernel
+//
+// Narrow heads (head_dim <= 32), SLIDING with dilation 1 and left, right >= 0:
+// one workgroup (4 waves) per 64 consecutive queries of one (batch, head),
+// one query per lane.  The K/V rows those queries read,
+// [64w-left, 64w+63+right], are staged in LDS as fp32 rows of DP + 4 floats
+// (DP = head_dim padded to 16 or 32; the 4-float pad makes the 16-byte reads
+// of 16 consecutive rows hit 64 distinct banks).  Wave v takes the v-th
+// quarter of each query's window, in groups of 16 keys (scores in registers,
+// one rescale per group), lane l reading row l + step so that a wave reads
+// consecutive rows; waves 1-3 leave (max, sum, acc) partials in LDS and wave
+// 0 merges them (log-sum-exp) and writes O.
+constexpr int kNarrowWaves = 4;
+
+template <int DP>
+constexpr int narrow_row() { return DP + 4; }
+
+template <typename T, int DP>
+__global__ __launch_bounds__(256) void narrow_kernel(const T* __restrict__ q, const T* __restrict__ k,
+                                                     const T* __restrict__ v, T* __restrict__ o, int64_t N,
+                                                     int64_t H, int D, int left, int right, float scale) {
+  extern __shared__ __attribute__((aligned(16))) float band[];  // K rows, V rows, then wave partials
+  constexpr int RS = narrow_row<DP>();
+  constexpr int PS = DP + 2;  // partial: acc[DP], max, sum
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t tiles = (N + 63) / 64;
+  const int64_t t = blockIdx.x % tiles;
+  const int64_t bh = blockIdx.x / tiles;
+  const int64_t h = bh % H, b = bh / H;
+  const int64_t rs = H * D;  // elements between consecutive tokens
+  const T* qb = q + (b * N * H + h) * D;
+  const T* kb = k + (b * N * H + h) * D;
+  const T* vb = v + (b * N * H + h) * D;
+  T* ob = o + (b * N * H + h) * D;
+
+  const int64_t i0 = 64 * t;
+  const int64_t j0 = i0 - left > 0 ? i0 - left : 0;
+  const int64_t j1 = i0 + 63 + right < N - 1 ? i0 + 63 + right : N - 1;
+  const int rows = (int)(j1 - j0 + 1);
+  float* kl = band;
+  float* vl = band + (size_t)rows * RS;
+  float* part = vl + (size_t)rows * RS;  // [wave 1..3][lane][PS]
+
+  // Staging in batches of 4 elements per thread: every load of a batch is
+  // issued (indices clamped into range, so unconditionally) before the
+  // stores that wait for them.
+  const int ne = rows * DP;
+  for (int e0 = 0; e0 < ne; e0 += 256 * 4) {
+    float kx[4], vx[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int e = min(e0 + tid + 256 * u, ne - 1);
+      const int r = e / DP, d = min(e % DP, D - 1);
+      const int64_t off = (j0 + r) * rs + d;
+      kx[u] = ld_f(kb + off);
+      vx[u] = ld_f(vb + off);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int e = e0 + tid + 256 * u;
+      if (e < ne) {
+        const int r = e / DP, d = e % DP;
+        kl[r * RS + d] = d < D ? kx[u] : 0.0f;
+        vl[r * RS + d] = d < D ? vx[u] : 0.0f;
+      }
+    }
+  }
+  const int64_t i = i0 + lane;
+  const int64_t ic = i < N ? i : N - 1;
+  float qv[DP];
+#pragma unroll
+  for (int d = 0; d < DP; ++d) {
+    const float x = ld_f(qb + ic * rs + (d < D ? d : D - 1));
+    qv[d] = d < D ? x : 0.0f;
+  }
+  __syncthreads();
+
+  // this wave's quarter of the query's window
+  const int64_t lo = i - left > 0 ? i - left : 0;
+  const int64_t hi = ic + right < N - 1 ? ic + right : N - 1;
+  const int64_t per = (hi - lo + kNarrowWaves) / kNarrowWaves;
+  const int64_t plo = lo + wv * per;
+  const int64_t phi = plo + per - 1 < hi ? plo + per - 1 : hi;
+  const float sl2 = scale * 1.4426950408889634f;  // scores in log2 units, exp2 below
+  float m = -INFINITY, l = 0.0f, acc[DP];
+#pragma unroll
+  for (int d = 0; d < DP; ++d) acc[d] = 0.0f;
+  for (int64_t g0 = plo; g0 <= phi; g0 += 16) {
+    float sc[16];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int64_t j = g0 + u;
+      const float* kr = kl + (j <= phi ? j - j0 : 0) * RS;
+      float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
+#pragma unroll
+      for (int d = 0; d < DP; d += 4) {
+        const float4 kk = *reinterpret_cast<const float4*>(kr + d);
+        d0 = fmaf(qv[d], kk.x, d0);
+        d1 = fmaf(qv[d + 1], kk.y, d1);
+        d2 = fmaf(qv[d + 2], kk.z, d2);
+        d3 = fmaf(qv[d + 3], kk.w, d3);
+      }
+      sc[u] = j <= phi ? ((d0 + d1) + (d2 + d3)) * sl2 : -INFINITY;
+      mx = fmaxf(mx, sc[u]);
+    }
+    const float mn = fmaxf(m, mx);  // finite: the group's first key is in the part
+    const float corr = __builtin_amdgcn_exp2f(m - mn);
+    l *= corr;
+#pragma unroll
+    for (int d = 0; d < DP; ++d) acc[d] *= corr;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const float p = __builtin_amdgcn_exp2f(sc[u] - mn);
+      l += p;
+      const float* vr = vl + (g0 + u <= phi ? g0 + u - j0 : 0) * RS;
+#pragma unroll
+      for (int d = 0; d < DP; d += 4) {
+        const float4 vv = *reinterpret_cast<const float4*>(vr + d);
+        acc[d] = fmaf(p, vv.x, acc[d]);
+        acc[d + 1] = fmaf(p, vv.y, acc[d + 1]);
+        acc[d + 2] = fmaf(p, vv.z, acc[d + 2]);
+        acc[d + 3] = fmaf(p, vv.w, acc[d + 3]);
+      }
+    }
+    m = mn;
+  }
+  if (wv > 0) {
+    float* pw = part + ((wv - 1) * 64 + lane) * PS;
+#pragma unroll
+    for (int d = 0; d < DP; ++d) pw[d] = acc[d];
+    pw[DP] = m;
+    pw[DP + 1] = l;
+  }
+  __syncthreads();
+  if (wv != 0 || i >= N) return;  // after the last barrier
+  for (int w = 1; w < kNarrowWaves; ++w) {
+    const float* pw = part + ((w - 1) * 64 + lane) * PS;
+    const float mw = pw[DP];
+    const float mn = fmaxf(m, mw);
+    if (mn == -INFINITY) continue;  // both parts empty
+    const float c0 = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
+    const float c1 = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - mn);
+    l = l * c0 + pw[DP + 1] * c1;
+#pragma unroll
+    for (int d = 0; d < DP; ++d) acc[d] = acc[d] * c0 + pw[d] * c1;
+    m = mn;
+  }
+  const float inv = hi >= lo ? 1.0f / l : 0.0f;
+#pragma unroll
+  for (int d = 0; d < DP; ++d)
+    if (d < D) ob[i * rs + d] = cvt_out<T>(acc[d] * inv);
+}
+
 // ------------------------------------------------------------------ backward row kernels
 //
 // Gradients of O = softmax(S) V, S = Q K^T * scale over each row's key set,
@@ -659,6 +815,40 @@ int launch_rows(const ma_attn_desc* d, const void* q, const void* k, const void*
   return 0;
 }
 
+// Narrow heads on the one-query-per-lane kernel (band rows staged in LDS).
+constexpr int64_t kNarrowLds = 64 * 1024;
+
+int64_t narrow_lds(const ma_attn_desc* d) {
+  const int64_t dp = d->head_dim <= 16 ? 16 : 32;
+  const int64_t rows = ma::imin64(64 + d->left + d->right, d->seq_len);
+  return (2 * rows * (dp + 4) + (kNarrowWaves - 1) * 64 * (dp + 2)) * 4;
+}
+
+bool narrow_applies(const ma_attn_desc* d) {
+  if (d->pattern != MA_ATTN_SLIDING || d->dilation != 1 || d->left < 0 || d->right < 0) return false;
+  if (d->head_dim < 1 || d->head_dim > 32 || d->left + d->right > (1 << 16)) return false;
+  const int64_t tiles = (d->seq_len + 63) / 64;
+  return narrow_lds(d) <= kNarrowLds && d->batch * d->num_heads * tiles <= (int64_t)INT32_MAX;
+}
+
+template <typename T>
+int launch_narrow(const ma_attn_desc* d, const void* q, const void* k, const void* v, void* o, hipStream_t st) {
+  const int64_t tiles = (d->seq_len + 63) / 64;
+  const float scale = scale_of(d);
+  const dim3 grid((unsigned)(d->batch * d->num_heads * tiles)), blk(64 * kNarrowWaves);
+  const uint32_t shm = (uint32_t)narrow_lds(d);
+  const T* tq = static_cast<const T*>(q);
+  const T* tk = static_cast<const T*>(k);
+  const T* tv = static_cast<const T*>(v);
+  T* to = static_cast<T*>(o);
+  const int D = (int)d->head_dim, L = (int)d->left, R = (int)d->right;
+  if (D <= 16)
+    launch(true, narrow_kernel<T, 16>, grid, blk, shm, st, tq, tk, tv, to, d->seq_len, d->num_heads, D, L, R, scale);
+  else
+    launch(true, narrow_kernel<T, 32>, grid, blk, shm, st, tq, tk, tv, to, d->seq_len, d->num_heads, D, L, R, scale);
+  return 0;
+}
+
 bool band_applies(const ma_attn_desc* d, const void* q, const void* k, const void* v, const void* o) {
   return d->pattern == MA_ATTN_SLIDING && (d->dtype == MA_ATTN_BF16 || d->dtype == MA_ATTN_F16) &&
          d->head_dim == kBandD && d->left >= 0 && d->right >= 0 && aligned16(q) && aligned16(k) &&
@@ -1087,6 +1277,18 @@ int ma_attn_forward(const ma_attn_desc* desc, const void* q, const void* k, cons
     rc = launch_block(desc, q, k, v, o, st);
   } else if (!want_rows && band_applies(desc, q, k, v, o)) {
     rc = launch_band(desc, q, k, v, o, st);
+  } else if (!want_rows && narrow_applies(desc)) {
+    switch (desc->dtype) {
+      case MA_ATTN_F32:
+        rc = launch_narrow<float>(desc, q, k, v, o, st);
+        break;
+      case MA_ATTN_BF16:
+        rc = launch_narrow<__bf16>(desc, q, k, v, o, st);
+        break;
+      default:
+        rc = launch_narrow<_Float16>(desc, q, k, v, o, st);
+        break;
+    }
   } else {
     switch (desc->dtype) {
       case MA_ATTN_F32:

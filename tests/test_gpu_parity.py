@@ -120,6 +120,18 @@ def test_band_kernel_geometry(ext, oracle, N, left, right, dil, dtype):
     assert _max_err(y, oracle.forward(spec, *up)) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("N,D,left,right", [(1000, 24, 40, 20), (777, 8, 100, 50), (300, 16, 63, 0),
+                                             (129, 32, 0, 5), (64, 13, 3, 3)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_narrow_head_geometry(ext, oracle, N, D, left, right, dtype):
+    """head_dim <= 32 sliding windows (one query per lane, window split over 4 waves)."""
+    shape = (2, N, 3, D)
+    (q, k, v), up = _inputs(shape, 1500 + N + D, dtype)
+    y = ext.sliding_forward(q, k, v, left, right)
+    spec = oracle.Spec(*shape, pattern="sliding", left=left, right=right)
+    assert _max_err(y, oracle.forward(spec, *up)) <= TOL[dtype]
+
+
 # ------------------------------------------------------- block-sparse and Longformer kernels
 
 def _random_table(nb, width, seed, rng_extra_pad=True):
