@@ -924,8 +924,14 @@ StreamPlan stream_plan(const ma_attn_desc* d) {
   p.tiles = (nr_max + 63) / 64;
   const int64_t streams = d->batch * d->num_heads * p.geom.dil;
   const int64_t per_cu = ma::imax64(1, ma::imin64(p.max_per_cu, (160 * 1024) / p.lds));
-  const int64_t target = 256 * per_cu;
-  p.chunk = ma::imax64(1, (streams * p.tiles + target - 1) / target);
+  const int64_t slots = 256 * per_cu;  // resident workgroups
+  // Workgroups per stream: as many as fit the resident slots in one wave
+  // (rounded per stream, a grid that overflows the slots by a few
+  // workgroups runs them alone afterwards: cfg4 with 24 streams took 2x).
+  // Even where the paired chunk order applies.
+  int64_t per_stream = ma::imax64(1, slots / streams);
+  if ((p.geom.right > 0 || lg) && per_stream > 1) per_stream &= ~1LL;
+  p.chunk = ma::imax64(1, (p.tiles + per_stream - 1) / per_stream);
   if (const char* e = getenv("MA_ATTN_STREAM_CHUNK")) p.chunk = ma::imax64(1, atoll(e));
   p.chunks = (p.tiles + p.chunk - 1) / p.chunk;
   p.wgs = streams * p.chunks;
