@@ -1176,7 +1176,9 @@ int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* 
                        !getenv("MA_ATTN_BWD_PER_TILE");
   auto kq = chunked ? &bwd_q_stream_kernel<P> : &bwd_q_kernel<P>;
   auto kkv = chunked ? &bwd_kv_stream_kernel<P> : &bwd_kv_kernel<P>;
-  a.chunk = (int32_t)ma::imax64(1, (streams * a.tiles + 511) / 512);
+  // chunks per stream fitted to the 512 resident workgroups (2 per CU)
+  const int64_t per_stream = ma::imax64(1, 512 / streams);
+  a.chunk = (int32_t)ma::imax64(1, (a.tiles + per_stream - 1) / per_stream);
   a.chunks = (int32_t)((a.tiles + a.chunk - 1) / a.chunk);
   const int64_t wgs = chunked ? streams * a.chunks : streams * a.tiles;
   static bool attr_set[2] = {false, false};
