@@ -15,8 +15,9 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
 SRC = os.path.join(PKG_DIR, "csrc", "ma_attn.hip")
 HEADERS = [os.path.join(PKG_DIR, "csrc", h) for h in ("pattern.h", "device_common.h", "stream_kernel.h",
-                                                         "block_kernel.h")] + \
-    [os.path.join(REPO_DIR, "include", "ma_attn.h")]
+                                                         "block_kernel.h", "backward_kernel.h",
+                                                         "tick_features.h")] + \
+    [os.path.join(REPO_DIR, "include", h) for h in ("ma_attn.h", "ma_features.h")]
 LIB = os.path.join(PKG_DIR, "libma_attn.so")
 ARCH = os.environ.get("MA_ATTN_ARCH", "gfx950")
 

@@ -29,11 +29,13 @@
 #include <string>
 
 #include "../../include/ma_attn.h"
+#include "../../include/ma_features.h"
 #include "device_common.h"
 #include "pattern.h"
 #include "stream_kernel.h"
 #include "block_kernel.h"
 #include "backward_kernel.h"
+#include "tick_features.h"
 
 namespace {
 
@@ -1383,6 +1385,36 @@ int ma_attn_backward_timed(const ma_attn_desc* desc, const void* q, const void* 
   const int rc = ma_attn_backward(desc, q, k, v, dout, dq, dk, dv, workspace, workspace_bytes, stream);
   g_ev_start = g_ev_stop = nullptr;
   return rc;
+}
+
+size_t ma_tick_features_workspace_size(int64_t n) {
+  (void)n;
+  return (size_t)ma_feat::kStatBlocks * ma_feat::kFeatures * 3 * sizeof(double);
+}
+
+int ma_tick_features(const double* timestamp, const double* price, const double* bid_price,
+                     const double* ask_price, const double* bid_volume, const double* ask_volume, int64_t n,
+                     float* out, double* stats, void* workspace, size_t workspace_bytes, void* stream) {
+  g_last_error.clear();
+  if (n < 0) return fail("ma_tick_features: negative tick count");
+  if (n == 0) return 0;
+  if (!timestamp || !price || !bid_price || !ask_price || !bid_volume || !ask_volume || !out || !stats)
+    return fail("ma_tick_features: null pointer");
+  if (!workspace || workspace_bytes < ma_tick_features_workspace_size(n))
+    return fail("ma_tick_features: workspace of %zu bytes needed, %zu given", ma_tick_features_workspace_size(n),
+                workspace_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  (void)hipGetLastError();
+  const ma_feat::TickCols c{timestamp, price, bid_price, ask_price, bid_volume, ask_volume};
+  const int blocks = (int)ma::imax64(1, ma::imin64(ma_feat::kStatBlocks, (n + 4095) / 4096));
+  double* partial = static_cast<double*>(workspace);
+  launch(false, ma_feat::features_stats, dim3((unsigned)blocks), dim3(ma_feat::kStatThreads), 0, st, c, n, partial);
+  launch(false, ma_feat::features_finish, dim3(1), dim3(64), 0, st, (const double*)partial, blocks, stats);
+  const int wblocks = (int)ma::imax64(1, ma::imin64(8192, (n + 1023) / 1024));
+  launch(true, ma_feat::features_write, dim3((unsigned)wblocks), dim3(256), 0, st, c, n, (const double*)stats, out);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail("ma_tick_features: kernel launch failed: %s", hipGetErrorString(e));
+  return 0;
 }
 
 int ma_attn_block_table(uint64_t seed, int64_t num_blocks, int64_t random_per_row, int32_t* out) {

@@ -8,22 +8,24 @@ import numpy as np
 import pytest
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(REPO, "include", "ma_attn.h")
+HEADERS = [os.path.join(REPO, "include", h) for h in ("ma_attn.h", "ma_features.h")]
 
 
 def _declared_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(ma_attn_\w+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(ma_(?:attn|tick)_\w+)\s*\(", text))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_symbol():
     import ma_attn
     names = _declared_functions()
-    assert len(names) >= 7
+    assert len(names) >= 11 and "ma_tick_features" in names
     lib = ctypes.CDLL(ma_attn.LIB_PATH)
     for n in names:
-        assert hasattr(lib, n), f"{n} declared in include/ma_attn.h but not exported"
+        assert hasattr(lib, n), f"{n} declared in include/ but not exported"
     assert ma_attn.LIB.ma_attn_abi_version() == ma_attn.ABI_VERSION
 
 
