@@ -22,6 +22,12 @@ forward pass over that batch.  Prints ONE JSON line:
 Inputs are resident in HBM before timing; 4+ distinct input sets (>1 GB in
 total) are rotated so the 256 MB MALL cannot serve a repeated set.
 
+Workload "ticks": the tick-feature pass (TickDataset preprocessing on the
+GPU, ma_tick_features) over 16M synthetic ticks; value = ticks/s, roofline =
+116 algorithmic bytes per tick (the six float64 columns read by the
+statistics kernel and again by the write kernel, 5 float32 written) over the
+pass's stamped duration.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
                        [--pass forward|backward]
 """
@@ -40,6 +46,9 @@ sys.path.insert(0, os.path.join(REPO, "ma-transformer_amd"))
 sys.path.insert(0, REPO)
 
 METRIC = "sparse-attn queries/sec + achieved HBM GB/s (% peak) at N=64K, w=64, 1 GPU"
+METRIC_TICKS = "tick-feature pass ticks/sec (TickDataset preprocessing), 1 GPU"
+TICKS_N = 1 << 24
+TICK_BYTES = 2 * 48 + 20  # two reads of 6 float64 columns, 5 float32 written
 METRIC_BWD = "sparse-attn backward queries/sec (dQ, dK, dV per query row), 1 GPU"
 HBM_PEAK_GBPS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
@@ -140,12 +149,99 @@ def cpu_baseline(B, H, N, D, dtype, pk, budget_s=12.0):
     }
 
 
+def cpu_baseline_ticks(n_total, budget_s=10.0):
+    """Oracle (numpy float64, one thread) on 2M-tick samples until ~budget_s."""
+    import numpy as np
+    from oracle import features as F
+    cols = F.synthetic_ticks(1 << 21, 77)
+    args = [cols[c] for c in ("timestamp", "price", "bid_price", "ask_price", "bid_volume", "ask_volume")]
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        F.tick_features(*args)
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= budget_s:
+            break
+    ticks = reps * (1 << 21)
+    return {"value": ticks / dt, "unit": "ticks/s", "cores": 1, "kind": "port",
+            "sample": f"oracle/features.py (numpy restatement of data_loader.py:15-28), {reps} x 2M ticks "
+                      f"({dt:.2f} s) of the {n_total}-tick workload's per-tick work on "
+                      f"{platform.processor() or platform.machine()} ({os.cpu_count()} host cpus, 1 used)"}
+
+
+def bench_ticks(args) -> int:
+    import torch
+    import tick_features as tf
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    n = TICKS_N
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(99)
+
+    def tick_set():
+        # synthetic ticks of the reference generator's shape, built on the device
+        ts = torch.sort(torch.rand(n, device=dev, dtype=torch.float64, generator=gen)).values
+        mid = 100.0 * torch.exp(torch.cumsum(torch.randn(n, device=dev, dtype=torch.float64, generator=gen), 0)
+                                * 1e-3)
+        half = mid * 1e-4 * (0.5 + torch.rand(n, device=dev, dtype=torch.float64, generator=gen))
+        side = torch.randint(-1, 2, (n,), device=dev, generator=gen).to(torch.float64)
+        vol = lambda: torch.clamp(torch.round(100.0 * (1 + 0.5 * torch.randn(n, device=dev, dtype=torch.float64,
+                                                                            generator=gen)).abs()), min=1.0)
+        return {"timestamp": ts, "price": mid + half * side, "bid_price": mid - half, "ask_price": mid + half,
+                "bid_volume": vol(), "ask_volume": vol()}
+
+    nsets = max(2, -(-(1 << 30) // (n * 68)))  # > 1 GB of inputs and outputs in rotation
+    sets = [tick_set() for _ in range(nsets)]
+    for i in range(args.warmup):
+        tf.compute_tick_features(sets[i % nsets])
+    stream = torch.cuda.current_stream(dev)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for i in range(args.steps):
+        tf.compute_tick_features(sets[i % nsets])
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = t0.elapsed_time(t1) / args.steps
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for a, b in ev:
+        a.record(stream)
+        b.record(stream)
+    torch.cuda.synchronize()
+    for i in range(args.steps):
+        tf.compute_tick_features(sets[i % nsets], events=ev[i])
+    torch.cuda.synchronize()
+    per = sorted(a.elapsed_time(b) for a, b in ev)
+    mean_ms = sum(per) / len(per)
+    alg = n * TICK_BYTES
+    gbps = alg / (mean_ms * 1e-3) / 1e9
+    out = {
+        "metric": METRIC_TICKS, "value": n / (ms_per_step * 1e-3), "unit": "ticks/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f64",
+        "data": f"synthetic GBM-shaped ticks built on the device, {nsets} rotated sets resident in HBM",
+        "config": {"workload": "tick-feature pass (TickDataset preprocessing)", "ticks": n},
+        "roofline": {"bound": "hbm", "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": gbps / HBM_PEAK_GBPS, "traffic": load_traffic("ticks")},
+        "kernel_us_mean": mean_ms * 1e3, "kernel_us_median": per[len(per) // 2] * 1e3,
+        "step_us_mean": ms_per_step * 1e3, "algorithmic_bytes_per_launch": alg,
+        "device": torch.cuda.get_device_name(dev),
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline_ticks(n)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="target", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="target", choices=sorted(WORKLOADS) + ["ticks"])
     ap.add_argument("--sets", type=int, default=0, help="input sets rotated (0: enough for >1 GB)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--pass", dest="which", choices=["forward", "backward"], default="forward",
@@ -155,6 +251,8 @@ def main() -> int:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "multi-GPU sharding is a design note, not a measured path.", file=sys.stderr)
         return 2
+    if args.workload == "ticks":
+        return bench_ticks(args)
 
     import torch
     import sparse_attention_cuda as ext

@@ -31,6 +31,17 @@ int ma_tick_features(const double* timestamp, const double* price, const double*
                      int64_t n, float* out, double* stats, void* workspace, size_t workspace_bytes,
                      void* stream);
 
+/*
+ * ma_tick_features with caller-created HIP events (hipEvent_t, either may be
+ * NULL) stamped on the pass's first kernel start and last kernel end
+ * (hipExtLaunchKernel), as ma_attn_forward_timed.  For timing; no
+ * counterpart in the reference.
+ */
+int ma_tick_features_timed(const double* timestamp, const double* price, const double* bid_price,
+                           const double* ask_price, const double* bid_volume, const double* ask_volume,
+                           int64_t n, float* out, double* stats, void* workspace, size_t workspace_bytes,
+                           void* stream, void* start_event, void* stop_event);
+
 #ifdef __cplusplus
 }
 #endif

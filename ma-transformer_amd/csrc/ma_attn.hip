@@ -1409,12 +1409,24 @@ int ma_tick_features(const double* timestamp, const double* price, const double*
   const int blocks = (int)ma::imax64(1, ma::imin64(ma_feat::kStatBlocks, (n + 4095) / 4096));
   double* partial = static_cast<double*>(workspace);
   launch(false, ma_feat::features_stats, dim3((unsigned)blocks), dim3(ma_feat::kStatThreads), 0, st, c, n, partial);
-  launch(false, ma_feat::features_finish, dim3(1), dim3(64), 0, st, (const double*)partial, blocks, stats);
+  launch(false, ma_feat::features_finish, dim3(1), dim3(ma_feat::kFinishThreads), 0, st, (const double*)partial, blocks, stats);
   const int wblocks = (int)ma::imax64(1, ma::imin64(8192, (n + 1023) / 1024));
   launch(true, ma_feat::features_write, dim3((unsigned)wblocks), dim3(256), 0, st, c, n, (const double*)stats, out);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail("ma_tick_features: kernel launch failed: %s", hipGetErrorString(e));
   return 0;
+}
+
+int ma_tick_features_timed(const double* timestamp, const double* price, const double* bid_price,
+                           const double* ask_price, const double* bid_volume, const double* ask_volume, int64_t n,
+                           float* out, double* stats, void* workspace, size_t workspace_bytes, void* stream,
+                           void* start_event, void* stop_event) {
+  g_ev_start = static_cast<hipEvent_t>(start_event);
+  g_ev_stop = static_cast<hipEvent_t>(stop_event);
+  const int rc = ma_tick_features(timestamp, price, bid_price, ask_price, bid_volume, ask_volume, n, out, stats,
+                                  workspace, workspace_bytes, stream);
+  g_ev_start = g_ev_stop = nullptr;
+  return rc;
 }
 
 int ma_attn_block_table(uint64_t seed, int64_t num_blocks, int64_t random_per_row, int32_t* out) {

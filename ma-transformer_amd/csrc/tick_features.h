@@ -10,11 +10,13 @@
 // and the sample standard deviation (ddof 1), and hands float32 rows to the
 // model.  Here the columns stay on the device (structure of arrays, float64)
 // and three launches produce the float32 [n, 5] rows:
-//   features_stats   grid-stride pass: per-block (count, mean, M2) of each
-//                    feature, combined across a block's threads in a fixed
-//                    tree (Chan et al.'s pairwise update);
-//   features_finish  one block: combines the per-block partials in block
-//                    order into mean and std (float64 [2][5]);
+//   features_stats   grid-stride pass: per-thread shifted sums turned into
+//                    (count, mean, M2) of each feature, combined across a
+//                    block's threads in a fixed tree (Chan et al.'s
+//                    pairwise update);
+//   features_finish  one wave per feature: combines the per-block partials
+//                    (strided per lane, then a fixed shuffle tree) into
+//                    mean and std (float64 [2][5]);
 //   features_write   grid-stride pass: (f - mean) / std, rounded once to
 //                    float32.
 // Each feature is formed with explicitly rounded float64 operations
@@ -62,68 +64,105 @@ __device__ __forceinline__ Moments merge(const Moments& a, const Moments& b) {
   if (a.n == 0.0) return b;
   if (b.n == 0.0) return a;
   const double n = a.n + b.n;
+  const double inv = 1.0 / n;
   const double d = b.mean - a.mean;
   Moments r;
   r.n = n;
-  r.mean = a.mean + d * (b.n / n);
-  r.m2 = a.m2 + b.m2 + d * d * (a.n * b.n / n);
+  r.mean = a.mean + d * (b.n * inv);
+  r.m2 = a.m2 + b.m2 + d * d * (a.n * b.n * inv);
   return r;
+}
+
+// Merge of one Moments per thread across a block of kStatThreads threads in a
+// fixed pairwise tree (thread t with t + w, w = 128, 64, ..., 1), so the
+// result does not depend on scheduling.  Valid in thread 0; sh is reusable
+// after the final barrier.
+__device__ __forceinline__ Moments block_merge(Moments m, double (*sh)[3]) {
+  const int t = threadIdx.x;
+  sh[t][0] = m.n;
+  sh[t][1] = m.mean;
+  sh[t][2] = m.m2;
+  __syncthreads();
+  for (int w = kStatThreads / 2; w > 0; w >>= 1) {
+    if (t < w) {
+      m = merge(m, Moments{sh[t + w][0], sh[t + w][1], sh[t + w][2]});
+      sh[t][0] = m.n;
+      sh[t][1] = m.mean;
+      sh[t][2] = m.m2;
+    }
+    __syncthreads();
+  }
+  return m;
 }
 
 __global__ __launch_bounds__(kStatThreads) void features_stats(TickCols c, int64_t n, double* partial) {
   __shared__ double sh[kStatThreads][3];
-  Moments acc[kFeatures];
+  // Shifted sums per thread (the shifted-data algorithm): s1 = sum(f - K),
+  // s2 = sum((f - K)^2) with K the thread's first value of the feature, so
+  // the loop has no division; M2 = s2 - s1^2 / cnt loses about
+  // eps * (1 + cnt (mean - K)^2 / M2) relative, O(eps) for K drawn from the
+  // column itself.
+  double shift[kFeatures], s1[kFeatures], s2[kFeatures];
 #pragma unroll
-  for (int k = 0; k < kFeatures; ++k) acc[k] = Moments{0.0, 0.0, 0.0};
+  for (int k = 0; k < kFeatures; ++k) shift[k] = s1[k] = s2[k] = 0.0;
+  double cnt = 0.0;
   const int64_t stride = (int64_t)gridDim.x * kStatThreads;
-  for (int64_t i = (int64_t)blockIdx.x * kStatThreads + threadIdx.x; i < n; i += stride) {
+  const int64_t i0 = (int64_t)blockIdx.x * kStatThreads + threadIdx.x;
+  if (i0 < n) tick_features(c, i0, shift);
+  for (int64_t i = i0; i < n; i += stride) {
     double f[kFeatures];
     tick_features(c, i, f);
+    cnt += 1.0;
 #pragma unroll
-    for (int k = 0; k < kFeatures; ++k) {  // Welford update
-      acc[k].n += 1.0;
-      const double d = f[k] - acc[k].mean;
-      acc[k].mean += d / acc[k].n;
-      acc[k].m2 += d * (f[k] - acc[k].mean);
+    for (int k = 0; k < kFeatures; ++k) {
+      const double d = f[k] - shift[k];
+      s1[k] += d;
+      s2[k] = fma(d, d, s2[k]);
     }
   }
   for (int k = 0; k < kFeatures; ++k) {
-    sh[threadIdx.x][0] = acc[k].n;
-    sh[threadIdx.x][1] = acc[k].mean;
-    sh[threadIdx.x][2] = acc[k].m2;
-    __syncthreads();
-    for (int w = kStatThreads / 2; w > 0; w >>= 1) {
-      if ((int)threadIdx.x < w) {
-        const Moments a{sh[threadIdx.x][0], sh[threadIdx.x][1], sh[threadIdx.x][2]};
-        const Moments b{sh[threadIdx.x + w][0], sh[threadIdx.x + w][1], sh[threadIdx.x + w][2]};
-        const Moments m = merge(a, b);
-        sh[threadIdx.x][0] = m.n;
-        sh[threadIdx.x][1] = m.mean;
-        sh[threadIdx.x][2] = m.m2;
-      }
-      __syncthreads();
+    Moments own{0.0, 0.0, 0.0};
+    if (cnt > 0.0) {
+      const double dm = s1[k] / cnt;
+      own = Moments{cnt, shift[k] + dm, fmax(s2[k] - s1[k] * dm, 0.0)};
     }
+    const Moments m = block_merge(own, sh);
     if (threadIdx.x == 0) {
       double* p = partial + ((int64_t)blockIdx.x * kFeatures + k) * 3;
-      p[0] = sh[0][0];
-      p[1] = sh[0][1];
-      p[2] = sh[0][2];
+      p[0] = m.n;
+      p[1] = m.mean;
+      p[2] = m.m2;
     }
-    __syncthreads();
   }
 }
 
-// stats: [0..4] means, [5..9] sample standard deviations (ddof 1)
-__global__ __launch_bounds__(64) void features_finish(const double* partial, int blocks, double* stats) {
-  const int k = threadIdx.x;
-  if (k >= kFeatures) return;
-  Moments m{0.0, 0.0, 0.0};
-  for (int b = 0; b < blocks; ++b) {
+// One wave per feature (kFeatures waves): lane l merges partials l, l + 64,
+// ... in order, then a fixed shuffle tree across the wave (lane l with
+// l + w, w = 32, ..., 1).  stats: [0..4] means, [5..9] sample standard
+// deviations (ddof 1; NaN for fewer than two ticks, as pandas).
+constexpr int kFinishThreads = 64 * kFeatures;
+
+__global__ __launch_bounds__(kFinishThreads) void features_finish(const double* partial, int blocks, double* stats) {
+  const int k = threadIdx.x >> 6, l = threadIdx.x & 63;
+  // the lane's partials are loaded before the first merge (kStatBlocks / 64 at most)
+  Moments part[kStatBlocks / 64];
+#pragma unroll
+  for (int j = 0; j < kStatBlocks / 64; ++j) {
+    const int b = l + 64 * j;
     const double* p = partial + ((int64_t)b * kFeatures + k) * 3;
-    m = merge(m, Moments{p[0], p[1], p[2]});
+    part[j] = b < blocks ? Moments{p[0], p[1], p[2]} : Moments{0.0, 0.0, 0.0};
   }
-  stats[k] = m.mean;
-  stats[kFeatures + k] = m.n > 1.0 ? sqrt(m.m2 / (m.n - 1.0)) : __builtin_nan("");
+  Moments m = part[0];
+#pragma unroll
+  for (int j = 1; j < kStatBlocks / 64; ++j) m = merge(m, part[j]);
+  for (int w = 32; w > 0; w >>= 1) {
+    const Moments o{__shfl_down(m.n, w), __shfl_down(m.mean, w), __shfl_down(m.m2, w)};
+    if (l < w) m = merge(m, o);
+  }
+  if (l == 0) {
+    stats[k] = m.mean;
+    stats[kFeatures + k] = m.n > 1.0 ? sqrt(m.m2 / (m.n - 1.0)) : __builtin_nan("");
+  }
 }
 
 __global__ __launch_bounds__(256) void features_write(TickCols c, int64_t n, const double* stats, float* out) {

@@ -25,12 +25,16 @@ _lib.ma_tick_features_workspace_size.argtypes = [ctypes.c_int64]
 _lib.ma_tick_features.restype = ctypes.c_int
 _lib.ma_tick_features.argtypes = [ctypes.c_void_p] * 6 + [ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
                                                           ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+_lib.ma_tick_features_timed.restype = ctypes.c_int
+_lib.ma_tick_features_timed.argtypes = _lib.ma_tick_features.argtypes + [ctypes.c_void_p] * 2
 
 
-def compute_tick_features(columns: dict):
+def compute_tick_features(columns: dict, events=None):
     """columns: the six raw tick columns (COLUMNS) as 1-D device tensors of one
     length.  Returns (float32 [n, 5] z-scored features, float64 [5] means,
-    float64 [5] sample stds), all on the device."""
+    float64 [5] sample stds), all on the device.  events: optional
+    (start, stop) torch.cuda.Event pair (recorded once already) stamped on the
+    pass's first kernel start and last kernel end."""
     cols = []
     for name in COLUMNS:
         t = columns[name]
@@ -47,8 +51,12 @@ def compute_tick_features(columns: dict):
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         stream = torch.cuda.current_stream(dev).cuda_stream
-        rc = _lib.ma_tick_features(*(c.data_ptr() for c in cols), n, out.data_ptr(), stats.data_ptr(),
-                                   ws.data_ptr(), nbytes, stream or None)
+        args = [*(c.data_ptr() for c in cols), n, out.data_ptr(), stats.data_ptr(), ws.data_ptr(), nbytes,
+                stream or None]
+        if events is not None:
+            rc = _lib.ma_tick_features_timed(*args, events[0].cuda_event or None, events[1].cuda_event or None)
+        else:
+            rc = _lib.ma_tick_features(*args)
     if rc != 0:
         raise RuntimeError(_ma.last_error())
     return out, stats[:5], stats[5:]

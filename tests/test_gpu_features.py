@@ -83,3 +83,19 @@ def test_tick_dataset_csv_matches_reference_items(tf, tmp_path):
     xb = torch.stack([ds[i][0] for i in range(64)])
     with torch.no_grad():
         assert m(xb).shape == (64, 1)
+
+
+def test_tick_features_timed_matches(tf):
+    """ma_tick_features_timed: the same rows and statistics, and a positive
+    stamped duration for the pass."""
+    from oracle import features as F
+    dc = _dev_cols(F.synthetic_ticks(50_000, 3))
+    z0, m0, s0 = tf.compute_tick_features(dc)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    b.record()
+    torch.cuda.synchronize()
+    z1, m1, s1 = tf.compute_tick_features(dc, events=(a, b))
+    torch.cuda.synchronize()
+    assert torch.equal(z0, z1) and torch.equal(m0, m1) and torch.equal(s0, s1)
+    assert a.elapsed_time(b) > 0
