@@ -149,6 +149,27 @@ def cpu_baseline(B, H, N, D, dtype, pk, budget_s=12.0):
     }
 
 
+def copy_bandwidth(dev, stream) -> float:
+    """GB/s of a 1 GiB torch copy on this box (read + write), for comparison
+    with the 8 TB/s spec; its dispatches also calibrate the rocprofv3 HBM
+    counters (FETCH_SIZE / WRITE_SIZE of a known byte count)."""
+    import torch
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    c0.record(stream)
+    for _ in range(10):
+        dst.copy_(src)
+    c1.record(stream)
+    torch.cuda.synchronize()
+    gbps = 2 * (1 << 30) * 10 / (c0.elapsed_time(c1) * 1e-3) / 1e9
+    del src, dst
+    return gbps
+
+
 def cpu_baseline_ticks(n_total, budget_s=10.0):
     """Oracle (numpy float64, one thread) on 2M-tick samples until ~budget_s."""
     import numpy as np
@@ -218,6 +239,8 @@ def bench_ticks(args) -> int:
     mean_ms = sum(per) / len(per)
     alg = n * TICK_BYTES
     gbps = alg / (mean_ms * 1e-3) / 1e9
+    del sets
+    copy_gbps = copy_bandwidth(dev, stream)
     out = {
         "metric": METRIC_TICKS, "value": n / (ms_per_step * 1e-3), "unit": "ticks/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
@@ -228,7 +251,7 @@ def bench_ticks(args) -> int:
                      "frac": gbps / HBM_PEAK_GBPS, "traffic": load_traffic("ticks")},
         "kernel_us_mean": mean_ms * 1e3, "kernel_us_median": per[len(per) // 2] * 1e3,
         "step_us_mean": ms_per_step * 1e3, "algorithmic_bytes_per_launch": alg,
-        "device": torch.cuda.get_device_name(dev),
+        "copy_kernel_gbps": copy_gbps, "device": torch.cuda.get_device_name(dev),
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline_ticks(n)
@@ -341,20 +364,7 @@ def main() -> int:
     achieved_gbps = alg_bytes / (mean_launch_ms * 1e-3) / 1e9
     traffic = None if bwd else load_traffic(args.workload)
 
-    # copy-kernel bandwidth on this box, for comparison with the 8 TB/s spec
-    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-    dst = torch.empty_like(src)
-    for _ in range(3):
-        dst.copy_(src)
-    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    c0.record(stream)
-    for _ in range(10):
-        dst.copy_(src)
-    c1.record(stream)
-    torch.cuda.synchronize()
-    copy_gbps = 2 * (1 << 30) * 10 / (c0.elapsed_time(c1) * 1e-3) / 1e9
-    del src, dst
+    copy_gbps = copy_bandwidth(dev, stream)
 
     # the bound is whichever peak the algorithmic work reaches first
     mfma_peak = MFMA_BF16_PEAK_TFLOPS if dt_name == "bf16" else MFMA_F32_PEAK_TFLOPS
