@@ -111,6 +111,16 @@ def load_traffic(workload: str):
     return float(m.group(1)) if m else None
 
 
+def load_mfma_busy(workload: str):
+    """MFMA busy % of the workload's dominant forward kernel, from the
+    committed rocprofv3 MfmaUtil summary, or None."""
+    path = os.path.join(REPO, "profiles", "mfma_busy_by_workload.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"^mfma_busy_pct\[" + re.escape(workload) + r"\]:\s*([0-9.eE+]+)", open(path).read(), re.M)
+    return float(m.group(1)) if m else None
+
+
 def cpu_baseline(B, H, N, D, dtype, pk, budget_s=12.0):
     """Oracle (single thread) on a bounded sample: whole heads until ~budget_s."""
     import numpy as np
@@ -400,6 +410,8 @@ def main() -> int:
         "flops_per_launch": flops,
         "tflops": flops / (mean_launch_ms * 1e-3) / 1e12,
         "mfma_bf16_frac_of_peak": (flops / (mean_launch_ms * 1e-3) / 1e12) / MFMA_BF16_PEAK_TFLOPS,
+        # rocprofv3 MfmaUtil of the forward kernel (committed summary), not measured in this run
+        "mfma_busy_pct": None if bwd else load_mfma_busy(args.workload),
         "copy_kernel_gbps": copy_gbps,
         "device": torch.cuda.get_device_name(dev),
     }
