@@ -13,7 +13,7 @@
 // LDS ring with the next block in flight into registers:
 //
 // bwd_q_kernel   query tile.  Each key block is staged as (K rows, K^T) and
-//   (V rows, V^T) -- the 16-bit stream layout with K or V in both parts.
+//   V rows -- the 16-bit stream layout with K in both parts.
 //   Pass 1 over the band: S^T = K Q^T and dP^T = V dO^T on 16x16x32 MFMA,
 //   online max / sum / sum(e * dp), giving lse2 and delta with no O.  Pass 2
 //   over the same blocks: dS^T from registers, dQ^T += K^T dS^T (pv2).
@@ -261,11 +261,13 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
   auto buf_of = [&](int e) { return resident ? (e < nb ? e : e - nb) : (e & 1); };
   auto off_of = [&](int e) { return e < (resident ? nb : items) ? (uint32_t)(64 * blk_of(e)) * tb : kOob; };
 
-  typename P::Slot xk, xv;
+  // V is read only as rows (dP^T = V dO^T): its transposed part stays unwritten
+  typename P::Slot xk;
+  typename P::Rows xv;
   P::load_slot(xk, Kr, Kr, off_of(0), tid, tb);
-  P::load_slot(xv, Vr, Vr, off_of(0), tid, tb);
+  P::load_rows(xv, Vr, off_of(0), tid, tb);
   P::store_slot(xk, ring, tid);
-  P::store_slot(xv, ring + P::kSlot, tid);
+  P::store_rows(xv, ring + P::kSlot, tid);
   __syncthreads();
 
   const float sl2 = a.scale_log2;
@@ -277,7 +279,7 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
 
   for (int e = 0; e < items; ++e) {
     P::load_slot(xk, Kr, Kr, off_of(e + 1), tid, tb);
-    P::load_slot(xv, Vr, Vr, off_of(e + 1), tid, tb);
+    P::load_rows(xv, Vr, off_of(e + 1), tid, tb);
     const uint8_t* sk = ring + buf_of(e) * kBuf;
     f32x4 s[4], dp[4];
     bwdq_scores<P>(sk, sk + P::kSlot, kl, qr, gr, 64 * blk_of(e), q0, L, R, dl, g, w.Nr, s, dp);
@@ -291,7 +293,7 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
     // barrier that ended item e-1); resident bands load nothing after pass 1
     if (!resident || e + 1 < nb) {
       P::store_slot(xk, ring + buf_of(e + 1) * kBuf, tid);
-      P::store_slot(xv, ring + buf_of(e + 1) * kBuf + P::kSlot, tid);
+      P::store_rows(xv, ring + buf_of(e + 1) * kBuf + P::kSlot, tid);
     }
     __syncthreads();
   }
@@ -371,6 +373,120 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdArgs a) {
   P::store_o(acc_k, a.scale, DKr, krow, g);
 }
 
+// ---------------------------------------------------------------- fixed-window interior tiles
+//
+// For a fixed band [m-L, m+R] (BASELINE causal 64: L = 63, R = 0) an interior
+// tile's geometry is compile-time, as in the forward's window_tile: a wave's
+// 16 rows touch NSUB sub-tiles of 16 streamed rows at fixed offsets from its
+// own (5 for causal 64, against 8 for whole 64-row blocks), and only the
+// first and last need a mask.  The scores of all of them stay in registers,
+// so the statistics need no online rescaling, and pass 2 reuses pass 1's
+// exponentials (p = e / l) instead of recomputing exp2.
+
+// bwd_q_stream_kernel, interior tile t: the wave's queries qa = 64t + 16wv
+// against key sub-tiles s = 4t + wv - CL + j, block s >> 2 in ring buffer
+// (s >> 2) & 1.  Gives lse2 and delta of query qa + c and dQ^T (unscaled).
+template <class P, int L, int R>
+__device__ __forceinline__ void bwdq_window_tile(const uint8_t* ring, uint32_t kl, uint32_t vl, const typename P::Q& qr,
+                                                 const typename P::Q& gr, int t, int wv, int dl, float sl2,
+                                                 float& lse2, float& dlt, f32x4 (&acc)[4]) {
+  using G = WinGeom<L, R, 64>;
+  constexpr int kBuf = 2 * P::kSlot;
+  f32x4 e[G::NSUB], dp[G::NSUB];
+  uint32_t kt[G::NSUB];  // K^T of sub-tile j (the K buffer's transposed part)
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < G::NSUB; ++j) {
+    const int s = 4 * t + wv - G::CL + j;
+    const uint32_t bb = (uint32_t)(((s >> 2) & 1) * kBuf);
+    const int u = s & 3;
+    kt[j] = bb + P::v_sub(u) + vl;
+    f32x4 z = P::qk(ring + bb + P::k_sub(u) + kl, qr);
+    dp[j] = P::qk(ring + bb + P::kSlot + P::k_sub(u) + kl, gr);
+    const int rel = 16 * (j - G::CL);     // key - query offsets span [rel-15, rel+15]
+    if (rel - 15 < -L || rel + 15 > R) {  // resolved at compile time
+#pragma unroll
+      for (int r = 0; r < 4; ++r) z[r] = (uint32_t)(dl + rel + r) <= (uint32_t)(L + R) ? z[r] : -INFINITY;
+    }
+    e[j] = z;
+    mx = fmaxf(mx, fmaxf(fmaxf(z[0], z[1]), fmaxf(z[2], z[3])));
+  }
+  const float m_use = col_max(mx) * sl2;  // finite: every query sees its own key
+  float l_run = 0.0f, a_run = 0.0f;
+#pragma unroll
+  for (int j = 0; j < G::NSUB; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float x = __builtin_amdgcn_exp2f(fmaf(e[j][r], sl2, -m_use));
+      e[j][r] = x;
+      l_run += x;
+      a_run = fmaf(x, dp[j][r], a_run);
+    }
+  const float l_tot = col_sum(l_run);
+  const float inv = __builtin_amdgcn_rcpf(l_tot);
+  lse2 = m_use + __log2f(l_tot);
+  dlt = col_sum(a_run) * inv;
+#pragma unroll
+  for (int j = 0; j < G::NSUB; j += 2) {
+    float d0[4], d1[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) d0[r] = e[j][r] * inv * (dp[j][r] - dlt);
+    if (j + 1 < G::NSUB) {  // resolved at compile time
+#pragma unroll
+      for (int r = 0; r < 4; ++r) d1[r] = e[j + 1][r] * inv * (dp[j + 1][r] - dlt);
+      P::pv2(ring + kt[j], ring + kt[j + 1], d0, d1, acc);
+    } else {
+      P::pv(ring + kt[j], d0, acc);
+    }
+  }
+}
+
+// bwd_kv_stream_kernel, interior tile t: the wave's keys ka = 64t + 16wv
+// against query sub-tiles s = 4t + wv - CR + j (the mirrored band: queries of
+// key k are [k-R, k+L]), block s >> 2 in ring buffer (s >> 2) & 1 with its
+// staged statistics.  dV^T and dK^T (unscaled) accumulate in acc_v, acc_k.
+template <class P, int L, int R>
+__device__ __forceinline__ void bwdkv_window_tile(const uint8_t* ring, uint32_t kl, uint32_t vl, const typename P::Q& kr,
+                                                  const typename P::Q& vr, int t, int wv, int g, int dl, float sl2,
+                                                  f32x4 (&acc_k)[4], f32x4 (&acc_v)[4]) {
+  using G = WinGeom<R, L, 64>;
+  constexpr int kBuf = 2 * P::kSlot + 512;
+  float p[G::NSUB][4], d[G::NSUB][4];
+  uint32_t qt[G::NSUB];  // Q^T of sub-tile j (dO^T at + kSlot)
+#pragma unroll
+  for (int j = 0; j < G::NSUB; ++j) {
+    const int s = 4 * t + wv - G::CL + j;
+    const uint32_t bb = (uint32_t)(((s >> 2) & 1) * kBuf);
+    const int u = s & 3;
+    qt[j] = bb + P::v_sub(u) + vl;
+    f32x4 z = P::qk(ring + bb + P::k_sub(u) + kl, kr);                  // S[query 4g+r][key c]
+    const f32x4 dz = P::qk(ring + bb + P::kSlot + P::k_sub(u) + kl, vr);  // dP[query][key c]
+    const int rel = 16 * (G::CL - j);     // key - query offsets span [rel-15, rel+15]
+    if (rel - 15 < -L || rel + 15 > R) {  // resolved at compile time
+#pragma unroll
+      for (int r = 0; r < 4; ++r) z[r] = (uint32_t)(dl + rel - r) <= (uint32_t)(L + R) ? z[r] : -INFINITY;
+    }
+    const float* st = reinterpret_cast<const float*>(ring + bb + 2 * P::kSlot);
+    const f32x4 lse = *reinterpret_cast<const f32x4*>(st + 16 * u + 4 * g);
+    const f32x4 del = *reinterpret_cast<const f32x4*>(st + 64 + 16 * u + 4 * g);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[j][r] = __builtin_amdgcn_exp2f(fmaf(z[r], sl2, -lse[r]));
+      d[j][r] = p[j][r] * (dz[r] - del[r]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < G::NSUB; j += 2) {
+    if (j + 1 < G::NSUB) {  // resolved at compile time
+      P::pv2(ring + qt[j] + P::kSlot, ring + qt[j + 1] + P::kSlot, p[j], p[j + 1], acc_v);  // dV^T += dO^T P
+      P::pv2(ring + qt[j], ring + qt[j + 1], d[j], d[j + 1], acc_k);                      // dK^T += Q^T dS
+    } else {
+      P::pv(ring + qt[j] + P::kSlot, p[j], acc_v);
+      P::pv(ring + qt[j], d[j], acc_k);
+    }
+  }
+}
+
 // ---------------------------------------------------------------- chunks of tiles per workgroup
 //
 // For bands of at most two 64-row blocks (windows like the BASELINE causal
@@ -407,7 +523,9 @@ __device__ __forceinline__ bool bwd_chunk(const BwdArgs& a, BwdChunk& w) {
   return w.t0 < w.t1;
 }
 
-template <class P>
+// FL >= 0: specialised for the band [m-FL, m+FR] (interior tiles take the
+// fixed-window tiles above); FL < 0: any band of at most two blocks.
+template <class P, int FL, int FR>
 __global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 slots x (K slot, V slot)
   using Elt = typename P::Elt;
@@ -437,12 +555,13 @@ __global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
   typename P::Q qr, gr, qn, gn;
   P::load_q(qr, Qr, (uint32_t)(64 * w.t0) * tb + lrow, g);
   P::load_q(gr, Gr, (uint32_t)(64 * w.t0) * tb + lrow, g);
-  typename P::Slot xk, xv;
+  typename P::Slot xk;
+  typename P::Rows xv;  // V is read only as rows
   for (int j = lo_of(w.t0); j <= hi_of(w.t0); ++j) {
     P::load_slot(xk, Kr, Kr, (uint32_t)(64 * j) * tb, tid, tb);
-    P::load_slot(xv, Vr, Vr, (uint32_t)(64 * j) * tb, tid, tb);
+    P::load_rows(xv, Vr, (uint32_t)(64 * j) * tb, tid, tb);
     P::store_slot(xk, ring + (j & 1) * kBuf, tid);
-    P::store_slot(xv, ring + (j & 1) * kBuf + P::kSlot, tid);
+    P::store_rows(xv, ring + (j & 1) * kBuf + P::kSlot, tid);
   }
   __syncthreads();
 
@@ -454,30 +573,42 @@ __global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
     const int nblk_new = more && hi_of(t + 1) > hi_of(t) ? hi_of(t + 1) : -1;
     const uint32_t noff = nblk_new >= 0 ? (uint32_t)(64 * nblk_new) * tb : kOob;
     P::load_slot(xk, Kr, Kr, noff, tid, tb);
-    P::load_slot(xv, Vr, Vr, noff, tid, tb);
+    P::load_rows(xv, Vr, noff, tid, tb);
     const uint32_t nrow = more ? (uint32_t)(64 * (t + 1)) * tb + lrow : kOob;
     P::load_q(qn, Qr, nrow, g);
     P::load_q(gn, Gr, nrow, g);
 
     const int q0 = 64 * t + 16 * wv;
-    const int lo = lo_of(t), hi = hi_of(t);  // hi - lo is 0 or 1
-    // Both blocks' scores stay in registers from pass 1 to pass 2.
-    float m_run = -INFINITY, l_run = 0.0f, a_run = 0.0f, lse2, dlt;
-    const uint8_t* sk0 = ring + (lo & 1) * kBuf;
-    const uint8_t* sk1 = ring + (hi & 1) * kBuf;
-    f32x4 s0[4], dp0[4], s1[4], dp1[4];
-    bwdq_scores<P>(sk0, sk0 + P::kSlot, kl, qr, gr, 64 * lo, q0, L, R, dl, g, w.Nr, s0, dp0);
-    bwdq_pass1(s0, dp0, sl2, m_run, l_run, a_run);
-    if (hi > lo) {
-      bwdq_scores<P>(sk1, sk1 + P::kSlot, kl, qr, gr, 64 * hi, q0, L, R, dl, g, w.Nr, s1, dp1);
-      bwdq_pass1(s1, dp1, sl2, m_run, l_run, a_run);
-    }
-    bwdq_stats(m_run, l_run, a_run, sl2, lse2, dlt);
+    float lse2, dlt;
     f32x4 acc[4];
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    bwdq_pass2<P>(sk0, vl, s0, dp0, sl2, lse2, dlt, acc);
-    if (hi > lo) bwdq_pass2<P>(sk1, vl, s1, dp1, sl2, lse2, dlt, acc);
+    bool done = false;
+    if constexpr (FL >= 0) {
+      // interior: every key sub-tile of every wave lies in [0, Nr)
+      using G = WinGeom<FL, FR, 64>;
+      if (4 * t - G::CL >= 0 && 16 * (4 * t + 3 - G::CL + G::NSUB) <= w.Nr) {
+        bwdq_window_tile<P, FL, FR>(ring, kl, vl, qr, gr, t, wv, dl, sl2, lse2, dlt, acc);
+        done = true;
+      }
+    }
+    if (!done) {
+      const int lo = lo_of(t), hi = hi_of(t);  // hi - lo is 0 or 1
+      // Both blocks' scores stay in registers from pass 1 to pass 2.
+      float m_run = -INFINITY, l_run = 0.0f, a_run = 0.0f;
+      const uint8_t* sk0 = ring + (lo & 1) * kBuf;
+      const uint8_t* sk1 = ring + (hi & 1) * kBuf;
+      f32x4 s0[4], dp0[4], s1[4], dp1[4];
+      bwdq_scores<P>(sk0, sk0 + P::kSlot, kl, qr, gr, 64 * lo, q0, L, R, dl, g, w.Nr, s0, dp0);
+      bwdq_pass1(s0, dp0, sl2, m_run, l_run, a_run);
+      if (hi > lo) {
+        bwdq_scores<P>(sk1, sk1 + P::kSlot, kl, qr, gr, 64 * hi, q0, L, R, dl, g, w.Nr, s1, dp1);
+        bwdq_pass1(s1, dp1, sl2, m_run, l_run, a_run);
+      }
+      bwdq_stats(m_run, l_run, a_run, sl2, lse2, dlt);
+      bwdq_pass2<P>(sk0, vl, s0, dp0, sl2, lse2, dlt, acc);
+      if (hi > lo) bwdq_pass2<P>(sk1, vl, s1, dp1, sl2, lse2, dlt, acc);
+    }
     P::store_o(acc, a.scale, DQr, (uint32_t)(64 * t) * tb + lrow, g);
     const int64_t srow = (((int64_t)w.b * a.N + w.rho + (int64_t)a.dil * (q0 + c)) * a.H + w.h);
     if (g == 0 && q0 + c < w.Nr) *reinterpret_cast<float2*>(a.stats + 2 * srow) = make_float2(lse2, dlt);
@@ -486,7 +617,7 @@ __global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
     __syncthreads();
     if (nblk_new >= 0) {
       P::store_slot(xk, ring + (nblk_new & 1) * kBuf, tid);
-      P::store_slot(xv, ring + (nblk_new & 1) * kBuf + P::kSlot, tid);
+      P::store_rows(xv, ring + (nblk_new & 1) * kBuf + P::kSlot, tid);
     }
     __syncthreads();
     qr = qn;
@@ -494,7 +625,7 @@ __global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
   }
 }
 
-template <class P>
+template <class P, int FL, int FR>
 __global__ __launch_bounds__(256, 2) void bwd_kv_stream_kernel(BwdArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 slots x (Q slot, dO slot, stats)
   using Elt = typename P::Elt;
@@ -555,11 +686,21 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_stream_kernel(BwdArgs a) {
     f32x4 acc_k[4], acc_v[4];
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) acc_k[dt] = acc_v[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int j = lo_of(t); j <= hi_of(t); ++j) {
-      const uint8_t* sq = ring + (j & 1) * kBuf;
-      bwdkv_block<P>(sq, sq + P::kSlot, reinterpret_cast<const float*>(sq + 2 * P::kSlot), kl, vl, kr, vr, 64 * j,
-                     k0, L, R, dl, g, w.Nr, a.scale_log2, acc_k, acc_v);
+    bool done = false;
+    if constexpr (FL >= 0) {
+      // interior: every query sub-tile of every wave lies in [0, Nr)
+      using G = WinGeom<FR, FL, 64>;
+      if (4 * t - G::CL >= 0 && 16 * (4 * t + 3 - G::CL + G::NSUB) <= w.Nr) {
+        bwdkv_window_tile<P, FL, FR>(ring, kl, vl, kr, vr, t, wv, g, dl, a.scale_log2, acc_k, acc_v);
+        done = true;
+      }
     }
+    if (!done)
+      for (int j = lo_of(t); j <= hi_of(t); ++j) {
+        const uint8_t* sq = ring + (j & 1) * kBuf;
+        bwdkv_block<P>(sq, sq + P::kSlot, reinterpret_cast<const float*>(sq + 2 * P::kSlot), kl, vl, kr, vr, 64 * j,
+                       k0, L, R, dl, g, w.Nr, a.scale_log2, acc_k, acc_v);
+      }
     const uint32_t orow = (uint32_t)(64 * t) * tb + lrow;
     P::store_o(acc_v, 1.0f, DVr, orow, g);
     P::store_o(acc_k, a.scale, DKr, orow, g);

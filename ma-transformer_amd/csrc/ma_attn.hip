@@ -1176,21 +1176,24 @@ int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* 
   const bool chunked = ma::floordiv64(63 + R, 64) - ma::floordiv64(-L, 64) + 1 <= 2 &&
                        ma::floordiv64(63 + L, 64) - ma::floordiv64(-R, 64) + 1 <= 2 &&
                        !getenv("MA_ATTN_BWD_PER_TILE");
-  auto kq = chunked ? &bwd_q_stream_kernel<P> : &bwd_q_kernel<P>;
-  auto kkv = chunked ? &bwd_kv_stream_kernel<P> : &bwd_kv_kernel<P>;
+  // the causal-64 band (BASELINE target, dilated config) has a fixed-window instantiation
+  const bool fixed = chunked && L == 63 && R == 0 && !getenv("MA_ATTN_BWD_NO_FIXED");
+  auto kq = !chunked ? &bwd_q_kernel<P> : fixed ? &bwd_q_stream_kernel<P, 63, 0> : &bwd_q_stream_kernel<P, -1, -1>;
+  auto kkv = !chunked ? &bwd_kv_kernel<P> : fixed ? &bwd_kv_stream_kernel<P, 63, 0> : &bwd_kv_stream_kernel<P, -1, -1>;
+  const int variant = !chunked ? 0 : fixed ? 2 : 1;
   // chunks per stream fitted to the 512 resident workgroups (2 per CU)
   const int64_t per_stream = ma::imax64(1, 512 / streams);
   a.chunk = (int32_t)ma::imax64(1, (a.tiles + per_stream - 1) / per_stream);
   a.chunks = (int32_t)((a.tiles + a.chunk - 1) / a.chunk);
   const int64_t wgs = chunked ? streams * a.chunks : streams * a.tiles;
-  static bool attr_set[2] = {false, false};
-  if (!attr_set[chunked]) {
+  static bool attr_set[3] = {false, false, false};
+  if (!attr_set[variant]) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kq), hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)shm_q) != hipSuccess ||
         hipFuncSetAttribute(reinterpret_cast<const void*>(kkv), hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)shm_kv) != hipSuccess)
       return fail("ma_attn_backward: cannot reserve LDS for the backward kernels");
-    attr_set[chunked] = true;
+    attr_set[variant] = true;
   }
   launch(false, kq, dim3((unsigned)wgs), dim3(256), (uint32_t)shm_q, st, a);
   launch(true, kkv, dim3((unsigned)wgs), dim3(256), (uint32_t)shm_kv, st, a);

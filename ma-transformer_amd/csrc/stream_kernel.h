@@ -108,6 +108,22 @@ struct HalfPath {
     s.r[3] = bload16(Vr, v + tb);
   }
 
+  // Row part only (a slot whose transposed part is never read).
+  struct Rows {
+    uint4 r[2];  // rows tid>>3 and (tid>>3)+32 at column tid&7
+  };
+  static __device__ __forceinline__ void load_rows(Rows& s, __amdgpu_buffer_rsrc_t Kr, uint32_t row_off, int tid,
+                                                   uint32_t tb) {
+    const uint32_t k = row_off + (tid >> 3) * tb + (tid & 7) * 16;
+    s.r[0] = bload16(Kr, k);
+    s.r[1] = bload16(Kr, k + 32 * tb);
+  }
+  static __device__ __forceinline__ void store_rows(const Rows& s, uint8_t* slot, int tid) {
+    const int chk = tid & 7;
+    *reinterpret_cast<uint4*>(slot + (tid >> 3) * kKRow + 16 * chk) = s.r[0];
+    *reinterpret_cast<uint4*>(slot + ((tid >> 3) + 32) * kKRow + 16 * chk) = s.r[1];
+  }
+
   // V^T words: (key 2kp, key 2kp+1) pairs of one head_dim row, built with v_perm.
   static __device__ __forceinline__ void store_slot(const Slot& s, uint8_t* slot, int tid) {
     const int chk = tid & 7;

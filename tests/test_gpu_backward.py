@@ -169,6 +169,31 @@ def test_backward_chunked(ext, oracle, N, H, left, right, dil):
     _check(got, oracle.backward(spec, *up), torch.bfloat16)
 
 
+@pytest.mark.parametrize("N,H,dil", [(5000, 16, 1), (4099, 8, 4)])
+def test_backward_chunked_generic(ext, oracle, monkeypatch, N, H, dil):
+    """The causal-64 band on the generic stream tiles (fixed-window tiles
+    switched off with MA_ATTN_BWD_NO_FIXED) stays correct."""
+    monkeypatch.setenv("MA_ATTN_BWD_NO_FIXED", "1")
+    shape = (2, N, H, 64)
+    (q, k, v, g), up = _case(shape, 890 + N + dil, torch.bfloat16)
+    got = ext.sliding_backward(q, k, v, g, 63, 0, dil)
+    spec = oracle.Spec(*shape, pattern="sliding", left=63, right=0, dilation=dil)
+    _check(got, oracle.backward(spec, *up), torch.bfloat16)
+
+
+@pytest.mark.parametrize("N", [64, 127, 128, 129, 191, 192, 255, 256, 257, 1000])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_backward_fixed_window_edges(ext, oracle, N, dtype):
+    """Causal 64 (fixed-window tiles inside, generic tiles at the sequence
+    ends): lengths around the interior-tile bounds (the dQ kernel's tile t
+    needs 64t + 64 <= N, the dK/dV kernel's 64t + 128 <= N)."""
+    shape = (1, N, 4, 64)
+    (q, k, v, g), up = _case(shape, 910 + N, dtype)
+    got = ext.sliding_backward(q, k, v, g, 63, 0, 1)
+    spec = oracle.Spec(*shape, pattern="sliding", left=63, right=0)
+    _check(got, oracle.backward(spec, *up), dtype)
+
+
 def test_backward_target_shape(ext, oracle):
     """The headline shape in bf16 (B=1 H=8 N=65536 D=64, causal w=64): whole
     gradients against the oracle."""
