@@ -134,15 +134,43 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void block_row_kernel(BlockArgs
     return cb >= 0 ? (uint32_t)(64 * cb) * tb : kOob;
   };
 
+  float m_run = -INFINITY, l_run = 0.0f;
+  f32x4 acc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const float sl2 = a.scale_log2;
+  const int ql = 16 * wv + c;
+
+  if (!dense && a.bpr <= 4) {
+    // Short rows (the BASELINE table has 4 entries): every block's loads are
+    // issued at once, so the row pays one HBM latency instead of one per
+    // block; the two-slot ring is filled twice.
+    typename P::Slot x[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) P::load_slot(x[e], Kr, Vr, blk_off(e), tid, tb);
+    P::store_slot(x[0], ring, tid);
+    P::store_slot(x[1], ring + P::kSlot, tid);
+    __syncthreads();
+    if (ne > 0) block_update<P>(ring, kl, vl, q, block_of(0), false, ql, N, g, sl2, m_run, l_run, acc);
+    if (ne > 1) block_update<P>(ring + P::kSlot, kl, vl, q, block_of(1), false, ql, N, g, sl2, m_run, l_run, acc);
+    if (ne > 2) {  // uniform
+      __syncthreads();
+      P::store_slot(x[2], ring, tid);
+      P::store_slot(x[3], ring + P::kSlot, tid);
+      __syncthreads();
+      block_update<P>(ring, kl, vl, q, block_of(2), false, ql, N, g, sl2, m_run, l_run, acc);
+      if (ne > 3) block_update<P>(ring + P::kSlot, kl, vl, q, block_of(3), false, ql, N, g, sl2, m_run, l_run, acc);
+    }
+    const float l_tot = col_sum(l_run);
+    P::store_o(acc, l_tot > 0.0f ? __builtin_amdgcn_rcpf(l_tot) : 0.0f, Or, qrow, g);
+    return;
+  }
+
   typename P::Slot nxt;
   P::load_slot(nxt, Kr, Vr, blk_off(0), tid, tb);
   P::store_slot(nxt, ring, tid);
   __syncthreads();
 
-  float m_run = -INFINITY, l_run = 0.0f;
-  f32x4 acc[4];
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   for (int e = 0; e < ne; ++e) {
     P::load_slot(nxt, Kr, Vr, blk_off(e + 1), tid, tb);
     const int cb = block_of(e);
