@@ -71,10 +71,14 @@ __device__ __forceinline__ void block_update(const uint8_t* slot, uint32_t kl, u
   for (int u = 0; u < 4; ++u) mx = fmaxf(mx, fmaxf(fmaxf(sc[u][0], sc[u][1]), fmaxf(sc[u][2], sc[u][3])));
   const float m_new = fmaxf(m_run, col_max(mx));
   const float m_use = m_new == -INFINITY ? 0.0f : m_new * sl2;
-  const float corr = __builtin_amdgcn_exp2f(m_run * sl2 - m_use);  // 0 on a row's first block
-  l_run *= corr;
+  // Rescale only when some lane's running max rose (wave-uniform test): on
+  // long rows the max settles after a few blocks and most blocks skip it.
+  if (__builtin_amdgcn_ballot_w64(m_new != m_run) != 0) {
+    const float corr = __builtin_amdgcn_exp2f(m_run * sl2 - m_use);  // 0 on a row's first block
+    l_run *= corr;
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt) acc[dt] *= corr;
+    for (int dt = 0; dt < 4; ++dt) acc[dt] *= corr;
+  }
   m_run = m_new;
 #pragma unroll
   for (int u = 0; u < 4; u += 2) {
