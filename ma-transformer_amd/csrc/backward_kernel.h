@@ -92,27 +92,37 @@ __device__ __forceinline__ void bwd_mask(f32x4& z, int x, int span, int idx0, in
 // One 64-row block of the streamed operand against this wave's 16 rows.
 
 // Scores S^T = K Q^T and dP^T = V dO^T of one key block (sk: (K, K^T) slot,
-// sv: (V, V^T) slot) for this wave's queries q0..q0+15, masked to the band.
+// sv: V rows) for this wave's queries q0..q0+15, masked to the band.
+// Returns the wave-uniform mask of live sub-tiles: a sub-tile with no key in
+// any of the 16 queries' bands (or past the end) is not computed (scores
+// -inf, dP 0), and the passes below skip it.
 template <class P>
-__device__ __forceinline__ void bwdq_scores(const uint8_t* sk, const uint8_t* sv, uint32_t kl, const typename P::Q& qr,
-                                            const typename P::Q& gr, int key0, int q0, int L, int R, int dl, int g,
-                                            int Nr, f32x4 (&s)[4], f32x4 (&dp)[4]) {
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    s[u] = P::qk(sk + P::k_sub(u) + kl, qr);
-    dp[u] = P::qk(sv + P::k_sub(u) + kl, gr);
-  }
+__device__ __forceinline__ int bwdq_scores(const uint8_t* sk, const uint8_t* sv, uint32_t kl, const typename P::Q& qr,
+                                           const typename P::Q& gr, int key0, int q0, int L, int R, int dl, int g,
+                                           int Nr, f32x4 (&s)[4], f32x4 (&dp)[4]) {
+  int live = 0;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int rel = key0 + 16 * u - q0;  // key - query offsets span [rel-15, rel+15]
+    if (rel + 15 < -L || rel - 15 > R || key0 + 16 * u >= Nr) {
+      s[u] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      dp[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      continue;
+    }
+    live |= 1 << u;
+    s[u] = P::qk(sk + P::k_sub(u) + kl, qr);
+    dp[u] = P::qk(sv + P::k_sub(u) + kl, gr);
     if (rel - 15 < -L || rel + 15 > R || key0 + 16 * u + 15 >= Nr)
       bwd_mask<1>(s[u], dl + rel, L + R, key0 + 16 * u + 4 * g, Nr);
   }
+  return live;
 }
 
-// Pass 1: online max (m_run, raw scores), sum of e = exp2(s*sl2 - m) and of e*dp.
-__device__ __forceinline__ void bwdq_pass1(const f32x4 (&s)[4], const f32x4 (&dp)[4], float sl2, float& m_run,
-                                           float& l_run, float& a_run) {
+// Pass 1: online max (m_run, raw scores), sum of e = exp2(s*sl2 - m) and of
+// e*dp over the live sub-tiles.
+__device__ __forceinline__ void bwdq_pass1(const f32x4 (&s)[4], const f32x4 (&dp)[4], int live, float sl2,
+                                           float& m_run, float& l_run, float& a_run) {
+  if (!live) return;  // uniform
   float mx = -INFINITY;
 #pragma unroll
   for (int u = 0; u < 4; ++u) mx = fmaxf(mx, fmaxf(fmaxf(s[u][0], s[u][1]), fmaxf(s[u][2], s[u][3])));
@@ -122,13 +132,15 @@ __device__ __forceinline__ void bwdq_pass1(const f32x4 (&s)[4], const f32x4 (&dp
   l_run *= corr;
   a_run *= corr;
 #pragma unroll
-  for (int u = 0; u < 4; ++u)
+  for (int u = 0; u < 4; ++u) {
+    if (!(live >> u & 1)) continue;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const float ex = __builtin_amdgcn_exp2f(fmaf(s[u][r], sl2, -m_use));
       l_run += ex;
       a_run = fmaf(ex, dp[u][r], a_run);
     }
+  }
   m_run = m_new;
 }
 
@@ -141,12 +153,14 @@ __device__ __forceinline__ void bwdq_stats(float m_run, float l_run, float a_run
   dlt = col_sum(a_run) / l_tot;
 }
 
-// Pass 2: dS^T in registers, dQ^T += K^T dS^T (sk's K^T part).
+// Pass 2: dS^T in registers, dQ^T += K^T dS^T (sk's K^T part), pairs of
+// sub-tiles with a live one.
 template <class P>
 __device__ __forceinline__ void bwdq_pass2(const uint8_t* sk, uint32_t vl, const f32x4 (&s)[4], const f32x4 (&dp)[4],
-                                           float sl2, float lse2, float dlt, f32x4 (&acc)[4]) {
+                                           int live, float sl2, float lse2, float dlt, f32x4 (&acc)[4]) {
 #pragma unroll
   for (int u = 0; u < 4; u += 2) {
+    if (!(live >> u & 3)) continue;  // uniform
     float d0[4], d1[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -165,20 +179,28 @@ __device__ __forceinline__ void bwdkv_block(const uint8_t* sq, const uint8_t* sg
                                             uint32_t vl, const typename P::Q& kr, const typename P::Q& vr, int qbase,
                                             int k0, int L, int R, int dl, int g, int Nr, float sl2,
                                             f32x4 (&acc_k)[4], f32x4 (&acc_v)[4]) {
+  // sub-tiles whose 16 queries have no band overlap with the wave's 16 keys
+  // (or lie past the end) are not computed; pairs with no live sub-tile are
+  // skipped (wave-uniform tests)
   f32x4 s[4], dp[4];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    s[u] = P::qk(sq + P::k_sub(u) + kl, kr);   // S[query 16u+4g+r][key c]
-    dp[u] = P::qk(sg + P::k_sub(u) + kl, vr);  // dP[query][key c]
-  }
+  int live = 0;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int rel = k0 - (qbase + 16 * u);  // key - query offsets span [rel-15, rel+15]
+    if (rel + 15 < -L || rel - 15 > R || qbase + 16 * u >= Nr) {
+      s[u] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      dp[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      continue;
+    }
+    live |= 1 << u;
+    s[u] = P::qk(sq + P::k_sub(u) + kl, kr);   // S[query 16u+4g+r][key c]
+    dp[u] = P::qk(sg + P::k_sub(u) + kl, vr);  // dP[query][key c]
     if (rel - 15 < -L || rel + 15 > R || qbase + 16 * u + 15 >= Nr)
       bwd_mask<-1>(s[u], dl + rel, L + R, qbase + 16 * u + 4 * g, Nr);
   }
 #pragma unroll
   for (int u = 0; u < 4; u += 2) {
+    if (!(live >> u & 3)) continue;
     const f32x4 lse0 = *reinterpret_cast<const f32x4*>(st + 16 * u + 4 * g);
     const f32x4 dl0 = *reinterpret_cast<const f32x4*>(st + 64 + 16 * u + 4 * g);
     const f32x4 lse1 = *reinterpret_cast<const f32x4*>(st + 16 * (u + 1) + 4 * g);
@@ -282,12 +304,12 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
     P::load_rows(xv, Vr, off_of(e + 1), tid, tb);
     const uint8_t* sk = ring + buf_of(e) * kBuf;
     f32x4 s[4], dp[4];
-    bwdq_scores<P>(sk, sk + P::kSlot, kl, qr, gr, 64 * blk_of(e), q0, L, R, dl, g, w.Nr, s, dp);
+    const int live = bwdq_scores<P>(sk, sk + P::kSlot, kl, qr, gr, 64 * blk_of(e), q0, L, R, dl, g, w.Nr, s, dp);
     if (e < nb) {  // pass 1
-      bwdq_pass1(s, dp, sl2, m_run, l_run, a_run);
+      bwdq_pass1(s, dp, live, sl2, m_run, l_run, a_run);
       if (e == nb - 1) bwdq_stats(m_run, l_run, a_run, sl2, lse2, dlt);
     } else {  // pass 2
-      bwdq_pass2<P>(sk, vl, s, dp, sl2, lse2, dlt, acc);
+      bwdq_pass2<P>(sk, vl, s, dp, live, sl2, lse2, dlt, acc);
     }
     // the next item goes into the buffer item e-1 used (every wave passed the
     // barrier that ended item e-1); resident bands load nothing after pass 1
@@ -599,15 +621,16 @@ __global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
       const uint8_t* sk0 = ring + (lo & 1) * kBuf;
       const uint8_t* sk1 = ring + (hi & 1) * kBuf;
       f32x4 s0[4], dp0[4], s1[4], dp1[4];
-      bwdq_scores<P>(sk0, sk0 + P::kSlot, kl, qr, gr, 64 * lo, q0, L, R, dl, g, w.Nr, s0, dp0);
-      bwdq_pass1(s0, dp0, sl2, m_run, l_run, a_run);
+      const int live0 = bwdq_scores<P>(sk0, sk0 + P::kSlot, kl, qr, gr, 64 * lo, q0, L, R, dl, g, w.Nr, s0, dp0);
+      bwdq_pass1(s0, dp0, live0, sl2, m_run, l_run, a_run);
+      int live1 = 0;
       if (hi > lo) {
-        bwdq_scores<P>(sk1, sk1 + P::kSlot, kl, qr, gr, 64 * hi, q0, L, R, dl, g, w.Nr, s1, dp1);
-        bwdq_pass1(s1, dp1, sl2, m_run, l_run, a_run);
+        live1 = bwdq_scores<P>(sk1, sk1 + P::kSlot, kl, qr, gr, 64 * hi, q0, L, R, dl, g, w.Nr, s1, dp1);
+        bwdq_pass1(s1, dp1, live1, sl2, m_run, l_run, a_run);
       }
       bwdq_stats(m_run, l_run, a_run, sl2, lse2, dlt);
-      bwdq_pass2<P>(sk0, vl, s0, dp0, sl2, lse2, dlt, acc);
-      if (hi > lo) bwdq_pass2<P>(sk1, vl, s1, dp1, sl2, lse2, dlt, acc);
+      bwdq_pass2<P>(sk0, vl, s0, dp0, live0, sl2, lse2, dlt, acc);
+      if (hi > lo) bwdq_pass2<P>(sk1, vl, s1, dp1, live1, sl2, lse2, dlt, acc);
     }
     P::store_o(acc, a.scale, DQr, (uint32_t)(64 * t) * tb + lrow, g);
     const int64_t srow = (((int64_t)w.b * a.N + w.rho + (int64_t)a.dil * (q0 + c)) * a.H + w.h);
