@@ -1,6 +1,7 @@
 // backward_kernel.h -- MFMA backward of banded attention (SLIDING with any
 // dilation, DENSE and causal as the band [i-(N-1), i+R]), head_dim 64,
-// bf16/fp16.
+// bf16/fp16 (16x16x32 MFMA) and fp32 (16x16x4 MFMA; 64-row blocks of two
+// 32-row fp32 slots).
 //
 // With s_ij = q_i.k_j (raw), p_ij = exp2(s_ij*scale*log2e - lse2_i),
 // dp_ij = dout_i.v_j and ds_ij = p_ij (dp_ij - delta_i):
@@ -49,6 +50,41 @@ struct BwdArgs {
   float scale, scale_log2;
   int32_t chunk, chunks;     // stream kernels: tiles per workgroup, workgroups per residue class
 };
+
+// One 64-row block of an operand: P::kSPB slots of P::kRows rows (one for
+// the 16-bit path, two for fp32), loaded into registers and written to
+// consecutive slots of a block buffer.  Blocks whose offset is out of range
+// (kOob) read nothing.
+template <class P>
+struct BlkSlots {
+  typename P::Slot s[P::kSPB];
+};
+template <class P>
+struct BlkRows {  // rows only (an operand never read transposed)
+  typename P::Rows s[P::kSPB];
+};
+template <class P>
+__device__ __forceinline__ void load_blk(BlkSlots<P>& b, __amdgpu_buffer_rsrc_t A, __amdgpu_buffer_rsrc_t B,
+                                         uint32_t off, int tid, uint32_t tb) {
+#pragma unroll
+  for (int i = 0; i < P::kSPB; ++i) P::load_slot(b.s[i], A, B, off + (uint32_t)(i * P::kRows) * tb, tid, tb);
+}
+template <class P>
+__device__ __forceinline__ void store_blk(const BlkSlots<P>& b, uint8_t* buf, int tid) {
+#pragma unroll
+  for (int i = 0; i < P::kSPB; ++i) P::store_slot(b.s[i], buf + i * P::kSlot, tid);
+}
+template <class P>
+__device__ __forceinline__ void load_rblk(BlkRows<P>& b, __amdgpu_buffer_rsrc_t A, uint32_t off, int tid,
+                                          uint32_t tb) {
+#pragma unroll
+  for (int i = 0; i < P::kSPB; ++i) P::load_rows(b.s[i], A, off + (uint32_t)(i * P::kRows) * tb, tid, tb);
+}
+template <class P>
+__device__ __forceinline__ void store_rblk(const BlkRows<P>& b, uint8_t* buf, int tid) {
+#pragma unroll
+  for (int i = 0; i < P::kSPB; ++i) P::store_rows(b.s[i], buf + i * P::kSlot, tid);
+}
 
 // Workgroup -> (b, h, rho, tile) and the residue class's resources.
 struct BwdTile {
@@ -110,8 +146,8 @@ __device__ __forceinline__ int bwdq_scores(const uint8_t* sk, const uint8_t* sv,
       continue;
     }
     live |= 1 << u;
-    s[u] = P::qk(sk + P::k_sub(u) + kl, qr);
-    dp[u] = P::qk(sv + P::k_sub(u) + kl, gr);
+    s[u] = P::qk(sk + P::blk_k(u) + kl, qr);
+    dp[u] = P::qk(sv + P::blk_k(u) + kl, gr);
     if (rel - 15 < -L || rel + 15 > R || key0 + 16 * u + 15 >= Nr)
       bwd_mask<1>(s[u], dl + rel, L + R, key0 + 16 * u + 4 * g, Nr);
   }
@@ -167,7 +203,7 @@ __device__ __forceinline__ void bwdq_pass2(const uint8_t* sk, uint32_t vl, const
       d0[r] = __builtin_amdgcn_exp2f(fmaf(s[u][r], sl2, -lse2)) * (dp[u][r] - dlt);
       d1[r] = __builtin_amdgcn_exp2f(fmaf(s[u + 1][r], sl2, -lse2)) * (dp[u + 1][r] - dlt);
     }
-    P::pv2(sk + P::v_sub(u) + vl, sk + P::v_sub(u + 1) + vl, d0, d1, acc);
+    P::pv2(sk + P::blk_v(u) + vl, sk + P::blk_v(u + 1) + vl, d0, d1, acc);
   }
 }
 
@@ -193,8 +229,8 @@ __device__ __forceinline__ void bwdkv_block(const uint8_t* sq, const uint8_t* sg
       continue;
     }
     live |= 1 << u;
-    s[u] = P::qk(sq + P::k_sub(u) + kl, kr);   // S[query 16u+4g+r][key c]
-    dp[u] = P::qk(sg + P::k_sub(u) + kl, vr);  // dP[query][key c]
+    s[u] = P::qk(sq + P::blk_k(u) + kl, kr);   // S[query 16u+4g+r][key c]
+    dp[u] = P::qk(sg + P::blk_k(u) + kl, vr);  // dP[query][key c]
     if (rel - 15 < -L || rel + 15 > R || qbase + 16 * u + 15 >= Nr)
       bwd_mask<-1>(s[u], dl + rel, L + R, qbase + 16 * u + 4 * g, Nr);
   }
@@ -213,8 +249,8 @@ __device__ __forceinline__ void bwdkv_block(const uint8_t* sq, const uint8_t* sg
       d0[r] = p0[r] * (dp[u][r] - dl0[r]);
       d1[r] = p1[r] * (dp[u + 1][r] - dl1[r]);
     }
-    P::pv2(sg + P::v_sub(u) + vl, sg + P::v_sub(u + 1) + vl, p0, p1, acc_v);  // dV^T += dO^T P
-    P::pv2(sq + P::v_sub(u) + vl, sq + P::v_sub(u + 1) + vl, d0, d1, acc_k);  // dK^T += Q^T dS
+    P::pv2(sg + P::blk_v(u) + vl, sg + P::blk_v(u + 1) + vl, p0, p1, acc_v);  // dV^T += dO^T P
+    P::pv2(sq + P::blk_v(u) + vl, sq + P::blk_v(u + 1) + vl, d0, d1, acc_k);  // dK^T += Q^T dS
   }
 }
 
@@ -247,7 +283,7 @@ template <class P>
 __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 buffers x (K slot, V slot)
   using Elt = typename P::Elt;
-  constexpr int kBuf = 2 * P::kSlot;
+  constexpr int kBuf = 2 * P::kBlk;
   BwdTile w;
   if (!bwd_tile<P>(a, w)) return;  // uniform, before any barrier
   const int tid = threadIdx.x;
@@ -284,12 +320,12 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
   auto off_of = [&](int e) { return e < (resident ? nb : items) ? (uint32_t)(64 * blk_of(e)) * tb : kOob; };
 
   // V is read only as rows (dP^T = V dO^T): its transposed part stays unwritten
-  typename P::Slot xk;
-  typename P::Rows xv;
-  P::load_slot(xk, Kr, Kr, off_of(0), tid, tb);
-  P::load_rows(xv, Vr, off_of(0), tid, tb);
-  P::store_slot(xk, ring, tid);
-  P::store_rows(xv, ring + P::kSlot, tid);
+  BlkSlots<P> xk;
+  BlkRows<P> xv;
+  load_blk<P>(xk, Kr, Kr, off_of(0), tid, tb);
+  load_rblk<P>(xv, Vr, off_of(0), tid, tb);
+  store_blk<P>(xk, ring, tid);
+  store_rblk<P>(xv, ring + P::kBlk, tid);
   __syncthreads();
 
   const float sl2 = a.scale_log2;
@@ -300,11 +336,11 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
   for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   for (int e = 0; e < items; ++e) {
-    P::load_slot(xk, Kr, Kr, off_of(e + 1), tid, tb);
-    P::load_rows(xv, Vr, off_of(e + 1), tid, tb);
+    load_blk<P>(xk, Kr, Kr, off_of(e + 1), tid, tb);
+    load_rblk<P>(xv, Vr, off_of(e + 1), tid, tb);
     const uint8_t* sk = ring + buf_of(e) * kBuf;
     f32x4 s[4], dp[4];
-    const int live = bwdq_scores<P>(sk, sk + P::kSlot, kl, qr, gr, 64 * blk_of(e), q0, L, R, dl, g, w.Nr, s, dp);
+    const int live = bwdq_scores<P>(sk, sk + P::kBlk, kl, qr, gr, 64 * blk_of(e), q0, L, R, dl, g, w.Nr, s, dp);
     if (e < nb) {  // pass 1
       bwdq_pass1(s, dp, live, sl2, m_run, l_run, a_run);
       if (e == nb - 1) bwdq_stats(m_run, l_run, a_run, sl2, lse2, dlt);
@@ -314,8 +350,8 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
     // the next item goes into the buffer item e-1 used (every wave passed the
     // barrier that ended item e-1); resident bands load nothing after pass 1
     if (!resident || e + 1 < nb) {
-      P::store_slot(xk, ring + buf_of(e + 1) * kBuf, tid);
-      P::store_rows(xv, ring + buf_of(e + 1) * kBuf + P::kSlot, tid);
+      store_blk<P>(xk, ring + buf_of(e + 1) * kBuf, tid);
+      store_rblk<P>(xv, ring + buf_of(e + 1) * kBuf + P::kBlk, tid);
     }
     __syncthreads();
   }
@@ -330,7 +366,7 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdArgs a) {
   // 2 buffers x (Q slot, dO slot, 64 lse2, 64 delta)
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
   using Elt = typename P::Elt;
-  constexpr int kBuf = 2 * P::kSlot + 512;
+  constexpr int kBuf = 2 * P::kBlk + 512;
   BwdTile w;
   if (!bwd_tile<P>(a, w)) return;
   const int tid = threadIdx.x;
@@ -364,13 +400,13 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdArgs a) {
   // thread tid < 64 carries the statistics of query row tid of the block
   auto stat_off = [&](int e) { return e < nb && tid < 64 ? (uint32_t)(64 * (qb_lo + e) + tid) * S.stride : kOob; };
 
-  typename P::Slot xq, xg;
-  P::load_slot(xq, Qr, Qr, off_of(0), tid, tb);
-  P::load_slot(xg, Gr, Gr, off_of(0), tid, tb);
+  BlkSlots<P> xq, xg;
+  load_blk<P>(xq, Qr, Qr, off_of(0), tid, tb);
+  load_blk<P>(xg, Gr, Gr, off_of(0), tid, tb);
   uint2 xs = bload8(S.r, stat_off(0));
-  P::store_slot(xq, ring, tid);
-  P::store_slot(xg, ring + P::kSlot, tid);
-  bwd_stage_stats(ring + 2 * P::kSlot, xs, tid);
+  store_blk<P>(xq, ring, tid);
+  store_blk<P>(xg, ring + P::kBlk, tid);
+  bwd_stage_stats(ring + 2 * P::kBlk, xs, tid);
   __syncthreads();
 
   const int dl = c - 4 * g + L;  // key - query + L of element 0, minus the sub-tile base
@@ -379,16 +415,16 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdArgs a) {
   for (int dt = 0; dt < 4; ++dt) acc_k[dt] = acc_v[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   for (int e = 0; e < nb; ++e) {
-    P::load_slot(xq, Qr, Qr, off_of(e + 1), tid, tb);
-    P::load_slot(xg, Gr, Gr, off_of(e + 1), tid, tb);
+    load_blk<P>(xq, Qr, Qr, off_of(e + 1), tid, tb);
+    load_blk<P>(xg, Gr, Gr, off_of(e + 1), tid, tb);
     xs = bload8(S.r, stat_off(e + 1));
     const uint8_t* sq = ring + (e & 1) * kBuf;
-    bwdkv_block<P>(sq, sq + P::kSlot, reinterpret_cast<const float*>(sq + 2 * P::kSlot), kl, vl, kr, vr,
+    bwdkv_block<P>(sq, sq + P::kBlk, reinterpret_cast<const float*>(sq + 2 * P::kBlk), kl, vl, kr, vr,
                    64 * (qb_lo + e), k0, L, R, dl, g, w.Nr, a.scale_log2, acc_k, acc_v);
     uint8_t* nx = ring + ((e + 1) & 1) * kBuf;
-    P::store_slot(xq, nx, tid);
-    P::store_slot(xg, nx + P::kSlot, tid);
-    bwd_stage_stats(nx + 2 * P::kSlot, xs, tid);
+    store_blk<P>(xq, nx, tid);
+    store_blk<P>(xg, nx + P::kBlk, tid);
+    bwd_stage_stats(nx + 2 * P::kBlk, xs, tid);
     __syncthreads();
   }
   P::store_o(acc_v, 1.0f, DVr, krow, g);
@@ -413,7 +449,7 @@ __device__ __forceinline__ void bwdq_window_tile(const uint8_t* ring, uint32_t k
                                                  const typename P::Q& gr, int t, int wv, int dl, float sl2,
                                                  float& lse2, float& dlt, f32x4 (&acc)[4]) {
   using G = WinGeom<L, R, 64>;
-  constexpr int kBuf = 2 * P::kSlot;
+  constexpr int kBuf = 2 * P::kBlk;
   f32x4 e[G::NSUB], dp[G::NSUB];
   uint32_t kt[G::NSUB];  // K^T of sub-tile j (the K buffer's transposed part)
   float mx = -INFINITY;
@@ -422,9 +458,9 @@ __device__ __forceinline__ void bwdq_window_tile(const uint8_t* ring, uint32_t k
     const int s = 4 * t + wv - G::CL + j;
     const uint32_t bb = (uint32_t)(((s >> 2) & 1) * kBuf);
     const int u = s & 3;
-    kt[j] = bb + P::v_sub(u) + vl;
-    f32x4 z = P::qk(ring + bb + P::k_sub(u) + kl, qr);
-    dp[j] = P::qk(ring + bb + P::kSlot + P::k_sub(u) + kl, gr);
+    kt[j] = bb + P::blk_v(u) + vl;
+    f32x4 z = P::qk(ring + bb + P::blk_k(u) + kl, qr);
+    dp[j] = P::qk(ring + bb + P::kBlk + P::blk_k(u) + kl, gr);
     const int rel = 16 * (j - G::CL);     // key - query offsets span [rel-15, rel+15]
     if (rel - 15 < -L || rel + 15 > R) {  // resolved at compile time
 #pragma unroll
@@ -472,23 +508,23 @@ __device__ __forceinline__ void bwdkv_window_tile(const uint8_t* ring, uint32_t 
                                                   const typename P::Q& vr, int t, int wv, int g, int dl, float sl2,
                                                   f32x4 (&acc_k)[4], f32x4 (&acc_v)[4]) {
   using G = WinGeom<R, L, 64>;
-  constexpr int kBuf = 2 * P::kSlot + 512;
+  constexpr int kBuf = 2 * P::kBlk + 512;
   float p[G::NSUB][4], d[G::NSUB][4];
-  uint32_t qt[G::NSUB];  // Q^T of sub-tile j (dO^T at + kSlot)
+  uint32_t qt[G::NSUB];  // Q^T of sub-tile j (dO^T at + kBlk)
 #pragma unroll
   for (int j = 0; j < G::NSUB; ++j) {
     const int s = 4 * t + wv - G::CL + j;
     const uint32_t bb = (uint32_t)(((s >> 2) & 1) * kBuf);
     const int u = s & 3;
-    qt[j] = bb + P::v_sub(u) + vl;
-    f32x4 z = P::qk(ring + bb + P::k_sub(u) + kl, kr);                  // S[query 4g+r][key c]
-    const f32x4 dz = P::qk(ring + bb + P::kSlot + P::k_sub(u) + kl, vr);  // dP[query][key c]
+    qt[j] = bb + P::blk_v(u) + vl;
+    f32x4 z = P::qk(ring + bb + P::blk_k(u) + kl, kr);                  // S[query 4g+r][key c]
+    const f32x4 dz = P::qk(ring + bb + P::kBlk + P::blk_k(u) + kl, vr);  // dP[query][key c]
     const int rel = 16 * (G::CL - j);     // key - query offsets span [rel-15, rel+15]
     if (rel - 15 < -L || rel + 15 > R) {  // resolved at compile time
 #pragma unroll
       for (int r = 0; r < 4; ++r) z[r] = (uint32_t)(dl + rel - r) <= (uint32_t)(L + R) ? z[r] : -INFINITY;
     }
-    const float* st = reinterpret_cast<const float*>(ring + bb + 2 * P::kSlot);
+    const float* st = reinterpret_cast<const float*>(ring + bb + 2 * P::kBlk);
     const f32x4 lse = *reinterpret_cast<const f32x4*>(st + 16 * u + 4 * g);
     const f32x4 del = *reinterpret_cast<const f32x4*>(st + 64 + 16 * u + 4 * g);
 #pragma unroll
@@ -500,10 +536,10 @@ __device__ __forceinline__ void bwdkv_window_tile(const uint8_t* ring, uint32_t 
 #pragma unroll
   for (int j = 0; j < G::NSUB; j += 2) {
     if (j + 1 < G::NSUB) {  // resolved at compile time
-      P::pv2(ring + qt[j] + P::kSlot, ring + qt[j + 1] + P::kSlot, p[j], p[j + 1], acc_v);  // dV^T += dO^T P
+      P::pv2(ring + qt[j] + P::kBlk, ring + qt[j + 1] + P::kBlk, p[j], p[j + 1], acc_v);  // dV^T += dO^T P
       P::pv2(ring + qt[j], ring + qt[j + 1], d[j], d[j + 1], acc_k);                      // dK^T += Q^T dS
     } else {
-      P::pv(ring + qt[j] + P::kSlot, p[j], acc_v);
+      P::pv(ring + qt[j] + P::kBlk, p[j], acc_v);
       P::pv(ring + qt[j], d[j], acc_k);
     }
   }
@@ -551,7 +587,7 @@ template <class P, int FL, int FR>
 __global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 slots x (K slot, V slot)
   using Elt = typename P::Elt;
-  constexpr int kBuf = 2 * P::kSlot;
+  constexpr int kBuf = 2 * P::kBlk;
   BwdChunk w;
   if (!bwd_chunk<P>(a, w)) return;  // uniform, before any barrier
   const int tid = threadIdx.x;
@@ -577,13 +613,13 @@ __global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
   typename P::Q qr, gr, qn, gn;
   P::load_q(qr, Qr, (uint32_t)(64 * w.t0) * tb + lrow, g);
   P::load_q(gr, Gr, (uint32_t)(64 * w.t0) * tb + lrow, g);
-  typename P::Slot xk;
-  typename P::Rows xv;  // V is read only as rows
+  BlkSlots<P> xk;
+  BlkRows<P> xv;  // V is read only as rows
   for (int j = lo_of(w.t0); j <= hi_of(w.t0); ++j) {
-    P::load_slot(xk, Kr, Kr, (uint32_t)(64 * j) * tb, tid, tb);
-    P::load_rows(xv, Vr, (uint32_t)(64 * j) * tb, tid, tb);
-    P::store_slot(xk, ring + (j & 1) * kBuf, tid);
-    P::store_rows(xv, ring + (j & 1) * kBuf + P::kSlot, tid);
+    load_blk<P>(xk, Kr, Kr, (uint32_t)(64 * j) * tb, tid, tb);
+    load_rblk<P>(xv, Vr, (uint32_t)(64 * j) * tb, tid, tb);
+    store_blk<P>(xk, ring + (j & 1) * kBuf, tid);
+    store_rblk<P>(xv, ring + (j & 1) * kBuf + P::kBlk, tid);
   }
   __syncthreads();
 
@@ -594,8 +630,8 @@ __global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
     const bool more = t + 1 < w.t1;
     const int nblk_new = more && hi_of(t + 1) > hi_of(t) ? hi_of(t + 1) : -1;
     const uint32_t noff = nblk_new >= 0 ? (uint32_t)(64 * nblk_new) * tb : kOob;
-    P::load_slot(xk, Kr, Kr, noff, tid, tb);
-    P::load_rows(xv, Vr, noff, tid, tb);
+    load_blk<P>(xk, Kr, Kr, noff, tid, tb);
+    load_rblk<P>(xv, Vr, noff, tid, tb);
     const uint32_t nrow = more ? (uint32_t)(64 * (t + 1)) * tb + lrow : kOob;
     P::load_q(qn, Qr, nrow, g);
     P::load_q(gn, Gr, nrow, g);
@@ -621,11 +657,11 @@ __global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
       const uint8_t* sk0 = ring + (lo & 1) * kBuf;
       const uint8_t* sk1 = ring + (hi & 1) * kBuf;
       f32x4 s0[4], dp0[4], s1[4], dp1[4];
-      const int live0 = bwdq_scores<P>(sk0, sk0 + P::kSlot, kl, qr, gr, 64 * lo, q0, L, R, dl, g, w.Nr, s0, dp0);
+      const int live0 = bwdq_scores<P>(sk0, sk0 + P::kBlk, kl, qr, gr, 64 * lo, q0, L, R, dl, g, w.Nr, s0, dp0);
       bwdq_pass1(s0, dp0, live0, sl2, m_run, l_run, a_run);
       int live1 = 0;
       if (hi > lo) {
-        live1 = bwdq_scores<P>(sk1, sk1 + P::kSlot, kl, qr, gr, 64 * hi, q0, L, R, dl, g, w.Nr, s1, dp1);
+        live1 = bwdq_scores<P>(sk1, sk1 + P::kBlk, kl, qr, gr, 64 * hi, q0, L, R, dl, g, w.Nr, s1, dp1);
         bwdq_pass1(s1, dp1, live1, sl2, m_run, l_run, a_run);
       }
       bwdq_stats(m_run, l_run, a_run, sl2, lse2, dlt);
@@ -639,8 +675,8 @@ __global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
     // the new block replaces block hi(t+1) - 2, which tile t may still read
     __syncthreads();
     if (nblk_new >= 0) {
-      P::store_slot(xk, ring + (nblk_new & 1) * kBuf, tid);
-      P::store_rows(xv, ring + (nblk_new & 1) * kBuf + P::kSlot, tid);
+      store_blk<P>(xk, ring + (nblk_new & 1) * kBuf, tid);
+      store_rblk<P>(xv, ring + (nblk_new & 1) * kBuf + P::kBlk, tid);
     }
     __syncthreads();
     qr = qn;
@@ -652,7 +688,7 @@ template <class P, int FL, int FR>
 __global__ __launch_bounds__(256, 2) void bwd_kv_stream_kernel(BwdArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 slots x (Q slot, dO slot, stats)
   using Elt = typename P::Elt;
-  constexpr int kBuf = 2 * P::kSlot + 512;
+  constexpr int kBuf = 2 * P::kBlk + 512;
   BwdChunk w;
   if (!bwd_chunk<P>(a, w)) return;
   const int tid = threadIdx.x;
@@ -680,16 +716,16 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_stream_kernel(BwdArgs a) {
   typename P::Q kr, vr, kn, vn;
   P::load_q(kr, Kr, (uint32_t)(64 * w.t0) * tb + lrow, g);
   P::load_q(vr, Vr, (uint32_t)(64 * w.t0) * tb + lrow, g);
-  typename P::Slot xq, xg;
+  BlkSlots<P> xq, xg;
   uint2 xs;
   for (int j = lo_of(w.t0); j <= hi_of(w.t0); ++j) {
-    P::load_slot(xq, Qr, Qr, (uint32_t)(64 * j) * tb, tid, tb);
-    P::load_slot(xg, Gr, Gr, (uint32_t)(64 * j) * tb, tid, tb);
+    load_blk<P>(xq, Qr, Qr, (uint32_t)(64 * j) * tb, tid, tb);
+    load_blk<P>(xg, Gr, Gr, (uint32_t)(64 * j) * tb, tid, tb);
     xs = bload8(S.r, stat_off(j));
     uint8_t* sb = ring + (j & 1) * kBuf;
-    P::store_slot(xq, sb, tid);
-    P::store_slot(xg, sb + P::kSlot, tid);
-    bwd_stage_stats(sb + 2 * P::kSlot, xs, tid);
+    store_blk<P>(xq, sb, tid);
+    store_blk<P>(xg, sb + P::kBlk, tid);
+    bwd_stage_stats(sb + 2 * P::kBlk, xs, tid);
   }
   __syncthreads();
 
@@ -698,8 +734,8 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_stream_kernel(BwdArgs a) {
     const bool more = t + 1 < w.t1;
     const int nblk_new = more && hi_of(t + 1) > hi_of(t) ? hi_of(t + 1) : -1;
     const uint32_t noff = nblk_new >= 0 ? (uint32_t)(64 * nblk_new) * tb : kOob;
-    P::load_slot(xq, Qr, Qr, noff, tid, tb);
-    P::load_slot(xg, Gr, Gr, noff, tid, tb);
+    load_blk<P>(xq, Qr, Qr, noff, tid, tb);
+    load_blk<P>(xg, Gr, Gr, noff, tid, tb);
     xs = bload8(S.r, stat_off(nblk_new));
     const uint32_t nrow = more ? (uint32_t)(64 * (t + 1)) * tb + lrow : kOob;
     P::load_q(kn, Kr, nrow, g);
@@ -721,7 +757,7 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_stream_kernel(BwdArgs a) {
     if (!done)
       for (int j = lo_of(t); j <= hi_of(t); ++j) {
         const uint8_t* sq = ring + (j & 1) * kBuf;
-        bwdkv_block<P>(sq, sq + P::kSlot, reinterpret_cast<const float*>(sq + 2 * P::kSlot), kl, vl, kr, vr, 64 * j,
+        bwdkv_block<P>(sq, sq + P::kBlk, reinterpret_cast<const float*>(sq + 2 * P::kBlk), kl, vl, kr, vr, 64 * j,
                        k0, L, R, dl, g, w.Nr, a.scale_log2, acc_k, acc_v);
       }
     const uint32_t orow = (uint32_t)(64 * t) * tb + lrow;
@@ -731,9 +767,9 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_stream_kernel(BwdArgs a) {
     __syncthreads();
     if (nblk_new >= 0) {
       uint8_t* sb = ring + (nblk_new & 1) * kBuf;
-      P::store_slot(xq, sb, tid);
-      P::store_slot(xg, sb + P::kSlot, tid);
-      bwd_stage_stats(sb + 2 * P::kSlot, xs, tid);
+      store_blk<P>(xq, sb, tid);
+      store_blk<P>(xg, sb + P::kBlk, tid);
+      bwd_stage_stats(sb + 2 * P::kBlk, xs, tid);
     }
     __syncthreads();
     kr = kn;

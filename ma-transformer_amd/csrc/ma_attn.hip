@@ -1132,12 +1132,12 @@ bool bwd_band(const ma_attn_desc* d, int64_t* left, int64_t* right, int64_t* dil
 }
 
 bool bwd_mfma_applies(const ma_attn_desc* d, const void* const* ptrs) {
-  if ((d->dtype != MA_ATTN_BF16 && d->dtype != MA_ATTN_F16) || d->head_dim != kHeadDim) return false;
+  if (d->head_dim != kHeadDim) return false;
   for (int i = 0; i < 7; ++i)
     if (!aligned16(ptrs[i])) return false;
   int64_t L, R, dil;
   if (!bwd_band(d, &L, &R, &dil)) return false;
-  const int64_t tb = dil * d->num_heads * kHeadDim * 2;
+  const int64_t tb = dil * d->num_heads * kHeadDim * (d->dtype == MA_ATTN_F32 ? 4 : 2);
   const int64_t nr = (d->seq_len + dil - 1) / dil;
   const int64_t tiles = (nr + 63) / 64;
   // byte offsets of rows (plus the out-of-range base) fit 32 bits; ids fit the grid
@@ -1165,11 +1165,12 @@ int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* 
   a.dil = (int32_t)dil;
   const int64_t nr = (d->seq_len + dil - 1) / dil;
   a.tiles = (int32_t)((nr + 63) / 64);
-  a.tok_bytes = (int32_t)(dil * d->num_heads * kHeadDim * 2);
+  a.tok_bytes = (int32_t)(dil * d->num_heads * kHeadDim * sizeof(typename P::Elt));
   a.scale = scale_of(d);
   a.scale_log2 = a.scale * 1.4426950408889634f;
   const int64_t streams = d->batch * d->num_heads * dil;
-  const size_t shm_q = 4 * (size_t)P::kSlot, shm_kv = 2 * (2 * (size_t)P::kSlot + 512);
+  // two block buffers each: (K, K^T) + V rows for dQ; (Q, Q^T) + (dO, dO^T) + statistics for dK/dV
+  const size_t shm_q = 4 * (size_t)P::kBlk, shm_kv = 2 * (2 * (size_t)P::kBlk + 512);
   // Bands of at most two 64-row blocks in both directions stream a chunk of
   // tiles per workgroup (two workgroups per CU, one wave of workgroups);
   // wider bands take one workgroup per tile.
@@ -1181,8 +1182,10 @@ int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* 
   auto kq = !chunked ? &bwd_q_kernel<P> : fixed ? &bwd_q_stream_kernel<P, 63, 0> : &bwd_q_stream_kernel<P, -1, -1>;
   auto kkv = !chunked ? &bwd_kv_kernel<P> : fixed ? &bwd_kv_stream_kernel<P, 63, 0> : &bwd_kv_stream_kernel<P, -1, -1>;
   const int variant = !chunked ? 0 : fixed ? 2 : 1;
-  // chunks per stream fitted to the 512 resident workgroups (2 per CU)
-  const int64_t per_stream = ma::imax64(1, 512 / streams);
+  // chunks per stream fitted to the resident workgroups (2 per CU for 16-bit,
+  // 1 for fp32, whose block buffers are twice the size)
+  const int64_t per_cu = ma::imax64(1, ma::imin64(2, (int64_t)(160 * 1024) / (int64_t)ma::imax64(shm_q, shm_kv)));
+  const int64_t per_stream = ma::imax64(1, 256 * per_cu / streams);
   a.chunk = (int32_t)ma::imax64(1, (a.tiles + per_stream - 1) / per_stream);
   a.chunks = (int32_t)((a.tiles + a.chunk - 1) / a.chunk);
   const int64_t wgs = chunked ? streams * a.chunks : streams * a.tiles;
@@ -1345,9 +1348,10 @@ int ma_attn_backward(const ma_attn_desc* desc, const void* q, const void* k, con
   const void* ptrs[7] = {q, k, v, dout, dq, dk, dv};
   int rc;
   if (strcmp(kernel_override(), "rows") != 0 && bwd_mfma_applies(desc, ptrs)) {
-    rc = desc->dtype == MA_ATTN_BF16
-             ? launch_backward_mfma<HalfPath<__bf16>>(desc, ptrs, reinterpret_cast<float*>(stats), st)
-             : launch_backward_mfma<HalfPath<_Float16>>(desc, ptrs, reinterpret_cast<float*>(stats), st);
+    float* sf = reinterpret_cast<float*>(stats);
+    rc = desc->dtype == MA_ATTN_BF16  ? launch_backward_mfma<HalfPath<__bf16>>(desc, ptrs, sf, st)
+         : desc->dtype == MA_ATTN_F16 ? launch_backward_mfma<HalfPath<_Float16>>(desc, ptrs, sf, st)
+                                      : launch_backward_mfma<F32Path>(desc, ptrs, sf, st);
     if (rc) return rc;
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail("ma_attn_backward: kernel launch failed: %s", hipGetErrorString(e));

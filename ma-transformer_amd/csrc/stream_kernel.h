@@ -147,6 +147,12 @@ struct HalfPath {
   static __device__ __forceinline__ uint32_t v_lane(int c, int g) { return kSlotK + c * kVRow + 8 * g; }
   static constexpr uint32_t k_sub(int u) { return u * 16 * kKRow; }
   static constexpr uint32_t v_sub(int u) { return u * 32; }
+  // 64-row blocks (the backward's unit) are one slot; sub-tile u (0..3) of a
+  // block: rows at blk_k(u), transposed part at blk_v(u) (from v_lane).
+  static constexpr int kSPB = 1;
+  static constexpr int kBlk = kSlot;
+  static constexpr uint32_t blk_k(int u) { return k_sub(u); }
+  static constexpr uint32_t blk_v(int u) { return v_sub(u); }
 
   // S^T of 16 keys x this wave's 16 queries (raw dot products).
   static __device__ __forceinline__ f32x4 qk(const uint8_t* kp, const Q& q) {
@@ -269,6 +275,28 @@ struct F32Path {
   static __device__ __forceinline__ uint32_t v_lane(int c, int g) { return kSlotK + 4 * g * kVRow + 16 * c; }
   static constexpr uint32_t k_sub(int u) { return u * 16 * kKRow; }
   static constexpr uint32_t v_sub(int u) { return u * 16 * kVRow; }
+  // 64-row blocks (the backward's unit) are two slots; sub-tile u (0..3) of a
+  // block: rows at blk_k(u), permuted rows at blk_v(u) (from v_lane).
+  static constexpr int kSPB = 2;
+  static constexpr int kBlk = 2 * kSlot;
+  static constexpr uint32_t blk_k(int u) { return (u >> 1) * kSlot + k_sub(u & 1); }
+  static constexpr uint32_t blk_v(int u) { return (u >> 1) * kSlot + v_sub(u & 1); }
+
+  // Row part only (an operand read only as rows): the K half of a slot.
+  struct Rows {
+    uint4 r[2];  // row tid>>3, head_dim chunks tid&7 and (tid&7)+8
+  };
+  static __device__ __forceinline__ void load_rows(Rows& s, __amdgpu_buffer_rsrc_t Kr, uint32_t row_off, int tid,
+                                                   uint32_t tb) {
+    const uint32_t row = row_off + (tid >> 3) * tb;
+    s.r[0] = bload16(Kr, row + 16 * (tid & 7));
+    s.r[1] = bload16(Kr, row + 16 * (tid & 7) + 128);
+  }
+  static __device__ __forceinline__ void store_rows(const Rows& s, uint8_t* slot, int tid) {
+    uint8_t* krow = slot + (tid >> 3) * kKRow;
+    *reinterpret_cast<uint4*>(krow + 16 * (tid & 7)) = s.r[0];
+    *reinterpret_cast<uint4*>(krow + 16 * (tid & 7) + 128) = s.r[1];
+  }
 
   static __device__ __forceinline__ f32x4 qk(const uint8_t* kp, const Q& q) {
     f32x4 z = f32x4{0.0f, 0.0f, 0.0f, 0.0f};

@@ -136,9 +136,9 @@ def test_dense_backward_geometry(ext, oracle, shape, causal, dtype):
 
 @pytest.mark.parametrize("N", [1, 64, 65, 300])
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_dense_backward_mfma(ext, oracle, N, causal, dtype):
-    """head_dim 64, 16-bit: the MFMA backward with the band [i-(N-1), i(+N-1)]."""
+    """head_dim 64: the MFMA backward with the band [i-(N-1), i(+N-1)]."""
     shape = (2, N, 3, 64)
     (q, k, v, g), up = _case(shape, 850 + N + causal, dtype)
     got = ext.dense_backward(q, k, v, g, causal)
@@ -146,43 +146,47 @@ def test_dense_backward_mfma(ext, oracle, N, causal, dtype):
 
 
 @pytest.mark.parametrize("N,left,right,dil", [(300, 63, 0, 1), (257, 32, 31, 4), (129, 2, 7, 3)])
-def test_sliding_backward_row_kernels(ext, oracle, monkeypatch, N, left, right, dil):
-    """The VALU row kernels for 16-bit head_dim 64 (the MFMA path's cases),
-    forced with MA_ATTN_KERNEL=rows, stay correct."""
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_sliding_backward_row_kernels(ext, oracle, monkeypatch, N, left, right, dil, dtype):
+    """The VALU row kernels for head_dim 64 (the MFMA path's cases), forced
+    with MA_ATTN_KERNEL=rows, stay correct."""
     monkeypatch.setenv("MA_ATTN_KERNEL", "rows")
     shape = (2, N, 3, 64)
-    (q, k, v, g), up = _case(shape, 860 + N, torch.bfloat16)
+    (q, k, v, g), up = _case(shape, 860 + N, dtype)
     got = ext.sliding_backward(q, k, v, g, left, right, dil)
     spec = oracle.Spec(*shape, pattern="sliding", left=left, right=right, dilation=dil)
-    _check(got, oracle.backward(spec, *up), torch.bfloat16)
+    _check(got, oracle.backward(spec, *up), dtype)
 
 
 @pytest.mark.parametrize("N,H,left,right,dil", [(5000, 16, 63, 0, 1), (4099, 8, 63, 0, 4), (3000, 8, 0, 0, 1),
                                                  (2500, 8, 10, 0, 3), (3333, 8, 0, 64, 1)])
-def test_backward_chunked(ext, oracle, N, H, left, right, dil):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_backward_chunked(ext, oracle, N, H, left, right, dil, dtype):
     """Bands of at most two blocks stream several tiles per workgroup (the
-    last chunk of each residue class ragged): whole gradients vs the oracle."""
+    last chunk of each residue class ragged): whole gradients vs the oracle.
+    fp32 runs the same kernels on 16x16x4 MFMA with two-slot blocks."""
     shape = (2, N, H, 64)
-    (q, k, v, g), up = _case(shape, 880 + N + dil, torch.bfloat16)
+    (q, k, v, g), up = _case(shape, 880 + N + dil, dtype)
     got = ext.sliding_backward(q, k, v, g, left, right, dil)
     spec = oracle.Spec(*shape, pattern="sliding", left=left, right=right, dilation=dil)
-    _check(got, oracle.backward(spec, *up), torch.bfloat16)
+    _check(got, oracle.backward(spec, *up), dtype)
 
 
 @pytest.mark.parametrize("N,H,dil", [(5000, 16, 1), (4099, 8, 4)])
-def test_backward_chunked_generic(ext, oracle, monkeypatch, N, H, dil):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_backward_chunked_generic(ext, oracle, monkeypatch, N, H, dil, dtype):
     """The causal-64 band on the generic stream tiles (fixed-window tiles
     switched off with MA_ATTN_BWD_NO_FIXED) stays correct."""
     monkeypatch.setenv("MA_ATTN_BWD_NO_FIXED", "1")
     shape = (2, N, H, 64)
-    (q, k, v, g), up = _case(shape, 890 + N + dil, torch.bfloat16)
+    (q, k, v, g), up = _case(shape, 890 + N + dil, dtype)
     got = ext.sliding_backward(q, k, v, g, 63, 0, dil)
     spec = oracle.Spec(*shape, pattern="sliding", left=63, right=0, dilation=dil)
-    _check(got, oracle.backward(spec, *up), torch.bfloat16)
+    _check(got, oracle.backward(spec, *up), dtype)
 
 
 @pytest.mark.parametrize("N", [64, 127, 128, 129, 191, 192, 255, 256, 257, 1000])
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_backward_fixed_window_edges(ext, oracle, N, dtype):
     """Causal 64 (fixed-window tiles inside, generic tiles at the sequence
     ends): lengths around the interior-tile bounds (the dQ kernel's tile t
