@@ -75,6 +75,9 @@ WORKLOADS = {
     # not a BASELINE config: the dense_forward(use_causal_mask=True) path at a long sequence
     "dense_causal_bf16": (1, 8, 16384, 64, "bf16", dict(pattern="dense", causal=True),
                           "dense causal (keys [0,i]), bf16, B=1 H=8 N=16384 D=64"),
+    # the reference's dense_forward dtype (fp32 only there)
+    "dense_causal_fp32": (1, 8, 16384, 64, "fp32", dict(pattern="dense", causal=True),
+                          "dense causal (keys [0,i]), fp32, B=1 H=8 N=16384 D=64"),
 }
 
 

@@ -51,41 +51,6 @@ struct BwdArgs {
   int32_t chunk, chunks;     // stream kernels: tiles per workgroup, workgroups per residue class
 };
 
-// One 64-row block of an operand: P::kSPB slots of P::kRows rows (one for
-// the 16-bit path, two for fp32), loaded into registers and written to
-// consecutive slots of a block buffer.  Blocks whose offset is out of range
-// (kOob) read nothing.
-template <class P>
-struct BlkSlots {
-  typename P::Slot s[P::kSPB];
-};
-template <class P>
-struct BlkRows {  // rows only (an operand never read transposed)
-  typename P::Rows s[P::kSPB];
-};
-template <class P>
-__device__ __forceinline__ void load_blk(BlkSlots<P>& b, __amdgpu_buffer_rsrc_t A, __amdgpu_buffer_rsrc_t B,
-                                         uint32_t off, int tid, uint32_t tb) {
-#pragma unroll
-  for (int i = 0; i < P::kSPB; ++i) P::load_slot(b.s[i], A, B, off + (uint32_t)(i * P::kRows) * tb, tid, tb);
-}
-template <class P>
-__device__ __forceinline__ void store_blk(const BlkSlots<P>& b, uint8_t* buf, int tid) {
-#pragma unroll
-  for (int i = 0; i < P::kSPB; ++i) P::store_slot(b.s[i], buf + i * P::kSlot, tid);
-}
-template <class P>
-__device__ __forceinline__ void load_rblk(BlkRows<P>& b, __amdgpu_buffer_rsrc_t A, uint32_t off, int tid,
-                                          uint32_t tb) {
-#pragma unroll
-  for (int i = 0; i < P::kSPB; ++i) P::load_rows(b.s[i], A, off + (uint32_t)(i * P::kRows) * tb, tid, tb);
-}
-template <class P>
-__device__ __forceinline__ void store_rblk(const BlkRows<P>& b, uint8_t* buf, int tid) {
-#pragma unroll
-  for (int i = 0; i < P::kSPB; ++i) P::store_rows(b.s[i], buf + i * P::kSlot, tid);
-}
-
 // Workgroup -> (b, h, rho, tile) and the residue class's resources.
 struct BwdTile {
   int b, h, rho, t, Nr, nblk;

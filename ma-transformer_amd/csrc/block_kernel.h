@@ -1,5 +1,6 @@
 // block_kernel.h -- block-sparse attention forward (block size 64, head_dim
-// 64, bf16/fp16) on MFMA.
+// 64, bf16/fp16 on 16x16x32 MFMA, fp32 on 16x16x4 MFMA with 64-row blocks of
+// two 32-row fp32 slots).
 //
 // Query block r attends the key blocks listed in row r of the block table
 // (ascending, -1 padded), each a dense 64x64 block product on MFMA.  One
@@ -54,7 +55,7 @@ __device__ __forceinline__ void block_update(const uint8_t* slot, uint32_t kl, u
   f32x4 sc[4];
   float mx = -INFINITY;
 #pragma unroll
-  for (int u = 0; u < 4; ++u) sc[u] = P::qk(slot + P::k_sub(u) + kl, q);
+  for (int u = 0; u < 4; ++u) sc[u] = P::qk(slot + P::blk_k(u) + kl, q);
   // One uniform branch after all four products, so they issue back to back.
   if (cb < 0 || diag || key0 + 63 >= N) {  // absent entry, causal diagonal, or keys past the end
     // key 16u + 4g + rr of the block is kept up to hi; the lane term stays
@@ -89,14 +90,13 @@ __device__ __forceinline__ void block_update(const uint8_t* slot, uint32_t kl, u
       p1[rr] = __builtin_amdgcn_exp2f(fmaf(sc[u + 1][rr], sl2, -m_use));
       l_run += p0[rr] + p1[rr];
     }
-    P::pv2(slot + P::v_sub(u) + vl, slot + P::v_sub(u + 1) + vl, p0, p1, acc);
+    P::pv2(slot + P::blk_v(u) + vl, slot + P::blk_v(u + 1) + vl, p0, p1, acc);
   }
 }
 
 template <class P>
 __global__ __launch_bounds__(256, P::kMinBlocks) void block_row_kernel(BlockArgs a) {
-  static_assert(P::kRows == 64, "block kernel walks 64-key slots");
-  __shared__ __attribute__((aligned(16))) uint8_t ring[2 * P::kSlot];
+  extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 block buffers of P::kBlk bytes
   using Elt = typename P::Elt;
 
   const int tid = threadIdx.x;
@@ -145,44 +145,47 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void block_row_kernel(BlockArgs
   const float sl2 = a.scale_log2;
   const int ql = 16 * wv + c;
 
-  if (!dense && a.bpr <= 4) {
-    // Short rows (the BASELINE table has 4 entries): every block's loads are
-    // issued at once, so the row pays one HBM latency instead of one per
-    // block; the two-slot ring is filled twice.
-    typename P::Slot x[4];
+  // 16-bit blocks only: four blocks of registers in flight fit there
+  if constexpr (P::kSPB == 1) {
+    if (!dense && a.bpr <= 4) {
+      // Short rows (the BASELINE table has 4 entries): every block's loads are
+      // issued at once, so the row pays one HBM latency instead of one per
+      // block; the two-slot ring is filled twice.
+      typename P::Slot x[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) P::load_slot(x[e], Kr, Vr, blk_off(e), tid, tb);
-    P::store_slot(x[0], ring, tid);
-    P::store_slot(x[1], ring + P::kSlot, tid);
-    __syncthreads();
-    if (ne > 0) block_update<P>(ring, kl, vl, q, block_of(0), false, ql, N, g, sl2, m_run, l_run, acc);
-    if (ne > 1) block_update<P>(ring + P::kSlot, kl, vl, q, block_of(1), false, ql, N, g, sl2, m_run, l_run, acc);
-    if (ne > 2) {  // uniform
+      for (int e = 0; e < 4; ++e) P::load_slot(x[e], Kr, Vr, blk_off(e), tid, tb);
+      P::store_slot(x[0], ring, tid);
+      P::store_slot(x[1], ring + P::kSlot, tid);
       __syncthreads();
-      P::store_slot(x[2], ring, tid);
-      P::store_slot(x[3], ring + P::kSlot, tid);
-      __syncthreads();
-      block_update<P>(ring, kl, vl, q, block_of(2), false, ql, N, g, sl2, m_run, l_run, acc);
-      if (ne > 3) block_update<P>(ring + P::kSlot, kl, vl, q, block_of(3), false, ql, N, g, sl2, m_run, l_run, acc);
+      if (ne > 0) block_update<P>(ring, kl, vl, q, block_of(0), false, ql, N, g, sl2, m_run, l_run, acc);
+      if (ne > 1) block_update<P>(ring + P::kSlot, kl, vl, q, block_of(1), false, ql, N, g, sl2, m_run, l_run, acc);
+      if (ne > 2) {  // uniform
+        __syncthreads();
+        P::store_slot(x[2], ring, tid);
+        P::store_slot(x[3], ring + P::kSlot, tid);
+        __syncthreads();
+        block_update<P>(ring, kl, vl, q, block_of(2), false, ql, N, g, sl2, m_run, l_run, acc);
+        if (ne > 3) block_update<P>(ring + P::kSlot, kl, vl, q, block_of(3), false, ql, N, g, sl2, m_run, l_run, acc);
+      }
+      const float l_tot = col_sum(l_run);
+      P::store_o(acc, l_tot > 0.0f ? __builtin_amdgcn_rcpf(l_tot) : 0.0f, Or, qrow, g);
+      return;
     }
-    const float l_tot = col_sum(l_run);
-    P::store_o(acc, l_tot > 0.0f ? __builtin_amdgcn_rcpf(l_tot) : 0.0f, Or, qrow, g);
-    return;
   }
 
-  typename P::Slot nxt;
-  P::load_slot(nxt, Kr, Vr, blk_off(0), tid, tb);
-  P::store_slot(nxt, ring, tid);
+  BlkSlots<P> nxt;
+  load_blk<P>(nxt, Kr, Vr, blk_off(0), tid, tb);
+  store_blk<P>(nxt, ring, tid);
   __syncthreads();
 
   for (int e = 0; e < ne; ++e) {
-    P::load_slot(nxt, Kr, Vr, blk_off(e + 1), tid, tb);
+    load_blk<P>(nxt, Kr, Vr, blk_off(e + 1), tid, tb);
     const int cb = block_of(e);
-    block_update<P>(ring + (e & 1) * P::kSlot, kl, vl, q, cb, dense && a.causal && cb == r, 16 * wv + c, N, g,
+    block_update<P>(ring + (e & 1) * P::kBlk, kl, vl, q, cb, dense && a.causal && cb == r, 16 * wv + c, N, g,
                     a.scale_log2, m_run, l_run, acc);
     // block e+1 goes into the slot block e-1 used (all waves passed the
     // barrier that ended iteration e-1)
-    if (e + 1 < ne) P::store_slot(nxt, ring + ((e + 1) & 1) * P::kSlot, tid);
+    if (e + 1 < ne) store_blk<P>(nxt, ring + ((e + 1) & 1) * P::kBlk, tid);
     __syncthreads();
   }
   const float l_tot = col_sum(l_run);

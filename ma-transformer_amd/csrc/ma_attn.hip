@@ -1058,16 +1058,24 @@ int launch_stream(const ma_attn_desc* d, const void* q, const void* k, const voi
 bool block_applies(const ma_attn_desc* d, const void* q, const void* k, const void* v, const void* o) {
   const bool blocks = d->pattern == MA_ATTN_BLOCK_SPARSE && d->block_size == 64;
   if (!(blocks || d->pattern == MA_ATTN_DENSE) || d->head_dim != kHeadDim) return false;
-  if (d->dtype != MA_ATTN_BF16 && d->dtype != MA_ATTN_F16) return false;
   if (!(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o))) return false;
-  const int64_t tb = d->num_heads * kHeadDim * 2;
+  const int64_t tb = d->num_heads * kHeadDim * (d->dtype == MA_ATTN_F32 ? 4 : 2);
   const int64_t nbq = (d->seq_len + 63) / 64;
   return (d->seq_len + 128) * tb < (1LL << 31) && d->batch * d->num_heads * nbq <= (int64_t)INT32_MAX;
 }
 
 template <class P>
-void launch_block_t(const BlockArgs& a, int64_t bh, hipStream_t st) {
-  launch(true, block_row_kernel<P>, dim3((unsigned)(bh * a.nbq)), dim3(256), 0, st, a);
+int launch_block_t(const BlockArgs& a, int64_t bh, hipStream_t st) {
+  constexpr size_t shm = 2 * (size_t)P::kBlk;  // two block buffers (fp32: 68 KB)
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&block_row_kernel<P>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess)
+      return fail("ma_attn: cannot reserve %zu B of LDS for the block kernel", shm);
+    attr_set = true;
+  }
+  launch(true, block_row_kernel<P>, dim3((unsigned)(bh * a.nbq)), dim3(256), (uint32_t)shm, st, a);
+  return 0;
 }
 
 int launch_block(const ma_attn_desc* d, const void* q, const void* k, const void* v, void* o, hipStream_t st) {
@@ -1085,11 +1093,9 @@ int launch_block(const ma_attn_desc* d, const void* q, const void* k, const void
   a.nbq = (int32_t)((d->seq_len + 63) / 64);
   a.scale_log2 = scale_of(d) * 1.4426950408889634f;
   const int64_t bh = d->batch * d->num_heads;
-  if (d->dtype == MA_ATTN_BF16)
-    launch_block_t<HalfPath<__bf16>>(a, bh, st);
-  else
-    launch_block_t<HalfPath<_Float16>>(a, bh, st);
-  return 0;
+  if (d->dtype == MA_ATTN_BF16) return launch_block_t<HalfPath<__bf16>>(a, bh, st);
+  if (d->dtype == MA_ATTN_F16) return launch_block_t<HalfPath<_Float16>>(a, bh, st);
+  return launch_block_t<F32Path>(a, bh, st);
 }
 
 // Backward: SLIDING and DENSE key sets (the reference's backward entry

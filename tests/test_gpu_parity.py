@@ -146,7 +146,7 @@ def _random_table(nb, width, seed, rng_extra_pad=True):
 
 
 @pytest.mark.parametrize("N", [64, 65, 200, 1000])
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_block_sparse_geometry(ext, oracle, N, dtype):
     shape = (2, N, 3, 64)
     (q, k, v), up = _inputs(shape, 500 + N, dtype, scale=0.5)
@@ -172,9 +172,10 @@ def test_longformer_geometry(ext, oracle, N, G, left, right, dtype):
 
 @pytest.mark.parametrize("N", [1, 63, 64, 65, 200, 1000])
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_dense_mfma_geometry(ext, oracle, N, causal, dtype):
-    """dense_forward at head_dim 64 in 16-bit (the block kernel with every block)."""
+    """dense_forward at head_dim 64 (the block kernel with every block; fp32
+    on 16x16x4 MFMA with two-slot blocks)."""
     shape = (2, N, 3, 64)
     (q, k, v), up = _inputs(shape, 1300 + N + causal, dtype)
     y = ext.dense_forward(q, k, v, causal)
@@ -183,12 +184,13 @@ def test_dense_mfma_geometry(ext, oracle, N, causal, dtype):
 
 
 @pytest.mark.parametrize("causal", [False, True])
-def test_dense_mfma_long(ext, oracle, causal):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_dense_mfma_long(ext, oracle, causal, dtype):
     """B=2 H=4 N=8000: many key blocks per row, causal rows in reverse order."""
-    (q, k, v), up = _inputs((2, 8000, 4, 64), 1400 + causal, torch.bfloat16)
+    (q, k, v), up = _inputs((2, 8000, 4, 64), 1400 + causal, dtype)
     y = ext.dense_forward(q, k, v, causal)
     spec = oracle.Spec(2, 8000, 4, 64, pattern="dense", causal=causal)
-    _check_sampled(oracle, spec, up, y, torch.bfloat16, (0, 4), [(0, 70), (3990, 4100), (7900, 8000)])
+    _check_sampled(oracle, spec, up, y, dtype, (0, 4), [(0, 70), (3990, 4100), (7900, 8000)])
 
 
 @pytest.mark.parametrize("width,padded", [(2, False), (2, True), (4, False), (4, True), (3, True)])
