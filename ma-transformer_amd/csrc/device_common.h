@@ -17,6 +17,9 @@ typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 // MFMA operand handling per 16-bit element type.
 //   x32 : 16x16x32 (8 elements of the contraction per lane)
@@ -34,9 +37,11 @@ struct Mma<__bf16> {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b),
                                                      c, 0, 0, 0);
   }
+  // x in the low half, y in the high half, each rounded to nearest even: one
+  // v_cvt_pk_bf16_f32 (converting the two separately and shifting them
+  // together costs four instructions)
   static __device__ __forceinline__ uint32_t pack2(float x, float y) {
-    const __bf16 a = static_cast<__bf16>(x), b = static_cast<__bf16>(y);
-    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x, y}, bf16x2));
   }
 };
 
@@ -50,9 +55,9 @@ struct Mma<_Float16> {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0,
                                                  0, 0);
   }
+  // one v_cvt_pk_f16_f32 (round to nearest even)
   static __device__ __forceinline__ uint32_t pack2(float x, float y) {
-    const _Float16 a = static_cast<_Float16>(x), b = static_cast<_Float16>(y);
-    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x, y}, f16x2));
   }
 };
 
