@@ -925,7 +925,13 @@ StreamPlan stream_plan(const ma_attn_desc* d) {
   const int64_t nr_max = (d->seq_len + p.geom.dil - 1) / p.geom.dil;
   p.tiles = (nr_max + 63) / 64;
   const int64_t streams = d->batch * d->num_heads * p.geom.dil;
-  const int64_t per_cu = ma::imax64(1, ma::imin64(p.max_per_cu, (160 * 1024) / p.lds));
+  int64_t per_cu = ma::imax64(1, ma::imin64(p.max_per_cu, (160 * 1024) / p.lds));
+  // A window with a right halo reads a halo block at both ends of a chunk.
+  // For 16-bit tiles (light compute) one chunk twice as long per CU pays
+  // that halo half as often and measured faster than two per CU (cfg2 bf16:
+  // 35.0 -> 32.5 us); fp32 tiles need the second workgroup to hide their
+  // MFMA latency (cfg2 fp32: 72 vs 82 us).
+  if (!f32 && !lg && p.geom.right > 0) per_cu = 1;
   const int64_t slots = 256 * per_cu;  // resident workgroups
   // Workgroups per stream: as many as fit the resident slots in one wave
   // (rounded per stream, a grid that overflows the slots by a few
