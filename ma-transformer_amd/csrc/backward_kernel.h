@@ -272,17 +272,19 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
   P::load_q(gr, Gr, qrow, g);
   const uint32_t kl = P::k_lane(c, g), vl = P::v_lane(c, g);
 
-  // key blocks of the band of this tile's queries
-  const int kb_lo = max(floordiv32(64 * w.t - L, 64), 0);
-  const int kb_hi = min(floordiv32(64 * w.t + 63 + R, 64), w.nblk - 1);
-  const int nb = kb_hi - kb_lo + 1;
+  // 64-row groups of keys from the band's first row, not from block
+  // boundaries: the tile's keys [64t-L, 64t+63+R] take ceil((64+L+R)/64)
+  // groups (2 for [i-32, i+31], which straddles 3 aligned blocks)
+  const int key_lo = max(64 * w.t - L, 0);
+  const int key_hi = min(64 * w.t + 63 + R, w.Nr - 1);
+  const int nb = (key_hi - key_lo) / 64 + 1;
   const int items = 2 * nb;  // pass 1, then pass 2 over the same blocks
   // A band of at most two blocks stays resident in the two buffers for pass
   // 2 (block j in buffer j); wider bands stream through them twice.
   const bool resident = nb <= 2;
-  auto blk_of = [&](int e) { return kb_lo + (e < nb ? e : e - nb); };
+  auto row_of = [&](int e) { return key_lo + 64 * (e < nb ? e : e - nb); };  // first key of item e's group
   auto buf_of = [&](int e) { return resident ? (e < nb ? e : e - nb) : (e & 1); };
-  auto off_of = [&](int e) { return e < (resident ? nb : items) ? (uint32_t)(64 * blk_of(e)) * tb : kOob; };
+  auto off_of = [&](int e) { return e < (resident ? nb : items) ? (uint32_t)row_of(e) * tb : kOob; };
 
   // V is read only as rows (dP^T = V dO^T): its transposed part stays unwritten
   BlkSlots<P> xk;
@@ -305,7 +307,7 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
     load_rblk<P>(xv, Vr, off_of(e + 1), tid, tb);
     const uint8_t* sk = ring + buf_of(e) * kBuf;
     f32x4 s[4], dp[4];
-    const int live = bwdq_scores<P>(sk, sk + P::kBlk, kl, qr, gr, 64 * blk_of(e), q0, L, R, dl, g, w.Nr, s, dp);
+    const int live = bwdq_scores<P>(sk, sk + P::kBlk, kl, qr, gr, row_of(e), q0, L, R, dl, g, w.Nr, s, dp);
     if (e < nb) {  // pass 1
       bwdq_pass1(s, dp, live, sl2, m_run, l_run, a_run);
       if (e == nb - 1) bwdq_stats(m_run, l_run, a_run, sl2, lse2, dlt);
@@ -357,13 +359,14 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdArgs a) {
   P::load_q(vr, Vr, krow, g);
   const uint32_t kl = P::k_lane(c, g), vl = P::v_lane(c, g);
 
-  // query blocks whose band reaches this tile's keys: queries [key-R, key+L]
-  const int qb_lo = max(floordiv32(64 * w.t - R, 64), 0);
-  const int qb_hi = min(floordiv32(64 * w.t + 63 + L, 64), w.nblk - 1);
-  const int nb = qb_hi - qb_lo + 1;
-  auto off_of = [&](int e) { return e < nb ? (uint32_t)(64 * (qb_lo + e)) * tb : kOob; };
+  // 64-row groups of queries from the first query that sees the tile's keys
+  // ([64t-R, 64t+63+L]), as the key groups of bwd_q_kernel
+  const int q_lo = max(64 * w.t - R, 0);
+  const int q_hi = min(64 * w.t + 63 + L, w.Nr - 1);
+  const int nb = (q_hi - q_lo) / 64 + 1;
+  auto off_of = [&](int e) { return e < nb ? (uint32_t)(q_lo + 64 * e) * tb : kOob; };
   // thread tid < 64 carries the statistics of query row tid of the block
-  auto stat_off = [&](int e) { return e < nb && tid < 64 ? (uint32_t)(64 * (qb_lo + e) + tid) * S.stride : kOob; };
+  auto stat_off = [&](int e) { return e < nb && tid < 64 ? (uint32_t)(q_lo + 64 * e + tid) * S.stride : kOob; };
 
   BlkSlots<P> xq, xg;
   load_blk<P>(xq, Qr, Qr, off_of(0), tid, tb);
@@ -385,7 +388,7 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdArgs a) {
     xs = bload8(S.r, stat_off(e + 1));
     const uint8_t* sq = ring + (e & 1) * kBuf;
     bwdkv_block<P>(sq, sq + P::kBlk, reinterpret_cast<const float*>(sq + 2 * P::kBlk), kl, vl, kr, vr,
-                   64 * (qb_lo + e), k0, L, R, dl, g, w.Nr, a.scale_log2, acc_k, acc_v);
+                   q_lo + 64 * e, k0, L, R, dl, g, w.Nr, a.scale_log2, acc_k, acc_v);
     uint8_t* nx = ring + ((e + 1) & 1) * kBuf;
     store_blk<P>(xq, nx, tid);
     store_blk<P>(xg, nx + P::kBlk, tid);
