@@ -79,13 +79,13 @@ __device__ __forceinline__ bool bwd_tile(const BwdArgs& a, BwdTile& w) {
 // Mask of one 16x16 product: element r of lane (c, g) pairs rows whose
 // key - query offset plus left is x + SGN*r (x per lane, see the callers),
 // and whose streamed row (key in bwd_q_kernel, query in bwd_kv_kernel) is
-// idx0 + r; kept iff the offset lies in [-left, right] and that row is below
-// lim.
+// idx0 + r; kept iff the offset lies in [-left, right] and that row lies in
+// [0, lim) (stream kernels' first block may start before row 0).
 template <int SGN>
 __device__ __forceinline__ void bwd_mask(f32x4& z, int x, int span, int idx0, int lim) {
 #pragma unroll
   for (int r = 0; r < 4; ++r)
-    z[r] = (uint32_t)(x + SGN * r) <= (uint32_t)span && idx0 + r < lim ? z[r] : -INFINITY;
+    z[r] = (uint32_t)(x + SGN * r) <= (uint32_t)span && (uint32_t)(idx0 + r) < (uint32_t)lim ? z[r] : -INFINITY;
 }
 
 // ---------------------------------------------------------------- per-block work
@@ -105,7 +105,7 @@ __device__ __forceinline__ int bwdq_scores(const uint8_t* sk, const uint8_t* sv,
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int rel = key0 + 16 * u - q0;  // key - query offsets span [rel-15, rel+15]
-    if (rel + 15 < -L || rel - 15 > R || key0 + 16 * u >= Nr) {
+    if (rel + 15 < -L || rel - 15 > R || key0 + 16 * u >= Nr || key0 + 16 * u + 15 < 0) {
       s[u] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
       dp[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       continue;
@@ -113,7 +113,7 @@ __device__ __forceinline__ int bwdq_scores(const uint8_t* sk, const uint8_t* sv,
     live |= 1 << u;
     s[u] = P::qk(sk + P::blk_k(u) + kl, qr);
     dp[u] = P::qk(sv + P::blk_k(u) + kl, gr);
-    if (rel - 15 < -L || rel + 15 > R || key0 + 16 * u + 15 >= Nr)
+    if (rel - 15 < -L || rel + 15 > R || key0 + 16 * u + 15 >= Nr || key0 + 16 * u < 0)
       bwd_mask<1>(s[u], dl + rel, L + R, key0 + 16 * u + 4 * g, Nr);
   }
   return live;
@@ -188,7 +188,7 @@ __device__ __forceinline__ void bwdkv_block(const uint8_t* sq, const uint8_t* sg
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int rel = k0 - (qbase + 16 * u);  // key - query offsets span [rel-15, rel+15]
-    if (rel + 15 < -L || rel - 15 > R || qbase + 16 * u >= Nr) {
+    if (rel + 15 < -L || rel - 15 > R || qbase + 16 * u >= Nr || qbase + 16 * u + 15 < 0) {
       s[u] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
       dp[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       continue;
@@ -196,7 +196,7 @@ __device__ __forceinline__ void bwdkv_block(const uint8_t* sq, const uint8_t* sg
     live |= 1 << u;
     s[u] = P::qk(sq + P::blk_k(u) + kl, kr);   // S[query 16u+4g+r][key c]
     dp[u] = P::qk(sg + P::blk_k(u) + kl, vr);  // dP[query][key c]
-    if (rel - 15 < -L || rel + 15 > R || qbase + 16 * u + 15 >= Nr)
+    if (rel - 15 < -L || rel + 15 > R || qbase + 16 * u + 15 >= Nr || qbase + 16 * u < 0)
       bwd_mask<-1>(s[u], dl + rel, L + R, qbase + 16 * u + 4 * g, Nr);
   }
 #pragma unroll
@@ -410,20 +410,23 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdArgs a) {
 // exponentials (p = e / l) instead of recomputing exp2.
 
 // bwd_q_stream_kernel, interior tile t: the wave's queries qa = 64t + 16wv
-// against key sub-tiles s = 4t + wv - CL + j, block s >> 2 in ring buffer
-// (s >> 2) & 1.  Gives lse2 and delta of query qa + c and dQ^T (unscaled).
+// against key sub-tiles s = 4t + wv - CL + j.  The kernel's blocks start at
+// row 64j - 16*(CL & 3), so sub-tile s lies in block (s + (CL & 3)) >> 2, in
+// ring buffer parity of that.  Gives lse2 and delta of query qa + c and dQ^T
+// (unscaled).
 template <class P, int L, int R>
 __device__ __forceinline__ void bwdq_window_tile(const uint8_t* ring, uint32_t kl, uint32_t vl, const typename P::Q& qr,
                                                  const typename P::Q& gr, int t, int wv, int dl, float sl2,
                                                  float& lse2, float& dlt, f32x4 (&acc)[4]) {
   using G = WinGeom<L, R, 64>;
   constexpr int kBuf = 2 * P::kBlk;
+  constexpr int kSh = G::CL & 3;
   f32x4 e[G::NSUB], dp[G::NSUB];
   uint32_t kt[G::NSUB];  // K^T of sub-tile j (the K buffer's transposed part)
   float mx = -INFINITY;
 #pragma unroll
   for (int j = 0; j < G::NSUB; ++j) {
-    const int s = 4 * t + wv - G::CL + j;
+    const int s = 4 * t + wv - G::CL + j + kSh;  // shifted-grid sub-tile index
     const uint32_t bb = (uint32_t)(((s >> 2) & 1) * kBuf);
     const int u = s & 3;
     kt[j] = bb + P::blk_v(u) + vl;
@@ -469,19 +472,21 @@ __device__ __forceinline__ void bwdq_window_tile(const uint8_t* ring, uint32_t k
 
 // bwd_kv_stream_kernel, interior tile t: the wave's keys ka = 64t + 16wv
 // against query sub-tiles s = 4t + wv - CR + j (the mirrored band: queries of
-// key k are [k-R, k+L]), block s >> 2 in ring buffer (s >> 2) & 1 with its
-// staged statistics.  dV^T and dK^T (unscaled) accumulate in acc_v, acc_k.
+// key k are [k-R, k+L]).  Blocks start at row 64j - 16*(CR & 3); sub-tile s
+// lies in block (s + (CR & 3)) >> 2 with its staged statistics.  dV^T and
+// dK^T (unscaled) accumulate in acc_v, acc_k.
 template <class P, int L, int R>
 __device__ __forceinline__ void bwdkv_window_tile(const uint8_t* ring, uint32_t kl, uint32_t vl, const typename P::Q& kr,
                                                   const typename P::Q& vr, int t, int wv, int g, int dl, float sl2,
                                                   f32x4 (&acc_k)[4], f32x4 (&acc_v)[4]) {
   using G = WinGeom<R, L, 64>;
   constexpr int kBuf = 2 * P::kBlk + 512;
+  constexpr int kSh = G::CL & 3;
   float p[G::NSUB][4], d[G::NSUB][4];
   uint32_t qt[G::NSUB];  // Q^T of sub-tile j (dO^T at + kBlk)
 #pragma unroll
   for (int j = 0; j < G::NSUB; ++j) {
-    const int s = 4 * t + wv - G::CL + j;
+    const int s = 4 * t + wv - G::CL + j + kSh;  // shifted-grid sub-tile index
     const uint32_t bb = (uint32_t)(((s >> 2) & 1) * kBuf);
     const int u = s & 3;
     qt[j] = bb + P::blk_v(u) + vl;
@@ -572,8 +577,16 @@ __global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
   const __amdgpu_buffer_rsrc_t Gr = make_rsrc(static_cast<const Elt*>(a.dout) + w.base, w.nrec);
   const __amdgpu_buffer_rsrc_t DQr = make_rsrc(static_cast<Elt*>(a.dq) + w.base, w.nrec);
 
-  auto lo_of = [&](int t) { return max(floordiv32(64 * t - L, 64), 0); };
-  auto hi_of = [&](int t) { return min(floordiv32(64 * t + 63 + R, 64), w.nblk - 1); };
+  // Key blocks are 64 rows from row ob = -16*(ceil(L/16) & 3), so that a
+  // band whose 64 + L + R keys fit two blocks meets exactly two ([i-32, i+31]
+  // straddles 3 aligned blocks, 2 shifted ones; causal 64 has ob = 0).  Rows
+  // of block 0 before row 0 get offsets that wrap past the buffer range and
+  // read zero, and their keys are masked.
+  const int ob = -16 * (((L + 15) >> 4) & 3);
+  const int nbs = floordiv32(w.Nr - 1 - ob, 64) + 1;
+  auto lo_of = [&](int t) { return max(floordiv32(64 * t - L - ob, 64), 0); };
+  auto hi_of = [&](int t) { return min(floordiv32(64 * t + 63 + R - ob, 64), nbs - 1); };
+  auto boff = [&](int j) { return (uint32_t)(64 * j + ob) * tb; };
   const uint32_t lrow = (uint32_t)(16 * wv + c) * tb;  // this lane's row within a tile
   const uint32_t kl = P::k_lane(c, g), vl = P::v_lane(c, g);
 
@@ -584,8 +597,8 @@ __global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
   BlkSlots<P> xk;
   BlkRows<P> xv;  // V is read only as rows
   for (int j = lo_of(w.t0); j <= hi_of(w.t0); ++j) {
-    load_blk<P>(xk, Kr, Kr, (uint32_t)(64 * j) * tb, tid, tb);
-    load_rblk<P>(xv, Vr, (uint32_t)(64 * j) * tb, tid, tb);
+    load_blk<P>(xk, Kr, Kr, boff(j), tid, tb);
+    load_rblk<P>(xv, Vr, boff(j), tid, tb);
     store_blk<P>(xk, ring + (j & 1) * kBuf, tid);
     store_rblk<P>(xv, ring + (j & 1) * kBuf + P::kBlk, tid);
   }
@@ -597,7 +610,7 @@ __global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
     // prefetch: tile t+1's new block and rows
     const bool more = t + 1 < w.t1;
     const int nblk_new = more && hi_of(t + 1) > hi_of(t) ? hi_of(t + 1) : -1;
-    const uint32_t noff = nblk_new >= 0 ? (uint32_t)(64 * nblk_new) * tb : kOob;
+    const uint32_t noff = nblk_new >= 0 ? boff(nblk_new) : kOob;
     load_blk<P>(xk, Kr, Kr, noff, tid, tb);
     load_rblk<P>(xv, Vr, noff, tid, tb);
     const uint32_t nrow = more ? (uint32_t)(64 * (t + 1)) * tb + lrow : kOob;
@@ -625,11 +638,11 @@ __global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
       const uint8_t* sk0 = ring + (lo & 1) * kBuf;
       const uint8_t* sk1 = ring + (hi & 1) * kBuf;
       f32x4 s0[4], dp0[4], s1[4], dp1[4];
-      const int live0 = bwdq_scores<P>(sk0, sk0 + P::kBlk, kl, qr, gr, 64 * lo, q0, L, R, dl, g, w.Nr, s0, dp0);
+      const int live0 = bwdq_scores<P>(sk0, sk0 + P::kBlk, kl, qr, gr, 64 * lo + ob, q0, L, R, dl, g, w.Nr, s0, dp0);
       bwdq_pass1(s0, dp0, live0, sl2, m_run, l_run, a_run);
       int live1 = 0;
       if (hi > lo) {
-        live1 = bwdq_scores<P>(sk1, sk1 + P::kBlk, kl, qr, gr, 64 * hi, q0, L, R, dl, g, w.Nr, s1, dp1);
+        live1 = bwdq_scores<P>(sk1, sk1 + P::kBlk, kl, qr, gr, 64 * hi + ob, q0, L, R, dl, g, w.Nr, s1, dp1);
         bwdq_pass1(s1, dp1, live1, sl2, m_run, l_run, a_run);
       }
       bwdq_stats(m_run, l_run, a_run, sl2, lse2, dlt);
@@ -675,9 +688,14 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_stream_kernel(BwdArgs a) {
   const __amdgpu_buffer_rsrc_t DVr = make_rsrc(static_cast<Elt*>(a.dv) + w.base, w.nrec);
   const BwdStats S = bwd_stats_rsrc(a, w.b, w.h, w.rho, w.Nr);
 
-  auto lo_of = [&](int t) { return max(floordiv32(64 * t - R, 64), 0); };
-  auto hi_of = [&](int t) { return min(floordiv32(64 * t + 63 + L, 64), w.nblk - 1); };
-  auto stat_off = [&](int j) { return j >= 0 && tid < 64 ? (uint32_t)(64 * j + tid) * S.stride : kOob; };
+  // Query blocks are 64 rows from row ob = -16*(ceil(R/16) & 3) (as the key
+  // blocks of bwd_q_stream_kernel, mirrored)
+  const int ob = -16 * (((R + 15) >> 4) & 3);
+  const int nbs = floordiv32(w.Nr - 1 - ob, 64) + 1;
+  auto lo_of = [&](int t) { return max(floordiv32(64 * t - R - ob, 64), 0); };
+  auto hi_of = [&](int t) { return min(floordiv32(64 * t + 63 + L - ob, 64), nbs - 1); };
+  auto boff = [&](int j) { return (uint32_t)(64 * j + ob) * tb; };
+  auto stat_off = [&](int j) { return j >= 0 && tid < 64 ? (uint32_t)(64 * j + ob + tid) * S.stride : kOob; };
   const uint32_t lrow = (uint32_t)(16 * wv + c) * tb;
   const uint32_t kl = P::k_lane(c, g), vl = P::v_lane(c, g);
 
@@ -687,8 +705,8 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_stream_kernel(BwdArgs a) {
   BlkSlots<P> xq, xg;
   uint2 xs;
   for (int j = lo_of(w.t0); j <= hi_of(w.t0); ++j) {
-    load_blk<P>(xq, Qr, Qr, (uint32_t)(64 * j) * tb, tid, tb);
-    load_blk<P>(xg, Gr, Gr, (uint32_t)(64 * j) * tb, tid, tb);
+    load_blk<P>(xq, Qr, Qr, boff(j), tid, tb);
+    load_blk<P>(xg, Gr, Gr, boff(j), tid, tb);
     xs = bload8(S.r, stat_off(j));
     uint8_t* sb = ring + (j & 1) * kBuf;
     store_blk<P>(xq, sb, tid);
@@ -701,7 +719,7 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_stream_kernel(BwdArgs a) {
   for (int t = w.t0; t < w.t1; ++t) {
     const bool more = t + 1 < w.t1;
     const int nblk_new = more && hi_of(t + 1) > hi_of(t) ? hi_of(t + 1) : -1;
-    const uint32_t noff = nblk_new >= 0 ? (uint32_t)(64 * nblk_new) * tb : kOob;
+    const uint32_t noff = nblk_new >= 0 ? boff(nblk_new) : kOob;
     load_blk<P>(xq, Qr, Qr, noff, tid, tb);
     load_blk<P>(xg, Gr, Gr, noff, tid, tb);
     xs = bload8(S.r, stat_off(nblk_new));
@@ -725,7 +743,7 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_stream_kernel(BwdArgs a) {
     if (!done)
       for (int j = lo_of(t); j <= hi_of(t); ++j) {
         const uint8_t* sq = ring + (j & 1) * kBuf;
-        bwdkv_block<P>(sq, sq + P::kBlk, reinterpret_cast<const float*>(sq + 2 * P::kBlk), kl, vl, kr, vr, 64 * j,
+        bwdkv_block<P>(sq, sq + P::kBlk, reinterpret_cast<const float*>(sq + 2 * P::kBlk), kl, vl, kr, vr, 64 * j + ob,
                        k0, L, R, dl, g, w.Nr, a.scale_log2, acc_k, acc_v);
       }
     const uint32_t orow = (uint32_t)(64 * t) * tb + lrow;

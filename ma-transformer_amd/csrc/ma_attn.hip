@@ -1183,17 +1183,27 @@ int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* 
   const int64_t streams = d->batch * d->num_heads * dil;
   // two block buffers each: (K, K^T) + V rows for dQ; (Q, Q^T) + (dO, dO^T) + statistics for dK/dV
   const size_t shm_q = 4 * (size_t)P::kBlk, shm_kv = 2 * (2 * (size_t)P::kBlk + 512);
-  // Bands of at most two 64-row blocks in both directions stream a chunk of
-  // tiles per workgroup (two workgroups per CU, one wave of workgroups);
-  // wider bands take one workgroup per tile.
-  const bool chunked = ma::floordiv64(63 + R, 64) - ma::floordiv64(-L, 64) + 1 <= 2 &&
-                       ma::floordiv64(63 + L, 64) - ma::floordiv64(-R, 64) + 1 <= 2 &&
+  // Bands that meet at most two 64-row blocks in both directions stream a
+  // chunk of tiles per workgroup; wider bands take one workgroup per tile.
+  // The stream kernels' blocks start at row -16*(ceil(L/16) & 3) (keys) and
+  // -16*(ceil(R/16) & 3) (queries), which fits [i-32, i+31] in two.
+  const int64_t obq = -16 * (((L + 15) / 16) & 3), obkv = -16 * (((R + 15) / 16) & 3);
+  const bool chunked = ma::floordiv64(63 + R - obq, 64) - ma::floordiv64(-L - obq, 64) + 1 <= 2 &&
+                       ma::floordiv64(63 + L - obkv, 64) - ma::floordiv64(-R - obkv, 64) + 1 <= 2 &&
                        !getenv("MA_ATTN_BWD_PER_TILE");
-  // the causal-64 band (BASELINE target, dilated config) has a fixed-window instantiation
-  const bool fixed = chunked && L == 63 && R == 0 && !getenv("MA_ATTN_BWD_NO_FIXED");
-  auto kq = !chunked ? &bwd_q_kernel<P> : fixed ? &bwd_q_stream_kernel<P, 63, 0> : &bwd_q_stream_kernel<P, -1, -1>;
-  auto kkv = !chunked ? &bwd_kv_kernel<P> : fixed ? &bwd_kv_stream_kernel<P, 63, 0> : &bwd_kv_stream_kernel<P, -1, -1>;
-  const int variant = !chunked ? 0 : fixed ? 2 : 1;
+  // fixed-window instantiations: causal 64 (BASELINE target, dilated config)
+  // and [i-32, i+31] (cfg 2)
+  const bool no_fixed = getenv("MA_ATTN_BWD_NO_FIXED") != nullptr;
+  const int fixed = !chunked || no_fixed ? 0 : L == 63 && R == 0 ? 1 : L == 32 && R == 31 ? 2 : 0;
+  auto kq = !chunked     ? &bwd_q_kernel<P>
+            : fixed == 1 ? &bwd_q_stream_kernel<P, 63, 0>
+            : fixed == 2 ? &bwd_q_stream_kernel<P, 32, 31>
+                         : &bwd_q_stream_kernel<P, -1, -1>;
+  auto kkv = !chunked     ? &bwd_kv_kernel<P>
+             : fixed == 1 ? &bwd_kv_stream_kernel<P, 63, 0>
+             : fixed == 2 ? &bwd_kv_stream_kernel<P, 32, 31>
+                          : &bwd_kv_stream_kernel<P, -1, -1>;
+  const int variant = !chunked ? 0 : 1 + fixed;
   // chunks per stream fitted to two rounds of the resident workgroups (2 per
   // CU for 16-bit, 1 for fp32, whose block buffers are twice the size): the
   // second round fills the slots the first round's faster workgroups leave.
@@ -1205,7 +1215,7 @@ int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* 
   if (const char* e = getenv("MA_ATTN_BWD_CHUNK")) a.chunk = (int32_t)ma::imax64(1, atoll(e));
   a.chunks = (int32_t)((a.tiles + a.chunk - 1) / a.chunk);
   const int64_t wgs = chunked ? streams * a.chunks : streams * a.tiles;
-  static bool attr_set[3] = {false, false, false};
+  static bool attr_set[4] = {false, false, false, false};
   if (!attr_set[variant]) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kq), hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)shm_q) != hipSuccess ||

@@ -159,7 +159,8 @@ def test_sliding_backward_row_kernels(ext, oracle, monkeypatch, N, left, right, 
 
 
 @pytest.mark.parametrize("N,H,left,right,dil", [(5000, 16, 63, 0, 1), (4099, 8, 63, 0, 4), (3000, 8, 0, 0, 1),
-                                                 (2500, 8, 10, 0, 3), (3333, 8, 0, 64, 1)])
+                                                 (2500, 8, 10, 0, 3), (3333, 8, 0, 64, 1), (4000, 8, 32, 31, 1),
+                                                 (3001, 8, 32, 31, 4), (2000, 8, 5, 40, 1), (2222, 8, 47, 16, 2)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_backward_chunked(ext, oracle, N, H, left, right, dil, dtype):
     """Bands of at most two blocks stream several tiles per workgroup (the
@@ -172,29 +173,30 @@ def test_backward_chunked(ext, oracle, N, H, left, right, dil, dtype):
     _check(got, oracle.backward(spec, *up), dtype)
 
 
-@pytest.mark.parametrize("N,H,dil", [(5000, 16, 1), (4099, 8, 4)])
+@pytest.mark.parametrize("N,H,left,right,dil", [(5000, 16, 63, 0, 1), (4099, 8, 63, 0, 4), (4000, 8, 32, 31, 1),
+                                                 (3001, 8, 32, 31, 4)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_backward_chunked_generic(ext, oracle, monkeypatch, N, H, dil, dtype):
-    """The causal-64 band on the generic stream tiles (fixed-window tiles
-    switched off with MA_ATTN_BWD_NO_FIXED) stays correct."""
+def test_backward_chunked_generic(ext, oracle, monkeypatch, N, H, left, right, dil, dtype):
+    """The bands with fixed-window tiles (causal 64, [i-32, i+31]) on the
+    generic stream tiles (MA_ATTN_BWD_NO_FIXED) stay correct."""
     monkeypatch.setenv("MA_ATTN_BWD_NO_FIXED", "1")
     shape = (2, N, H, 64)
     (q, k, v, g), up = _case(shape, 890 + N + dil, dtype)
-    got = ext.sliding_backward(q, k, v, g, 63, 0, dil)
-    spec = oracle.Spec(*shape, pattern="sliding", left=63, right=0, dilation=dil)
+    got = ext.sliding_backward(q, k, v, g, left, right, dil)
+    spec = oracle.Spec(*shape, pattern="sliding", left=left, right=right, dilation=dil)
     _check(got, oracle.backward(spec, *up), dtype)
 
 
 @pytest.mark.parametrize("N", [64, 127, 128, 129, 191, 192, 255, 256, 257, 1000])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-def test_backward_fixed_window_edges(ext, oracle, N, dtype):
-    """Causal 64 (fixed-window tiles inside, generic tiles at the sequence
-    ends): lengths around the interior-tile bounds (the dQ kernel's tile t
-    needs 64t + 64 <= N, the dK/dV kernel's 64t + 128 <= N)."""
+@pytest.mark.parametrize("left,right", [(63, 0), (32, 31)])
+def test_backward_fixed_window_edges(ext, oracle, N, dtype, left, right):
+    """The fixed-window bands (fixed-window tiles inside, generic tiles at
+    the sequence ends): lengths around the interior-tile bounds."""
     shape = (1, N, 4, 64)
     (q, k, v, g), up = _case(shape, 910 + N, dtype)
-    got = ext.sliding_backward(q, k, v, g, 63, 0, 1)
-    spec = oracle.Spec(*shape, pattern="sliding", left=63, right=0)
+    got = ext.sliding_backward(q, k, v, g, left, right, 1)
+    spec = oracle.Spec(*shape, pattern="sliding", left=left, right=right)
     _check(got, oracle.backward(spec, *up), dtype)
 
 
