@@ -43,6 +43,17 @@ __all__ = ["forward", "dense_forward", "backward", "dense_backward", "sliding_fo
 
 def _check(*ts: torch.Tensor) -> None:
     """The reference's TORCH_CHECKs (sparse_attention_kernel.cu:427-432) as RuntimeError."""
+    # one pass for the common valid call; any failure takes the ordered checks below
+    try:
+        t0 = ts[0]
+        dt, shape, dev = t0.dtype, t0.shape, t0.get_device()
+        ok = dt in _ma.DTYPES and len(shape) == 4 and dev >= 0
+        for t in ts:
+            ok = ok and t.get_device() == dev and t.dtype == dt and t.shape == shape and t.is_contiguous()
+        if ok and all(isinstance(t, torch.Tensor) for t in ts):
+            return
+    except (AttributeError, TypeError):
+        pass
     for t in ts:
         if not isinstance(t, torch.Tensor):
             raise RuntimeError("Inputs must be tensors")
@@ -87,19 +98,43 @@ class kernel_events:
         return False
 
 
+# Host path per call: descriptors (and their workspace sizes) are cached per
+# call signature; the launch stream is read as a raw handle, and the device
+# is switched only when the inputs are not on the current one.
+_desc_cache: dict = {}
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_current_device = getattr(torch._C, "_cuda_getDevice", None)
+
+
+def _desc_of(B, N, H, D, dtype, pattern, kw, backward=False):
+    key = (B, N, H, D, dtype, pattern, backward, tuple(sorted(kw.items())))
+    hit = _desc_cache.get(key)
+    if hit is None:
+        if len(_desc_cache) > 512:
+            _desc_cache.clear()
+        desc = _ma.make_desc(B, N, H, D, _ma.DTYPES[dtype], pattern, **kw)
+        nbytes = _ma.backward_workspace_size(desc) if backward else _ma.workspace_size(desc)
+        hit = _desc_cache[key] = (desc, nbytes)
+    return hit
+
+
+def _on_device(dev: int, fn):
+    """Run fn(stream) with dev current and its current stream's raw handle."""
+    if _raw_stream is not None and _current_device is not None and _current_device() == dev:
+        return fn(_raw_stream(dev))
+    with torch.cuda.device(dev):
+        return fn(torch.cuda.current_stream(dev).cuda_stream)
+
+
 def _launch(q, k, v, pattern, **kw) -> torch.Tensor:
     _check(q, k, v)
     B, N, H, D = q.shape
     out = torch.empty_like(q)
-    desc = _ma.make_desc(B, N, H, D, _ma.DTYPES[q.dtype], pattern, **kw)
-    ws = None
-    nbytes = _ma.workspace_size(desc)
-    if nbytes:
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
-    with torch.cuda.device(q.device):
-        stream = torch.cuda.current_stream(q.device).cuda_stream
-        _ma.forward_raw(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                        ws.data_ptr() if ws is not None else 0, nbytes, stream, _events)
+    desc, nbytes = _desc_of(B, N, H, D, q.dtype, pattern, kw)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes else None
+    _on_device(q.get_device(), lambda stream: _ma.forward_raw(
+        desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), ws.data_ptr() if ws is not None else 0,
+        nbytes, stream, _events))
     return out
 
 
@@ -220,13 +255,11 @@ def _backward(q, k, v, grad_out, pattern, **kw) -> List[torch.Tensor]:
     _check(q, k, v, grad_out)
     B, N, H, D = q.shape
     dq, dk, dv = (torch.empty_like(q) for _ in range(3))
-    desc = _ma.make_desc(B, N, H, D, _ma.DTYPES[q.dtype], pattern, **kw)
-    nbytes = _ma.backward_workspace_size(desc)
+    desc, nbytes = _desc_of(B, N, H, D, q.dtype, pattern, kw, backward=True)
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
-    with torch.cuda.device(q.device):
-        stream = torch.cuda.current_stream(q.device).cuda_stream
-        _ma.backward_raw(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), grad_out.data_ptr(),
-                         dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), nbytes, stream, _events)
+    _on_device(q.get_device(), lambda stream: _ma.backward_raw(
+        desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), grad_out.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+        dv.data_ptr(), ws.data_ptr(), nbytes, stream, _events))
     return [dq, dk, dv]
 
 
