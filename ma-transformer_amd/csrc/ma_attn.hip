@@ -944,7 +944,7 @@ StreamPlan stream_plan(const ma_attn_desc* d) {
   p.chunks = (p.tiles + p.chunk - 1) / p.chunk;
   p.wgs = streams * p.chunks;
   p.tok_bytes = p.geom.dil * d->num_heads * kHeadDim * (f32 ? 4 : 2);
-  p.partial_bytes = lg ? streams * p.chunks * 4 * 16 * kPartial * (int64_t)sizeof(float) : 0;
+  p.partial_bytes = lg ? streams * p.chunks * 16 * kPartial * (int64_t)sizeof(float) : 0;
   return p;
 }
 
@@ -1017,8 +1017,8 @@ int launch_stream_half(const ma_attn_desc* d, const StreamArgs& a, const StreamP
   if (p.geom.G == 0) return launch_stream_any<P, false>(a, p.slots, p.wgs, st);
   const int rc = launch_stream_any<P, true>(a, p.slots, p.wgs, st);
   if (rc) return rc;
-  launch(true, longformer_combine<T>, dim3((unsigned)(d->batch * d->num_heads * p.geom.G)), dim3(64), 0, st,
-                     a.partials, static_cast<T*>(a.o), (int)(p.chunks * 4), (int)p.geom.G, (int)d->num_heads,
+  launch(true, longformer_combine<T>, dim3((unsigned)(d->batch * d->num_heads * p.geom.G)), dim3(256), 0, st,
+                     a.partials, static_cast<T*>(a.o), (int)p.chunks, (int)p.geom.G, (int)d->num_heads,
                      d->seq_len);
   return 0;
 }

@@ -44,7 +44,7 @@ struct StreamArgs {
   int32_t tok_bytes;  // bytes between consecutive rows of a residue class (dil * H * 64 * elt)
   float scale_log2;   // softmax scale * log2(e)
   int32_t num_global;  // Longformer: global tokens 0..G-1 (G <= 16)
-  float* partials;     // Longformer: [B*H][chunks*4][16][kPartial] per-wave softmax partials of the global rows
+  float* partials;     // Longformer: [B*H][chunks][16][kPartial] per-chunk softmax partials of the global rows
   int32_t pairs;       // 1: chunks 2p and 2p+1 share an XCD (grid a multiple of 16, chunks even)
 };
 
@@ -745,40 +745,101 @@ __global__ __launch_bounds__(256, LG ? 2 : P::kMinBlocks) void stream_kernel(Str
     step(tfirst + (n + 1) * dir, Y, X);
   }
 
-  if (LG) {  // this wave's partial for global query c: [64 unnormalised O][log2-scaled max][denominator]
+  if (LG) {
+    // Each wave's partial for global query c ([64 unnormalised O][log2-scaled
+    // max][denominator]) goes to LDS (the ring is free after the last tile's
+    // barrier; rows of 68 floats keep the 16 B stores aligned); the 4 waves'
+    // partials of a query then merge (log-sum-exp) into one per chunk, so the
+    // combine reads a quarter as many.
+    constexpr int kRowF = 68;
     const float l_tot = col_sum(lg);
-    float* dst = a.partials + ((((int64_t)b * a.H + h) * a.chunks + chunk_id) * 4 + wv) * 16 * kPartial + c * kPartial;
-    P::store_acc(accg, dst, g);
+    float* shp = reinterpret_cast<float*>(ring) + (wv * 16 + c) * kRowF;
+    P::store_acc(accg, shp, g);
     if (g == 0) {
-      dst[kHeadDim] = mg == -INFINITY ? -INFINITY : mg * a.scale_log2;
-      dst[kHeadDim + 1] = l_tot;
+      shp[kHeadDim] = mg == -INFINITY ? -INFINITY : mg * a.scale_log2;
+      shp[kHeadDim + 1] = l_tot;
     }
+    __syncthreads();
+    const int qq = tid >> 4, d0 = 4 * (tid & 15);  // global query qq, head_dim d0..d0+3
+    const float* sp = reinterpret_cast<const float*>(ring) + qq * kRowF;
+    float mw[4], mt = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      mw[w] = sp[w * 16 * kRowF + kHeadDim];
+      mt = fmaxf(mt, mw[w]);
+    }
+    float lt = 0.0f;
+    f32x4 at = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (mt != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float cw = __builtin_amdgcn_exp2f(mw[w] - mt);  // 0 for a wave that saw no key
+        lt = fmaf(sp[w * 16 * kRowF + kHeadDim + 1], cw, lt);
+        at += *reinterpret_cast<const f32x4*>(sp + w * 16 * kRowF + d0) * cw;
+      }
+    }
+    float* dst = a.partials + ((((int64_t)b * a.H + h) * a.chunks + chunk_id) * 16 + qq) * kPartial;
+    *reinterpret_cast<float2*>(dst + d0) = make_float2(at[0], at[1]);  // rows of 66 floats: 8 B aligned
+    *reinterpret_cast<float2*>(dst + d0 + 2) = make_float2(at[2], at[3]);
+    if ((tid & 15) == 0) *reinterpret_cast<float2*>(dst + kHeadDim) = make_float2(mt, lt);
   }
 }
 
 // Global query rows of Longformer: merge the per-wave partials of every chunk
-// (log-sum-exp combine) into O rows 0..G-1.  One workgroup of 64 threads
-// (one per head_dim element) per (batch, head, global row).
+// (log-sum-exp combine) into O rows 0..G-1.  One workgroup of 4 waves per
+// (batch, head, global row), over one partial per chunk; thread (wave w,
+// lane d) owns head_dim element d of the partials p = w, w+4, ...  Each wave takes its partials' maximum
+// first, so the weighted sums that follow have no dependence between
+// iterations (their loads overlap), then the 4 wave results merge in LDS.
+// (A single wave folding the partials one by one in an online merge waited
+// out one load round trip per partial: 42 us at cfg 4.)
 template <typename Elt>
-__global__ __launch_bounds__(64) void longformer_combine(const float* __restrict__ partials, Elt* __restrict__ o,
-                                                         int nparts, int G, int H, int64_t N) {
-  const int d = threadIdx.x;
+__global__ __launch_bounds__(256) void longformer_combine(const float* __restrict__ partials, Elt* __restrict__ o,
+                                                          int nparts, int G, int H, int64_t N) {
+  __shared__ float sh[4][kPartial];
+  const int d = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
   const int gq = blockIdx.x % G;
   const int bh = blockIdx.x / G;  // b * H + h
   const int h = bh % H;
   const int b = bh / H;
-  float m = -INFINITY, l = 0.0f, acc = 0.0f;
-  for (int p = 0; p < nparts; ++p) {
-    const float* src = partials + (((int64_t)bh * nparts + p) * 16 + gq) * kPartial;
-    const float mp = src[kHeadDim];
-    if (mp == -INFINITY) continue;
-    const float mn = fmaxf(m, mp);
-    const float ca = __builtin_amdgcn_exp2f(m - mn), cb = __builtin_amdgcn_exp2f(mp - mn);
-    l = l * ca + src[kHeadDim + 1] * cb;
-    acc = acc * ca + src[d] * cb;
-    m = mn;
+  // partial p of this global row: base + p * 16 * kPartial
+  const float* base = partials + ((int64_t)bh * nparts * 16 + gq) * kPartial;
+  constexpr int64_t kStride = 16 * kPartial;
+  float m = -INFINITY;
+#pragma unroll 8
+  for (int p = wv; p < nparts; p += 4) m = fmaxf(m, base[p * kStride + kHeadDim]);
+  float l = 0.0f, acc = 0.0f;
+  if (m != -INFINITY) {
+#pragma unroll 8
+    for (int p = wv; p < nparts; p += 4) {
+      const float* src = base + p * kStride;
+      const float w = __builtin_amdgcn_exp2f(src[kHeadDim] - m);  // 0 for a partial that saw no key
+      l = fmaf(src[kHeadDim + 1], w, l);
+      acc = fmaf(src[d], w, acc);
+    }
   }
-  o[(((int64_t)b * N + gq) * H + h) * kHeadDim + d] = static_cast<Elt>(l > 0.0f ? acc / l : 0.0f);
+  sh[wv][d] = acc;
+  if (d == 0) {
+    sh[wv][kHeadDim] = m;
+    sh[wv][kHeadDim + 1] = l;
+  }
+  __syncthreads();
+  if (wv == 0) {
+    float mt = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) mt = fmaxf(mt, sh[w][kHeadDim]);
+    float lt = 0.0f, at = 0.0f;
+    if (mt != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float c = __builtin_amdgcn_exp2f(sh[w][kHeadDim] - mt);
+        lt = fmaf(sh[w][kHeadDim + 1], c, lt);
+        at = fmaf(sh[w][d], c, at);
+      }
+    }
+    o[(((int64_t)b * N + gq) * H + h) * kHeadDim + d] = static_cast<Elt>(lt > 0.0f ? at / lt : 0.0f);
+  }
 }
 
 }  // namespace ma_dev
