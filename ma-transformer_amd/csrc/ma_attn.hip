@@ -252,14 +252,21 @@ __global__ __launch_bounds__(256) void narrow_kernel(const T* __restrict__ q, co
   float* vl = band + (size_t)rows * RS;
   float* part = vl + (size_t)rows * RS;  // [wave 1..3][lane][PS]
 
-  // Staging in batches of 4 elements per thread: every load of a batch is
+  // The lane's query row is loaded first (it depends on nothing), then the
+  // band in batches of 8 elements per thread: every load of a batch is
   // issued (indices clamped into range, so unconditionally) before the
-  // stores that wait for them.
-  const int ne = rows * DP;
-  for (int e0 = 0; e0 < ne; e0 += 256 * 4) {
-    float kx[4], vx[4];
+  // stores that wait for them, and the BASELINE band (127 rows of 16) is one
+  // batch -- a single global round trip before the barrier.
+  const int64_t i = i0 + lane;
+  const int64_t ic = i < N ? i : N - 1;
+  float qv[DP];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+  for (int d = 0; d < DP; ++d) qv[d] = ld_f(qb + ic * rs + (d < D ? d : D - 1));
+  const int ne = rows * DP;
+  for (int e0 = 0; e0 < ne; e0 += 256 * 8) {
+    float kx[8], vx[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
       const int e = min(e0 + tid + 256 * u, ne - 1);
       const int r = e / DP, d = min(e % DP, D - 1);
       const int64_t off = (j0 + r) * rs + d;
@@ -267,7 +274,7 @@ __global__ __launch_bounds__(256) void narrow_kernel(const T* __restrict__ q, co
       vx[u] = ld_f(vb + off);
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < 8; ++u) {
       const int e = e0 + tid + 256 * u;
       if (e < ne) {
         const int r = e / DP, d = e % DP;
@@ -276,14 +283,8 @@ __global__ __launch_bounds__(256) void narrow_kernel(const T* __restrict__ q, co
       }
     }
   }
-  const int64_t i = i0 + lane;
-  const int64_t ic = i < N ? i : N - 1;
-  float qv[DP];
 #pragma unroll
-  for (int d = 0; d < DP; ++d) {
-    const float x = ld_f(qb + ic * rs + (d < D ? d : D - 1));
-    qv[d] = d < D ? x : 0.0f;
-  }
+  for (int d = 0; d < DP; ++d) qv[d] = d < D ? qv[d] : 0.0f;
   __syncthreads();
 
   // this wave's quarter of the query's window
