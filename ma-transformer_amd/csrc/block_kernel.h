@@ -15,7 +15,10 @@
 // Measured alternatives that did not pay on the 4-wide BASELINE table: a
 // workgroup walking a run of consecutive rows with two blocks in flight
 // (the same time at best, slower with more rows per run), because a row's
-// time is not its load latency alone.
+// time is not its load latency alone; and a row-pipelined walk (all 4
+// blocks of a row in LDS, the next row's loads in flight, 2 workgroups per
+// CU): 65 against 50 us, since a row's dependent MFMA / softmax chain needs
+// the 4 workgroups per CU of this kernel to hide it.
 #pragma once
 
 #include "stream_kernel.h"

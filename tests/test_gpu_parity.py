@@ -209,6 +209,24 @@ def test_block_sparse_many_rows(ext, oracle, width, padded):
     _check_sampled(oracle, spec, up, y, torch.bfloat16, (15, 16), [(0, 4000)])
 
 
+@pytest.mark.parametrize("shape", [
+    (1, 64, 1, 64),     # one row
+    (1, 448, 1, 64),    # 7 rows: fewer than the 8 XCDs
+    (3, 190, 3, 64),    # 27 rows, not a multiple of 8
+    (1, 6400, 11, 64),  # 1100 rows
+])
+def test_block_sparse_every_row(ext, oracle, shape):
+    """Row counts around the XCD renumbering (tables of <= 4 entries): every
+    (batch, head, block) row is computed once.  All rows are checked."""
+    B, N, H, D = shape
+    (q, k, v), up = _inputs(shape, 7000 + N + H, torch.bfloat16, scale=0.5)
+    nb = (N + 63) // 64
+    for tab in (ext.make_block_table(31 + N, nb, min(2, max(nb - 2, 0))).numpy(), _random_table(nb, 4, N)):
+        y = ext.block_sparse_forward(q, k, v, torch.from_numpy(tab), 64)
+        spec = oracle.Spec(*shape, pattern="block_sparse", block_size=64, table=tab)
+        assert _max_err(y, oracle.forward(spec, *up)) <= TOL[torch.bfloat16]
+
+
 def test_block_table_validation(ext):
     q = torch.randn(1, 128, 1, 64, device="cuda", dtype=torch.bfloat16)
     ok = torch.tensor([[0, -1, -1], [0, 1, -1]], dtype=torch.int32)
