@@ -97,6 +97,63 @@ __device__ __forceinline__ void block_update(const uint8_t* slot, uint32_t kl, u
   }
 }
 
+// The same update over two blocks at once (the slot pair at `slots`), one
+// max and one rescale for their 128 keys: the two blocks' eight QK products
+// and then their sixteen P.V products issue back to back, so a row of four
+// blocks is two dependent score -> max -> exp -> P.V chains instead of four.
+// No causal diagonal here (table rows only).
+template <class P>
+__device__ __forceinline__ void block_pair_update(const uint8_t* slots, uint32_t kl, uint32_t vl,
+                                                  const typename P::Q& q, int cb0, int cb1, int N, int g, float sl2,
+                                                  float& m_run, float& l_run, f32x4 (&acc)[4]) {
+  const int cb[2] = {cb0, cb1};
+  f32x4 sc[2][4];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) sc[b][u] = P::qk(slots + b * P::kSlot + P::blk_k(u) + kl, q);
+  const int lk = 4 * g;
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    if (cb[b] < 0 || 64 * cb[b] + 63 >= N) {  // uniform: absent entry or keys past the end
+      const int hi = cb[b] < 0 ? -1 : N - 64 * cb[b] - 1;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) sc[b][u][rr] = lk <= hi - 16 * u - rr ? sc[b][u][rr] : -INFINITY;
+    }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      mx = fmaxf(mx, fmaxf(fmaxf(sc[b][u][0], sc[b][u][1]), fmaxf(sc[b][u][2], sc[b][u][3])));
+  const float m_new = fmaxf(m_run, col_max(mx));
+  const float m_use = m_new == -INFINITY ? 0.0f : m_new * sl2;
+  if (__builtin_amdgcn_ballot_w64(m_new != m_run) != 0) {
+    const float corr = __builtin_amdgcn_exp2f(m_run * sl2 - m_use);  // 0 on a row's first pair
+    l_run *= corr;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) acc[dt] *= corr;
+  }
+  m_run = m_new;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int u = 0; u < 4; u += 2) {
+      float p0[4], p1[4];
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        p0[rr] = __builtin_amdgcn_exp2f(fmaf(sc[b][u][rr], sl2, -m_use));
+        p1[rr] = __builtin_amdgcn_exp2f(fmaf(sc[b][u + 1][rr], sl2, -m_use));
+        l_run += p0[rr] + p1[rr];
+      }
+      const uint8_t* slot = slots + b * P::kSlot;
+      P::pv2(slot + P::blk_v(u) + vl, slot + P::blk_v(u + 1) + vl, p0, p1, acc);
+    }
+}
+
 template <class P>
 __global__ __launch_bounds__(256, P::kMinBlocks) void block_row_kernel(BlockArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 block buffers of P::kBlk bytes
@@ -160,15 +217,14 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void block_row_kernel(BlockArgs
       P::store_slot(x[0], ring, tid);
       P::store_slot(x[1], ring + P::kSlot, tid);
       __syncthreads();
-      if (ne > 0) block_update<P>(ring, kl, vl, q, block_of(0), false, ql, N, g, sl2, m_run, l_run, acc);
-      if (ne > 1) block_update<P>(ring + P::kSlot, kl, vl, q, block_of(1), false, ql, N, g, sl2, m_run, l_run, acc);
+      // an absent second entry of a pair is a masked block (its loads read zeros)
+      if (ne > 0) block_pair_update<P>(ring, kl, vl, q, block_of(0), block_of(1), N, g, sl2, m_run, l_run, acc);
       if (ne > 2) {  // uniform
         __syncthreads();
         P::store_slot(x[2], ring, tid);
         P::store_slot(x[3], ring + P::kSlot, tid);
         __syncthreads();
-        block_update<P>(ring, kl, vl, q, block_of(2), false, ql, N, g, sl2, m_run, l_run, acc);
-        if (ne > 3) block_update<P>(ring + P::kSlot, kl, vl, q, block_of(3), false, ql, N, g, sl2, m_run, l_run, acc);
+        block_pair_update<P>(ring, kl, vl, q, block_of(2), block_of(3), N, g, sl2, m_run, l_run, acc);
       }
       const float l_tot = col_sum(l_run);
       P::store_o(acc, l_tot > 0.0f ? __builtin_amdgcn_rcpf(l_tot) : 0.0f, Or, qrow, g);
