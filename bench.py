@@ -78,12 +78,29 @@ WORKLOADS = {
     # the reference's dense_forward dtype (fp32 only there)
     "dense_causal_fp32": (1, 8, 16384, 64, "fp32", dict(pattern="dense", causal=True),
                           "dense causal (keys [0,i]), fp32, B=1 H=8 N=16384 D=64"),
+    # the generic index-set path (explicit key lists, row kernel) on the target's key sets
+    "index_set": (1, 8, 65536, 64, "bf16", dict(pattern="index_set", left=63, right=0),
+                  "the target's causal w=64 key sets given as an explicit index set (CSR), bf16, "
+                  "B=1 H=8 N=65536 D=64"),
 }
+
+
+def window_csr(N: int, left: int, right: int):
+    """CSR (int64 offsets [N+1], int32 keys) of the window [i-left, i+right] n [0,N)."""
+    import numpy as np
+    i = np.arange(N, dtype=np.int64)
+    lo, hi = np.maximum(i - left, 0), np.minimum(i + right, N - 1)
+    offsets = np.zeros(N + 1, dtype=np.int64)
+    offsets[1:] = np.cumsum(hi - lo + 1)
+    keys = (np.repeat(lo - offsets[:-1], hi - lo + 1) + np.arange(offsets[-1])).astype(np.int32)
+    return offsets, keys
 
 
 def key_count(N: int, pk: dict) -> int:
     """sum_i |S_i| for one (b, h) -- closed forms of the index sets."""
     p = pk["pattern"]
+    if p == "index_set":  # built as a window
+        p = "sliding"
     if p == "sliding":
         dil = pk.get("dilation", 1)
         total = 0
@@ -138,9 +155,13 @@ def cpu_baseline(B, H, N, D, dtype, pk, budget_s=12.0):
     if pk["pattern"] == "block_sparse":
         nb = (N + pk["block_size"] - 1) // pk["block_size"]
         table = O.block_table(pk["seed"], nb, pk["extra"])
+    offsets = keys = None
+    if pk["pattern"] == "index_set":
+        offsets, keys = window_csr(N, pk["left"], pk["right"])
     spec = O.Spec(B, N, H, D, pattern=pk["pattern"], left=pk.get("left", 0), right=pk.get("right", 0),
                   dilation=pk.get("dilation", 1), block_size=pk.get("block_size", 64), table=table,
-                  num_global=pk.get("num_global", 0), causal=pk.get("causal", False))
+                  num_global=pk.get("num_global", 0), causal=pk.get("causal", False),
+                  offsets=offsets, keys=keys)
     # time one head first, then as many whole heads as fit the budget
     t0 = time.perf_counter()
     O.forward(spec, q, k, v, heads=(0, 1))
@@ -332,6 +353,10 @@ def main() -> int:
         launch = lambda s: ext.block_sparse_forward(s[0], s[1], s[2], table, pk["block_size"])
     elif pk["pattern"] == "dense":
         launch = lambda s: ext.dense_forward(s[0], s[1], s[2], pk["causal"])
+    elif pk["pattern"] == "index_set":
+        offsets, keys = window_csr(N, pk["left"], pk["right"])
+        iset = ext.IndexSet(torch.from_numpy(offsets), torch.from_numpy(keys), N, dev)
+        launch = lambda s: ext.index_set_forward(s[0], s[1], s[2], iset)
     else:
         launch = lambda s: ext.longformer_forward(s[0], s[1], s[2], pk["left"], pk["right"], pk["num_global"])
 
@@ -372,6 +397,8 @@ def main() -> int:
 
     queries = B * H * N
     alg_bytes = tensors * B * N * H * D * elt
+    if pk["pattern"] == "index_set":  # plus the key lists, read once
+        alg_bytes += 8 * (N + 1) + 4 * key_count(N, pk)
     # forward: Q.K^T and P.V; backward: S, dP = dO.V^T, dV, dQ, dK (2 FLOP per MAC)
     flops = (10 if bwd else 4) * D * key_count(N, pk) * B * H
     achieved_gbps = alg_bytes / (mean_launch_ms * 1e-3) / 1e9

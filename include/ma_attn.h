@@ -19,6 +19,13 @@
  *   LONGFORMER   i <  num_global: [0, N)
  *                i >= num_global: { i - left .. i + right } U [0, num_global)
  *                (set union, every key once)
+ *   INDEX_SET    index_keys[index_offsets[i] .. index_offsets[i+1]): an
+ *                explicit key set per query row (CSR), shared by every
+ *                (batch, head), as the reference's generic COO attention
+ *                (src/csrc/sparse_attention.cpp:11-152) takes one pattern for
+ *                all of them.  Keys ascending and distinct within a row: the
+ *                reference path exponentiates a repeated entry twice
+ *                (:98-108); here a key set is a set.
  * An empty S_i gives an all-zero output row (src/csrc/ma_core.cpp:212).
  *
  * Return codes: 0 on success, non-zero on invalid input or launch failure;
@@ -45,7 +52,8 @@ enum ma_attn_pattern {
   MA_ATTN_SLIDING = 0,
   MA_ATTN_DENSE = 1,
   MA_ATTN_BLOCK_SPARSE = 2,
-  MA_ATTN_LONGFORMER = 3
+  MA_ATTN_LONGFORMER = 3,
+  MA_ATTN_INDEX_SET = 4
 };
 
 typedef struct ma_attn_desc {
@@ -67,6 +75,11 @@ typedef struct ma_attn_desc {
   int64_t num_global;         /* LONGFORMER: global tokens at positions 0..G-1 */
   float scale;                /* softmax scale; 0 => 1.0f / sqrtf((float)head_dim) */
   int32_t reserved1;
+  const int64_t* index_offsets; /* INDEX_SET: device int64 [seq_len + 1], non-decreasing,
+                                   index_offsets[0] = 0, index_offsets[seq_len] = num_indices */
+  const int32_t* index_keys;    /* INDEX_SET: device int32 [num_indices], each row's keys
+                                   ascending and distinct, in [0, seq_len) */
+  int64_t num_indices;          /* INDEX_SET: length of index_keys */
 } ma_attn_desc;
 
 /*
@@ -78,7 +91,11 @@ typedef struct ma_attn_desc {
  *   ma_core::compute_sparse_attention  src/csrc/ma_core.cpp:160-246
  *   ma_core::compute_dense_attention   src/csrc/ma_core.cpp:66-157,
  * and gives the block-sparse / Longformer patterns of
- *   src/csrc/sparse_attention.cpp:203-259 a working forward.
+ *   src/csrc/sparse_attention.cpp:203-259 and the generic index-set attention
+ *   of :11-152 (INDEX_SET) a working forward.  INDEX_SET reads its offsets
+ *   and keys as given, with every access kept inside them: a row's offsets
+ *   are clamped into [0, num_indices] and keys outside [0, seq_len) are
+ *   skipped, so malformed sets give wrong rows, never a fault.
  * workspace: device memory of ma_attn_workspace_size(desc) bytes (may be NULL
  * when that size is 0).  stream: a hipStream_t (NULL = default stream).
  */
@@ -152,8 +169,9 @@ int ma_attn_block_table(uint64_t seed, int64_t num_blocks,
 /*
  * Host: the ascending key list S_i of query row i for desc (block_table, if
  * used, is a HOST pointer here).  Writes min(|S_i|, cap) keys to keys_out and
- * returns |S_i|, or -1 on invalid input.  The same closed forms drive the
- * kernels; this exposes them for bit-exact index checks.  Replaces the COO
+ * returns |S_i|, or -1 on invalid input (INDEX_SET included: its sets are
+ * the caller's own input).  The same closed forms drive the kernels; this
+ * exposes them for bit-exact index checks.  Replaces the COO
  * generators create_sliding_window_pattern (src/csrc/ma_core.cpp:34-48) and
  * SlidingWindow/Longformer generate_sparse_pattern
  * (src/csrc/sparse_attention.cpp:181-259).
@@ -164,7 +182,7 @@ int64_t ma_attn_row_keys(const ma_attn_desc* desc, const int32_t* host_block_tab
 /* ABI version of this header (bumped on incompatible change). */
 int ma_attn_abi_version(void);
 
-#define MA_ATTN_ABI_VERSION 3
+#define MA_ATTN_ABI_VERSION 4
 
 #ifdef __cplusplus
 }

@@ -8,10 +8,12 @@
 //                    major, V transposed) and both contractions run on MFMA
 //                    (16x16x32 for Q.K^T, 16x16x16 for P.V) with an online
 //                    softmax held in registers.  One O store per row.
+//   gather_rows_kernel<T>  head_dim 64, any key set (index sets among them)
+//                    the tiled kernels do not take: one wave per query row,
+//                    8 whole K or V rows per load instruction.
 //   rows_kernel<T>   every pattern / dtype / head_dim <= 512: one wave per
 //                    query row, lanes over keys for the scores, lanes over
-//                    head_dim for P.V.  Used where the tiled kernel does not
-//                    apply.
+//                    head_dim for P.V.  Used where no other kernel applies.
 //
 // Semantics follow ma_core::compute_sparse_attention
 // (/root/reference src/csrc/ma_core.cpp:160-246): softmax over the row's key
@@ -159,8 +161,10 @@ __global__ __launch_bounds__(256) void rows_kernel(const T* __restrict__ q, cons
 
   for (int64_t c0 = 0; c0 < cnt; c0 += 64) {
     const int64_t t = c0 + lane;
-    const bool valid = t < cnt;
-    const int64_t j = valid ? ma::key_at(pp, rk, i, t) : 0;
+    const int64_t jk0 = t < cnt ? ma::key_at(pp, rk, i, t) : -1;
+    // closed-form keys are always in range; an index set's are checked here
+    const bool valid = jk0 >= 0 && jk0 < N;
+    const int64_t j = valid ? jk0 : 0;
     float s = -INFINITY;
     if (valid) {
       const T* kr = kb + j * rs;
@@ -168,9 +172,11 @@ __global__ __launch_bounds__(256) void rows_kernel(const T* __restrict__ q, cons
       for (int64_t d = 0; d < D; ++d) dot = fmaf(qw[d], ld_f(kr + d), dot);
       s = dot * scale;
     }
-    const float mn = fmaxf(m, wave_max(s));  // finite: lane 0 is valid
-    const float corr = expf(m - mn);
-    const float p = valid ? expf(s - mn) : 0.0f;
+    // mn is -inf only while every key so far was skipped (index sets)
+    const float mn = fmaxf(m, wave_max(s));
+    const float mu = mn == -INFINITY ? 0.0f : mn;
+    const float corr = expf(m - mu);
+    const float p = valid ? expf(s - mu) : 0.0f;
     l = l * corr + wave_sum(p);
 #pragma unroll
     for (int c = 0; c < DPL; ++c) acc[c] *= corr;
@@ -187,7 +193,7 @@ __global__ __launch_bounds__(256) void rows_kernel(const T* __restrict__ q, cons
     }
     m = mn;
   }
-  const float inv = cnt > 0 ? 1.0f / l : 0.0f;
+  const float inv = cnt > 0 && l != 0.0f ? 1.0f / l : 0.0f;
   if constexpr (STATS) {
     float part = 0.0f;
 #pragma unroll
@@ -748,6 +754,9 @@ ma::PatternParams params_of(const ma_attn_desc* d, const int32_t* table) {
   p.table = table;
   p.bpr = d->blocks_per_row;
   p.num_global = d->num_global;
+  p.offsets = d->index_offsets;
+  p.keys = d->index_keys;
+  p.nnz = d->num_indices;
   return p;
 }
 
@@ -774,6 +783,11 @@ int validate(const ma_attn_desc* d) {
       break;
     case MA_ATTN_LONGFORMER:
       if (d->num_global < 0) return fail("ma_attn: num_global must be >= 0");
+      break;
+    case MA_ATTN_INDEX_SET:
+      if (d->num_indices < 0) return fail("ma_attn: num_indices must be >= 0");
+      if (!d->index_offsets && d->seq_len > 0) return fail("ma_attn: index_offsets is null");
+      if (!d->index_keys && d->num_indices > 0) return fail("ma_attn: index_keys is null");
       break;
     default:
       return fail("ma_attn: unknown pattern %d", d->pattern);
@@ -815,6 +829,170 @@ int launch_rows(const ma_attn_desc* d, const void* q, const void* k, const void*
   else
     MA_ROWS(8);
 #undef MA_ROWS
+  return 0;
+}
+
+// ------------------------------------------------------------------ gather_rows_kernel
+//
+// Head_dim 64, any key set (explicit index sets, and the patterns the tiled
+// kernels do not take), with every gather a whole-row read.  A wave takes 4
+// query rows (consecutive positions of one head), 16 lanes each: rows in
+// flight hide the dependent offsets ->
+// keys -> K -> V round trips, which bound this kernel.  Lane (r =
+// (lane>>2)&3, c = lane&3) of a row holds head_dim 16c .. 16c+15 of the
+// query.  A 32-key chunk is 8 passes of 4 keys, key 4*pass + r in pass
+// `pass`: each pass reads 4 whole K rows per query row and sums the 4 partial
+// dots of a key across its lanes; after the chunk's max the same keys' V rows
+// go into the lane's 16 accumulators.  The 4 key slots' accumulators are added
+// across lanes at the end and lanes with r = 0 write the row.
+template <typename T>
+__device__ __forceinline__ void unpack8(const T* p, float (&x)[8]) {
+  if constexpr (sizeof(T) == 4) {
+    const uint4 a = *reinterpret_cast<const uint4*>(p);
+    const uint4 b = *reinterpret_cast<const uint4*>(p + 4);
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = __uint_as_float(w[e]);
+  } else {
+    const uint4 a = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = static_cast<float>(__builtin_bit_cast(T, (uint16_t)(w[e] & 0xffffu)));
+      x[2 * e + 1] = static_cast<float>(__builtin_bit_cast(T, (uint16_t)(w[e] >> 16)));
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void gather_rows_kernel(const T* __restrict__ q, const T* __restrict__ k,
+                                                          const T* __restrict__ v, T* __restrict__ o, int64_t B,
+                                                          int64_t H, ma::PatternParams pp, float scale) {
+  constexpr int D = 64;
+  constexpr int QPW = 4;  // query rows per wave (16 lanes each)
+  constexpr int NP = 8;   // passes per chunk, 4 keys per pass (16: 680 vs 575 us, fewer waves)
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int qs = lane >> 4;        // the lane's query row in the wave
+  const int r4 = (lane >> 2) & 3;  // key slot in a pass
+  const int c4 = lane & 3;         // head_dim 16*c4 .. 16*c4+15
+  const int64_t N = pp.n;
+  // A workgroup takes 16 consecutive positions of one (batch, head), so the
+  // neighbouring queries' key rows meet in one L1; XCD x takes the x-th
+  // eighth of the workgroups, so a head's key rows stay in one L2.
+  const int64_t nblk = (N + 15) / 16;
+  const int64_t g = xcd_row_order((int)blockIdx.x, (int)gridDim.x);
+  const int64_t bh = g / nblk;
+  const int64_t i0 = (g % nblk) * 16 + wv * QPW;  // the wave's first position
+  if (i0 >= N) return;                             // uniform; no barrier in this kernel
+  const int64_t b = bh / H;
+  const int64_t h = bh % H;
+  const int64_t ip = i0 + qs;
+  const bool row_ok = ip < N;
+  const int64_t i = row_ok ? ip : i0;
+  const int64_t rr = (b * N + i) * H + h;
+  const int64_t rs = H * D;  // elements between consecutive tokens
+
+  float qv[16];
+  {
+    float x[8];
+    unpack8(q + rr * D + 16 * c4, x);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qv[e] = x[e];
+    unpack8(q + rr * D + 16 * c4 + 8, x);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qv[8 + e] = x[e];
+  }
+  const T* kb = k + (b * N * H + h) * D + 16 * c4;
+  const T* vb = v + (b * N * H + h) * D + 16 * c4;
+  const ma::RowKeys rk = ma::row_keys(pp, i);
+  const int64_t cnt = row_ok ? rk.count : 0;
+  int64_t cmax = cnt;  // the wave walks as many chunks as its longest row needs
+#pragma unroll
+  for (int sh = 16; sh <= 32; sh <<= 1) cmax = ma::imax64(cmax, (int64_t)__shfl_xor((long long)cmax, sh, 64));
+
+  float m = -INFINITY, l = 0.0f;
+  float acc[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+
+  for (int64_t c0 = 0; c0 < cmax; c0 += 4 * NP) {
+    float s[NP];
+    int32_t j[NP];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int ps = 0; ps < NP; ++ps) {
+      const int64_t t = c0 + 4 * ps + r4;
+      const int64_t jk = t < cnt ? ma::key_at(pp, rk, i, t) : -1;
+      const bool valid = jk >= 0 && jk < N;  // an index set's keys are checked here
+      j[ps] = valid ? (int32_t)jk : -1;
+      const T* kr = kb + (valid ? jk : 0) * rs;
+      float x[8], dot = 0.0f;
+      unpack8(kr, x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dot = fmaf(qv[e], x[e], dot);
+      unpack8(kr + 8, x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dot = fmaf(qv[8 + e], x[e], dot);
+      dot += __shfl_xor(dot, 1, 64);
+      dot += __shfl_xor(dot, 2, 64);
+      s[ps] = valid ? dot * scale : -INFINITY;
+      mx = fmaxf(mx, s[ps]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
+    // mn is -inf only while every key so far was skipped
+    const float mn = fmaxf(m, mx);
+    const float mu = mn == -INFINITY ? 0.0f : mn;
+    const float corr = expf(m - mu);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] *= corr;
+    float ls = 0.0f;
+#pragma unroll
+    for (int ps = 0; ps < NP; ++ps) {
+      if (j[ps] >= 0) {
+        const float p = expf(s[ps] - mu);
+        ls += p;
+        const T* vr = vb + (int64_t)j[ps] * rs;
+        float x[8];
+        unpack8(vr, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, x[e], acc[e]);
+        unpack8(vr + 8, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[8 + e] = fmaf(p, x[e], acc[8 + e]);
+      }
+    }
+    ls += __shfl_xor(ls, 4, 64);
+    ls += __shfl_xor(ls, 8, 64);
+    l = l * corr + ls;
+    m = mn;
+  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    acc[e] += __shfl_xor(acc[e], 4, 64);
+    acc[e] += __shfl_xor(acc[e], 8, 64);
+  }
+  const float inv = cnt > 0 && l != 0.0f ? 1.0f / l : 0.0f;
+  if (row_ok && r4 == 0) {
+    T* orow = o + rr * D + 16 * c4;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) orow[e] = cvt_out<T>(acc[e] * inv);
+  }
+}
+
+bool gather_applies(const ma_attn_desc* d, const void* q, const void* k, const void* v, const void* o) {
+  return d->head_dim == 64 && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
+}
+
+template <typename T>
+int launch_gather(const ma_attn_desc* d, const void* q, const void* k, const void* v, void* o, hipStream_t st) {
+  // one workgroup per 16 positions of one (batch, head): 4 waves of 4 rows
+  const int64_t blocks = d->batch * d->num_heads * ((d->seq_len + 15) / 16);
+  if (blocks > (int64_t)INT32_MAX) return fail("ma_attn: problem too large for one launch");
+  launch(true, gather_rows_kernel<T>, dim3((unsigned)blocks), dim3(256), 0u, st, static_cast<const T*>(q),
+         static_cast<const T*>(k), static_cast<const T*>(v), static_cast<T*>(o), d->batch, d->num_heads,
+         params_of(d, d->block_table), scale_of(d));
   return 0;
 }
 
@@ -1320,6 +1498,18 @@ int ma_attn_forward(const ma_attn_desc* desc, const void* q, const void* k, cons
     rc = launch_block(desc, q, k, v, o, st);
   } else if (!want_rows && band_applies(desc, q, k, v, o)) {
     rc = launch_band(desc, q, k, v, o, st);
+  } else if (!want_rows && gather_applies(desc, q, k, v, o)) {
+    switch (desc->dtype) {
+      case MA_ATTN_F32:
+        rc = launch_gather<float>(desc, q, k, v, o, st);
+        break;
+      case MA_ATTN_BF16:
+        rc = launch_gather<__bf16>(desc, q, k, v, o, st);
+        break;
+      default:
+        rc = launch_gather<_Float16>(desc, q, k, v, o, st);
+        break;
+    }
   } else if (!want_rows && narrow_applies(desc)) {
     switch (desc->dtype) {
       case MA_ATTN_F32:
@@ -1508,6 +1698,10 @@ int64_t ma_attn_row_keys(const ma_attn_desc* desc, const int32_t* host_block_tab
   if (validate(desc)) return -1;
   if (desc->pattern == MA_ATTN_BLOCK_SPARSE && !host_block_table) {
     fail("ma_attn_row_keys: block table required");
+    return -1;
+  }
+  if (desc->pattern == MA_ATTN_INDEX_SET) {
+    fail("ma_attn_row_keys: an index set's keys are the caller's own input");
     return -1;
   }
   const ma::PatternParams pp = params_of(desc, host_block_table);

@@ -15,6 +15,10 @@
 //                entries c >= 0 (ascending), cf. sparse_attention.cpp:203-231
 //   LONGFORMER   i < G: [0,N); else [0,G) U [max(i-left,G), min(i+right,N-1)]
 //                (sparse_attention.cpp:234-259 without its duplicate entries)
+//   INDEX_SET    keys[offsets[i] .. offsets[i+1]) (CSR, one pattern for all
+//                (batch, head), as the generic COO attention of
+//                sparse_attention.cpp:11-152); the row range is clamped into
+//                [0, nnz], so any offsets array reads inside the key array
 #pragma once
 
 #include <stdint.h>
@@ -27,7 +31,7 @@
 
 namespace ma {
 
-enum Pattern : int32_t { kSliding = 0, kDense = 1, kBlockSparse = 2, kLongformer = 3 };
+enum Pattern : int32_t { kSliding = 0, kDense = 1, kBlockSparse = 2, kLongformer = 3, kIndexSet = 4 };
 
 struct PatternParams {
   int64_t n;         // sequence length
@@ -38,6 +42,9 @@ struct PatternParams {
   const int32_t* table;  // host or device pointer, matching the caller
   int64_t bpr;           // table width
   int64_t num_global;
+  const int64_t* offsets;  // INDEX_SET: [n + 1] row offsets into keys
+  const int32_t* keys;     // INDEX_SET: [nnz] key positions
+  int64_t nnz;
 };
 
 MA_HD int64_t imin64(int64_t a, int64_t b) { return a < b ? a : b; }
@@ -50,7 +57,8 @@ MA_HD int64_t floordiv64(int64_t a, int64_t d) {
 }
 
 // A row's key set as up to two arithmetic segments (SLIDING, DENSE,
-// LONGFORMER) or a table walk (BLOCK_SPARSE).
+// LONGFORMER), a table walk (BLOCK_SPARSE) or a slice of the key array
+// (INDEX_SET: keys[start0 + t]).
 struct RowKeys {
   int64_t count;
   // segment 0: keys start0 + step0 * t for t < len0
@@ -109,6 +117,14 @@ MA_HD RowKeys row_keys(const PatternParams& p, int64_t i) {
       }
       break;
     }
+    case kIndexSet: {
+      const int64_t lo = imin64(imax64(p.offsets[i], 0), p.nnz);
+      const int64_t hi = imin64(imax64(p.offsets[i + 1], lo), p.nnz);
+      r.count = hi - lo;
+      r.start0 = lo;
+      r.len0 = r.count;
+      break;
+    }
     default:
       r.count = -1;
   }
@@ -131,6 +147,7 @@ MA_HD int64_t block_key(const PatternParams& p, int64_t i, int64_t t) {
 // t-th key (0 <= t < rk.count) of row i.
 MA_HD int64_t key_at(const PatternParams& p, const RowKeys& rk, int64_t i, int64_t t) {
   if (p.pattern == kBlockSparse) return block_key(p, i, t);
+  if (p.pattern == kIndexSet) return p.keys[rk.start0 + t];
   return t < rk.len0 ? rk.start0 + rk.step0 * t : rk.start1 + (t - rk.len0);
 }
 

@@ -23,8 +23,10 @@ part of this package).
 
 New, keyword-only constructor arguments select the BASELINE patterns and
 default to the reference behaviour: ``pattern`` ("sliding", "dense",
-"block_sparse", "longformer"), ``causal``, ``window_left``, ``window_right``,
-``dilation``, ``block_size``, ``block_table``, ``num_global_tokens``.
+"block_sparse", "longformer", "index_set"), ``causal``, ``window_left``,
+``window_right``, ``dilation``, ``block_size``, ``block_table``,
+``num_global_tokens``, ``index_set`` (an explicit key set per query row: a
+``sparse_attention_cuda.IndexSet`` or an (offsets, keys) CSR pair).
 """
 from __future__ import annotations
 
@@ -65,7 +67,7 @@ except ImportError:  # pragma: no cover - depends on the environment
 class PatternSpec:
     """A resolved index-set choice (see include/ma_attn.h for the sets)."""
 
-    pattern: str = "sliding"       # sliding | dense | block_sparse | longformer
+    pattern: str = "sliding"       # sliding | dense | block_sparse | longformer | index_set
     left: int = 64
     right: int = 64
     dilation: int = 1
@@ -73,6 +75,12 @@ class PatternSpec:
     block_size: int = 64
     block_table: Optional[torch.Tensor] = None
     num_global: int = 0
+    index_set: Optional[object] = None  # IndexSet or (offsets, keys)
+
+    def _csr(self, device):
+        s = self.index_set
+        off, keys = (s.offsets, s.keys[:s.num_indices]) if hasattr(s, "offsets") else s
+        return (torch.as_tensor(off, device=device).long(), torch.as_tensor(keys, device=device).long())
 
     def mask(self, N: int, device) -> torch.Tensor:
         """[N, N] boolean membership mask (for the PyTorch paths)."""
@@ -95,6 +103,12 @@ class PatternSpec:
             G = self.num_global
             local = (j >= i - self.left) & (j <= i + self.right)
             return (i < G) | (j < G) | local
+        if self.pattern == "index_set":
+            off, keys = self._csr(device)
+            rows = torch.repeat_interleave(torch.arange(N, device=device), off[1:] - off[:-1])
+            m = torch.zeros(N, N, dtype=torch.bool, device=device)
+            m[rows, keys] = True
+            return m
         raise ValueError(f"unknown pattern {self.pattern}")
 
 
@@ -113,6 +127,8 @@ def _native_forward(q, k, v, sparse, window_size, use_causal_mask, spec: Optiona
         return ext.block_sparse_forward(cq, ck, cv, spec.block_table, spec.block_size)
     if spec.pattern == "longformer":
         return ext.longformer_forward(cq, ck, cv, spec.left, spec.right, spec.num_global)
+    if spec.pattern == "index_set":
+        return ext.index_set_forward(cq, ck, cv, spec.index_set)
     raise ValueError(f"unknown pattern {spec.pattern}")
 
 
@@ -264,7 +280,7 @@ def pytorch_sparse_attention(query: torch.Tensor, key: torch.Tensor, value: torc
     return torch.cat(out, dim=1).contiguous()
 
 
-_PATTERNS = ("sliding", "dense", "block_sparse", "longformer")
+_PATTERNS = ("sliding", "dense", "block_sparse", "longformer", "index_set")
 
 
 class MACoreAttention(nn.Module):
@@ -280,7 +296,8 @@ class MACoreAttention(nn.Module):
                  pattern: Optional[str] = None, causal: bool = False,
                  window_left: Optional[int] = None, window_right: Optional[int] = None,
                  dilation: int = 1, block_size: int = 64,
-                 block_table: Optional[torch.Tensor] = None, num_global_tokens: int = 0):
+                 block_table: Optional[torch.Tensor] = None, num_global_tokens: int = 0,
+                 index_set: Optional[object] = None):
         super().__init__()
         self.sparse = sparse
         if self.sparse:
@@ -292,9 +309,9 @@ class MACoreAttention(nn.Module):
         self.use_causal_mask = use_causal_mask
         self.fallback_training = fallback_training
         self.spec = self._resolve(pattern, causal, window_left, window_right, dilation,
-                                  block_size, block_table, num_global_tokens)
+                                  block_size, block_table, num_global_tokens, index_set)
 
-    def _resolve(self, pattern, causal, left, right, dilation, block_size, table, num_global):
+    def _resolve(self, pattern, causal, left, right, dilation, block_size, table, num_global, index_set):
         if pattern is None and not causal and left is None and right is None and dilation == 1:
             return None  # reference behaviour
         pattern = pattern or ("sliding" if self.sparse else "dense")
@@ -312,12 +329,14 @@ class MACoreAttention(nn.Module):
             if table is None:
                 raise ValueError("block_sparse pattern needs block_table")
             table = torch.as_tensor(table, dtype=torch.int32)
+        if pattern == "index_set" and index_set is None:
+            raise ValueError("index_set pattern needs index_set")
         if pattern == "dense":
             causal = causal or self.use_causal_mask
         return PatternSpec(pattern=pattern, left=int(left or 0), right=int(right or 0),
                            dilation=int(dilation), causal=bool(causal),
                            block_size=int(block_size), block_table=table,
-                           num_global=int(num_global))
+                           num_global=int(num_global), index_set=index_set)
 
     def forward(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor) -> torch.Tensor:
         if query.dim() != 4 or key.dim() != 4 or value.dim() != 4:

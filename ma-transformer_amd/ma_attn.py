@@ -17,8 +17,8 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("MA_ATTN_LIB", os.path.join(_HERE, "libma_attn.so"))
 
 F32, BF16, F16 = 0, 1, 2
-SLIDING, DENSE, BLOCK_SPARSE, LONGFORMER = 0, 1, 2, 3
-ABI_VERSION = 3
+SLIDING, DENSE, BLOCK_SPARSE, LONGFORMER, INDEX_SET = 0, 1, 2, 3, 4
+ABI_VERSION = 4
 
 DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 
@@ -44,6 +44,9 @@ class Desc(ctypes.Structure):
         ("num_global", ctypes.c_int64),
         ("scale", ctypes.c_float),
         ("reserved1", ctypes.c_int32),
+        ("index_offsets", ctypes.c_void_p),
+        ("index_keys", ctypes.c_void_p),
+        ("num_indices", ctypes.c_int64),
     ]
 
 
@@ -93,7 +96,7 @@ def last_error() -> str:
 
 def make_desc(B, N, H, D, dtype_code, pattern, left=0, right=0, dilation=1, causal=False,
               block_size=64, block_table_ptr=0, blocks_per_row=0, num_global=0,
-              scale=0.0) -> Desc:
+              scale=0.0, index_offsets_ptr=0, index_keys_ptr=0, num_indices=0) -> Desc:
     d = Desc()
     d.batch, d.seq_len, d.num_heads, d.head_dim = int(B), int(N), int(H), int(D)
     d.dtype, d.pattern = int(dtype_code), int(pattern)
@@ -104,6 +107,9 @@ def make_desc(B, N, H, D, dtype_code, pattern, left=0, right=0, dilation=1, caus
     d.blocks_per_row = int(blocks_per_row)
     d.num_global = int(num_global)
     d.scale = float(scale)
+    d.index_offsets = int(index_offsets_ptr) or None
+    d.index_keys = int(index_keys_ptr) or None
+    d.num_indices = int(num_indices)
     return d
 
 
@@ -182,4 +188,4 @@ def default_scale(D: int) -> float:
 
 __all__ = ["LIB", "Desc", "make_desc", "forward_raw", "validate", "workspace_size",
            "block_table", "row_keys", "last_error", "DTYPES", "default_scale",
-           "SLIDING", "DENSE", "BLOCK_SPARSE", "LONGFORMER", "F32", "BF16", "F16"]
+           "SLIDING", "DENSE", "BLOCK_SPARSE", "LONGFORMER", "INDEX_SET", "F32", "BF16", "F16"]

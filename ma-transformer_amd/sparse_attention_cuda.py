@@ -21,6 +21,8 @@ New pattern entry points (not in the reference):
     BlockTable(block_table, seq_len, block_size=64)   (checked once, on the device)
     longformer_forward(q, k, v, left, right=0, num_global=16)
     make_block_table(seed, num_blocks, random_per_row=2)
+    index_set_forward(q, k, v, index_set)              (explicit key set per query row)
+    IndexSet(offsets, keys, seq_len), IndexSet.from_coo(rows, cols, seq_len)
 
 Forward and backward are hand-written HIP kernels (libma_attn.so).  The
 backward recomputes the softmax from q, k, v as the reference's does, for the
@@ -38,7 +40,7 @@ import ma_attn as _ma
 
 __all__ = ["forward", "dense_forward", "backward", "dense_backward", "sliding_forward",
            "sliding_backward", "block_sparse_forward", "longformer_forward", "make_block_table",
-           "BlockTable"]
+           "BlockTable", "IndexSet", "index_set_forward"]
 
 
 def _check(*ts: torch.Tensor) -> None:
@@ -247,6 +249,84 @@ def longformer_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tens
     """Rows i < G attend all keys; others attend [i-left, i+right] U [0, G)."""
     return _launch(query, key, value, _ma.LONGFORMER, left=int(left), right=int(right),
                    num_global=int(num_global))
+
+
+def _validated_index_set(offsets, keys, seq_len: int):
+    """Host int64 offsets and int32 keys after the layout checks of an index set:
+    offsets [S+1] non-decreasing from 0 to len(keys); keys in [0, S), strictly
+    ascending within each row."""
+    if not isinstance(offsets, torch.Tensor) or not isinstance(keys, torch.Tensor):
+        raise RuntimeError("index set offsets and keys must be tensors")
+    off = offsets.detach().to("cpu", torch.int64).contiguous()
+    kk = keys.detach().to("cpu", torch.int64).contiguous()
+    N = int(seq_len)
+    if off.dim() != 1 or off.numel() != N + 1:
+        raise RuntimeError(f"index set offsets must be [S+1={N + 1}]")
+    if kk.dim() != 1:
+        raise RuntimeError("index set keys must be 1-D")
+    nnz = kk.numel()
+    if int(off[0]) != 0 or int(off[-1]) != nnz or bool((off[1:] < off[:-1]).any()):
+        raise RuntimeError("index set offsets must run non-decreasing from 0 to len(keys)")
+    if nnz and (bool((kk < 0).any()) or bool((kk >= N).any())):
+        raise RuntimeError(f"index set keys must lie in [0, S={N})")
+    if nnz > 1:
+        bad = kk[1:] <= kk[:-1]
+        starts = off[1:N]
+        starts = starts[(starts > 0) & (starts < nnz)]
+        bad[starts - 1] = False  # a new row may restart low
+        if bool(bad.any()):
+            raise RuntimeError("index set rows must be strictly ascending (each key once)")
+    return off, kk.to(torch.int32)
+
+
+class IndexSet:
+    """An explicit key set per query row (CSR), checked once and kept on the device.
+
+    Row i attends keys[offsets[i]:offsets[i+1]] in every (batch, head): the
+    reference's generic COO attention (src/csrc/sparse_attention.cpp:11-152)
+    with one pattern for all of them.  ``from_coo`` takes the reference's
+    (row, col) entry lists and drops repeated entries.
+    """
+
+    def __init__(self, offsets: torch.Tensor, keys: torch.Tensor, seq_len: int, device=None):
+        self.seq_len = int(seq_len)
+        off, kk = _validated_index_set(offsets, keys, self.seq_len)
+        dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self.offsets = off.to(dev)
+        self.keys = (kk if kk.numel() else torch.zeros(1, dtype=torch.int32)).to(dev)
+        self.num_indices = int(kk.numel())
+
+    @staticmethod
+    def from_coo(rows, cols, seq_len: int, device=None) -> "IndexSet":
+        r = torch.as_tensor(rows, dtype=torch.int64).reshape(-1)
+        c = torch.as_tensor(cols, dtype=torch.int64).reshape(-1)
+        N = int(seq_len)
+        if r.numel() != c.numel():
+            raise RuntimeError("rows and cols must have the same length")
+        if r.numel() and (bool((r < 0).any()) or bool((r >= N).any())):
+            raise RuntimeError(f"rows must lie in [0, S={N})")
+        pairs = torch.unique(r * max(N, 1) + c) if r.numel() else r  # sorted by (row, col), repeats dropped
+        rr, cc = pairs // max(N, 1), pairs % max(N, 1)
+        offsets = torch.zeros(N + 1, dtype=torch.int64)
+        offsets[1:] = torch.cumsum(torch.bincount(rr, minlength=N)[:N], 0)
+        return IndexSet(offsets, cc, N, device)
+
+
+def index_set_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                      index_set) -> torch.Tensor:
+    """Query i attends exactly the keys of row i of index_set (an IndexSet, or
+    an (offsets, keys) pair checked at every call).  Empty rows give zeros."""
+    _check(query, key, value)
+    B, N, H, D = query.shape
+    if not isinstance(index_set, IndexSet):
+        offsets, keys = index_set
+        index_set = IndexSet(offsets, keys, N, query.device)
+    if index_set.seq_len != N:
+        raise RuntimeError(f"IndexSet was made for S={index_set.seq_len}; called with S={N}")
+    if index_set.offsets.device != query.device:
+        raise RuntimeError("IndexSet is on another device than the inputs")
+    return _launch(query, key, value, _ma.INDEX_SET, index_offsets_ptr=index_set.offsets.data_ptr(),
+                   index_keys_ptr=index_set.keys.data_ptr(), num_indices=index_set.num_indices)
 
 
 # ---------------------------------------------------------------- backward (HIP kernels)

@@ -37,6 +37,15 @@
  *   3 LONGFORMER   i < G: [0,N); else [i-left, i+right] U [0,G), no duplicates
  *                  (intent of sparse_attention.cpp:234-259 and
  *                   whitepaper :109-124)
+ *   4 INDEX_SET    keys[offsets[i] .. offsets[i+1]) given by the caller (CSR),
+ *                  every key once and ascending: the generic COO attention of
+ *                  sparse_attention.cpp:11-152 over a set.  That path scales
+ *                  Q before the dot product (:25-26) where ma_core scales the
+ *                  dot (:209); with D a power of 4 the scale is a power of two
+ *                  and the two orders give the same bits.  Its one-pattern-
+ *                  for-all-heads rule is kept; its double exponentiation of a
+ *                  repeated entry (:98-108) is not: repeated or unsorted keys
+ *                  are rejected (-1).
  */
 #include <math.h>
 #include <stdint.h>
@@ -52,6 +61,9 @@ typedef struct oracle_spec {
   const int32_t* table; /* host, [ceil(N/bs), bpr] */
   int64_t bpr;
   int64_t num_global;
+  const int64_t* offsets; /* INDEX_SET: host [N+1] */
+  const int32_t* keys;    /* INDEX_SET: host [nnz] */
+  int64_t nnz;
 } oracle_spec;
 
 static int64_t imax(int64_t a, int64_t b) { return a > b ? a : b; }
@@ -113,11 +125,36 @@ int64_t oracle_row_keys(const oracle_spec* s, int64_t i, int64_t* out, int64_t c
       }
       break;
     }
+    case 4: { /* INDEX_SET */
+      const int64_t a = s->offsets[i], b = s->offsets[i + 1];
+      if (a < 0 || b < a || b > s->nnz) return -1;
+      for (int64_t t = a; t < b; ++t) {
+        const int64_t j = s->keys[t];
+        if (j < 0 || j >= N || (t > a && j <= s->keys[t - 1])) return -1;
+        PUSH(j);
+      }
+      break;
+    }
     default:
       return -1;
   }
 #undef PUSH
   return n;
+}
+
+/* INDEX_SET well-formed: offsets from 0 to nnz, non-decreasing; each row's
+ * keys strictly ascending inside [0,N).  Other patterns: always 1. */
+static int index_set_ok(const oracle_spec* s) {
+  if (s->pattern != 4) return 1;
+  if (s->N > 0 && (!s->offsets || s->offsets[0] != 0 || s->offsets[s->N] != s->nnz)) return 0;
+  if (s->nnz > 0 && !s->keys) return 0;
+  for (int64_t i = 0; i < s->N; ++i) {
+    const int64_t a = s->offsets[i], b = s->offsets[i + 1];
+    if (b < a) return 0;
+    for (int64_t t = a; t < b; ++t)
+      if (s->keys[t] < 0 || s->keys[t] >= s->N || (t > a && s->keys[t] <= s->keys[t - 1])) return 0;
+  }
+  return 1;
 }
 
 /*
@@ -128,7 +165,7 @@ int oracle_forward_f32(const oracle_spec* s, const float* q, const float* k,
                        const float* v, float* o, int64_t h_lo, int64_t h_hi,
                        int64_t i_lo, int64_t i_hi) {
   const int64_t N = s->N, H = s->H, D = s->D;
-  if (N < 0 || H < 0 || D <= 0) return -1;
+  if (N < 0 || H < 0 || D <= 0 || !index_set_ok(s)) return -1;
   const float scale = 1.0f / sqrtf((float)D);
   int64_t cap = N > 0 ? N : 1;
   int64_t* keys = (int64_t*)malloc(sizeof(int64_t) * (size_t)cap);
@@ -197,7 +234,7 @@ int oracle_backward_f32(const oracle_spec* s, const float* q, const float* k,
                         const float* v, const float* dout, float* dq, float* dk,
                         float* dv) {
   const int64_t N = s->N, H = s->H, D = s->D, B = s->B;
-  if (N < 0 || H < 0 || D <= 0 || B < 0) return -1;
+  if (N < 0 || H < 0 || D <= 0 || B < 0 || !index_set_ok(s)) return -1;
   const float scale = 1.0f / sqrtf((float)D);
   const int64_t total = B * N * H * D;
   for (int64_t x = 0; x < total; ++x) dq[x] = dk[x] = dv[x] = 0.0f;

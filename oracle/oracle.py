@@ -35,7 +35,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 REF_PATH = os.path.join(HERE, "_ref", "libma_core_ref.so")
 
-PATTERNS = {"sliding": 0, "dense": 1, "block_sparse": 2, "longformer": 3}
+PATTERNS = {"sliding": 0, "dense": 1, "block_sparse": 2, "longformer": 3, "index_set": 4}
 
 
 class _Spec(ctypes.Structure):
@@ -45,6 +45,8 @@ class _Spec(ctypes.Structure):
         ("left", ctypes.c_int64), ("right", ctypes.c_int64), ("dilation", ctypes.c_int64),
         ("block_size", ctypes.c_int64), ("table", ctypes.POINTER(ctypes.c_int32)),
         ("bpr", ctypes.c_int64), ("num_global", ctypes.c_int64),
+        ("offsets", ctypes.POINTER(ctypes.c_int64)), ("keys", ctypes.POINTER(ctypes.c_int32)),
+        ("nnz", ctypes.c_int64),
     ]
 
 
@@ -84,7 +86,8 @@ class Spec:
     """Pattern parameters (same meaning as ma_attn_desc)."""
 
     def __init__(self, B, N, H, D, pattern="sliding", left=0, right=0, dilation=1,
-                 causal=False, block_size=64, table=None, num_global=0):
+                 causal=False, block_size=64, table=None, num_global=0, offsets=None, keys=None):
+        """offsets, keys: the INDEX_SET pattern's CSR rows (int64 [N+1], int32 [nnz])."""
         self.B, self.N, self.H, self.D = int(B), int(N), int(H), int(D)
         self.pattern = pattern
         self.left, self.right, self.dilation = int(left), int(right), int(dilation)
@@ -92,6 +95,8 @@ class Spec:
         self.block_size = int(block_size)
         self.table = None if table is None else np.ascontiguousarray(table, dtype=np.int32)
         self.num_global = int(num_global)
+        self.offsets = None if offsets is None else np.ascontiguousarray(offsets, dtype=np.int64)
+        self.keys = None if keys is None else np.ascontiguousarray(keys, dtype=np.int32)
 
     def _c(self):
         s = _Spec()
@@ -107,6 +112,12 @@ class Spec:
             s.table = ctypes.POINTER(ctypes.c_int32)()
             s.bpr = 0
         s.num_global = self.num_global
+        if self.offsets is not None:
+            s.offsets = self.offsets.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))
+            keys = self.keys if self.keys is not None and self.keys.size else np.zeros(1, np.int32)
+            self._keys_c = keys  # kept alive with the struct
+            s.keys = keys.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+            s.nnz = 0 if self.keys is None else int(self.keys.size)
         return s
 
 
@@ -191,6 +202,8 @@ def member(spec: Spec, i: int, j: int) -> bool:
         if i < G:
             return True
         return j < G or (i - spec.left <= j <= i + spec.right)
+    if spec.pattern == "index_set":
+        return bool(np.any(spec.keys[spec.offsets[i]:spec.offsets[i + 1]] == j))
     raise ValueError(spec.pattern)
 
 

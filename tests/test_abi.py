@@ -29,10 +29,23 @@ def test_library_exports_every_declared_symbol():
     assert ma_attn.LIB.ma_attn_abi_version() == ma_attn.ABI_VERSION
 
 
-def test_desc_layout_matches_header():
+def test_desc_layout_matches_header(tmp_path):
+    """Every field of the ctypes Desc sits at the offset the C compiler gives
+    the header's struct (gcc on include/ma_attn.h), and the sizes agree."""
+    import subprocess
     import ma_attn
-    # int64 x4, int32 x2, int64 x3, int32 x2, int64, ptr, int64 x2, float, int32
-    assert ctypes.sizeof(ma_attn.Desc) == 4 * 8 + 2 * 4 + 3 * 8 + 2 * 4 + 8 + 8 + 2 * 8 + 4 + 4
+    names = [f[0] for f in ma_attn.Desc._fields_]
+    src = tmp_path / "probe.c"
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "ma_attn.h"\nint main(void) {\n'
+                   + "".join(f'  printf("{n} %zu\\n", offsetof(ma_attn_desc, {n}));\n' for n in names)
+                   + '  printf("sizeof %zu\\n", sizeof(ma_attn_desc));\n  return 0;\n}\n')
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-I", os.path.join(REPO, "include"), str(src), "-o", str(exe)], check=True)
+    got = dict(line.split() for line in subprocess.run([str(exe)], check=True, capture_output=True,
+                                                       text=True).stdout.splitlines())
+    for n in names:
+        assert int(got[n]) == getattr(ma_attn.Desc, n).offset, n
+    assert int(got["sizeof"]) == ctypes.sizeof(ma_attn.Desc)
 
 
 @pytest.mark.parametrize("kw,msg", [

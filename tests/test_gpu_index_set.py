@@ -1,0 +1,113 @@
+"""INDEX_SET on the GPU (row kernel, any dtype and head_dim) against the
+oracle: random key sets with empty and full rows, sets equal to the closed-
+form patterns, the reference's Longformer COO list (repeated entries) as a
+set, and the layer routed to it.  Tolerances: max-abs 1e-5 (fp32) / 2e-2
+(16-bit)."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import qkv
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 2e-2}
+
+
+@pytest.fixture(scope="module")
+def ext():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    import sparse_attention_cuda
+    return sparse_attention_cuda
+
+
+def _inputs(shape, seed, dtype):
+    arrs = qkv(shape, seed)
+    dev = [torch.from_numpy(a).to(dtype).to("cuda") for a in arrs]
+    return dev, [t.float().cpu().numpy() for t in dev]
+
+
+def _random_csr(rng, N, density):
+    rows = [np.flatnonzero(rng.random(N) < density) for _ in range(N)]
+    off = np.zeros(N + 1, dtype=np.int64)
+    off[1:] = np.cumsum([len(r) for r in rows])
+    keys = np.concatenate(rows).astype(np.int32) if off[-1] else np.zeros(0, np.int32)
+    return off, keys
+
+
+def _err(o, ref):
+    o = o.float().cpu().numpy()
+    assert np.isfinite(o).all()
+    return float(np.abs(o - ref).max())
+
+
+@pytest.mark.parametrize("N,D,density", [(1, 16, 1.0), (77, 64, 0.0), (77, 64, 0.1), (300, 64, 0.02),
+                                         (200, 16, 0.5), (129, 130, 0.2), (64, 64, 1.0)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_random_index_sets(ext, oracle, N, D, density, dtype):
+    rng = np.random.default_rng(N * 7 + D)
+    off, keys = _random_csr(rng, N, density)
+    shape = (2, N, 3, D)
+    dev, up = _inputs(shape, 8000 + N, dtype)
+    iset = ext.IndexSet(torch.from_numpy(off), torch.from_numpy(keys), N)
+    o = ext.index_set_forward(*dev, iset)
+    spec = oracle.Spec(*shape, pattern="index_set", offsets=off, keys=keys)
+    assert _err(o, oracle.forward(spec, *up)) <= TOL[dtype]
+    # the (offsets, keys) pair, checked at the call, gives the same bits
+    assert torch.equal(ext.index_set_forward(*dev, (torch.from_numpy(off), torch.from_numpy(keys))), o)
+
+
+def test_index_set_of_causal_window(ext, oracle):
+    """The causal-64 window as an explicit set matches sliding_forward."""
+    N, shape = 2048, (1, 2048, 2, 64)
+    spec = oracle.Spec(*shape, pattern="sliding", left=63, right=0)
+    i = np.arange(N)
+    lo = np.maximum(i - 63, 0)
+    off = np.zeros(N + 1, dtype=np.int64)
+    off[1:] = np.cumsum(i - lo + 1)
+    keys = np.concatenate([np.arange(a, b + 1) for a, b in zip(lo, i)]).astype(np.int32)
+    dev, up = _inputs(shape, 8100, torch.bfloat16)
+    o = ext.index_set_forward(*dev, ext.IndexSet(torch.from_numpy(off), torch.from_numpy(keys), N))
+    assert _err(o, oracle.forward(spec, *up)) <= TOL[torch.bfloat16]
+    assert float((o.float() - ext.sliding_forward(*dev, 63, 0).float()).abs().max()) <= TOL[torch.bfloat16]
+
+
+def test_reference_longformer_coo_as_set(ext, oracle):
+    """LongformerAttention::generate_sparse_pattern (sparse_attention.cpp:234-259)
+    lists a symmetric window plus the first G rows and columns, some entries
+    twice; as a set it is longformer_forward(left=w, right=w, G)."""
+    N, w, G = 300, 5, 4
+    rows, cols = [], []
+    for i in range(N):
+        for j in range(max(0, i - w), min(N, i + w + 1)):
+            rows.append(i), cols.append(j)
+    for g in range(G):
+        for j in range(N):
+            rows += [g, j]
+            cols += [j, g]
+    shape = (1, N, 2, 64)
+    dev, up = _inputs(shape, 8200, torch.float32)
+    o = ext.index_set_forward(*dev, ext.IndexSet.from_coo(rows, cols, N))
+    spec = oracle.Spec(*shape, pattern="longformer", left=w, right=w, num_global=G)
+    assert _err(o, oracle.forward(spec, *up)) <= 1e-5
+    assert _err(o, ext.longformer_forward(*dev, w, w, G).cpu().numpy()) <= 1e-5
+
+
+def test_layer_index_set(ext, oracle):
+    """MACoreAttention(pattern="index_set"): the engine in eval mode, the
+    PyTorch mask path (and its autograd) in training mode."""
+    from layers.ma_core_bridge import MACoreAttention
+    rng = np.random.default_rng(3)
+    N, shape = 90, (2, 90, 2, 32)
+    off, keys = _random_csr(rng, N, 0.1)
+    iset = ext.IndexSet(torch.from_numpy(off), torch.from_numpy(keys), N)
+    dev, up = _inputs(shape, 8300, torch.float32)
+    att = MACoreAttention(sparse=True, window_size=4, pattern="index_set", index_set=iset)
+    ref = oracle.forward(oracle.Spec(*shape, pattern="index_set", offsets=off, keys=keys), *up)
+    assert _err(att.eval()(*dev), ref) <= 1e-5
+    q = dev[0].clone().requires_grad_(True)
+    out = att.train()(q, dev[1], dev[2])
+    assert _err(out.detach(), ref) <= 1e-5
+    out.sum().backward()
+    assert torch.isfinite(q.grad).all()
