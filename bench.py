@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the sparse-attention forward hot path on one MI355X.
 
-Default workload (BASELINE.json metric): causal sliding-window attention,
+Default workload (the headline metric): causal sliding-window attention,
 bf16, B=1 H=8 N=65536 D=64, window 64 (keys [i-63, i]).  A "step" is one
 forward pass over that batch.  Prints ONE JSON line:
 
@@ -72,7 +72,7 @@ WORKLOADS = {
                   "dilated causal window (i-4k, k<64), fp32, B=1 H=8 N=65536 D=64"),
     "cfg5_bf16": (1, 8, 65536, 64, "bf16", dict(pattern="sliding", left=63, right=0, dilation=4),
                   "dilated causal window (i-4k, k<64), bf16, B=1 H=8 N=65536 D=64"),
-    # not a BASELINE config: the dense_forward(use_causal_mask=True) path at a long sequence
+    # not one of the headline configs: the dense_forward(use_causal_mask=True) path at a long sequence
     "dense_causal_bf16": (1, 8, 16384, 64, "bf16", dict(pattern="dense", causal=True),
                           "dense causal (keys [0,i]), bf16, B=1 H=8 N=16384 D=64"),
     # the reference's dense_forward dtype (fp32 only there)

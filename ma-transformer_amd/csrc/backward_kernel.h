@@ -401,7 +401,7 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdArgs a) {
 
 // ---------------------------------------------------------------- fixed-window interior tiles
 //
-// For a fixed band [m-L, m+R] (BASELINE causal 64: L = 63, R = 0) an interior
+// For a fixed band [m-L, m+R] (the causal 64 window: L = 63, R = 0) an interior
 // tile's geometry is compile-time, as in the forward's window_tile: a wave's
 // 16 rows touch NSUB sub-tiles of 16 streamed rows at fixed offsets from its
 // own (5 for causal 64, against 8 for whole 64-row blocks), and only the
@@ -520,7 +520,7 @@ __device__ __forceinline__ void bwdkv_window_tile(const uint8_t* ring, uint32_t 
 
 // ---------------------------------------------------------------- chunks of tiles per workgroup
 //
-// For bands of at most two 64-row blocks (windows like the BASELINE causal
+// For bands of at most two 64-row blocks (windows like the causal
 // 64): one workgroup streams a chunk of consecutive tiles of a residue class.
 // The band's two blocks sit in two LDS slots (block j in slot j & 1); moving
 // to tile t+1 adds at most one block, prefetched into registers while tile t

@@ -12,7 +12,8 @@
 // over the (batch, head) stream, so a ragged last block reads zero rows
 // (masked) and its stores are dropped.
 //
-// Measured alternatives that did not pay on the 4-wide BASELINE table: a
+// Measured alternatives that did not pay on 4-wide tables (diagonal, previous
+// and two random blocks): a
 // workgroup walking a run of consecutive rows with two blocks in flight
 // (the same time at best, slower with more rows per run), because a row's
 // time is not its load latency alone; and a row-pipelined walk (all 4
@@ -208,7 +209,7 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void block_row_kernel(BlockArgs
   // 16-bit blocks only: four blocks of registers in flight fit there
   if constexpr (P::kSPB == 1) {
     if (!dense && a.bpr <= 4) {
-      // Short rows (the BASELINE table has 4 entries): every block's loads are
+      // Short rows (diagonal + previous + 2 random blocks: 4 entries): every block's loads are
       // issued at once, so the row pays one HBM latency instead of one per
       // block; the two-slot ring is filled twice.
       typename P::Slot x[4];

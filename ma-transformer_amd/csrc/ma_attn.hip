@@ -261,7 +261,7 @@ __global__ __launch_bounds__(256) void narrow_kernel(const T* __restrict__ q, co
   // The lane's query row is loaded first (it depends on nothing), then the
   // band in batches of 8 elements per thread: every load of a batch is
   // issued (indices clamped into range, so unconditionally) before the
-  // stores that wait for them, and the BASELINE band (127 rows of 16) is one
+  // stores that wait for them, and the causal-64 band at head_dim 16 (127 rows of 16) is one
   // batch -- a single global round trip before the barrier.
   const int64_t i = i0 + lane;
   const int64_t ic = i < N ? i : N - 1;
@@ -1165,7 +1165,8 @@ int launch_stream_t(const StreamArgs& a, int64_t wgs, hipStream_t st) {
   return 0;
 }
 
-// Fixed-window instantiations (the BASELINE windows); other windows run the
+// Fixed-window instantiations (the benchmark windows: causal 64, [i-32, i+31],
+// Longformer causal 128); other windows run the
 // generic kernel with `slots` ring slots.
 template <class P, bool LG>
 int launch_stream_any(const StreamArgs& a, int64_t slots, int64_t wgs, hipStream_t st) {
@@ -1370,7 +1371,7 @@ int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* 
   const bool chunked = ma::floordiv64(63 + R - obq, 64) - ma::floordiv64(-L - obq, 64) + 1 <= 2 &&
                        ma::floordiv64(63 + L - obkv, 64) - ma::floordiv64(-R - obkv, 64) + 1 <= 2 &&
                        !getenv("MA_ATTN_BWD_PER_TILE");
-  // fixed-window instantiations: causal 64 (BASELINE target, dilated config)
+  // fixed-window instantiations: causal 64 (also per residue class of a dilated window)
   // and [i-32, i+31] (cfg 2)
   const bool no_fixed = getenv("MA_ATTN_BWD_NO_FIXED") != nullptr;
   const int fixed = !chunked || no_fixed ? 0 : L == 63 && R == 0 ? 1 : L == 32 && R == 31 ? 2 : 0;

@@ -21,7 +21,7 @@ call raises -- there is no silent fallback on a GPU.  CPU tensors use the
 PyTorch reference implementations (the reference's ma_core CPU engine is not
 part of this package).
 
-New, keyword-only constructor arguments select the BASELINE patterns and
+New, keyword-only constructor arguments select the benchmark patterns and
 default to the reference behaviour: ``pattern`` ("sliding", "dense",
 "block_sparse", "longformer", "index_set"), ``causal``, ``window_left``,
 ``window_right``, ``dilation``, ``block_size``, ``block_table``,

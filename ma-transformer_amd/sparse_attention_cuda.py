@@ -14,7 +14,7 @@ The dtype set is widened from float32 to float32 / bfloat16 / float16; the
 output has the input dtype.  Kernels run asynchronously on the current HIP
 stream (torch.cuda.current_stream(), as :450 uses the current CUDA stream).
 
-New pattern entry points (not in the reference):
+New pattern entry points (not in the reference; the benchmark patterns):
 
     sliding_forward(q, k, v, left, right, dilation=1)
     block_sparse_forward(q, k, v, block_table, block_size=64)

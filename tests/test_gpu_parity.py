@@ -3,7 +3,7 @@ against the CPU oracle on identical seeded inputs.
 
 Tolerances (north_star): max-abs <= 1e-5 for float32; <= 2e-2 for bfloat16 /
 float16, measured against the float32 oracle run on the upcast 16-bit inputs.
-Full-size BASELINE configs compare the oracle on sampled row ranges (first,
+Full-size benchmark configs compare the oracle on sampled row ranges (first,
 middle and last rows of some heads) -- the oracle computes exactly those rows.
 """
 import os
@@ -243,7 +243,7 @@ def test_block_table_validation(ext):
         ext.block_sparse_forward(q[:, :64].contiguous(), q[:, :64].contiguous(), q[:, :64].contiguous(), bt, 64)
 
 
-# ------------------------------------------------------- BASELINE configs
+# ------------------------------------------------------- benchmark configs
 
 def test_cfg1_causal_fp32(ext, oracle):
     """B=1 H=4 N=1024 D=16, causal window 64, float32 -- whole output."""
