@@ -111,3 +111,15 @@ def test_layer_index_set(ext, oracle):
     assert _err(out.detach(), ref) <= 1e-5
     out.sum().backward()
     assert torch.isfinite(q.grad).all()
+
+
+def test_index_set_rejections(ext):
+    """A set made for another length, or a malformed pair, raises before any launch."""
+    q = torch.randn(1, 10, 1, 64, device="cuda")
+    s = ext.IndexSet(torch.tensor([0] * 9), torch.zeros(0, dtype=torch.int32), 8)
+    with pytest.raises(RuntimeError, match="S=8"):
+        ext.index_set_forward(q, q, q, s)
+    with pytest.raises(RuntimeError, match="ascending"):
+        ext.index_set_forward(q, q, q, (torch.tensor([0, 2] + [2] * 9), torch.tensor([3, 3])))
+    empty = ext.IndexSet(torch.zeros(11, dtype=torch.int64), torch.zeros(0, dtype=torch.int32), 10)
+    assert torch.equal(ext.index_set_forward(q, q, q, empty), torch.zeros_like(q))

@@ -131,3 +131,18 @@ def test_abi_index_set_rules():
     ma_attn.validate(d)
     with pytest.raises(ValueError, match="own input"):
         ma_attn.row_keys(d, 0)
+
+
+def test_bench_window_csr_matches_oracle(oracle):
+    """bench.py's index_set workload builds the target's window as a set: the
+    same rows as the oracle's closed form, and the key count it reports."""
+    import bench
+    N = 300
+    off, keys = bench.window_csr(N, 63, 0)
+    spec = oracle.Spec(1, N, 1, 16, pattern="sliding", left=63, right=0)
+    for i in range(N):
+        assert keys[off[i]:off[i + 1]].tolist() == oracle.row_keys(spec, i).tolist()
+    assert int(off[-1]) == bench.key_count(N, dict(pattern="index_set", left=63, right=0))
+    off, keys = bench.window_csr(50, 3, 5)
+    spec = oracle.Spec(1, 50, 1, 16, pattern="sliding", left=3, right=5)
+    assert all(keys[off[i]:off[i + 1]].tolist() == oracle.row_keys(spec, i).tolist() for i in range(50))
