@@ -4,7 +4,7 @@ Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline
 leg import this module, and only as the checker / the timed CPU baseline.  The
 product (``ma-transformer_amd/``) never imports it.
 
-Three independent statements of the same semantics live here:
+Independent statements of the same semantics live here:
 
 * ``forward`` -- ctypes over ``liboracle.so`` (oracle.c), the op-for-op
   restatement of ``ma_core::compute_sparse_attention``
