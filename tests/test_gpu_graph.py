@@ -25,6 +25,8 @@ def test_graph_capture_replays(ext):
     q, k, v, g = (torch.randn(shape, device="cuda", generator=gen).to(torch.bfloat16) for _ in range(4))
     qf, kf, vf, gf = (t.float() for t in (q, k, v, g))
     table = ext.BlockTable(ext.make_block_table(7, 64, 2), 4096, 64)
+    rows = torch.arange(4096).repeat_interleave(3)
+    iset = ext.IndexSet.from_coo(rows, (rows * 7 + torch.arange(3).repeat(4096) * 13) % 4096, 4096)
 
     def work():
         return [ext.sliding_forward(q, k, v, 63, 0),
@@ -32,6 +34,7 @@ def test_graph_capture_replays(ext):
                 ext.block_sparse_forward(q, k, v, table, 64),
                 ext.longformer_forward(q, k, v, 127, 0, 16),  # workspace of partials + combine launch
                 ext.dense_forward(qf, kf, vf, True),
+                ext.index_set_forward(q, k, v, iset),  # gather kernel over a device-resident set
                 *ext.sliding_backward(q, k, v, g, 63, 0, 1),  # statistics workspace, two launches
                 *ext.sliding_backward(qf, kf, vf, gf, 63, 0, 1)]
 
