@@ -80,6 +80,11 @@ typedef struct ma_attn_desc {
   const int32_t* index_keys;    /* INDEX_SET: device int32 [num_indices], each row's keys
                                    ascending and distinct, in [0, seq_len) */
   int64_t num_indices;          /* INDEX_SET: length of index_keys */
+  const int64_t* index_t_offsets; /* INDEX_SET backward only: the transposed set, device int64
+                                     [seq_len + 1]: key j is listed by the queries
+                                     index_t_queries[index_t_offsets[j] .. index_t_offsets[j+1]) */
+  const int32_t* index_t_queries; /* INDEX_SET backward only: device int32 [num_indices], ascending
+                                     per key */
 } ma_attn_desc;
 
 /*
@@ -116,8 +121,10 @@ size_t ma_attn_workspace_size(const ma_attn_desc* desc);
  *   sparse_backward_cuda  src/cuda/sparse_attention_kernel.cu:459-497 (SLIDING, left=right=w;
  *                         kernel :265-346)
  *   dense_backward_cuda   src/cuda/sparse_attention_kernel.cu:383-418 (DENSE; kernel :104-175)
- * generalised to any left/right/dilation and to bf16/fp16 (fp32 arithmetic).
- * Other patterns return non-zero.  workspace: device memory of
+ * generalised to any left/right/dilation and to bf16/fp16 (fp32 arithmetic),
+ * and for INDEX_SET, which also needs the transposed set (index_t_offsets,
+ * index_t_queries: for each key, the queries that list it).  Other patterns
+ * return non-zero.  workspace: device memory of
  * ma_attn_backward_workspace_size(desc) bytes (per-row softmax statistics).
  */
 int ma_attn_backward(const ma_attn_desc* desc, const void* q, const void* k,
@@ -182,7 +189,7 @@ int64_t ma_attn_row_keys(const ma_attn_desc* desc, const int32_t* host_block_tab
 /* ABI version of this header (bumped on incompatible change). */
 int ma_attn_abi_version(void);
 
-#define MA_ATTN_ABI_VERSION 4
+#define MA_ATTN_ABI_VERSION 5
 
 #ifdef __cplusplus
 }

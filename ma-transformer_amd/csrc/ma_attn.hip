@@ -202,7 +202,7 @@ __global__ __launch_bounds__(256) void rows_kernel(const T* __restrict__ q, cons
       if (d < D) part = fmaf(ld_f(dout + rr * D + d), acc[c] * inv, part);
     }
     const float delta = wave_sum(part);
-    if (lane == 0) stats[rr] = RowStat{cnt > 0 ? m + logf(l) : 0.0f, delta};
+    if (lane == 0) stats[rr] = RowStat{cnt > 0 && l > 0.0f ? m + logf(l) : 0.0f, delta};
   } else {
     T* orow = o + rr * D;
 #pragma unroll
@@ -427,8 +427,9 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const T* __restrict__ q, co
   for (int c = 0; c < DPL; ++c) acc[c] = 0.0f;
   for (int64_t c0 = 0; c0 < cnt; c0 += 64) {
     const int64_t t = c0 + lane;
-    const bool valid = t < cnt;
-    const int64_t j = valid ? ma::key_at(pp, rk, i, t) : 0;
+    const int64_t j0 = t < cnt ? ma::key_at(pp, rk, i, t) : -1;
+    const bool valid = j0 >= 0 && j0 < N;  // an index set's keys are checked here
+    const int64_t j = valid ? j0 : 0;
     float ds = 0.0f;
     if (valid) {
       const T* kr = kb + j * rs;
@@ -501,8 +502,9 @@ __global__ __launch_bounds__(256) void bwd_dkv_kernel(const T* __restrict__ q, c
   for (int c = 0; c < DPL; ++c) acc_k[c] = acc_v[c] = 0.0f;
   for (int64_t c0 = 0; c0 < cnt; c0 += 64) {
     const int64_t t = c0 + lane;
-    const bool valid = t < cnt;
-    const int64_t i = valid ? ma::key_at(pt, rq, j, t) : 0;
+    const int64_t i0 = t < cnt ? ma::key_at(pt, rq, j, t) : -1;
+    const bool valid = i0 >= 0 && i0 < N;  // a transposed index set's queries are checked here
+    const int64_t i = valid ? i0 : 0;
     float p = 0.0f, ds = 0.0f;
     if (valid) {
       const T* qr = qb + i * rs;
@@ -1287,12 +1289,18 @@ int launch_block(const ma_attn_desc* d, const void* q, const void* k, const void
 // Backward: SLIDING and DENSE key sets (the reference's backward entry
 // points), any dtype, head_dim <= 512.
 bool backward_supported(const ma_attn_desc* d) {
-  return d->pattern == MA_ATTN_SLIDING || d->pattern == MA_ATTN_DENSE;
+  return d->pattern == MA_ATTN_SLIDING || d->pattern == MA_ATTN_DENSE || d->pattern == MA_ATTN_INDEX_SET;
 }
 
-// The query sets T_j = {i : j in S_i} as a SLIDING pattern.
+// The query sets T_j = {i : j in S_i}: a SLIDING pattern for the banded
+// sets, the caller's transposed CSR for an index set.
 ma::PatternParams transposed_params(const ma_attn_desc* d) {
   ma::PatternParams p = params_of(d, nullptr);
+  if (d->pattern == MA_ATTN_INDEX_SET) {
+    p.offsets = d->index_t_offsets;
+    p.keys = d->index_t_queries;
+    return p;
+  }
   if (d->pattern == MA_ATTN_DENSE) {
     p.pattern = ma::kSliding;
     p.dilation = 1;
@@ -1553,7 +1561,11 @@ int ma_attn_backward(const ma_attn_desc* desc, const void* q, const void* k, con
   g_last_error.clear();
   if (validate(desc)) return 1;
   if (!backward_supported(desc))
-    return fail("ma_attn_backward: pattern %d has no backward (SLIDING and DENSE only)", desc->pattern);
+    return fail("ma_attn_backward: pattern %d has no backward (SLIDING, DENSE and INDEX_SET only)",
+                desc->pattern);
+  if (desc->pattern == MA_ATTN_INDEX_SET && desc->seq_len > 0 &&
+      (!desc->index_t_offsets || (desc->num_indices > 0 && !desc->index_t_queries)))
+    return fail("ma_attn_backward: an index set needs its transposed set (index_t_offsets, index_t_queries)");
   const int64_t rows = desc->batch * desc->seq_len * desc->num_heads;
   if (rows == 0 || desc->head_dim == 0) return 0;
   if (!q || !k || !v || !dout || !dq || !dk || !dv) return fail("ma_attn_backward: null tensor pointer");

@@ -146,7 +146,7 @@ def pytorch_pattern_attention(query, key, value, spec: PatternSpec) -> torch.Ten
 
 class MACoreAttentionFunction(torch.autograd.Function):
     """Autograd function: native forward; native backward (HIP kernels that
-    recompute the softmax) for the sliding and dense patterns.
+    recompute the softmax) for the sliding, dense and index-set patterns.
 
     Reference: src/layers/ma_core_bridge.py:44-154.  The extra trailing
     argument ``spec`` (a PatternSpec or None) selects a non-reference pattern.
@@ -177,13 +177,15 @@ class MACoreAttentionFunction(torch.autograd.Function):
     def backward(ctx, grad_output: torch.Tensor) -> Tuple[Optional[torch.Tensor], ...]:
         query, key, value = ctx.saved_tensors
         spec = ctx.spec
-        native = spec is None or spec.pattern in ("sliding", "dense")
+        native = spec is None or spec.pattern in ("sliding", "dense", "index_set")
         if _HAS_SPARSE_CUDA and query.is_cuda and native:
             ext = sparse_attention_cuda
             cq, ck, cv, cgo = (t.contiguous() for t in (query, key, value, grad_output))
             cgo = cgo.to(cq.dtype)
             if spec is not None and spec.pattern == "sliding":
                 dQ, dK, dV = ext.sliding_backward(cq, ck, cv, cgo, spec.left, spec.right, spec.dilation)
+            elif spec is not None and spec.pattern == "index_set":
+                dQ, dK, dV = ext.index_set_backward(cq, ck, cv, cgo, spec.index_set)
             elif spec is not None:
                 dQ, dK, dV = ext.dense_backward(cq, ck, cv, cgo, spec.causal)
             elif ctx.sparse:

@@ -18,7 +18,7 @@ LIB_PATH = os.environ.get("MA_ATTN_LIB", os.path.join(_HERE, "libma_attn.so"))
 
 F32, BF16, F16 = 0, 1, 2
 SLIDING, DENSE, BLOCK_SPARSE, LONGFORMER, INDEX_SET = 0, 1, 2, 3, 4
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 
@@ -47,6 +47,8 @@ class Desc(ctypes.Structure):
         ("index_offsets", ctypes.c_void_p),
         ("index_keys", ctypes.c_void_p),
         ("num_indices", ctypes.c_int64),
+        ("index_t_offsets", ctypes.c_void_p),
+        ("index_t_queries", ctypes.c_void_p),
     ]
 
 
@@ -96,7 +98,8 @@ def last_error() -> str:
 
 def make_desc(B, N, H, D, dtype_code, pattern, left=0, right=0, dilation=1, causal=False,
               block_size=64, block_table_ptr=0, blocks_per_row=0, num_global=0,
-              scale=0.0, index_offsets_ptr=0, index_keys_ptr=0, num_indices=0) -> Desc:
+              scale=0.0, index_offsets_ptr=0, index_keys_ptr=0, num_indices=0, index_t_offsets_ptr=0,
+              index_t_queries_ptr=0) -> Desc:
     d = Desc()
     d.batch, d.seq_len, d.num_heads, d.head_dim = int(B), int(N), int(H), int(D)
     d.dtype, d.pattern = int(dtype_code), int(pattern)
@@ -110,6 +113,8 @@ def make_desc(B, N, H, D, dtype_code, pattern, left=0, right=0, dilation=1, caus
     d.index_offsets = int(index_offsets_ptr) or None
     d.index_keys = int(index_keys_ptr) or None
     d.num_indices = int(num_indices)
+    d.index_t_offsets = int(index_t_offsets_ptr) or None
+    d.index_t_queries = int(index_t_queries_ptr) or None
     return d
 
 

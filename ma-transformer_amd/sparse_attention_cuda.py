@@ -40,7 +40,7 @@ import ma_attn as _ma
 
 __all__ = ["forward", "dense_forward", "backward", "dense_backward", "sliding_forward",
            "sliding_backward", "block_sparse_forward", "longformer_forward", "make_block_table",
-           "BlockTable", "IndexSet", "index_set_forward"]
+           "BlockTable", "IndexSet", "index_set_forward", "index_set_backward"]
 
 
 def _check(*ts: torch.Tensor) -> None:
@@ -295,6 +295,16 @@ class IndexSet:
         self.offsets = off.to(dev)
         self.keys = (kk if kk.numel() else torch.zeros(1, dtype=torch.int32)).to(dev)
         self.num_indices = int(kk.numel())
+        # the transposed set (for each key, the queries that list it, ascending),
+        # which the backward's dK/dV pass walks
+        N = self.seq_len
+        rows = torch.repeat_interleave(torch.arange(N, dtype=torch.int64), off[1:] - off[:-1])
+        order = torch.sort(kk.long(), stable=True).indices
+        t_off = torch.zeros(N + 1, dtype=torch.int64)
+        t_off[1:] = torch.cumsum(torch.bincount(kk.long(), minlength=N)[:N], 0) if kk.numel() else 0
+        t_q = rows[order].to(torch.int32)
+        self.t_offsets = t_off.to(dev)
+        self.t_queries = (t_q if t_q.numel() else torch.zeros(1, dtype=torch.int32)).to(dev)
 
     @staticmethod
     def from_coo(rows, cols, seq_len: int, device=None) -> "IndexSet":
@@ -327,6 +337,24 @@ def index_set_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tenso
         raise RuntimeError("IndexSet is on another device than the inputs")
     return _launch(query, key, value, _ma.INDEX_SET, index_offsets_ptr=index_set.offsets.data_ptr(),
                    index_keys_ptr=index_set.keys.data_ptr(), num_indices=index_set.num_indices)
+
+
+def index_set_backward(query, key, value, grad_out, index_set) -> List[torch.Tensor]:
+    """dQ, dK, dV of index_set_forward (row kernels; the reference's generic
+    COO path has no backward).  index_set as for index_set_forward."""
+    _check(query, key, value, grad_out)
+    N = query.shape[1]
+    if not isinstance(index_set, IndexSet):
+        offsets, keys = index_set
+        index_set = IndexSet(offsets, keys, N, query.device)
+    if index_set.seq_len != N:
+        raise RuntimeError(f"IndexSet was made for S={index_set.seq_len}; called with S={N}")
+    if index_set.offsets.device != query.device:
+        raise RuntimeError("IndexSet is on another device than the inputs")
+    return _backward(query, key, value, grad_out, _ma.INDEX_SET,
+                     index_offsets_ptr=index_set.offsets.data_ptr(), index_keys_ptr=index_set.keys.data_ptr(),
+                     num_indices=index_set.num_indices, index_t_offsets_ptr=index_set.t_offsets.data_ptr(),
+                     index_t_queries_ptr=index_set.t_queries.data_ptr())
 
 
 # ---------------------------------------------------------------- backward (HIP kernels)

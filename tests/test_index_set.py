@@ -146,3 +146,15 @@ def test_bench_window_csr_matches_oracle(oracle):
     off, keys = bench.window_csr(50, 3, 5)
     spec = oracle.Spec(1, 50, 1, 16, pattern="sliding", left=3, right=5)
     assert all(keys[off[i]:off[i + 1]].tolist() == oracle.row_keys(spec, i).tolist() for i in range(50))
+
+
+def test_index_set_transpose():
+    """IndexSet's transposed set (queries per key, ascending) against brute force."""
+    import sparse_attention_cuda as ext
+    rng = np.random.default_rng(9)
+    N = 40
+    rows, cols = np.nonzero(rng.random((N, N)) < 0.15)
+    s = ext.IndexSet.from_coo(rows, cols, N, device="cpu")
+    t_off, t_q = s.t_offsets.tolist(), s.t_queries.tolist()
+    for j in range(N):
+        assert t_q[t_off[j]:t_off[j + 1]] == sorted(int(i) for i in rows[cols == j])
