@@ -146,7 +146,9 @@ def pytorch_pattern_attention(query, key, value, spec: PatternSpec) -> torch.Ten
 
 class MACoreAttentionFunction(torch.autograd.Function):
     """Autograd function: native forward; native backward (HIP kernels that
-    recompute the softmax) for the sliding, dense and index-set patterns.
+    recompute the softmax) for every pattern: sliding and dense on their own
+    kernels, index sets, block-sparse and Longformer on the index-set row
+    kernels (the latter two as their explicit key sets).
 
     Reference: src/layers/ma_core_bridge.py:44-154.  The extra trailing
     argument ``spec`` (a PatternSpec or None) selects a non-reference pattern.
@@ -177,7 +179,7 @@ class MACoreAttentionFunction(torch.autograd.Function):
     def backward(ctx, grad_output: torch.Tensor) -> Tuple[Optional[torch.Tensor], ...]:
         query, key, value = ctx.saved_tensors
         spec = ctx.spec
-        native = spec is None or spec.pattern in ("sliding", "dense", "index_set")
+        native = spec is None or spec.pattern in ("sliding", "dense", "index_set", "block_sparse", "longformer")
         if _HAS_SPARSE_CUDA and query.is_cuda and native:
             ext = sparse_attention_cuda
             cq, ck, cv, cgo = (t.contiguous() for t in (query, key, value, grad_output))
@@ -186,6 +188,13 @@ class MACoreAttentionFunction(torch.autograd.Function):
                 dQ, dK, dV = ext.sliding_backward(cq, ck, cv, cgo, spec.left, spec.right, spec.dilation)
             elif spec is not None and spec.pattern == "index_set":
                 dQ, dK, dV = ext.index_set_backward(cq, ck, cv, cgo, spec.index_set)
+            elif spec is not None and spec.pattern in ("block_sparse", "longformer"):
+                # the pattern's key sets as an explicit set (built once, cached)
+                kw = (dict(block_table=spec.block_table, block_size=spec.block_size)
+                      if spec.pattern == "block_sparse" else
+                      dict(left=spec.left, right=spec.right, num_global=spec.num_global))
+                iset = ext.pattern_index_set(spec.pattern, cq.shape[1], cq.device, **kw)
+                dQ, dK, dV = ext.index_set_backward(cq, ck, cv, cgo, iset)
             elif spec is not None:
                 dQ, dK, dV = ext.dense_backward(cq, ck, cv, cgo, spec.causal)
             elif ctx.sparse:
@@ -195,8 +204,8 @@ class MACoreAttentionFunction(torch.autograd.Function):
             return (dQ if ctx.needs_input_grad[0] else None,
                     dK if ctx.needs_input_grad[1] else None,
                     dV if ctx.needs_input_grad[2] else None, None, None, None, None)
-        # Block-sparse / Longformer (no native backward) and host tensors:
-        # recompute with the PyTorch implementation and differentiate (:140-154)
+        # Host tensors: recompute with the PyTorch implementation and
+        # differentiate, as the reference does (:140-154)
         with torch.enable_grad():
             q, k, v = (t.detach().requires_grad_(True) for t in (query, key, value))
             if spec is not None:

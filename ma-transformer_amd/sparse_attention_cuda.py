@@ -40,7 +40,7 @@ import ma_attn as _ma
 
 __all__ = ["forward", "dense_forward", "backward", "dense_backward", "sliding_forward",
            "sliding_backward", "block_sparse_forward", "longformer_forward", "make_block_table",
-           "BlockTable", "IndexSet", "index_set_forward", "index_set_backward"]
+           "BlockTable", "IndexSet", "index_set_forward", "index_set_backward", "pattern_index_set"]
 
 
 def _check(*ts: torch.Tensor) -> None:
@@ -320,6 +320,38 @@ class IndexSet:
         offsets = torch.zeros(N + 1, dtype=torch.int64)
         offsets[1:] = torch.cumsum(torch.bincount(rr, minlength=N)[:N], 0)
         return IndexSet(offsets, cc, N, device)
+
+
+_pattern_sets: dict = {}
+
+
+def pattern_index_set(pattern: str, seq_len: int, device, **kw) -> IndexSet:
+    """The key sets of a closed-form pattern ("block_sparse" with block_table=
+    and block_size=, "longformer" with left=, right=, num_global=) as an
+    IndexSet, from the engine's own enumerator (ma_attn_row_keys), so its
+    backward (index_set_backward) is the exact gradient of that pattern's
+    forward.  Cached per pattern, length and device."""
+    code = {"block_sparse": _ma.BLOCK_SPARSE, "longformer": _ma.LONGFORMER}[pattern]
+    table = kw.pop("block_table", None)
+    host_table = None
+    if table is not None:
+        host_table = (table.tensor if isinstance(table, BlockTable) else torch.as_tensor(table)) \
+            .detach().to("cpu", torch.int32).contiguous()
+        kw["blocks_per_row"] = int(host_table.shape[1])
+    key = (pattern, int(seq_len), str(device), tuple(sorted(kw.items())),
+           None if host_table is None else host_table.numpy().tobytes())
+    hit = _pattern_sets.get(key)
+    if hit is None:
+        if len(_pattern_sets) > 16:
+            _pattern_sets.clear()
+        tptr = host_table.data_ptr() if host_table is not None else 0  # host pointer: enumeration only
+        desc = _ma.make_desc(1, seq_len, 1, 64, _ma.F32, code, block_table_ptr=tptr, **kw)
+        rows = [_ma.row_keys(desc, i, host_table) for i in range(seq_len)]
+        offsets = torch.zeros(seq_len + 1, dtype=torch.int64)
+        offsets[1:] = torch.cumsum(torch.tensor([len(r) for r in rows], dtype=torch.int64), 0)
+        keys = torch.tensor([j for r in rows for j in r], dtype=torch.int32)
+        hit = _pattern_sets[key] = IndexSet(offsets, keys, seq_len, device)
+    return hit
 
 
 def index_set_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,

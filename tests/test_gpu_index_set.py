@@ -167,3 +167,34 @@ def test_layer_index_set_training_native(ext, oracle, monkeypatch):
     ref = oracle.backward(spec, *up, np.ones(shape, np.float32))
     for t, r in zip((q, k, v), ref):
         assert float(np.abs(t.grad.cpu().numpy() - r).max()) <= 1e-4
+
+
+@pytest.mark.parametrize("pattern,kw", [
+    ("longformer", dict(window_left=20, window_right=3, num_global_tokens=5)),
+    ("block_sparse", dict(block_size=64)),
+])
+def test_layer_pattern_training_native(ext, oracle, monkeypatch, pattern, kw):
+    """Block-sparse and Longformer train on the engine too: their key sets
+    become an IndexSet (once) and index_set_backward gives the gradients."""
+    from layers.ma_core_bridge import MACoreAttention
+    calls = []
+    f = ext.index_set_backward
+    monkeypatch.setattr(ext, "index_set_backward", lambda *a, **k_: calls.append(1) or f(*a, **k_))
+    N, shape = 200, (2, 200, 2, 64)
+    okw = {}
+    if pattern == "block_sparse":
+        tab = ext.make_block_table(3, 4, 1).numpy()
+        kw = dict(kw, block_table=torch.from_numpy(tab))
+        okw = dict(block_size=64, table=tab)
+    else:
+        okw = dict(left=20, right=3, num_global=5)
+    dev, up = _inputs(shape, 8700, torch.float32)
+    q, k, v = (t.clone().requires_grad_(True) for t in dev)
+    att = MACoreAttention(sparse=True, window_size=4, pattern=pattern, fallback_training=False, **kw).train()
+    out = att(q, k, v)
+    spec = oracle.Spec(*shape, pattern=pattern, **okw)
+    assert float(np.abs(out.detach().cpu().numpy() - oracle.forward(spec, *up)).max()) <= 1e-5
+    out.sum().backward()
+    assert calls == [1]
+    for t, r in zip((q, k, v), oracle.backward(spec, *up, np.ones(shape, np.float32))):
+        assert float(np.abs(t.grad.cpu().numpy() - r).max()) <= 1e-4

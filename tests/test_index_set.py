@@ -158,3 +158,23 @@ def test_index_set_transpose():
     t_off, t_q = s.t_offsets.tolist(), s.t_queries.tolist()
     for j in range(N):
         assert t_q[t_off[j]:t_off[j + 1]] == sorted(int(i) for i in rows[cols == j])
+
+
+@pytest.mark.parametrize("pattern,kw,okw", [
+    ("longformer", dict(left=7, right=2, num_global=3), dict(left=7, right=2, num_global=3)),
+    ("block_sparse", dict(block_size=16), dict(block_size=16)),
+])
+def test_pattern_index_set_matches_oracle(oracle, pattern, kw, okw):
+    """The explicit set the layer trains block-sparse / Longformer on holds
+    exactly the oracle's key lists."""
+    import sparse_attention_cuda as ext
+    N = 90
+    if pattern == "block_sparse":
+        tab = oracle.block_table(4, 6, 2)
+        kw = dict(kw, block_table=torch.from_numpy(tab))
+        okw = dict(okw, table=tab)
+    s = ext.pattern_index_set(pattern, N, "cpu", **kw)
+    spec = oracle.Spec(1, N, 1, 16, pattern=pattern, **okw)
+    off, keys = s.offsets.tolist(), s.keys.tolist()
+    for i in range(N):
+        assert keys[off[i]:off[i + 1]] == oracle.row_keys(spec, i).tolist()
