@@ -866,10 +866,14 @@ __device__ __forceinline__ void unpack8(const T* p, float (&x)[8]) {
   }
 }
 
-template <typename T>
+// STATS (backward): the row's softmax statistics {lse, delta} instead of O,
+// as rows_kernel<STATS>.
+template <typename T, bool STATS = false>
 __global__ __launch_bounds__(256) void gather_rows_kernel(const T* __restrict__ q, const T* __restrict__ k,
                                                           const T* __restrict__ v, T* __restrict__ o, int64_t B,
-                                                          int64_t H, ma::PatternParams pp, float scale) {
+                                                          int64_t H, ma::PatternParams pp, float scale,
+                                                          const T* __restrict__ dout = nullptr,
+                                                          RowStat* __restrict__ stats = nullptr) {
   constexpr int D = 64;
   constexpr int QPW = 4;  // query rows per wave (16 lanes each)
   constexpr int NP = 8;   // passes per chunk, 4 keys per pass (16: 680 vs 575 us, fewer waves)
@@ -976,10 +980,131 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const T* __restrict__ 
     acc[e] += __shfl_xor(acc[e], 8, 64);
   }
   const float inv = cnt > 0 && l != 0.0f ? 1.0f / l : 0.0f;
-  if (row_ok && r4 == 0) {
-    T* orow = o + rr * D + 16 * c4;
+  if constexpr (STATS) {
+    float gv[16], part = 0.0f;
+    unpack8(dout + rr * D + 16 * c4, *reinterpret_cast<float(*)[8]>(gv));
+    unpack8(dout + rr * D + 16 * c4 + 8, *reinterpret_cast<float(*)[8]>(gv + 8));
 #pragma unroll
-    for (int e = 0; e < 16; ++e) orow[e] = cvt_out<T>(acc[e] * inv);
+    for (int e = 0; e < 16; ++e) part = fmaf(gv[e], acc[e] * inv, part);
+    part += __shfl_xor(part, 1, 64);
+    part += __shfl_xor(part, 2, 64);
+    if (row_ok && lane % 16 == 0) stats[rr] = RowStat{cnt > 0 && l > 0.0f ? m + logf(l) : 0.0f, part};
+  } else {
+    if (row_ok && r4 == 0) {
+      T* orow = o + rr * D + 16 * c4;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) orow[e] = cvt_out<T>(acc[e] * inv);
+    }
+  }
+}
+
+// Backward at head_dim 64 over any key set, with the gather layout of
+// gather_rows_kernel (4 rows per wave, 16 lanes per row, 4 partners per pass,
+// whole-row reads), given the rows' {lse, delta}:
+//   KV = false: row = query i over its keys t:   dq_i = scale * sum_t ds_it k_t
+//   KV = true:  row = key j over its queries t:  dk_j = scale * sum_t ds_tj q_t,
+//                                                dv_j = sum_t p_tj dO_t
+// with p = exp(q.k * scale - lse_query), ds = p * (dO.v - delta_query).  The
+// partner rows loaded for the two dot products are the ones accumulated, so
+// each partner is read once.
+template <typename T, bool KV>
+__global__ __launch_bounds__(256) void gather_bwd_kernel(const T* __restrict__ q, const T* __restrict__ k,
+                                                         const T* __restrict__ v, const T* __restrict__ dout,
+                                                         const RowStat* __restrict__ stats, T* __restrict__ out1,
+                                                         T* __restrict__ out2, int64_t B, int64_t H,
+                                                         ma::PatternParams pp, float scale) {
+  constexpr int D = 64;
+  constexpr int QPW = 4;
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int qs = lane >> 4;
+  const int r4 = (lane >> 2) & 3;
+  const int c4 = lane & 3;
+  const int64_t N = pp.n;
+  const int64_t nblk = (N + 15) / 16;
+  const int64_t g = xcd_row_order((int)blockIdx.x, (int)gridDim.x);
+  const int64_t bh = g / nblk;
+  const int64_t i0 = (g % nblk) * 16 + wv * QPW;
+  if (i0 >= N) return;  // uniform; no barrier in this kernel
+  const int64_t b = bh / H;
+  const int64_t h = bh % H;
+  const int64_t ip = i0 + qs;
+  const bool row_ok = ip < N;
+  const int64_t i = row_ok ? ip : i0;
+  const int64_t rr = (b * N + i) * H + h;
+  const int64_t rs = H * D;
+  const int64_t sbase = b * N * H + h;  // stats index of position 0 of this (batch, head)
+
+  // own rows: (q_i, dO_i) for dq, (k_j, v_j) for dk/dv; partners the other pair
+  float av[16], bv[16];
+  {
+    const T* A = (KV ? k : q) + rr * D + 16 * c4;
+    const T* Bp = (KV ? v : dout) + rr * D + 16 * c4;
+    unpack8(A, *reinterpret_cast<float(*)[8]>(av));
+    unpack8(A + 8, *reinterpret_cast<float(*)[8]>(av + 8));
+    unpack8(Bp, *reinterpret_cast<float(*)[8]>(bv));
+    unpack8(Bp + 8, *reinterpret_cast<float(*)[8]>(bv + 8));
+  }
+  const T* xb = (KV ? q : k) + (b * N * H + h) * D + 16 * c4;
+  const T* yb = (KV ? dout : v) + (b * N * H + h) * D + 16 * c4;
+  RowStat own = RowStat{0.0f, 0.0f};
+  if (!KV) own = stats[rr];
+  const ma::RowKeys rk = ma::row_keys(pp, i);
+  const int64_t cnt = row_ok ? rk.count : 0;
+  int64_t cmax = cnt;
+#pragma unroll
+  for (int sh = 16; sh <= 32; sh <<= 1) cmax = ma::imax64(cmax, (int64_t)__shfl_xor((long long)cmax, sh, 64));
+
+  float acc1[16], acc2[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc1[e] = acc2[e] = 0.0f;
+  for (int64_t c0 = 0; c0 < cmax; c0 += 4) {
+    const int64_t t = c0 + r4;
+    const int64_t jk = t < cnt ? ma::key_at(pp, rk, i, t) : -1;
+    const bool valid = jk >= 0 && jk < N;  // an index set's entries are checked here
+    const int64_t pr = valid ? jk : 0;
+    float x[16], y[16];
+    unpack8(xb + pr * rs, *reinterpret_cast<float(*)[8]>(x));
+    unpack8(xb + pr * rs + 8, *reinterpret_cast<float(*)[8]>(x + 8));
+    unpack8(yb + pr * rs, *reinterpret_cast<float(*)[8]>(y));
+    unpack8(yb + pr * rs + 8, *reinterpret_cast<float(*)[8]>(y + 8));
+    float sd = 0.0f, pd = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      sd = fmaf(av[e], x[e], sd);
+      pd = fmaf(bv[e], y[e], pd);
+    }
+    sd += __shfl_xor(sd, 1, 64);
+    sd += __shfl_xor(sd, 2, 64);
+    pd += __shfl_xor(pd, 1, 64);
+    pd += __shfl_xor(pd, 2, 64);
+    const RowStat st = KV ? stats[sbase + pr * H] : own;
+    const float p = valid ? expf(sd * scale - st.lse) : 0.0f;
+    const float ds = p * (pd - st.delta);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      acc1[e] = fmaf(ds, x[e], acc1[e]);
+      if (KV) acc2[e] = fmaf(p, y[e], acc2[e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    acc1[e] += __shfl_xor(acc1[e], 4, 64);
+    acc1[e] += __shfl_xor(acc1[e], 8, 64);
+    if (KV) {
+      acc2[e] += __shfl_xor(acc2[e], 4, 64);
+      acc2[e] += __shfl_xor(acc2[e], 8, 64);
+    }
+  }
+  if (row_ok && r4 == 0) {
+    T* o1 = out1 + rr * D + 16 * c4;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o1[e] = cvt_out<T>(acc1[e] * scale);
+    if (KV) {
+      T* o2 = out2 + rr * D + 16 * c4;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o2[e] = cvt_out<T>(acc2[e]);
+    }
   }
 }
 
@@ -994,7 +1119,7 @@ int launch_gather(const ma_attn_desc* d, const void* q, const void* k, const voi
   if (blocks > (int64_t)INT32_MAX) return fail("ma_attn: problem too large for one launch");
   launch(true, gather_rows_kernel<T>, dim3((unsigned)blocks), dim3(256), 0u, st, static_cast<const T*>(q),
          static_cast<const T*>(k), static_cast<const T*>(v), static_cast<T*>(o), d->batch, d->num_heads,
-         params_of(d, d->block_table), scale_of(d));
+         params_of(d, d->block_table), scale_of(d), (const T*)nullptr, (RowStat*)nullptr);
   return 0;
 }
 
@@ -1435,6 +1560,20 @@ int launch_backward(const ma_attn_desc* d, const void* q, const void* k, const v
   const T* tg = static_cast<const T*>(dout);
   const dim3 grid((unsigned)blocks), blk(256);
   const int64_t B = d->batch, H = d->num_heads, D = d->head_dim;
+  if (D == 64 && strcmp(kernel_override(), "rows") != 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
+      aligned16(dout) && aligned16(dq) && aligned16(dk) && aligned16(dv)) {
+    // head_dim 64: the gather layout (whole-row reads, 4 rows per wave)
+    const int64_t gblocks = B * H * ((d->seq_len + 15) / 16);
+    if (gblocks > (int64_t)INT32_MAX) return fail("ma_attn: problem too large for one launch");
+    const dim3 gg((unsigned)gblocks);
+    launch(false, gather_rows_kernel<T, true>, gg, blk, 0u, st, tq, tk, tv, (T*)nullptr, B, H, pp, scale, tg,
+           stats);
+    launch(false, gather_bwd_kernel<T, false>, gg, blk, 0u, st, tq, tk, tv, tg, (const RowStat*)stats,
+           static_cast<T*>(dq), (T*)nullptr, B, H, pp, scale);
+    launch(true, gather_bwd_kernel<T, true>, gg, blk, 0u, st, tq, tk, tv, tg, (const RowStat*)stats,
+           static_cast<T*>(dk), static_cast<T*>(dv), B, H, pt, scale);
+    return 0;
+  }
 #define MA_BWD(N_)                                                                                          \
   do {                                                                                                      \
     launch(false, rows_kernel<T, N_, true>, grid, blk, (uint32_t)shm1, st, tq, tk, tv, (T*)nullptr, B, H, D, pp, \
