@@ -186,10 +186,30 @@ int ma_attn_block_table(uint64_t seed, int64_t num_blocks,
 int64_t ma_attn_row_keys(const ma_attn_desc* desc, const int32_t* host_block_table,
                          int64_t i, int64_t* keys_out, int64_t cap);
 
+/*
+ * Host: every row's key list of desc at once, as CSR.  offsets_out (host
+ * int64 [seq_len + 1], may be NULL) receives the row offsets; keys_out (host
+ * int32 [keys_cap], may be NULL) the keys, row after row, each row ascending.
+ * Returns the total key count (nnz), or -1 on invalid input or when keys_out
+ * is given and keys_cap < nnz.  Call once with keys_out = NULL for the count.
+ * The same closed forms as ma_attn_row_keys, one call instead of one per row.
+ * Replaces the reference's whole-pattern COO generators
+ * create_sliding_window_pattern (src/csrc/ma_core.cpp:34-48) and
+ * generate_sparse_pattern (src/csrc/sparse_attention.cpp:181-259), which emit
+ * (row, col) lists of the same entries.
+ */
+int64_t ma_attn_pattern_csr(const ma_attn_desc* desc, const int32_t* host_block_table,
+                            int64_t* offsets_out, int32_t* keys_out, int64_t keys_cap);
+
+/* Re-reads the kernel-selection switches (MA_ATTN_KERNEL, MA_ATTN_NO_FIXED,
+ * MA_ATTN_BWD_NO_FIXED) from the environment; the library reads them once when
+ * it loads.  For tests and A/B timing; no reference counterpart. */
+void ma_attn_reload_options(void);
+
 /* ABI version of this header (bumped on incompatible change). */
 int ma_attn_abi_version(void);
 
-#define MA_ATTN_ABI_VERSION 5
+#define MA_ATTN_ABI_VERSION 6
 
 #ifdef __cplusplus
 }

@@ -28,7 +28,10 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
+#include <set>
 #include <string>
+#include <utility>
 
 #include "../../include/ma_attn.h"
 #include "../../include/ma_features.h"
@@ -51,6 +54,60 @@ int fail(const char* fmt, ...) {
   va_end(ap);
   g_last_error = buf;
   return 1;
+}
+
+// ------------------------------------------------------------------ options
+//
+// Kernel-selection switches for tests and A/B timing, read from the
+// environment once, when the library loads (ma_attn_reload_options reads
+// them again):
+//   MA_ATTN_KERNEL=rows     every launch on the generic row kernels
+//   MA_ATTN_KERNEL=band     16-bit windows on the band kernel, not the stream kernel
+//   MA_ATTN_NO_FIXED=1      forward windows on the generic stream tiles
+//   MA_ATTN_BWD_NO_FIXED=1  backward windows on the generic stream tiles
+struct Options {
+  bool force_rows, force_band, no_fixed, bwd_no_fixed;
+};
+
+Options read_options() {
+  const char* k = getenv("MA_ATTN_KERNEL");
+  Options o;
+  o.force_rows = k && strcmp(k, "rows") == 0;
+  o.force_band = k && strcmp(k, "band") == 0;
+  o.no_fixed = getenv("MA_ATTN_NO_FIXED") != nullptr;
+  o.bwd_no_fixed = getenv("MA_ATTN_BWD_NO_FIXED") != nullptr;
+  return o;
+}
+
+Options g_opt = read_options();
+
+// ------------------------------------------------------------------ devices
+//
+// The device a launch runs on is its stream's (the null stream: the current
+// device's).
+int stream_device(hipStream_t st, int* dev) {
+  const hipError_t e = st ? hipStreamGetDevice(st, dev) : hipGetDevice(dev);
+  if (e != hipSuccess) return fail("ma_attn: cannot query the stream's device: %s", hipGetErrorString(e));
+  return 0;
+}
+
+// Raises a kernel's dynamic-LDS limit to `shm` bytes once per (kernel,
+// device), with that device current; safe from any number of threads.
+int reserve_lds(const void* kern, size_t shm, hipStream_t st) {
+  int dev = 0;
+  if (stream_device(st, &dev)) return 1;
+  static std::mutex mu;
+  static std::set<std::pair<const void*, int>> done;
+  std::lock_guard<std::mutex> lock(mu);
+  if (done.count({kern, dev})) return 0;
+  int cur = 0;
+  if (hipGetDevice(&cur) != hipSuccess) return fail("ma_attn: hipGetDevice failed");
+  if (cur != dev && hipSetDevice(dev) != hipSuccess) return fail("ma_attn: cannot select device %d", dev);
+  const hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+  if (cur != dev) (void)hipSetDevice(cur);
+  if (e != hipSuccess) return fail("ma_attn: cannot reserve %zu B of LDS: %s", shm, hipGetErrorString(e));
+  done.insert({kern, dev});
+  return 0;
 }
 
 using namespace ma_dev;
@@ -1246,7 +1303,6 @@ StreamPlan stream_plan(const ma_attn_desc* d) {
   int64_t per_stream = ma::imax64(1, slots / streams);
   if ((p.geom.right > 0 || lg) && per_stream > 1) per_stream &= ~1LL;
   p.chunk = ma::imax64(1, (p.tiles + per_stream - 1) / per_stream);
-  if (const char* e = getenv("MA_ATTN_STREAM_CHUNK")) p.chunk = ma::imax64(1, atoll(e));
   p.chunks = (p.tiles + p.chunk - 1) / p.chunk;
   p.wgs = streams * p.chunks;
   p.tok_bytes = p.geom.dil * d->num_heads * kHeadDim * (f32 ? 4 : 2);
@@ -1272,22 +1328,11 @@ bool stream_applies(const ma_attn_desc* d, const void* q, const void* k, const v
   return p.tok_bytes < (1LL << 24) && rows * p.tok_bytes + 256 < (1LL << 31);
 }
 
-const char* kernel_override() {
-  const char* s = getenv("MA_ATTN_KERNEL");  // "stream" | "band" | "rows" (testing / A-B timing)
-  return s ? s : "";
-}
-
 template <class P, int NSLOT, int FL, int FR, bool LG>
 int launch_stream_t(const StreamArgs& a, int64_t wgs, hipStream_t st) {
   const size_t shm = (size_t)(NSLOT + (LG ? 1 : 0)) * P::kSlot;
   auto kern = &stream_kernel<P, NSLOT, kStreamSG, FL, FR, LG>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)shm) != hipSuccess)
-      return fail("ma_attn: cannot reserve %zu B of LDS for the stream kernel", shm);
-    attr_set = true;
-  }
+  if (reserve_lds(reinterpret_cast<const void*>(kern), shm, st)) return 1;
   launch(!LG, kern, dim3((unsigned)wgs), dim3(256), (uint32_t)shm, st, a);  // Longformer: combine is last
   return 0;
 }
@@ -1298,7 +1343,7 @@ int launch_stream_t(const StreamArgs& a, int64_t wgs, hipStream_t st) {
 template <class P, bool LG>
 int launch_stream_any(const StreamArgs& a, int64_t slots, int64_t wgs, hipStream_t st) {
   constexpr int RS = P::kRows;
-  if (!getenv("MA_ATTN_NO_FIXED")) {
+  if (!g_opt.no_fixed) {
     if constexpr (!LG) {
       if (a.left == 63 && a.right == 0) return launch_stream_t<P, WinGeom<63, 0, RS>::NSLOT, 63, 0, LG>(a, wgs, st);
       if (a.left == 32 && a.right == 31)
@@ -1380,13 +1425,7 @@ bool block_applies(const ma_attn_desc* d, const void* q, const void* k, const vo
 template <class P>
 int launch_block_t(const BlockArgs& a, int64_t bh, hipStream_t st) {
   constexpr size_t shm = 2 * (size_t)P::kBlk;  // two block buffers (fp32: 68 KB)
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&block_row_kernel<P>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess)
-      return fail("ma_attn: cannot reserve %zu B of LDS for the block kernel", shm);
-    attr_set = true;
-  }
+  if (reserve_lds(reinterpret_cast<const void*>(&block_row_kernel<P>), shm, st)) return 1;
   launch(true, block_row_kernel<P>, dim3((unsigned)(bh * a.nbq)), dim3(256), (uint32_t)shm, st, a);
   return 0;
 }
@@ -1502,11 +1541,10 @@ int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* 
   // -16*(ceil(R/16) & 3) (queries), which fits [i-32, i+31] in two.
   const int64_t obq = -16 * (((L + 15) / 16) & 3), obkv = -16 * (((R + 15) / 16) & 3);
   const bool chunked = ma::floordiv64(63 + R - obq, 64) - ma::floordiv64(-L - obq, 64) + 1 <= 2 &&
-                       ma::floordiv64(63 + L - obkv, 64) - ma::floordiv64(-R - obkv, 64) + 1 <= 2 &&
-                       !getenv("MA_ATTN_BWD_PER_TILE");
+                       ma::floordiv64(63 + L - obkv, 64) - ma::floordiv64(-R - obkv, 64) + 1 <= 2;
   // fixed-window instantiations: causal 64 (also per residue class of a dilated window)
   // and [i-32, i+31] (cfg 2)
-  const bool no_fixed = getenv("MA_ATTN_BWD_NO_FIXED") != nullptr;
+  const bool no_fixed = g_opt.bwd_no_fixed;
   const int fixed = !chunked || no_fixed ? 0 : L == 63 && R == 0 ? 1 : L == 32 && R == 31 ? 2 : 0;
   auto kq = !chunked     ? &bwd_q_kernel<P>
             : fixed == 1 ? &bwd_q_stream_kernel<P, 63, 0>
@@ -1525,18 +1563,11 @@ int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* 
   const int64_t per_cu = ma::imax64(1, ma::imin64(2, (int64_t)(160 * 1024) / (int64_t)ma::imax64(shm_q, shm_kv)));
   const int64_t per_stream = ma::imax64(1, 2 * 256 * per_cu / streams);
   a.chunk = (int32_t)ma::imax64(1, (a.tiles + per_stream - 1) / per_stream);
-  if (const char* e = getenv("MA_ATTN_BWD_CHUNK")) a.chunk = (int32_t)ma::imax64(1, atoll(e));
   a.chunks = (int32_t)((a.tiles + a.chunk - 1) / a.chunk);
   const int64_t wgs = chunked ? streams * a.chunks : streams * a.tiles;
-  static bool attr_set[4] = {false, false, false, false};
-  if (!attr_set[variant]) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kq), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)shm_q) != hipSuccess ||
-        hipFuncSetAttribute(reinterpret_cast<const void*>(kkv), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)shm_kv) != hipSuccess)
-      return fail("ma_attn_backward: cannot reserve LDS for the backward kernels");
-    attr_set[variant] = true;
-  }
+  if (reserve_lds(reinterpret_cast<const void*>(kq), shm_q, st) ||
+      reserve_lds(reinterpret_cast<const void*>(kkv), shm_kv, st))
+    return 1;
   launch(false, kq, dim3((unsigned)wgs), dim3(256), (uint32_t)shm_q, st, a);
   launch(true, kkv, dim3((unsigned)wgs), dim3(256), (uint32_t)shm_kv, st, a);
   return 0;
@@ -1560,7 +1591,7 @@ int launch_backward(const ma_attn_desc* d, const void* q, const void* k, const v
   const T* tg = static_cast<const T*>(dout);
   const dim3 grid((unsigned)blocks), blk(256);
   const int64_t B = d->batch, H = d->num_heads, D = d->head_dim;
-  if (D == 64 && strcmp(kernel_override(), "rows") != 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
+  if (D == 64 && !g_opt.force_rows && aligned16(q) && aligned16(k) && aligned16(v) &&
       aligned16(dout) && aligned16(dq) && aligned16(dk) && aligned16(dv)) {
     // head_dim 64: the gather layout (whole-row reads, 4 rows per wave)
     const int64_t gblocks = B * H * ((d->seq_len + 15) / 16);
@@ -1594,6 +1625,9 @@ int launch_backward(const ma_attn_desc* d, const void* q, const void* k, const v
 #undef MA_BWD
   return 0;
 }
+
+int forward_launch(const ma_attn_desc* desc, const void* q, const void* k, const void* v, void* o,
+                   void* workspace, size_t workspace_bytes, hipStream_t st);
 
 uint64_t splitmix64(uint64_t* s) {
   uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
@@ -1634,12 +1668,19 @@ int ma_attn_forward(const ma_attn_desc* desc, const void* q, const void* k, cons
   const int64_t rows = desc->batch * desc->seq_len * desc->num_heads;
   if (rows == 0 || desc->head_dim == 0) return 0;
   if (!q || !k || !v || !o) return fail("ma_attn: null tensor pointer");
-  hipStream_t st = static_cast<hipStream_t>(stream);
+  return forward_launch(desc, q, k, v, o, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"
+
+namespace {
+
+int forward_launch(const ma_attn_desc* desc, const void* q, const void* k, const void* v, void* o,
+                   void* workspace, size_t workspace_bytes, hipStream_t st) {
   (void)hipGetLastError();  // launch errors below must be ours
   int rc;
-  const char* force = kernel_override();
-  const bool want_rows = strcmp(force, "rows") == 0;
-  const bool want_band = strcmp(force, "band") == 0;
+  const bool want_rows = g_opt.force_rows;
+  const bool want_band = g_opt.force_band;
   if (!want_rows && !want_band && stream_applies(desc, q, k, v, o)) {
     rc = launch_stream(desc, q, k, v, o, workspace, workspace_bytes, st);
   } else if (!want_rows && block_applies(desc, q, k, v, o)) {
@@ -1689,6 +1730,10 @@ int ma_attn_forward(const ma_attn_desc* desc, const void* q, const void* k, cons
   return 0;
 }
 
+}  // namespace
+
+extern "C" {
+
 size_t ma_attn_backward_workspace_size(const ma_attn_desc* desc) {
   g_last_error.clear();
   if (validate(desc)) return 0;
@@ -1716,7 +1761,7 @@ int ma_attn_backward(const ma_attn_desc* desc, const void* q, const void* k, con
   RowStat* stats = static_cast<RowStat*>(workspace);
   const void* ptrs[7] = {q, k, v, dout, dq, dk, dv};
   int rc;
-  if (strcmp(kernel_override(), "rows") != 0 && bwd_mfma_applies(desc, ptrs)) {
+  if (!g_opt.force_rows && bwd_mfma_applies(desc, ptrs)) {
     float* sf = reinterpret_cast<float*>(stats);
     rc = desc->dtype == MA_ATTN_BF16  ? launch_backward_mfma<HalfPath<__bf16>>(desc, ptrs, sf, st)
          : desc->dtype == MA_ATTN_F16 ? launch_backward_mfma<HalfPath<_Float16>>(desc, ptrs, sf, st)
@@ -1861,5 +1906,51 @@ int64_t ma_attn_row_keys(const ma_attn_desc* desc, const int32_t* host_block_tab
   for (int64_t t = 0; t < rk.count && t < cap; ++t) keys_out[t] = ma::key_at(pp, rk, i, t);
   return rk.count;
 }
+
+int64_t ma_attn_pattern_csr(const ma_attn_desc* desc, const int32_t* host_block_table, int64_t* offsets_out,
+                            int32_t* keys_out, int64_t keys_cap) {
+  g_last_error.clear();
+  if (validate(desc)) return -1;
+  if (desc->pattern == MA_ATTN_BLOCK_SPARSE && !host_block_table && desc->seq_len > 0) {
+    fail("ma_attn_pattern_csr: block table required");
+    return -1;
+  }
+  if (desc->pattern == MA_ATTN_INDEX_SET) {
+    fail("ma_attn_pattern_csr: an index set's keys are the caller's own input");
+    return -1;
+  }
+  const ma::PatternParams pp = params_of(desc, host_block_table);
+  const int64_t N = desc->seq_len;
+  int64_t nnz = 0;
+  for (int64_t i = 0; i < N; ++i) {
+    if (offsets_out) offsets_out[i] = nnz;
+    nnz += ma::row_keys(pp, i).count;
+  }
+  if (offsets_out) offsets_out[N] = nnz;
+  if (!keys_out) return nnz;
+  if (keys_cap < nnz) {
+    fail("ma_attn_pattern_csr: %lld keys do not fit a buffer of %lld", (long long)nnz, (long long)keys_cap);
+    return -1;
+  }
+  int64_t at = 0;
+  for (int64_t i = 0; i < N; ++i) {
+    const ma::RowKeys rk = ma::row_keys(pp, i);
+    if (pp.pattern == ma::kBlockSparse) {
+      // the row's table entries in order: whole blocks, clipped at N
+      const int64_t bs = pp.block_size, row = i / bs;
+      for (int64_t e = 0; e < pp.bpr; ++e) {
+        const int32_t c = pp.table[row * pp.bpr + e];
+        if (c < 0) continue;
+        const int64_t end = ma::imin64((int64_t)c * bs + bs, N);
+        for (int64_t j = (int64_t)c * bs; j < end; ++j) keys_out[at++] = (int32_t)j;
+      }
+    } else {
+      for (int64_t t = 0; t < rk.count; ++t) keys_out[at++] = (int32_t)ma::key_at(pp, rk, i, t);
+    }
+  }
+  return nnz;
+}
+
+void ma_attn_reload_options(void) { g_opt = read_options(); }
 
 }  // extern "C"

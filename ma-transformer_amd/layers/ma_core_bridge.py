@@ -9,17 +9,18 @@ Keeps the public surface of the reference bridge
 * ``create_attention_layer``   factory (:333-352)
 * ``pytorch_dense_attention``, ``pytorch_sparse_attention`` the PyTorch
                                reference implementations (:184-247)
-* ``pytorch_to_ma_core``, ``ma_core_to_pytorch`` converters (:157-181), live
-                               only when the reference's CPU ``ma_core`` module
-                               is importable.
+* ``pytorch_to_ma_core``, ``ma_core_to_pytorch`` converters (:157-181) to and
+                               from this package's ``ma_core`` module (host
+                               Tensors whose attention runs on the GPU kernels).
 
 Routing differs from the reference in one deliberate way: device tensors of
 every supported dtype (float32, bfloat16, float16) go to the native HIP
 kernels; the reference sent non-float32 device tensors to a Python loop
 (:77-80).  If device tensors arrive and the native library is missing, the
 call raises -- there is no silent fallback on a GPU.  CPU tensors use the
-PyTorch reference implementations (the reference's ma_core CPU engine is not
-part of this package).
+PyTorch reference implementations, as the reference's CPU branch computes on
+the host; ``ma_core`` (whose attention stages host buffers to the GPU) is
+reached through the converters, as the reference's bridge reaches it.
 
 New, keyword-only constructor arguments select the benchmark patterns and
 default to the reference behaviour: ``pattern`` ("sliding", "dense",
@@ -57,9 +58,9 @@ def _try_import_sparse_ext():
 sparse_attention_cuda = _try_import_sparse_ext()
 _HAS_SPARSE_CUDA = sparse_attention_cuda is not None
 
-try:  # the reference's CPU engine, only for the two converters
+try:  # this package's ma_core module (the reference's src/csrc surface), for the two converters
     import ma_core  # type: ignore  # noqa: F401
-except ImportError:  # pragma: no cover - depends on the environment
+except ImportError:  # pragma: no cover - without libma_attn.so
     ma_core = None
 
 
@@ -221,12 +222,9 @@ class MACoreAttentionFunction(torch.autograd.Function):
 
 
 def pytorch_to_ma_core(tensor: torch.Tensor):
-    """Convert a tensor to a reference ``ma_core.Tensor`` (:157-168).
-
-    Requires the reference's CPU module ``ma_core``; not shipped here.
-    """
+    """Convert a tensor to an ``ma_core.Tensor`` (host float32 copy; :157-168)."""
     if ma_core is None:
-        raise ImportError("ma_core (the reference CPU engine) is not installed")
+        raise ImportError("ma_core needs libma_attn.so, which is not loaded")
     cpu_tensor = tensor.detach().cpu().contiguous()
     mc = ma_core.create_tensor(list(cpu_tensor.shape))
     mc.copy_from_numpy(cpu_tensor.numpy())
@@ -234,7 +232,7 @@ def pytorch_to_ma_core(tensor: torch.Tensor):
 
 
 def ma_core_to_pytorch(mc_tensor, device: torch.device, dtype: torch.dtype) -> torch.Tensor:
-    """Convert a reference ``ma_core.Tensor`` back to torch (:171-181)."""
+    """Convert an ``ma_core.Tensor`` back to torch (:171-181)."""
     out = torch.from_numpy(mc_tensor.to_numpy())
     if out.dtype != dtype:
         out = out.to(dtype)

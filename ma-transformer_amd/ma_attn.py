@@ -18,7 +18,7 @@ LIB_PATH = os.environ.get("MA_ATTN_LIB", os.path.join(_HERE, "libma_attn.so"))
 
 F32, BF16, F16 = 0, 1, 2
 SLIDING, DENSE, BLOCK_SPARSE, LONGFORMER, INDEX_SET = 0, 1, 2, 3, 4
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 
@@ -84,6 +84,11 @@ def _open():
     lib.ma_attn_row_keys.restype = ctypes.c_int64
     lib.ma_attn_row_keys.argtypes = [ctypes.POINTER(Desc), ctypes.c_void_p, ctypes.c_int64,
                                      ctypes.c_void_p, ctypes.c_int64]
+    lib.ma_attn_pattern_csr.restype = ctypes.c_int64
+    lib.ma_attn_pattern_csr.argtypes = [ctypes.POINTER(Desc), ctypes.c_void_p, ctypes.c_void_p,
+                                        ctypes.c_void_p, ctypes.c_int64]
+    lib.ma_attn_reload_options.restype = None
+    lib.ma_attn_reload_options.argtypes = []
     if lib.ma_attn_abi_version() != ABI_VERSION:
         raise ImportError("libma_attn.so ABI version mismatch; rebuild it")
     return lib
@@ -185,6 +190,30 @@ def row_keys(desc: Desc, i: int, host_table: torch.Tensor | None = None) -> list
     return list(buf[:n])
 
 
+def pattern_csr(desc: Desc, host_table: torch.Tensor | None = None):
+    """Every row's key list of desc as CSR (host int64 offsets [N+1], int32
+    keys), from the engine's closed forms in one call (ma_attn_pattern_csr)."""
+    N = int(desc.seq_len)
+    offsets = torch.empty(N + 1, dtype=torch.int64)
+    tptr = None
+    if host_table is not None:
+        host_table = host_table.to(torch.int32).contiguous()
+        tptr = host_table.data_ptr()
+    nnz = LIB.ma_attn_pattern_csr(ctypes.byref(desc), tptr, offsets.data_ptr(), None, 0)
+    if nnz < 0:
+        raise ValueError(last_error())
+    keys = torch.empty(max(int(nnz), 1), dtype=torch.int32)
+    got = LIB.ma_attn_pattern_csr(ctypes.byref(desc), tptr, None, keys.data_ptr(), int(nnz))
+    if got != nnz:
+        raise ValueError(last_error())
+    return offsets, keys[:nnz]
+
+
+def reload_options() -> None:
+    """Re-read the MA_ATTN_* kernel-selection switches from the environment."""
+    LIB.ma_attn_reload_options()
+
+
 def default_scale(D: int) -> float:
     """1.0f / sqrtf((float)D) in float32, as src/csrc/ma_core.cpp:188."""
     import numpy as np
@@ -192,5 +221,5 @@ def default_scale(D: int) -> float:
 
 
 __all__ = ["LIB", "Desc", "make_desc", "forward_raw", "validate", "workspace_size",
-           "block_table", "row_keys", "last_error", "DTYPES", "default_scale",
+           "block_table", "row_keys", "pattern_csr", "reload_options", "last_error", "DTYPES", "default_scale",
            "SLIDING", "DENSE", "BLOCK_SPARSE", "LONGFORMER", "INDEX_SET", "F32", "BF16", "F16"]

@@ -208,7 +208,9 @@ class BlockTable:
             raise RuntimeError("block_size must be >= 1")
         nb = (self.seq_len + self.block_size - 1) // self.block_size
         dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
-        self.tensor = _validated_table(block_table, nb).to(dev)
+        self.host = _validated_table(block_table, nb)  # checked host copy (index enumeration)
+        self.tensor = self.host.to(dev)
+        self._index_set = None  # the table's key sets as an IndexSet, built on first use
 
     @property
     def width(self) -> int:
@@ -325,32 +327,45 @@ class IndexSet:
 _pattern_sets: dict = {}
 
 
+def _enumerated_set(code: int, seq_len: int, device, host_table=None, **kw) -> "IndexSet":
+    tptr = host_table.data_ptr() if host_table is not None else 0  # host pointer: enumeration only
+    if host_table is not None:
+        kw["blocks_per_row"] = int(host_table.shape[1])
+    desc = _ma.make_desc(1, seq_len, 1, 64, _ma.F32, code, block_table_ptr=tptr, **kw)
+    offsets, keys = _ma.pattern_csr(desc, host_table)
+    return IndexSet(offsets, keys, seq_len, device)
+
+
 def pattern_index_set(pattern: str, seq_len: int, device, **kw) -> IndexSet:
     """The key sets of a closed-form pattern ("block_sparse" with block_table=
     and block_size=, "longformer" with left=, right=, num_global=) as an
-    IndexSet, from the engine's own enumerator (ma_attn_row_keys), so its
+    IndexSet, from the engine's own enumerator (ma_attn_pattern_csr), so its
     backward (index_set_backward) is the exact gradient of that pattern's
-    forward.  Cached per pattern, length and device."""
-    code = {"block_sparse": _ma.BLOCK_SPARSE, "longformer": _ma.LONGFORMER}[pattern]
-    table = kw.pop("block_table", None)
-    host_table = None
-    if table is not None:
-        host_table = (table.tensor if isinstance(table, BlockTable) else torch.as_tensor(table)) \
-            .detach().to("cpu", torch.int32).contiguous()
-        kw["blocks_per_row"] = int(host_table.shape[1])
-    key = (pattern, int(seq_len), str(device), tuple(sorted(kw.items())),
-           None if host_table is None else host_table.numpy().tobytes())
+    forward.  A BlockTable keeps its set (built on first use, no host transfer
+    after that); Longformer sets are cached per geometry and device; a plain
+    tensor table is copied to the host and enumerated at every call."""
+    if pattern == "block_sparse":
+        table = kw.pop("block_table")
+        bs = int(kw.pop("block_size", 64))
+        if isinstance(table, BlockTable):
+            if table.seq_len != seq_len or table.block_size != bs:
+                raise RuntimeError("BlockTable was made for another sequence length or block size")
+            hit = table._index_set
+            if hit is None or hit.offsets.device != torch.device(device):
+                hit = table._index_set = _enumerated_set(_ma.BLOCK_SPARSE, seq_len, device, table.host,
+                                                         block_size=bs)
+            return hit
+        nb = (int(seq_len) + bs - 1) // bs
+        return _enumerated_set(_ma.BLOCK_SPARSE, seq_len, device, _validated_table(torch.as_tensor(table), nb),
+                               block_size=bs)
+    if pattern != "longformer":
+        raise ValueError(f"no closed-form index set for pattern {pattern!r}")
+    key = (int(seq_len), str(device), tuple(sorted(kw.items())))
     hit = _pattern_sets.get(key)
     if hit is None:
         if len(_pattern_sets) > 16:
             _pattern_sets.clear()
-        tptr = host_table.data_ptr() if host_table is not None else 0  # host pointer: enumeration only
-        desc = _ma.make_desc(1, seq_len, 1, 64, _ma.F32, code, block_table_ptr=tptr, **kw)
-        rows = [_ma.row_keys(desc, i, host_table) for i in range(seq_len)]
-        offsets = torch.zeros(seq_len + 1, dtype=torch.int64)
-        offsets[1:] = torch.cumsum(torch.tensor([len(r) for r in rows], dtype=torch.int64), 0)
-        keys = torch.tensor([j for r in rows for j in r], dtype=torch.int32)
-        hit = _pattern_sets[key] = IndexSet(offsets, keys, seq_len, device)
+        hit = _pattern_sets[key] = _enumerated_set(_ma.LONGFORMER, seq_len, device, **kw)
     return hit
 
 

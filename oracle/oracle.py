@@ -275,6 +275,8 @@ def _load_ref():
         lib.ref_sliding_pattern.restype = ctypes.c_int64
         lib.ref_sliding_pattern.argtypes = [ctypes.c_int64, ctypes.c_int64,
                                             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+        lib.ref_pattern_statistics.restype = ctypes.c_int64
+        lib.ref_pattern_statistics.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_char_p, ctypes.c_int64]
         _ref = lib
     return _ref
 
@@ -321,3 +323,13 @@ def ref_sliding_pattern(N: int, w: int):
     if n < 0:
         raise RuntimeError("reference create_sliding_window_pattern raised")
     return rows[:n], cols[:n]
+
+
+def ref_pattern_statistics(N: int, w: int) -> str:
+    """The reference's get_pattern_statistics of create_sliding_window_pattern(N, w)."""
+    lib = _load_ref()
+    buf = ctypes.create_string_buffer(1024)
+    n = lib.ref_pattern_statistics(N, w, buf, 1024)
+    if n < 0 or n >= 1024:
+        raise RuntimeError("reference get_pattern_statistics raised")
+    return buf.value.decode()

@@ -10,10 +10,12 @@
 //   ma_core::compute_sparse_attention   ma_core.cpp:160-246
 //   ma_core::compute_dense_attention    ma_core.cpp:66-157
 //   ma_core::create_sliding_window_pattern  ma_core.cpp:34-48
+//   ma_core::get_pattern_statistics         ma_core.cpp:51-63
 // so tests can hold the oracle restatement against the reference's own bits.
 #include <cstdint>
 #include <cstring>
 #include <exception>
+#include <string>
 #include <vector>
 
 #include "ma_core.hpp"
@@ -59,6 +61,23 @@ extern "C" int64_t ref_sliding_pattern(int64_t N, int64_t w, int64_t* rows, int6
     for (int64_t e = 0; e < n && e < cap; ++e) {
       rows[e] = p.row_indices[e];
       cols[e] = p.col_indices[e];
+    }
+    return n;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
+// get_pattern_statistics(create_sliding_window_pattern(N, w)) as a C string;
+// returns its length (written up to cap - 1 bytes plus a NUL), -1 on error.
+extern "C" int64_t ref_pattern_statistics(int64_t N, int64_t w, char* out, int64_t cap) {
+  try {
+    const std::string s = ma_core::get_pattern_statistics(ma_core::create_sliding_window_pattern(N, w));
+    const int64_t n = static_cast<int64_t>(s.size());
+    if (cap > 0) {
+      const int64_t m = n < cap - 1 ? n : cap - 1;
+      std::memcpy(out, s.data(), static_cast<size_t>(m));
+      out[m] = 0;
     }
     return n;
   } catch (const std::exception&) {

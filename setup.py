@@ -50,7 +50,7 @@ setup(
     version="0.1.0",
     description="MI355X sparse-attention forward (drop-in for ma-transformer's sparse_attention_cuda)",
     package_dir={"": "ma-transformer_amd"},
-    py_modules=["sparse_attention_cuda", "ma_attn"],
+    py_modules=["sparse_attention_cuda", "ma_attn", "ma_core", "model", "tick_features"],
     packages=["layers"],
     cmdclass={"build_ext": build_hip, "build_py": build_py},
     python_requires=">=3.9",

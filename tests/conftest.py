@@ -31,3 +31,18 @@ def oracle():
     if not os.path.exists(O.LIB_PATH):
         O.build()
     return O
+
+
+@pytest.fixture
+def kernel_env(monkeypatch):
+    """Set MA_ATTN_* kernel-selection switches for one test: the library reads
+    them when it loads, so they are re-read after setting and after the test."""
+    import ma_attn
+
+    def set_env(name, value):
+        monkeypatch.setenv(name, value)
+        ma_attn.reload_options()
+
+    yield set_env
+    monkeypatch.undo()
+    ma_attn.reload_options()

@@ -10,11 +10,14 @@ so the committed numbers are the reference's bits, not this repo's:
   ref_sparse_s33_w0.npz   (2,33,2,16) W=0 (O must equal V)
   ref_dense_s32.npz       (1,32,2,16) causal and non-causal compute_dense_attention
   ref_patterns.npz        nnz of create_sliding_window_pattern for
-                          (4,4), (4,10), (16,3), (2,1), (1024,64)
+                          (4,4), (4,10), (16,3), (2,1), (1024,64), and the (row, col)
+                          entries for the small (N, w) cases listed in `small`
+  ref_pattern_stats.json  get_pattern_statistics strings of sliding patterns
   block_table_seed1234_nb256_r2.bin  int32 [256,4]: the frozen block table of the
                           block-sparse config (seed 1234, 2 random blocks per row),
                           from oracle.block_table (SplitMix64 spec in oracle.c)
 """
+import json
 import os
 import sys
 
@@ -57,7 +60,19 @@ def main():
 
     cases = np.array([(4, 4), (4, 10), (16, 3), (2, 1), (1024, 64)], dtype=np.int64)
     nnz = np.array([len(O.ref_sliding_pattern(int(n), int(w))[0]) for n, w in cases], dtype=np.int64)
-    np.savez(os.path.join(HERE, "ref_patterns.npz"), cases=cases, nnz=nnz)
+    # the COO entries themselves, in the reference's order, for the small cases
+    small = np.array([(4, 4), (4, 10), (16, 3), (2, 1), (8, 2), (5, 0), (6, -1)], dtype=np.int64)
+    coo = {}
+    for n, w in small:
+        r, c = O.ref_sliding_pattern(int(n), int(w))
+        coo[f"rows_{n}_{w}"], coo[f"cols_{n}_{w}"] = r, c
+    np.savez(os.path.join(HERE, "ref_patterns.npz"), cases=cases, nnz=nnz, small=small, **coo)
+
+    # get_pattern_statistics strings (ma_core.cpp:51-63) of create_sliding_window_pattern
+    stats = {f"{n},{w}": O.ref_pattern_statistics(n, w)
+             for n, w in ((16, 3), (4, 4), (8, 1), (1024, 64), (7, 2), (100, 10))}
+    with open(os.path.join(HERE, "ref_pattern_stats.json"), "w") as f:
+        json.dump(stats, f, indent=1, sort_keys=True)
 
     O.block_table(1234, 256, 2).astype("<i4").tofile(
         os.path.join(HERE, "block_table_seed1234_nb256_r2.bin"))

@@ -18,7 +18,7 @@ def _run(code: str):
     return subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=300)
 
 
-@pytest.mark.parametrize("module", ["ma_attn", "sparse_attention_cuda"])
+@pytest.mark.parametrize("module", ["ma_attn", "sparse_attention_cuda", "ma_core"])
 def test_engine_modules_refuse_without_library(module):
     r = _run(f"import {module}")
     assert r.returncode != 0

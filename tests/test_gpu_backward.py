@@ -147,10 +147,10 @@ def test_dense_backward_mfma(ext, oracle, N, causal, dtype):
 
 @pytest.mark.parametrize("N,left,right,dil", [(300, 63, 0, 1), (257, 32, 31, 4), (129, 2, 7, 3)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_sliding_backward_row_kernels(ext, oracle, monkeypatch, N, left, right, dil, dtype):
+def test_sliding_backward_row_kernels(ext, oracle, kernel_env, N, left, right, dil, dtype):
     """The VALU row kernels for head_dim 64 (the MFMA path's cases), forced
     with MA_ATTN_KERNEL=rows, stay correct."""
-    monkeypatch.setenv("MA_ATTN_KERNEL", "rows")
+    kernel_env("MA_ATTN_KERNEL", "rows")
     shape = (2, N, 3, 64)
     (q, k, v, g), up = _case(shape, 860 + N, dtype)
     got = ext.sliding_backward(q, k, v, g, left, right, dil)
@@ -176,10 +176,10 @@ def test_backward_chunked(ext, oracle, N, H, left, right, dil, dtype):
 @pytest.mark.parametrize("N,H,left,right,dil", [(5000, 16, 63, 0, 1), (4099, 8, 63, 0, 4), (4000, 8, 32, 31, 1),
                                                  (3001, 8, 32, 31, 4)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_backward_chunked_generic(ext, oracle, monkeypatch, N, H, left, right, dil, dtype):
+def test_backward_chunked_generic(ext, oracle, kernel_env, N, H, left, right, dil, dtype):
     """The bands with fixed-window tiles (causal 64, [i-32, i+31]) on the
     generic stream tiles (MA_ATTN_BWD_NO_FIXED) stay correct."""
-    monkeypatch.setenv("MA_ATTN_BWD_NO_FIXED", "1")
+    kernel_env("MA_ATTN_BWD_NO_FIXED", "1")
     shape = (2, N, H, 64)
     (q, k, v, g), up = _case(shape, 890 + N + dil, dtype)
     got = ext.sliding_backward(q, k, v, g, left, right, dil)
