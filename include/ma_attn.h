@@ -201,6 +201,23 @@ int64_t ma_attn_row_keys(const ma_attn_desc* desc, const int32_t* host_block_tab
 int64_t ma_attn_pattern_csr(const ma_attn_desc* desc, const int32_t* host_block_table,
                             int64_t* offsets_out, int32_t* keys_out, int64_t keys_cap);
 
+/*
+ * ma_attn_forward for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference.  It takes no workspace and allocates
+ * nothing: the only kernel that needs scratch (the Longformer stream kernel's
+ * per-chunk partials, ma_attn_workspace_size(desc) bytes) uses a static device
+ * array of MA_ATTN_NOALLOC_SCRATCH_BYTES that the library holds on every GPU
+ * it runs on until the process ends.  A call needing more is rejected with a
+ * message and launches nothing.  Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (concurrent streams or threads) race.
+ * Outputs are identical to ma_attn_forward's on the same inputs.
+ */
+int ma_attn_forward_noalloc(const ma_attn_desc* desc, const void* q, const void* k,
+                            const void* v, void* o, void* stream);
+
+#define MA_ATTN_NOALLOC_SCRATCH_BYTES (8u << 20)
+
 /* Re-reads the kernel-selection switches (MA_ATTN_KERNEL, MA_ATTN_NO_FIXED,
  * MA_ATTN_BWD_NO_FIXED) from the environment; the library reads them once when
  * it loads.  For tests and A/B timing; no reference counterpart. */

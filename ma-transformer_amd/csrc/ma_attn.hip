@@ -42,6 +42,13 @@
 #include "backward_kernel.h"
 #include "tick_features.h"
 
+// Scratch of ma_attn_forward_noalloc: device memory the library owns, one
+// copy per GPU (each at its own address), held until the process ends.  Host
+// code never names this array in a launch or a copy: its name is a host-side
+// stand-in, not a device address.  scratch_of_stream() gives the address on
+// the stream's device (hipGetSymbolAddress, once per device).
+static __device__ __align__(256) unsigned char scratch[MA_ATTN_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -1626,6 +1633,34 @@ int launch_backward(const ma_attn_desc* d, const void* q, const void* k, const v
   return 0;
 }
 
+// Device address of `scratch` on the stream's device, looked up once per
+// device with that device current.
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+
+int scratch_of_stream(hipStream_t st, void** out) {
+  int dev = 0;
+  if (stream_device(st, &dev)) return 1;
+  if (dev < 0 || dev >= kMaxDevices) return fail("ma_attn: device %d out of range", dev);
+  std::call_once(g_scratch_once[dev], [dev] {
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+    void* ptr = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    g_scratch_err[dev] = e;
+    g_scratch_ptr[dev] = e == hipSuccess ? ptr : nullptr;
+  });
+  if (g_scratch_err[dev] != hipSuccess || !g_scratch_ptr[dev])
+    return fail("ma_attn: cannot locate the static scratch on device %d: %s", dev,
+                hipGetErrorString(g_scratch_err[dev]));
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
 int forward_launch(const ma_attn_desc* desc, const void* q, const void* k, const void* v, void* o,
                    void* workspace, size_t workspace_bytes, hipStream_t st);
 
@@ -1669,6 +1704,26 @@ int ma_attn_forward(const ma_attn_desc* desc, const void* q, const void* k, cons
   if (rows == 0 || desc->head_dim == 0) return 0;
   if (!q || !k || !v || !o) return fail("ma_attn: null tensor pointer");
   return forward_launch(desc, q, k, v, o, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int ma_attn_forward_noalloc(const ma_attn_desc* desc, const void* q, const void* k, const void* v, void* o,
+                            void* stream) {
+  g_last_error.clear();
+  if (validate(desc)) return 1;
+  const int64_t rows = desc->batch * desc->seq_len * desc->num_heads;
+  if (rows == 0 || desc->head_dim == 0) return 0;
+  if (!q || !k || !v || !o) return fail("ma_attn: null tensor pointer");
+  // the scratch the kernels that take this call would need (the Longformer
+  // stream kernel's per-chunk partials; nothing for every other kernel)
+  const size_t need = stream_applies(desc, q, k, v, o) ? (size_t)stream_plan(desc).partial_bytes : 0;
+  if (need > (size_t)MA_ATTN_NOALLOC_SCRATCH_BYTES)
+    return fail("ma_attn_forward_noalloc: this call needs %zu bytes of scratch, above the %zu bytes of the "
+                "library's static scratch; use ma_attn_forward with a workspace",
+                need, (size_t)MA_ATTN_NOALLOC_SCRATCH_BYTES);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  if (need > 0 && scratch_of_stream(st, &ws)) return 1;
+  return forward_launch(desc, q, k, v, o, ws, need, st);
 }
 
 }  // extern "C"

@@ -87,6 +87,8 @@ def _open():
     lib.ma_attn_pattern_csr.restype = ctypes.c_int64
     lib.ma_attn_pattern_csr.argtypes = [ctypes.POINTER(Desc), ctypes.c_void_p, ctypes.c_void_p,
                                         ctypes.c_void_p, ctypes.c_int64]
+    lib.ma_attn_forward_noalloc.restype = ctypes.c_int
+    lib.ma_attn_forward_noalloc.argtypes = [ctypes.POINTER(Desc)] + [ctypes.c_void_p] * 5
     lib.ma_attn_reload_options.restype = None
     lib.ma_attn_reload_options.argtypes = []
     if lib.ma_attn_abi_version() != ABI_VERSION:
@@ -209,9 +211,20 @@ def pattern_csr(desc: Desc, host_table: torch.Tensor | None = None):
     return offsets, keys[:nnz]
 
 
+def forward_noalloc_raw(desc: Desc, q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, stream: int = 0) -> None:
+    """ma_attn_forward_noalloc: no workspace, no allocation (the library's
+    static scratch).  Raises RuntimeError on rejection."""
+    rc = LIB.ma_attn_forward_noalloc(ctypes.byref(desc), q_ptr, k_ptr, v_ptr, o_ptr, stream or None)
+    if rc != 0:
+        raise RuntimeError(last_error())
+
+
 def reload_options() -> None:
     """Re-read the MA_ATTN_* kernel-selection switches from the environment."""
     LIB.ma_attn_reload_options()
+
+
+NOALLOC_SCRATCH_BYTES = 8 << 20  # MA_ATTN_NOALLOC_SCRATCH_BYTES
 
 
 def default_scale(D: int) -> float:
@@ -220,6 +233,6 @@ def default_scale(D: int) -> float:
     return float(np.float32(1.0) / np.sqrt(np.float32(D)))
 
 
-__all__ = ["LIB", "Desc", "make_desc", "forward_raw", "validate", "workspace_size",
+__all__ = ["LIB", "Desc", "make_desc", "forward_raw", "forward_noalloc_raw", "validate", "workspace_size",
            "block_table", "row_keys", "pattern_csr", "reload_options", "last_error", "DTYPES", "default_scale",
            "SLIDING", "DENSE", "BLOCK_SPARSE", "LONGFORMER", "INDEX_SET", "F32", "BF16", "F16"]
