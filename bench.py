@@ -28,6 +28,11 @@ GPU, ma_tick_features) over 16M synthetic ticks; value = ticks/s, roofline =
 statistics kernel and again by the write kernel, 5 float32 written) over the
 pass's stamped duration.
 
+Workload "encoder_layer": the reference model's inference (batch 64, sequence
+10, model_dim 64, 4 layers) with each encoder layer as one fused HIP kernel,
+against the same weights run as the layer's separate operations; value =
+sequences/s, with per-layer latencies of both forms.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
                        [--pass forward|backward]
 """
@@ -292,6 +297,103 @@ def bench_ticks(args) -> int:
     return 0
 
 
+ENC = dict(batch=64, seq_len=10, input_dim=5, model_dim=64, num_layers=4, window=3)
+METRIC_ENC = "TransformerModel inference sequences/sec (reference config, eval), 1 GPU"
+
+
+def bench_encoder(args) -> int:
+    """The reference model's inference at its training configuration
+    (configs/default_config.yaml: batch 64, sequence 10, input_dim 5;
+    model_dim 64 and 4 layers from its grid), each encoder layer as one fused
+    HIP kernel (fused_layers=True) against the same weights run as the
+    layer's separate operations.  value = sequences/s of the fused model;
+    per-layer latencies of both forms are reported beside it.
+
+    --layer-form fused|ops times only that form's model forward (warmup +
+    steps forwards and nothing else), so a kernel trace of the run gives the
+    launches of one forward: each kernel's calls / (warmup + steps)."""
+    import torch
+    import model as M
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    torch.manual_seed(0)
+    c = ENC
+    fused = M.TransformerModel(input_dim=c["input_dim"], model_dim=c["model_dim"], num_heads=2,
+                               num_layers=c["num_layers"], fused_layers=True).to(dev).eval()
+    ops = M.TransformerModel(input_dim=c["input_dim"], model_dim=c["model_dim"], num_heads=2,
+                             num_layers=c["num_layers"], fused_layers=False).to(dev).eval()
+    ops.load_state_dict(fused.state_dict())
+    src = torch.randn(c["batch"], c["seq_len"], c["input_dim"], device=dev)
+    x = torch.randn(c["batch"], c["seq_len"], c["model_dim"], device=dev)
+    layer_f, layer_o = fused.encoder_layers[0], ops.encoder_layers[0]
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn, steps):
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record(stream)
+        for _ in range(steps):
+            fn()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / steps
+
+    form = args.layer_form
+    base = {"unit": "sequences/s", "n_gpus": 1, "steps": args.steps, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic N(0,1) ticks, random-init weights of the reference architecture",
+            "device": torch.cuda.get_device_name(dev)}
+    if form != "both":
+        m = fused if form == "fused" else ops
+        with torch.no_grad():
+            warm = args.warmup if args.warmup is not None else 100
+            for _ in range(warm):
+                m(src)
+            ms = timed(lambda: m(src), args.steps)
+        print(json.dumps({"metric": METRIC_ENC + f" ({form} layers)", "value": c["batch"] / (ms * 1e-3),
+                          "warmup": warm, "ms_per_step": ms, **base,
+                          "config": {"workload": f"TransformerModel eval forward, {form} encoder layers", **c},
+                          "forwards_run": warm + args.steps}), flush=True)
+        return 0
+
+    with torch.no_grad():
+        err = (fused(src) - ops(src)).abs().max().item()
+        for fn in (lambda: fused(src), lambda: ops(src), lambda: layer_f(x), lambda: layer_o(x)):
+            args.warmup = run_warmup(args.warmup, lambda i: fn())
+        ms_model_f = timed(lambda: fused(src), args.steps)
+        ms_model_o = timed(lambda: ops(src), args.steps)
+        ms_layer_f = timed(lambda: layer_f(x), args.steps)
+        ms_layer_o = timed(lambda: layer_o(x), args.steps)
+        # the kernel alone: one launch per layer, back to back on the stream
+        import ma_attn as _ma
+        out = torch.empty_like(x)
+        L = M._layer_desc(layer_f, c["batch"], c["seq_len"], dev)
+        raw = stream.cuda_stream
+        ms_kernel = timed(lambda: _ma.encoder_layer_forward_raw(L, x.data_ptr(), 0, out.data_ptr(), raw),
+                          args.steps)
+    rows, d, f = c["batch"] * c["seq_len"], c["model_dim"], 4 * c["model_dim"]
+    keys = sum(min(c["seq_len"] - 1, i + c["window"]) - max(0, i - c["window"]) + 1
+               for i in range(c["seq_len"])) * c["batch"]
+    flops = 4 * d * keys + 2 * rows * d * f * 2  # attention (Q.K^T, P.V) + the two Linear layers
+    tflops = flops / (ms_kernel * 1e-3) / 1e12
+    print(json.dumps({
+        "metric": METRIC_ENC, "value": c["batch"] / (ms_model_f * 1e-3), "warmup": args.warmup,
+        "ms_per_step": ms_model_f, **base,
+        "config": {"workload": "TransformerModel eval forward, fused encoder layers", **c},
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": tflops / MFMA_F32_PEAK_TFLOPS, "traffic": None,
+                     "note": "launch-latency bound: 40 workgroups of 16 tokens"},
+        "model_ms_fused": ms_model_f, "model_ms_ops": ms_model_o,
+        "layer_us_fused": ms_layer_f * 1e3, "layer_us_ops": ms_layer_o * 1e3,
+        "layer_kernel_us_back_to_back": ms_kernel * 1e3, "flops_per_layer": flops,
+        "max_abs_diff_fused_vs_ops": err,
+    }), flush=True)
+    return 0
+
+
 def run_warmup(warmup, step) -> int:
     """Untimed launches before the timed region; returns how many ran.
 
@@ -326,9 +428,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=None,
                     help="untimed launches first (default: ~0.1 s of launches, 20..2000, so the GPU's "
                          "clocks settle before the timed region)")
-    ap.add_argument("--workload", default="target", choices=sorted(WORKLOADS) + ["ticks"])
+    ap.add_argument("--workload", default="target", choices=sorted(WORKLOADS) + ["ticks", "encoder_layer"])
     ap.add_argument("--sets", type=int, default=0, help="input sets rotated (0: enough for >1 GB)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--layer-form", choices=["both", "fused", "ops"], default="both",
+                    help="encoder_layer workload: time both model forms (default) or only one")
     ap.add_argument("--pass", dest="which", choices=["forward", "backward"], default="forward",
                     help="backward: dQ, dK, dV from (Q, K, V, dO) (sliding and dense patterns)")
     args = ap.parse_args()
@@ -338,6 +442,8 @@ def main() -> int:
         return 2
     if args.workload == "ticks":
         return bench_ticks(args)
+    if args.workload == "encoder_layer":
+        return bench_encoder(args)
 
     import torch
     import sparse_attention_cuda as ext

@@ -10,16 +10,22 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
-SRC = os.path.join(PKG_DIR, "csrc", "ma_attn.hip")
-HEADERS = [os.path.join(PKG_DIR, "csrc", h) for h in ("pattern.h", "device_common.h", "stream_kernel.h",
-                                                         "block_kernel.h", "backward_kernel.h",
-                                                         "tick_features.h")] + \
-    [os.path.join(REPO_DIR, "include", h) for h in ("ma_attn.h", "ma_features.h")]
+CSRC = os.path.join(PKG_DIR, "csrc")
+# one object per translation unit, compiled in parallel, then linked
+SOURCES = [os.path.join(CSRC, f) for f in ("ma_attn.hip", "encoder_layer.hip")]
+HEADERS = [os.path.join(CSRC, h) for h in ("pattern.h", "device_common.h", "stream_kernel.h",
+                                           "block_kernel.h", "backward_kernel.h", "tick_features.h")] + \
+    [os.path.join(REPO_DIR, "include", h) for h in ("ma_attn.h", "ma_features.h", "ma_encoder.h")]
 LIB = os.path.join(PKG_DIR, "libma_attn.so")
+BUILD_DIR = os.path.join(PKG_DIR, "_build")
 ARCH = os.environ.get("MA_ATTN_ARCH", "gfx950")
+
+# packed-FP32 VALU forms are kept out of the device code on purpose
+FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
 def hipcc() -> str:
@@ -29,20 +35,16 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm toolchain required to build libma_attn.so)")
 
 
-def command(out: str = LIB) -> list:
-    return [
-        hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
-        # packed-FP32 VALU forms are kept out of the device code on purpose
-        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        "-I", os.path.join(REPO_DIR, "include"),
-        "-o", out, SRC,
-    ]
+def compile_command(src: str, obj: str) -> list:
+    return [hipcc(), f"--offload-arch={ARCH}", *FLAGS, "-I", os.path.join(REPO_DIR, "include"),
+            "-c", "-o", obj, src]
 
 
-def build(verbose: bool = True) -> str:
-    """Always recompiles; writes atomically so a loaded library is never torn."""
-    tmp = LIB + ".tmp"
-    cmd = command(tmp)
+def link_command(objs: list, out: str = LIB) -> list:
+    return [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", out, *objs]
+
+
+def _run(cmd: list, verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -52,6 +54,18 @@ def build(verbose: bool = True) -> str:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
     if err.strip() and verbose:
         print(err, file=sys.stderr)
+
+
+def build(verbose: bool = True) -> str:
+    """Always recompiles every translation unit (in parallel) and links;
+    writes atomically so a loaded library is never torn."""
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    objs = [os.path.join(BUILD_DIR, os.path.basename(s) + ".o") for s in SOURCES]
+    with ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
+        for f in [pool.submit(_run, compile_command(s, o), verbose) for s, o in zip(SOURCES, objs)]:
+            f.result()
+    tmp = LIB + ".tmp"
+    _run(link_command(objs, tmp), verbose)
     os.replace(tmp, LIB)
     return LIB
 

@@ -63,6 +63,20 @@ int fail(const char* fmt, ...) {
   return 1;
 }
 
+}  // namespace
+
+// The library's one error channel, shared with the other translation units
+// (ma_attn_last_error() reads it).
+namespace ma_host {
+void clear_error() { g_last_error.clear(); }
+int set_error(const char* msg) {
+  g_last_error = msg;
+  return 1;
+}
+}  // namespace ma_host
+
+namespace {
+
 // ------------------------------------------------------------------ options
 //
 // Kernel-selection switches for tests and A/B timing, read from the

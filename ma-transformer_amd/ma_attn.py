@@ -52,6 +52,28 @@ class Desc(ctypes.Structure):
     ]
 
 
+class EncoderLayer(ctypes.Structure):
+    """Mirror of ``ma_encoder_layer`` (include/ma_encoder.h)."""
+
+    _fields_ = [
+        ("batch", ctypes.c_int64),
+        ("seq_len", ctypes.c_int64),
+        ("d_model", ctypes.c_int64),
+        ("d_ff", ctypes.c_int64),
+        ("window", ctypes.c_int64),
+        ("ln_eps", ctypes.c_float),
+        ("reserved", ctypes.c_int32),
+        ("norm1_weight", ctypes.c_void_p),
+        ("norm1_bias", ctypes.c_void_p),
+        ("linear1_weight", ctypes.c_void_p),
+        ("linear1_bias", ctypes.c_void_p),
+        ("linear2_weight", ctypes.c_void_p),
+        ("linear2_bias", ctypes.c_void_p),
+        ("norm2_weight", ctypes.c_void_p),
+        ("norm2_bias", ctypes.c_void_p),
+    ]
+
+
 def _open():
     if not os.path.exists(LIB_PATH):
         raise ImportError(
@@ -89,6 +111,8 @@ def _open():
                                         ctypes.c_void_p, ctypes.c_int64]
     lib.ma_attn_forward_noalloc.restype = ctypes.c_int
     lib.ma_attn_forward_noalloc.argtypes = [ctypes.POINTER(Desc)] + [ctypes.c_void_p] * 5
+    lib.ma_encoder_layer_forward.restype = ctypes.c_int
+    lib.ma_encoder_layer_forward.argtypes = [ctypes.POINTER(EncoderLayer)] + [ctypes.c_void_p] * 4
     lib.ma_attn_reload_options.restype = None
     lib.ma_attn_reload_options.argtypes = []
     if lib.ma_attn_abi_version() != ABI_VERSION:
@@ -219,6 +243,15 @@ def forward_noalloc_raw(desc: Desc, q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: i
         raise RuntimeError(last_error())
 
 
+def encoder_layer_forward_raw(layer: EncoderLayer, src_ptr: int, attn_ptr: int, out_ptr: int,
+                              stream: int = 0) -> None:
+    """ma_encoder_layer_forward (attn_ptr 0: the kernel computes the attention).
+    Raises RuntimeError on rejection."""
+    rc = LIB.ma_encoder_layer_forward(ctypes.byref(layer), src_ptr, attn_ptr or None, out_ptr, stream or None)
+    if rc != 0:
+        raise RuntimeError(last_error())
+
+
 def reload_options() -> None:
     """Re-read the MA_ATTN_* kernel-selection switches from the environment."""
     LIB.ma_attn_reload_options()
@@ -234,5 +267,5 @@ def default_scale(D: int) -> float:
 
 
 __all__ = ["LIB", "Desc", "make_desc", "forward_raw", "forward_noalloc_raw", "validate", "workspace_size",
-           "block_table", "row_keys", "pattern_csr", "reload_options", "last_error", "DTYPES", "default_scale",
+           "block_table", "row_keys", "pattern_csr", "reload_options", "last_error", "EncoderLayer", "encoder_layer_forward_raw", "DTYPES", "default_scale",
            "SLIDING", "DENSE", "BLOCK_SPARSE", "LONGFORMER", "INDEX_SET", "F32", "BF16", "F16"]

@@ -10,6 +10,14 @@ and forward semantics, including PositionalEncoding indexing its table by
 ``x.size(0)`` as the reference does (:19-20).  The attention inside each
 layer is ``layers.SparseAttention``: the HIP kernels in eval mode, the
 PyTorch path in training mode unless ``fallback_training=False``.
+
+``fused=True`` (layer) / ``fused_layers=True`` (model), keyword-only and off
+by default, runs each layer's inference forward as one HIP kernel
+(ma_encoder_layer_forward, include/ma_encoder.h): attention, residual,
+LayerNorm1, linear1, ReLU, linear2, residual and LayerNorm2 without
+intermediate tensors.  It applies to float32 device inputs when the layer is
+in eval mode (dropout the identity) and no gradient is being recorded; a call
+that records gradients, or a training-mode call, runs the operations above.
 """
 from __future__ import annotations
 
@@ -39,12 +47,71 @@ class PositionalEncoding(nn.Module):
         return x + self.pe[:x.size(0), :]
 
 
+def _fused_applies(layer: nn.Module, src: torch.Tensor) -> bool:
+    if not (src.is_cuda and src.dtype == torch.float32) or src.dim() != 3:
+        return False
+    if layer.training and any(m.p > 0 for m in (layer.dropout, layer.dropout1, layer.dropout2)):
+        return False
+    if torch.is_grad_enabled() and (src.requires_grad or any(p.requires_grad for p in layer.parameters())):
+        return False
+    return True
+
+
+def _layer_desc(layer, B: int, S: int, device):
+    """The layer's ma_encoder_layer descriptor, cached on the layer per shape,
+    device and parameter storage (rebuilt when any of them changes)."""
+    import ma_attn as _ma
+    params = (layer.norm1.weight, layer.norm1.bias, layer.linear1.weight, layer.linear1.bias,
+              layer.linear2.weight, layer.linear2.bias, layer.norm2.weight, layer.norm2.bias)
+    key = (B, S, device, int(layer.self_attn.window_size), layer.norm1.eps, layer.norm2.eps,
+           tuple(p.data_ptr() for p in params))
+    hit = getattr(layer, "_fused_desc", None)
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    if layer.norm2.eps != layer.norm1.eps:
+        raise RuntimeError("the fused layer takes one LayerNorm eps for both norms")
+    for p in params:
+        if p.device != device or p.dtype != torch.float32 or not p.is_contiguous():
+            raise RuntimeError("fused layer parameters must be contiguous float32 on the input's device")
+    L = _ma.EncoderLayer()
+    L.batch, L.seq_len, L.d_model = B, S, layer.linear1.in_features
+    L.d_ff = layer.linear1.out_features
+    L.window = int(layer.self_attn.window_size)
+    L.ln_eps = float(layer.norm1.eps)
+    (L.norm1_weight, L.norm1_bias, L.linear1_weight, L.linear1_bias, L.linear2_weight, L.linear2_bias,
+     L.norm2_weight, L.norm2_bias) = (p.data_ptr() for p in params)
+    layer._fused_desc = (key, L)
+    return L
+
+
+def encoder_layer_forward(layer: "CustomTransformerEncoderLayer", src: torch.Tensor,
+                          attn: torch.Tensor = None) -> torch.Tensor:
+    """One HIP launch for layer(src) in inference ([B, S, d_model] float32 on
+    the device).  attn None: the kernel computes the layer's sliding-window
+    attention too; otherwise only the block after the attention runs."""
+    import ma_attn as _ma
+    from sparse_attention_cuda import _on_device
+    src = src.contiguous()
+    B, S, Dm = src.shape
+    if Dm != layer.linear1.in_features:
+        raise RuntimeError(f"input width {Dm} != d_model {layer.linear1.in_features}")
+    L = _layer_desc(layer, B, S, src.device)
+    out = torch.empty_like(src)
+    a = attn.contiguous() if attn is not None else None
+    aptr = a.data_ptr() if a is not None else 0
+    _on_device(src.get_device(), lambda stream: _ma.encoder_layer_forward_raw(L, src.data_ptr(), aptr,
+                                                                              out.data_ptr(), stream))
+    return out
+
+
 class CustomTransformerEncoderLayer(nn.Module):
     """Self-attention (SparseAttention) + feed-forward, each with residual,
     dropout and post-LayerNorm (reference model.py:28-52)."""
 
-    def __init__(self, d_model, num_heads, dropout=0.1, window_size=3, *, fallback_training=True):
+    def __init__(self, d_model, num_heads, dropout=0.1, window_size=3, *, fallback_training=True,
+                 fused=False):
         super().__init__()
+        self.fused = bool(fused)
         self.self_attn = SparseAttention(window_size=window_size, fallback_training=fallback_training)
         self.linear1 = nn.Linear(d_model, d_model * 4)
         self.dropout = nn.Dropout(dropout)
@@ -55,6 +122,11 @@ class CustomTransformerEncoderLayer(nn.Module):
         self.dropout2 = nn.Dropout(dropout)
 
     def forward(self, src):
+        if self.fused and _fused_applies(self, src):
+            if self.self_attn.use_ma_core:
+                return encoder_layer_forward(self, src)
+            # the layer's own PyTorch attention (a different mask), then the fused block
+            return encoder_layer_forward(self, src, self.self_attn(src, src, src))
         attn = self.self_attn(src, src, src)
         src = self.norm1(src + self.dropout1(attn))
         ff = self.linear2(self.dropout(F.relu(self.linear1(src))))
@@ -68,14 +140,14 @@ class TransformerModel(nn.Module):
     single-head)."""
 
     def __init__(self, input_dim, model_dim, num_heads, num_layers, dropout=0.1, *,
-                 fallback_training=True):
+                 fallback_training=True, fused_layers=False):
         super().__init__()
         self.model_dim = model_dim
         self.encoder = nn.Linear(input_dim, model_dim)
         self.pos_encoder = PositionalEncoding(model_dim)
         self.encoder_layers = nn.ModuleList([
             CustomTransformerEncoderLayer(d_model=model_dim, num_heads=num_heads, dropout=dropout,
-                                          fallback_training=fallback_training)
+                                          fallback_training=fallback_training, fused=fused_layers)
             for _ in range(num_layers)
         ])
         self.decoder = nn.Linear(model_dim, 1)

@@ -8,21 +8,21 @@ import numpy as np
 import pytest
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = [os.path.join(REPO, "include", h) for h in ("ma_attn.h", "ma_features.h")]
+HEADERS = [os.path.join(REPO, "include", h) for h in ("ma_attn.h", "ma_features.h", "ma_encoder.h")]
 
 
 def _declared_functions():
     names = set()
     for h in HEADERS:
         text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
-        names |= set(re.findall(r"\b(ma_(?:attn|tick)_\w+)\s*\(", text))
+        names |= set(re.findall(r"\b(ma_(?:attn|tick|encoder)_\w+)\s*\(", text))
     return sorted(names)
 
 
 def test_library_exports_every_declared_symbol():
     import ma_attn
     names = _declared_functions()
-    assert len(names) >= 11 and "ma_tick_features" in names
+    assert len(names) >= 11 and "ma_tick_features" in names and "ma_encoder_layer_forward" in names
     lib = ctypes.CDLL(ma_attn.LIB_PATH)
     for n in names:
         assert hasattr(lib, n), f"{n} declared in include/ but not exported"
