@@ -434,7 +434,8 @@ def main() -> int:
     ap.add_argument("--layer-form", choices=["both", "fused", "ops"], default="both",
                     help="encoder_layer workload: time both model forms (default) or only one")
     ap.add_argument("--pass", dest="which", choices=["forward", "backward"], default="forward",
-                    help="backward: dQ, dK, dV from (Q, K, V, dO) (sliding and dense patterns)")
+                    help="backward: dQ, dK, dV from (Q, K, V, dO) (block-sparse, Longformer and index "
+                         "sets through index_set_backward over their key sets)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -453,9 +454,6 @@ def main() -> int:
         return 1
     B, H, N, D, dt_name, pk, desc = WORKLOADS[args.workload]
     bwd = args.which == "backward"
-    if bwd and pk["pattern"] not in ("sliding", "dense"):
-        print(f"bench.py: no backward for pattern {pk['pattern']}", file=sys.stderr)
-        return 2
     dtype = {"bf16": torch.bfloat16, "fp32": torch.float32}[dt_name]
     elt = 2 if dt_name == "bf16" else 4
     dev = torch.device("cuda", 0)
@@ -476,8 +474,22 @@ def main() -> int:
     if bwd and pk["pattern"] == "sliding":
         launch = lambda s: ext.sliding_backward(s[0], s[1], s[2], s[3], pk["left"], pk["right"],
                                                 pk.get("dilation", 1))
-    elif bwd:
+    elif bwd and pk["pattern"] == "dense":
         launch = lambda s: ext.dense_backward(s[0], s[1], s[2], s[3], pk["causal"])
+    elif bwd:
+        # block-sparse, Longformer and explicit sets train on index_set_backward
+        # over the pattern's key sets as one IndexSet (built once, as the layer does)
+        if pk["pattern"] == "index_set":
+            offsets, keys = window_csr(N, pk["left"], pk["right"])
+            iset = ext.IndexSet(torch.from_numpy(offsets), torch.from_numpy(keys), N, dev)
+        elif pk["pattern"] == "block_sparse":
+            nb = (N + pk["block_size"] - 1) // pk["block_size"]
+            table = ext.BlockTable(ext.make_block_table(pk["seed"], nb, pk["extra"]), N, pk["block_size"], dev)
+            iset = ext.pattern_index_set("block_sparse", N, dev, block_table=table, block_size=pk["block_size"])
+        else:
+            iset = ext.pattern_index_set("longformer", N, dev, left=pk["left"], right=pk["right"],
+                                         num_global=pk["num_global"])
+        launch = lambda s: ext.index_set_backward(s[0], s[1], s[2], s[3], iset)
     elif pk["pattern"] == "sliding":
         launch = lambda s: ext.sliding_forward(s[0], s[1], s[2], pk["left"], pk["right"], pk.get("dilation", 1))
     elif pk["pattern"] == "block_sparse":
@@ -530,8 +542,9 @@ def main() -> int:
 
     queries = B * H * N
     alg_bytes = tensors * B * N * H * D * elt
-    if pk["pattern"] == "index_set":  # plus the key lists, read once
-        alg_bytes += 8 * (N + 1) + 4 * key_count(N, pk)
+    if pk["pattern"] == "index_set" or (bwd and pk["pattern"] not in ("sliding", "dense")):
+        # plus the key lists read once (the backward: the set and its transpose)
+        alg_bytes += (2 if bwd else 1) * (8 * (N + 1) + 4 * key_count(N, pk))
     # forward: Q.K^T and P.V; backward: S, dP = dO.V^T, dV, dQ, dK (2 FLOP per MAC)
     flops = (10 if bwd else 4) * D * key_count(N, pk) * B * H
     achieved_gbps = alg_bytes / (mean_launch_ms * 1e-3) / 1e9

@@ -387,7 +387,8 @@ def index_set_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tenso
 
 
 def index_set_backward(query, key, value, grad_out, index_set) -> List[torch.Tensor]:
-    """dQ, dK, dV of index_set_forward (row kernels; the reference's generic
+    """dQ, dK, dV of index_set_forward (gather kernels at head_dim 64, row
+    kernels otherwise; the reference's generic
     COO path has no backward).  index_set as for index_set_forward."""
     _check(query, key, value, grad_out)
     N = query.shape[1]

@@ -46,3 +46,28 @@ def kernel_env(monkeypatch):
     yield set_env
     monkeypatch.undo()
     ma_attn.reload_options()
+
+
+# Gradient tolerances: float32 max-abs <= 1e-4; bfloat16 / float16 per element
+# |got - ref| <= GRAD16_ATOL + GRAD16_RTOL * |ref| (the kernels compute in fp32
+# on the 16-bit inputs, with 16-bit P and dS operands on the MFMA path, and
+# round each gradient once to the input dtype).
+GRAD32_ATOL = 1e-4
+GRAD16_ATOL = 1e-2
+GRAD16_RTOL = 1e-2
+
+
+def check_grad(name, got, ref, is_f32):
+    """Assert one gradient tensor (numpy float32) against the oracle's; prints
+    the max error and, for 16-bit, the worst ratio to the per-element bound."""
+    assert np.isfinite(got).all(), f"{name}: non-finite"
+    if got.size == 0:
+        return
+    err = np.abs(got - ref)
+    if is_f32:
+        print(f"  {name}: max|err| = {err.max():.3e} (tol {GRAD32_ATOL:.0e})", flush=True)
+        assert err.max() <= GRAD32_ATOL, (name, float(err.max()))
+        return
+    ratio = err / (GRAD16_ATOL + GRAD16_RTOL * np.abs(ref))
+    print(f"  {name}: max|err| = {err.max():.3e}, worst err/(atol + rtol|ref|) = {ratio.max():.3f}", flush=True)
+    assert ratio.max() <= 1.0, (name, float(err.max()), float(ratio.max()))

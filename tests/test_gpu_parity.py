@@ -250,7 +250,9 @@ def test_cfg1_causal_fp32(ext, oracle):
     (q, k, v), up = _inputs((1, 1024, 4, 16), 1235, torch.float32)
     y = ext.sliding_forward(q, k, v, 63, 0)
     spec = oracle.Spec(1, 1024, 4, 16, pattern="sliding", left=63, right=0)
-    assert _max_err(y, oracle.forward(spec, *up)) <= 1e-5
+    err = _max_err(y, oracle.forward(spec, *up))
+    print(f"  cfg1 fp32 whole output: max|err| = {err:.3e}", flush=True)
+    assert err <= 1e-5
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -270,6 +272,7 @@ def test_cfg5_dilated(ext, oracle, dtype):
     y = ext.sliding_forward(q, k, v, 63, 0, 4)
     spec = oracle.Spec(1, 65536, 8, 64, pattern="sliding", left=63, right=0, dilation=4)
     _check_sampled(oracle, spec, up, y, dtype, (0, 8), [(0, 600), (30000, 30300), (65000, 65536)])
+    _check_sampled(oracle, spec, up, y, dtype, (5, 6), [(0, 65536)])  # one whole head
 
 
 def test_target_causal_bf16(ext, oracle):
@@ -288,6 +291,7 @@ def test_cfg3_block_sparse(ext, oracle):
     y = ext.block_sparse_forward(q, k, v, table, 64)
     spec = oracle.Spec(2, 16384, 8, 64, pattern="block_sparse", block_size=64, table=table.numpy())
     _check_sampled(oracle, spec, up, y, torch.bfloat16, (0, 2), [(0, 256), (8000, 8256), (16128, 16384)])
+    _check_sampled(oracle, spec, up, y, torch.bfloat16, (6, 7), [(0, 16384)])  # one whole head
 
 
 def test_cfg4_longformer(ext, oracle):
@@ -296,6 +300,7 @@ def test_cfg4_longformer(ext, oracle):
     y = ext.longformer_forward(q, k, v, 127, 0, 16)
     spec = oracle.Spec(2, 32768, 12, 64, pattern="longformer", left=127, right=0, num_global=16)
     _check_sampled(oracle, spec, up, y, torch.bfloat16, (0, 2), [(0, 300), (16000, 16100), (32700, 32768)])
+    _check_sampled(oracle, spec, up, y, torch.bfloat16, (9, 10), [(0, 32768)])  # one whole head, globals included
 
 
 # ------------------------------------------------------- properties at full size
