@@ -15,7 +15,8 @@ forward pass over that batch.  Prints ONE JSON line:
              the library stamps on the kernels' own dispatches
              (ma_attn_forward_timed, hipExtLaunchKernel) in a second pass of
              K launches; traffic = measured HBM bytes per launch from the
-             committed rocprofv3 counter summary
+             committed rocprofv3 counter summary (roofline.traffic_source
+             names it: it is not measured in this run)
   cpu_baseline  the CPU oracle (restatement of ma_core.cpp:160-246) on this
              host, single thread, bounded sample of the same workload
 
@@ -286,7 +287,8 @@ def bench_ticks(args) -> int:
         "data": f"synthetic GBM-shaped ticks built on the device, {nsets} rotated sets resident in HBM",
         "config": {"workload": "tick-feature pass (TickDataset preprocessing)", "ticks": n},
         "roofline": {"bound": "hbm", "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": gbps / HBM_PEAK_GBPS, "traffic": load_traffic("ticks")},
+                     "frac": gbps / HBM_PEAK_GBPS, "traffic": load_traffic("ticks"),
+                     "traffic_source": "profiles/traffic_ticks.txt (rocprofv3 FETCH_SIZE + WRITE_SIZE, committed)"},
         "kernel_us_mean": mean_ms * 1e3, "kernel_us_median": per[len(per) // 2] * 1e3,
         "step_us_mean": ms_per_step * 1e3, "algorithmic_bytes_per_launch": alg,
         "copy_kernel_gbps": copy_gbps, "device": torch.cuda.get_device_name(dev),
@@ -555,12 +557,15 @@ def main() -> int:
     # the bound is whichever peak the algorithmic work reaches first
     mfma_peak = MFMA_BF16_PEAK_TFLOPS if dt_name == "bf16" else MFMA_F32_PEAK_TFLOPS
     tflops = flops / (mean_launch_ms * 1e-3) / 1e12
+    # traffic is not measured in this run: it is the committed rocprofv3 counter summary
+    tsrc = f"profiles/traffic_{args.workload}.txt (rocprofv3 FETCH_SIZE + WRITE_SIZE, committed)" \
+        if traffic is not None else None
     if flops / alg_bytes > mfma_peak * 1e12 / (HBM_PEAK_GBPS * 1e9):
         roofline = {"bound": "mfma", "achieved": tflops, "peak": mfma_peak, "unit": "TFLOP/s",
-                    "frac": tflops / mfma_peak, "traffic": traffic}
+                    "frac": tflops / mfma_peak, "traffic": traffic, "traffic_source": tsrc}
     else:
         roofline = {"bound": "hbm", "achieved": achieved_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                    "frac": achieved_gbps / HBM_PEAK_GBPS, "traffic": traffic}
+                    "frac": achieved_gbps / HBM_PEAK_GBPS, "traffic": traffic, "traffic_source": tsrc}
     out = {
         "metric": METRIC_BWD if bwd else METRIC,
         "value": queries / (ms_per_step * 1e-3),
@@ -588,6 +593,7 @@ def main() -> int:
         "mfma_bf16_frac_of_peak": (flops / (mean_launch_ms * 1e-3) / 1e12) / MFMA_BF16_PEAK_TFLOPS,
         # rocprofv3 MfmaUtil of the forward kernel (committed summary), not measured in this run
         "mfma_busy_pct": None if bwd else load_mfma_busy(args.workload),
+        "mfma_busy_source": None if bwd else "profiles/mfma_busy_by_workload.md (rocprofv3 MfmaUtil, committed)",
         "copy_kernel_gbps": copy_gbps,
         "device": torch.cuda.get_device_name(dev),
     }
