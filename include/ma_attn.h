@@ -56,6 +56,36 @@ enum ma_attn_pattern {
   MA_ATTN_INDEX_SET = 4
 };
 
+/*
+ * The 64x64-tile form of an INDEX_SET key set (ma_attn_tile_plan builds it
+ * on the host; the caller copies the blob to the device).  Entries are the
+ * (query tile t, key block c) pairs that hold at least one key of the set,
+ * ordered by tile, then block.  All offsets are bytes into the blob.
+ */
+typedef struct ma_attn_tile_header {
+  int64_t seq_len;        /* N of the set */
+  int64_t num_tiles;      /* ceil(N / 64): query tiles, and key blocks */
+  int64_t num_entries;
+  int64_t seg;            /* entries per work item: longer tile rows (and key-block
+                             columns) are split over several items, merged after */
+  int64_t num_q_items;    /* query-side work items (forward, statistics, dQ) */
+  int64_t num_q_split;    /* query tiles split over more than one item */
+  int64_t num_q_partials; /* items of split query tiles: one partial result each */
+  int64_t num_k_items;    /* key-side work items (dK, dV) */
+  int64_t num_k_split;
+  int64_t num_k_partials;
+  int64_t off_blk;        /* int32 [num_entries]: key block, bit 30 set when all 64x64 pairs are in the set */
+  int64_t off_mask;       /* uint64 [num_entries][64]: bit k of word r <=> key 64*blk + k in S_(64*tile + r) */
+  int64_t off_kmask;      /* uint64 [num_entries][64]: the transpose, bit r of word k (same condition) */
+  int64_t off_tile;       /* int32 [num_entries]: query tile of the entry */
+  int64_t off_kentry;     /* int32 [num_entries]: entry ids ordered by key block, then tile */
+  int64_t off_q_items;    /* int32 [num_q_items][4]: tile, first entry, end entry, partial slot or -1 */
+  int64_t off_q_split;    /* int32 [num_q_split][4]: tile, first slot, slot count, 0 */
+  int64_t off_k_items;    /* int32 [num_k_items][4]: key block, first and end position in kentry, slot or -1 */
+  int64_t off_k_split;    /* int32 [num_k_split][4]: key block, first slot, slot count, 0 */
+  int64_t total_bytes;
+} ma_attn_tile_header;
+
 typedef struct ma_attn_desc {
   int64_t batch;
   int64_t seq_len;
@@ -85,6 +115,10 @@ typedef struct ma_attn_desc {
                                      index_t_queries[index_t_offsets[j] .. index_t_offsets[j+1]) */
   const int32_t* index_t_queries; /* INDEX_SET backward only: device int32 [num_indices], ascending
                                      per key */
+  const ma_attn_tile_header* tile_header; /* INDEX_SET, optional: HOST copy of the set's tile plan
+                                             header; with tile_plan, head_dim 64 runs the tiled
+                                             MFMA kernels (forward and backward) */
+  const void* tile_plan;                  /* INDEX_SET, optional: DEVICE copy of the whole plan */
 } ma_attn_desc;
 
 /*
@@ -223,10 +257,24 @@ int ma_attn_forward_noalloc(const ma_attn_desc* desc, const void* q, const void*
  * it loads.  For tests and A/B timing; no reference counterpart. */
 void ma_attn_reload_options(void);
 
+/*
+ * Host: the tile plan of a CSR key set (host offsets [seq_len + 1], keys
+ * [offsets[seq_len]], each row ascending, keys in [0, seq_len)).  seg: entries
+ * per work item (0: the library's default).  With plan NULL, fills header
+ * only (sizes and offsets); then, given plan of header->total_bytes bytes,
+ * writes the whole plan (the header first).  Returns 0, or -1 on invalid
+ * input.  No reference counterpart: the reference's generic COO attention
+ * (src/csrc/sparse_attention.cpp:11-152) scans an N x N score matrix per
+ * (batch, head); the plan is what lets this engine run an explicit set on
+ * 64x64 MFMA tiles with per-row bit masks.
+ */
+int ma_attn_tile_plan(int64_t seq_len, const int64_t* offsets, const int32_t* keys, int64_t seg,
+                      ma_attn_tile_header* header, void* plan, size_t plan_bytes);
+
 /* ABI version of this header (bumped on incompatible change). */
 int ma_attn_abi_version(void);
 
-#define MA_ATTN_ABI_VERSION 6
+#define MA_ATTN_ABI_VERSION 7
 
 #ifdef __cplusplus
 }

@@ -27,11 +27,13 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 #include <set>
 #include <string>
 #include <utility>
+#include <vector>
 
 #include "../../include/ma_attn.h"
 #include "../../include/ma_features.h"
@@ -40,6 +42,7 @@
 #include "stream_kernel.h"
 #include "block_kernel.h"
 #include "backward_kernel.h"
+#include "tile_kernel.h"
 #include "tick_features.h"
 
 // Scratch of ma_attn_forward_noalloc: device memory the library owns, one
@@ -866,6 +869,13 @@ int validate(const ma_attn_desc* d) {
       break;
     case MA_ATTN_INDEX_SET:
       if (d->num_indices < 0) return fail("ma_attn: num_indices must be >= 0");
+      if (d->tile_header && !d->tile_plan) return fail("ma_attn: tile_header given without tile_plan");
+      if (d->tile_header && (d->tile_header->seq_len != d->seq_len || d->tile_header->num_tiles != (d->seq_len + 63) / 64 ||
+                             d->tile_header->num_entries < 0 || d->tile_header->num_q_items < (d->seq_len + 63) / 64 ||
+                             d->tile_header->num_k_items < (d->seq_len + 63) / 64 || d->tile_header->num_q_partials < 0 ||
+                             d->tile_header->num_k_partials < 0 || d->tile_header->num_q_split < 0 ||
+                             d->tile_header->num_k_split < 0))
+        return fail("ma_attn: the tile plan does not belong to a set of seq_len %lld", (long long)d->seq_len);
       if (!d->index_offsets && d->seq_len > 0) return fail("ma_attn: index_offsets is null");
       if (!d->index_keys && d->num_indices > 0) return fail("ma_attn: index_keys is null");
       break;
@@ -1678,6 +1688,130 @@ int scratch_of_stream(hipStream_t st, void** out) {
 int forward_launch(const ma_attn_desc* desc, const void* q, const void* k, const void* v, void* o,
                    void* workspace, size_t workspace_bytes, hipStream_t st);
 
+// ------------------------------------------------------------------ tiled index sets
+//
+// INDEX_SET with a tile plan (ma_attn_tile_plan), head_dim 64, 16-byte
+// aligned tensors: tile_kernel.h.  Workspace: the partial results of split
+// work items, per (batch, head): forward [q partials][64][kTilePart] floats;
+// backward the statistics, then one region the three passes reuse in turn
+// ([q partials][64][kTilePart], [q partials][64][64], [k partials][64][128]).
+bool tiles_apply(const ma_attn_desc* d, const void* const* ptrs, int n) {
+  if (d->pattern != MA_ATTN_INDEX_SET || !d->tile_header || !d->tile_plan || d->head_dim != kHeadDim) return false;
+  if (g_opt.force_rows) return false;
+  for (int i = 0; i < n; ++i)
+    if (!aligned16(ptrs[i])) return false;
+  const ma_attn_tile_header& h = *d->tile_header;
+  const int64_t tb = d->num_heads * kHeadDim * (d->dtype == MA_ATTN_F32 ? 4 : 2);
+  const int64_t items = h.num_q_items > h.num_k_items ? h.num_q_items : h.num_k_items;
+  return (d->seq_len + 64) * tb < (1LL << 31) && d->batch * d->num_heads * items <= (int64_t)INT32_MAX &&
+         h.num_entries < (1LL << 30) && h.num_tiles < (1LL << 25) && (d->seq_len + 64) * d->num_heads * 8 < (1LL << 31);
+}
+
+int64_t tiles_fwd_part_bytes(const ma_attn_desc* d) {
+  return d->batch * d->num_heads * d->tile_header->num_q_partials * 64 * kTilePart * (int64_t)sizeof(float);
+}
+
+int64_t tiles_bwd_part_bytes(const ma_attn_desc* d) {
+  const ma_attn_tile_header& h = *d->tile_header;
+  const int64_t q = h.num_q_partials * 64 * kTilePart, k = h.num_k_partials * 64 * 128;
+  return d->batch * d->num_heads * (q > k ? q : k) * (int64_t)sizeof(float);
+}
+
+int64_t stats_bytes(const ma_attn_desc* d) {
+  return (d->batch * d->seq_len * d->num_heads * (int64_t)sizeof(RowStat) + 255) / 256 * 256;
+}
+
+TileArgs tile_args(const ma_attn_desc* d, bool kside) {
+  const ma_attn_tile_header& h = *d->tile_header;
+  const uint8_t* base = static_cast<const uint8_t*>(d->tile_plan);
+  TileArgs a;
+  memset(&a, 0, sizeof(a));
+  a.blk = reinterpret_cast<const int32_t*>(base + h.off_blk);
+  a.mask = reinterpret_cast<const uint64_t*>(base + h.off_mask);
+  a.kmask = reinterpret_cast<const uint64_t*>(base + h.off_kmask);
+  a.etile = reinterpret_cast<const int32_t*>(base + h.off_tile);
+  a.kentry = reinterpret_cast<const int32_t*>(base + h.off_kentry);
+  a.items = reinterpret_cast<const int32_t*>(base + (kside ? h.off_k_items : h.off_q_items));
+  a.split = reinterpret_cast<const int32_t*>(base + (kside ? h.off_k_split : h.off_q_split));
+  a.nitems = (int32_t)(kside ? h.num_k_items : h.num_q_items);
+  a.nsplit = (int32_t)(kside ? h.num_k_split : h.num_q_split);
+  a.npart = (int32_t)(kside ? h.num_k_partials : h.num_q_partials);
+  a.nent = (int32_t)h.num_entries;
+  a.ntiles = (int32_t)h.num_tiles;
+  a.N = (int32_t)d->seq_len;
+  a.H = (int32_t)d->num_heads;
+  a.scale = scale_of(d);
+  a.scale_log2 = a.scale * 1.4426950408889634f;
+  return a;
+}
+
+template <class P>
+int launch_tiles_fwd(const ma_attn_desc* d, const void* q, const void* k, const void* v, void* o, void* ws,
+                     size_t ws_bytes, hipStream_t st) {
+  const int64_t need = tiles_fwd_part_bytes(d);
+  if ((int64_t)ws_bytes < need || (need > 0 && !ws))
+    return fail("ma_attn: workspace of %lld bytes required (ma_attn_workspace_size), got %zu", (long long)need,
+                ws_bytes);
+  TileArgs a = tile_args(d, false);
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.part = static_cast<float*>(ws);
+  const int64_t bh = d->batch * d->num_heads;
+  const size_t shm = 2 * (size_t)P::kBlk;
+  auto kf = &tile_fwd_kernel<P, false>;
+  if (reserve_lds(reinterpret_cast<const void*>(kf), shm, st)) return 1;
+  launch(a.nsplit == 0, kf, dim3((unsigned)(bh * a.nitems)), dim3(256), (uint32_t)shm, st, a);
+  if (a.nsplit > 0)
+    launch(true, tile_combine_kernel<typename P::Elt, false>, dim3((unsigned)(bh * a.nsplit)), dim3(256), 0u, st,
+           a);
+  return 0;
+}
+
+template <class P>
+int launch_tiles_bwd(const ma_attn_desc* d, const void* const* ptrs, void* ws, hipStream_t st) {
+  TileArgs a = tile_args(d, false);
+  a.q = ptrs[0];
+  a.k = ptrs[1];
+  a.v = ptrs[2];
+  a.dout = ptrs[3];
+  a.o = const_cast<void*>(ptrs[4]);  // dQ
+  a.dk = const_cast<void*>(ptrs[5]);
+  a.dv = const_cast<void*>(ptrs[6]);
+  a.stats = static_cast<float*>(ws);
+  a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + stats_bytes(d));
+  const int64_t bh = d->batch * d->num_heads;
+  using Elt = typename P::Elt;
+  auto kf = &tile_fwd_kernel<P, true>;
+  auto kq = &tile_dq_kernel<P>;
+  auto kkv = &tile_dkv_kernel<P>;
+  const size_t shm_f = 2 * (size_t)P::kBlk, shm_q = 4 * (size_t)P::kBlk, shm_kv = 2 * (2 * (size_t)P::kBlk + 512);
+  if (reserve_lds(reinterpret_cast<const void*>(kf), shm_f, st) ||
+      reserve_lds(reinterpret_cast<const void*>(kq), shm_q, st) ||
+      reserve_lds(reinterpret_cast<const void*>(kkv), shm_kv, st))
+    return 1;
+  // statistics {lse2, delta}, then dQ (query side)
+  launch(false, kf, dim3((unsigned)(bh * a.nitems)), dim3(256), (uint32_t)shm_f, st, a);
+  if (a.nsplit > 0)
+    launch(false, tile_combine_kernel<Elt, true>, dim3((unsigned)(bh * a.nsplit)), dim3(256), 0u, st, a);
+  launch(false, kq, dim3((unsigned)(bh * a.nitems)), dim3(256), (uint32_t)shm_q, st, a);
+  if (a.nsplit > 0) launch(false, tile_sum_kernel<Elt, 64>, dim3((unsigned)(bh * a.nsplit)), dim3(256), 0u, st, a);
+  // dK, dV (key side)
+  TileArgs b = tile_args(d, true);
+  b.q = a.q;
+  b.k = a.k;
+  b.v = a.v;
+  b.dout = a.dout;
+  b.dk = a.dk;
+  b.dv = a.dv;
+  b.stats = a.stats;
+  b.part = a.part;
+  launch(b.nsplit == 0, kkv, dim3((unsigned)(bh * b.nitems)), dim3(256), (uint32_t)shm_kv, st, b);
+  if (b.nsplit > 0) launch(true, tile_sum_kernel<Elt, 128>, dim3((unsigned)(bh * b.nsplit)), dim3(256), 0u, st, b);
+  return 0;
+}
+
 uint64_t splitmix64(uint64_t* s) {
   uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
   z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -1701,11 +1835,13 @@ int ma_attn_validate(const ma_attn_desc* desc) {
 size_t ma_attn_workspace_size(const ma_attn_desc* desc) {
   g_last_error.clear();
   if (validate(desc)) return 0;
-  if (desc->pattern != MA_ATTN_LONGFORMER || desc->head_dim != kHeadDim || desc->dtype == MA_ATTN_F32) return 0;
-  if (desc->batch * desc->seq_len * desc->num_heads == 0) return 0;
-  // the size the stream kernel needs whenever it may take this descriptor
+  if (desc->batch * desc->seq_len * desc->num_heads == 0 || desc->head_dim != kHeadDim) return 0;
+  // the size the kernels need whenever they may take this descriptor
   // (pointer alignment is not known here; 16-byte-aligned tensors are assumed)
   static const char dummy[16] __attribute__((aligned(16))) = {0};
+  const void* const ptrs[4] = {dummy, dummy, dummy, dummy};
+  if (tiles_apply(desc, ptrs, 4)) return (size_t)tiles_fwd_part_bytes(desc);
+  if (desc->pattern != MA_ATTN_LONGFORMER || desc->dtype == MA_ATTN_F32) return 0;
   if (!stream_applies(desc, dummy, dummy, dummy, dummy)) return 0;
   return (size_t)stream_plan(desc).partial_bytes;
 }
@@ -1728,8 +1864,12 @@ int ma_attn_forward_noalloc(const ma_attn_desc* desc, const void* q, const void*
   if (rows == 0 || desc->head_dim == 0) return 0;
   if (!q || !k || !v || !o) return fail("ma_attn: null tensor pointer");
   // the scratch the kernels that take this call would need (the Longformer
-  // stream kernel's per-chunk partials; nothing for every other kernel)
-  const size_t need = stream_applies(desc, q, k, v, o) ? (size_t)stream_plan(desc).partial_bytes : 0;
+  // stream kernel's per-chunk partials, a tiled index set's split partials;
+  // nothing for every other kernel)
+  const void* const qkvo[4] = {q, k, v, o};
+  const size_t need = stream_applies(desc, q, k, v, o) ? (size_t)stream_plan(desc).partial_bytes
+                      : tiles_apply(desc, qkvo, 4)     ? (size_t)tiles_fwd_part_bytes(desc)
+                                                       : 0;
   if (need > (size_t)MA_ATTN_NOALLOC_SCRATCH_BYTES)
     return fail("ma_attn_forward_noalloc: this call needs %zu bytes of scratch, above the %zu bytes of the "
                 "library's static scratch; use ma_attn_forward with a workspace",
@@ -1747,6 +1887,7 @@ namespace {
 int forward_launch(const ma_attn_desc* desc, const void* q, const void* k, const void* v, void* o,
                    void* workspace, size_t workspace_bytes, hipStream_t st) {
   (void)hipGetLastError();  // launch errors below must be ours
+  const void* const qkvo[4] = {q, k, v, o};
   int rc;
   const bool want_rows = g_opt.force_rows;
   const bool want_band = g_opt.force_band;
@@ -1756,6 +1897,18 @@ int forward_launch(const ma_attn_desc* desc, const void* q, const void* k, const
     rc = launch_block(desc, q, k, v, o, st);
   } else if (!want_rows && band_applies(desc, q, k, v, o)) {
     rc = launch_band(desc, q, k, v, o, st);
+  } else if (tiles_apply(desc, qkvo, 4)) {
+    switch (desc->dtype) {
+      case MA_ATTN_F32:
+        rc = launch_tiles_fwd<F32Path>(desc, q, k, v, o, workspace, workspace_bytes, st);
+        break;
+      case MA_ATTN_BF16:
+        rc = launch_tiles_fwd<HalfPath<__bf16>>(desc, q, k, v, o, workspace, workspace_bytes, st);
+        break;
+      default:
+        rc = launch_tiles_fwd<HalfPath<_Float16>>(desc, q, k, v, o, workspace, workspace_bytes, st);
+        break;
+    }
   } else if (!want_rows && gather_applies(desc, q, k, v, o)) {
     switch (desc->dtype) {
       case MA_ATTN_F32:
@@ -1806,6 +1959,10 @@ extern "C" {
 size_t ma_attn_backward_workspace_size(const ma_attn_desc* desc) {
   g_last_error.clear();
   if (validate(desc)) return 0;
+  static const char dummy[16] __attribute__((aligned(16))) = {0};
+  const void* const ptrs[7] = {dummy, dummy, dummy, dummy, dummy, dummy, dummy};
+  if (desc->batch * desc->seq_len * desc->num_heads > 0 && tiles_apply(desc, ptrs, 7))
+    return (size_t)(stats_bytes(desc) + tiles_bwd_part_bytes(desc));
   return (size_t)(desc->batch * desc->seq_len * desc->num_heads) * sizeof(RowStat);
 }
 
@@ -1830,6 +1987,18 @@ int ma_attn_backward(const ma_attn_desc* desc, const void* q, const void* k, con
   RowStat* stats = static_cast<RowStat*>(workspace);
   const void* ptrs[7] = {q, k, v, dout, dq, dk, dv};
   int rc;
+  if (tiles_apply(desc, ptrs, 7)) {
+    const size_t need_t = (size_t)(stats_bytes(desc) + tiles_bwd_part_bytes(desc));
+    if (workspace_bytes < need_t)
+      return fail("ma_attn_backward: workspace of %zu bytes needed, %zu given", need_t, workspace_bytes);
+    rc = desc->dtype == MA_ATTN_BF16  ? launch_tiles_bwd<HalfPath<__bf16>>(desc, ptrs, workspace, st)
+         : desc->dtype == MA_ATTN_F16 ? launch_tiles_bwd<HalfPath<_Float16>>(desc, ptrs, workspace, st)
+                                      : launch_tiles_bwd<F32Path>(desc, ptrs, workspace, st);
+    if (rc) return rc;
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail("ma_attn_backward: kernel launch failed: %s", hipGetErrorString(e));
+    return 0;
+  }
   if (!g_opt.force_rows && bwd_mfma_applies(desc, ptrs)) {
     float* sf = reinterpret_cast<float*>(stats);
     rc = desc->dtype == MA_ATTN_BF16  ? launch_backward_mfma<HalfPath<__bf16>>(desc, ptrs, sf, st)
@@ -2018,6 +2187,158 @@ int64_t ma_attn_pattern_csr(const ma_attn_desc* desc, const int32_t* host_block_
     }
   }
   return nnz;
+}
+
+int ma_attn_tile_plan(int64_t N, const int64_t* off, const int32_t* keys, int64_t seg, ma_attn_tile_header* hdr,
+                      void* plan, size_t plan_bytes) {
+  g_last_error.clear();
+  if (!hdr) return fail("ma_attn_tile_plan: null header"), -1;
+  if (N < 0 || N > (int64_t)INT32_MAX - 64) return fail("ma_attn_tile_plan: seq_len out of range"), -1;
+  if (N > 0 && !off) return fail("ma_attn_tile_plan: null offsets"), -1;
+  if (seg <= 0) seg = kTileSeg;
+  const int64_t nnz = N > 0 ? off[N] : 0;
+  if (N > 0 && off[0] != 0) return fail("ma_attn_tile_plan: offsets[0] must be 0"), -1;
+  if (nnz > 0 && !keys) return fail("ma_attn_tile_plan: null keys"), -1;
+  for (int64_t i = 0; i < N; ++i) {
+    if (off[i + 1] < off[i] || off[i + 1] > nnz) return fail("ma_attn_tile_plan: offsets not non-decreasing"), -1;
+    for (int64_t x = off[i]; x < off[i + 1]; ++x)
+      if (keys[x] < 0 || keys[x] >= N || (x > off[i] && keys[x] <= keys[x - 1]))
+        return fail("ma_attn_tile_plan: keys must be in [0, N) and strictly ascending per row"), -1;
+  }
+  const int64_t nt = (N + 63) / 64;
+  // distinct key blocks of each query tile, ascending
+  std::vector<int32_t> mark((size_t)nt, -1), tile_first((size_t)nt + 1, 0), ent_blk;
+  std::vector<int32_t> list;
+  for (int64_t t = 0; t < nt; ++t) {
+    list.clear();
+    const int64_t r1 = std::min<int64_t>(N, 64 * t + 64);
+    for (int64_t i = 64 * t; i < r1; ++i)
+      for (int64_t x = off[i]; x < off[i + 1]; ++x) {
+        const int32_t c = keys[x] >> 6;
+        if (mark[c] != (int32_t)t) {
+          mark[c] = (int32_t)t;
+          list.push_back(c);
+        }
+      }
+    std::sort(list.begin(), list.end());
+    ent_blk.insert(ent_blk.end(), list.begin(), list.end());
+    tile_first[t + 1] = (int32_t)ent_blk.size();
+  }
+  const int64_t ne = (int64_t)ent_blk.size();
+  // work items: every tile / key block gets at least one (an empty one writes zeros)
+  std::vector<int32_t> kcount((size_t)nt, 0);
+  for (int32_t c : ent_blk) ++kcount[c];
+  auto items_of = [&](int64_t n) { return n <= seg ? (int64_t)1 : (n + seg - 1) / seg; };
+  int64_t qi = 0, qs = 0, qp = 0, ki = 0, ks = 0, kp = 0;
+  for (int64_t t = 0; t < nt; ++t) {
+    const int64_t n = tile_first[t + 1] - tile_first[t], m = items_of(n);
+    qi += m;
+    if (m > 1) ++qs, qp += m;
+    const int64_t mk = items_of(kcount[t]);
+    ki += mk;
+    if (mk > 1) ++ks, kp += mk;
+  }
+  ma_attn_tile_header h;
+  memset(&h, 0, sizeof(h));
+  h.seq_len = N;
+  h.num_tiles = nt;
+  h.num_entries = ne;
+  h.seg = seg;
+  h.num_q_items = qi;
+  h.num_q_split = qs;
+  h.num_q_partials = qp;
+  h.num_k_items = ki;
+  h.num_k_split = ks;
+  h.num_k_partials = kp;
+  int64_t at = 256;  // the header's copy comes first
+  auto take = [&](int64_t bytes) {
+    const int64_t o = at;
+    at += (bytes + 255) / 256 * 256;
+    return o;
+  };
+  h.off_blk = take(4 * ne);
+  h.off_mask = take(8 * 64 * ne);
+  h.off_kmask = take(8 * 64 * ne);
+  h.off_tile = take(4 * ne);
+  h.off_kentry = take(4 * ne);
+  h.off_q_items = take(16 * qi);
+  h.off_q_split = take(16 * qs);
+  h.off_k_items = take(16 * ki);
+  h.off_k_split = take(16 * ks);
+  h.total_bytes = at;
+  *hdr = h;
+  if (!plan) return 0;
+  if (plan_bytes < (size_t)h.total_bytes) return fail("ma_attn_tile_plan: plan buffer too small"), -1;
+  uint8_t* base = static_cast<uint8_t*>(plan);
+  memset(base, 0, (size_t)h.total_bytes);
+  memcpy(base, &h, sizeof(h));
+  int32_t* blk = reinterpret_cast<int32_t*>(base + h.off_blk);
+  uint64_t* mask = reinterpret_cast<uint64_t*>(base + h.off_mask);
+  int32_t* etile = reinterpret_cast<int32_t*>(base + h.off_tile);
+  int32_t* kentry = reinterpret_cast<int32_t*>(base + h.off_kentry);
+  std::vector<int32_t> pos((size_t)nt, 0);
+  for (int64_t t = 0; t < nt; ++t) {
+    const int32_t e0 = tile_first[t], e1 = tile_first[t + 1];
+    for (int32_t e = e0; e < e1; ++e) {
+      pos[ent_blk[e]] = e;
+      blk[e] = ent_blk[e];
+      etile[e] = (int32_t)t;
+    }
+    const int64_t r1 = std::min<int64_t>(N, 64 * t + 64);
+    for (int64_t i = 64 * t; i < r1; ++i)
+      for (int64_t x = off[i]; x < off[i + 1]; ++x)
+        mask[(int64_t)pos[keys[x] >> 6] * 64 + (i - 64 * t)] |= 1ull << (keys[x] & 63);
+    // full entries: every row and key of the block exists and every pair is in the set
+    if (64 * t + 63 < N)
+      for (int32_t e = e0; e < e1; ++e) {
+        bool full = 64 * (int64_t)ent_blk[e] + 63 < N;
+        for (int r = 0; r < 64 && full; ++r) full = mask[(int64_t)e * 64 + r] == ~0ull;
+        if (full) blk[e] |= 1 << 30;
+      }
+  }
+  // the transposed masks: bit r of word k
+  uint64_t* kmask = reinterpret_cast<uint64_t*>(base + h.off_kmask);
+  for (int64_t e = 0; e < ne; ++e)
+    for (int r = 0; r < 64; ++r) {
+      uint64_t w = mask[e * 64 + r];
+      while (w) {
+        const int k = __builtin_ctzll(w);
+        kmask[e * 64 + k] |= 1ull << r;
+        w &= w - 1;
+      }
+    }
+  // entries by key block, then tile (stable: entries are in tile order)
+  std::vector<int32_t> kfirst((size_t)nt + 1, 0);
+  for (int64_t c = 0; c < nt; ++c) kfirst[c + 1] = kfirst[c] + kcount[c];
+  {
+    std::vector<int32_t> fill(kfirst.begin(), kfirst.end() - 1);
+    for (int64_t e = 0; e < ne; ++e) kentry[fill[ent_blk[e]]++] = (int32_t)e;
+  }
+  int32_t* q_items = reinterpret_cast<int32_t*>(base + h.off_q_items);
+  int32_t* q_split = reinterpret_cast<int32_t*>(base + h.off_q_split);
+  int32_t* k_items = reinterpret_cast<int32_t*>(base + h.off_k_items);
+  int32_t* k_split = reinterpret_cast<int32_t*>(base + h.off_k_split);
+  auto emit = [&](int32_t* items, int32_t* split, int64_t& ni, int64_t& ns, int64_t& np, int32_t id, int32_t a,
+                  int32_t b) {
+    const int64_t n = b - a, m = items_of(n);
+    if (m == 1) {
+      int32_t* it = items + 4 * ni++;
+      it[0] = id, it[1] = a, it[2] = b, it[3] = -1;
+      return;
+    }
+    int32_t* sp = split + 4 * ns++;
+    sp[0] = id, sp[1] = (int32_t)np, sp[2] = (int32_t)m, sp[3] = 0;
+    for (int64_t j = 0; j < m; ++j) {
+      int32_t* it = items + 4 * ni++;
+      it[0] = id, it[1] = a + (int32_t)(j * seg), it[2] = (int32_t)std::min<int64_t>(b, a + (j + 1) * seg);
+      it[3] = (int32_t)np++;
+    }
+  };
+  int64_t ni = 0, ns = 0, np = 0;
+  for (int64_t t = 0; t < nt; ++t) emit(q_items, q_split, ni, ns, np, (int32_t)t, tile_first[t], tile_first[t + 1]);
+  ni = ns = np = 0;
+  for (int64_t c = 0; c < nt; ++c) emit(k_items, k_split, ni, ns, np, (int32_t)c, kfirst[c], kfirst[c + 1]);
+  return 0;
 }
 
 void ma_attn_reload_options(void) { g_opt = read_options(); }

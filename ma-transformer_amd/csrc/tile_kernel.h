@@ -1,0 +1,535 @@
+// tile_kernel.h -- explicit key sets (INDEX_SET) on 64x64 MFMA tiles, head
+// dim 64, bf16/fp16 (16x16x32 MFMA) and fp32 (16x16x4).
+//
+// The set comes as a tile plan (ma_attn_tile_plan): the (query tile, key
+// block) entries that hold any key, each with 64 row masks (bit k of word r:
+// key 64*blk + k in S_(64*tile + r)) and their transpose.  An entry whose
+// 64x64 pairs are all in the set is flagged full and computed unmasked.
+// Work items are runs of at most `seg` entries of one query tile (or one
+// key block): a tile with more is split over several items whose partial
+// results a combine kernel merges, so one long row (a Longformer global row,
+// a global key's column) does not hold up the launch.
+//
+//   tile_fwd_kernel      O (or, with STATS, the backward's {lse2, delta}):
+//                        one workgroup per (batch, head, item), 4 waves x 16
+//                        queries; key blocks through a two-buffer LDS ring
+//                        with the next block (and its mask word) in flight,
+//                        online softmax in registers.
+//   tile_combine_kernel  log-sum-exp merge of a split tile's partials.
+//   tile_dq_kernel       dQ over a query tile's entries (statistics given):
+//                        K staged as (K, K^T), V as rows; dS in registers,
+//                        dQ^T += K^T dS^T.
+//   tile_dkv_kernel      dK, dV over a key block's entries: each entry's
+//                        query tile staged as (Q, Q^T), (dO, dO^T) and its 64
+//                        statistics; dV^T += dO^T P, dK^T += Q^T dS.
+//   tile_sum_kernel      sums a split tile's (or key block's) partial dQ /
+//                        dK, dV.
+// Each output row has one writer; no atomics.  Every global access is a
+// range-checked buffer operation on the (batch, head) stream or an index
+// inside the plan's arrays.
+#pragma once
+
+#include "backward_kernel.h"
+#include "block_kernel.h"
+
+namespace ma_dev {
+
+constexpr int kTileFull = 1 << 30;   // entry flag: every pair of the 64x64 block is in the set
+constexpr int kTileSeg = 16;         // default entries per work item
+constexpr int kTilePart = 68;        // floats per row of a forward partial: 64 O, log2 max, sum, 2 pad
+
+struct TileArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* dout;
+  void* o;  // forward: O; backward: dQ
+  void* dk;
+  void* dv;
+  const int32_t* blk;     // [entries] key block | kTileFull
+  const uint64_t* mask;   // [entries][64] row masks
+  const uint64_t* kmask;  // [entries][64] column masks
+  const int32_t* etile;   // [entries] query tile of the entry
+  const int32_t* kentry;  // [entries] entry ids by key block
+  const int32_t* items;   // [nitems][4]
+  const int32_t* split;   // [nsplit][4]
+  float* stats;           // [B*N*H][2] {lse2, delta}
+  float* part;            // [B*H][npart][...] partial results of split items
+  int32_t N, H, nitems, nsplit, npart;
+  int32_t nent, ntiles;  // plan sizes: every index read from the plan is clamped to them
+  float scale, scale_log2;
+};
+
+__device__ __forceinline__ int clampi(int x, int lo, int hi) { return x < lo ? lo : (x > hi ? hi : x); }
+
+// Work item `it` of the plan: (tile or key block, first, end, slot), clamped
+// so that any plan content stays inside the plan's arrays.
+struct TileItem {
+  int id, e0, e1, slot;
+};
+__device__ __forceinline__ TileItem tile_item(const TileArgs& a, int it) {
+  TileItem w;
+  w.id = clampi(a.items[4 * it], 0, a.ntiles - 1);
+  w.e0 = clampi(a.items[4 * it + 1], 0, a.nent);
+  w.e1 = clampi(a.items[4 * it + 2], w.e0, a.nent);
+  w.slot = clampi(a.items[4 * it + 3], -1, a.npart - 1);
+  return w;
+}
+
+// Scores of one 64-key (or 64-query) block whose bit w of `m` keeps element
+// 16u + 4g + rr: sc[u][rr] with w = 16u + 4g + rr.
+__device__ __forceinline__ void apply_mask(f32x4 (&sc)[4], uint64_t m, int g) {
+  const uint32_t lo = (uint32_t)m, hi = (uint32_t)(m >> 32);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const uint32_t w = (u < 2 ? lo : hi) >> (16 * (u & 1) + 4 * g);
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) sc[u][rr] = (w >> rr) & 1u ? sc[u][rr] : -INFINITY;
+  }
+}
+
+// dot(x, O) of one query row over the head_dim values this lane holds (x in
+// the Q register layout of P, which is also the accumulator layout).
+template <class P>
+__device__ __forceinline__ float lane_dot(const typename P::Q& x, const f32x4 (&acc)[4]) {
+  float d = 0.0f;
+  if constexpr (P::kSPB == 1) {
+    using T = typename P::Elt;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t w[4] = {x.r[h].x, x.r[h].y, x.r[h].z, x.r[h].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = static_cast<float>(__builtin_bit_cast(T, (uint16_t)(w[j] & 0xffffu)));
+        const float hi = static_cast<float>(__builtin_bit_cast(T, (uint16_t)(w[j] >> 16)));
+        const f32x4& a = acc[2 * h + (j >> 1)];
+        d = fmaf(lo, a[2 * (j & 1)], d);
+        d = fmaf(hi, a[2 * (j & 1) + 1], d);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 xv = __builtin_bit_cast(f32x4, x.r[j]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) d = fmaf(xv[r], acc[j][r], d);
+    }
+  }
+  return d;
+}
+
+// One 64-key block of the lane's query row into the online softmax.
+template <class P>
+__device__ __forceinline__ void tile_update(const uint8_t* slot, uint32_t kl, uint32_t vl, const typename P::Q& q,
+                                            bool full, uint64_t mw, int g, float sl2, float& m_run, float& l_run,
+                                            f32x4 (&acc)[4]) {
+  f32x4 sc[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) sc[u] = P::qk(slot + P::blk_k(u) + kl, q);
+  if (!full) apply_mask(sc, mw, g);  // uniform
+  float mx = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) mx = fmaxf(mx, fmaxf(fmaxf(sc[u][0], sc[u][1]), fmaxf(sc[u][2], sc[u][3])));
+  const float m_new = fmaxf(m_run, col_max(mx));
+  const float m_use = m_new == -INFINITY ? 0.0f : m_new * sl2;
+  if (__builtin_amdgcn_ballot_w64(m_new != m_run) != 0) {
+    const float corr = __builtin_amdgcn_exp2f(m_run * sl2 - m_use);  // 0 on a row's first live block
+    l_run *= corr;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) acc[dt] *= corr;
+  }
+  m_run = m_new;
+#pragma unroll
+  for (int u = 0; u < 4; u += 2) {
+    float p0[4], p1[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      p0[rr] = __builtin_amdgcn_exp2f(fmaf(sc[u][rr], sl2, -m_use));
+      p1[rr] = __builtin_amdgcn_exp2f(fmaf(sc[u + 1][rr], sl2, -m_use));
+      l_run += p0[rr] + p1[rr];
+    }
+    P::pv2(slot + P::blk_v(u) + vl, slot + P::blk_v(u + 1) + vl, p0, p1, acc);
+  }
+}
+
+struct TileCtx {
+  int b, h, bh;
+  uint32_t tb;
+  int64_t base;
+  uint32_t nrec;
+};
+
+template <class P>
+__device__ __forceinline__ TileCtx tile_ctx(const TileArgs& a, int bh) {
+  TileCtx x;
+  x.bh = bh;
+  x.h = bh % a.H;
+  x.b = bh / a.H;
+  x.tb = (uint32_t)a.H * kHeadDim * sizeof(typename P::Elt);
+  x.base = ((int64_t)x.b * a.N * a.H + x.h) * kHeadDim;
+  x.nrec = (uint32_t)((int64_t)(a.N - 1) * x.tb + kHeadDim * sizeof(typename P::Elt));
+  return x;
+}
+
+// ---------------------------------------------------------------- forward / statistics
+
+template <class P, bool STATS>
+__global__ __launch_bounds__(256, P::kMinBlocks) void tile_fwd_kernel(TileArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 block buffers of P::kBlk bytes
+  using Elt = typename P::Elt;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15;
+  const int g = lane >> 4;
+
+  const int wg = xcd_row_order(blockIdx.x, gridDim.x);
+  const int it = wg % a.nitems;
+  const TileCtx x = tile_ctx<P>(a, wg / a.nitems);
+  const TileItem w = tile_item(a, it);
+  const int t = w.id, e0 = w.e0, e1 = w.e1, slot = w.slot;
+  const uint32_t tb = x.tb;
+  const __amdgpu_buffer_rsrc_t Qr = make_rsrc(static_cast<const Elt*>(a.q) + x.base, x.nrec);
+  const __amdgpu_buffer_rsrc_t Kr = make_rsrc(static_cast<const Elt*>(a.k) + x.base, x.nrec);
+  const __amdgpu_buffer_rsrc_t Vr = make_rsrc(static_cast<const Elt*>(a.v) + x.base, x.nrec);
+
+  const int ql = 16 * wv + c;  // the lane's query row within the tile
+  const uint32_t qrow = (uint32_t)(64 * t + ql) * tb;
+  typename P::Q q;
+  P::load_q(q, Qr, qrow, g);
+  const uint32_t kl = P::k_lane(c, g), vl = P::v_lane(c, g);
+  auto blk_off = [&](int e) { return e < e1 ? (uint32_t)(64 * (a.blk[e] & (kTileFull - 1))) * tb : kOob; };
+
+  float m_run = -INFINITY, l_run = 0.0f;
+  f32x4 acc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const float sl2 = a.scale_log2;
+
+  if (e0 < e1) {  // uniform
+    BlkSlots<P> nxt;
+    load_blk<P>(nxt, Kr, Vr, blk_off(e0), tid, tb);
+    uint64_t mw_next = a.mask[(int64_t)e0 * 64 + ql];
+    store_blk<P>(nxt, ring, tid);
+    __syncthreads();
+    for (int e = e0; e < e1; ++e) {
+      const bool full = (a.blk[e] & kTileFull) != 0;
+      const uint64_t mw = mw_next;
+      load_blk<P>(nxt, Kr, Vr, blk_off(e + 1), tid, tb);
+      if (e + 1 < e1) mw_next = a.mask[(int64_t)(e + 1) * 64 + ql];
+      tile_update<P>(ring + ((e - e0) & 1) * P::kBlk, kl, vl, q, full, mw, g, sl2, m_run, l_run, acc);
+      // the next block goes into the buffer the previous one used (every
+      // wave passed the barrier that ended it)
+      if (e + 1 < e1) store_blk<P>(nxt, ring + ((e + 1 - e0) & 1) * P::kBlk, tid);
+      __syncthreads();
+    }
+  }
+  const float l_tot = col_sum(l_run);
+  if (slot < 0) {
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if constexpr (!STATS) {
+      const __amdgpu_buffer_rsrc_t Or = make_rsrc(static_cast<Elt*>(a.o) + x.base, x.nrec);
+      P::store_o(acc, inv, Or, qrow, g);
+    } else {
+      // delta = dout . O of the row (O in fp32 registers), lse2 in log2 units
+      const __amdgpu_buffer_rsrc_t Gr = make_rsrc(static_cast<const Elt*>(a.dout) + x.base, x.nrec);
+      typename P::Q gq;
+      P::load_q(gq, Gr, qrow, g);
+      const float dlt = col_sum(lane_dot<P>(gq, acc)) * inv;
+      const float lse2 = l_tot > 0.0f ? m_run * sl2 + __log2f(l_tot) : 0.0f;
+      const int64_t i = 64 * (int64_t)t + ql;
+      if (g == 0 && i < a.N)
+        *reinterpret_cast<float2*>(a.stats + 2 * (((int64_t)x.b * a.N + i) * a.H + x.h)) = make_float2(lse2, dlt);
+    }
+  } else {
+    float* dst = a.part + (((int64_t)x.bh * a.npart + slot) * 64 + ql) * kTilePart;
+    P::store_acc(acc, dst, g);
+    if (g == 0) *reinterpret_cast<float2*>(dst + 64) = make_float2(m_run == -INFINITY ? -INFINITY : m_run * sl2, l_tot);
+  }
+}
+
+// Merge of a split query tile's partials: thread (row tid/4, quarter tid%4)
+// owns head_dim 16*quarter .. +15 of query row 64t + tid/4.
+template <typename Elt, bool STATS>
+__global__ __launch_bounds__(256) void tile_combine_kernel(TileArgs a) {
+  const int s = blockIdx.x % a.nsplit;
+  const int bh = blockIdx.x / a.nsplit;
+  const int h = bh % a.H, b = bh / a.H;
+  const int t = clampi(a.split[4 * s], 0, a.ntiles - 1);
+  const int first = clampi(a.split[4 * s + 1], 0, a.npart);
+  const int cnt = clampi(a.split[4 * s + 2], 0, a.npart - first);
+  const int row = threadIdx.x >> 2, qd = threadIdx.x & 3;
+  const float* p0 = a.part + (((int64_t)bh * a.npart + first) * 64 + row) * kTilePart;
+  constexpr int64_t kStride = 64 * kTilePart;
+  float m = -INFINITY;
+  for (int k = 0; k < cnt; ++k) m = fmaxf(m, p0[k * kStride + 64]);
+  float l = 0.0f, o[16];
+#pragma unroll
+  for (int d = 0; d < 16; ++d) o[d] = 0.0f;
+  if (m != -INFINITY) {
+    for (int k = 0; k < cnt; ++k) {
+      const float* src = p0 + k * kStride;
+      const float w = __builtin_amdgcn_exp2f(src[64] - m);  // 0 for a partial that saw no key
+      l = fmaf(src[65], w, l);
+#pragma unroll
+      for (int d = 0; d < 16; d += 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(src + 16 * qd + d);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[d + j] = fmaf(v[j], w, o[d + j]);
+      }
+    }
+  }
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  const int64_t i = 64 * (int64_t)t + row;
+  if (i >= a.N) return;
+  const int64_t off = (((int64_t)b * a.N + i) * a.H + h) * kHeadDim + 16 * qd;
+  if constexpr (!STATS) {
+    Elt* dst = static_cast<Elt*>(a.o) + off;
+#pragma unroll
+    for (int d = 0; d < 16; ++d) dst[d] = static_cast<Elt>(o[d] * inv);
+  } else {
+    const Elt* gsrc = static_cast<const Elt*>(a.dout) + off;
+    float dlt = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 16; ++d) dlt = fmaf(static_cast<float>(gsrc[d]), o[d], dlt);
+    dlt += __shfl_xor(dlt, 1, 64);
+    dlt += __shfl_xor(dlt, 2, 64);
+    if (qd == 0)
+      *reinterpret_cast<float2*>(a.stats + 2 * (((int64_t)b * a.N + i) * a.H + h)) =
+          make_float2(l > 0.0f ? m + __log2f(l) : 0.0f, dlt * inv);
+  }
+}
+
+// ---------------------------------------------------------------- dQ
+
+template <class P>
+__global__ __launch_bounds__(256, 2) void tile_dq_kernel(TileArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 buffers x ((K, K^T) slot, V rows)
+  using Elt = typename P::Elt;
+  constexpr int kBuf = 2 * P::kBlk;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15;
+  const int g = lane >> 4;
+
+  const int wg = xcd_row_order(blockIdx.x, gridDim.x);
+  const int it = wg % a.nitems;
+  const TileCtx x = tile_ctx<P>(a, wg / a.nitems);
+  const TileItem w = tile_item(a, it);
+  const int t = w.id, e0 = w.e0, e1 = w.e1, slot = w.slot;
+  const uint32_t tb = x.tb;
+  const __amdgpu_buffer_rsrc_t Qr = make_rsrc(static_cast<const Elt*>(a.q) + x.base, x.nrec);
+  const __amdgpu_buffer_rsrc_t Kr = make_rsrc(static_cast<const Elt*>(a.k) + x.base, x.nrec);
+  const __amdgpu_buffer_rsrc_t Vr = make_rsrc(static_cast<const Elt*>(a.v) + x.base, x.nrec);
+  const __amdgpu_buffer_rsrc_t Gr = make_rsrc(static_cast<const Elt*>(a.dout) + x.base, x.nrec);
+
+  const int ql = 16 * wv + c;
+  const int64_t i = 64 * (int64_t)t + ql;
+  const uint32_t qrow = (uint32_t)i * tb;
+  typename P::Q qr, gr;
+  P::load_q(qr, Qr, qrow, g);
+  P::load_q(gr, Gr, qrow, g);
+  float2 st = make_float2(0.0f, 0.0f);
+  if (i < a.N) st = *reinterpret_cast<const float2*>(a.stats + 2 * (((int64_t)x.b * a.N + i) * a.H + x.h));
+  const float lse2 = st.x, dlt = st.y;
+  const uint32_t kl = P::k_lane(c, g), vl = P::v_lane(c, g);
+  auto blk_off = [&](int e) { return e < e1 ? (uint32_t)(64 * (a.blk[e] & (kTileFull - 1))) * tb : kOob; };
+
+  f32x4 acc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const float sl2 = a.scale_log2;
+
+  if (e0 < e1) {  // uniform
+    // V is read only as rows (dP^T = V dO^T): its transposed part stays unwritten
+    BlkSlots<P> xk;
+    BlkRows<P> xv;
+    load_blk<P>(xk, Kr, Kr, blk_off(e0), tid, tb);
+    load_rblk<P>(xv, Vr, blk_off(e0), tid, tb);
+    uint64_t mw_next = a.mask[(int64_t)e0 * 64 + ql];
+    store_blk<P>(xk, ring, tid);
+    store_rblk<P>(xv, ring + P::kBlk, tid);
+    __syncthreads();
+    for (int e = e0; e < e1; ++e) {
+      const bool full = (a.blk[e] & kTileFull) != 0;
+      const uint64_t mw = mw_next;
+      load_blk<P>(xk, Kr, Kr, blk_off(e + 1), tid, tb);
+      load_rblk<P>(xv, Vr, blk_off(e + 1), tid, tb);
+      if (e + 1 < e1) mw_next = a.mask[(int64_t)(e + 1) * 64 + ql];
+      const uint8_t* sk = ring + ((e - e0) & 1) * kBuf;
+      f32x4 s[4], dp[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        s[u] = P::qk(sk + P::blk_k(u) + kl, qr);
+        dp[u] = P::qk(sk + P::kBlk + P::blk_k(u) + kl, gr);
+      }
+      if (!full) apply_mask(s, mw, g);
+      bwdq_pass2<P>(sk, vl, s, dp, 0xF, sl2, lse2, dlt, acc);
+      if (e + 1 < e1) {
+        uint8_t* nx = ring + ((e + 1 - e0) & 1) * kBuf;
+        store_blk<P>(xk, nx, tid);
+        store_rblk<P>(xv, nx + P::kBlk, tid);
+      }
+      __syncthreads();
+    }
+  }
+  if (slot < 0) {
+    const __amdgpu_buffer_rsrc_t DQr = make_rsrc(static_cast<Elt*>(a.o) + x.base, x.nrec);
+    P::store_o(acc, a.scale, DQr, qrow, g);
+  } else {
+    P::store_acc(acc, a.part + (((int64_t)x.bh * a.npart + slot) * 64 + ql) * 64, g);
+  }
+}
+
+// ---------------------------------------------------------------- dK, dV
+
+template <class P>
+__global__ __launch_bounds__(256, 1 + (P::kSPB == 1)) void tile_dkv_kernel(TileArgs a) {
+  // 2 buffers x ((Q, Q^T) slot, (dO, dO^T) slot, 64 lse2, 64 delta)
+  extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
+  using Elt = typename P::Elt;
+  constexpr int kBuf = 2 * P::kBlk + 512;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15;
+  const int g = lane >> 4;
+
+  const int wg = xcd_row_order(blockIdx.x, gridDim.x);
+  const int it = wg % a.nitems;
+  const TileCtx x = tile_ctx<P>(a, wg / a.nitems);
+  const TileItem w = tile_item(a, it);
+  const int kb = w.id, p0 = w.e0, p1 = w.e1, slot = w.slot;
+  const uint32_t tb = x.tb;
+  const __amdgpu_buffer_rsrc_t Qr = make_rsrc(static_cast<const Elt*>(a.q) + x.base, x.nrec);
+  const __amdgpu_buffer_rsrc_t Kr = make_rsrc(static_cast<const Elt*>(a.k) + x.base, x.nrec);
+  const __amdgpu_buffer_rsrc_t Vr = make_rsrc(static_cast<const Elt*>(a.v) + x.base, x.nrec);
+  const __amdgpu_buffer_rsrc_t Gr = make_rsrc(static_cast<const Elt*>(a.dout) + x.base, x.nrec);
+  // statistics of the (batch, head): row i at float2 index i * H
+  const uint32_t sstride = (uint32_t)a.H * 8u;
+  const __amdgpu_buffer_rsrc_t Sr =
+      make_rsrc(a.stats + 2 * ((int64_t)x.b * a.N * a.H + x.h), (uint32_t)(a.N - 1) * sstride + 8u);
+
+  const int kl_ = 16 * wv + c;  // the lane's key within the block
+  const uint32_t krow = (uint32_t)(64 * kb + kl_) * tb;
+  typename P::Q kr, vr;
+  P::load_q(kr, Kr, krow, g);
+  P::load_q(vr, Vr, krow, g);
+  const uint32_t kl = P::k_lane(c, g), vl = P::v_lane(c, g);
+
+  auto ent = [&](int p) { return clampi(a.kentry[p], 0, a.nent - 1); };
+  auto tile_of = [&](int p) { return clampi(a.etile[ent(p)], 0, a.ntiles - 1); };
+  auto q_off = [&](int p) { return p < p1 ? (uint32_t)(64 * tile_of(p)) * tb : kOob; };
+  // thread tid < 64 carries the statistics of query row tid of the entry's tile
+  auto st_off = [&](int p) { return p < p1 && tid < 64 ? (uint32_t)(64 * tile_of(p) + tid) * sstride : kOob; };
+
+  f32x4 acc_k[4], acc_v[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) acc_k[dt] = acc_v[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const float sl2 = a.scale_log2;
+
+  if (p0 < p1) {  // uniform
+    BlkSlots<P> xq, xg;
+    load_blk<P>(xq, Qr, Qr, q_off(p0), tid, tb);
+    load_blk<P>(xg, Gr, Gr, q_off(p0), tid, tb);
+    uint2 xs = bload8(Sr, st_off(p0));
+    uint64_t mw_next = a.kmask[(int64_t)ent(p0) * 64 + kl_];
+    store_blk<P>(xq, ring, tid);
+    store_blk<P>(xg, ring + P::kBlk, tid);
+    bwd_stage_stats(ring + 2 * P::kBlk, xs, tid);
+    __syncthreads();
+    for (int p = p0; p < p1; ++p) {
+      const bool full = (a.blk[ent(p)] & kTileFull) != 0;
+      const uint64_t mw = mw_next;
+      load_blk<P>(xq, Qr, Qr, q_off(p + 1), tid, tb);
+      load_blk<P>(xg, Gr, Gr, q_off(p + 1), tid, tb);
+      xs = bload8(Sr, st_off(p + 1));
+      if (p + 1 < p1) mw_next = a.kmask[(int64_t)ent(p + 1) * 64 + kl_];
+      const uint8_t* sq = ring + ((p - p0) & 1) * kBuf;
+      const uint8_t* sg = sq + P::kBlk;
+      const float* stf = reinterpret_cast<const float*>(sq + 2 * P::kBlk);
+      f32x4 s[4], dp[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        s[u] = P::qk(sq + P::blk_k(u) + kl, kr);   // S[query 16u+4g+r][key c]
+        dp[u] = P::qk(sg + P::blk_k(u) + kl, vr);  // dP[query][key c]
+      }
+      if (!full) apply_mask(s, mw, g);
+#pragma unroll
+      for (int u = 0; u < 4; u += 2) {
+        const f32x4 lse0 = *reinterpret_cast<const f32x4*>(stf + 16 * u + 4 * g);
+        const f32x4 dl0 = *reinterpret_cast<const f32x4*>(stf + 64 + 16 * u + 4 * g);
+        const f32x4 lse1 = *reinterpret_cast<const f32x4*>(stf + 16 * (u + 1) + 4 * g);
+        const f32x4 dl1 = *reinterpret_cast<const f32x4*>(stf + 64 + 16 * (u + 1) + 4 * g);
+        float pa[4], pb[4], da[4], db[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          pa[r] = __builtin_amdgcn_exp2f(fmaf(s[u][r], sl2, -lse0[r]));
+          pb[r] = __builtin_amdgcn_exp2f(fmaf(s[u + 1][r], sl2, -lse1[r]));
+          da[r] = pa[r] * (dp[u][r] - dl0[r]);
+          db[r] = pb[r] * (dp[u + 1][r] - dl1[r]);
+        }
+        P::pv2(sg + P::blk_v(u) + vl, sg + P::blk_v(u + 1) + vl, pa, pb, acc_v);  // dV^T += dO^T P
+        P::pv2(sq + P::blk_v(u) + vl, sq + P::blk_v(u + 1) + vl, da, db, acc_k);  // dK^T += Q^T dS
+      }
+      if (p + 1 < p1) {
+        uint8_t* nx = ring + ((p + 1 - p0) & 1) * kBuf;
+        store_blk<P>(xq, nx, tid);
+        store_blk<P>(xg, nx + P::kBlk, tid);
+        bwd_stage_stats(nx + 2 * P::kBlk, xs, tid);
+      }
+      __syncthreads();
+    }
+  }
+  if (slot < 0) {
+    const __amdgpu_buffer_rsrc_t DKr = make_rsrc(static_cast<Elt*>(a.dk) + x.base, x.nrec);
+    const __amdgpu_buffer_rsrc_t DVr = make_rsrc(static_cast<Elt*>(a.dv) + x.base, x.nrec);
+    P::store_o(acc_v, 1.0f, DVr, krow, g);
+    P::store_o(acc_k, a.scale, DKr, krow, g);
+  } else {
+    float* dst = a.part + (((int64_t)x.bh * a.npart + slot) * 64 + kl_) * 128;
+    P::store_acc(acc_k, dst, g);
+    P::store_acc(acc_v, dst + 64, g);
+  }
+}
+
+// Sum of a split tile's (or key block's) partial rows into the output(s):
+// thread (row tid/4, quarter tid%4) owns head_dim 16*quarter .. +15.
+// WIDTH 64: dQ (scaled); WIDTH 128: dK (scaled) then dV.
+template <typename Elt, int WIDTH>
+__global__ __launch_bounds__(256) void tile_sum_kernel(TileArgs a) {
+  const int s = blockIdx.x % a.nsplit;
+  const int bh = blockIdx.x / a.nsplit;
+  const int h = bh % a.H, b = bh / a.H;
+  const int t = clampi(a.split[4 * s], 0, a.ntiles - 1);
+  const int first = clampi(a.split[4 * s + 1], 0, a.npart);
+  const int cnt = clampi(a.split[4 * s + 2], 0, a.npart - first);
+  const int row = threadIdx.x >> 2, qd = threadIdx.x & 3;
+  const int64_t i = 64 * (int64_t)t + row;
+  if (i >= a.N) return;
+  const float* p0 = a.part + (((int64_t)bh * a.npart + first) * 64 + row) * WIDTH;
+  constexpr int64_t kStride = 64 * WIDTH;
+  const int64_t off = (((int64_t)b * a.N + i) * a.H + h) * kHeadDim + 16 * qd;
+#pragma unroll
+  for (int part = 0; part < WIDTH / 64; ++part) {
+    float o[16];
+#pragma unroll
+    for (int d = 0; d < 16; ++d) o[d] = 0.0f;
+    for (int k = 0; k < cnt; ++k) {
+      const float* src = p0 + k * kStride + 64 * part + 16 * qd;
+#pragma unroll
+      for (int d = 0; d < 16; d += 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(src + d);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[d + j] += v[j];
+      }
+    }
+    const float sc = part == 0 ? a.scale : 1.0f;  // dQ and dK carry the softmax scale, dV not
+    Elt* dst = static_cast<Elt*>(part == 0 ? (WIDTH == 64 ? a.o : a.dk) : a.dv) + off;
+#pragma unroll
+    for (int d = 0; d < 16; ++d) dst[d] = static_cast<Elt>(o[d] * sc);
+  }
+}
+
+}  // namespace ma_dev

@@ -18,9 +18,18 @@ LIB_PATH = os.environ.get("MA_ATTN_LIB", os.path.join(_HERE, "libma_attn.so"))
 
 F32, BF16, F16 = 0, 1, 2
 SLIDING, DENSE, BLOCK_SPARSE, LONGFORMER, INDEX_SET = 0, 1, 2, 3, 4
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+
+
+class TileHeader(ctypes.Structure):
+    """Mirror of ``ma_attn_tile_header`` (include/ma_attn.h)."""
+
+    _fields_ = [(n, ctypes.c_int64) for n in (
+        "seq_len", "num_tiles", "num_entries", "seg", "num_q_items", "num_q_split", "num_q_partials",
+        "num_k_items", "num_k_split", "num_k_partials", "off_blk", "off_mask", "off_kmask", "off_tile",
+        "off_kentry", "off_q_items", "off_q_split", "off_k_items", "off_k_split", "total_bytes")]
 
 
 class Desc(ctypes.Structure):
@@ -49,6 +58,8 @@ class Desc(ctypes.Structure):
         ("num_indices", ctypes.c_int64),
         ("index_t_offsets", ctypes.c_void_p),
         ("index_t_queries", ctypes.c_void_p),
+        ("tile_header", ctypes.c_void_p),
+        ("tile_plan", ctypes.c_void_p),
     ]
 
 
@@ -113,6 +124,9 @@ def _open():
     lib.ma_attn_forward_noalloc.argtypes = [ctypes.POINTER(Desc)] + [ctypes.c_void_p] * 5
     lib.ma_encoder_layer_forward.restype = ctypes.c_int
     lib.ma_encoder_layer_forward.argtypes = [ctypes.POINTER(EncoderLayer)] + [ctypes.c_void_p] * 4
+    lib.ma_attn_tile_plan.restype = ctypes.c_int
+    lib.ma_attn_tile_plan.argtypes = [ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                      ctypes.POINTER(TileHeader), ctypes.c_void_p, ctypes.c_size_t]
     lib.ma_attn_reload_options.restype = None
     lib.ma_attn_reload_options.argtypes = []
     if lib.ma_attn_abi_version() != ABI_VERSION:
@@ -130,7 +144,7 @@ def last_error() -> str:
 def make_desc(B, N, H, D, dtype_code, pattern, left=0, right=0, dilation=1, causal=False,
               block_size=64, block_table_ptr=0, blocks_per_row=0, num_global=0,
               scale=0.0, index_offsets_ptr=0, index_keys_ptr=0, num_indices=0, index_t_offsets_ptr=0,
-              index_t_queries_ptr=0) -> Desc:
+              index_t_queries_ptr=0, tile_header_ptr=0, tile_plan_ptr=0) -> Desc:
     d = Desc()
     d.batch, d.seq_len, d.num_heads, d.head_dim = int(B), int(N), int(H), int(D)
     d.dtype, d.pattern = int(dtype_code), int(pattern)
@@ -146,6 +160,8 @@ def make_desc(B, N, H, D, dtype_code, pattern, left=0, right=0, dilation=1, caus
     d.num_indices = int(num_indices)
     d.index_t_offsets = int(index_t_offsets_ptr) or None
     d.index_t_queries = int(index_t_queries_ptr) or None
+    d.tile_header = int(tile_header_ptr) or None
+    d.tile_plan = int(tile_plan_ptr) or None
     return d
 
 
@@ -235,6 +251,33 @@ def pattern_csr(desc: Desc, host_table: torch.Tensor | None = None):
     return offsets, keys[:nnz]
 
 
+def tile_header_of(offsets: torch.Tensor, keys: torch.Tensor, seq_len: int, seg: int = 0) -> TileHeader:
+    """Sizes of a CSR key set's tile plan (ma_attn_tile_plan without the plan)."""
+    off = offsets.to(torch.int64).contiguous()
+    kk = keys.to(torch.int32).contiguous()
+    hdr = TileHeader()
+    if LIB.ma_attn_tile_plan(int(seq_len), off.data_ptr(), kk.data_ptr() if kk.numel() else None, int(seg),
+                             ctypes.byref(hdr), None, 0) != 0:
+        raise ValueError(last_error())
+    return hdr
+
+
+def tile_plan(offsets: torch.Tensor, keys: torch.Tensor, seq_len: int, seg: int = 0):
+    """The 64x64-tile plan of a CSR key set (host int64 offsets, int32 keys):
+    (TileHeader, host uint8 tensor of header.total_bytes).  ma_attn_tile_plan."""
+    off = offsets.to(torch.int64).contiguous()
+    kk = keys.to(torch.int32).contiguous()
+    hdr = TileHeader()
+    kptr = kk.data_ptr() if kk.numel() else None
+    if LIB.ma_attn_tile_plan(int(seq_len), off.data_ptr(), kptr, int(seg), ctypes.byref(hdr), None, 0) != 0:
+        raise ValueError(last_error())
+    blob = torch.empty(int(hdr.total_bytes), dtype=torch.uint8)
+    if LIB.ma_attn_tile_plan(int(seq_len), off.data_ptr(), kptr, int(seg), ctypes.byref(hdr), blob.data_ptr(),
+                             blob.numel()) != 0:
+        raise ValueError(last_error())
+    return hdr, blob
+
+
 def forward_noalloc_raw(desc: Desc, q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, stream: int = 0) -> None:
     """ma_attn_forward_noalloc: no workspace, no allocation (the library's
     static scratch).  Raises RuntimeError on rejection."""
@@ -267,5 +310,5 @@ def default_scale(D: int) -> float:
 
 
 __all__ = ["LIB", "Desc", "make_desc", "forward_raw", "forward_noalloc_raw", "validate", "workspace_size",
-           "block_table", "row_keys", "pattern_csr", "reload_options", "last_error", "EncoderLayer", "encoder_layer_forward_raw", "DTYPES", "default_scale",
+           "block_table", "row_keys", "pattern_csr", "tile_plan", "tile_header_of", "TileHeader", "reload_options", "last_error", "EncoderLayer", "encoder_layer_forward_raw", "DTYPES", "default_scale",
            "SLIDING", "DENSE", "BLOCK_SPARSE", "LONGFORMER", "INDEX_SET", "F32", "BF16", "F16"]

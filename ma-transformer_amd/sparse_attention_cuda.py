@@ -32,6 +32,7 @@ sliding and dense patterns, in the input dtype:
 """
 from __future__ import annotations
 
+import ctypes
 from typing import List
 
 import torch
@@ -290,10 +291,23 @@ class IndexSet:
     (row, col) entry lists and drops repeated entries.
     """
 
-    def __init__(self, offsets: torch.Tensor, keys: torch.Tensor, seq_len: int, device=None):
+    def __init__(self, offsets: torch.Tensor, keys: torch.Tensor, seq_len: int, device=None, tiles="auto",
+                 tile_seg: int = 0):
+        """tiles: "auto" builds the set's 64x64 tile plan (the tiled MFMA
+        kernels, head_dim 64) when the set's keys cluster in blocks -- at
+        least 1/16 of each touched 64x64 block on average; True always
+        builds it, False never (the gather kernels).  tile_seg: blocks per
+        work item of the tiled kernels (0: the library's default)."""
         self.seq_len = int(seq_len)
         off, kk = _validated_index_set(offsets, keys, self.seq_len)
         dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self.tile_header = self.tile_plan = None
+        if tiles and self.seq_len > 0:
+            hdr = _ma.tile_header_of(off, kk, self.seq_len, tile_seg)
+            dense_work = hdr.num_entries * 4096
+            if tiles is True or (dense_work <= 16 * max(int(kk.numel()), 1) and hdr.total_bytes <= (512 << 20)):
+                self.tile_header, blob = _ma.tile_plan(off, kk, self.seq_len, tile_seg)
+                self.tile_plan = blob.to(dev)
         self.offsets = off.to(dev)
         self.keys = (kk if kk.numel() else torch.zeros(1, dtype=torch.int32)).to(dev)
         self.num_indices = int(kk.numel())
@@ -307,6 +321,11 @@ class IndexSet:
         t_q = rows[order].to(torch.int32)
         self.t_offsets = t_off.to(dev)
         self.t_queries = (t_q if t_q.numel() else torch.zeros(1, dtype=torch.int32)).to(dev)
+
+    def _tile_kw(self) -> dict:
+        if self.tile_plan is None:
+            return {}
+        return dict(tile_header_ptr=ctypes.addressof(self.tile_header), tile_plan_ptr=self.tile_plan.data_ptr())
 
     @staticmethod
     def from_coo(rows, cols, seq_len: int, device=None) -> "IndexSet":
@@ -383,7 +402,8 @@ def index_set_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tenso
     if index_set.offsets.device != query.device:
         raise RuntimeError("IndexSet is on another device than the inputs")
     return _launch(query, key, value, _ma.INDEX_SET, index_offsets_ptr=index_set.offsets.data_ptr(),
-                   index_keys_ptr=index_set.keys.data_ptr(), num_indices=index_set.num_indices)
+                   index_keys_ptr=index_set.keys.data_ptr(), num_indices=index_set.num_indices,
+                   **index_set._tile_kw())
 
 
 def index_set_backward(query, key, value, grad_out, index_set) -> List[torch.Tensor]:
@@ -402,7 +422,7 @@ def index_set_backward(query, key, value, grad_out, index_set) -> List[torch.Ten
     return _backward(query, key, value, grad_out, _ma.INDEX_SET,
                      index_offsets_ptr=index_set.offsets.data_ptr(), index_keys_ptr=index_set.keys.data_ptr(),
                      num_indices=index_set.num_indices, index_t_offsets_ptr=index_set.t_offsets.data_ptr(),
-                     index_t_queries_ptr=index_set.t_queries.data_ptr())
+                     index_t_queries_ptr=index_set.t_queries.data_ptr(), **index_set._tile_kw())
 
 
 # ---------------------------------------------------------------- backward (HIP kernels)
