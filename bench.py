@@ -19,6 +19,9 @@ forward pass over that batch.  Prints ONE JSON line:
              names it: it is not measured in this run)
   cpu_baseline  the CPU oracle (restatement of ma_core.cpp:160-246) on this
              host, single thread, bounded sample of the same workload
+  pattern_copy  sliding windows: the stream kernel's access pattern without
+             its arithmetic (ma_attn_copy_probe), timed the same way -- the
+             copy speed that pattern reaches on the device
 
 Inputs are resident in HBM before timing; 4+ distinct input sets (>1 GB in
 total) are rotated so the 256 MB MALL cannot serve a repeated set.
@@ -542,6 +545,36 @@ def main() -> int:
     per_launch_ms = sorted(a.elapsed_time(b) for a, b in ev)
     mean_launch_ms = sum(per_launch_ms) / len(per_launch_ms)
 
+    # The stream kernel's access pattern without its arithmetic (ma_attn_copy_probe,
+    # same workgroups, tiles and halo blocks), timed the same way on the same
+    # rotated inputs: the copy speed this pattern reaches on this device.
+    probe_us = None
+    if not bwd and pk["pattern"] == "sliding":
+        import ma_attn as _ma
+        pdesc = _ma.make_desc(B, N, H, D, _ma.DTYPES[dtype], _ma.SLIDING, left=pk["left"], right=pk["right"],
+                              dilation=pk.get("dilation", 1))
+        pout = torch.empty_like(sets[0][0])
+        raw = stream.cuda_stream
+        try:
+            for i in range(20):
+                s_ = sets[i % nsets]
+                _ma.copy_probe_raw(pdesc, s_[0].data_ptr(), s_[1].data_ptr(), s_[2].data_ptr(), pout.data_ptr(), raw)
+            pev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                   for _ in range(args.steps)]
+            for a_, b_ in pev:
+                a_.record(stream)
+                b_.record(stream)
+            torch.cuda.synchronize()
+            for i in range(args.steps):
+                s_ = sets[i % nsets]
+                _ma.copy_probe_raw(pdesc, s_[0].data_ptr(), s_[1].data_ptr(), s_[2].data_ptr(), pout.data_ptr(), raw,
+                                   (pev[i][0].cuda_event, pev[i][1].cuda_event))
+            torch.cuda.synchronize()
+            probe_us = 1e3 * sum(a_.elapsed_time(b_) for a_, b_ in pev) / len(pev)
+        except RuntimeError:
+            probe_us = None  # the stream kernel does not take this shape
+        del pout
+
     queries = B * H * N
     alg_bytes = tensors * B * N * H * D * elt
     if pk["pattern"] == "index_set" or (bwd and pk["pattern"] not in ("sliding", "dense")):
@@ -597,6 +630,13 @@ def main() -> int:
         "copy_kernel_gbps": copy_gbps,
         "device": torch.cuda.get_device_name(dev),
     }
+    if probe_us is not None:
+        # algorithmic bytes over the probe's mean stamped duration, and the
+        # kernel's speed as a fraction of it
+        out["pattern_copy"] = {"kernel_us_mean": probe_us,
+                               "gbps": (4 * B * N * H * D * elt) / (probe_us * 1e-6) / 1e9,
+                               "kernel_frac_of_pattern_copy": probe_us / (mean_launch_ms * 1e3),
+                               "source": "ma_attn_copy_probe (same workgroups, tiles and halo blocks, no arithmetic)"}
     if bwd:
         out["pass"] = "backward"
     if not args.no_cpu_baseline and not bwd:

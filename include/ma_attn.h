@@ -271,6 +271,22 @@ void ma_attn_reload_options(void);
 int ma_attn_tile_plan(int64_t seq_len, const int64_t* offsets, const int32_t* keys, int64_t seg,
                       ma_attn_tile_header* header, void* plan, size_t plan_bytes);
 
+/*
+ * Measurement: the forward stream kernel's memory traffic for desc (SLIDING,
+ * head_dim 64) without its arithmetic -- the same workgroups, chunks, 64-row
+ * tiles of one (batch, head) and halo blocks, writing o = q xor k xor v
+ * bitwise.  Gives the copy speed of the stream kernel's access pattern on the
+ * device, the ceiling that kernel runs against.  Returns non-zero when the
+ * stream kernel would not take desc.  The _timed form stamps the kernel's
+ * start and stop on two caller-created events, as ma_attn_forward_timed.
+ * No reference counterpart.
+ */
+int ma_attn_copy_probe(const ma_attn_desc* desc, const void* q, const void* k, const void* v,
+                       void* o, void* stream);
+int ma_attn_copy_probe_timed(const ma_attn_desc* desc, const void* q, const void* k,
+                             const void* v, void* o, void* stream, void* start_event,
+                             void* stop_event);
+
 /* ABI version of this header (bumped on incompatible change). */
 int ma_attn_abi_version(void);
 

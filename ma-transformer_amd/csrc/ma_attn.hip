@@ -2189,6 +2189,53 @@ int64_t ma_attn_pattern_csr(const ma_attn_desc* desc, const int32_t* host_block_
   return nnz;
 }
 
+int ma_attn_copy_probe(const ma_attn_desc* desc, const void* q, const void* k, const void* v, void* o,
+                       void* stream) {
+  g_last_error.clear();
+  if (validate(desc)) return 1;
+  if (desc->pattern != MA_ATTN_SLIDING) return fail("ma_attn_copy_probe: SLIDING descriptors only");
+  if (desc->batch * desc->seq_len * desc->num_heads == 0) return 0;
+  if (!q || !k || !v || !o) return fail("ma_attn: null tensor pointer");
+  if (!stream_applies(desc, q, k, v, o))
+    return fail("ma_attn_copy_probe: the stream kernel does not take this descriptor (head_dim 64, "
+                "left, right >= 0, 16-byte aligned tensors)");
+  const StreamPlan p = stream_plan(desc);
+  StreamArgs a;
+  memset(&a, 0, sizeof(a));
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.N = desc->seq_len;
+  a.H = desc->num_heads;
+  a.left = (int32_t)p.geom.left;
+  a.right = (int32_t)p.geom.right;
+  a.dil = (int32_t)p.geom.dil;
+  a.tiles = (int32_t)p.tiles;
+  a.chunk = (int32_t)p.chunk;
+  a.chunks = (int32_t)p.chunks;
+  a.tok_bytes = (int32_t)p.tok_bytes;
+  a.pairs = p.geom.right > 0 && p.wgs % 16 == 0 && p.chunks % 2 == 0 ? 1 : 0;  // as launch_stream
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  (void)hipGetLastError();
+  if (desc->dtype == MA_ATTN_F32)
+    launch(true, copy_probe_kernel<256>, dim3((unsigned)p.wgs), dim3(256), 0u, st, a);
+  else
+    launch(true, copy_probe_kernel<128>, dim3((unsigned)p.wgs), dim3(256), 0u, st, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail("ma_attn_copy_probe: kernel launch failed: %s", hipGetErrorString(e));
+  return 0;
+}
+
+int ma_attn_copy_probe_timed(const ma_attn_desc* desc, const void* q, const void* k, const void* v, void* o,
+                             void* stream, void* start_event, void* stop_event) {
+  g_ev_start = static_cast<hipEvent_t>(start_event);
+  g_ev_stop = static_cast<hipEvent_t>(stop_event);
+  const int rc = ma_attn_copy_probe(desc, q, k, v, o, stream);
+  g_ev_start = g_ev_stop = nullptr;
+  return rc;
+}
+
 int ma_attn_tile_plan(int64_t N, const int64_t* off, const int32_t* keys, int64_t seg, ma_attn_tile_header* hdr,
                       void* plan, size_t plan_bytes) {
   g_last_error.clear();

@@ -843,3 +843,88 @@ __global__ __launch_bounds__(256) void longformer_combine(const float* __restric
 }
 
 }  // namespace ma_dev
+
+namespace ma_dev {
+
+// ---------------------------------------------------------------- copy probe
+//
+// The stream kernel's memory traffic without its arithmetic: the same
+// workgroups, chunks and 64-row tiles of one (batch, head, residue class),
+// the same halo blocks before (and, with a right window, after) each chunk,
+// O = Q xor K xor V bitwise.  It measures what this access pattern can move
+// on the device -- the ceiling a bandwidth-bound stream kernel runs against.
+// EB: bytes per head row (128 for 16-bit, 256 for fp32).
+template <int EB>
+__global__ __launch_bounds__(256) void copy_probe_kernel(StreamArgs a) {
+  constexpr int CPR = EB / 16;              // 16-byte chunks per row
+  constexpr int NU = 64 * CPR / 256;        // uint4 per thread per tile and tensor
+  const int tid = threadIdx.x;
+  int lin = blockIdx.x;
+  if (a.pairs) {
+    const int x = lin & 7, i = lin >> 3;
+    lin = 16 * (i >> 1) + 2 * x + (i & 1);
+  }
+  const int chunk_id = lin % a.chunks;
+  lin /= a.chunks;
+  const int rho = lin % a.dil;
+  lin /= a.dil;
+  const int h = lin % (int)a.H;
+  const int b = lin / (int)a.H;
+  const int Nr = (int)((a.N - rho + a.dil - 1) / a.dil);
+  const int tiles_r = (Nr + 63) >> 6;
+  const int t0 = chunk_id * a.chunk;
+  const int t1 = min(t0 + a.chunk, tiles_r);
+  if (t0 >= t1) return;
+  const uint32_t tb = (uint32_t)a.tok_bytes;
+  const int nblk = (Nr + 63) >> 6;
+  const int hlo = max(floordiv32(t0 * 64 - a.left, 64), 0);               // first halo block before the chunk
+  const int hhi = min(floordiv32((t1 - 1) * 64 + 63 + a.right, 64), nblk - 1);  // last block after it
+  const int base_row = hlo * 64;
+  const int64_t base = (((int64_t)b * a.N + rho) * a.H + h) * EB + (int64_t)base_row * tb;  // bytes
+  const int64_t range = (int64_t)(Nr - 1 - base_row) * tb + EB;
+  const uint32_t nrec = (uint32_t)(range < 0x7FFFFFFF ? range : 0x7FFFFFFF);
+  const __amdgpu_buffer_rsrc_t Qr = make_rsrc(static_cast<const uint8_t*>(a.q) + base, nrec);
+  const __amdgpu_buffer_rsrc_t Kr = make_rsrc(static_cast<const uint8_t*>(a.k) + base, nrec);
+  const __amdgpu_buffer_rsrc_t Vr = make_rsrc(static_cast<const uint8_t*>(a.v) + base, nrec);
+  const __amdgpu_buffer_rsrc_t Or = make_rsrc(static_cast<uint8_t*>(a.o) + base, nrec);
+  auto off = [&](int blk, int j) {
+    const int e = tid + 256 * j;
+    return (uint32_t)(blk * 64 + e / CPR - base_row) * tb + (uint32_t)(e % CPR) * 16;
+  };
+  // halo blocks: K and V rows the window reads outside the chunk's own tiles
+  uint4 hx = make_uint4(0u, 0u, 0u, 0u);
+  for (int blk = hlo; blk <= hhi; ++blk) {
+    if (blk >= t0 && blk < t1) continue;
+#pragma unroll
+    for (int j = 0; j < NU; ++j) {
+      const uint4 x = bload16(Kr, off(blk, j)), y = bload16(Vr, off(blk, j));
+      hx.x ^= x.x ^ y.x;
+      hx.y ^= x.y ^ y.y;
+    }
+  }
+  uint4 x[3][NU];
+#pragma unroll
+  for (int j = 0; j < NU; ++j) {
+    x[0][j] = bload16(Qr, off(t0, j));
+    x[1][j] = bload16(Kr, off(t0, j));
+    x[2][j] = bload16(Vr, off(t0, j));
+  }
+  for (int t = t0; t < t1; ++t) {
+    uint4 y[NU];
+#pragma unroll
+    for (int j = 0; j < NU; ++j)
+      y[j] = make_uint4(x[0][j].x ^ x[1][j].x ^ x[2][j].x ^ hx.x, x[0][j].y ^ x[1][j].y ^ x[2][j].y ^ hx.y,
+                        x[0][j].z ^ x[1][j].z ^ x[2][j].z, x[0][j].w ^ x[1][j].w ^ x[2][j].w);
+    const uint32_t nx = t + 1 < t1 ? 0u : kOob;
+#pragma unroll
+    for (int j = 0; j < NU; ++j) {
+      x[0][j] = bload16(Qr, nx + off(t + 1, j));
+      x[1][j] = bload16(Kr, nx + off(t + 1, j));
+      x[2][j] = bload16(Vr, nx + off(t + 1, j));
+    }
+#pragma unroll
+    for (int j = 0; j < NU; ++j) bstore16(Or, off(t, j), y[j]);
+  }
+}
+
+}  // namespace ma_dev
