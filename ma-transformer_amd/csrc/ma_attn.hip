@@ -1791,10 +1791,12 @@ int launch_tiles_bwd(const ma_attn_desc* d, const void* const* ptrs, void* ws, h
       reserve_lds(reinterpret_cast<const void*>(kq), shm_q, st) ||
       reserve_lds(reinterpret_cast<const void*>(kkv), shm_kv, st))
     return 1;
-  // statistics {lse2, delta}, then dQ (query side)
-  launch(false, kf, dim3((unsigned)(bh * a.nitems)), dim3(256), (uint32_t)shm_f, st, a);
-  if (a.nsplit > 0)
+  // split tiles: statistics from partials and their merge; then dQ (unsplit
+  // tiles compute their own statistics there)
+  if (a.nsplit > 0) {
+    launch(false, kf, dim3((unsigned)(bh * a.nitems)), dim3(256), (uint32_t)shm_f, st, a);
     launch(false, tile_combine_kernel<Elt, true>, dim3((unsigned)(bh * a.nsplit)), dim3(256), 0u, st, a);
+  }
   launch(false, kq, dim3((unsigned)(bh * a.nitems)), dim3(256), (uint32_t)shm_q, st, a);
   if (a.nsplit > 0) launch(false, tile_sum_kernel<Elt, 64>, dim3((unsigned)(bh * a.nsplit)), dim3(256), 0u, st, a);
   // dK, dV (key side)

@@ -10,15 +10,17 @@
 // results a combine kernel merges, so one long row (a Longformer global row,
 // a global key's column) does not hold up the launch.
 //
-//   tile_fwd_kernel      O (or, with STATS, the backward's {lse2, delta}):
-//                        one workgroup per (batch, head, item), 4 waves x 16
+//   tile_fwd_kernel      O (or, with STATS, a split tile's backward {lse2,
+//                        delta} partials): one workgroup per (batch, head,
+//                        item), 4 waves x 16
 //                        queries; key blocks through a two-buffer LDS ring
 //                        with the next block (and its mask word) in flight,
 //                        online softmax in registers.
 //   tile_combine_kernel  log-sum-exp merge of a split tile's partials.
-//   tile_dq_kernel       dQ over a query tile's entries (statistics given):
-//                        K staged as (K, K^T), V as rows; dS in registers,
-//                        dQ^T += K^T dS^T.
+//   tile_dq_kernel       dQ over a query tile's entries (an unsplit tile
+//                        first computes its own statistics in a pass over
+//                        them): K staged as (K, K^T), V as rows; dS in
+//                        registers, dQ^T += K^T dS^T.
 //   tile_dkv_kernel      dK, dV over a key block's entries: each entry's
 //                        query tile staged as (Q, Q^T), (dO, dO^T) and its 64
 //                        statistics; dV^T += dO^T P, dK^T += Q^T dS.
@@ -188,6 +190,7 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void tile_fwd_kernel(TileArgs a
   const TileCtx x = tile_ctx<P>(a, wg / a.nitems);
   const TileItem w = tile_item(a, it);
   const int t = w.id, e0 = w.e0, e1 = w.e1, slot = w.slot;
+  if (STATS && slot < 0) return;  // uniform: an unsplit tile's statistics come from its dQ pass
   const uint32_t tb = x.tb;
   const __amdgpu_buffer_rsrc_t Qr = make_rsrc(static_cast<const Elt*>(a.q) + x.base, x.nrec);
   const __amdgpu_buffer_rsrc_t Kr = make_rsrc(static_cast<const Elt*>(a.k) + x.base, x.nrec);
@@ -301,6 +304,22 @@ __global__ __launch_bounds__(256) void tile_combine_kernel(TileArgs a) {
 }
 
 // ---------------------------------------------------------------- dQ
+//
+// An unsplit tile (one work item) computes its own statistics: pass 1 over
+// its entries gives {lse2, delta} (online max, sum of e and of e*dP, no O),
+// pass 2 dQ; with at most two entries both blocks stay resident in the two
+// buffers between the passes.  A split tile's items read the statistics the
+// merge of its partials wrote.  Every tile's statistics land in the
+// workspace for the dK/dV pass.
+
+// {lse2, delta} of the lane's query from pass 1's running sums (0, 0 for a
+// row with no key).
+__device__ __forceinline__ void tile_stats(float m_run, float l_run, float a_run, float sl2, float& lse2,
+                                           float& dlt) {
+  const float l_tot = col_sum(l_run), a_tot = col_sum(a_run);
+  lse2 = l_tot > 0.0f ? m_run * sl2 + __log2f(l_tot) : 0.0f;
+  dlt = l_tot > 0.0f ? a_tot / l_tot : 0.0f;
+}
 
 template <class P>
 __global__ __launch_bounds__(256, 2) void tile_dq_kernel(TileArgs a) {
@@ -330,34 +349,50 @@ __global__ __launch_bounds__(256, 2) void tile_dq_kernel(TileArgs a) {
   typename P::Q qr, gr;
   P::load_q(qr, Qr, qrow, g);
   P::load_q(gr, Gr, qrow, g);
-  float2 st = make_float2(0.0f, 0.0f);
-  if (i < a.N) st = *reinterpret_cast<const float2*>(a.stats + 2 * (((int64_t)x.b * a.N + i) * a.H + x.h));
-  const float lse2 = st.x, dlt = st.y;
+  float* srow = a.stats + 2 * (((int64_t)x.b * a.N + i) * a.H + x.h);
+  const bool own = slot < 0;  // uniform: statistics from its own first pass
+  float lse2 = 0.0f, dlt = 0.0f;
+  if (!own && i < a.N) {
+    const float2 st = *reinterpret_cast<const float2*>(srow);
+    lse2 = st.x;
+    dlt = st.y;
+  }
   const uint32_t kl = P::k_lane(c, g), vl = P::v_lane(c, g);
-  auto blk_off = [&](int e) { return e < e1 ? (uint32_t)(64 * (a.blk[e] & (kTileFull - 1))) * tb : kOob; };
+
+  // items: pass 1 (own statistics only) over the entries, then pass 2
+  const int ne = e1 - e0;
+  const int nit = own ? 2 * ne : ne;
+  const bool resident = own && ne <= 2;
+  auto entry_of = [&](int k) { return e0 + (own && k >= ne ? k - ne : k); };
+  auto buf_of = [&](int k) { return resident ? (k < ne ? k : k - ne) : (k & 1); };
+  auto loads = [&](int k) { return k < nit && (!resident || k < ne); };
+  auto blk_off = [&](int k) {
+    return loads(k) ? (uint32_t)(64 * (a.blk[entry_of(k)] & (kTileFull - 1))) * tb : kOob;
+  };
 
   f32x4 acc[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   const float sl2 = a.scale_log2;
+  float m_run = -INFINITY, l_run = 0.0f, a_run = 0.0f;
 
-  if (e0 < e1) {  // uniform
+  if (nit > 0) {  // uniform
     // V is read only as rows (dP^T = V dO^T): its transposed part stays unwritten
     BlkSlots<P> xk;
     BlkRows<P> xv;
-    load_blk<P>(xk, Kr, Kr, blk_off(e0), tid, tb);
-    load_rblk<P>(xv, Vr, blk_off(e0), tid, tb);
-    uint64_t mw_next = a.mask[(int64_t)e0 * 64 + ql];
+    load_blk<P>(xk, Kr, Kr, blk_off(0), tid, tb);
+    load_rblk<P>(xv, Vr, blk_off(0), tid, tb);
+    uint64_t mw_next = a.mask[(int64_t)entry_of(0) * 64 + ql];
     store_blk<P>(xk, ring, tid);
     store_rblk<P>(xv, ring + P::kBlk, tid);
     __syncthreads();
-    for (int e = e0; e < e1; ++e) {
-      const bool full = (a.blk[e] & kTileFull) != 0;
+    for (int k = 0; k < nit; ++k) {
+      const bool full = (a.blk[entry_of(k)] & kTileFull) != 0;
       const uint64_t mw = mw_next;
-      load_blk<P>(xk, Kr, Kr, blk_off(e + 1), tid, tb);
-      load_rblk<P>(xv, Vr, blk_off(e + 1), tid, tb);
-      if (e + 1 < e1) mw_next = a.mask[(int64_t)(e + 1) * 64 + ql];
-      const uint8_t* sk = ring + ((e - e0) & 1) * kBuf;
+      load_blk<P>(xk, Kr, Kr, blk_off(k + 1), tid, tb);
+      load_rblk<P>(xv, Vr, blk_off(k + 1), tid, tb);
+      if (k + 1 < nit) mw_next = a.mask[(int64_t)entry_of(k + 1) * 64 + ql];
+      const uint8_t* sk = ring + buf_of(k) * kBuf;
       f32x4 s[4], dp[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -365,14 +400,23 @@ __global__ __launch_bounds__(256, 2) void tile_dq_kernel(TileArgs a) {
         dp[u] = P::qk(sk + P::kBlk + P::blk_k(u) + kl, gr);
       }
       if (!full) apply_mask(s, mw, g);
-      bwdq_pass2<P>(sk, vl, s, dp, 0xF, sl2, lse2, dlt, acc);
-      if (e + 1 < e1) {
-        uint8_t* nx = ring + ((e + 1 - e0) & 1) * kBuf;
+      if (own && k < ne) {  // pass 1
+        bwdq_pass1(s, dp, 0xF, sl2, m_run, l_run, a_run);
+        if (k == ne - 1) tile_stats(m_run, l_run, a_run, sl2, lse2, dlt);
+      } else {
+        bwdq_pass2<P>(sk, vl, s, dp, 0xF, sl2, lse2, dlt, acc);
+      }
+      if (loads(k + 1)) {
+        uint8_t* nx = ring + buf_of(k + 1) * kBuf;
         store_blk<P>(xk, nx, tid);
         store_rblk<P>(xv, nx + P::kBlk, tid);
       }
       __syncthreads();
     }
+  }
+  if (own) {
+    if (ne == 0) tile_stats(m_run, l_run, a_run, sl2, lse2, dlt);  // a tile with no key: zeros
+    if (g == 0 && i < a.N) *reinterpret_cast<float2*>(srow) = make_float2(lse2, dlt);
   }
   if (slot < 0) {
     const __amdgpu_buffer_rsrc_t DQr = make_rsrc(static_cast<Elt*>(a.o) + x.base, x.nrec);
