@@ -42,6 +42,7 @@
 #include "stream_kernel.h"
 #include "block_kernel.h"
 #include "backward_kernel.h"
+#include "bwd_fused_kernel.h"
 #include "tile_kernel.h"
 #include "tick_features.h"
 
@@ -89,8 +90,9 @@ namespace {
 //   MA_ATTN_KERNEL=band     16-bit windows on the band kernel, not the stream kernel
 //   MA_ATTN_NO_FIXED=1      forward windows on the generic stream tiles
 //   MA_ATTN_BWD_NO_FIXED=1  backward windows on the generic stream tiles
+//   MA_ATTN_BWD_UNFUSED=1   the causal-64 16-bit backward as two launches (dQ, then dK/dV)
 struct Options {
-  bool force_rows, force_band, no_fixed, bwd_no_fixed;
+  bool force_rows, force_band, no_fixed, bwd_no_fixed, bwd_unfused;
 };
 
 Options read_options() {
@@ -100,6 +102,7 @@ Options read_options() {
   o.force_band = k && strcmp(k, "band") == 0;
   o.no_fixed = getenv("MA_ATTN_NO_FIXED") != nullptr;
   o.bwd_no_fixed = getenv("MA_ATTN_BWD_NO_FIXED") != nullptr;
+  o.bwd_unfused = getenv("MA_ATTN_BWD_UNFUSED") != nullptr;
   return o;
 }
 
@@ -1577,6 +1580,22 @@ int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* 
   // and [i-32, i+31] (cfg 2)
   const bool no_fixed = g_opt.bwd_no_fixed;
   const int fixed = !chunked || no_fixed ? 0 : L == 63 && R == 0 ? 1 : L == 32 && R == 31 ? 2 : 0;
+  if constexpr (P::kSPB == 1) {
+    if (fixed == 1 && !g_opt.bwd_unfused) {
+      // the causal 64 window in 16 bits: one fused launch (bwd_fused_kernel.h),
+      // two 36.5 KB ring slots, two workgroups per CU; chunks fitted to one
+      // round of the resident workgroups (measured on the target: 116.5 us at
+      // one round, chunk 16; 126.8-136.5 us at two to six rounds)
+      const size_t shm = 2 * (size_t)FusedSlot::kBytes;
+      const int64_t per_stream = ma::imax64(1, 256 * 2 / streams);
+      a.chunk = (int32_t)ma::imax64(1, (a.tiles + per_stream - 1) / per_stream);
+      a.chunks = (int32_t)((a.tiles + a.chunk - 1) / a.chunk);
+      auto kf = &bwd_fused_kernel<P>;
+      if (reserve_lds(reinterpret_cast<const void*>(kf), shm, st)) return 1;
+      launch(true, kf, dim3((unsigned)(streams * a.chunks)), dim3(256), (uint32_t)shm, st, a);
+      return 0;
+    }
+  }
   auto kq = !chunked     ? &bwd_q_kernel<P>
             : fixed == 1 ? &bwd_q_stream_kernel<P, 63, 0>
             : fixed == 2 ? &bwd_q_stream_kernel<P, 32, 31>
@@ -1585,7 +1604,6 @@ int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* 
              : fixed == 1 ? &bwd_kv_stream_kernel<P, 63, 0>
              : fixed == 2 ? &bwd_kv_stream_kernel<P, 32, 31>
                           : &bwd_kv_stream_kernel<P, -1, -1>;
-  const int variant = !chunked ? 0 : 1 + fixed;
   // chunks per stream fitted to two rounds of the resident workgroups (2 per
   // CU for 16-bit, 1 for fp32, whose block buffers are twice the size): the
   // second round fills the slots the first round's faster workgroups leave.
