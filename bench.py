@@ -583,7 +583,8 @@ def main() -> int:
     # forward: Q.K^T and P.V; backward: S, dP = dO.V^T, dV, dQ, dK (2 FLOP per MAC)
     flops = (10 if bwd else 4) * D * key_count(N, pk) * B * H
     achieved_gbps = alg_bytes / (mean_launch_ms * 1e-3) / 1e9
-    traffic = None if bwd else load_traffic(args.workload)
+    tkey = args.workload + ("_backward" if bwd else "")
+    traffic = load_traffic(tkey)
 
     copy_gbps = copy_bandwidth(dev, stream)
 
@@ -591,7 +592,7 @@ def main() -> int:
     mfma_peak = MFMA_BF16_PEAK_TFLOPS if dt_name == "bf16" else MFMA_F32_PEAK_TFLOPS
     tflops = flops / (mean_launch_ms * 1e-3) / 1e12
     # traffic is not measured in this run: it is the committed rocprofv3 counter summary
-    tsrc = f"profiles/traffic_{args.workload}.txt (rocprofv3 FETCH_SIZE + WRITE_SIZE, committed)" \
+    tsrc = f"profiles/traffic_{tkey}.txt (rocprofv3 FETCH_SIZE + WRITE_SIZE, committed)" \
         if traffic is not None else None
     if flops / alg_bytes > mfma_peak * 1e12 / (HBM_PEAK_GBPS * 1e9):
         roofline = {"bound": "mfma", "achieved": tflops, "peak": mfma_peak, "unit": "TFLOP/s",

@@ -1,32 +1,36 @@
 // bwd_fused_kernel.h -- one-launch backward of the causal 64-key window
 // (keys [m-63, m] on a residue class m of any dilation), bf16/fp16, head_dim
 // 64.  Same arithmetic as bwd_q_stream_kernel + bwd_kv_stream_kernel
-// (backward_kernel.h), in one pass over the inputs.
+// (backward_kernel.h), in one pass over the inputs, each probability and
+// its dS computed once.
 //
 // One workgroup (4 waves) streams a chunk [t0, t1) of the 64-row tiles of one
-// (batch, head, residue class).  Step t holds tiles t-1 and t in a two-slot
-// LDS ring; a slot is the tile's K, V, Q and dO rows (row-major, 144 B rows)
-// and its 64 {lse2, delta}:
-//   query pass, tile t: S^T = K Q^T and dP^T = V dO^T over the 5 key
-//     sub-tiles of each wave's 16 queries (in tiles t-1 and t), lse2 and
-//     delta of the queries in registers (two-pass softmax, every score
-//     resident), dS^T = P^T (dP^T - delta), dQ^T += K^T dS^T.  dQ is stored,
-//     {lse2, delta} go to the slot.
-//   key pass, tile t-1 (complete now: the queries of its keys lie in tiles
-//     t-1 and t, both with statistics): S = Q K^T and dP = dO V^T over the 5
-//     query sub-tiles of each wave's 16 keys, P and dS from the slots'
-//     statistics, dV^T += dO^T P and dK^T += Q^T dS.
-// The transposed operands (K^T, Q^T, dO^T) are read from the row-major slots
-// with gfx950's LDS transpose read (ds_read_b64_tr_b16), so no slot carries a
-// transposed copy: two slots of 36.5 KB, two workgroups per CU.  While step t
-// computes, tile t+1's four row blocks are in flight into registers.
+// (batch, head, residue class).  LDS holds the K, V rows of tiles t-1 and t
+// (a two-slot ring), the Q, dO rows of tile t, and an exchange area for the
+// probabilities and dS of tile t's queries, all row-major.  Step t:
+//   query pass: each wave's 16 queries of tile t against their 5 key
+//     sub-tiles (in tiles t-1, t): S^T = K Q^T, dP^T = V dO^T, lse and delta
+//     in registers (two-pass softmax, every score resident), P^T and
+//     dS^T = P^T (dP^T - delta) in registers; dQ^T += K^T dS^T and dQ
+//     stored.  P and dS (16-bit, the MFMA operands) go to the exchange area
+//     as [query][key window] rows: one 8-byte write per lane and sub-tile.
+//   key pass: wave w owns keys 16w..16w+15 of tile t-1 and of tile t.  Tile
+//     t's query sub-tiles that see them (w+1 and 4-w of them) add
+//     dV^T += dO^T P and dK^T += Q^T dS: P, dS columns from the exchange area
+//     and dO^T, Q^T all through gfx950's LDS transpose read
+//     (ds_read_b64_tr_b16), which turns row-major [query][key] into the MFMA
+//     operand layout.  Tile t-1's keys are then complete (their queries lie
+//     in tiles t-1 and t) and stored; tile t's partial sums carry to step t+1.
+// No slot holds a transposed copy and no statistics leave registers: 73 KB
+// of LDS, two workgroups per CU.  While step t computes, tile t+1's four row
+// blocks are in flight into registers.
 //
-// Each chunk also runs the query pass of tile t1 (statistics only: its dQ
-// belongs to the next chunk) to complete key tile t1-1, and reads tile
+// Each chunk also runs the query pass of tile t1 (without storing its dQ,
+// which belongs to the next chunk) to complete key tile t1-1, and reads tile
 // t0-1's K, V for the query pass of tile t0.  Chunks are dealt to XCDs in
 // contiguous runs, so those re-reads of a neighbour's rows meet in one L2.
 // Every other Q, K, V, dO row crosses HBM once; dQ, dK, dV are written once,
-// with one writer per row.  No statistics reach HBM.
+// with one writer per row.
 //
 // Rows before row 0 (tile -1) read as zero and their keys are masked; rows
 // at or past the class end read as zero (their dO is zero, so they add
@@ -38,40 +42,80 @@
 
 namespace ma_dev {
 
-struct FusedSlot {
-  static constexpr int kRow = 144;          // bytes per row (128 + 16 pad)
-  static constexpr int kMat = 64 * kRow;    // one 64-row matrix
-  static constexpr int kK = 0, kV = kMat, kQ = 2 * kMat, kG = 3 * kMat, kSt = 4 * kMat;
-  static constexpr int kBytes = 4 * kMat + 512;  // + 64 lse2, 64 delta
+// Rows of 136 B (34 dwords), 8-byte aligned.  Measured on gfx950 with every
+// wave of a CU on one pattern: a 16-byte read of row c at column 16g (the
+// MFMA row operands) takes 8.8 cycles per wave at this stride against 16.6
+// at 144 B and 68 at 128 B; the transpose read of 4 contiguous 8-byte pieces
+// per row 7.3 (pieces 16 bytes apart: 11.5 at any stride).
+struct FusedLds {
+  static constexpr int kRow = 136;                // bytes per K/V/Q/dO row (128 + 8 pad)
+  static constexpr int kMat = 64 * kRow;          // one 64-row matrix
+  static constexpr int kRing = 2 * kMat;          // one ring slot: K rows, V rows
+  static constexpr int kQ = 2 * kRing;            // tile t's Q rows
+  static constexpr int kG = kQ + kMat;            // tile t's dO rows
+  static constexpr int kXRow = 176;               // exchange row: 80 keys (160 B) + 16 pad
+  static constexpr int kXW = 16 * kXRow;          // one wave's 16 query rows
+  static constexpr int kXP = kG + kMat;           // P, 4 waves
+  static constexpr int kXD = kXP + 4 * kXW;       // dS, 4 waves
+  static constexpr int kBytes = kXD + 4 * kXW;    // 74752
 };
 
-// A operand words of M^T for the MFMA head_dim tile dt from a row-major
-// 16-row sub-tile of M: lane (c, g) receives M[4g + e][d(dt, c)], e = 0..3,
-// with d(dt, m) = 32(dt>>1) + 8(m>>2) + 4(dt&1) + (m&3), the head_dim order
-// of the 16-bit path's O^T tiles.  The transpose read gives lane i of a
-// 16-lane group element i%4 of the 8-byte chunk addressed by lane 4e + i/4,
-// so lane l addresses row l>>2 at head_dim 32(dt>>1) + 8(l&3) + 4(dt&1):
-// `p` = sub-tile base + tr_lane(lane) + tr_dt(dt).
-__device__ __forceinline__ uint32_t tr_lane(int lane) { return (lane >> 2) * FusedSlot::kRow + 16 * (lane & 3); }
-__device__ __forceinline__ constexpr uint32_t tr_dt(int dt) { return 64 * (dt >> 1) + 8 * (dt & 1); }
-
+// Transposed operand words from row-major 16-bit rows (gfx950 LDS transpose
+// read): within each 16-lane group, lane i receives element i%4 of the
+// 8-byte chunk addressed by lane 4e + i/4, for e = 0..3.
 __device__ __forceinline__ uint2 tr_read(const uint8_t* p) {
   typedef short v4s __attribute__((ext_vector_type(4)));
   const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(p));
   return __builtin_bit_cast(uint2, r);
 }
 
-// acc += M^T X^T over two 16-row sub-tiles m0, m1 of M (rows = the
-// contraction), x0/x1 the lane's 4 values of each (rows 4g..4g+3, column c):
-// one 16x16x32 MFMA per head_dim tile, as HalfPath::pv2.
+// A operand of M^T for head_dim tile dt from a 16-row sub-tile of a
+// row-major K/V/Q/dO matrix: lane (c, g) receives M[4g + e][16dt + c],
+// e = 0..3 (head_dim in natural order, so a lane group's pieces are
+// contiguous).  Lane l addresses row l>>2 at head_dim 16dt + 4(l&3):
+// sub-tile base + tr_lane(lane) + 32dt.  The products' accumulators then
+// hold head_dim 16dt + 4g..4g+3 of column c in acc[dt] (store_nat).
+__device__ __forceinline__ uint32_t tr_lane(int lane) { return (lane >> 2) * FusedLds::kRow + 8 * (lane & 3); }
+__device__ __forceinline__ constexpr uint32_t tr_dt(int dt) { return 32 * dt; }
+
+// dQ, dK or dV row c from natural-order accumulators (lane (c, g): head_dim
+// 16dt + 4g..4g+3 in acc[dt]), times `scale`, in 16-byte stores: lane groups
+// g and g^1 trade halves with v_permlane16_swap (odd 16-lane rows of the
+// first operand with even rows of the second), after which an even g holds
+// head_dim 4g..4g+7 and 32+4g..32+4g+7, an odd g head_dim 4g+12.. and
+// 4g+44.. (8 each).
 template <typename T>
-__device__ __forceinline__ void pv2_tr(const uint8_t* m0, const uint8_t* m1, const float (&x0)[4],
-                                       const float (&x1)[4], f32x4 (&acc)[4]) {
-  uint4 b;
-  b.x = Mma<T>::pack2(x0[0], x0[1]);
-  b.y = Mma<T>::pack2(x0[2], x0[3]);
-  b.z = Mma<T>::pack2(x1[0], x1[1]);
-  b.w = Mma<T>::pack2(x1[2], x1[3]);
+__device__ __forceinline__ void store_nat(const f32x4 (&acc)[4], float scale, __amdgpu_buffer_rsrc_t r, uint32_t row,
+                                          int g) {
+  uint32_t w[4][2];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    w[dt][0] = Mma<T>::pack2(acc[dt][0] * scale, acc[dt][1] * scale);
+    w[dt][1] = Mma<T>::pack2(acc[dt][2] * scale, acc[dt][3] * scale);
+  }
+  const uint32_t off = row + 8 * (g & ~1) + 32 * (g & 1);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    uint32_t x[4];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const auto sw = __builtin_amdgcn_permlane16_swap(w[2 * h][k], w[2 * h + 1][k], false, false);
+      x[k] = sw[0];
+      x[2 + k] = sw[1];
+    }
+    bstore16(r, off + 64 * h, make_uint4(x[0], x[1], x[2], x[3]));
+  }
+}
+
+// B operand of one exchange column block: lane (c, g) receives X[4g + e][16jj
+// + c] of a wave's 16 x 80 rows (e = 0..3) when lane l addresses row l>>2 at
+// key 16jj + 4(l&3): wave block base + x_lane(lane) + 32jj.
+__device__ __forceinline__ uint32_t x_lane(int lane) { return (lane >> 2) * FusedLds::kXRow + 8 * (lane & 3); }
+
+// acc += M^T X^T over two 16-row sub-tiles of M (the contraction), b the
+// packed 16-bit values of both (4 each): one 16x16x32 MFMA per head_dim tile.
+template <typename T>
+__device__ __forceinline__ void pv2_tr(const uint8_t* m0, const uint8_t* m1, uint4 b, f32x4 (&acc)[4]) {
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
     const uint2 a0 = tr_read(m0 + tr_dt(dt));
@@ -82,36 +126,61 @@ __device__ __forceinline__ void pv2_tr(const uint8_t* m0, const uint8_t* m1, con
 
 // The same over one sub-tile (16x16x16 MFMA).
 template <typename T>
-__device__ __forceinline__ void pv_tr(const uint8_t* m0, const float (&x0)[4], f32x4 (&acc)[4]) {
-  uint2 b;
-  b.x = Mma<T>::pack2(x0[0], x0[1]);
-  b.y = Mma<T>::pack2(x0[2], x0[3]);
+__device__ __forceinline__ void pv_tr(const uint8_t* m0, uint2 b, f32x4 (&acc)[4]) {
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) acc[dt] = Mma<T>::x16(tr_read(m0 + tr_dt(dt)), b, acc[dt]);
 }
 
-// The register operand of row r of a slot matrix (lane (c, g): head_dim
-// 8g..8g+7 and 32+8g..32+8g+7), as HalfPath::load_q from global memory.
+// 16 bytes at an 8-byte aligned LDS address.
+__device__ __forceinline__ uint4 lds16(const uint8_t* p) {
+  const uint2 lo = *reinterpret_cast<const uint2*>(p);
+  const uint2 hi = *reinterpret_cast<const uint2*>(p + 8);
+  return make_uint4(lo.x, lo.y, hi.x, hi.y);
+}
+
+// The register operand of row r of a row-major matrix in LDS (lane (c, g):
+// head_dim 8g..8g+7 and 32+8g..32+8g+7), as HalfPath::load_q from memory.
 template <class P>
 __device__ __forceinline__ void lds_q(typename P::Q& x, const uint8_t* mat, int r, int g) {
-  x.r[0] = *reinterpret_cast<const uint4*>(mat + r * FusedSlot::kRow + 16 * g);
-  x.r[1] = *reinterpret_cast<const uint4*>(mat + r * FusedSlot::kRow + 16 * g + 64);
+  x.r[0] = lds16(mat + r * FusedLds::kRow + 16 * g);
+  x.r[1] = lds16(mat + r * FusedLds::kRow + 16 * g + 64);
+}
+
+// S^T of the 16 rows at kp (lane (c, g): row c, head_dim 8g.. and 32+8g..)
+// against the register operand q, as HalfPath::qk.
+template <typename T, class Q>
+__device__ __forceinline__ f32x4 lds_qk(const uint8_t* kp, const Q& q) {
+  f32x4 z = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  z = Mma<T>::x32(lds16(kp), q.r[0], z);
+  return Mma<T>::x32(lds16(kp + 64), q.r[1], z);
+}
+
+// Row block of a tile into LDS: rows tid>>3 and (tid>>3)+32, 16-byte column
+// tid&7 (as HalfPath::store_rows, in 8-byte halves).
+template <class P>
+__device__ __forceinline__ void lds_rows(const typename P::Rows& x, uint8_t* mat, int tid) {
+  uint8_t* p0 = mat + (tid >> 3) * FusedLds::kRow + 16 * (tid & 7);
+  uint8_t* p1 = p0 + 32 * FusedLds::kRow;
+  *reinterpret_cast<uint2*>(p0) = make_uint2(x.r[0].x, x.r[0].y);
+  *reinterpret_cast<uint2*>(p0 + 8) = make_uint2(x.r[0].z, x.r[0].w);
+  *reinterpret_cast<uint2*>(p1) = make_uint2(x.r[1].x, x.r[1].y);
+  *reinterpret_cast<uint2*>(p1 + 8) = make_uint2(x.r[1].z, x.r[1].w);
 }
 
 // Query pass of tile t for wave wv: queries 64t + 16wv + c against key
-// sub-tiles s = 4t + wv - 4 + j, j = 0..4 (sub-tile s in slot (s >> 2) & 1).
-// EDGE (t = 0): keys below row 0 are masked too.  Gives lse2, delta of the
-// lane's query and dQ^T (unscaled) in acc.
+// sub-tiles s = 4t + wv - 4 + j, j = 0..4 (sub-tile s in ring slot
+// (s >> 2) & 1).  EDGE (t = 0): keys below row 0 are masked too.  Leaves
+// dQ^T (unscaled) in acc and the wave's P, dS in its exchange rows (row c,
+// keys 16j..16j+15 of its window).
 template <class P, bool EDGE>
-__device__ __forceinline__ void fused_qpass(const uint8_t* ring, int t, int wv, int c, int g, int lane, float sl2,
-                                            float& lse2, float& dlt, f32x4 (&acc)[4]) {
+__device__ __forceinline__ void fused_qpass(uint8_t* lds, int t, int wv, int c, int g, int lane, float sl2,
+                                            f32x4 (&acc)[4]) {
   using T = typename P::Elt;
   constexpr int NS = 5, CL = 4;
-  const uint8_t* st = ring + (t & 1) * FusedSlot::kBytes;
   typename P::Q qb, gb;
-  lds_q<P>(qb, st + FusedSlot::kQ, 16 * wv + c, g);
-  lds_q<P>(gb, st + FusedSlot::kG, 16 * wv + c, g);
-  const uint32_t kl = c * FusedSlot::kRow + 16 * g;
+  lds_q<P>(qb, lds + FusedLds::kQ, 16 * wv + c, g);
+  lds_q<P>(gb, lds + FusedLds::kG, 16 * wv + c, g);
+  const uint32_t kl = c * FusedLds::kRow + 16 * g;
   const uint32_t trl = tr_lane(lane);
   const int dl = 4 * g - c + 63;  // key - query + 63 of element 0, minus the sub-tile offset
   f32x4 e[NS], dp[NS];
@@ -120,10 +189,10 @@ __device__ __forceinline__ void fused_qpass(const uint8_t* ring, int t, int wv, 
 #pragma unroll
   for (int j = 0; j < NS; ++j) {
     const int s = 4 * t + wv - CL + j;
-    const uint32_t sub = (uint32_t)(((s >> 2) & 1) * FusedSlot::kBytes + 16 * (s & 3) * FusedSlot::kRow);
-    kt[j] = sub + FusedSlot::kK + trl;
-    f32x4 z = P::qk(ring + sub + FusedSlot::kK + kl, qb);
-    dp[j] = P::qk(ring + sub + FusedSlot::kV + kl, gb);
+    const uint32_t sub = (uint32_t)(((s >> 2) & 1) * FusedLds::kRing + 16 * (s & 3) * FusedLds::kRow);
+    kt[j] = sub + trl;
+    f32x4 z = lds_qk<T>(lds + sub + kl, qb);
+    dp[j] = lds_qk<T>(lds + sub + FusedLds::kMat + kl, gb);
     const int rel = 16 * (j - CL);
     if (j == 0 || j == NS - 1) {  // resolved at compile time: the band's two edge sub-tiles
 #pragma unroll
@@ -147,74 +216,45 @@ __device__ __forceinline__ void fused_qpass(const uint8_t* ring, int t, int wv, 
       l_run += x;
       a_run = fmaf(x, dp[j][r], a_run);
     }
-  const float l_tot = col_sum(l_run);
-  const float inv = __builtin_amdgcn_rcpf(l_tot);
-  lse2 = m_use + __log2f(l_tot);
-  dlt = col_sum(a_run) * inv;
+  const float inv = __builtin_amdgcn_rcpf(col_sum(l_run));
+  const float dlt = col_sum(a_run) * inv;
+  uint8_t* xp = lds + FusedLds::kXP + wv * FusedLds::kXW + c * FusedLds::kXRow + 8 * g;
+  uint8_t* xd = xp + (FusedLds::kXD - FusedLds::kXP);
+  uint2 pd[NS];  // packed dS of sub-tile j (keys 4g..4g+3)
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    float pr[4], dr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      pr[r] = e[j][r] * inv;
+      dr[r] = pr[r] * (dp[j][r] - dlt);
+    }
+    const uint2 pp = make_uint2(Mma<T>::pack2(pr[0], pr[1]), Mma<T>::pack2(pr[2], pr[3]));
+    pd[j] = make_uint2(Mma<T>::pack2(dr[0], dr[1]), Mma<T>::pack2(dr[2], dr[3]));
+    *reinterpret_cast<uint2*>(xp + 32 * j) = pp;
+    *reinterpret_cast<uint2*>(xd + 32 * j) = pd[j];
+  }
 #pragma unroll
   for (int j = 0; j < NS; j += 2) {
-    float d0[4], d1[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) d0[r] = e[j][r] * inv * (dp[j][r] - dlt);
-    if (j + 1 < NS) {  // resolved at compile time
-#pragma unroll
-      for (int r = 0; r < 4; ++r) d1[r] = e[j + 1][r] * inv * (dp[j + 1][r] - dlt);
-      pv2_tr<T>(ring + kt[j], ring + kt[j + 1], d0, d1, acc);
-    } else {
-      pv_tr<T>(ring + kt[j], d0, acc);
-    }
+    if (j + 1 < NS)  // resolved at compile time
+      pv2_tr<T>(lds + kt[j], lds + kt[j + 1], make_uint4(pd[j].x, pd[j].y, pd[j + 1].x, pd[j + 1].y), acc);
+    else
+      pv_tr<T>(lds + kt[j], pd[j], acc);
   }
 }
 
-// Key pass of key tile kt for wave wv: keys 64kt + 16wv + c against query
-// sub-tiles s = 4kt + wv + j, j = 0..4 (in tiles kt and kt+1).  dV^T and
-// dK^T (unscaled) accumulate in acc_v, acc_k.
+// One (query sub-tile jq of tile t, key column block jj of wave jq's window)
+// pair of the key pass: dV^T += dO^T P, dK^T += Q^T dS over the 16 queries.
 template <class P>
-__device__ __forceinline__ void fused_kpass(const uint8_t* ring, int kt, int wv, int c, int g, int lane, float sl2,
+__device__ __forceinline__ void fused_kpair(const uint8_t* lds, int jq, int jj, uint32_t trl, uint32_t xl,
                                             f32x4 (&acc_k)[4], f32x4 (&acc_v)[4]) {
   using T = typename P::Elt;
-  constexpr int NS = 5;
-  const uint8_t* sk = ring + (kt & 1) * FusedSlot::kBytes;
-  typename P::Q kb, vb;
-  lds_q<P>(kb, sk + FusedSlot::kK, 16 * wv + c, g);
-  lds_q<P>(vb, sk + FusedSlot::kV, 16 * wv + c, g);
-  const uint32_t kl = c * FusedSlot::kRow + 16 * g;
-  const uint32_t trl = tr_lane(lane);
-  const int dl = c - 4 * g + 63;  // key - query + 63 of element 0, plus the sub-tile offset
-  float p[NS][4], d[NS][4];
-  uint32_t qt[NS];  // sub-tile j's Q rows (transpose-read base); dO rows at + (kG - kQ)
-#pragma unroll
-  for (int j = 0; j < NS; ++j) {
-    const int s = 4 * kt + wv + j;
-    const uint32_t slot = (uint32_t)(((s >> 2) & 1) * FusedSlot::kBytes);
-    const uint32_t sub = slot + 16 * (s & 3) * FusedSlot::kRow;
-    qt[j] = sub + FusedSlot::kQ + trl;
-    f32x4 z = P::qk(ring + sub + FusedSlot::kQ + kl, kb);         // S[query 16s+4g+r][key c]
-    const f32x4 dz = P::qk(ring + sub + FusedSlot::kG + kl, vb);  // dP[query][key c]
-    if (j == 0 || j == NS - 1) {  // resolved at compile time
-#pragma unroll
-      for (int r = 0; r < 4; ++r) z[r] = (uint32_t)(dl - 16 * j - r) <= 63u ? z[r] : -INFINITY;
-    }
-    const float* sts = reinterpret_cast<const float*>(ring + slot + FusedSlot::kSt);
-    const f32x4 lse = *reinterpret_cast<const f32x4*>(sts + 16 * (s & 3) + 4 * g);
-    const f32x4 del = *reinterpret_cast<const f32x4*>(sts + 64 + 16 * (s & 3) + 4 * g);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      p[j][r] = __builtin_amdgcn_exp2f(fmaf(z[r], sl2, -lse[r]));
-      d[j][r] = p[j][r] * (dz[r] - del[r]);
-    }
-  }
-  constexpr uint32_t kGQ = FusedSlot::kG - FusedSlot::kQ;
-#pragma unroll
-  for (int j = 0; j < NS; j += 2) {
-    if (j + 1 < NS) {  // resolved at compile time
-      pv2_tr<T>(ring + qt[j] + kGQ, ring + qt[j + 1] + kGQ, p[j], p[j + 1], acc_v);  // dV^T += dO^T P
-      pv2_tr<T>(ring + qt[j], ring + qt[j + 1], d[j], d[j + 1], acc_k);              // dK^T += Q^T dS
-    } else {
-      pv_tr<T>(ring + qt[j] + kGQ, p[j], acc_v);
-      pv_tr<T>(ring + qt[j], d[j], acc_k);
-    }
-  }
+  const uint32_t xo = jq * FusedLds::kXW + xl + 32 * jj;
+  const uint2 bp = tr_read(lds + FusedLds::kXP + xo);
+  const uint2 bd = tr_read(lds + FusedLds::kXD + xo);
+  const uint32_t sub = 16 * jq * FusedLds::kRow + trl;
+  pv_tr<T>(lds + FusedLds::kG + sub, bp, acc_v);
+  pv_tr<T>(lds + FusedLds::kQ + sub, bd, acc_k);
 }
 
 // Tile x's four row blocks in flight: thread tid carries rows tid>>3 and
@@ -225,27 +265,8 @@ struct FusedRows {
 };
 
 template <class P>
-__device__ __forceinline__ void fused_load(FusedRows<P>& x, __amdgpu_buffer_rsrc_t Kr, __amdgpu_buffer_rsrc_t Vr,
-                                           __amdgpu_buffer_rsrc_t Qr, __amdgpu_buffer_rsrc_t Gr, uint32_t off_kv,
-                                           uint32_t off_qg, int tid, uint32_t tb) {
-  P::load_rows(x.k, Kr, off_kv, tid, tb);
-  P::load_rows(x.v, Vr, off_kv, tid, tb);
-  P::load_rows(x.q, Qr, off_qg, tid, tb);
-  P::load_rows(x.g, Gr, off_qg, tid, tb);
-}
-
-template <class P>
-__device__ __forceinline__ void fused_store(const FusedRows<P>& x, uint8_t* slot, int tid) {
-  P::store_rows(x.k, slot + FusedSlot::kK, tid);
-  P::store_rows(x.v, slot + FusedSlot::kV, tid);
-  P::store_rows(x.q, slot + FusedSlot::kQ, tid);
-  P::store_rows(x.g, slot + FusedSlot::kG, tid);
-}
-
-template <class P>
 __global__ __launch_bounds__(256, 2) void bwd_fused_kernel(BwdArgs a) {
-  static_assert(P::kKRow == FusedSlot::kRow, "slot rows are the 16-bit path's");
-  extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 x FusedSlot
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // FusedLds
   using Elt = typename P::Elt;
   // chunks dealt to XCDs in contiguous runs (neighbouring chunks share an L2)
   int lin = xcd_row_order(blockIdx.x, gridDim.x);
@@ -279,53 +300,74 @@ __global__ __launch_bounds__(256, 2) void bwd_fused_kernel(BwdArgs a) {
   const __amdgpu_buffer_rsrc_t DVr = make_rsrc(static_cast<Elt*>(a.dv) + base, nrec);
   auto toff = [&](int x) { return (uint32_t)(64 * x) * tb; };  // x >= 0
   const uint32_t lrow = (uint32_t)(16 * wv + c) * tb;
+  const uint32_t trl = tr_lane(lane), xl = x_lane(lane);
 
-  // prologue: tile t0-1's K, V (zero before row 0) and tile t0's rows
+  // prologue: tile t0-1's K, V (zero before row 0), tile t0's K, V, Q, dO
   FusedRows<P> x;
-  fused_load<P>(x, Kr, Vr, Qr, Gr, t0 > 0 ? toff(t0 - 1) : kOob, kOob, tid, tb);
-  fused_store<P>(x, ring + ((t0 - 1) & 1) * FusedSlot::kBytes, tid);
-  fused_load<P>(x, Kr, Vr, Qr, Gr, toff(t0), toff(t0), tid, tb);
-  fused_store<P>(x, ring + (t0 & 1) * FusedSlot::kBytes, tid);
+  P::load_rows(x.k, Kr, t0 > 0 ? toff(t0 - 1) : kOob, tid, tb);
+  P::load_rows(x.v, Vr, t0 > 0 ? toff(t0 - 1) : kOob, tid, tb);
+  uint8_t* s0 = lds + ((t0 - 1) & 1) * FusedLds::kRing;
+  lds_rows<P>(x.k, s0, tid);
+  lds_rows<P>(x.v, s0 + FusedLds::kMat, tid);
+  P::load_rows(x.k, Kr, toff(t0), tid, tb);
+  P::load_rows(x.v, Vr, toff(t0), tid, tb);
+  P::load_rows(x.q, Qr, toff(t0), tid, tb);
+  P::load_rows(x.g, Gr, toff(t0), tid, tb);
+  uint8_t* s1 = lds + (t0 & 1) * FusedLds::kRing;
+  lds_rows<P>(x.k, s1, tid);
+  lds_rows<P>(x.v, s1 + FusedLds::kMat, tid);
+  lds_rows<P>(x.q, lds + FusedLds::kQ, tid);
+  lds_rows<P>(x.g, lds + FusedLds::kG, tid);
   __syncthreads();
 
   const float sl2 = a.scale_log2;
+  // dK^T, dV^T of keys 16wv..16wv+15 of the previous tile, partial
+  f32x4 acc_k[4], acc_v[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) acc_k[dt] = acc_v[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   for (int t = t0; t <= t1; ++t) {
     // tile t+1's rows in flight (past the class end they read as zero)
     const bool more = t < t1;
-    if (more) fused_load<P>(x, Kr, Vr, Qr, Gr, toff(t + 1), toff(t + 1), tid, tb);
+    if (more) {
+      P::load_rows(x.k, Kr, toff(t + 1), tid, tb);
+      P::load_rows(x.v, Vr, toff(t + 1), tid, tb);
+      P::load_rows(x.q, Qr, toff(t + 1), tid, tb);
+      P::load_rows(x.g, Gr, toff(t + 1), tid, tb);
+    }
 
-    // query pass of tile t: dQ (owned for t < t1) and the statistics
+    // query pass of tile t: dQ (this chunk's for t < t1), P and dS exchanged
     {
-      float lse2, dlt;
       f32x4 acc[4];
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       if (t == 0)
-        fused_qpass<P, true>(ring, t, wv, c, g, lane, sl2, lse2, dlt, acc);
+        fused_qpass<P, true>(lds, t, wv, c, g, lane, sl2, acc);
       else
-        fused_qpass<P, false>(ring, t, wv, c, g, lane, sl2, lse2, dlt, acc);
-      if (t < t1) P::store_o(acc, a.scale, DQr, toff(t) + lrow, g);
-      float* sts = reinterpret_cast<float*>(ring + (t & 1) * FusedSlot::kBytes + FusedSlot::kSt);
-      if (g == 0) {
-        sts[16 * wv + c] = lse2;
-        sts[64 + 16 * wv + c] = dlt;
-      }
+        fused_qpass<P, false>(lds, t, wv, c, g, lane, sl2, acc);
+      if (t < t1) store_nat<Elt>(acc, a.scale, DQr, toff(t) + lrow, g);
     }
     __syncthreads();
 
-    // key pass of tile t-1
+    // key pass: tile t's queries into keys 16wv.. of tile t-1 (then
+    // complete) and of tile t (carried)
     if (t > t0) {
-      f32x4 acc_k[4], acc_v[4];
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) acc_k[dt] = acc_v[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      fused_kpass<P>(ring, t - 1, wv, c, g, lane, sl2, acc_k, acc_v);
-      P::store_o(acc_v, 1.0f, DVr, toff(t - 1) + lrow, g);
-      P::store_o(acc_k, a.scale, DKr, toff(t - 1) + lrow, g);
+      for (int jq = 0; jq <= wv; ++jq) fused_kpair<P>(lds, jq, wv - jq, trl, xl, acc_k, acc_v);
+      store_nat<Elt>(acc_v, 1.0f, DVr, toff(t - 1) + lrow, g);
+      store_nat<Elt>(acc_k, a.scale, DKr, toff(t - 1) + lrow, g);
     }
-    // tile t+1 replaces tile t-1, which both passes have finished reading
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) acc_k[dt] = acc_v[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (more)
+      for (int jq = wv; jq < 4; ++jq) fused_kpair<P>(lds, jq, 4 + wv - jq, trl, xl, acc_k, acc_v);
+    // tile t+1 replaces tile t-1's K, V and tile t's Q, dO, which both
+    // passes have finished reading
     __syncthreads();
     if (more) {
-      fused_store<P>(x, ring + ((t + 1) & 1) * FusedSlot::kBytes, tid);
+      uint8_t* sn = lds + ((t + 1) & 1) * FusedLds::kRing;
+      lds_rows<P>(x.k, sn, tid);
+      lds_rows<P>(x.v, sn + FusedLds::kMat, tid);
+      lds_rows<P>(x.q, lds + FusedLds::kQ, tid);
+      lds_rows<P>(x.g, lds + FusedLds::kG, tid);
       __syncthreads();
     }
   }

@@ -1583,10 +1583,10 @@ int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* 
   if constexpr (P::kSPB == 1) {
     if (fixed == 1 && !g_opt.bwd_unfused) {
       // the causal 64 window in 16 bits: one fused launch (bwd_fused_kernel.h),
-      // two 36.5 KB ring slots, two workgroups per CU; chunks fitted to one
-      // round of the resident workgroups (measured on the target: 116.5 us at
-      // one round, chunk 16; 126.8-136.5 us at two to six rounds)
-      const size_t shm = 2 * (size_t)FusedSlot::kBytes;
+      // 73 KB of LDS, two workgroups per CU; chunks fitted to one round of
+      // the resident workgroups (measured on the target: one round, chunk 16,
+      // 10-15 % faster than two to six rounds)
+      const size_t shm = (size_t)FusedLds::kBytes;
       const int64_t per_stream = ma::imax64(1, 256 * 2 / streams);
       a.chunk = (int32_t)ma::imax64(1, (a.tiles + per_stream - 1) / per_stream);
       a.chunks = (int32_t)((a.tiles + a.chunk - 1) / a.chunk);
