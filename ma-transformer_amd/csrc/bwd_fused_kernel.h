@@ -21,7 +21,7 @@
 //     (ds_read_b64_tr_b16), which turns row-major [query][key] into the MFMA
 //     operand layout.  Tile t-1's keys are then complete (their queries lie
 //     in tiles t-1 and t) and stored; tile t's partial sums carry to step t+1.
-// No slot holds a transposed copy and no statistics leave registers: 73 KB
+// No slot holds a transposed copy and no statistics leave registers: 76 KB
 // of LDS, two workgroups per CU.  While step t computes, tile t+1's four row
 // blocks are in flight into registers.
 //
@@ -42,13 +42,10 @@
 
 namespace ma_dev {
 
-// Rows of 136 B (34 dwords), 8-byte aligned.  Measured on gfx950 with every
-// wave of a CU on one pattern: a 16-byte read of row c at column 16g (the
-// MFMA row operands) takes 8.8 cycles per wave at this stride against 16.6
-// at 144 B and 68 at 128 B; the transpose read of 4 contiguous 8-byte pieces
-// per row 7.3 (pieces 16 bytes apart: 11.5 at any stride).
+// Rows of 144 B, the 16-bit path's padded rows (136 B rows, read as 8-byte
+// pairs, halved the bank-conflict counter and left the time unchanged).
 struct FusedLds {
-  static constexpr int kRow = 136;                // bytes per K/V/Q/dO row (128 + 8 pad)
+  static constexpr int kRow = 144;                // bytes per K/V/Q/dO row (128 + 16 pad)
   static constexpr int kMat = 64 * kRow;          // one 64-row matrix
   static constexpr int kRing = 2 * kMat;          // one ring slot: K rows, V rows
   static constexpr int kQ = 2 * kRing;            // tile t's Q rows
@@ -57,7 +54,7 @@ struct FusedLds {
   static constexpr int kXW = 16 * kXRow;          // one wave's 16 query rows
   static constexpr int kXP = kG + kMat;           // P, 4 waves
   static constexpr int kXD = kXP + 4 * kXW;       // dS, 4 waves
-  static constexpr int kBytes = kXD + 4 * kXW;    // 74752
+  static constexpr int kBytes = kXD + 4 * kXW;    // 77824
 };
 
 // Transposed operand words from row-major 16-bit rows (gfx950 LDS transpose
@@ -72,7 +69,8 @@ __device__ __forceinline__ uint2 tr_read(const uint8_t* p) {
 // A operand of M^T for head_dim tile dt from a 16-row sub-tile of a
 // row-major K/V/Q/dO matrix: lane (c, g) receives M[4g + e][16dt + c],
 // e = 0..3 (head_dim in natural order, so a lane group's pieces are
-// contiguous).  Lane l addresses row l>>2 at head_dim 16dt + 4(l&3):
+// contiguous: about 2 % faster on the target than the permuted order
+// of the 16-bit path's O^T tiles, whose pieces lie 16 bytes apart).  Lane l addresses row l>>2 at head_dim 16dt + 4(l&3):
 // sub-tile base + tr_lane(lane) + 32dt.  The products' accumulators then
 // hold head_dim 16dt + 4g..4g+3 of column c in acc[dt] (store_nat).
 __device__ __forceinline__ uint32_t tr_lane(int lane) { return (lane >> 2) * FusedLds::kRow + 8 * (lane & 3); }
@@ -131,40 +129,12 @@ __device__ __forceinline__ void pv_tr(const uint8_t* m0, uint2 b, f32x4 (&acc)[4
   for (int dt = 0; dt < 4; ++dt) acc[dt] = Mma<T>::x16(tr_read(m0 + tr_dt(dt)), b, acc[dt]);
 }
 
-// 16 bytes at an 8-byte aligned LDS address.
-__device__ __forceinline__ uint4 lds16(const uint8_t* p) {
-  const uint2 lo = *reinterpret_cast<const uint2*>(p);
-  const uint2 hi = *reinterpret_cast<const uint2*>(p + 8);
-  return make_uint4(lo.x, lo.y, hi.x, hi.y);
-}
-
 // The register operand of row r of a row-major matrix in LDS (lane (c, g):
 // head_dim 8g..8g+7 and 32+8g..32+8g+7), as HalfPath::load_q from memory.
 template <class P>
 __device__ __forceinline__ void lds_q(typename P::Q& x, const uint8_t* mat, int r, int g) {
-  x.r[0] = lds16(mat + r * FusedLds::kRow + 16 * g);
-  x.r[1] = lds16(mat + r * FusedLds::kRow + 16 * g + 64);
-}
-
-// S^T of the 16 rows at kp (lane (c, g): row c, head_dim 8g.. and 32+8g..)
-// against the register operand q, as HalfPath::qk.
-template <typename T, class Q>
-__device__ __forceinline__ f32x4 lds_qk(const uint8_t* kp, const Q& q) {
-  f32x4 z = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  z = Mma<T>::x32(lds16(kp), q.r[0], z);
-  return Mma<T>::x32(lds16(kp + 64), q.r[1], z);
-}
-
-// Row block of a tile into LDS: rows tid>>3 and (tid>>3)+32, 16-byte column
-// tid&7 (as HalfPath::store_rows, in 8-byte halves).
-template <class P>
-__device__ __forceinline__ void lds_rows(const typename P::Rows& x, uint8_t* mat, int tid) {
-  uint8_t* p0 = mat + (tid >> 3) * FusedLds::kRow + 16 * (tid & 7);
-  uint8_t* p1 = p0 + 32 * FusedLds::kRow;
-  *reinterpret_cast<uint2*>(p0) = make_uint2(x.r[0].x, x.r[0].y);
-  *reinterpret_cast<uint2*>(p0 + 8) = make_uint2(x.r[0].z, x.r[0].w);
-  *reinterpret_cast<uint2*>(p1) = make_uint2(x.r[1].x, x.r[1].y);
-  *reinterpret_cast<uint2*>(p1 + 8) = make_uint2(x.r[1].z, x.r[1].w);
+  x.r[0] = *reinterpret_cast<const uint4*>(mat + r * FusedLds::kRow + 16 * g);
+  x.r[1] = *reinterpret_cast<const uint4*>(mat + r * FusedLds::kRow + 16 * g + 64);
 }
 
 // Query pass of tile t for wave wv: queries 64t + 16wv + c against key
@@ -191,8 +161,8 @@ __device__ __forceinline__ void fused_qpass(uint8_t* lds, int t, int wv, int c, 
     const int s = 4 * t + wv - CL + j;
     const uint32_t sub = (uint32_t)(((s >> 2) & 1) * FusedLds::kRing + 16 * (s & 3) * FusedLds::kRow);
     kt[j] = sub + trl;
-    f32x4 z = lds_qk<T>(lds + sub + kl, qb);
-    dp[j] = lds_qk<T>(lds + sub + FusedLds::kMat + kl, gb);
+    f32x4 z = P::qk(lds + sub + kl, qb);
+    dp[j] = P::qk(lds + sub + FusedLds::kMat + kl, gb);
     const int rel = 16 * (j - CL);
     if (j == 0 || j == NS - 1) {  // resolved at compile time: the band's two edge sub-tiles
 #pragma unroll
@@ -266,6 +236,7 @@ struct FusedRows {
 
 template <class P>
 __global__ __launch_bounds__(256, 2) void bwd_fused_kernel(BwdArgs a) {
+  static_assert(P::kKRow == FusedLds::kRow, "LDS rows are the 16-bit path's");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // FusedLds
   using Elt = typename P::Elt;
   // chunks dealt to XCDs in contiguous runs (neighbouring chunks share an L2)
@@ -307,17 +278,17 @@ __global__ __launch_bounds__(256, 2) void bwd_fused_kernel(BwdArgs a) {
   P::load_rows(x.k, Kr, t0 > 0 ? toff(t0 - 1) : kOob, tid, tb);
   P::load_rows(x.v, Vr, t0 > 0 ? toff(t0 - 1) : kOob, tid, tb);
   uint8_t* s0 = lds + ((t0 - 1) & 1) * FusedLds::kRing;
-  lds_rows<P>(x.k, s0, tid);
-  lds_rows<P>(x.v, s0 + FusedLds::kMat, tid);
+  P::store_rows(x.k, s0, tid);
+  P::store_rows(x.v, s0 + FusedLds::kMat, tid);
   P::load_rows(x.k, Kr, toff(t0), tid, tb);
   P::load_rows(x.v, Vr, toff(t0), tid, tb);
   P::load_rows(x.q, Qr, toff(t0), tid, tb);
   P::load_rows(x.g, Gr, toff(t0), tid, tb);
   uint8_t* s1 = lds + (t0 & 1) * FusedLds::kRing;
-  lds_rows<P>(x.k, s1, tid);
-  lds_rows<P>(x.v, s1 + FusedLds::kMat, tid);
-  lds_rows<P>(x.q, lds + FusedLds::kQ, tid);
-  lds_rows<P>(x.g, lds + FusedLds::kG, tid);
+  P::store_rows(x.k, s1, tid);
+  P::store_rows(x.v, s1 + FusedLds::kMat, tid);
+  P::store_rows(x.q, lds + FusedLds::kQ, tid);
+  P::store_rows(x.g, lds + FusedLds::kG, tid);
   __syncthreads();
 
   const float sl2 = a.scale_log2;
@@ -364,10 +335,10 @@ __global__ __launch_bounds__(256, 2) void bwd_fused_kernel(BwdArgs a) {
     __syncthreads();
     if (more) {
       uint8_t* sn = lds + ((t + 1) & 1) * FusedLds::kRing;
-      lds_rows<P>(x.k, sn, tid);
-      lds_rows<P>(x.v, sn + FusedLds::kMat, tid);
-      lds_rows<P>(x.q, lds + FusedLds::kQ, tid);
-      lds_rows<P>(x.g, lds + FusedLds::kG, tid);
+      P::store_rows(x.k, sn, tid);
+      P::store_rows(x.v, sn + FusedLds::kMat, tid);
+      P::store_rows(x.q, lds + FusedLds::kQ, tid);
+      P::store_rows(x.g, lds + FusedLds::kG, tid);
       __syncthreads();
     }
   }

@@ -1583,7 +1583,7 @@ int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* 
   if constexpr (P::kSPB == 1) {
     if (fixed == 1 && !g_opt.bwd_unfused) {
       // the causal 64 window in 16 bits: one fused launch (bwd_fused_kernel.h),
-      // 73 KB of LDS, two workgroups per CU; chunks fitted to one round of
+      // 76 KB of LDS, two workgroups per CU; chunks fitted to one round of
       // the resident workgroups (measured on the target: one round, chunk 16,
       // 10-15 % faster than two to six rounds)
       const size_t shm = (size_t)FusedLds::kBytes;
