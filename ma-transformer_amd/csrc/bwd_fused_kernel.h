@@ -1,40 +1,47 @@
-// bwd_fused_kernel.h -- one-launch backward of the causal 64-key window
-// (keys [m-63, m] on a residue class m of any dilation), bf16/fp16, head_dim
-// 64.  Same arithmetic as bwd_q_stream_kernel + bwd_kv_stream_kernel
+// bwd_fused_kernel.h -- one-launch backward of the fixed windows whose
+// query tiles meet two key blocks and key blocks two query tiles: the causal
+// 64 window (keys [m-63, m] on a residue class m of any dilation) and
+// [m-32, m+31] (on the shifted key grid, blocks from row -32), bf16/fp16,
+// head_dim 64.  Same arithmetic as bwd_q_stream_kernel + bwd_kv_stream_kernel
 // (backward_kernel.h), in one pass over the inputs, each probability and
 // its dS computed once.
 //
-// One workgroup (4 waves) streams a chunk [t0, t1) of the 64-row tiles of one
-// (batch, head, residue class).  LDS holds the K, V rows of tiles t-1 and t
-// (a two-slot ring), the Q, dO rows of tile t, and an exchange area for the
-// probabilities and dS of tile t's queries, all row-major.  Step t:
+// One workgroup (4 waves) streams a chunk [t0, t1) of the 64-row query tiles
+// of one (batch, head, residue class).  Query tile t meets key blocks kb and
+// kb+1 (kb = t-1 for the causal window, t on the shifted grid), and key
+// block kb is seen by query tiles t-1 and t.  LDS holds the K, V rows of
+// blocks kb, kb+1 (a two-slot ring), the Q, dO rows of tile t, and an
+// exchange area for the probabilities and dS of tile t's queries, all
+// row-major.  Step t:
 //   query pass: each wave's 16 queries of tile t against their 5 key
-//     sub-tiles (in tiles t-1, t): S^T = K Q^T, dP^T = V dO^T, lse and delta
-//     in registers (two-pass softmax, every score resident), P^T and
-//     dS^T = P^T (dP^T - delta) in registers; dQ^T += K^T dS^T and dQ
-//     stored.  P and dS (16-bit, the MFMA operands) go to the exchange area
-//     as [query][key window] rows: one 8-byte write per lane and sub-tile.
-//   key pass: wave w owns keys 16w..16w+15 of tile t-1 and of tile t.  Tile
-//     t's query sub-tiles that see them (w+1 and 4-w of them) add
-//     dV^T += dO^T P and dK^T += Q^T dS: P, dS columns from the exchange area
-//     and dO^T, Q^T all through gfx950's LDS transpose read
-//     (ds_read_b64_tr_b16), which turns row-major [query][key] into the MFMA
-//     operand layout.  Tile t-1's keys are then complete (their queries lie
-//     in tiles t-1 and t) and stored; tile t's partial sums carry to step t+1.
+//     sub-tiles: S^T = K Q^T, dP^T = V dO^T, lse and delta in registers
+//     (two-pass softmax, every score resident), P^T and dS^T = P^T (dP^T -
+//     delta) in registers; dQ^T += K^T dS^T and dQ stored.  P and dS (16-bit,
+//     the MFMA operands) go to the exchange area as [query][key window] rows:
+//     one 8-byte write per lane and sub-tile.
+//   key pass: wave w owns keys 16w..16w+15 of blocks kb and kb+1.  Tile t's
+//     query sub-tiles that see them (w+1 and 4-w of them) add dV^T += dO^T P
+//     and dK^T += Q^T dS: P, dS columns from the exchange area and dO^T, Q^T
+//     all through gfx950's LDS transpose read (ds_read_b64_tr_b16), which
+//     turns row-major [query][key] into the MFMA operand layout.  Block kb is
+//     then complete and stored; block kb+1's partial sums carry to step t+1.
 // No slot holds a transposed copy and no statistics leave registers: 76 KB
-// of LDS, two workgroups per CU.  While step t computes, tile t+1's four row
-// blocks are in flight into registers.
+// of LDS, two workgroups per CU.  While step t computes, step t+1's key
+// block and query tile are in flight into registers.
 //
-// Each chunk also runs the query pass of tile t1 (without storing its dQ,
-// which belongs to the next chunk) to complete key tile t1-1, and reads tile
-// t0-1's K, V for the query pass of tile t0.  Chunks are dealt to XCDs in
-// contiguous runs, so those re-reads of a neighbour's rows meet in one L2.
-// Every other Q, K, V, dO row crosses HBM once; dQ, dK, dV are written once,
-// with one writer per row.
+// A chunk owns query tiles [t0, t1) and key blocks [t0, t1) (the last chunk
+// also the blocks past its last tile).  It also runs the query passes of the
+// neighbouring tiles that reach its blocks (tile t1 for the causal window,
+// t0-1 on the shifted grid), without storing their dQ, and reads the key
+// block before its first step.  Chunks are dealt to XCDs in contiguous runs,
+// so those re-reads of a neighbour's rows meet in one L2.  Every other Q, K,
+// V, dO row crosses HBM once; dQ, dK, dV are written once, with one writer
+// per row.
 //
-// Rows before row 0 (tile -1) read as zero and their keys are masked; rows
-// at or past the class end read as zero (their dO is zero, so they add
-// nothing to dK, dV) and their stores are dropped by the buffer range check.
+// Rows outside the residue class read as zero.  Keys outside it are masked;
+// a query row past the end (zero dO) adds nothing to dK, dV, and gets
+// P = dS = 0 if no key of its window is left; stores outside the class are
+// dropped by the buffer range check.
 #pragma once
 
 #include "backward_kernel.h"
@@ -137,45 +144,68 @@ __device__ __forceinline__ void lds_q(typename P::Q& x, const uint8_t* mat, int 
   x.r[1] = *reinterpret_cast<const uint4*>(mat + r * FusedLds::kRow + 16 * g + 64);
 }
 
+// Band geometry of the fused kernel, [m - FL, m + FR] on a residue class:
+// key blocks are 64 rows from row OB (the two-launch kernels' shifted grid:
+// -16 * (ceil(FL/16) mod 4)), so query tile t meets key blocks t + KB0 and
+// t + KB0 + 1 and key block j is seen by query tiles j - KB0 - 1 and j - KB0.
+// A wave's 16 queries 16q.. meet key sub-tiles (16 keys) q - CL .. q - CL + 4.
+template <int FL, int FR>
+struct FusedBand {
+  static constexpr int CL = (FL + 15) / 16;
+  static constexpr int NSUB = (15 + FR) / 16 + CL + 1;
+  static constexpr int OB = -16 * (CL & 3);
+  static constexpr int OB16 = OB / 16;
+  static constexpr int KB0 = (-FL - OB) >= 0 ? (-FL - OB) / 64 : -((FL + OB + 63) / 64);
+  static_assert(NSUB == 5, "the exchange rows hold 5 sub-tiles per query");
+  static_assert((63 + FR - OB) / 64 - KB0 == 1, "the band meets two key blocks per query tile");
+};
+
 // Query pass of tile t for wave wv: queries 64t + 16wv + c against key
-// sub-tiles s = 4t + wv - 4 + j, j = 0..4 (sub-tile s in ring slot
-// (s >> 2) & 1).  EDGE (t = 0): keys below row 0 are masked too.  Leaves
-// dQ^T (unscaled) in acc and the wave's P, dS in its exchange rows (row c,
-// keys 16j..16j+15 of its window).
-template <class P, bool EDGE>
-__device__ __forceinline__ void fused_qpass(uint8_t* lds, int t, int wv, int c, int g, int lane, float sl2,
+// sub-tiles s = 4t + wv - CL + j, j = 0..4, sub-tile s in key block
+// (s - OB16) >> 2, ring slot of its parity.  EDGE (a tile whose window
+// reaches below row 0 or past row Nr-1): keys outside [0, Nr) are masked
+// too, and a row with no key left (a row past the end) gets P = dS = 0.
+// Leaves dQ^T (unscaled) in acc and the wave's P, dS in its exchange rows
+// (row c, keys 16j..16j+15 of its window).
+template <class P, int FL, int FR, bool EDGE>
+__device__ __forceinline__ void fused_qpass(uint8_t* lds, int t, int wv, int c, int g, int lane, float sl2, int Nr,
                                             f32x4 (&acc)[4]) {
   using T = typename P::Elt;
-  constexpr int NS = 5, CL = 4;
+  using B = FusedBand<FL, FR>;
+  constexpr int NS = B::NSUB, CL = B::CL;
   typename P::Q qb, gb;
   lds_q<P>(qb, lds + FusedLds::kQ, 16 * wv + c, g);
   lds_q<P>(gb, lds + FusedLds::kG, 16 * wv + c, g);
   const uint32_t kl = c * FusedLds::kRow + 16 * g;
   const uint32_t trl = tr_lane(lane);
-  const int dl = 4 * g - c + 63;  // key - query + 63 of element 0, minus the sub-tile offset
+  const int dl = 4 * g - c + FL;  // key - query + FL of element 0, minus the sub-tile offset
   f32x4 e[NS], dp[NS];
   uint32_t kt[NS];  // sub-tile j's K rows (transpose-read base)
   float mx = -INFINITY;
 #pragma unroll
   for (int j = 0; j < NS; ++j) {
     const int s = 4 * t + wv - CL + j;
-    const uint32_t sub = (uint32_t)(((s >> 2) & 1) * FusedLds::kRing + 16 * (s & 3) * FusedLds::kRow);
+    const int sb = s - B::OB16;  // sub-tile index on the key-block grid
+    const uint32_t sub = (uint32_t)(((sb >> 2) & 1) * FusedLds::kRing + 16 * (sb & 3) * FusedLds::kRow);
     kt[j] = sub + trl;
     f32x4 z = P::qk(lds + sub + kl, qb);
     dp[j] = P::qk(lds + sub + FusedLds::kMat + kl, gb);
+    constexpr int kSpan = FL + FR;
     const int rel = 16 * (j - CL);
-    if (j == 0 || j == NS - 1) {  // resolved at compile time: the band's two edge sub-tiles
+    if (rel - 15 < -FL || rel + 15 > FR) {  // resolved at compile time: the band's edge sub-tiles
 #pragma unroll
-      for (int r = 0; r < 4; ++r) z[r] = (uint32_t)(dl + rel + r) <= 63u ? z[r] : -INFINITY;
+      for (int r = 0; r < 4; ++r) z[r] = (uint32_t)(dl + rel + r) <= (uint32_t)kSpan ? z[r] : -INFINITY;
     }
     if constexpr (EDGE) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) z[r] = 16 * s + 4 * g + r >= 0 ? z[r] : -INFINITY;
+      for (int r = 0; r < 4; ++r) z[r] = (uint32_t)(16 * s + 4 * g + r) < (uint32_t)Nr ? z[r] : -INFINITY;
     }
     e[j] = z;
     mx = fmaxf(mx, fmaxf(fmaxf(z[0], z[1]), fmaxf(z[2], z[3])));
   }
-  const float m_use = col_max(mx) * sl2;  // finite: every query sees its own key
+  // every row inside the sequence sees its own key; a row past the end may see none
+  const float m_all = col_max(mx);
+  const float m_use = EDGE && m_all == -INFINITY ? 0.0f : m_all * sl2;
   float l_run = 0.0f, a_run = 0.0f;
 #pragma unroll
   for (int j = 0; j < NS; ++j)
@@ -186,7 +216,8 @@ __device__ __forceinline__ void fused_qpass(uint8_t* lds, int t, int wv, int c, 
       l_run += x;
       a_run = fmaf(x, dp[j][r], a_run);
     }
-  const float inv = __builtin_amdgcn_rcpf(col_sum(l_run));
+  const float l_tot = col_sum(l_run);
+  const float inv = EDGE && !(l_tot > 0.0f) ? 0.0f : __builtin_amdgcn_rcpf(l_tot);
   const float dlt = col_sum(a_run) * inv;
   uint8_t* xp = lds + FusedLds::kXP + wv * FusedLds::kXW + c * FusedLds::kXRow + 8 * g;
   uint8_t* xd = xp + (FusedLds::kXD - FusedLds::kXP);
@@ -234,9 +265,10 @@ struct FusedRows {
   typename P::Rows k, v, q, g;
 };
 
-template <class P>
+template <class P, int FL, int FR>
 __global__ __launch_bounds__(256, 2) void bwd_fused_kernel(BwdArgs a) {
   static_assert(P::kKRow == FusedLds::kRow, "LDS rows are the 16-bit path's");
+  using B = FusedBand<FL, FR>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // FusedLds
   using Elt = typename P::Elt;
   // chunks dealt to XCDs in contiguous runs (neighbouring chunks share an L2)
@@ -248,10 +280,16 @@ __global__ __launch_bounds__(256, 2) void bwd_fused_kernel(BwdArgs a) {
   const int h = lin % (int)a.H;
   const int b = lin / (int)a.H;
   const int Nr = (int)((a.N - rho + a.dil - 1) / a.dil);
-  const int nblk = (Nr + 63) >> 6;
+  const int nblk = (Nr + 63) >> 6;                        // query tiles
+  const int nkb = floordiv32(Nr - 1 - B::OB, 64) + 1;     // key blocks
   const int t0 = chunk_id * a.chunk;
   const int t1 = min(t0 + a.chunk, nblk);
   if (t0 >= t1) return;  // uniform, before any barrier
+  // this chunk's key blocks (the last chunk also takes those past its tiles),
+  // and its steps: the query tiles whose dQ it owns or that reach its keys
+  const int k0 = t0, k1 = t1 == nblk ? nkb : t1;
+  const int s0 = max(min(t0, k0 - B::KB0 - 1), 0);
+  const int s1 = max(t1 - 1, k1 - 1 - B::KB0);
   const uint32_t tb = (uint32_t)a.tok_bytes;
   const int64_t base = (((int64_t)b * a.N + rho) * a.H + h) * kHeadDim;
   const uint32_t nrec = (uint32_t)((int64_t)(Nr - 1) * tb + kHeadDim * sizeof(Elt));
@@ -269,74 +307,78 @@ __global__ __launch_bounds__(256, 2) void bwd_fused_kernel(BwdArgs a) {
   const __amdgpu_buffer_rsrc_t DQr = make_rsrc(static_cast<Elt*>(a.dq) + base, nrec);
   const __amdgpu_buffer_rsrc_t DKr = make_rsrc(static_cast<Elt*>(a.dk) + base, nrec);
   const __amdgpu_buffer_rsrc_t DVr = make_rsrc(static_cast<Elt*>(a.dv) + base, nrec);
-  auto toff = [&](int x) { return (uint32_t)(64 * x) * tb; };  // x >= 0
+  auto qoff = [&](int x) { return (uint32_t)(64 * x) * tb; };  // query tile x >= 0
+  // first row of key block j; rows below 0 wrap past the buffer range, so
+  // they read as zero and their stores are dropped
+  auto koff = [&](int j) { return (uint32_t)(64 * j + B::OB) * tb; };
+  auto slot = [&](int j) { return lds + (j & 1) * FusedLds::kRing; };
   const uint32_t lrow = (uint32_t)(16 * wv + c) * tb;
   const uint32_t trl = tr_lane(lane), xl = x_lane(lane);
 
-  // prologue: tile t0-1's K, V (zero before row 0), tile t0's K, V, Q, dO
+  // prologue: the two key blocks of step s0 and its query tile
   FusedRows<P> x;
-  P::load_rows(x.k, Kr, t0 > 0 ? toff(t0 - 1) : kOob, tid, tb);
-  P::load_rows(x.v, Vr, t0 > 0 ? toff(t0 - 1) : kOob, tid, tb);
-  uint8_t* s0 = lds + ((t0 - 1) & 1) * FusedLds::kRing;
-  P::store_rows(x.k, s0, tid);
-  P::store_rows(x.v, s0 + FusedLds::kMat, tid);
-  P::load_rows(x.k, Kr, toff(t0), tid, tb);
-  P::load_rows(x.v, Vr, toff(t0), tid, tb);
-  P::load_rows(x.q, Qr, toff(t0), tid, tb);
-  P::load_rows(x.g, Gr, toff(t0), tid, tb);
-  uint8_t* s1 = lds + (t0 & 1) * FusedLds::kRing;
-  P::store_rows(x.k, s1, tid);
-  P::store_rows(x.v, s1 + FusedLds::kMat, tid);
+  const int kb_first = s0 + B::KB0;
+  P::load_rows(x.k, Kr, koff(kb_first), tid, tb);
+  P::load_rows(x.v, Vr, koff(kb_first), tid, tb);
+  P::store_rows(x.k, slot(kb_first), tid);
+  P::store_rows(x.v, slot(kb_first) + FusedLds::kMat, tid);
+  P::load_rows(x.k, Kr, koff(kb_first + 1), tid, tb);
+  P::load_rows(x.v, Vr, koff(kb_first + 1), tid, tb);
+  P::load_rows(x.q, Qr, qoff(s0), tid, tb);
+  P::load_rows(x.g, Gr, qoff(s0), tid, tb);
+  P::store_rows(x.k, slot(kb_first + 1), tid);
+  P::store_rows(x.v, slot(kb_first + 1) + FusedLds::kMat, tid);
   P::store_rows(x.q, lds + FusedLds::kQ, tid);
   P::store_rows(x.g, lds + FusedLds::kG, tid);
   __syncthreads();
 
   const float sl2 = a.scale_log2;
-  // dK^T, dV^T of keys 16wv..16wv+15 of the previous tile, partial
+  // dK^T, dV^T of keys 16wv..16wv+15 of the block carried between steps
   f32x4 acc_k[4], acc_v[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) acc_k[dt] = acc_v[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  for (int t = t0; t <= t1; ++t) {
-    // tile t+1's rows in flight (past the class end they read as zero)
-    const bool more = t < t1;
+  for (int t = s0; t <= s1; ++t) {
+    const int kb = t + B::KB0;  // key blocks kb, kb+1 in the ring
+    // step t+1's new key block and query tile in flight (past the class end
+    // they read as zero)
+    const bool more = t < s1;
     if (more) {
-      P::load_rows(x.k, Kr, toff(t + 1), tid, tb);
-      P::load_rows(x.v, Vr, toff(t + 1), tid, tb);
-      P::load_rows(x.q, Qr, toff(t + 1), tid, tb);
-      P::load_rows(x.g, Gr, toff(t + 1), tid, tb);
+      P::load_rows(x.k, Kr, koff(kb + 2), tid, tb);
+      P::load_rows(x.v, Vr, koff(kb + 2), tid, tb);
+      P::load_rows(x.q, Qr, qoff(t + 1), tid, tb);
+      P::load_rows(x.g, Gr, qoff(t + 1), tid, tb);
     }
 
-    // query pass of tile t: dQ (this chunk's for t < t1), P and dS exchanged
+    // query pass of tile t: dQ (stored when this chunk owns it), P and dS exchanged
     {
       f32x4 acc[4];
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      if (t == 0)
-        fused_qpass<P, true>(lds, t, wv, c, g, lane, sl2, acc);
+      if (64 * t - FL < 0 || 64 * t + 63 + FR >= Nr)
+        fused_qpass<P, FL, FR, true>(lds, t, wv, c, g, lane, sl2, Nr, acc);
       else
-        fused_qpass<P, false>(lds, t, wv, c, g, lane, sl2, acc);
-      if (t < t1) store_nat<Elt>(acc, a.scale, DQr, toff(t) + lrow, g);
+        fused_qpass<P, FL, FR, false>(lds, t, wv, c, g, lane, sl2, Nr, acc);
+      if (t >= t0 && t < t1) store_nat<Elt>(acc, a.scale, DQr, qoff(t) + lrow, g);
     }
     __syncthreads();
 
-    // key pass: tile t's queries into keys 16wv.. of tile t-1 (then
-    // complete) and of tile t (carried)
-    if (t > t0) {
+    // key pass: tile t's queries into keys 16wv.. of block kb (then complete)
+    // and of block kb+1 (carried)
+    if (kb >= k0 && kb < k1) {
       for (int jq = 0; jq <= wv; ++jq) fused_kpair<P>(lds, jq, wv - jq, trl, xl, acc_k, acc_v);
-      store_nat<Elt>(acc_v, 1.0f, DVr, toff(t - 1) + lrow, g);
-      store_nat<Elt>(acc_k, a.scale, DKr, toff(t - 1) + lrow, g);
+      store_nat<Elt>(acc_v, 1.0f, DVr, koff(kb) + lrow, g);
+      store_nat<Elt>(acc_k, a.scale, DKr, koff(kb) + lrow, g);
     }
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) acc_k[dt] = acc_v[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    if (more)
+    if (kb + 1 >= k0 && kb + 1 < k1)
       for (int jq = wv; jq < 4; ++jq) fused_kpair<P>(lds, jq, 4 + wv - jq, trl, xl, acc_k, acc_v);
-    // tile t+1 replaces tile t-1's K, V and tile t's Q, dO, which both
+    // step t+1's rows replace key block kb and tile t's Q, dO, which both
     // passes have finished reading
     __syncthreads();
     if (more) {
-      uint8_t* sn = lds + ((t + 1) & 1) * FusedLds::kRing;
-      P::store_rows(x.k, sn, tid);
-      P::store_rows(x.v, sn + FusedLds::kMat, tid);
+      P::store_rows(x.k, slot(kb + 2), tid);
+      P::store_rows(x.v, slot(kb + 2) + FusedLds::kMat, tid);
       P::store_rows(x.q, lds + FusedLds::kQ, tid);
       P::store_rows(x.g, lds + FusedLds::kG, tid);
       __syncthreads();

@@ -90,7 +90,7 @@ namespace {
 //   MA_ATTN_KERNEL=band     16-bit windows on the band kernel, not the stream kernel
 //   MA_ATTN_NO_FIXED=1      forward windows on the generic stream tiles
 //   MA_ATTN_BWD_NO_FIXED=1  backward windows on the generic stream tiles
-//   MA_ATTN_BWD_UNFUSED=1   the causal-64 16-bit backward as two launches (dQ, then dK/dV)
+//   MA_ATTN_BWD_UNFUSED=1   the fixed-window 16-bit backward as two launches (dQ, then dK/dV)
 struct Options {
   bool force_rows, force_band, no_fixed, bwd_no_fixed, bwd_unfused;
 };
@@ -1581,8 +1581,8 @@ int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* 
   const bool no_fixed = g_opt.bwd_no_fixed;
   const int fixed = !chunked || no_fixed ? 0 : L == 63 && R == 0 ? 1 : L == 32 && R == 31 ? 2 : 0;
   if constexpr (P::kSPB == 1) {
-    if (fixed == 1 && !g_opt.bwd_unfused) {
-      // the causal 64 window in 16 bits: one fused launch (bwd_fused_kernel.h),
+    if (fixed != 0 && !g_opt.bwd_unfused) {
+      // the fixed windows in 16 bits: one fused launch (bwd_fused_kernel.h),
       // 76 KB of LDS, two workgroups per CU; chunks fitted to one round of
       // the resident workgroups (measured on the target: one round, chunk 16,
       // 10-15 % faster than two to six rounds)
@@ -1590,7 +1590,7 @@ int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* 
       const int64_t per_stream = ma::imax64(1, 256 * 2 / streams);
       a.chunk = (int32_t)ma::imax64(1, (a.tiles + per_stream - 1) / per_stream);
       a.chunks = (int32_t)((a.tiles + a.chunk - 1) / a.chunk);
-      auto kf = &bwd_fused_kernel<P>;
+      auto kf = fixed == 1 ? &bwd_fused_kernel<P, 63, 0> : &bwd_fused_kernel<P, 32, 31>;
       if (reserve_lds(reinterpret_cast<const void*>(kf), shm, st)) return 1;
       launch(true, kf, dim3((unsigned)(streams * a.chunks)), dim3(256), (uint32_t)shm, st, a);
       return 0;

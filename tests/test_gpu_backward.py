@@ -185,32 +185,35 @@ def test_backward_chunked_generic(ext, oracle, kernel_env, N, H, left, right, di
     _check(got, oracle.backward(spec, *up), dtype)
 
 
-@pytest.mark.parametrize("N,H,dil", [(5000, 16, 1), (4099, 8, 4), (300, 2, 1)])
+@pytest.mark.parametrize("N,H,left,right,dil", [(5000, 16, 63, 0, 1), (4099, 8, 63, 0, 4), (300, 2, 63, 0, 1),
+                                                 (4000, 8, 32, 31, 1), (3001, 8, 32, 31, 4), (257, 2, 32, 31, 1)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_backward_unfused_causal64(ext, oracle, kernel_env, N, H, dil, dtype):
-    """The causal 64 window in 16 bits on the two-launch kernels (dQ, then
-    dK/dV; MA_ATTN_BWD_UNFUSED) instead of the fused one: whole gradients vs
-    the oracle."""
+def test_backward_unfused_fixed_windows(ext, oracle, kernel_env, N, H, left, right, dil, dtype):
+    """The fixed windows in 16 bits on the two-launch kernels (dQ, then
+    dK/dV; MA_ATTN_BWD_UNFUSED) instead of the fused one: whole gradients
+    vs the oracle."""
     kernel_env("MA_ATTN_BWD_UNFUSED", "1")
     shape = (2, N, H, 64)
     (q, k, v, g), up = _case(shape, 870 + N + dil, dtype)
-    got = ext.sliding_backward(q, k, v, g, 63, 0, dil)
-    spec = oracle.Spec(*shape, pattern="sliding", left=63, right=0, dilation=dil)
+    got = ext.sliding_backward(q, k, v, g, left, right, dil)
+    spec = oracle.Spec(*shape, pattern="sliding", left=left, right=right, dilation=dil)
     _check(got, oracle.backward(spec, *up), dtype)
 
 
-@pytest.mark.parametrize("dil", [1, 4])
-def test_backward_fused_matches_unfused_full_size(ext, kernel_env, dil):
-    """B=1 H=8 N=65536 D=64 bf16, causal 64 (the target; dilation 4 is cfg
-    5): the fused kernel's gradients against the two-launch kernels'.  Both
-    run the same fixed-window arithmetic on interior tiles; they may differ
-    only at the sequence ends (the two-launch kernels' generic edge tiles)."""
-    shape = (1, 65536, 8, 64)
-    gen = torch.Generator(device="cuda").manual_seed(41 + dil)
+@pytest.mark.parametrize("shape,left,right,dil", [((1, 65536, 8, 64), 63, 0, 1), ((1, 65536, 8, 64), 63, 0, 4),
+                                                  ((4, 8192, 8, 64), 32, 31, 1)])
+def test_backward_fused_matches_unfused_full_size(ext, kernel_env, shape, left, right, dil):
+    """bf16 at the target shape (causal 64; dilation 4 is cfg 5) and at cfg
+    2's ([i-32, i+31], B=4 H=8 N=8192): the fused kernel's gradients against
+    the two-launch kernels'.  Both run the same fixed-window score arithmetic
+    on interior tiles; P and dS enter dK, dV through the fused kernel's
+    exchange (P as e/l instead of exp2(s - lse)), so elements differ by
+    roundings."""
+    gen = torch.Generator(device="cuda").manual_seed(41 + dil + left)
     q, k, v, g = (torch.randn(shape, device="cuda", generator=gen).bfloat16() for _ in range(4))
-    fused = ext.sliding_backward(q, k, v, g, 63, 0, dil)
+    fused = ext.sliding_backward(q, k, v, g, left, right, dil)
     kernel_env("MA_ATTN_BWD_UNFUSED", "1")
-    split = ext.sliding_backward(q, k, v, g, 63, 0, dil)
+    split = ext.sliding_backward(q, k, v, g, left, right, dil)
     for name, a, b in zip("qkv", fused, split):
         a, b = a.float(), b.float()
         diff = (a - b).abs()
