@@ -476,6 +476,7 @@ def main() -> int:
               for _ in range(4 if bwd else 3)]
         sets.append((ts[0], ts[1], ts[2], ts[3] if bwd else None))  # (Q, K, V, dO)
 
+    iset = None  # the IndexSet of the index-set launches
     if bwd and pk["pattern"] == "sliding":
         launch = lambda s: ext.sliding_backward(s[0], s[1], s[2], s[3], pk["left"], pk["right"],
                                                 pk.get("dilation", 1))
@@ -577,9 +578,17 @@ def main() -> int:
 
     queries = B * H * N
     alg_bytes = tensors * B * N * H * D * elt
+    set_source = None
     if pk["pattern"] == "index_set" or (bwd and pk["pattern"] not in ("sliding", "dense")):
-        # plus the key lists read once (the backward: the set and its transpose)
-        alg_bytes += (2 if bwd else 1) * (8 * (N + 1) + 4 * key_count(N, pk))
+        # plus the set's description, read once per pass: the tile plan the
+        # kernels read when the set has one (built once on the host), else the
+        # key lists (the backward: the set and its transpose)
+        if iset.tile_plan is not None:
+            alg_bytes += (2 if bwd else 1) * int(iset.tile_header.total_bytes)
+            set_source = "tile plan (ma_attn_tile_plan), %d B" % int(iset.tile_header.total_bytes)
+        else:
+            alg_bytes += (2 if bwd else 1) * (8 * (N + 1) + 4 * key_count(N, pk))
+            set_source = "key lists (CSR)"
     # forward: Q.K^T and P.V; backward: S, dP = dO.V^T, dV, dQ, dK (2 FLOP per MAC)
     flops = (10 if bwd else 4) * D * key_count(N, pk) * B * H
     achieved_gbps = alg_bytes / (mean_launch_ms * 1e-3) / 1e9
@@ -622,6 +631,7 @@ def main() -> int:
         "kernel_us_median": per_launch_ms[len(per_launch_ms) // 2] * 1e3,
         "step_us_mean": ms_per_step * 1e3,
         "algorithmic_bytes_per_launch": alg_bytes,
+        "key_set_bytes_counted": set_source,
         "flops_per_launch": flops,
         "tflops": flops / (mean_launch_ms * 1e-3) / 1e12,
         "mfma_bf16_frac_of_peak": (flops / (mean_launch_ms * 1e-3) / 1e12) / MFMA_BF16_PEAK_TFLOPS,
