@@ -64,15 +64,6 @@ struct FusedLds {
   static constexpr int kBytes = kXD + 4 * kXW;    // 77824
 };
 
-// Transposed operand words from row-major 16-bit rows (gfx950 LDS transpose
-// read): within each 16-lane group, lane i receives element i%4 of the
-// 8-byte chunk addressed by lane 4e + i/4, for e = 0..3.
-__device__ __forceinline__ uint2 tr_read(const uint8_t* p) {
-  typedef short v4s __attribute__((ext_vector_type(4)));
-  const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(p));
-  return __builtin_bit_cast(uint2, r);
-}
-
 // A operand of M^T for head_dim tile dt from a 16-row sub-tile of a
 // row-major K/V/Q/dO matrix: lane (c, g) receives M[4g + e][16dt + c],
 // e = 0..3 (head_dim in natural order, so a lane group's pieces are

@@ -103,6 +103,19 @@ __device__ __forceinline__ void bstore16(__amdgpu_buffer_rsrc_t r, uint32_t off,
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, x), r, (int)off, 0, 0);
 }
 
+// ---------------------------------------------------------------- LDS transpose read
+//
+// gfx950's ds_read_b64_tr_b16 on row-major 16-bit rows: within each 16-lane
+// group, lane i receives element i%4 of the 8-byte piece addressed by lane
+// 4e + i/4, for e = 0..3 (checked on the device).  With lane l addressing
+// row l>>2, a lane group reads 4 rows and each lane ends with one column of
+// them: the MFMA operand layout of the transposed matrix.
+__device__ __forceinline__ uint2 tr_read(const uint8_t* p) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(p));
+  return __builtin_bit_cast(uint2, r);
+}
+
 // ---------------------------------------------------------------- reductions
 //
 // Over the 4 lanes {l, l^16, l^32, l^48} (the lane groups that share one MFMA

@@ -54,44 +54,30 @@ constexpr int kPartial = kHeadDim + 2;
 
 // ---------------------------------------------------------------- 16-bit path
 //
-// Q.K^T on 16x16x32 MFMA (K rows row-major in LDS), P.V with V transposed in
-// LDS (V^T rows = head_dim): interior tiles pair sub-tiles on 16x16x32 MFMA
-// (pv2), edge tiles take one sub-tile per 16x16x16 MFMA (pv; pairing there
-// spilled registers at the 128-register budget and was measured slower).  O^T tile dt row m is head_dim
-// d(dt, m) = 32*(dt>>1) + 8*(m>>2) + 4*(dt&1) + (m&3), so lane (query c,
-// group g) ends with O[c][8g..8g+7] in acc[0..1] and O[c][32+8g..32+8g+7] in
-// acc[2..3]: two 16 B stores per lane.  The permutation is applied where V^T
-// rows are written: head_dim d(dt, m) lives in LDS row 16*dt + m, so the
-// P.V operand reads are plain consecutive rows (bank-conflict free with the
-// 144 B row stride).
-__device__ __forceinline__ constexpr int vt_row_of_tile(int dt) { return 16 * dt; }
-// LDS row of head_dim d: the inverse of d(dt, m) above.
-__device__ __forceinline__ int vt_row_of_dim(int d) {
-  return 16 * (2 * (d >> 5) + ((d >> 2) & 1)) + 4 * ((d >> 3) & 3) + (d & 3);
-}
-
+// Q.K^T on 16x16x32 MFMA (K rows row-major in LDS).  P.V on MFMA with the
+// V^T operand read from row-major V rows through the LDS transpose read
+// (tr_read): interior tiles pair sub-tiles on 16x16x32 MFMA (pv2), edge tiles
+// take one sub-tile per 16x16x16 MFMA (pv; pairing there spilled registers at
+// the 128-register budget and was measured slower).  O^T tile dt row m is
+// head_dim d(dt, m) = 32*(dt>>1) + 8*(m>>2) + 4*(dt&1) + (m&3), so lane
+// (query c, group g) ends with O[c][8g..8g+7] in acc[0..1] and
+// O[c][32+8g..32+8g+7] in acc[2..3]: two 16 B stores per lane.  For that
+// order lane l of a transpose read addresses V row l>>2 at head_dim
+// 32*(dt>>1) + 8*(l&3) + 4*(dt&1): v_lane + v_tr(dt).
 template <typename T>
 struct HalfPath {
   using Elt = T;
-  static constexpr int kRows = 64;                         // keys per ring slot
-  static constexpr int kKRow = 144;                        // bytes per K row in LDS (128 + 16 pad)
-  static constexpr int kVRow = 144;                        // bytes per V^T row (64 keys * 2 + 16 pad)
-  static constexpr int kSlotK = kRows * kKRow;             // 9216
-  static constexpr int kSlot = kSlotK + kHeadDim * kVRow;  // 18432
-  static constexpr int kMinBlocks = 4;                     // launch bound (workgroups per CU)
+  static constexpr int kRows = 64;                 // keys per ring slot
+  static constexpr int kKRow = 144;                // bytes per K or V row in LDS (128 + 16 pad)
+  static constexpr int kSlotK = kRows * kKRow;     // 9216
+  static constexpr int kSlot = 2 * kSlotK;         // 18432: K rows, then V rows
+  static constexpr int kMinBlocks = 4;             // launch bound (workgroups per CU)
   struct Q {
     uint4 r[2];  // query c, head_dim 8g..8g+7 and 32+8g..32+8g+7
   };
   struct Slot {
-    uint4 r[4];  // K rows tid>>3 and (tid>>3)+32 at column tid&7; V rows 2(tid&31), +1 at column v_chunk(tid)
+    uint4 r[4];  // K then V rows tid>>3 and (tid>>3)+32 at 16-byte column tid&7
   };
-
-  // 16 B head_dim chunk of V a thread carries: a wave's two 32-lane halves take
-  // chunks c and c+2, whose V^T rows lie 8 rows (32 banks) apart.
-  static __device__ __forceinline__ int v_chunk(int tid) {
-    const int w = tid >> 6;
-    return 4 * (w >> 1) + (w & 1) + 2 * ((tid >> 5) & 1);
-  }
 
   static __device__ __forceinline__ void load_q(Q& q, __amdgpu_buffer_rsrc_t Qr, uint32_t row, int g) {
     q.r[0] = bload16(Qr, row + 16 * g);
@@ -103,12 +89,19 @@ struct HalfPath {
     const uint32_t k = row_off + (tid >> 3) * tb + (tid & 7) * 16;
     s.r[0] = bload16(Kr, k);
     s.r[1] = bload16(Kr, k + 32 * tb);
-    const uint32_t v = row_off + 2 * (tid & 31) * tb + v_chunk(tid) * 16;
-    s.r[2] = bload16(Vr, v);
-    s.r[3] = bload16(Vr, v + tb);
+    s.r[2] = bload16(Vr, k);
+    s.r[3] = bload16(Vr, k + 32 * tb);
   }
 
-  // Row part only (a slot whose transposed part is never read).
+  static __device__ __forceinline__ void store_slot(const Slot& s, uint8_t* slot, int tid) {
+    uint8_t* p = slot + (tid >> 3) * kKRow + 16 * (tid & 7);
+    *reinterpret_cast<uint4*>(p) = s.r[0];
+    *reinterpret_cast<uint4*>(p + 32 * kKRow) = s.r[1];
+    *reinterpret_cast<uint4*>(p + kSlotK) = s.r[2];
+    *reinterpret_cast<uint4*>(p + kSlotK + 32 * kKRow) = s.r[3];
+  }
+
+  // First matrix only (a slot whose second part is never read).
   struct Rows {
     uint4 r[2];  // rows tid>>3 and (tid>>3)+32 at column tid&7
   };
@@ -124,31 +117,17 @@ struct HalfPath {
     *reinterpret_cast<uint4*>(slot + ((tid >> 3) + 32) * kKRow + 16 * chk) = s.r[1];
   }
 
-  // V^T words: (key 2kp, key 2kp+1) pairs of one head_dim row, built with v_perm.
-  static __device__ __forceinline__ void store_slot(const Slot& s, uint8_t* slot, int tid) {
-    const int chk = tid & 7;
-    *reinterpret_cast<uint4*>(slot + (tid >> 3) * kKRow + 16 * chk) = s.r[0];
-    *reinterpret_cast<uint4*>(slot + ((tid >> 3) + 32) * kKRow + 16 * chk) = s.r[1];
-    const int kp = tid & 31, chv = v_chunk(tid);
-    const uint32_t w0[4] = {s.r[2].x, s.r[2].y, s.r[2].z, s.r[2].w};
-    const uint32_t w1[4] = {s.r[3].x, s.r[3].y, s.r[3].z, s.r[3].w};
-    // head_dim 8chv + j -> LDS row vt_row_of_dim(8chv) + 16*(j>>2) + (j&3)
-    uint8_t* col = slot + kSlotK + vt_row_of_dim(8 * chv) * kVRow + 4 * kp;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int r0 = 16 * (e >> 1) + 2 * (e & 1);  // rows of head_dim 8chv + 2e and 8chv + 2e + 1
-      *reinterpret_cast<uint32_t*>(col + r0 * kVRow) = __builtin_amdgcn_perm(w1[e], w0[e], 0x05040100u);
-      *reinterpret_cast<uint32_t*>(col + (r0 + 1) * kVRow) = __builtin_amdgcn_perm(w1[e], w0[e], 0x07060302u);
-    }
-  }
-
   // Lane byte offsets inside a slot, and of sub-tile u (16 keys) of a slot.
   static __device__ __forceinline__ uint32_t k_lane(int c, int g) { return c * kKRow + 16 * g; }
-  static __device__ __forceinline__ uint32_t v_lane(int c, int g) { return kSlotK + c * kVRow + 8 * g; }
+  static __device__ __forceinline__ uint32_t v_lane(int c, int g) {
+    return kSlotK + (4 * g + (c >> 2)) * kKRow + 16 * (c & 3);  // lane 16g + c: row l>>2, piece l&3
+  }
+  static constexpr uint32_t v_tr(int dt) { return 64 * (dt >> 1) + 8 * (dt & 1); }
   static constexpr uint32_t k_sub(int u) { return u * 16 * kKRow; }
-  static constexpr uint32_t v_sub(int u) { return u * 32; }
+  static constexpr uint32_t v_sub(int u) { return u * 16 * kKRow; }
   // 64-row blocks (the backward's unit) are one slot; sub-tile u (0..3) of a
-  // block: rows at blk_k(u), transposed part at blk_v(u) (from v_lane).
+  // block: rows at blk_k(u), the second matrix's transpose reads at blk_v(u)
+  // (from v_lane).
   static constexpr int kSPB = 1;
   static constexpr int kBlk = kSlot;
   static constexpr uint32_t blk_k(int u) { return k_sub(u); }
@@ -169,10 +148,7 @@ struct HalfPath {
     pb.x = Mma<T>::pack2(p[0], p[1]);
     pb.y = Mma<T>::pack2(p[2], p[3]);
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      const uint2 va = *reinterpret_cast<const uint2*>(vp + vt_row_of_tile(dt) * kVRow);
-      acc[dt] = Mma<T>::x16(va, pb, acc[dt]);
-    }
+    for (int dt = 0; dt < 4; ++dt) acc[dt] = Mma<T>::x16(tr_read(vp + v_tr(dt)), pb, acc[dt]);
   }
 
   // The same over two sub-tiles (any two, e.g. from different slots) on one
@@ -189,8 +165,8 @@ struct HalfPath {
     pb.w = Mma<T>::pack2(p1[2], p1[3]);
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
-      const uint2 a0 = *reinterpret_cast<const uint2*>(vp0 + vt_row_of_tile(dt) * kVRow);
-      const uint2 a1 = *reinterpret_cast<const uint2*>(vp1 + vt_row_of_tile(dt) * kVRow);
+      const uint2 a0 = tr_read(vp0 + v_tr(dt));
+      const uint2 a1 = tr_read(vp1 + v_tr(dt));
       acc[dt] = Mma<T>::x32(make_uint4(a0.x, a0.y, a1.x, a1.y), pb, acc[dt]);
     }
   }
