@@ -1804,7 +1804,8 @@ int launch_tiles_bwd(const ma_attn_desc* d, const void* const* ptrs, void* ws, h
   auto kf = &tile_fwd_kernel<P, true>;
   auto kq = &tile_dq_kernel<P>;
   auto kkv = &tile_dkv_kernel<P>;
-  const size_t shm_f = 2 * (size_t)P::kBlk, shm_q = 4 * (size_t)P::kBlk, shm_kv = 2 * (2 * (size_t)P::kBlk + 512);
+  const size_t shm_f = 2 * (size_t)P::kBlk, shm_q = 2 * (size_t)PairLds<P>::kBytes,
+               shm_kv = 2 * ((size_t)PairLds<P>::kBytes + 512);
   if (reserve_lds(reinterpret_cast<const void*>(kf), shm_f, st) ||
       reserve_lds(reinterpret_cast<const void*>(kq), shm_q, st) ||
       reserve_lds(reinterpret_cast<const void*>(kkv), shm_kv, st))

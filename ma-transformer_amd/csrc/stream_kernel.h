@@ -72,6 +72,7 @@ struct HalfPath {
   static constexpr int kSlotK = kRows * kKRow;     // 9216
   static constexpr int kSlot = 2 * kSlotK;         // 18432: K rows, then V rows
   static constexpr int kMinBlocks = 4;             // launch bound (workgroups per CU)
+  static constexpr bool kTrRows = true;            // transposed operands read from rows (tr_read)
   struct Q {
     uint4 r[2];  // query c, head_dim 8g..8g+7 and 32+8g..32+8g+7
   };
@@ -212,6 +213,7 @@ struct F32Path {
   static constexpr int kSlotK = kRows * kKRow;   // 8704
   static constexpr int kSlot = 2 * kSlotK;       // 17408
   static constexpr int kMinBlocks = 2;
+  static constexpr bool kTrRows = false;  // a matrix read transposed is staged twice (rows, permuted rows)
   struct Q {
     uint4 r[4];  // query c, head_dim chunk g + 4j (j = 0..3)
   };

@@ -19,11 +19,13 @@
 //   tile_combine_kernel  log-sum-exp merge of a split tile's partials.
 //   tile_dq_kernel       dQ over a query tile's entries (an unsplit tile
 //                        first computes its own statistics in a pass over
-//                        them): K staged as (K, K^T), V as rows; dS in
+//                        them): K and V rows (16-bit, K^T through the
+//                        LDS transpose read; fp32 stages K as (K, K^T)); dS in
 //                        registers, dQ^T += K^T dS^T.
 //   tile_dkv_kernel      dK, dV over a key block's entries: each entry's
-//                        query tile staged as (Q, Q^T), (dO, dO^T) and its 64
-//                        statistics; dV^T += dO^T P, dK^T += Q^T dS.
+//                        query tile staged as Q and dO rows (16-bit; fp32
+//                        (Q, Q^T), (dO, dO^T)) and its 64 statistics;
+//                        dV^T += dO^T P, dK^T += Q^T dS.
 //   tile_sum_kernel      sums a split tile's (or key block's) partial dQ /
 //                        dK, dV.
 // Each output row has one writer; no atomics.  Every global access is a
@@ -171,6 +173,66 @@ __device__ __forceinline__ TileCtx tile_ctx(const TileArgs& a, int bh) {
   x.base = ((int64_t)x.b * a.N * a.H + x.h) * kHeadDim;
   x.nrec = (uint32_t)((int64_t)(a.N - 1) * x.tb + kHeadDim * sizeof(typename P::Elt));
   return x;
+}
+
+// LDS of one streamed entry in the backward passes: two matrices (K and V
+// for dQ, Q and dO for dK/dV).  The 16-bit path keeps both as rows in one
+// slot and reads a transpose with tr_read; fp32 stages a matrix that is read
+// transposed as a (rows, permuted rows) slot pair, so the entry takes two.
+// kT1 / kT2: the transposed operand of the first / second matrix, relative
+// to buffer + blk_v(u) + v_lane.
+template <class P>
+struct PairLds {
+  static constexpr bool kTr = P::kTrRows;
+  static constexpr int kBytes = (kTr ? 1 : 2) * P::kBlk;
+  static constexpr int kRows2 = kTr ? P::kSlotK : P::kBlk;  // the second matrix's rows
+  static constexpr int kT1 = kTr ? -P::kSlotK : 0;
+  static constexpr int kT2 = kTr ? 0 : P::kBlk;
+};
+
+// An entry's two matrices in flight into registers, and their store into
+// a PairLds buffer: dQ pass (K read as rows and transposed, V as rows) ...
+template <class P>
+struct KvRegs {
+  BlkSlots<P> k;  // 16-bit: K and V rows in one slot
+  BlkRows<P> v;   // fp32: V rows
+};
+template <class P>
+__device__ __forceinline__ void kv_load(KvRegs<P>& x, __amdgpu_buffer_rsrc_t Kr, __amdgpu_buffer_rsrc_t Vr,
+                                        uint32_t off, int tid, uint32_t tb) {
+  if constexpr (P::kTrRows) {
+    load_blk<P>(x.k, Kr, Vr, off, tid, tb);
+  } else {
+    load_blk<P>(x.k, Kr, Kr, off, tid, tb);
+    load_rblk<P>(x.v, Vr, off, tid, tb);
+  }
+}
+template <class P>
+__device__ __forceinline__ void kv_store(const KvRegs<P>& x, uint8_t* buf, int tid) {
+  store_blk<P>(x.k, buf, tid);
+  if constexpr (!P::kTrRows) store_rblk<P>(x.v, buf + P::kBlk, tid);
+}
+
+// ... and dK/dV pass (Q and dO, each read as rows and transposed).
+template <class P>
+struct QgRegs {
+  BlkSlots<P> q;  // 16-bit: Q and dO rows in one slot
+  BlkSlots<P> g;  // fp32: dO
+};
+template <class P>
+__device__ __forceinline__ void qg_load(QgRegs<P>& x, __amdgpu_buffer_rsrc_t Qr, __amdgpu_buffer_rsrc_t Gr,
+                                        uint32_t off, int tid, uint32_t tb) {
+  if constexpr (P::kTrRows) {
+    load_blk<P>(x.q, Qr, Gr, off, tid, tb);
+  } else {
+    load_blk<P>(x.q, Qr, Qr, off, tid, tb);
+    load_blk<P>(x.g, Gr, Gr, off, tid, tb);
+  }
+}
+template <class P>
+__device__ __forceinline__ void qg_store(const QgRegs<P>& x, uint8_t* buf, int tid) {
+  store_blk<P>(x.q, buf, tid);
+  if constexpr (!P::kTrRows) store_blk<P>(x.g, buf + P::kBlk, tid);
 }
 
 // ---------------------------------------------------------------- forward / statistics
@@ -322,10 +384,11 @@ __device__ __forceinline__ void tile_stats(float m_run, float l_run, float a_run
 }
 
 template <class P>
-__global__ __launch_bounds__(256, 2) void tile_dq_kernel(TileArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 buffers x ((K, K^T) slot, V rows)
+__global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dq_kernel(TileArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 buffers x PairLds (K, V)
   using Elt = typename P::Elt;
-  constexpr int kBuf = 2 * P::kBlk;
+  using PL = PairLds<P>;
+  constexpr int kBuf = PL::kBytes;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -378,38 +441,33 @@ __global__ __launch_bounds__(256, 2) void tile_dq_kernel(TileArgs a) {
 
   if (nit > 0) {  // uniform
     // V is read only as rows (dP^T = V dO^T): its transposed part stays unwritten
-    BlkSlots<P> xk;
-    BlkRows<P> xv;
-    load_blk<P>(xk, Kr, Kr, blk_off(0), tid, tb);
-    load_rblk<P>(xv, Vr, blk_off(0), tid, tb);
+    KvRegs<P> xk;
+    kv_load<P>(xk, Kr, Vr, blk_off(0), tid, tb);
     uint64_t mw_next = a.mask[(int64_t)entry_of(0) * 64 + ql];
-    store_blk<P>(xk, ring, tid);
-    store_rblk<P>(xv, ring + P::kBlk, tid);
+    kv_store<P>(xk, ring, tid);
     __syncthreads();
     for (int k = 0; k < nit; ++k) {
       const bool full = (a.blk[entry_of(k)] & kTileFull) != 0;
       const uint64_t mw = mw_next;
-      load_blk<P>(xk, Kr, Kr, blk_off(k + 1), tid, tb);
-      load_rblk<P>(xv, Vr, blk_off(k + 1), tid, tb);
+      kv_load<P>(xk, Kr, Vr, blk_off(k + 1), tid, tb);
       if (k + 1 < nit) mw_next = a.mask[(int64_t)entry_of(k + 1) * 64 + ql];
       const uint8_t* sk = ring + buf_of(k) * kBuf;
       f32x4 s[4], dp[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         s[u] = P::qk(sk + P::blk_k(u) + kl, qr);
-        dp[u] = P::qk(sk + P::kBlk + P::blk_k(u) + kl, gr);
+        dp[u] = P::qk(sk + PL::kRows2 + P::blk_k(u) + kl, gr);
       }
       if (!full) apply_mask(s, mw, g);
       if (own && k < ne) {  // pass 1
         bwdq_pass1(s, dp, 0xF, sl2, m_run, l_run, a_run);
         if (k == ne - 1) tile_stats(m_run, l_run, a_run, sl2, lse2, dlt);
       } else {
-        bwdq_pass2<P>(sk, vl, s, dp, 0xF, sl2, lse2, dlt, acc);
+        bwdq_pass2<P>(sk, vl + PL::kT1, s, dp, 0xF, sl2, lse2, dlt, acc);
       }
       if (loads(k + 1)) {
         uint8_t* nx = ring + buf_of(k + 1) * kBuf;
-        store_blk<P>(xk, nx, tid);
-        store_rblk<P>(xv, nx + P::kBlk, tid);
+        kv_store<P>(xk, nx, tid);
       }
       __syncthreads();
     }
@@ -429,11 +487,12 @@ __global__ __launch_bounds__(256, 2) void tile_dq_kernel(TileArgs a) {
 // ---------------------------------------------------------------- dK, dV
 
 template <class P>
-__global__ __launch_bounds__(256, 1 + (P::kSPB == 1)) void tile_dkv_kernel(TileArgs a) {
-  // 2 buffers x ((Q, Q^T) slot, (dO, dO^T) slot, 64 lse2, 64 delta)
+__global__ __launch_bounds__(256, P::kTrRows ? 3 : 1) void tile_dkv_kernel(TileArgs a) {
+  // 2 buffers x (PairLds (Q, dO), 64 lse2, 64 delta)
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
   using Elt = typename P::Elt;
-  constexpr int kBuf = 2 * P::kBlk + 512;
+  using PL = PairLds<P>;
+  constexpr int kBuf = PL::kBytes + 512;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -461,6 +520,7 @@ __global__ __launch_bounds__(256, 1 + (P::kSPB == 1)) void tile_dkv_kernel(TileA
   P::load_q(kr, Kr, krow, g);
   P::load_q(vr, Vr, krow, g);
   const uint32_t kl = P::k_lane(c, g), vl = P::v_lane(c, g);
+  const uint32_t vq = vl + PL::kT1, vg = vl + PL::kT2;  // lane offsets of the Q^T and dO^T reads
 
   auto ent = [&](int p) { return clampi(a.kentry[p], 0, a.nent - 1); };
   auto tile_of = [&](int p) { return clampi(a.etile[ent(p)], 0, a.ntiles - 1); };
@@ -474,25 +534,22 @@ __global__ __launch_bounds__(256, 1 + (P::kSPB == 1)) void tile_dkv_kernel(TileA
   const float sl2 = a.scale_log2;
 
   if (p0 < p1) {  // uniform
-    BlkSlots<P> xq, xg;
-    load_blk<P>(xq, Qr, Qr, q_off(p0), tid, tb);
-    load_blk<P>(xg, Gr, Gr, q_off(p0), tid, tb);
+    QgRegs<P> xq;
+    qg_load<P>(xq, Qr, Gr, q_off(p0), tid, tb);
     uint2 xs = bload8(Sr, st_off(p0));
     uint64_t mw_next = a.kmask[(int64_t)ent(p0) * 64 + kl_];
-    store_blk<P>(xq, ring, tid);
-    store_blk<P>(xg, ring + P::kBlk, tid);
-    bwd_stage_stats(ring + 2 * P::kBlk, xs, tid);
+    qg_store<P>(xq, ring, tid);
+    bwd_stage_stats(ring + PL::kBytes, xs, tid);
     __syncthreads();
     for (int p = p0; p < p1; ++p) {
       const bool full = (a.blk[ent(p)] & kTileFull) != 0;
       const uint64_t mw = mw_next;
-      load_blk<P>(xq, Qr, Qr, q_off(p + 1), tid, tb);
-      load_blk<P>(xg, Gr, Gr, q_off(p + 1), tid, tb);
+      qg_load<P>(xq, Qr, Gr, q_off(p + 1), tid, tb);
       xs = bload8(Sr, st_off(p + 1));
       if (p + 1 < p1) mw_next = a.kmask[(int64_t)ent(p + 1) * 64 + kl_];
       const uint8_t* sq = ring + ((p - p0) & 1) * kBuf;
-      const uint8_t* sg = sq + P::kBlk;
-      const float* stf = reinterpret_cast<const float*>(sq + 2 * P::kBlk);
+      const uint8_t* sg = sq + PL::kRows2;
+      const float* stf = reinterpret_cast<const float*>(sq + PL::kBytes);
       f32x4 s[4], dp[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -514,14 +571,13 @@ __global__ __launch_bounds__(256, 1 + (P::kSPB == 1)) void tile_dkv_kernel(TileA
           da[r] = pa[r] * (dp[u][r] - dl0[r]);
           db[r] = pb[r] * (dp[u + 1][r] - dl1[r]);
         }
-        P::pv2(sg + P::blk_v(u) + vl, sg + P::blk_v(u + 1) + vl, pa, pb, acc_v);  // dV^T += dO^T P
-        P::pv2(sq + P::blk_v(u) + vl, sq + P::blk_v(u + 1) + vl, da, db, acc_k);  // dK^T += Q^T dS
+        P::pv2(sq + P::blk_v(u) + vg, sq + P::blk_v(u + 1) + vg, pa, pb, acc_v);  // dV^T += dO^T P
+        P::pv2(sq + P::blk_v(u) + vq, sq + P::blk_v(u + 1) + vq, da, db, acc_k);  // dK^T += Q^T dS
       }
       if (p + 1 < p1) {
         uint8_t* nx = ring + ((p + 1 - p0) & 1) * kBuf;
-        store_blk<P>(xq, nx, tid);
-        store_blk<P>(xg, nx + P::kBlk, tid);
-        bwd_stage_stats(nx + 2 * P::kBlk, xs, tid);
+        qg_store<P>(xq, nx, tid);
+        bwd_stage_stats(nx + PL::kBytes, xs, tid);
       }
       __syncthreads();
     }
