@@ -13,14 +13,16 @@
 // band's 64-row blocks of the other operand streaming through a two-buffer
 // LDS ring with the next block in flight into registers:
 //
-// bwd_q_kernel   query tile.  Each key block is staged as (K rows, K^T) and
-//   V rows -- the 16-bit stream layout with K in both parts.
+// bwd_q_kernel   query tile.  Each key block is staged as K and V rows (the
+//   16-bit path reads K^T from the K rows through the LDS transpose read;
+//   fp32 stages K as (K rows, K^T) beside the V rows).
 //   Pass 1 over the band: S^T = K Q^T and dP^T = V dO^T on 16x16x32 MFMA,
 //   online max / sum / sum(e * dp), giving lse2 and delta with no O.  Pass 2
 //   over the same blocks: dS^T from registers, dQ^T += K^T dS^T (pv2).
 //   Writes dq and the per-row {lse2, delta}.
 // bwd_kv_kernel  key tile, after bwd_q_kernel.  Each query block is staged
-//   as (Q rows, Q^T), (dO rows, dO^T) and its 64 {lse2, delta}.  S = Q K^T
+//   as Q and dO rows (fp32: (Q rows, Q^T), (dO rows, dO^T)) and its 64
+//   {lse2, delta}.  S = Q K^T
 //   and dP = dO V^T with the tile's K, V rows as the register operand (the
 //   MFMA output lands as lane (key c, group g) holding queries 4g..4g+3,
 //   which is the B operand of the next products); dV^T += dO^T P and
@@ -50,6 +52,66 @@ struct BwdArgs {
   float scale, scale_log2;
   int32_t chunk, chunks;     // stream kernels: tiles per workgroup, workgroups per residue class
 };
+
+// LDS of one streamed block in the backward passes: two matrices (K and V
+// for dQ, Q and dO for dK/dV).  The 16-bit path keeps both as rows in one
+// slot and reads a transpose with tr_read; fp32 stages a matrix that is read
+// transposed as a (rows, permuted rows) slot pair, so the entry takes two.
+// kT1 / kT2: the transposed operand of the first / second matrix, relative
+// to buffer + blk_v(u) + v_lane.
+template <class P>
+struct PairLds {
+  static constexpr bool kTr = P::kTrRows;
+  static constexpr int kBytes = (kTr ? 1 : 2) * P::kBlk;
+  static constexpr int kRows2 = kTr ? P::kSlotK : P::kBlk;  // the second matrix's rows
+  static constexpr int kT1 = kTr ? -P::kSlotK : 0;
+  static constexpr int kT2 = kTr ? 0 : P::kBlk;
+};
+
+// A block's two matrices in flight into registers, and their store into
+// a PairLds buffer: dQ pass (K read as rows and transposed, V as rows) ...
+template <class P>
+struct KvRegs {
+  BlkSlots<P> k;  // 16-bit: K and V rows in one slot
+  BlkRows<P> v;   // fp32: V rows
+};
+template <class P>
+__device__ __forceinline__ void kv_load(KvRegs<P>& x, __amdgpu_buffer_rsrc_t Kr, __amdgpu_buffer_rsrc_t Vr,
+                                        uint32_t off, int tid, uint32_t tb) {
+  if constexpr (P::kTrRows) {
+    load_blk<P>(x.k, Kr, Vr, off, tid, tb);
+  } else {
+    load_blk<P>(x.k, Kr, Kr, off, tid, tb);
+    load_rblk<P>(x.v, Vr, off, tid, tb);
+  }
+}
+template <class P>
+__device__ __forceinline__ void kv_store(const KvRegs<P>& x, uint8_t* buf, int tid) {
+  store_blk<P>(x.k, buf, tid);
+  if constexpr (!P::kTrRows) store_rblk<P>(x.v, buf + P::kBlk, tid);
+}
+
+// ... and dK/dV pass (Q and dO, each read as rows and transposed).
+template <class P>
+struct QgRegs {
+  BlkSlots<P> q;  // 16-bit: Q and dO rows in one slot
+  BlkSlots<P> g;  // fp32: dO
+};
+template <class P>
+__device__ __forceinline__ void qg_load(QgRegs<P>& x, __amdgpu_buffer_rsrc_t Qr, __amdgpu_buffer_rsrc_t Gr,
+                                        uint32_t off, int tid, uint32_t tb) {
+  if constexpr (P::kTrRows) {
+    load_blk<P>(x.q, Qr, Gr, off, tid, tb);
+  } else {
+    load_blk<P>(x.q, Qr, Qr, off, tid, tb);
+    load_blk<P>(x.g, Gr, Gr, off, tid, tb);
+  }
+}
+template <class P>
+__device__ __forceinline__ void qg_store(const QgRegs<P>& x, uint8_t* buf, int tid) {
+  store_blk<P>(x.q, buf, tid);
+  if constexpr (!P::kTrRows) store_blk<P>(x.g, buf + P::kBlk, tid);
+}
 
 // Workgroup -> (b, h, rho, tile) and the residue class's resources.
 struct BwdTile {
@@ -172,12 +234,14 @@ __device__ __forceinline__ void bwdq_pass2(const uint8_t* sk, uint32_t vl, const
   }
 }
 
-// One query block (sq: (Q, Q^T), sg: (dO, dO^T), st: 64 lse2 then 64 delta)
-// against this wave's keys k0..k0+15 (kr, vr: their K and V rows):
-// dV^T += dO^T P and dK^T += Q^T dS.
+// One query block (PairLds buffer sq: Q, dO; sg: the dO rows; st: 64 lse2
+// then 64 delta) against this wave's keys k0..k0+15 (kr, vr: their K and V
+// rows): dV^T += dO^T P and dK^T += Q^T dS (Q^T, dO^T reads at lane offsets
+// vq, vg from sq + blk_v(u)).
 template <class P>
 __device__ __forceinline__ void bwdkv_block(const uint8_t* sq, const uint8_t* sg, const float* st, uint32_t kl,
-                                            uint32_t vl, const typename P::Q& kr, const typename P::Q& vr, int qbase,
+                                            uint32_t vq, uint32_t vg, const typename P::Q& kr, const typename P::Q& vr,
+                                            int qbase,
                                             int k0, int L, int R, int dl, int g, int Nr, float sl2,
                                             f32x4 (&acc_k)[4], f32x4 (&acc_v)[4]) {
   // sub-tiles whose 16 queries have no band overlap with the wave's 16 keys
@@ -214,8 +278,8 @@ __device__ __forceinline__ void bwdkv_block(const uint8_t* sq, const uint8_t* sg
       d0[r] = p0[r] * (dp[u][r] - dl0[r]);
       d1[r] = p1[r] * (dp[u + 1][r] - dl1[r]);
     }
-    P::pv2(sg + P::blk_v(u) + vl, sg + P::blk_v(u + 1) + vl, p0, p1, acc_v);  // dV^T += dO^T P
-    P::pv2(sq + P::blk_v(u) + vl, sq + P::blk_v(u + 1) + vl, d0, d1, acc_k);  // dK^T += Q^T dS
+    P::pv2(sq + P::blk_v(u) + vg, sq + P::blk_v(u + 1) + vg, p0, p1, acc_v);  // dV^T += dO^T P
+    P::pv2(sq + P::blk_v(u) + vq, sq + P::blk_v(u + 1) + vq, d0, d1, acc_k);  // dK^T += Q^T dS
   }
 }
 
@@ -246,9 +310,10 @@ __device__ __forceinline__ BwdStats bwd_stats_rsrc(const BwdArgs& a, int b, int 
 
 template <class P>
 __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 buffers x (K slot, V slot)
+  extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 buffers x PairLds (K, V)
   using Elt = typename P::Elt;
-  constexpr int kBuf = 2 * P::kBlk;
+  using PL = PairLds<P>;
+  constexpr int kBuf = PL::kBytes;
   BwdTile w;
   if (!bwd_tile<P>(a, w)) return;  // uniform, before any barrier
   const int tid = threadIdx.x;
@@ -286,13 +351,9 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
   auto buf_of = [&](int e) { return resident ? (e < nb ? e : e - nb) : (e & 1); };
   auto off_of = [&](int e) { return e < (resident ? nb : items) ? (uint32_t)row_of(e) * tb : kOob; };
 
-  // V is read only as rows (dP^T = V dO^T): its transposed part stays unwritten
-  BlkSlots<P> xk;
-  BlkRows<P> xv;
-  load_blk<P>(xk, Kr, Kr, off_of(0), tid, tb);
-  load_rblk<P>(xv, Vr, off_of(0), tid, tb);
-  store_blk<P>(xk, ring, tid);
-  store_rblk<P>(xv, ring + P::kBlk, tid);
+  KvRegs<P> xk;  // V is read only as rows (dP^T = V dO^T)
+  kv_load<P>(xk, Kr, Vr, off_of(0), tid, tb);
+  kv_store<P>(xk, ring, tid);
   __syncthreads();
 
   const float sl2 = a.scale_log2;
@@ -303,23 +364,19 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
   for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   for (int e = 0; e < items; ++e) {
-    load_blk<P>(xk, Kr, Kr, off_of(e + 1), tid, tb);
-    load_rblk<P>(xv, Vr, off_of(e + 1), tid, tb);
+    kv_load<P>(xk, Kr, Vr, off_of(e + 1), tid, tb);
     const uint8_t* sk = ring + buf_of(e) * kBuf;
     f32x4 s[4], dp[4];
-    const int live = bwdq_scores<P>(sk, sk + P::kBlk, kl, qr, gr, row_of(e), q0, L, R, dl, g, w.Nr, s, dp);
+    const int live = bwdq_scores<P>(sk, sk + PL::kRows2, kl, qr, gr, row_of(e), q0, L, R, dl, g, w.Nr, s, dp);
     if (e < nb) {  // pass 1
       bwdq_pass1(s, dp, live, sl2, m_run, l_run, a_run);
       if (e == nb - 1) bwdq_stats(m_run, l_run, a_run, sl2, lse2, dlt);
     } else {  // pass 2
-      bwdq_pass2<P>(sk, vl, s, dp, live, sl2, lse2, dlt, acc);
+      bwdq_pass2<P>(sk, vl + PL::kT1, s, dp, live, sl2, lse2, dlt, acc);
     }
     // the next item goes into the buffer item e-1 used (every wave passed the
     // barrier that ended item e-1); resident bands load nothing after pass 1
-    if (!resident || e + 1 < nb) {
-      store_blk<P>(xk, ring + buf_of(e + 1) * kBuf, tid);
-      store_rblk<P>(xv, ring + buf_of(e + 1) * kBuf + P::kBlk, tid);
-    }
+    if (!resident || e + 1 < nb) kv_store<P>(xk, ring + buf_of(e + 1) * kBuf, tid);
     __syncthreads();
   }
   P::store_o(acc, a.scale, DQr, qrow, g);
@@ -330,10 +387,11 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
 
 template <class P>
 __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdArgs a) {
-  // 2 buffers x (Q slot, dO slot, 64 lse2, 64 delta)
+  // 2 buffers x (PairLds (Q, dO), 64 lse2, 64 delta)
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
   using Elt = typename P::Elt;
-  constexpr int kBuf = 2 * P::kBlk + 512;
+  using PL = PairLds<P>;
+  constexpr int kBuf = PL::kBytes + 512;
   BwdTile w;
   if (!bwd_tile<P>(a, w)) return;
   const int tid = threadIdx.x;
@@ -368,13 +426,11 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdArgs a) {
   // thread tid < 64 carries the statistics of query row tid of the block
   auto stat_off = [&](int e) { return e < nb && tid < 64 ? (uint32_t)(q_lo + 64 * e + tid) * S.stride : kOob; };
 
-  BlkSlots<P> xq, xg;
-  load_blk<P>(xq, Qr, Qr, off_of(0), tid, tb);
-  load_blk<P>(xg, Gr, Gr, off_of(0), tid, tb);
+  QgRegs<P> xq;
+  qg_load<P>(xq, Qr, Gr, off_of(0), tid, tb);
   uint2 xs = bload8(S.r, stat_off(0));
-  store_blk<P>(xq, ring, tid);
-  store_blk<P>(xg, ring + P::kBlk, tid);
-  bwd_stage_stats(ring + 2 * P::kBlk, xs, tid);
+  qg_store<P>(xq, ring, tid);
+  bwd_stage_stats(ring + PL::kBytes, xs, tid);
   __syncthreads();
 
   const int dl = c - 4 * g + L;  // key - query + L of element 0, minus the sub-tile base
@@ -383,16 +439,14 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdArgs a) {
   for (int dt = 0; dt < 4; ++dt) acc_k[dt] = acc_v[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   for (int e = 0; e < nb; ++e) {
-    load_blk<P>(xq, Qr, Qr, off_of(e + 1), tid, tb);
-    load_blk<P>(xg, Gr, Gr, off_of(e + 1), tid, tb);
+    qg_load<P>(xq, Qr, Gr, off_of(e + 1), tid, tb);
     xs = bload8(S.r, stat_off(e + 1));
     const uint8_t* sq = ring + (e & 1) * kBuf;
-    bwdkv_block<P>(sq, sq + P::kBlk, reinterpret_cast<const float*>(sq + 2 * P::kBlk), kl, vl, kr, vr,
-                   q_lo + 64 * e, k0, L, R, dl, g, w.Nr, a.scale_log2, acc_k, acc_v);
+    bwdkv_block<P>(sq, sq + PL::kRows2, reinterpret_cast<const float*>(sq + PL::kBytes), kl, vl + PL::kT1,
+                   vl + PL::kT2, kr, vr, q_lo + 64 * e, k0, L, R, dl, g, w.Nr, a.scale_log2, acc_k, acc_v);
     uint8_t* nx = ring + ((e + 1) & 1) * kBuf;
-    store_blk<P>(xq, nx, tid);
-    store_blk<P>(xg, nx + P::kBlk, tid);
-    bwd_stage_stats(nx + 2 * P::kBlk, xs, tid);
+    qg_store<P>(xq, nx, tid);
+    bwd_stage_stats(nx + PL::kBytes, xs, tid);
     __syncthreads();
   }
   P::store_o(acc_v, 1.0f, DVr, krow, g);
@@ -419,7 +473,8 @@ __device__ __forceinline__ void bwdq_window_tile(const uint8_t* ring, uint32_t k
                                                  const typename P::Q& gr, int t, int wv, int dl, float sl2,
                                                  float& lse2, float& dlt, f32x4 (&acc)[4]) {
   using G = WinGeom<L, R, 64>;
-  constexpr int kBuf = 2 * P::kBlk;
+  using PL = PairLds<P>;
+  constexpr int kBuf = PL::kBytes;
   constexpr int kSh = G::CL & 3;
   f32x4 e[G::NSUB], dp[G::NSUB];
   uint32_t kt[G::NSUB];  // K^T of sub-tile j (the K buffer's transposed part)
@@ -429,9 +484,9 @@ __device__ __forceinline__ void bwdq_window_tile(const uint8_t* ring, uint32_t k
     const int s = 4 * t + wv - G::CL + j + kSh;  // shifted-grid sub-tile index
     const uint32_t bb = (uint32_t)(((s >> 2) & 1) * kBuf);
     const int u = s & 3;
-    kt[j] = bb + P::blk_v(u) + vl;
+    kt[j] = bb + P::blk_v(u) + vl + PL::kT1;
     f32x4 z = P::qk(ring + bb + P::blk_k(u) + kl, qr);
-    dp[j] = P::qk(ring + bb + P::kBlk + P::blk_k(u) + kl, gr);
+    dp[j] = P::qk(ring + bb + PL::kRows2 + P::blk_k(u) + kl, gr);
     const int rel = 16 * (j - G::CL);     // key - query offsets span [rel-15, rel+15]
     if (rel - 15 < -L || rel + 15 > R) {  // resolved at compile time
 #pragma unroll
@@ -480,7 +535,8 @@ __device__ __forceinline__ void bwdkv_window_tile(const uint8_t* ring, uint32_t 
                                                   const typename P::Q& vr, int t, int wv, int g, int dl, float sl2,
                                                   f32x4 (&acc_k)[4], f32x4 (&acc_v)[4]) {
   using G = WinGeom<R, L, 64>;
-  constexpr int kBuf = 2 * P::kBlk + 512;
+  using PL = PairLds<P>;
+  constexpr int kBuf = PL::kBytes + 512;
   constexpr int kSh = G::CL & 3;
   float p[G::NSUB][4], d[G::NSUB][4];
   uint32_t qt[G::NSUB];  // Q^T of sub-tile j (dO^T at + kBlk)
@@ -489,15 +545,15 @@ __device__ __forceinline__ void bwdkv_window_tile(const uint8_t* ring, uint32_t 
     const int s = 4 * t + wv - G::CL + j + kSh;  // shifted-grid sub-tile index
     const uint32_t bb = (uint32_t)(((s >> 2) & 1) * kBuf);
     const int u = s & 3;
-    qt[j] = bb + P::blk_v(u) + vl;
+    qt[j] = bb + P::blk_v(u) + vl;  // + kT1: Q^T, + kT2: dO^T
     f32x4 z = P::qk(ring + bb + P::blk_k(u) + kl, kr);                  // S[query 4g+r][key c]
-    const f32x4 dz = P::qk(ring + bb + P::kBlk + P::blk_k(u) + kl, vr);  // dP[query][key c]
+    const f32x4 dz = P::qk(ring + bb + PL::kRows2 + P::blk_k(u) + kl, vr);  // dP[query][key c]
     const int rel = 16 * (G::CL - j);     // key - query offsets span [rel-15, rel+15]
     if (rel - 15 < -L || rel + 15 > R) {  // resolved at compile time
 #pragma unroll
       for (int r = 0; r < 4; ++r) z[r] = (uint32_t)(dl + rel - r) <= (uint32_t)(L + R) ? z[r] : -INFINITY;
     }
-    const float* st = reinterpret_cast<const float*>(ring + bb + 2 * P::kBlk);
+    const float* st = reinterpret_cast<const float*>(ring + bb + PL::kBytes);
     const f32x4 lse = *reinterpret_cast<const f32x4*>(st + 16 * u + 4 * g);
     const f32x4 del = *reinterpret_cast<const f32x4*>(st + 64 + 16 * u + 4 * g);
 #pragma unroll
@@ -509,11 +565,11 @@ __device__ __forceinline__ void bwdkv_window_tile(const uint8_t* ring, uint32_t 
 #pragma unroll
   for (int j = 0; j < G::NSUB; j += 2) {
     if (j + 1 < G::NSUB) {  // resolved at compile time
-      P::pv2(ring + qt[j] + P::kBlk, ring + qt[j + 1] + P::kBlk, p[j], p[j + 1], acc_v);  // dV^T += dO^T P
-      P::pv2(ring + qt[j], ring + qt[j + 1], d[j], d[j + 1], acc_k);                      // dK^T += Q^T dS
+      P::pv2(ring + (qt[j] + PL::kT2), ring + (qt[j + 1] + PL::kT2), p[j], p[j + 1], acc_v);  // dV^T += dO^T P
+      P::pv2(ring + (qt[j] + PL::kT1), ring + (qt[j + 1] + PL::kT1), d[j], d[j + 1], acc_k);  // dK^T += Q^T dS
     } else {
-      P::pv(ring + qt[j] + P::kBlk, p[j], acc_v);
-      P::pv(ring + qt[j], d[j], acc_k);
+      P::pv(ring + (qt[j] + PL::kT2), p[j], acc_v);
+      P::pv(ring + (qt[j] + PL::kT1), d[j], acc_k);
     }
   }
 }
@@ -560,7 +616,8 @@ template <class P, int FL, int FR>
 __global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 slots x (K slot, V slot)
   using Elt = typename P::Elt;
-  constexpr int kBuf = 2 * P::kBlk;
+  using PL = PairLds<P>;
+  constexpr int kBuf = PL::kBytes;
   BwdChunk w;
   if (!bwd_chunk<P>(a, w)) return;  // uniform, before any barrier
   const int tid = threadIdx.x;
@@ -594,13 +651,10 @@ __global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
   typename P::Q qr, gr, qn, gn;
   P::load_q(qr, Qr, (uint32_t)(64 * w.t0) * tb + lrow, g);
   P::load_q(gr, Gr, (uint32_t)(64 * w.t0) * tb + lrow, g);
-  BlkSlots<P> xk;
-  BlkRows<P> xv;  // V is read only as rows
+  KvRegs<P> xk;  // V is read only as rows
   for (int j = lo_of(w.t0); j <= hi_of(w.t0); ++j) {
-    load_blk<P>(xk, Kr, Kr, boff(j), tid, tb);
-    load_rblk<P>(xv, Vr, boff(j), tid, tb);
-    store_blk<P>(xk, ring + (j & 1) * kBuf, tid);
-    store_rblk<P>(xv, ring + (j & 1) * kBuf + P::kBlk, tid);
+    kv_load<P>(xk, Kr, Vr, boff(j), tid, tb);
+    kv_store<P>(xk, ring + (j & 1) * kBuf, tid);
   }
   __syncthreads();
 
@@ -611,8 +665,7 @@ __global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
     const bool more = t + 1 < w.t1;
     const int nblk_new = more && hi_of(t + 1) > hi_of(t) ? hi_of(t + 1) : -1;
     const uint32_t noff = nblk_new >= 0 ? boff(nblk_new) : kOob;
-    load_blk<P>(xk, Kr, Kr, noff, tid, tb);
-    load_rblk<P>(xv, Vr, noff, tid, tb);
+    kv_load<P>(xk, Kr, Vr, noff, tid, tb);
     const uint32_t nrow = more ? (uint32_t)(64 * (t + 1)) * tb + lrow : kOob;
     P::load_q(qn, Qr, nrow, g);
     P::load_q(gn, Gr, nrow, g);
@@ -638,16 +691,17 @@ __global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
       const uint8_t* sk0 = ring + (lo & 1) * kBuf;
       const uint8_t* sk1 = ring + (hi & 1) * kBuf;
       f32x4 s0[4], dp0[4], s1[4], dp1[4];
-      const int live0 = bwdq_scores<P>(sk0, sk0 + P::kBlk, kl, qr, gr, 64 * lo + ob, q0, L, R, dl, g, w.Nr, s0, dp0);
+      const int live0 = bwdq_scores<P>(sk0, sk0 + PL::kRows2, kl, qr, gr, 64 * lo + ob, q0, L, R, dl, g, w.Nr, s0,
+                                       dp0);
       bwdq_pass1(s0, dp0, live0, sl2, m_run, l_run, a_run);
       int live1 = 0;
       if (hi > lo) {
-        live1 = bwdq_scores<P>(sk1, sk1 + P::kBlk, kl, qr, gr, 64 * hi + ob, q0, L, R, dl, g, w.Nr, s1, dp1);
+        live1 = bwdq_scores<P>(sk1, sk1 + PL::kRows2, kl, qr, gr, 64 * hi + ob, q0, L, R, dl, g, w.Nr, s1, dp1);
         bwdq_pass1(s1, dp1, live1, sl2, m_run, l_run, a_run);
       }
       bwdq_stats(m_run, l_run, a_run, sl2, lse2, dlt);
-      bwdq_pass2<P>(sk0, vl, s0, dp0, live0, sl2, lse2, dlt, acc);
-      if (hi > lo) bwdq_pass2<P>(sk1, vl, s1, dp1, live1, sl2, lse2, dlt, acc);
+      bwdq_pass2<P>(sk0, vl + PL::kT1, s0, dp0, live0, sl2, lse2, dlt, acc);
+      if (hi > lo) bwdq_pass2<P>(sk1, vl + PL::kT1, s1, dp1, live1, sl2, lse2, dlt, acc);
     }
     P::store_o(acc, a.scale, DQr, (uint32_t)(64 * t) * tb + lrow, g);
     const int64_t srow = (((int64_t)w.b * a.N + w.rho + (int64_t)a.dil * (q0 + c)) * a.H + w.h);
@@ -656,8 +710,7 @@ __global__ __launch_bounds__(256, 2) void bwd_q_stream_kernel(BwdArgs a) {
     // the new block replaces block hi(t+1) - 2, which tile t may still read
     __syncthreads();
     if (nblk_new >= 0) {
-      store_blk<P>(xk, ring + (nblk_new & 1) * kBuf, tid);
-      store_rblk<P>(xv, ring + (nblk_new & 1) * kBuf + P::kBlk, tid);
+      kv_store<P>(xk, ring + (nblk_new & 1) * kBuf, tid);
     }
     __syncthreads();
     qr = qn;
@@ -669,7 +722,8 @@ template <class P, int FL, int FR>
 __global__ __launch_bounds__(256, 2) void bwd_kv_stream_kernel(BwdArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 slots x (Q slot, dO slot, stats)
   using Elt = typename P::Elt;
-  constexpr int kBuf = 2 * P::kBlk + 512;
+  using PL = PairLds<P>;
+  constexpr int kBuf = PL::kBytes + 512;
   BwdChunk w;
   if (!bwd_chunk<P>(a, w)) return;
   const int tid = threadIdx.x;
@@ -702,16 +756,14 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_stream_kernel(BwdArgs a) {
   typename P::Q kr, vr, kn, vn;
   P::load_q(kr, Kr, (uint32_t)(64 * w.t0) * tb + lrow, g);
   P::load_q(vr, Vr, (uint32_t)(64 * w.t0) * tb + lrow, g);
-  BlkSlots<P> xq, xg;
+  QgRegs<P> xq;
   uint2 xs;
   for (int j = lo_of(w.t0); j <= hi_of(w.t0); ++j) {
-    load_blk<P>(xq, Qr, Qr, boff(j), tid, tb);
-    load_blk<P>(xg, Gr, Gr, boff(j), tid, tb);
+    qg_load<P>(xq, Qr, Gr, boff(j), tid, tb);
     xs = bload8(S.r, stat_off(j));
     uint8_t* sb = ring + (j & 1) * kBuf;
-    store_blk<P>(xq, sb, tid);
-    store_blk<P>(xg, sb + P::kBlk, tid);
-    bwd_stage_stats(sb + 2 * P::kBlk, xs, tid);
+    qg_store<P>(xq, sb, tid);
+    bwd_stage_stats(sb + PL::kBytes, xs, tid);
   }
   __syncthreads();
 
@@ -720,8 +772,7 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_stream_kernel(BwdArgs a) {
     const bool more = t + 1 < w.t1;
     const int nblk_new = more && hi_of(t + 1) > hi_of(t) ? hi_of(t + 1) : -1;
     const uint32_t noff = nblk_new >= 0 ? boff(nblk_new) : kOob;
-    load_blk<P>(xq, Qr, Qr, noff, tid, tb);
-    load_blk<P>(xg, Gr, Gr, noff, tid, tb);
+    qg_load<P>(xq, Qr, Gr, noff, tid, tb);
     xs = bload8(S.r, stat_off(nblk_new));
     const uint32_t nrow = more ? (uint32_t)(64 * (t + 1)) * tb + lrow : kOob;
     P::load_q(kn, Kr, nrow, g);
@@ -743,7 +794,8 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_stream_kernel(BwdArgs a) {
     if (!done)
       for (int j = lo_of(t); j <= hi_of(t); ++j) {
         const uint8_t* sq = ring + (j & 1) * kBuf;
-        bwdkv_block<P>(sq, sq + P::kBlk, reinterpret_cast<const float*>(sq + 2 * P::kBlk), kl, vl, kr, vr, 64 * j + ob,
+        bwdkv_block<P>(sq, sq + PL::kRows2, reinterpret_cast<const float*>(sq + PL::kBytes), kl, vl + PL::kT1,
+                       vl + PL::kT2, kr, vr, 64 * j + ob,
                        k0, L, R, dl, g, w.Nr, a.scale_log2, acc_k, acc_v);
       }
     const uint32_t orow = (uint32_t)(64 * t) * tb + lrow;
@@ -753,9 +805,8 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_stream_kernel(BwdArgs a) {
     __syncthreads();
     if (nblk_new >= 0) {
       uint8_t* sb = ring + (nblk_new & 1) * kBuf;
-      store_blk<P>(xq, sb, tid);
-      store_blk<P>(xg, sb + P::kBlk, tid);
-      bwd_stage_stats(sb + 2 * P::kBlk, xs, tid);
+      qg_store<P>(xq, sb, tid);
+      bwd_stage_stats(sb + PL::kBytes, xs, tid);
     }
     __syncthreads();
     kr = kn;

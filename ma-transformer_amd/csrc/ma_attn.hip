@@ -1567,8 +1567,9 @@ int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* 
   a.scale = scale_of(d);
   a.scale_log2 = a.scale * 1.4426950408889634f;
   const int64_t streams = d->batch * d->num_heads * dil;
-  // two block buffers each: (K, K^T) + V rows for dQ; (Q, Q^T) + (dO, dO^T) + statistics for dK/dV
-  const size_t shm_q = 4 * (size_t)P::kBlk, shm_kv = 2 * (2 * (size_t)P::kBlk + 512);
+  // two block buffers each: K, V for dQ; Q, dO + statistics for dK/dV (PairLds: rows only on
+  // the 16-bit path, fp32 with the staged transposes)
+  const size_t shm_q = 2 * (size_t)PairLds<P>::kBytes, shm_kv = 2 * ((size_t)PairLds<P>::kBytes + 512);
   // Bands that meet at most two 64-row blocks in both directions stream a
   // chunk of tiles per workgroup; wider bands take one workgroup per tile.
   // The stream kernels' blocks start at row -16*(ceil(L/16) & 3) (keys) and

@@ -175,66 +175,6 @@ __device__ __forceinline__ TileCtx tile_ctx(const TileArgs& a, int bh) {
   return x;
 }
 
-// LDS of one streamed entry in the backward passes: two matrices (K and V
-// for dQ, Q and dO for dK/dV).  The 16-bit path keeps both as rows in one
-// slot and reads a transpose with tr_read; fp32 stages a matrix that is read
-// transposed as a (rows, permuted rows) slot pair, so the entry takes two.
-// kT1 / kT2: the transposed operand of the first / second matrix, relative
-// to buffer + blk_v(u) + v_lane.
-template <class P>
-struct PairLds {
-  static constexpr bool kTr = P::kTrRows;
-  static constexpr int kBytes = (kTr ? 1 : 2) * P::kBlk;
-  static constexpr int kRows2 = kTr ? P::kSlotK : P::kBlk;  // the second matrix's rows
-  static constexpr int kT1 = kTr ? -P::kSlotK : 0;
-  static constexpr int kT2 = kTr ? 0 : P::kBlk;
-};
-
-// An entry's two matrices in flight into registers, and their store into
-// a PairLds buffer: dQ pass (K read as rows and transposed, V as rows) ...
-template <class P>
-struct KvRegs {
-  BlkSlots<P> k;  // 16-bit: K and V rows in one slot
-  BlkRows<P> v;   // fp32: V rows
-};
-template <class P>
-__device__ __forceinline__ void kv_load(KvRegs<P>& x, __amdgpu_buffer_rsrc_t Kr, __amdgpu_buffer_rsrc_t Vr,
-                                        uint32_t off, int tid, uint32_t tb) {
-  if constexpr (P::kTrRows) {
-    load_blk<P>(x.k, Kr, Vr, off, tid, tb);
-  } else {
-    load_blk<P>(x.k, Kr, Kr, off, tid, tb);
-    load_rblk<P>(x.v, Vr, off, tid, tb);
-  }
-}
-template <class P>
-__device__ __forceinline__ void kv_store(const KvRegs<P>& x, uint8_t* buf, int tid) {
-  store_blk<P>(x.k, buf, tid);
-  if constexpr (!P::kTrRows) store_rblk<P>(x.v, buf + P::kBlk, tid);
-}
-
-// ... and dK/dV pass (Q and dO, each read as rows and transposed).
-template <class P>
-struct QgRegs {
-  BlkSlots<P> q;  // 16-bit: Q and dO rows in one slot
-  BlkSlots<P> g;  // fp32: dO
-};
-template <class P>
-__device__ __forceinline__ void qg_load(QgRegs<P>& x, __amdgpu_buffer_rsrc_t Qr, __amdgpu_buffer_rsrc_t Gr,
-                                        uint32_t off, int tid, uint32_t tb) {
-  if constexpr (P::kTrRows) {
-    load_blk<P>(x.q, Qr, Gr, off, tid, tb);
-  } else {
-    load_blk<P>(x.q, Qr, Qr, off, tid, tb);
-    load_blk<P>(x.g, Gr, Gr, off, tid, tb);
-  }
-}
-template <class P>
-__device__ __forceinline__ void qg_store(const QgRegs<P>& x, uint8_t* buf, int tid) {
-  store_blk<P>(x.q, buf, tid);
-  if constexpr (!P::kTrRows) store_blk<P>(x.g, buf + P::kBlk, tid);
-}
-
 // ---------------------------------------------------------------- forward / statistics
 
 template <class P, bool STATS>
