@@ -19,9 +19,9 @@ forward pass over that batch.  Prints ONE JSON line:
              names it: it is not measured in this run)
   cpu_baseline  the CPU oracle (restatement of ma_core.cpp:160-246) on this
              host, single thread, bounded sample of the same workload
-  pattern_copy  sliding windows: the stream kernel's access pattern without
-             its arithmetic (ma_attn_copy_probe), timed the same way -- the
-             copy speed that pattern reaches on the device
+  pattern_copy  sliding, Longformer and block-sparse forward: the kernel's
+             access pattern without its arithmetic (ma_attn_copy_probe), timed
+             the same way -- the copy speed that pattern reaches on the device
 
 Inputs are resident in HBM before timing; 4+ distinct input sets (>1 GB in
 total) are rotated so the 256 MB MALL cannot serve a repeated set.
@@ -546,14 +546,27 @@ def main() -> int:
     per_launch_ms = sorted(a.elapsed_time(b) for a, b in ev)
     mean_launch_ms = sum(per_launch_ms) / len(per_launch_ms)
 
-    # The stream kernel's access pattern without its arithmetic (ma_attn_copy_probe,
-    # same workgroups, tiles and halo blocks), timed the same way on the same
-    # rotated inputs: the copy speed this pattern reaches on this device.
+    # The kernel's access pattern without its arithmetic (ma_attn_copy_probe),
+    # timed the same way on the same rotated inputs: the copy speed this
+    # pattern reaches on this device.  Sliding windows: the stream kernel's
+    # workgroups, tiles and halo blocks; Longformer: the same for its window
+    # (the 16 global rows each workgroup also reads are left out); block-sparse:
+    # the block-row kernel's workgroups and listed blocks.
     probe_us = None
-    if not bwd and pk["pattern"] == "sliding":
+    probe_src = None
+    if not bwd and pk["pattern"] in ("sliding", "longformer", "block_sparse"):
         import ma_attn as _ma
-        pdesc = _ma.make_desc(B, N, H, D, _ma.DTYPES[dtype], _ma.SLIDING, left=pk["left"], right=pk["right"],
-                              dilation=pk.get("dilation", 1))
+        if pk["pattern"] == "block_sparse":
+            pdesc = _ma.make_desc(B, N, H, D, _ma.DTYPES[dtype], _ma.BLOCK_SPARSE, block_size=pk["block_size"],
+                                  block_table_ptr=table.tensor.data_ptr(), blocks_per_row=table.width)
+            probe_src = "ma_attn_copy_probe (block_row_kernel's workgroups and listed blocks, no arithmetic)"
+        else:
+            pdesc = _ma.make_desc(B, N, H, D, _ma.DTYPES[dtype], _ma.SLIDING, left=pk["left"], right=pk["right"],
+                                  dilation=pk.get("dilation", 1))
+            probe_src = ("ma_attn_copy_probe (same workgroups, tiles and halo blocks, no arithmetic)"
+                         if pk["pattern"] == "sliding" else
+                         "ma_attn_copy_probe (the stream kernel's window pattern without the global rows, "
+                         "no arithmetic)")
         pout = torch.empty_like(sets[0][0])
         raw = stream.cuda_stream
         try:
@@ -647,7 +660,7 @@ def main() -> int:
         out["pattern_copy"] = {"kernel_us_mean": probe_us,
                                "gbps": (4 * B * N * H * D * elt) / (probe_us * 1e-6) / 1e9,
                                "kernel_frac_of_pattern_copy": probe_us / (mean_launch_ms * 1e3),
-                               "source": "ma_attn_copy_probe (same workgroups, tiles and halo blocks, no arithmetic)"}
+                               "source": probe_src}
     if bwd:
         out["pass"] = "backward"
     if not args.no_cpu_baseline and not bwd:

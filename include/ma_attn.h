@@ -272,14 +272,17 @@ int ma_attn_tile_plan(int64_t seq_len, const int64_t* offsets, const int32_t* ke
                       ma_attn_tile_header* header, void* plan, size_t plan_bytes);
 
 /*
- * Measurement: the forward stream kernel's memory traffic for desc (SLIDING,
- * head_dim 64) without its arithmetic -- the same workgroups, chunks, 64-row
- * tiles of one (batch, head) and halo blocks, writing o = q xor k xor v
- * bitwise.  Gives the copy speed of the stream kernel's access pattern on the
- * device, the ceiling that kernel runs against.  Returns non-zero when the
- * stream kernel would not take desc.  The _timed form stamps the kernel's
- * start and stop on two caller-created events, as ma_attn_forward_timed.
- * No reference counterpart.
+ * Measurement: a forward kernel's memory traffic for desc without its
+ * arithmetic.  SLIDING (head_dim 64): the stream kernel's workgroups, chunks,
+ * 64-row tiles of one (batch, head) and halo blocks, writing o = q xor k xor v
+ * bitwise.  BLOCK_SPARSE (block_size 64, head_dim 64, blocks_per_row <= 4, a
+ * device table as ma_attn_forward takes): the block-row kernel's workgroups,
+ * each reading its row's Q tile and listed K/V blocks and writing
+ * o[i] = q[i] xor (xor over the row's blocks c of k[64c + i%64] xor
+ * v[64c + i%64]).  Gives the copy speed of that kernel's access pattern on the
+ * device, the ceiling it runs against.  Returns non-zero when the kernel would
+ * not take desc.  The _timed form stamps the kernel's start and stop on two
+ * caller-created events, as ma_attn_forward_timed.  No reference counterpart.
  */
 int ma_attn_copy_probe(const ma_attn_desc* desc, const void* q, const void* k, const void* v,
                        void* o, void* stream);

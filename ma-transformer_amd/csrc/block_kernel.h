@@ -252,4 +252,62 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void block_row_kernel(BlockArgs
   P::store_o(acc, l_tot > 0.0f ? __builtin_amdgcn_rcpf(l_tot) : 0.0f, Or, qrow, g);
 }
 
+// ---------------------------------------------------------------- copy probe
+//
+// block_row_kernel's memory traffic without its arithmetic: the same grid and
+// workgroup order, each workgroup reading its row's Q tile and the K and V
+// blocks its table row lists (every block's loads in flight at once, as the
+// kernel issues them for rows of up to 4 entries), and writing
+// O[i] = Q[i] xor (xor over the row's entries c of K[64c + i%64] xor
+// V[64c + i%64]) bitwise.  Gives the copy speed of that access pattern on the
+// device.  EB: bytes per head row (128 for 16-bit, 256 for fp32); table-driven
+// rows of at most 4 entries.
+template <int EB>
+__global__ __launch_bounds__(256) void block_probe_kernel(BlockArgs a) {
+  constexpr int CPR = EB / 16;        // 16-byte chunks per row
+  constexpr int NU = 64 * CPR / 256;  // uint4 per thread per 64-row tile
+  const int tid = threadIdx.x;
+  const int wg = xcd_row_order(blockIdx.x, gridDim.x);
+  const int r = wg % a.nbq;
+  const int bh = wg / a.nbq;
+  const int h = bh % a.H;
+  const int b = bh / a.H;
+  const int N = a.N;
+  const uint32_t tb = (uint32_t)a.H * EB;
+  const int64_t base = ((int64_t)b * N * a.H + h) * EB;  // bytes
+  const uint32_t nrec = (uint32_t)((int64_t)(N - 1) * tb + EB);
+  const __amdgpu_buffer_rsrc_t Qr = make_rsrc(static_cast<const uint8_t*>(a.q) + base, nrec);
+  const __amdgpu_buffer_rsrc_t Kr = make_rsrc(static_cast<const uint8_t*>(a.k) + base, nrec);
+  const __amdgpu_buffer_rsrc_t Vr = make_rsrc(static_cast<const uint8_t*>(a.v) + base, nrec);
+  const __amdgpu_buffer_rsrc_t Or = make_rsrc(static_cast<uint8_t*>(a.o) + base, nrec);
+  const int32_t* row = a.table + (int64_t)r * a.bpr;
+  auto off = [&](int j) {
+    const int e = tid + 256 * j;
+    return (uint32_t)(e / CPR) * tb + (uint32_t)(e % CPR) * 16;
+  };
+  uint4 x[NU];
+  const uint32_t qo = (uint32_t)(64 * r) * tb;
+#pragma unroll
+  for (int j = 0; j < NU; ++j) x[j] = bload16(Qr, qo + off(j));
+  uint4 kv[4][2][NU];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int cb = e < a.bpr ? row[e] : -1;
+    const uint32_t bo = cb >= 0 ? (uint32_t)(64 * cb) * tb : kOob;
+#pragma unroll
+    for (int j = 0; j < NU; ++j) {
+      kv[e][0][j] = bload16(Kr, bo + off(j));
+      kv[e][1][j] = bload16(Vr, bo + off(j));
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+#pragma unroll
+    for (int j = 0; j < NU; ++j)
+      x[j] = make_uint4(x[j].x ^ kv[e][0][j].x ^ kv[e][1][j].x, x[j].y ^ kv[e][0][j].y ^ kv[e][1][j].y,
+                        x[j].z ^ kv[e][0][j].z ^ kv[e][1][j].z, x[j].w ^ kv[e][0][j].w ^ kv[e][1][j].w);
+#pragma unroll
+  for (int j = 0; j < NU; ++j) bstore16(Or, qo + off(j), x[j]);
+}
+
 }  // namespace ma_dev

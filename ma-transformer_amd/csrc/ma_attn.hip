@@ -2215,9 +2215,36 @@ int ma_attn_copy_probe(const ma_attn_desc* desc, const void* q, const void* k, c
                        void* stream) {
   g_last_error.clear();
   if (validate(desc)) return 1;
-  if (desc->pattern != MA_ATTN_SLIDING) return fail("ma_attn_copy_probe: SLIDING descriptors only");
+  if (desc->pattern != MA_ATTN_SLIDING && desc->pattern != MA_ATTN_BLOCK_SPARSE)
+    return fail("ma_attn_copy_probe: SLIDING and BLOCK_SPARSE descriptors only");
   if (desc->batch * desc->seq_len * desc->num_heads == 0) return 0;
   if (!q || !k || !v || !o) return fail("ma_attn: null tensor pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (desc->pattern == MA_ATTN_BLOCK_SPARSE) {
+    if (!block_applies(desc, q, k, v, o) || desc->blocks_per_row > 4)
+      return fail("ma_attn_copy_probe: the block-row kernel does not take this descriptor (block_size 64, "
+                  "head_dim 64, at most 4 blocks per row, 16-byte aligned tensors)");
+    BlockArgs a;
+    memset(&a, 0, sizeof(a));
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.o = o;
+    a.table = desc->block_table;
+    a.N = (int32_t)desc->seq_len;
+    a.H = (int32_t)desc->num_heads;
+    a.bpr = (int32_t)desc->blocks_per_row;
+    a.nbq = (int32_t)((desc->seq_len + 63) / 64);
+    const unsigned grid = (unsigned)(desc->batch * desc->num_heads * a.nbq);
+    (void)hipGetLastError();
+    if (desc->dtype == MA_ATTN_F32)
+      launch(true, block_probe_kernel<256>, dim3(grid), dim3(256), 0u, st, a);
+    else
+      launch(true, block_probe_kernel<128>, dim3(grid), dim3(256), 0u, st, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail("ma_attn_copy_probe: kernel launch failed: %s", hipGetErrorString(e));
+    return 0;
+  }
   if (!stream_applies(desc, q, k, v, o))
     return fail("ma_attn_copy_probe: the stream kernel does not take this descriptor (head_dim 64, "
                 "left, right >= 0, 16-byte aligned tensors)");
@@ -2238,7 +2265,6 @@ int ma_attn_copy_probe(const ma_attn_desc* desc, const void* q, const void* k, c
   a.chunks = (int32_t)p.chunks;
   a.tok_bytes = (int32_t)p.tok_bytes;
   a.pairs = p.geom.right > 0 && p.wgs % 16 == 0 && p.chunks % 2 == 0 ? 1 : 0;  // as launch_stream
-  hipStream_t st = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
   if (desc->dtype == MA_ATTN_F32)
     launch(true, copy_probe_kernel<256>, dim3((unsigned)p.wgs), dim3(256), 0u, st, a);

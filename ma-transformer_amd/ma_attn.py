@@ -299,7 +299,8 @@ def encoder_layer_forward_raw(layer: EncoderLayer, src_ptr: int, attn_ptr: int, 
 
 def copy_probe_raw(desc: Desc, q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, stream: int = 0,
                    events=None) -> None:
-    """ma_attn_copy_probe(_timed): the stream kernel's traffic without its arithmetic."""
+    """ma_attn_copy_probe(_timed): a forward kernel's traffic without its arithmetic
+    (SLIDING: the stream kernel's; BLOCK_SPARSE: the block-row kernel's)."""
     e0, e1 = events if events else (None, None)
     if LIB.ma_attn_copy_probe_timed(ctypes.byref(desc), q_ptr, k_ptr, v_ptr, o_ptr, stream or None, e0 or None,
                                     e1 or None) != 0:

@@ -1,6 +1,8 @@
-"""ma_attn_copy_probe (the stream kernel's access pattern without its
-arithmetic, a measurement entry point): every O element is Q xor K xor V of
-its own position, for the window shapes bench.py measures it on."""
+"""ma_attn_copy_probe (a forward kernel's access pattern without its
+arithmetic, a measurement entry point).  SLIDING: every O element is Q xor K
+xor V of its own position, for the window shapes bench.py measures it on.
+BLOCK_SPARSE: O row i is Q row i xor the K and V rows at the same offset in
+every block its table row lists."""
 import pytest
 import torch
 
@@ -32,6 +34,47 @@ def test_copy_probe_covers_every_element(shape, left, right, dil, dtype):
     got = o.view(torch.int32).reshape(-1, 4)
     assert torch.equal(got[:, 2:], w[:, 2:])
     assert not torch.equal(o.view(it), torch.full_like(o, 3.0).view(it))
+
+
+@pytest.mark.parametrize("shape,dtype,width", [
+    ((2, 1000, 4, 64), torch.bfloat16, 4),
+    ((1, 4096, 8, 64), torch.float16, 4),
+    ((2, 1500, 2, 64), torch.float32, 4),
+    ((1, 777, 3, 64), torch.bfloat16, 3),
+])
+def test_block_probe_reads_every_listed_block(shape, dtype, width):
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    import ma_attn
+    import sparse_attention_cuda as sac
+    B, N, H, D = shape
+    nb = (N + 63) // 64
+    table = sac.make_block_table(7, nb, 2)
+    if width < 4:  # rows of 3 entries, every third row padded after its first two
+        table = table[:, :width].clone()
+        table[::3, 2] = -1
+    tab = sac._validated_table(table, nb)
+    g = torch.Generator(device="cuda").manual_seed(2)
+    q, k, v = (torch.randn(shape, device="cuda", generator=g).to(dtype) for _ in range(3))
+    o = torch.full_like(q, 3.0)
+    dtab = tab.to("cuda")
+    desc = ma_attn.make_desc(*shape, ma_attn.DTYPES[dtype], ma_attn.BLOCK_SPARSE, block_size=64,
+                             block_table_ptr=dtab.data_ptr(), blocks_per_row=tab.shape[1])
+    ma_attn.copy_probe_raw(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                           torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    it = torch.int16 if dtype != torch.float32 else torch.int32
+    pad = nb * 64 - N
+    kp = torch.nn.functional.pad(k.view(it), (0, 0, 0, 0, 0, pad))  # rows past N read as zero
+    vp = torch.nn.functional.pad(v.view(it), (0, 0, 0, 0, 0, pad))
+    want = q.view(it).clone()
+    i = torch.arange(N, device="cuda")
+    for e in range(tab.shape[1]):
+        c = dtab[i // 64, e].long()
+        src = torch.where(c >= 0, 64 * c + i % 64, 0)
+        x = kp[:, src] ^ vp[:, src]
+        want ^= torch.where((c >= 0).view(1, N, 1, 1), x, torch.zeros_like(x))
+    assert torch.equal(o.view(it), want)
 
 
 def test_copy_probe_rejects_other_patterns():
