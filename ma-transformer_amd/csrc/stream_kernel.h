@@ -276,6 +276,36 @@ struct F32Path {
     *reinterpret_cast<uint4*>(krow + 16 * (tid & 7) + 128) = s.r[1];
   }
 
+  // A sub-tile's operands as registers, for a caller that reads the next
+  // sub-tile's operands from LDS while this one computes: K rows (QK^T) and
+  // permuted V rows (P.V), four 16 B reads each.  (qk / pv below read as they
+  // go; issuing all four reads first measured slower in the block kernel.)
+  using Ops = f32x4[4];
+  static __device__ __forceinline__ void ld_k(const uint8_t* kp, Ops& a) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a[j] = __builtin_bit_cast(f32x4, *reinterpret_cast<const uint4*>(kp + 64 * j));
+  }
+  static __device__ __forceinline__ void ld_v(const uint8_t* vp, Ops& va) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) va[r] = __builtin_bit_cast(f32x4, *reinterpret_cast<const uint4*>(vp + r * kVRow));
+  }
+  static __device__ __forceinline__ f32x4 qk_ops(const Ops& a, const Q& q) {
+    f32x4 z = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 b = __builtin_bit_cast(f32x4, q.r[j]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) z = mfma_f32(a[j][r], b[r], z);
+    }
+    return z;
+  }
+  static __device__ __forceinline__ void pv_ops(const Ops& va, const float (&p)[4], f32x4 (&acc)[4]) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) acc[dt] = mfma_f32(va[r][dt], p[r], acc[dt]);
+  }
+
   static __device__ __forceinline__ f32x4 qk(const uint8_t* kp, const Q& q) {
     f32x4 z = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -473,6 +503,60 @@ __device__ __forceinline__ void window_tile(const uint8_t* ring, uint32_t kl, ui
   constexpr int kSubs = P::kRows / 16;
   f32x4 sc[G::NSUB];
   uint32_t vaddr[G::NSUB];
+  if constexpr (!P::kTrRows && !LG) {
+    // fp32: each sub-tile's 16 MFMAs run while the next sub-tile's operands
+    // are read from LDS into the other register buffer; the scheduling
+    // barriers keep the compiler from sinking those reads to their use.
+    uint32_t kaddr[G::NSUB];
+#pragma unroll
+    for (int j = 0; j < G::NSUB; ++j) {
+      const int u = wv + 3 * G::CL + j;
+      const uint32_t sb = (uint32_t)((((t - G::CL) * (4 / kSubs) + u / kSubs) % G::NSLOT) * P::kSlot);
+      kaddr[j] = sb + P::k_sub(u % kSubs) + kl;
+      vaddr[j] = sb + P::v_sub(u % kSubs) + vl;
+    }
+    typename P::Ops ob[2];
+    P::ld_k(ring + kaddr[0], ob[0]);
+#pragma unroll
+    for (int j = 0; j < G::NSUB; ++j) {
+      if (j + 1 < G::NSUB) P::ld_k(ring + kaddr[j + 1], ob[(j + 1) & 1]);
+      else P::ld_v(ring + vaddr[0], ob[(j + 1) & 1]);  // the first P.V operand
+      __builtin_amdgcn_sched_barrier(0);
+      f32x4 z = P::qk_ops(ob[j & 1], q);
+      __builtin_amdgcn_sched_barrier(0);
+      const int rel = 16 * (j - G::CL);
+      if (rel - 15 < -L || rel + 15 > R) {  // resolved at compile time
+#pragma unroll
+        for (int r = 0; r < 4; ++r) z[r] = (uint32_t)(dl + rel + r) <= (uint32_t)(L + R) ? z[r] : -INFINITY;
+      }
+      sc[j] = z;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < G::NSUB; ++j) mx = fmaxf(mx, fmaxf(fmaxf(sc[j][0], sc[j][1]), fmaxf(sc[j][2], sc[j][3])));
+    const float m_use = col_max(mx) * sl2;  // finite: every query sees its own key
+    float l_run = 0.0f;
+    f32x4 acc[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    constexpr int kV0 = G::NSUB & 1;  // buffer holding the first P.V operand
+#pragma unroll
+    for (int j = 0; j < G::NSUB; ++j) {
+      if (j + 1 < G::NSUB) P::ld_v(ring + vaddr[j + 1], ob[(kV0 + j + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      float p[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[r] = __builtin_amdgcn_exp2f(fmaf(sc[j][r], sl2, -m_use));
+        l_run += p[r];
+      }
+      P::pv_ops(ob[(kV0 + j) & 1], p, acc);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const float l_tot = col_sum(l_run);
+    P::store_o(acc, __builtin_amdgcn_rcpf(l_tot), Or, orow, g);
+    return;
+  }
   f32x4 zg = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   float mx = -INFINITY;
   if (LG) {  // Longformer global keys 0..ng-1 (interior tiles: no window key is below ng)
