@@ -13,15 +13,15 @@
 // band's 64-row blocks of the other operand streaming through a two-buffer
 // LDS ring with the next block in flight into registers:
 //
-// bwd_q_kernel   query tile.  Each key block is staged as K and V rows (the
-//   16-bit path reads K^T from the K rows through the LDS transpose read;
-//   fp32 stages K as (K rows, K^T) beside the V rows).
+// bwd_q_kernel   query tile.  Each key block is staged as K and V rows in one
+//   slot; K^T comes from the K rows (16-bit: the LDS transpose read; fp32:
+//   16-byte reads of the column-permuted rows).
 //   Pass 1 over the band: S^T = K Q^T and dP^T = V dO^T on 16x16x32 MFMA,
 //   online max / sum / sum(e * dp), giving lse2 and delta with no O.  Pass 2
 //   over the same blocks: dS^T from registers, dQ^T += K^T dS^T (pv2).
 //   Writes dq and the per-row {lse2, delta}.
 // bwd_kv_kernel  key tile, after bwd_q_kernel.  Each query block is staged
-//   as Q and dO rows (fp32: (Q rows, Q^T), (dO rows, dO^T)) and its 64
+//   as Q and dO rows in one slot (Q^T, dO^T read from them) and its 64
 //   {lse2, delta}.  S = Q K^T
 //   and dP = dO V^T with the tile's K, V rows as the register operand (the
 //   MFMA output lands as lane (key c, group g) holding queries 4g..4g+3,
@@ -54,63 +54,46 @@ struct BwdArgs {
 };
 
 // LDS of one streamed block in the backward passes: two matrices (K and V
-// for dQ, Q and dO for dK/dV).  The 16-bit path keeps both as rows in one
-// slot and reads a transpose with tr_read; fp32 stages a matrix that is read
-// transposed as a (rows, permuted rows) slot pair, so the entry takes two.
-// kT1 / kT2: the transposed operand of the first / second matrix, relative
-// to buffer + blk_v(u) + v_lane.
+// for dQ, Q and dO for dK/dV) in one block buffer, the first in the slots'
+// first halves, the second in their second halves; a matrix read transposed
+// is read from the same rows (16-bit: tr_read; fp32: permuted columns).
+// kRows2: the second matrix's rows relative to the first's; kT1 / kT2: the
+// transposed operand of the first / second matrix, relative to buffer +
+// blk_v(u) + v_lane.
 template <class P>
 struct PairLds {
-  static constexpr bool kTr = P::kTrRows;
-  static constexpr int kBytes = (kTr ? 1 : 2) * P::kBlk;
-  static constexpr int kRows2 = kTr ? P::kSlotK : P::kBlk;  // the second matrix's rows
-  static constexpr int kT1 = kTr ? -P::kSlotK : 0;
-  static constexpr int kT2 = kTr ? 0 : P::kBlk;
+  static constexpr int kBytes = P::kBlk;
+  static constexpr int kRows2 = P::kSlotK;
+  static constexpr int kT1 = -P::kSlotK;
+  static constexpr int kT2 = 0;
 };
 
-// A block's two matrices in flight into registers, and their store into
-// a PairLds buffer: dQ pass (K read as rows and transposed, V as rows) ...
+// A block's two matrices in flight into registers, and their store into a
+// PairLds buffer: dQ pass (K read as rows and transposed, V as rows) and
+// dK/dV pass (Q and dO, each read as rows and transposed).
 template <class P>
 struct KvRegs {
-  BlkSlots<P> k;  // 16-bit: K and V rows in one slot
-  BlkRows<P> v;   // fp32: V rows
+  BlkSlots<P> k;
 };
 template <class P>
 __device__ __forceinline__ void kv_load(KvRegs<P>& x, __amdgpu_buffer_rsrc_t Kr, __amdgpu_buffer_rsrc_t Vr,
                                         uint32_t off, int tid, uint32_t tb) {
-  if constexpr (P::kTrRows) {
-    load_blk<P>(x.k, Kr, Vr, off, tid, tb);
-  } else {
-    load_blk<P>(x.k, Kr, Kr, off, tid, tb);
-    load_rblk<P>(x.v, Vr, off, tid, tb);
-  }
+  load_blk<P>(x.k, Kr, Vr, off, tid, tb);
 }
 template <class P>
 __device__ __forceinline__ void kv_store(const KvRegs<P>& x, uint8_t* buf, int tid) {
   store_blk<P>(x.k, buf, tid);
-  if constexpr (!P::kTrRows) store_rblk<P>(x.v, buf + P::kBlk, tid);
 }
-
-// ... and dK/dV pass (Q and dO, each read as rows and transposed).
 template <class P>
-struct QgRegs {
-  BlkSlots<P> q;  // 16-bit: Q and dO rows in one slot
-  BlkSlots<P> g;  // fp32: dO
-};
+using QgRegs = KvRegs<P>;
 template <class P>
 __device__ __forceinline__ void qg_load(QgRegs<P>& x, __amdgpu_buffer_rsrc_t Qr, __amdgpu_buffer_rsrc_t Gr,
                                         uint32_t off, int tid, uint32_t tb) {
-  if constexpr (P::kTrRows) {
-    load_blk<P>(x.q, Qr, Gr, off, tid, tb);
-  } else {
-    load_blk<P>(x.q, Qr, Qr, off, tid, tb);
-    load_blk<P>(x.g, Gr, Gr, off, tid, tb);
-  }
+  load_blk<P>(x.k, Qr, Gr, off, tid, tb);
 }
 template <class P>
 __device__ __forceinline__ void qg_store(const QgRegs<P>& x, uint8_t* buf, int tid) {
-  store_blk<P>(x.q, buf, tid);
-  if constexpr (!P::kTrRows) store_blk<P>(x.g, buf + P::kBlk, tid);
+  store_blk<P>(x.k, buf, tid);
 }
 
 // Workgroup -> (b, h, rho, tile) and the residue class's resources.

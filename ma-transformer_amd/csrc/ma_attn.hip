@@ -2015,7 +2015,7 @@ int ma_attn_backward(const ma_attn_desc* desc, const void* q, const void* k, con
       return fail("ma_attn_backward: workspace of %zu bytes needed, %zu given", need_t, workspace_bytes);
     rc = desc->dtype == MA_ATTN_BF16  ? launch_tiles_bwd<HalfPath<__bf16>>(desc, ptrs, workspace, st)
          : desc->dtype == MA_ATTN_F16 ? launch_tiles_bwd<HalfPath<_Float16>>(desc, ptrs, workspace, st)
-                                      : launch_tiles_bwd<F32Path>(desc, ptrs, workspace, st);
+                                      : launch_tiles_bwd<F32BwdPath>(desc, ptrs, workspace, st);
     if (rc) return rc;
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail("ma_attn_backward: kernel launch failed: %s", hipGetErrorString(e));
@@ -2025,7 +2025,7 @@ int ma_attn_backward(const ma_attn_desc* desc, const void* q, const void* k, con
     float* sf = reinterpret_cast<float*>(stats);
     rc = desc->dtype == MA_ATTN_BF16  ? launch_backward_mfma<HalfPath<__bf16>>(desc, ptrs, sf, st)
          : desc->dtype == MA_ATTN_F16 ? launch_backward_mfma<HalfPath<_Float16>>(desc, ptrs, sf, st)
-                                      : launch_backward_mfma<F32Path>(desc, ptrs, sf, st);
+                                      : launch_backward_mfma<F32BwdPath>(desc, ptrs, sf, st);
     if (rc) return rc;
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail("ma_attn_backward: kernel launch failed: %s", hipGetErrorString(e));

@@ -427,7 +427,7 @@ __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dq_kernel(TileAr
 // ---------------------------------------------------------------- dK, dV
 
 template <class P>
-__global__ __launch_bounds__(256, P::kTrRows ? 3 : 1) void tile_dkv_kernel(TileArgs a) {
+__global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dkv_kernel(TileArgs a) {
   // 2 buffers x (PairLds (Q, dO), 64 lse2, 64 delta)
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
   using Elt = typename P::Elt;
