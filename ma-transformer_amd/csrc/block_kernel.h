@@ -240,6 +240,7 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void block_row_kernel(BlockArgs
 
   for (int e = 0; e < ne; ++e) {
     load_blk<P>(nxt, Kr, Vr, blk_off(e + 1), tid, tb);
+    __builtin_amdgcn_sched_barrier(0);
     const int cb = block_of(e);
     block_update<P>(ring + (e & 1) * P::kBlk, kl, vl, q, cb, dense && a.causal && cb == r, 16 * wv + c, N, g,
                     a.scale_log2, m_run, l_run, acc);
