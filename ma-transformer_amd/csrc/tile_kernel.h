@@ -203,7 +203,6 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void tile_fwd_kernel(TileArgs a
   typename P::Q q;
   P::load_q(q, Qr, qrow, g);
   const uint32_t kl = P::k_lane(c, g), vl = P::v_lane(c, g);
-  auto blk_off = [&](int e) { return e < e1 ? (uint32_t)(64 * (a.blk[e] & (kTileFull - 1))) * tb : kOob; };
 
   float m_run = -INFINITY, l_run = 0.0f;
   f32x4 acc[4];
@@ -212,21 +211,28 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void tile_fwd_kernel(TileArgs a
   const float sl2 = a.scale_log2;
 
   if (e0 < e1) {  // uniform
+    // entry e+2's flags word is read at step e (f0, f1: entries e, e+1)
+    int f0 = a.blk[e0];
+    int f1 = e0 + 1 < e1 ? a.blk[e0 + 1] : 0;
+    auto off_of = [&](int e, int f) { return e < e1 ? (uint32_t)(64 * (f & (kTileFull - 1))) * tb : kOob; };
     BlkSlots<P> nxt;
-    load_blk<P>(nxt, Kr, Vr, blk_off(e0), tid, tb);
+    load_blk<P>(nxt, Kr, Vr, off_of(e0, f0), tid, tb);
     uint64_t mw_next = a.mask[(int64_t)e0 * 64 + ql];
     store_blk<P>(nxt, ring, tid);
     __syncthreads();
     for (int e = e0; e < e1; ++e) {
-      const bool full = (a.blk[e] & kTileFull) != 0;
+      const bool full = (f0 & kTileFull) != 0;
       const uint64_t mw = mw_next;
-      load_blk<P>(nxt, Kr, Vr, blk_off(e + 1), tid, tb);
+      load_blk<P>(nxt, Kr, Vr, off_of(e + 1, f1), tid, tb);
       if (e + 1 < e1) mw_next = a.mask[(int64_t)(e + 1) * 64 + ql];
+      const int f2 = e + 2 < e1 ? a.blk[e + 2] : 0;
       tile_update<P>(ring + ((e - e0) & 1) * P::kBlk, kl, vl, q, full, mw, g, sl2, m_run, l_run, acc);
       // the next block goes into the buffer the previous one used (every
       // wave passed the barrier that ended it)
       if (e + 1 < e1) store_blk<P>(nxt, ring + ((e + 1 - e0) & 1) * P::kBlk, tid);
       __syncthreads();
+      f0 = f1;
+      f1 = f2;
     }
   }
   const float l_tot = col_sum(l_run);
@@ -369,9 +375,6 @@ __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dq_kernel(TileAr
   auto entry_of = [&](int k) { return e0 + (own && k >= ne ? k - ne : k); };
   auto buf_of = [&](int k) { return resident ? (k < ne ? k : k - ne) : (k & 1); };
   auto loads = [&](int k) { return k < nit && (!resident || k < ne); };
-  auto blk_off = [&](int k) {
-    return loads(k) ? (uint32_t)(64 * (a.blk[entry_of(k)] & (kTileFull - 1))) * tb : kOob;
-  };
 
   f32x4 acc[4];
 #pragma unroll
@@ -380,17 +383,22 @@ __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dq_kernel(TileAr
   float m_run = -INFINITY, l_run = 0.0f, a_run = 0.0f;
 
   if (nit > 0) {  // uniform
-    // V is read only as rows (dP^T = V dO^T): its transposed part stays unwritten
+    // The flags word of step k+2's entry is read at step k, so that no
+    // block's loads wait on a plan lookup (f0, f1: steps k, k+1).
+    int f0 = a.blk[entry_of(0)];
+    int f1 = nit > 1 ? a.blk[entry_of(1)] : 0;
+    auto off_of = [&](int k, int f) { return loads(k) ? (uint32_t)(64 * (f & (kTileFull - 1))) * tb : kOob; };
     KvRegs<P> xk;
-    kv_load<P>(xk, Kr, Vr, blk_off(0), tid, tb);
+    kv_load<P>(xk, Kr, Vr, off_of(0, f0), tid, tb);
     uint64_t mw_next = a.mask[(int64_t)entry_of(0) * 64 + ql];
     kv_store<P>(xk, ring, tid);
     __syncthreads();
     for (int k = 0; k < nit; ++k) {
-      const bool full = (a.blk[entry_of(k)] & kTileFull) != 0;
+      const bool full = (f0 & kTileFull) != 0;
       const uint64_t mw = mw_next;
-      kv_load<P>(xk, Kr, Vr, blk_off(k + 1), tid, tb);
+      kv_load<P>(xk, Kr, Vr, off_of(k + 1, f1), tid, tb);
       if (k + 1 < nit) mw_next = a.mask[(int64_t)entry_of(k + 1) * 64 + ql];
+      const int f2 = k + 2 < nit ? a.blk[entry_of(k + 2)] : 0;
       const uint8_t* sk = ring + buf_of(k) * kBuf;
       f32x4 s[4], dp[4];
 #pragma unroll
@@ -410,6 +418,8 @@ __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dq_kernel(TileAr
         kv_store<P>(xk, nx, tid);
       }
       __syncthreads();
+      f0 = f1;
+      f1 = f2;
     }
   }
   if (own) {
@@ -474,6 +484,18 @@ __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dkv_kernel(TileA
   const float sl2 = a.scale_log2;
 
   if (p0 < p1) {  // uniform
+    // Plan words are read once each and a step ahead of use, so that no
+    // step's block loads wait on a chain of plan lookups: entry p+3 is read at
+    // step p, its tile and flags word at step p+1, and the block loads of
+    // step p+2 use them.  Words are kept as read and clamped at their use, so
+    // that no load is waited on in the step that issues it.  (e*, t*, f*:
+    // entry, query tile, flags word of entries p+1, p+2.)
+    auto ce = [&](int e) { return clampi(e, 0, a.nent - 1); };
+    auto ct = [&](int t) { return clampi(t, 0, a.ntiles - 1); };
+    int e1 = p0 + 1 < p1 ? a.kentry[p0 + 1] : 0;
+    int e2 = p0 + 2 < p1 ? a.kentry[p0 + 2] : 0;
+    int f0 = a.blk[ent(p0)];
+    int t1 = p0 + 1 < p1 ? a.etile[ce(e1)] : 0, f1 = p0 + 1 < p1 ? a.blk[ce(e1)] : 0;
     QgRegs<P> xq;
     qg_load<P>(xq, Qr, Gr, q_off(p0), tid, tb);
     uint2 xs = bload8(Sr, st_off(p0));
@@ -482,11 +504,14 @@ __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dkv_kernel(TileA
     bwd_stage_stats(ring + PL::kBytes, xs, tid);
     __syncthreads();
     for (int p = p0; p < p1; ++p) {
-      const bool full = (a.blk[ent(p)] & kTileFull) != 0;
+      const bool full = (f0 & kTileFull) != 0;
       const uint64_t mw = mw_next;
-      qg_load<P>(xq, Qr, Gr, q_off(p + 1), tid, tb);
-      xs = bload8(Sr, st_off(p + 1));
-      if (p + 1 < p1) mw_next = a.kmask[(int64_t)ent(p + 1) * 64 + kl_];
+      const bool more = p + 1 < p1;
+      qg_load<P>(xq, Qr, Gr, more ? (uint32_t)(64 * ct(t1)) * tb : kOob, tid, tb);
+      xs = bload8(Sr, more && tid < 64 ? (uint32_t)(64 * ct(t1) + tid) * sstride : kOob);
+      if (more) mw_next = a.kmask[(int64_t)ce(e1) * 64 + kl_];
+      const int e3 = p + 3 < p1 ? a.kentry[p + 3] : 0;
+      const int t2 = p + 2 < p1 ? a.etile[ce(e2)] : 0, f2 = p + 2 < p1 ? a.blk[ce(e2)] : 0;
       const uint8_t* sq = ring + ((p - p0) & 1) * kBuf;
       const uint8_t* sg = sq + PL::kRows2;
       const float* stf = reinterpret_cast<const float*>(sq + PL::kBytes);
@@ -514,12 +539,17 @@ __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dkv_kernel(TileA
         P::pv2(sq + P::blk_v(u) + vg, sq + P::blk_v(u + 1) + vg, pa, pb, acc_v);  // dV^T += dO^T P
         P::pv2(sq + P::blk_v(u) + vq, sq + P::blk_v(u + 1) + vq, da, db, acc_k);  // dK^T += Q^T dS
       }
-      if (p + 1 < p1) {
+      if (more) {
         uint8_t* nx = ring + ((p + 1 - p0) & 1) * kBuf;
         qg_store<P>(xq, nx, tid);
         bwd_stage_stats(nx + PL::kBytes, xs, tid);
       }
       __syncthreads();
+      f0 = f1;
+      e1 = e2;
+      t1 = t2;
+      f1 = f2;
+      e2 = e3;
     }
   }
   if (slot < 0) {
