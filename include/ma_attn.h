@@ -84,6 +84,8 @@ typedef struct ma_attn_tile_header {
   int64_t off_k_items;    /* int32 [num_k_items][4]: key block, first and end position in kentry, slot or -1 */
   int64_t off_k_split;    /* int32 [num_k_split][4]: key block, first slot, slot count, 0 */
   int64_t total_bytes;
+  int64_t num_masked;     /* entries without bit 30 (not every pair in the set); -1 after the
+                             sizes-only call (plan NULL).  0 lets the kernels skip all mask work */
 } ma_attn_tile_header;
 
 typedef struct ma_attn_desc {
@@ -293,7 +295,7 @@ int ma_attn_copy_probe_timed(const ma_attn_desc* desc, const void* q, const void
 /* ABI version of this header (bumped on incompatible change). */
 int ma_attn_abi_version(void);
 
-#define MA_ATTN_ABI_VERSION 7
+#define MA_ATTN_ABI_VERSION 8
 
 #ifdef __cplusplus
 }

@@ -877,7 +877,8 @@ int validate(const ma_attn_desc* d) {
                              d->tile_header->num_entries < 0 || d->tile_header->num_q_items < (d->seq_len + 63) / 64 ||
                              d->tile_header->num_k_items < (d->seq_len + 63) / 64 || d->tile_header->num_q_partials < 0 ||
                              d->tile_header->num_k_partials < 0 || d->tile_header->num_q_split < 0 ||
-                             d->tile_header->num_k_split < 0))
+                             d->tile_header->num_k_split < 0 || d->tile_header->num_masked < -1 ||
+                             d->tile_header->num_masked > d->tile_header->num_entries))
         return fail("ma_attn: the tile plan does not belong to a set of seq_len %lld", (long long)d->seq_len);
       if (!d->index_offsets && d->seq_len > 0) return fail("ma_attn: index_offsets is null");
       if (!d->index_keys && d->num_indices > 0) return fail("ma_attn: index_keys is null");
@@ -1779,7 +1780,9 @@ int launch_tiles_fwd(const ma_attn_desc* d, const void* q, const void* k, const 
   a.part = static_cast<float*>(ws);
   const int64_t bh = d->batch * d->num_heads;
   const size_t shm = 2 * (size_t)P::kBlk;
-  auto kf = &tile_fwd_kernel<P, false>;
+  // a plan of full entries only (block tables) takes the kernels with no mask work
+  auto kf = d->tile_header->num_masked != 0 ? &tile_fwd_kernel<P, false, true>
+                                            : &tile_fwd_kernel<P, false, false>;
   if (reserve_lds(reinterpret_cast<const void*>(kf), shm, st)) return 1;
   launch(a.nsplit == 0, kf, dim3((unsigned)(bh * a.nitems)), dim3(256), (uint32_t)shm, st, a);
   if (a.nsplit > 0)
@@ -1802,9 +1805,10 @@ int launch_tiles_bwd(const ma_attn_desc* d, const void* const* ptrs, void* ws, h
   a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + stats_bytes(d));
   const int64_t bh = d->batch * d->num_heads;
   using Elt = typename P::Elt;
-  auto kf = &tile_fwd_kernel<P, true>;
-  auto kq = &tile_dq_kernel<P>;
-  auto kkv = &tile_dkv_kernel<P>;
+  const bool masked = d->tile_header->num_masked != 0;
+  auto kf = masked ? &tile_fwd_kernel<P, true, true> : &tile_fwd_kernel<P, true, false>;
+  auto kq = masked ? &tile_dq_kernel<P, true> : &tile_dq_kernel<P, false>;
+  auto kkv = masked ? &tile_dkv_kernel<P, true> : &tile_dkv_kernel<P, false>;
   const size_t shm_f = 2 * (size_t)P::kBlk, shm_q = 2 * (size_t)PairLds<P>::kBytes,
                shm_kv = 2 * ((size_t)PairLds<P>::kBytes + 512);
   if (reserve_lds(reinterpret_cast<const void*>(kf), shm_f, st) ||
@@ -2361,6 +2365,7 @@ int ma_attn_tile_plan(int64_t N, const int64_t* off, const int32_t* keys, int64_
   h.off_k_items = take(16 * ki);
   h.off_k_split = take(16 * ks);
   h.total_bytes = at;
+  h.num_masked = -1;  // known once the masks are built
   *hdr = h;
   if (!plan) return 0;
   if (plan_bytes < (size_t)h.total_bytes) return fail("ma_attn_tile_plan: plan buffer too small"), -1;
@@ -2391,6 +2396,10 @@ int ma_attn_tile_plan(int64_t N, const int64_t* off, const int32_t* keys, int64_
         if (full) blk[e] |= 1 << 30;
       }
   }
+  int64_t masked = 0;
+  for (int64_t e = 0; e < ne; ++e) masked += (blk[e] & (1 << 30)) == 0;
+  hdr->num_masked = masked;
+  reinterpret_cast<ma_attn_tile_header*>(base)->num_masked = masked;
   // the transposed masks: bit r of word k
   uint64_t* kmask = reinterpret_cast<uint64_t*>(base + h.off_kmask);
   for (int64_t e = 0; e < ne; ++e)

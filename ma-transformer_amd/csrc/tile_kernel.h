@@ -92,6 +92,27 @@ __device__ __forceinline__ void apply_mask(f32x4 (&sc)[4], uint64_t m, int g) {
   }
 }
 
+// Wave-uniform mask of the 16-wide sub-tiles of an entry that hold a pair of
+// this wave's 16 rows: bit u is set when some lane's mask word (its row's
+// keys, or its key's queries) has a bit in 16u..16u+15.  Empty sub-tiles are
+// not computed: a Longformer global key block holds one live sub-tile of
+// four, and a causal window's edge blocks are triangles of sub-tiles.
+__device__ __forceinline__ int live_subtiles(uint64_t mw, bool full) {
+  if (full) return 0xF;  // uniform
+  int live = 0;
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+    live |= (__builtin_amdgcn_ballot_w64(((mw >> (16 * u)) & 0xFFFFull) != 0) != 0 ? 1 : 0) << u;
+  return live;
+}
+
+// Compile-time "every sub-tile live": a full entry's products issue back to
+// back with no per-sub-tile branch.
+template <bool B>
+struct AllLive {
+  static constexpr bool value = B;
+};
+
 // dot(x, O) of one query row over the head_dim values this lane holds (x in
 // the Q register layout of P, which is also the accumulator layout).
 template <class P>
@@ -123,13 +144,18 @@ __device__ __forceinline__ float lane_dot(const typename P::Q& x, const f32x4 (&
 }
 
 // One 64-key block of the lane's query row into the online softmax.
-template <class P>
-__device__ __forceinline__ void tile_update(const uint8_t* slot, uint32_t kl, uint32_t vl, const typename P::Q& q,
-                                            bool full, uint64_t mw, int g, float sl2, float& m_run, float& l_run,
-                                            f32x4 (&acc)[4]) {
+template <class P, bool ALL>
+__device__ __forceinline__ void tile_update_live(const uint8_t* slot, uint32_t kl, uint32_t vl,
+                                                 const typename P::Q& q, bool full, uint64_t mw, int live, int g,
+                                                 float sl2, float& m_run, float& l_run, f32x4 (&acc)[4]) {
   f32x4 sc[4];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) sc[u] = P::qk(slot + P::blk_k(u) + kl, q);
+  for (int u = 0; u < 4; ++u) {
+    if (ALL || (live >> u & 1))
+      sc[u] = P::qk(slot + P::blk_k(u) + kl, q);
+    else
+      sc[u] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  }
   if (!full) apply_mask(sc, mw, g);  // uniform
   float mx = -INFINITY;
 #pragma unroll
@@ -145,6 +171,7 @@ __device__ __forceinline__ void tile_update(const uint8_t* slot, uint32_t kl, ui
   m_run = m_new;
 #pragma unroll
   for (int u = 0; u < 4; u += 2) {
+    if (!ALL && !(live >> u & 3)) continue;  // uniform: both sub-tiles empty
     float p0[4], p1[4];
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
@@ -154,6 +181,18 @@ __device__ __forceinline__ void tile_update(const uint8_t* slot, uint32_t kl, ui
     }
     P::pv2(slot + P::blk_v(u) + vl, slot + P::blk_v(u + 1) + vl, p0, p1, acc);
   }
+}
+
+// MASKED false: the plan has no masked entry, every sub-tile is live.
+template <class P, bool MASKED>
+__device__ __forceinline__ void tile_update(const uint8_t* slot, uint32_t kl, uint32_t vl, const typename P::Q& q,
+                                            bool full, uint64_t mw, int g, float sl2, float& m_run, float& l_run,
+                                            f32x4 (&acc)[4]) {
+  const int live = MASKED ? live_subtiles(mw, full) : 0xF;
+  if (live == 0xF)  // uniform
+    tile_update_live<P, true>(slot, kl, vl, q, full, mw, live, g, sl2, m_run, l_run, acc);
+  else if (live)  // no key of this block for the wave's rows: nothing to add
+    tile_update_live<P, false>(slot, kl, vl, q, full, mw, live, g, sl2, m_run, l_run, acc);
 }
 
 struct TileCtx {
@@ -177,7 +216,7 @@ __device__ __forceinline__ TileCtx tile_ctx(const TileArgs& a, int bh) {
 
 // ---------------------------------------------------------------- forward / statistics
 
-template <class P, bool STATS>
+template <class P, bool STATS, bool MASKED>
 __global__ __launch_bounds__(256, P::kMinBlocks) void tile_fwd_kernel(TileArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 block buffers of P::kBlk bytes
   using Elt = typename P::Elt;
@@ -210,7 +249,23 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void tile_fwd_kernel(TileArgs a
   for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   const float sl2 = a.scale_log2;
 
-  if (e0 < e1) {  // uniform
+  if (e1 - e0 <= 2 && e0 < e1) {  // uniform
+    // Both blocks are loaded at once and the two entries run with no
+    // barrier between them, so each wave computes only its own live
+    // sub-tiles of the two (a causal window's edge blocks are triangles).
+    const int fa = a.blk[e0], fb = e0 + 1 < e1 ? a.blk[e0 + 1] : 0;
+    BlkSlots<P> xa, xb;
+    load_blk<P>(xa, Kr, Vr, (uint32_t)(64 * (fa & (kTileFull - 1))) * tb, tid, tb);
+    load_blk<P>(xb, Kr, Vr, e0 + 1 < e1 ? (uint32_t)(64 * (fb & (kTileFull - 1))) * tb : kOob, tid, tb);
+    const uint64_t ma = a.mask[(int64_t)e0 * 64 + ql];
+    const uint64_t mb = e0 + 1 < e1 ? a.mask[(int64_t)(e0 + 1) * 64 + ql] : 0;
+    store_blk<P>(xa, ring, tid);
+    if (e0 + 1 < e1) store_blk<P>(xb, ring + P::kBlk, tid);
+    __syncthreads();
+    tile_update<P, MASKED>(ring, kl, vl, q, (fa & kTileFull) != 0, ma, g, sl2, m_run, l_run, acc);
+    if (e0 + 1 < e1)
+      tile_update<P, MASKED>(ring + P::kBlk, kl, vl, q, (fb & kTileFull) != 0, mb, g, sl2, m_run, l_run, acc);
+  } else if (e0 < e1) {  // uniform
     // entry e+2's flags word is read at step e (f0, f1: entries e, e+1)
     int f0 = a.blk[e0];
     int f1 = e0 + 1 < e1 ? a.blk[e0 + 1] : 0;
@@ -226,7 +281,7 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void tile_fwd_kernel(TileArgs a
       load_blk<P>(nxt, Kr, Vr, off_of(e + 1, f1), tid, tb);
       if (e + 1 < e1) mw_next = a.mask[(int64_t)(e + 1) * 64 + ql];
       const int f2 = e + 2 < e1 ? a.blk[e + 2] : 0;
-      tile_update<P>(ring + ((e - e0) & 1) * P::kBlk, kl, vl, q, full, mw, g, sl2, m_run, l_run, acc);
+      tile_update<P, MASKED>(ring + ((e - e0) & 1) * P::kBlk, kl, vl, q, full, mw, g, sl2, m_run, l_run, acc);
       // the next block goes into the buffer the previous one used (every
       // wave passed the barrier that ended it)
       if (e + 1 < e1) store_blk<P>(nxt, ring + ((e + 1 - e0) & 1) * P::kBlk, tid);
@@ -329,7 +384,7 @@ __device__ __forceinline__ void tile_stats(float m_run, float l_run, float a_run
   dlt = l_tot > 0.0f ? a_tot / l_tot : 0.0f;
 }
 
-template <class P>
+template <class P, bool MASKED>
 __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dq_kernel(TileArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 buffers x PairLds (K, V)
   using Elt = typename P::Elt;
@@ -382,7 +437,60 @@ __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dq_kernel(TileAr
   const float sl2 = a.scale_log2;
   float m_run = -INFINITY, l_run = 0.0f, a_run = 0.0f;
 
-  if (nit > 0) {  // uniform
+  // Step k's products on the block in buffer sk: pass 1 (statistics) or
+  // pass 2 (dQ) of its entry.
+  auto step_live = [&](auto all, int k, const uint8_t* sk, bool full, uint64_t mw, int live)
+                       __attribute__((always_inline)) {
+    constexpr bool kAll = decltype(all)::value;
+    if (kAll) live = 0xF;
+    f32x4 s[4], dp[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (kAll || (live >> u & 1)) {  // uniform
+        s[u] = P::qk(sk + P::blk_k(u) + kl, qr);
+        dp[u] = P::qk(sk + PL::kRows2 + P::blk_k(u) + kl, gr);
+      } else {
+        s[u] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        dp[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+    }
+    if (!full) apply_mask(s, mw, g);
+    if (own && k < ne) {  // pass 1
+      bwdq_pass1(s, dp, live, sl2, m_run, l_run, a_run);
+      if (k == ne - 1) tile_stats(m_run, l_run, a_run, sl2, lse2, dlt);
+    } else {
+      bwdq_pass2<P>(sk, vl + PL::kT1, s, dp, live, sl2, lse2, dlt, acc);
+    }
+  };
+  auto step = [&](int k, const uint8_t* sk, bool full, uint64_t mw) __attribute__((always_inline)) {
+    const int live = MASKED ? live_subtiles(mw, full) : 0xF;
+    if (live == 0xF)  // uniform
+      step_live(AllLive<true>{}, k, sk, full, mw, live);
+    else
+      step_live(AllLive<false>{}, k, sk, full, mw, live);
+  };
+
+  if (resident && ne > 0) {  // uniform
+    // Both blocks are loaded at once and the steps run with no barrier
+    // between them, so each wave computes only its own live sub-tiles of
+    // the two entries.  On a causal window one wave has all four sub-tiles
+    // of one block and one of the other; with a barrier per step every step
+    // would last as long as its busiest wave.
+    const int fa = a.blk[e0];
+    const int fb = ne > 1 ? a.blk[e0 + 1] : 0;
+    KvRegs<P> xa, xb;
+    kv_load<P>(xa, Kr, Vr, (uint32_t)(64 * (fa & (kTileFull - 1))) * tb, tid, tb);
+    kv_load<P>(xb, Kr, Vr, ne > 1 ? (uint32_t)(64 * (fb & (kTileFull - 1))) * tb : kOob, tid, tb);
+    const uint64_t ma = a.mask[(int64_t)e0 * 64 + ql];
+    const uint64_t mb = ne > 1 ? a.mask[(int64_t)(e0 + 1) * 64 + ql] : 0;
+    kv_store<P>(xa, ring, tid);
+    if (ne > 1) kv_store<P>(xb, ring + kBuf, tid);
+    __syncthreads();
+    for (int k = 0; k < nit; ++k) {
+      const int j = k < ne ? k : k - ne;
+      step(k, ring + j * kBuf, ((j ? fb : fa) & kTileFull) != 0, j ? mb : ma);
+    }
+  } else if (nit > 0) {  // uniform
     // The flags word of step k+2's entry is read at step k, so that no
     // block's loads wait on a plan lookup (f0, f1: steps k, k+1).
     int f0 = a.blk[entry_of(0)];
@@ -399,20 +507,7 @@ __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dq_kernel(TileAr
       kv_load<P>(xk, Kr, Vr, off_of(k + 1, f1), tid, tb);
       if (k + 1 < nit) mw_next = a.mask[(int64_t)entry_of(k + 1) * 64 + ql];
       const int f2 = k + 2 < nit ? a.blk[entry_of(k + 2)] : 0;
-      const uint8_t* sk = ring + buf_of(k) * kBuf;
-      f32x4 s[4], dp[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        s[u] = P::qk(sk + P::blk_k(u) + kl, qr);
-        dp[u] = P::qk(sk + PL::kRows2 + P::blk_k(u) + kl, gr);
-      }
-      if (!full) apply_mask(s, mw, g);
-      if (own && k < ne) {  // pass 1
-        bwdq_pass1(s, dp, 0xF, sl2, m_run, l_run, a_run);
-        if (k == ne - 1) tile_stats(m_run, l_run, a_run, sl2, lse2, dlt);
-      } else {
-        bwdq_pass2<P>(sk, vl + PL::kT1, s, dp, 0xF, sl2, lse2, dlt, acc);
-      }
+      step(k, ring + buf_of(k) * kBuf, full, mw);
       if (loads(k + 1)) {
         uint8_t* nx = ring + buf_of(k + 1) * kBuf;
         kv_store<P>(xk, nx, tid);
@@ -436,7 +531,7 @@ __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dq_kernel(TileAr
 
 // ---------------------------------------------------------------- dK, dV
 
-template <class P>
+template <class P, bool MASKED>
 __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dkv_kernel(TileArgs a) {
   // 2 buffers x (PairLds (Q, dO), 64 lse2, 64 delta)
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
@@ -483,7 +578,77 @@ __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dkv_kernel(TileA
   for (int dt = 0; dt < 4; ++dt) acc_k[dt] = acc_v[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   const float sl2 = a.scale_log2;
 
-  if (p0 < p1) {  // uniform
+  // One entry's products on the query block in buffer sq (Q, dO rows, then
+  // the block's statistics).
+  auto step_live = [&](auto all, const uint8_t* sq, bool full, uint64_t mw, int live)
+                       __attribute__((always_inline)) {
+    constexpr bool kAll = decltype(all)::value;
+    const uint8_t* sg = sq + PL::kRows2;
+    const float* stf = reinterpret_cast<const float*>(sq + PL::kBytes);
+    f32x4 s[4], dp[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (kAll || (live >> u & 1)) {  // uniform
+        s[u] = P::qk(sq + P::blk_k(u) + kl, kr);   // S[query 16u+4g+r][key c]
+        dp[u] = P::qk(sg + P::blk_k(u) + kl, vr);  // dP[query][key c]
+      } else {
+        s[u] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        dp[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+    }
+    if (!full) apply_mask(s, mw, g);
+#pragma unroll
+    for (int u = 0; u < 4; u += 2) {
+      if (!kAll && !(live >> u & 3)) continue;  // uniform: both sub-tiles empty
+      const f32x4 lse0 = *reinterpret_cast<const f32x4*>(stf + 16 * u + 4 * g);
+      const f32x4 dl0 = *reinterpret_cast<const f32x4*>(stf + 64 + 16 * u + 4 * g);
+      const f32x4 lse1 = *reinterpret_cast<const f32x4*>(stf + 16 * (u + 1) + 4 * g);
+      const f32x4 dl1 = *reinterpret_cast<const f32x4*>(stf + 64 + 16 * (u + 1) + 4 * g);
+      float pa[4], pb[4], da[4], db[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pa[r] = __builtin_amdgcn_exp2f(fmaf(s[u][r], sl2, -lse0[r]));
+        pb[r] = __builtin_amdgcn_exp2f(fmaf(s[u + 1][r], sl2, -lse1[r]));
+        da[r] = pa[r] * (dp[u][r] - dl0[r]);
+        db[r] = pb[r] * (dp[u + 1][r] - dl1[r]);
+      }
+      P::pv2(sq + P::blk_v(u) + vg, sq + P::blk_v(u + 1) + vg, pa, pb, acc_v);  // dV^T += dO^T P
+      P::pv2(sq + P::blk_v(u) + vq, sq + P::blk_v(u + 1) + vq, da, db, acc_k);  // dK^T += Q^T dS
+    }
+  };
+  auto step = [&](const uint8_t* sq, bool full, uint64_t mw) __attribute__((always_inline)) {
+    // query sub-tiles that list one of the wave's keys
+    const int live = MASKED ? live_subtiles(mw, full) : 0xF;
+    if (live == 0xF)  // uniform
+      step_live(AllLive<true>{}, sq, full, mw, live);
+    else if (live)
+      step_live(AllLive<false>{}, sq, full, mw, live);
+  };
+
+  if (p1 - p0 <= 2 && p0 < p1) {  // uniform
+    // Both query blocks are loaded at once and the two entries run with no
+    // barrier between them, so each wave computes only its own live
+    // sub-tiles of the two (a causal window gives one wave all four query
+    // sub-tiles of one block and one of the other).
+    const int ta = tile_of(p0), tb2 = p0 + 1 < p1 ? tile_of(p0 + 1) : 0;
+    const int fa = a.blk[ent(p0)], fb = p0 + 1 < p1 ? a.blk[ent(p0 + 1)] : 0;
+    QgRegs<P> xa, xb;
+    qg_load<P>(xa, Qr, Gr, (uint32_t)(64 * ta) * tb, tid, tb);
+    qg_load<P>(xb, Qr, Gr, p0 + 1 < p1 ? (uint32_t)(64 * tb2) * tb : kOob, tid, tb);
+    const uint2 sa = bload8(Sr, st_off(p0));
+    const uint2 sb = bload8(Sr, st_off(p0 + 1));
+    const uint64_t ma = a.kmask[(int64_t)ent(p0) * 64 + kl_];
+    const uint64_t mb = p0 + 1 < p1 ? a.kmask[(int64_t)ent(p0 + 1) * 64 + kl_] : 0;
+    qg_store<P>(xa, ring, tid);
+    bwd_stage_stats(ring + PL::kBytes, sa, tid);
+    if (p0 + 1 < p1) {
+      qg_store<P>(xb, ring + kBuf, tid);
+      bwd_stage_stats(ring + kBuf + PL::kBytes, sb, tid);
+    }
+    __syncthreads();
+    step(ring, (fa & kTileFull) != 0, ma);
+    if (p0 + 1 < p1) step(ring + kBuf, (fb & kTileFull) != 0, mb);
+  } else if (p0 < p1) {  // uniform
     // Plan words are read once each and a step ahead of use, so that no
     // step's block loads wait on a chain of plan lookups: entry p+3 is read at
     // step p, its tile and flags word at step p+1, and the block loads of
@@ -512,33 +677,7 @@ __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dkv_kernel(TileA
       if (more) mw_next = a.kmask[(int64_t)ce(e1) * 64 + kl_];
       const int e3 = p + 3 < p1 ? a.kentry[p + 3] : 0;
       const int t2 = p + 2 < p1 ? a.etile[ce(e2)] : 0, f2 = p + 2 < p1 ? a.blk[ce(e2)] : 0;
-      const uint8_t* sq = ring + ((p - p0) & 1) * kBuf;
-      const uint8_t* sg = sq + PL::kRows2;
-      const float* stf = reinterpret_cast<const float*>(sq + PL::kBytes);
-      f32x4 s[4], dp[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        s[u] = P::qk(sq + P::blk_k(u) + kl, kr);   // S[query 16u+4g+r][key c]
-        dp[u] = P::qk(sg + P::blk_k(u) + kl, vr);  // dP[query][key c]
-      }
-      if (!full) apply_mask(s, mw, g);
-#pragma unroll
-      for (int u = 0; u < 4; u += 2) {
-        const f32x4 lse0 = *reinterpret_cast<const f32x4*>(stf + 16 * u + 4 * g);
-        const f32x4 dl0 = *reinterpret_cast<const f32x4*>(stf + 64 + 16 * u + 4 * g);
-        const f32x4 lse1 = *reinterpret_cast<const f32x4*>(stf + 16 * (u + 1) + 4 * g);
-        const f32x4 dl1 = *reinterpret_cast<const f32x4*>(stf + 64 + 16 * (u + 1) + 4 * g);
-        float pa[4], pb[4], da[4], db[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          pa[r] = __builtin_amdgcn_exp2f(fmaf(s[u][r], sl2, -lse0[r]));
-          pb[r] = __builtin_amdgcn_exp2f(fmaf(s[u + 1][r], sl2, -lse1[r]));
-          da[r] = pa[r] * (dp[u][r] - dl0[r]);
-          db[r] = pb[r] * (dp[u + 1][r] - dl1[r]);
-        }
-        P::pv2(sq + P::blk_v(u) + vg, sq + P::blk_v(u + 1) + vg, pa, pb, acc_v);  // dV^T += dO^T P
-        P::pv2(sq + P::blk_v(u) + vq, sq + P::blk_v(u + 1) + vq, da, db, acc_k);  // dK^T += Q^T dS
-      }
+      step(ring + ((p - p0) & 1) * kBuf, full, mw);
       if (more) {
         uint8_t* nx = ring + ((p + 1 - p0) & 1) * kBuf;
         qg_store<P>(xq, nx, tid);

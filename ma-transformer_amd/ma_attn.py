@@ -18,7 +18,7 @@ LIB_PATH = os.environ.get("MA_ATTN_LIB", os.path.join(_HERE, "libma_attn.so"))
 
 F32, BF16, F16 = 0, 1, 2
 SLIDING, DENSE, BLOCK_SPARSE, LONGFORMER, INDEX_SET = 0, 1, 2, 3, 4
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 
@@ -29,7 +29,7 @@ class TileHeader(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int64) for n in (
         "seq_len", "num_tiles", "num_entries", "seg", "num_q_items", "num_q_split", "num_q_partials",
         "num_k_items", "num_k_split", "num_k_partials", "off_blk", "off_mask", "off_kmask", "off_tile",
-        "off_kentry", "off_q_items", "off_q_split", "off_k_items", "off_k_split", "total_bytes")]
+        "off_kentry", "off_q_items", "off_q_split", "off_k_items", "off_k_split", "total_bytes", "num_masked")]
 
 
 class Desc(ctypes.Structure):

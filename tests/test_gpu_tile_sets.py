@@ -103,12 +103,13 @@ def test_tiled_matches_gather(ext, dtype):
     assert float((oa.float() - ob.float()).abs().max()) <= TOL[dtype]
 
 
-@pytest.mark.parametrize("pattern", ["block_sparse", "longformer"])
+@pytest.mark.parametrize("pattern,N", [("block_sparse", 1500), ("block_sparse", 1536), ("longformer", 1500)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_pattern_sets_on_tiles(ext, oracle, pattern, dtype):
+def test_pattern_sets_on_tiles(ext, oracle, pattern, N, dtype):
     """The key sets block-sparse and Longformer train on (pattern_index_set)
-    get a tile plan; their tiled backward matches the oracle's."""
-    N = 1500
+    get a tile plan; their tiled forward and backward match the oracle's.  A
+    block table over whole blocks (N a multiple of 64) gives a plan with no
+    masked entry, which runs the kernels' mask-free variant."""
     shape = (2, N, 2, 64)
     if pattern == "block_sparse":
         nb = (N + 63) // 64
@@ -119,7 +120,11 @@ def test_pattern_sets_on_tiles(ext, oracle, pattern, dtype):
         iset = ext.pattern_index_set("longformer", N, "cuda", left=127, right=0, num_global=16)
         spec = oracle.Spec(*shape, pattern="longformer", left=127, right=0, num_global=16)
     assert iset.tile_plan is not None
+    assert (iset.tile_header.num_masked == 0) == (pattern == "block_sparse" and N % 64 == 0)
     dev, up = _inputs(shape, 9400, dtype)
+    out = ext.index_set_forward(*dev[:3], iset)
+    err = float(np.abs(out.float().cpu().numpy() - oracle.forward(spec, *up[:3])).max())
+    assert err <= TOL[dtype], err
     got = ext.index_set_backward(*dev, iset)
     for name, a, b in zip("qkv", got, oracle.backward(spec, *up)):
         check_grad("d" + name, a.float().cpu().numpy(), b, dtype == torch.float32)

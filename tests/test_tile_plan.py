@@ -79,6 +79,10 @@ def test_tile_plan_matches_brute_force(N, density, fr, fc, seg):
         cols = np.array([sum(1 << int(r) for r in np.nonzero(sub[:, k])[0]) for k in range(64)], dtype=np.uint64)
         assert np.array_equal(p["mask"][e], rows) and np.array_equal(p["kmask"][e], cols), e
         assert bool(p["blk"][e] & FULL) == bool(sub.all() and r1 == 64 and k1 == 64), e
+    # the header counts the entries that are not full (the kernels' mask-free variant needs 0)
+    n_full = sum(bool(m[64 * t:64 * t + 64, 64 * c:64 * c + 64].all()) and 64 * t + 64 <= N and 64 * c + 64 <= N
+                 for t, c in pairs)
+    assert hdr.num_masked == len(pairs) - n_full
     # key-block order of the entries
     assert [(int(blk[e]), int(p["tile"][e])) for e in p["kentry"]] == sorted((c, t) for t, c in pairs)
     # work items
