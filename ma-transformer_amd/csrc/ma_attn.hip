@@ -1786,8 +1786,8 @@ int launch_tiles_fwd(const ma_attn_desc* d, const void* q, const void* k, const 
   if (reserve_lds(reinterpret_cast<const void*>(kf), shm, st)) return 1;
   launch(a.nsplit == 0, kf, dim3((unsigned)(bh * a.nitems)), dim3(256), (uint32_t)shm, st, a);
   if (a.nsplit > 0)
-    launch(true, tile_combine_kernel<typename P::Elt, false>, dim3((unsigned)(bh * a.nsplit)), dim3(256), 0u, st,
-           a);
+    launch(true, tile_combine_kernel<typename P::Elt, false>, dim3((unsigned)(bh * a.nsplit * (64 / kMergeRows))),
+           dim3(256), 0u, st, a);
   return 0;
 }
 
@@ -1819,10 +1819,12 @@ int launch_tiles_bwd(const ma_attn_desc* d, const void* const* ptrs, void* ws, h
   // tiles compute their own statistics there)
   if (a.nsplit > 0) {
     launch(false, kf, dim3((unsigned)(bh * a.nitems)), dim3(256), (uint32_t)shm_f, st, a);
-    launch(false, tile_combine_kernel<Elt, true>, dim3((unsigned)(bh * a.nsplit)), dim3(256), 0u, st, a);
+    launch(false, tile_combine_kernel<Elt, true>, dim3((unsigned)(bh * a.nsplit * (64 / kMergeRows))), dim3(256), 0u,
+           st, a);
   }
   launch(false, kq, dim3((unsigned)(bh * a.nitems)), dim3(256), (uint32_t)shm_q, st, a);
-  if (a.nsplit > 0) launch(false, tile_sum_kernel<Elt, 64>, dim3((unsigned)(bh * a.nsplit)), dim3(256), 0u, st, a);
+  if (a.nsplit > 0)
+    launch(false, tile_sum_kernel<Elt, 64>, dim3((unsigned)(bh * a.nsplit * (64 / kMergeRows))), dim3(256), 0u, st, a);
   // dK, dV (key side)
   TileArgs b = tile_args(d, true);
   b.q = a.q;
@@ -1834,7 +1836,8 @@ int launch_tiles_bwd(const ma_attn_desc* d, const void* const* ptrs, void* ws, h
   b.stats = a.stats;
   b.part = a.part;
   launch(b.nsplit == 0, kkv, dim3((unsigned)(bh * b.nitems)), dim3(256), (uint32_t)shm_kv, st, b);
-  if (b.nsplit > 0) launch(true, tile_sum_kernel<Elt, 128>, dim3((unsigned)(bh * b.nsplit)), dim3(256), 0u, st, b);
+  if (b.nsplit > 0)
+    launch(true, tile_sum_kernel<Elt, 128>, dim3((unsigned)(bh * b.nsplit * (64 / kMergeRows))), dim3(256), 0u, st, b);
   return 0;
 }
 

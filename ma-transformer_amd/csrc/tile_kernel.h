@@ -39,7 +39,7 @@
 namespace ma_dev {
 
 constexpr int kTileFull = 1 << 30;   // entry flag: every pair of the 64x64 block is in the set
-constexpr int kTileSeg = 16;         // default entries per work item
+constexpr int kTileSeg = 16;        // default entries per work item
 constexpr int kTilePart = 68;        // floats per row of a forward partial: 64 O, log2 max, sum, 2 pad
 
 struct TileArgs {
@@ -314,53 +314,62 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void tile_fwd_kernel(TileArgs a
   }
 }
 
-// Merge of a split query tile's partials: thread (row tid/4, quarter tid%4)
-// owns head_dim 16*quarter .. +15 of query row 64t + tid/4.
+// Merge of a split query tile's partials.  Workgroup (split tile, 16-row
+// quarter of the tile); thread (row tid/16, column tid%16) owns head_dim
+// 4*column .. +3 of one row, so a tile's merge spreads over 4 workgroups of
+// independent, unrolled partial loads (the partials of one split tile are
+// read once).
+constexpr int kMergeRows = 16;  // rows per merge workgroup
 template <typename Elt, bool STATS>
 __global__ __launch_bounds__(256) void tile_combine_kernel(TileArgs a) {
-  const int s = blockIdx.x % a.nsplit;
-  const int bh = blockIdx.x / a.nsplit;
+  constexpr int kQuarters = 64 / kMergeRows;
+  const int rq = blockIdx.x % kQuarters;
+  const int s = (blockIdx.x / kQuarters) % a.nsplit;
+  const int bh = blockIdx.x / kQuarters / a.nsplit;
   const int h = bh % a.H, b = bh / a.H;
   const int t = clampi(a.split[4 * s], 0, a.ntiles - 1);
   const int first = clampi(a.split[4 * s + 1], 0, a.npart);
   const int cnt = clampi(a.split[4 * s + 2], 0, a.npart - first);
-  const int row = threadIdx.x >> 2, qd = threadIdx.x & 3;
+  const int row = kMergeRows * rq + (threadIdx.x >> 4), col = threadIdx.x & 15;
   const float* p0 = a.part + (((int64_t)bh * a.npart + first) * 64 + row) * kTilePart;
   constexpr int64_t kStride = 64 * kTilePart;
   float m = -INFINITY;
+#pragma unroll 8
   for (int k = 0; k < cnt; ++k) m = fmaxf(m, p0[k * kStride + 64]);
-  float l = 0.0f, o[16];
-#pragma unroll
-  for (int d = 0; d < 16; ++d) o[d] = 0.0f;
+  float l = 0.0f;
+  f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
   if (m != -INFINITY) {
+#pragma unroll 8
     for (int k = 0; k < cnt; ++k) {
       const float* src = p0 + k * kStride;
       const float w = __builtin_amdgcn_exp2f(src[64] - m);  // 0 for a partial that saw no key
       l = fmaf(src[65], w, l);
+      const f32x4 v = *reinterpret_cast<const f32x4*>(src + 4 * col);
 #pragma unroll
-      for (int d = 0; d < 16; d += 4) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(src + 16 * qd + d);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) o[d + j] = fmaf(v[j], w, o[d + j]);
-      }
+      for (int j = 0; j < 4; ++j) o[j] = fmaf(v[j], w, o[j]);
     }
   }
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
   const int64_t i = 64 * (int64_t)t + row;
-  if (i >= a.N) return;
-  const int64_t off = (((int64_t)b * a.N + i) * a.H + h) * kHeadDim + 16 * qd;
+  const int64_t off = (((int64_t)b * a.N + i) * a.H + h) * kHeadDim + 4 * col;
   if constexpr (!STATS) {
+    if (i >= a.N) return;
     Elt* dst = static_cast<Elt*>(a.o) + off;
 #pragma unroll
-    for (int d = 0; d < 16; ++d) dst[d] = static_cast<Elt>(o[d] * inv);
+    for (int j = 0; j < 4; ++j) dst[j] = static_cast<Elt>(o[j] * inv);
   } else {
-    const Elt* gsrc = static_cast<const Elt*>(a.dout) + off;
     float dlt = 0.0f;
+    if (i < a.N) {
+      const Elt* gsrc = static_cast<const Elt*>(a.dout) + off;
 #pragma unroll
-    for (int d = 0; d < 16; ++d) dlt = fmaf(static_cast<float>(gsrc[d]), o[d], dlt);
+      for (int j = 0; j < 4; ++j) dlt = fmaf(static_cast<float>(gsrc[j]), o[j], dlt);
+    }
+    // the row's 16 columns are 16 consecutive lanes
     dlt += __shfl_xor(dlt, 1, 64);
     dlt += __shfl_xor(dlt, 2, 64);
-    if (qd == 0)
+    dlt += __shfl_xor(dlt, 4, 64);
+    dlt += __shfl_xor(dlt, 8, 64);
+    if (col == 0 && i < a.N)
       *reinterpret_cast<float2*>(a.stats + 2 * (((int64_t)b * a.N + i) * a.H + h)) =
           make_float2(l > 0.0f ? m + __log2f(l) : 0.0f, dlt * inv);
   }
@@ -371,7 +380,8 @@ __global__ __launch_bounds__(256) void tile_combine_kernel(TileArgs a) {
 // An unsplit tile (one work item) computes its own statistics: pass 1 over
 // its entries gives {lse2, delta} (online max, sum of e and of e*dP, no O),
 // pass 2 dQ; with at most two entries both blocks stay resident in the two
-// buffers between the passes.  A split tile's items read the statistics the
+// buffers between the passes, and with more pass 2 runs backwards so that
+// it starts on the two blocks pass 1 ended with.  A split tile's items read the statistics the
 // merge of its partials wrote.  Every tile's statistics land in the
 // workspace for the dK/dV pass.
 
@@ -427,9 +437,12 @@ __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dq_kernel(TileAr
   const int ne = e1 - e0;
   const int nit = own ? 2 * ne : ne;
   const bool resident = own && ne <= 2;
-  auto entry_of = [&](int k) { return e0 + (own && k >= ne ? k - ne : k); };
-  auto buf_of = [&](int k) { return resident ? (k < ne ? k : k - ne) : (k & 1); };
-  auto loads = [&](int k) { return k < nit && (!resident || k < ne); };
+  // Streamed order (more than two entries): pass 2 walks the entries in
+  // reverse, so its first two blocks are still in the two buffers where
+  // pass 1 left them; every block sits in the buffer of its entry's parity.
+  auto entry_of = [&](int k) { return e0 + (own && k >= ne ? 2 * ne - 1 - k : k); };
+  auto buf_of = [&](int k) { return (entry_of(k) - e0) & 1; };
+  auto loads = [&](int k) { return k < nit && (!own || k < ne || k >= ne + 2); };
 
   f32x4 acc[4];
 #pragma unroll
@@ -703,41 +716,40 @@ __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dkv_kernel(TileA
   }
 }
 
-// Sum of a split tile's (or key block's) partial rows into the output(s):
-// thread (row tid/4, quarter tid%4) owns head_dim 16*quarter .. +15.
-// WIDTH 64: dQ (scaled); WIDTH 128: dK (scaled) then dV.
+// Sum of a split tile's (or key block's) partial rows into the output(s).
+// Workgroup (split tile, 16-row quarter); thread (row tid/16, column tid%16)
+// owns head_dim 4*column .. +3 of one row and loops over the partials with
+// unrolled, independent loads.  WIDTH 64: dQ (scaled); WIDTH 128: dK (scaled)
+// then dV.
 template <typename Elt, int WIDTH>
 __global__ __launch_bounds__(256) void tile_sum_kernel(TileArgs a) {
-  const int s = blockIdx.x % a.nsplit;
-  const int bh = blockIdx.x / a.nsplit;
+  constexpr int kQuarters = 64 / kMergeRows;
+  const int rq = blockIdx.x % kQuarters;
+  const int s = (blockIdx.x / kQuarters) % a.nsplit;
+  const int bh = blockIdx.x / kQuarters / a.nsplit;
   const int h = bh % a.H, b = bh / a.H;
   const int t = clampi(a.split[4 * s], 0, a.ntiles - 1);
   const int first = clampi(a.split[4 * s + 1], 0, a.npart);
   const int cnt = clampi(a.split[4 * s + 2], 0, a.npart - first);
-  const int row = threadIdx.x >> 2, qd = threadIdx.x & 3;
+  const int row = kMergeRows * rq + (threadIdx.x >> 4), col = threadIdx.x & 15;
   const int64_t i = 64 * (int64_t)t + row;
   if (i >= a.N) return;
-  const float* p0 = a.part + (((int64_t)bh * a.npart + first) * 64 + row) * WIDTH;
+  const float* p0 = a.part + (((int64_t)bh * a.npart + first) * 64 + row) * WIDTH + 4 * col;
   constexpr int64_t kStride = 64 * WIDTH;
-  const int64_t off = (((int64_t)b * a.N + i) * a.H + h) * kHeadDim + 16 * qd;
+  const int64_t off = (((int64_t)b * a.N + i) * a.H + h) * kHeadDim + 4 * col;
 #pragma unroll
   for (int part = 0; part < WIDTH / 64; ++part) {
-    float o[16];
-#pragma unroll
-    for (int d = 0; d < 16; ++d) o[d] = 0.0f;
+    f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 8
     for (int k = 0; k < cnt; ++k) {
-      const float* src = p0 + k * kStride + 64 * part + 16 * qd;
+      const f32x4 v = *reinterpret_cast<const f32x4*>(p0 + k * kStride + 64 * part);
 #pragma unroll
-      for (int d = 0; d < 16; d += 4) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(src + d);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) o[d + j] += v[j];
-      }
+      for (int j = 0; j < 4; ++j) o[j] += v[j];
     }
     const float sc = part == 0 ? a.scale : 1.0f;  // dQ and dK carry the softmax scale, dV not
     Elt* dst = static_cast<Elt*>(part == 0 ? (WIDTH == 64 ? a.o : a.dk) : a.dv) + off;
 #pragma unroll
-    for (int d = 0; d < 16; ++d) dst[d] = static_cast<Elt>(o[d] * sc);
+    for (int j = 0; j < 4; ++j) dst[j] = static_cast<Elt>(o[j] * sc);
   }
 }
 
