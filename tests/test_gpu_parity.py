@@ -415,3 +415,20 @@ def test_timed_entry_points(ext):
     torch.cuda.synchronize()
     assert all(torch.equal(a, b) for a, b in zip(got_g, ref_g))
     assert e0.elapsed_time(e1) > 0.0
+
+
+@pytest.mark.parametrize("shape", [(1, 0, 2, 64), (0, 37, 2, 64), (2, 0, 3, 16)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_empty_inputs(ext, shape, dtype):
+    """Empty batches or sequences launch nothing and return empty outputs of
+    the inputs' shape, forward and backward, on every entry point."""
+    q = torch.randn(shape, device="cuda").to(dtype)
+    for y in (ext.forward(q, q, q, 8), ext.dense_forward(q, q, q, True), ext.sliding_forward(q, q, q, 63, 0),
+              ext.longformer_forward(q, q, q, 127, 0, 16)):
+        assert y.shape == q.shape and y.dtype == dtype
+    for grads in (ext.backward(q, q, q, q, 8), ext.dense_backward(q, q, q, q, True),
+                  ext.sliding_backward(q, q, q, q, 32, 31)):
+        assert [tuple(g.shape) for g in grads] == [tuple(shape)] * 3
+    torch.cuda.synchronize()
+    y = ext.forward(*[torch.randn(1, 16, 1, 16, device="cuda")] * 3, 2)  # still usable afterwards
+    assert torch.isfinite(y).all()
