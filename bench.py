@@ -37,8 +37,14 @@ Workload "encoder_layer": the reference model's inference (batch 64, sequence
 against the same weights run as the layer's separate operations; value =
 sequences/s, with per-layer latencies of both forms.
 
+With --pass backward --saved-stats (block-sparse, Longformer and index-set
+workloads), the backward runs from the forward's saved O and per-row
+statistics (ma_attn_backward_saved), the form the autograd layer trains with;
+the forward runs once per input set before timing, and the algorithmic bytes
+count O and the statistics read as well.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
-                       [--pass forward|backward]
+                       [--pass forward|backward] [--saved-stats]
 """
 from __future__ import annotations
 
@@ -441,6 +447,9 @@ def main() -> int:
     ap.add_argument("--pass", dest="which", choices=["forward", "backward"], default="forward",
                     help="backward: dQ, dK, dV from (Q, K, V, dO) (block-sparse, Longformer and index "
                          "sets through index_set_backward over their key sets)")
+    ap.add_argument("--saved-stats", action="store_true",
+                    help="with --pass backward on block-sparse, Longformer and index sets: the backward from "
+                         "the forward's saved O and statistics (the forward runs once per input set, untimed)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -459,13 +468,19 @@ def main() -> int:
         return 1
     B, H, N, D, dt_name, pk, desc = WORKLOADS[args.workload]
     bwd = args.which == "backward"
+    saved = bwd and args.saved_stats
+    if args.saved_stats and (not bwd or pk["pattern"] in ("sliding", "dense")):
+        print("bench.py: --saved-stats applies to --pass backward on block_sparse, longformer and index_set "
+              "workloads", file=sys.stderr)
+        return 2
     dtype = {"bf16": torch.bfloat16, "fp32": torch.float32}[dt_name]
     elt = 2 if dt_name == "bf16" else 4
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
 
-    # tensors touched per step: Q, K, V, O (forward); Q, K, V, dO, dQ, dK, dV (backward)
-    tensors = 7 if bwd else 4
+    # tensors touched per step: Q, K, V, O (forward); Q, K, V, dO, dQ, dK, dV (backward; and O from
+    # saved statistics)
+    tensors = 8 if saved else (7 if bwd else 4)
     set_bytes = tensors * B * N * H * D * elt
     nsets = args.sets or max(4, -(-(1 << 30) // set_bytes))
     gen = torch.Generator(device=dev)
@@ -495,7 +510,20 @@ def main() -> int:
         else:
             iset = ext.pattern_index_set("longformer", N, dev, left=pk["left"], right=pk["right"],
                                          num_global=pk["num_global"])
-        launch = lambda s: ext.index_set_backward(s[0], s[1], s[2], s[3], iset)
+        if saved:
+            # each input set's forward output and statistics, as the layer's autograd keeps them
+            for n_, s_ in enumerate(sets):
+                if pk["pattern"] == "index_set":
+                    o_, l_ = ext.index_set_forward(s_[0], s_[1], s_[2], iset, return_lse=True)
+                elif pk["pattern"] == "block_sparse":
+                    o_, l_ = ext.block_sparse_forward(s_[0], s_[1], s_[2], table, pk["block_size"], return_lse=True)
+                else:
+                    o_, l_ = ext.longformer_forward(s_[0], s_[1], s_[2], pk["left"], pk["right"], pk["num_global"],
+                                                    return_lse=True)
+                sets[n_] = s_ + (o_, l_)
+            launch = lambda s: ext.index_set_backward(s[0], s[1], s[2], s[3], iset, out=s[4], lse=s[5])
+        else:
+            launch = lambda s: ext.index_set_backward(s[0], s[1], s[2], s[3], iset)
     elif pk["pattern"] == "sliding":
         launch = lambda s: ext.sliding_forward(s[0], s[1], s[2], pk["left"], pk["right"], pk.get("dilation", 1))
     elif pk["pattern"] == "block_sparse":
@@ -590,7 +618,7 @@ def main() -> int:
         del pout
 
     queries = B * H * N
-    alg_bytes = tensors * B * N * H * D * elt
+    alg_bytes = tensors * B * N * H * D * elt + (4 * B * N * H if saved else 0)  # + the statistics read
     set_source = None
     if pk["pattern"] == "index_set" or (bwd and pk["pattern"] not in ("sliding", "dense")):
         # plus the set's description, read once per pass: the tile plan the
@@ -605,7 +633,7 @@ def main() -> int:
     # forward: Q.K^T and P.V; backward: S, dP = dO.V^T, dV, dQ, dK (2 FLOP per MAC)
     flops = (10 if bwd else 4) * D * key_count(N, pk) * B * H
     achieved_gbps = alg_bytes / (mean_launch_ms * 1e-3) / 1e9
-    tkey = args.workload + ("_backward" if bwd else "")
+    tkey = args.workload + ("_backward_saved" if saved else ("_backward" if bwd else ""))
     traffic = load_traffic(tkey)
 
     copy_gbps = copy_bandwidth(dev, stream)
@@ -662,7 +690,7 @@ def main() -> int:
                                "kernel_frac_of_pattern_copy": probe_us / (mean_launch_ms * 1e3),
                                "source": probe_src}
     if bwd:
-        out["pass"] = "backward"
+        out["pass"] = "backward_saved_statistics" if saved else "backward"
     if not args.no_cpu_baseline and not bwd:
         out["cpu_baseline"] = cpu_baseline(B, H, N, D, dt_name, pk)
     print(json.dumps(out), flush=True)

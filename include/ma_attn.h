@@ -190,6 +190,40 @@ int ma_attn_backward_timed(const ma_attn_desc* desc, const void* q, const void* 
                            void* dv, void* workspace, size_t workspace_bytes,
                            void* stream, void* start_event, void* stop_event);
 
+/*
+ * Training pair with saved statistics.  No reference counterpart: the
+ * reference's backward recomputes every softmax from q, k, v
+ * (src/cuda/sparse_attention_kernel.cu:265-346, its autograd path
+ * src/layers/ma_core_bridge.py:116-154); a forward that also keeps each
+ * row's statistic lets the backward skip that.
+ *
+ * ma_attn_forward_lse: ma_attn_forward (same o, same workspace) that also
+ * writes lse[(b*N + i)*H + h] (float32, B*N*H entries): log2 of row i's
+ * softmax denominator sum_j 2^(scale*log2(e)*q_i.k_j) (0 for a row with no
+ * key).  Taken by the kernels that produce it at head_dim 64: BLOCK_SPARSE
+ * (block size 64) and DENSE on the block-row kernel, LONGFORMER in 16 bits,
+ * INDEX_SET with a tile plan; otherwise non-zero with an error.
+ *
+ * ma_attn_backward_saved: the gradients of ma_attn_backward from the
+ * forward's o and lse (delta_i = dout_i . o_i), for an INDEX_SET with a tile
+ * plan, which may hold the key sets of a BLOCK_SPARSE or LONGFORMER forward
+ * (ma_attn_pattern_csr enumerates them).  Workspace:
+ * ma_attn_backward_workspace_size(desc).  The _timed form stamps its kernels
+ * as ma_attn_backward_timed does.
+ */
+int ma_attn_forward_lse(const ma_attn_desc* desc, const void* q, const void* k,
+                        const void* v, void* o, float* lse, void* workspace,
+                        size_t workspace_bytes, void* stream);
+int ma_attn_backward_saved(const ma_attn_desc* desc, const void* q, const void* k,
+                           const void* v, const void* o, const float* lse,
+                           const void* dout, void* dq, void* dk, void* dv,
+                           void* workspace, size_t workspace_bytes, void* stream);
+int ma_attn_backward_saved_timed(const ma_attn_desc* desc, const void* q, const void* k,
+                                 const void* v, const void* o, const float* lse,
+                                 const void* dout, void* dq, void* dk, void* dv,
+                                 void* workspace, size_t workspace_bytes, void* stream,
+                                 void* start_event, void* stop_event);
+
 /* Validates desc without launching; 0 when ma_attn_forward would accept it.
  * Mirrors the checks of sparse_attention_kernel.cu:427-432. */
 int ma_attn_validate(const ma_attn_desc* desc);
@@ -295,7 +329,7 @@ int ma_attn_copy_probe_timed(const ma_attn_desc* desc, const void* q, const void
 /* ABI version of this header (bumped on incompatible change). */
 int ma_attn_abi_version(void);
 
-#define MA_ATTN_ABI_VERSION 8
+#define MA_ATTN_ABI_VERSION 9
 
 #ifdef __cplusplus
 }

@@ -35,6 +35,7 @@ struct BlockArgs {
   int32_t N, H, bpr, nbq;
   float scale_log2;
   int32_t causal;  // with a null table: keys [0, i]
+  float* lse;      // optional: each query row's softmax statistic (store_lse), [B*N*H]
 };
 
 // Workgroups are dispatched round-robin over the 8 XCDs, each with its own
@@ -229,6 +230,7 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void block_row_kernel(BlockArgs
       }
       const float l_tot = col_sum(l_run);
       P::store_o(acc, l_tot > 0.0f ? __builtin_amdgcn_rcpf(l_tot) : 0.0f, Or, qrow, g);
+      store_lse(a.lse, ((int64_t)b * N + 64 * r + ql) * a.H + h, 64 * r + ql < N, m_run, l_tot, sl2, g);
       return;
     }
   }
@@ -251,6 +253,7 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void block_row_kernel(BlockArgs
   }
   const float l_tot = col_sum(l_run);
   P::store_o(acc, l_tot > 0.0f ? __builtin_amdgcn_rcpf(l_tot) : 0.0f, Or, qrow, g);
+  store_lse(a.lse, ((int64_t)b * N + 64 * r + ql) * a.H + h, 64 * r + ql < N, m_run, l_tot, sl2, g);
 }
 
 // ---------------------------------------------------------------- copy probe

@@ -1406,12 +1406,12 @@ int launch_stream_half(const ma_attn_desc* d, const StreamArgs& a, const StreamP
   if (rc) return rc;
   launch(true, longformer_combine<T>, dim3((unsigned)(d->batch * d->num_heads * p.geom.G)), dim3(256), 0, st,
                      a.partials, static_cast<T*>(a.o), (int)p.chunks, (int)p.geom.G, (int)d->num_heads,
-                     d->seq_len);
+                     d->seq_len, a.lse);
   return 0;
 }
 
-int launch_stream(const ma_attn_desc* d, const void* q, const void* k, const void* v, void* o, void* ws,
-                  size_t ws_bytes, hipStream_t st) {
+int launch_stream(const ma_attn_desc* d, const void* q, const void* k, const void* v, void* o, float* lse,
+                  void* ws, size_t ws_bytes, hipStream_t st) {
   const StreamPlan p = stream_plan(d);
   if ((int64_t)ws_bytes < p.partial_bytes || (p.partial_bytes > 0 && !ws))
     return fail("ma_attn: workspace of %lld bytes required (ma_attn_workspace_size), got %zu",
@@ -1433,6 +1433,7 @@ int launch_stream(const ma_attn_desc* d, const void* q, const void* k, const voi
   a.scale_log2 = scale_of(d) * 1.4426950408889634f;
   a.num_global = (int32_t)p.geom.G;
   a.partials = static_cast<float*>(ws);
+  a.lse = lse;  // Longformer only (forward_launch refuses it elsewhere)
   // Chunk pairs on one XCD (neighbours' shared halo block read at the same
   // moment into one L2): measured faster with a right halo (cfg2 bf16 37.5 ->
   // 36.8 us) and for Longformer (cfg4 184 -> 179 us); neutral on causal
@@ -1465,8 +1466,10 @@ int launch_block_t(const BlockArgs& a, int64_t bh, hipStream_t st) {
   return 0;
 }
 
-int launch_block(const ma_attn_desc* d, const void* q, const void* k, const void* v, void* o, hipStream_t st) {
+int launch_block(const ma_attn_desc* d, const void* q, const void* k, const void* v, void* o, float* lse,
+                 hipStream_t st) {
   BlockArgs a;
+  a.lse = lse;
   a.q = q;
   a.k = k;
   a.v = v;
@@ -1705,7 +1708,7 @@ int scratch_of_stream(hipStream_t st, void** out) {
   return 0;
 }
 
-int forward_launch(const ma_attn_desc* desc, const void* q, const void* k, const void* v, void* o,
+int forward_launch(const ma_attn_desc* desc, const void* q, const void* k, const void* v, void* o, float* lse,
                    void* workspace, size_t workspace_bytes, hipStream_t st);
 
 // ------------------------------------------------------------------ tiled index sets
@@ -1766,8 +1769,8 @@ TileArgs tile_args(const ma_attn_desc* d, bool kside) {
 }
 
 template <class P>
-int launch_tiles_fwd(const ma_attn_desc* d, const void* q, const void* k, const void* v, void* o, void* ws,
-                     size_t ws_bytes, hipStream_t st) {
+int launch_tiles_fwd(const ma_attn_desc* d, const void* q, const void* k, const void* v, void* o, float* lse,
+                     void* ws, size_t ws_bytes, hipStream_t st) {
   const int64_t need = tiles_fwd_part_bytes(d);
   if ((int64_t)ws_bytes < need || (need > 0 && !ws))
     return fail("ma_attn: workspace of %lld bytes required (ma_attn_workspace_size), got %zu", (long long)need,
@@ -1777,6 +1780,7 @@ int launch_tiles_fwd(const ma_attn_desc* d, const void* q, const void* k, const 
   a.k = k;
   a.v = v;
   a.o = o;
+  a.lse = lse;
   a.part = static_cast<float*>(ws);
   const int64_t bh = d->batch * d->num_heads;
   const size_t shm = 2 * (size_t)P::kBlk;
@@ -1791,9 +1795,14 @@ int launch_tiles_fwd(const ma_attn_desc* d, const void* q, const void* k, const 
   return 0;
 }
 
+// fo, lse: the forward's O and statistics (ma_attn_backward_saved), or null:
+// then the statistics are recomputed.
 template <class P>
-int launch_tiles_bwd(const ma_attn_desc* d, const void* const* ptrs, void* ws, hipStream_t st) {
+int launch_tiles_bwd(const ma_attn_desc* d, const void* const* ptrs, void* ws, hipStream_t st, const void* fo,
+                     const float* lse) {
   TileArgs a = tile_args(d, false);
+  a.fo = fo;
+  a.lse = const_cast<float*>(lse);
   a.q = ptrs[0];
   a.k = ptrs[1];
   a.v = ptrs[2];
@@ -1807,7 +1816,9 @@ int launch_tiles_bwd(const ma_attn_desc* d, const void* const* ptrs, void* ws, h
   using Elt = typename P::Elt;
   const bool masked = d->tile_header->num_masked != 0;
   auto kf = masked ? &tile_fwd_kernel<P, true, true> : &tile_fwd_kernel<P, true, false>;
-  auto kq = masked ? &tile_dq_kernel<P, true> : &tile_dq_kernel<P, false>;
+  const bool saved = lse != nullptr;
+  auto kq = saved ? (masked ? &tile_dq_kernel<P, true, true> : &tile_dq_kernel<P, false, true>)
+                  : (masked ? &tile_dq_kernel<P, true, false> : &tile_dq_kernel<P, false, false>);
   auto kkv = masked ? &tile_dkv_kernel<P, true> : &tile_dkv_kernel<P, false>;
   const size_t shm_f = 2 * (size_t)P::kBlk, shm_q = 2 * (size_t)PairLds<P>::kBytes,
                shm_kv = 2 * ((size_t)PairLds<P>::kBytes + 512);
@@ -1816,8 +1827,9 @@ int launch_tiles_bwd(const ma_attn_desc* d, const void* const* ptrs, void* ws, h
       reserve_lds(reinterpret_cast<const void*>(kkv), shm_kv, st))
     return 1;
   // split tiles: statistics from partials and their merge; then dQ (unsplit
-  // tiles compute their own statistics there)
-  if (a.nsplit > 0) {
+  // tiles compute their own statistics there).  From saved statistics every
+  // tile takes them in the dQ pass.
+  if (a.nsplit > 0 && !saved) {
     launch(false, kf, dim3((unsigned)(bh * a.nitems)), dim3(256), (uint32_t)shm_f, st, a);
     launch(false, tile_combine_kernel<Elt, true>, dim3((unsigned)(bh * a.nsplit * (64 / kMergeRows))), dim3(256), 0u,
            st, a);
@@ -1882,7 +1894,17 @@ int ma_attn_forward(const ma_attn_desc* desc, const void* q, const void* k, cons
   const int64_t rows = desc->batch * desc->seq_len * desc->num_heads;
   if (rows == 0 || desc->head_dim == 0) return 0;
   if (!q || !k || !v || !o) return fail("ma_attn: null tensor pointer");
-  return forward_launch(desc, q, k, v, o, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+  return forward_launch(desc, q, k, v, o, nullptr, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int ma_attn_forward_lse(const ma_attn_desc* desc, const void* q, const void* k, const void* v, void* o,
+                        float* lse, void* workspace, size_t workspace_bytes, void* stream) {
+  g_last_error.clear();
+  if (validate(desc)) return 1;
+  const int64_t rows = desc->batch * desc->seq_len * desc->num_heads;
+  if (rows == 0 || desc->head_dim == 0) return 0;
+  if (!q || !k || !v || !o || !lse) return fail("ma_attn_forward_lse: null tensor pointer");
+  return forward_launch(desc, q, k, v, o, lse, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 int ma_attn_forward_noalloc(const ma_attn_desc* desc, const void* q, const void* k, const void* v, void* o,
@@ -1906,36 +1928,45 @@ int ma_attn_forward_noalloc(const ma_attn_desc* desc, const void* q, const void*
   hipStream_t st = static_cast<hipStream_t>(stream);
   void* ws = nullptr;
   if (need > 0 && scratch_of_stream(st, &ws)) return 1;
-  return forward_launch(desc, q, k, v, o, ws, need, st);
+  return forward_launch(desc, q, k, v, o, nullptr, ws, need, st);
 }
 
 }  // extern "C"
 
 namespace {
 
-int forward_launch(const ma_attn_desc* desc, const void* q, const void* k, const void* v, void* o,
+// lse: optional per-row softmax statistics (ma_attn_forward_lse), written by
+// the block-row, tiled and 16-bit Longformer stream kernels; other kernels
+// refuse it.
+int forward_launch(const ma_attn_desc* desc, const void* q, const void* k, const void* v, void* o, float* lse,
                    void* workspace, size_t workspace_bytes, hipStream_t st) {
   (void)hipGetLastError();  // launch errors below must be ours
   const void* const qkvo[4] = {q, k, v, o};
   int rc;
   const bool want_rows = g_opt.force_rows;
   const bool want_band = g_opt.force_band;
-  if (!want_rows && !want_band && stream_applies(desc, q, k, v, o)) {
-    rc = launch_stream(desc, q, k, v, o, workspace, workspace_bytes, st);
-  } else if (!want_rows && block_applies(desc, q, k, v, o)) {
-    rc = launch_block(desc, q, k, v, o, st);
+  const bool stream = !want_rows && !want_band && stream_applies(desc, q, k, v, o);
+  const bool block = !stream && !want_rows && block_applies(desc, q, k, v, o);
+  if (lse && !block && !tiles_apply(desc, qkvo, 4) &&
+      !(stream && desc->pattern == MA_ATTN_LONGFORMER && desc->num_global > 0))
+    return fail("ma_attn_forward_lse: these kernels write no statistics (block-sparse, dense, Longformer in "
+                "16 bits and index sets with a tile plan do, at head_dim 64)");
+  if (stream) {
+    rc = launch_stream(desc, q, k, v, o, lse, workspace, workspace_bytes, st);
+  } else if (block) {
+    rc = launch_block(desc, q, k, v, o, lse, st);
   } else if (!want_rows && band_applies(desc, q, k, v, o)) {
     rc = launch_band(desc, q, k, v, o, st);
   } else if (tiles_apply(desc, qkvo, 4)) {
     switch (desc->dtype) {
       case MA_ATTN_F32:
-        rc = launch_tiles_fwd<F32Path>(desc, q, k, v, o, workspace, workspace_bytes, st);
+        rc = launch_tiles_fwd<F32Path>(desc, q, k, v, o, lse, workspace, workspace_bytes, st);
         break;
       case MA_ATTN_BF16:
-        rc = launch_tiles_fwd<HalfPath<__bf16>>(desc, q, k, v, o, workspace, workspace_bytes, st);
+        rc = launch_tiles_fwd<HalfPath<__bf16>>(desc, q, k, v, o, lse, workspace, workspace_bytes, st);
         break;
       default:
-        rc = launch_tiles_fwd<HalfPath<_Float16>>(desc, q, k, v, o, workspace, workspace_bytes, st);
+        rc = launch_tiles_fwd<HalfPath<_Float16>>(desc, q, k, v, o, lse, workspace, workspace_bytes, st);
         break;
     }
   } else if (!want_rows && gather_applies(desc, q, k, v, o)) {
@@ -2020,9 +2051,10 @@ int ma_attn_backward(const ma_attn_desc* desc, const void* q, const void* k, con
     const size_t need_t = (size_t)(stats_bytes(desc) + tiles_bwd_part_bytes(desc));
     if (workspace_bytes < need_t)
       return fail("ma_attn_backward: workspace of %zu bytes needed, %zu given", need_t, workspace_bytes);
-    rc = desc->dtype == MA_ATTN_BF16  ? launch_tiles_bwd<HalfPath<__bf16>>(desc, ptrs, workspace, st)
-         : desc->dtype == MA_ATTN_F16 ? launch_tiles_bwd<HalfPath<_Float16>>(desc, ptrs, workspace, st)
-                                      : launch_tiles_bwd<F32BwdPath>(desc, ptrs, workspace, st);
+    rc = desc->dtype == MA_ATTN_BF16 ? launch_tiles_bwd<HalfPath<__bf16>>(desc, ptrs, workspace, st, nullptr, nullptr)
+         : desc->dtype == MA_ATTN_F16
+             ? launch_tiles_bwd<HalfPath<_Float16>>(desc, ptrs, workspace, st, nullptr, nullptr)
+             : launch_tiles_bwd<F32BwdPath>(desc, ptrs, workspace, st, nullptr, nullptr);
     if (rc) return rc;
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail("ma_attn_backward: kernel launch failed: %s", hipGetErrorString(e));
@@ -2061,6 +2093,45 @@ int ma_attn_forward_timed(const ma_attn_desc* desc, const void* q, const void* k
   g_ev_start = static_cast<hipEvent_t>(start_event);
   g_ev_stop = static_cast<hipEvent_t>(stop_event);
   const int rc = ma_attn_forward(desc, q, k, v, o, workspace, workspace_bytes, stream);
+  g_ev_start = g_ev_stop = nullptr;
+  return rc;
+}
+
+int ma_attn_backward_saved(const ma_attn_desc* desc, const void* q, const void* k, const void* v, const void* o,
+                           const float* lse, const void* dout, void* dq, void* dk, void* dv, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  g_last_error.clear();
+  if (validate(desc)) return 1;
+  const int64_t rows = desc->batch * desc->seq_len * desc->num_heads;
+  if (rows == 0 || desc->head_dim == 0) return 0;
+  if (!q || !k || !v || !o || !lse || !dout || !dq || !dk || !dv)
+    return fail("ma_attn_backward_saved: null tensor pointer");
+  const void* ptrs[8] = {q, k, v, dout, dq, dk, dv, o};
+  if (!tiles_apply(desc, ptrs, 8))
+    return fail("ma_attn_backward_saved: takes an INDEX_SET with a tile plan, head_dim 64, 16-byte aligned tensors");
+  const size_t need = (size_t)(stats_bytes(desc) + tiles_bwd_part_bytes(desc));
+  if (!workspace || workspace_bytes < need)
+    return fail("ma_attn_backward_saved: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  (void)hipGetLastError();
+  const int rc = desc->dtype == MA_ATTN_BF16 ? launch_tiles_bwd<HalfPath<__bf16>>(desc, ptrs, workspace, st, o, lse)
+                 : desc->dtype == MA_ATTN_F16
+                     ? launch_tiles_bwd<HalfPath<_Float16>>(desc, ptrs, workspace, st, o, lse)
+                     : launch_tiles_bwd<F32BwdPath>(desc, ptrs, workspace, st, o, lse);
+  if (rc) return rc;
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail("ma_attn_backward_saved: kernel launch failed: %s", hipGetErrorString(e));
+  return 0;
+}
+
+int ma_attn_backward_saved_timed(const ma_attn_desc* desc, const void* q, const void* k, const void* v,
+                                 const void* o, const float* lse, const void* dout, void* dq, void* dk, void* dv,
+                                 void* workspace, size_t workspace_bytes, void* stream, void* start_event,
+                                 void* stop_event) {
+  g_ev_start = static_cast<hipEvent_t>(start_event);
+  g_ev_stop = static_cast<hipEvent_t>(stop_event);
+  const int rc =
+      ma_attn_backward_saved(desc, q, k, v, o, lse, dout, dq, dk, dv, workspace, workspace_bytes, stream);
   g_ev_start = g_ev_stop = nullptr;
   return rc;
 }

@@ -45,12 +45,22 @@ struct StreamArgs {
   float scale_log2;   // softmax scale * log2(e)
   int32_t num_global;  // Longformer: global tokens 0..G-1 (G <= 16)
   float* partials;     // Longformer: [B*H][chunks][16][kPartial] per-chunk softmax partials of the global rows
+  float* lse;          // Longformer, optional: each query row's softmax statistic (store_lse), [B*N*H]
   int32_t pairs;       // 1: chunks 2p and 2p+1 share an XCD (grid a multiple of 16, chunks even)
 };
 
 // One partial of a global query row: unnormalised O (64), running max of the
 // log2-scaled scores, and the softmax denominator.
 constexpr int kPartial = kHeadDim + 2;
+
+// A query row's softmax statistic for a backward from saved statistics:
+// log2 of its softmax denominator sum_j 2^(s_j * sl2) over the raw scores
+// s_j, i.e. m * sl2 + log2(l) for the running max m and the sum l taken
+// against it (0 for a row with no key).  One lane group (g == 0) writes it.
+__device__ __forceinline__ void store_lse(float* lse, int64_t row, bool valid, float m_raw, float l_tot, float sl2,
+                                          int g) {
+  if (lse && g == 0 && valid) lse[row] = l_tot > 0.0f ? m_raw * sl2 + __log2f(l_tot) : 0.0f;
+}
 
 // ---------------------------------------------------------------- 16-bit path
 //
@@ -419,8 +429,11 @@ __device__ __forceinline__ uint32_t ring_slot_bytes(int s) {
 // across groups of SG sub-tiles), P.V on MFMA, one store per O row.  Used for
 // tiles at the sequence edges and for windows without a fixed instantiation.
 // Rows >= Nr compute on zero Q rows and their stores fall outside the buffer.
+// Both tile forms return the lane's query row's softmax statistic (log2 of its
+// denominator in units of the scaled scores), which only the Longformer
+// instantiation stores.
 template <class P, int NSLOT, int SG, bool LG>
-__device__ __forceinline__ void stream_tile(const uint8_t* ring, uint32_t kl, uint32_t vl, const typename P::Q& q,
+__device__ __forceinline__ float stream_tile(const uint8_t* ring, uint32_t kl, uint32_t vl, const typename P::Q& q,
                                             int qa, int Nr, int L, int R, float sl2, __amdgpu_buffer_rsrc_t Or,
                                             uint32_t orow, int g, int dl, int G) {
   constexpr int kSubs = P::kRows / 16;
@@ -500,6 +513,7 @@ __device__ __forceinline__ void stream_tile(const uint8_t* ring, uint32_t kl, ui
   }
   const float l_tot = col_sum(l_run);
   P::store_o(acc, l_tot > 0.0f ? __builtin_amdgcn_rcpf(l_tot) : 0.0f, Or, orow, g);
+  return l_tot > 0.0f ? m_run * sl2 + __log2f(l_tot) : 0.0f;
 }
 
 // Compile-time geometry of a fixed window [i-L, i+R]: a wave's 16 queries at
@@ -518,7 +532,7 @@ struct WinGeom {
 // tile's slot rotation), the per-lane mask compares are loop-invariant, and
 // the softmax is two-pass.
 template <class P, int L, int R, bool LG>
-__device__ __forceinline__ void window_tile(const uint8_t* ring, uint32_t kl, uint32_t vl, const typename P::Q& q,
+__device__ __forceinline__ float window_tile(const uint8_t* ring, uint32_t kl, uint32_t vl, const typename P::Q& q,
                                             int t, int wv, float sl2, __amdgpu_buffer_rsrc_t Or, uint32_t orow,
                                             int g, int dl, int ng) {
   using G = WinGeom<L, R, P::kRows>;
@@ -577,7 +591,7 @@ __device__ __forceinline__ void window_tile(const uint8_t* ring, uint32_t kl, ui
     }
     const float l_tot = col_sum(l_run);
     P::store_o(acc, __builtin_amdgcn_rcpf(l_tot), Or, orow, g);
-    return;
+    return m_use + __log2f(l_tot);
   }
   f32x4 zg = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   float mx = -INFINITY;
@@ -633,6 +647,7 @@ __device__ __forceinline__ void window_tile(const uint8_t* ring, uint32_t kl, ui
   }
   const float l_tot = col_sum(l_run);
   P::store_o(acc, __builtin_amdgcn_rcpf(l_tot), Or, orow, g);
+  return m_use + __log2f(l_tot);
 }
 
 // ---------------------------------------------------------------- kernel
@@ -783,11 +798,16 @@ __global__ __launch_bounds__(256, LG ? 2 : P::kMinBlocks) void stream_kernel(Str
     }
 
     const uint32_t orow = row_off(t * 64) + q_lane;
+    float lse2;
     if (kFixed && t >= t_int_lo && t < t_int_hi)
-      window_tile<P, FLc, FRc, LG>(ring, kl, vl, qc, t, wv, a.scale_log2, Or, orow, g, dl, G);
+      lse2 = window_tile<P, FLc, FRc, LG>(ring, kl, vl, qc, t, wv, a.scale_log2, Or, orow, g, dl, G);
     else
-      stream_tile<P, NSLOT, SG, LG>(ring, kl, vl, qc, t * 64 + 16 * wv, Nr, L, R, a.scale_log2, Or, orow, g, dl,
-                                    G);
+      lse2 = stream_tile<P, NSLOT, SG, LG>(ring, kl, vl, qc, t * 64 + 16 * wv, Nr, L, R, a.scale_log2, Or, orow,
+                                           g, dl, G);
+    if constexpr (LG) {  // dilation 1: query m is token m (rows 0..G-1 are rewritten by the combine)
+      const int m = t * 64 + 16 * wv + c;
+      if (a.lse && g == 0 && m < Nr) a.lse[((int64_t)b * a.N + m) * a.H + h] = lse2;
+    }
     if (LG) {  // global query rows against keys 64t + 16wv .. +15 (in the ring at tile t)
       const int key0 = t * 64 + 16 * wv;
       constexpr int kSubs = RS / 16;
@@ -879,7 +899,7 @@ __global__ __launch_bounds__(256, LG ? 2 : P::kMinBlocks) void stream_kernel(Str
 // out one load round trip per partial: 42 us at cfg 4.)
 template <typename Elt>
 __global__ __launch_bounds__(256) void longformer_combine(const float* __restrict__ partials, Elt* __restrict__ o,
-                                                          int nparts, int G, int H, int64_t N) {
+                                                          int nparts, int G, int H, int64_t N, float* lse) {
   __shared__ float sh[4][kPartial];
   const int d = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
@@ -923,6 +943,8 @@ __global__ __launch_bounds__(256) void longformer_combine(const float* __restric
       }
     }
     o[(((int64_t)b * N + gq) * H + h) * kHeadDim + d] = static_cast<Elt>(lt > 0.0f ? at / lt : 0.0f);
+    // the global row's statistic (mt is in log2 units of the scaled scores)
+    if (lse && d == 0) lse[((int64_t)b * N + gq) * H + h] = lt > 0.0f ? mt + __log2f(lt) : 0.0f;
   }
 }
 

@@ -59,6 +59,9 @@ struct TileArgs {
   const int32_t* split;   // [nsplit][4]
   float* stats;           // [B*N*H][2] {lse2, delta}
   float* part;            // [B*H][npart][...] partial results of split items
+  float* lse;             // forward: optional output of each row's statistic (store_lse); backward from
+                          // saved statistics: the forward's, read
+  const void* fo;         // backward from saved statistics: the forward's O (delta = dO . O)
   int32_t N, H, nitems, nsplit, npart;
   int32_t nent, ntiles;  // plan sizes: every index read from the plan is clamped to them
   float scale, scale_log2;
@@ -104,6 +107,37 @@ __device__ __forceinline__ int live_subtiles(uint64_t mw, bool full) {
   for (int u = 0; u < 4; ++u)
     live |= (__builtin_amdgcn_ballot_w64(((mw >> (16 * u)) & 0xFFFFull) != 0) != 0 ? 1 : 0) << u;
   return live;
+}
+
+// dot(x, y) of one row over the head_dim values this lane holds, both in the
+// Q register layout of P (their sum over the row's four lane groups is the
+// row's dot product).
+template <class P>
+__device__ __forceinline__ float q_dot(const typename P::Q& x, const typename P::Q& y) {
+  float d = 0.0f;
+  if constexpr (P::kSPB == 1) {
+    using T = typename P::Elt;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t wx[4] = {x.r[h].x, x.r[h].y, x.r[h].z, x.r[h].w};
+      const uint32_t wy[4] = {y.r[h].x, y.r[h].y, y.r[h].z, y.r[h].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        d = fmaf(static_cast<float>(__builtin_bit_cast(T, (uint16_t)(wx[j] & 0xffffu))),
+                 static_cast<float>(__builtin_bit_cast(T, (uint16_t)(wy[j] & 0xffffu))), d);
+        d = fmaf(static_cast<float>(__builtin_bit_cast(T, (uint16_t)(wx[j] >> 16))),
+                 static_cast<float>(__builtin_bit_cast(T, (uint16_t)(wy[j] >> 16))), d);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 xv = __builtin_bit_cast(f32x4, x.r[j]), yv = __builtin_bit_cast(f32x4, y.r[j]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) d = fmaf(xv[r], yv[r], d);
+    }
+  }
+  return d;
 }
 
 // Compile-time "every sub-tile live": a full entry's products issue back to
@@ -296,6 +330,8 @@ __global__ __launch_bounds__(256, P::kMinBlocks) void tile_fwd_kernel(TileArgs a
     if constexpr (!STATS) {
       const __amdgpu_buffer_rsrc_t Or = make_rsrc(static_cast<Elt*>(a.o) + x.base, x.nrec);
       P::store_o(acc, inv, Or, qrow, g);
+      const int64_t i = 64 * (int64_t)t + ql;
+      store_lse(a.lse, ((int64_t)x.b * a.N + i) * a.H + x.h, i < a.N, m_run, l_tot, sl2, g);
     } else {
       // delta = dout . O of the row (O in fp32 registers), lse2 in log2 units
       const __amdgpu_buffer_rsrc_t Gr = make_rsrc(static_cast<const Elt*>(a.dout) + x.base, x.nrec);
@@ -357,6 +393,8 @@ __global__ __launch_bounds__(256) void tile_combine_kernel(TileArgs a) {
     Elt* dst = static_cast<Elt*>(a.o) + off;
 #pragma unroll
     for (int j = 0; j < 4; ++j) dst[j] = static_cast<Elt>(o[j] * inv);
+    // m is already in log2 units of the scaled scores here
+    if (a.lse && col == 0) a.lse[((int64_t)b * a.N + i) * a.H + h] = l > 0.0f ? m + __log2f(l) : 0.0f;
   } else {
     float dlt = 0.0f;
     if (i < a.N) {
@@ -377,7 +415,9 @@ __global__ __launch_bounds__(256) void tile_combine_kernel(TileArgs a) {
 
 // ---------------------------------------------------------------- dQ
 //
-// An unsplit tile (one work item) computes its own statistics: pass 1 over
+// SAVED (a backward from the forward's saved statistics): every tile takes
+// lse2 from the forward and delta = dO . O of its rows, and runs pass 2 only.
+// Otherwise an unsplit tile (one work item) computes its own statistics: pass 1 over
 // its entries gives {lse2, delta} (online max, sum of e and of e*dP, no O),
 // pass 2 dQ; with at most two entries both blocks stay resident in the two
 // buffers between the passes, and with more pass 2 runs backwards so that
@@ -394,7 +434,7 @@ __device__ __forceinline__ void tile_stats(float m_run, float l_run, float a_run
   dlt = l_tot > 0.0f ? a_tot / l_tot : 0.0f;
 }
 
-template <class P, bool MASKED>
+template <class P, bool MASKED, bool SAVED>
 __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dq_kernel(TileArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 buffers x PairLds (K, V)
   using Elt = typename P::Elt;
@@ -424,9 +464,14 @@ __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dq_kernel(TileAr
   P::load_q(qr, Qr, qrow, g);
   P::load_q(gr, Gr, qrow, g);
   float* srow = a.stats + 2 * (((int64_t)x.b * a.N + i) * a.H + x.h);
-  const bool own = slot < 0;  // uniform: statistics from its own first pass
+  const bool own = !SAVED && slot < 0;  // uniform: statistics from its own first pass
   float lse2 = 0.0f, dlt = 0.0f;
-  if (!own && i < a.N) {
+  typename P::Q fo_row;  // SAVED: the row's O (delta = dO . O)
+  if constexpr (SAVED) {
+    const __amdgpu_buffer_rsrc_t Fr = make_rsrc(static_cast<const Elt*>(a.fo) + x.base, x.nrec);
+    P::load_q(fo_row, Fr, qrow, g);
+    if (i < a.N) lse2 = a.lse[((int64_t)x.b * a.N + i) * a.H + x.h];
+  } else if (!own && i < a.N) {
     const float2 st = *reinterpret_cast<const float2*>(srow);
     lse2 = st.x;
     dlt = st.y;
@@ -436,7 +481,7 @@ __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dq_kernel(TileAr
   // items: pass 1 (own statistics only) over the entries, then pass 2
   const int ne = e1 - e0;
   const int nit = own ? 2 * ne : ne;
-  const bool resident = own && ne <= 2;
+  const bool resident = ne <= 2;
   // Streamed order (more than two entries): pass 2 walks the entries in
   // reverse, so its first two blocks are still in the two buffers where
   // pass 1 left them; every block sits in the buffer of its entry's parity.
@@ -449,6 +494,16 @@ __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dq_kernel(TileAr
   for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   const float sl2 = a.scale_log2;
   float m_run = -INFINITY, l_run = 0.0f, a_run = 0.0f;
+
+  // SAVED: delta once the first blocks' loads are in flight (it waits on the
+  // O row's load), and both statistics for the dK/dV pass (every item of a
+  // split tile writes the same values).
+  auto saved_stats = [&]() __attribute__((always_inline)) {
+    if constexpr (SAVED) {
+      dlt = col_sum(q_dot<P>(gr, fo_row));
+      if (g == 0 && i < a.N) *reinterpret_cast<float2*>(srow) = make_float2(lse2, dlt);
+    }
+  };
 
   // Step k's products on the block in buffer sk: pass 1 (statistics) or
   // pass 2 (dQ) of its entry.
@@ -496,6 +551,7 @@ __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dq_kernel(TileAr
     kv_load<P>(xb, Kr, Vr, ne > 1 ? (uint32_t)(64 * (fb & (kTileFull - 1))) * tb : kOob, tid, tb);
     const uint64_t ma = a.mask[(int64_t)e0 * 64 + ql];
     const uint64_t mb = ne > 1 ? a.mask[(int64_t)(e0 + 1) * 64 + ql] : 0;
+    saved_stats();
     kv_store<P>(xa, ring, tid);
     if (ne > 1) kv_store<P>(xb, ring + kBuf, tid);
     __syncthreads();
@@ -512,6 +568,7 @@ __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dq_kernel(TileAr
     KvRegs<P> xk;
     kv_load<P>(xk, Kr, Vr, off_of(0, f0), tid, tb);
     uint64_t mw_next = a.mask[(int64_t)entry_of(0) * 64 + ql];
+    saved_stats();
     kv_store<P>(xk, ring, tid);
     __syncthreads();
     for (int k = 0; k < nit; ++k) {
@@ -530,6 +587,7 @@ __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dq_kernel(TileAr
       f1 = f2;
     }
   }
+  if (nit == 0) saved_stats();  // SAVED, a tile with no key: its statistics still go to the dK/dV pass
   if (own) {
     if (ne == 0) tile_stats(m_run, l_run, a_run, sl2, lse2, dlt);  // a tile with no key: zeros
     if (g == 0 && i < a.N) *reinterpret_cast<float2*>(srow) = make_float2(lse2, dlt);

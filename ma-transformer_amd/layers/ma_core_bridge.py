@@ -113,9 +113,39 @@ class PatternSpec:
         raise ValueError(f"unknown pattern {self.pattern}")
 
 
-def _native_forward(q, k, v, sparse, window_size, use_causal_mask, spec: Optional[PatternSpec]):
+def _pattern_set(spec: PatternSpec, seq_len: int, device):
+    """The explicit key sets the native backward of a block-sparse, Longformer
+    or index-set pattern runs on (pattern_index_set builds and caches them)."""
+    ext = sparse_attention_cuda
+    if spec.pattern == "index_set":
+        return spec.index_set
+    kw = (dict(block_table=spec.block_table, block_size=spec.block_size)
+          if spec.pattern == "block_sparse" else
+          dict(left=spec.left, right=spec.right, num_global=spec.num_global))
+    return ext.pattern_index_set(spec.pattern, seq_len, device, **kw)
+
+
+def _saved_statistics_pay(iset) -> bool:
+    """Whether the backward should run from the forward's saved statistics:
+    a tile plan whose query tiles average more than two entries.  There the
+    dQ pass would stream the tile's key blocks twice; on two-entry tiles both
+    blocks stay resident and reading O costs more than the statistics pass it
+    replaces (bench.py --saved-stats: cfg3 backward 152 -> 131 us, cfg4
+    548 -> 434 us, the target's sets 188 -> 194 us)."""
+    h = getattr(iset, "tile_header", None)
+    return h is not None and int(h.num_entries) > 2 * int(h.num_q_items)
+
+
+def _native_forward(q, k, v, sparse, window_size, use_causal_mask, spec: Optional[PatternSpec],
+                    return_lse: bool = False):
     ext = sparse_attention_cuda
     cq, ck, cv = q.contiguous(), k.contiguous(), v.contiguous()
+    if return_lse:  # block-sparse, Longformer and index sets only
+        if spec.pattern == "block_sparse":
+            return ext.block_sparse_forward(cq, ck, cv, spec.block_table, spec.block_size, return_lse=True)
+        if spec.pattern == "longformer":
+            return ext.longformer_forward(cq, ck, cv, spec.left, spec.right, spec.num_global, return_lse=True)
+        return ext.index_set_forward(cq, ck, cv, spec.index_set, return_lse=True)
     if spec is None:
         if sparse:
             return ext.forward(cq, ck, cv, int(window_size))
@@ -146,10 +176,12 @@ def pytorch_pattern_attention(query, key, value, spec: PatternSpec) -> torch.Ten
 
 
 class MACoreAttentionFunction(torch.autograd.Function):
-    """Autograd function: native forward; native backward (HIP kernels that
-    recompute the softmax) for every pattern: sliding and dense on their own
-    kernels, index sets, block-sparse and Longformer on the index-set row
-    kernels (the latter two as their explicit key sets).
+    """Autograd function: native forward; native backward for every pattern:
+    sliding and dense on their own kernels (which recompute the softmax),
+    index sets, block-sparse and Longformer on the tiled index-set kernels
+    (the latter two as their explicit key sets).  When those sets' tiles
+    average more than two entries, the forward also keeps each row's softmax
+    statistic and the backward starts from it and the saved output.
 
     Reference: src/layers/ma_core_bridge.py:44-154.  The extra trailing
     argument ``spec`` (a PatternSpec or None) selects a non-reference pattern.
@@ -159,17 +191,32 @@ class MACoreAttentionFunction(torch.autograd.Function):
     def forward(ctx, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                 sparse: bool = False, window_size: int = 64,
                 use_causal_mask: bool = False, spec: Optional[PatternSpec] = None) -> torch.Tensor:
-        ctx.save_for_backward(query, key, value)
         ctx.sparse = sparse
         ctx.window_size = window_size
         ctx.use_causal_mask = use_causal_mask
         ctx.spec = spec
+        ctx.saved_set = None
         on_device = query.is_cuda or key.is_cuda or value.is_cuda
         if on_device:
             if not _HAS_SPARSE_CUDA:
                 raise RuntimeError("device tensors given but the native sparse-attention "
                                    "library (libma_attn.so) is not loaded")
+            if (any(ctx.needs_input_grad[:3]) and spec is not None
+                    and spec.pattern in ("block_sparse", "longformer", "index_set")):
+                iset = _pattern_set(spec, query.shape[1], query.device)
+                if _saved_statistics_pay(iset):
+                    try:
+                        out, lse = _native_forward(query, key, value, sparse, window_size, use_causal_mask, spec,
+                                                   return_lse=True)
+                    except RuntimeError:  # a kernel that writes no statistics takes this shape
+                        pass
+                    else:
+                        ctx.saved_set = iset
+                        ctx.save_for_backward(query, key, value, out, lse)
+                        return out
+            ctx.save_for_backward(query, key, value)
             return _native_forward(query, key, value, sparse, window_size, use_causal_mask, spec)
+        ctx.save_for_backward(query, key, value)
         if spec is not None:
             return pytorch_pattern_attention(query, key, value, spec)
         if sparse:
@@ -178,24 +225,23 @@ class MACoreAttentionFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_output: torch.Tensor) -> Tuple[Optional[torch.Tensor], ...]:
-        query, key, value = ctx.saved_tensors
+        query, key, value = ctx.saved_tensors[:3]
         spec = ctx.spec
         native = spec is None or spec.pattern in ("sliding", "dense", "index_set", "block_sparse", "longformer")
         if _HAS_SPARSE_CUDA and query.is_cuda and native:
             ext = sparse_attention_cuda
             cq, ck, cv, cgo = (t.contiguous() for t in (query, key, value, grad_output))
             cgo = cgo.to(cq.dtype)
-            if spec is not None and spec.pattern == "sliding":
+            if ctx.saved_set is not None:  # from the forward's output and statistics
+                out, lse = ctx.saved_tensors[3:]
+                dQ, dK, dV = ext.index_set_backward(cq, ck, cv, cgo, ctx.saved_set, out=out, lse=lse)
+            elif spec is not None and spec.pattern == "sliding":
                 dQ, dK, dV = ext.sliding_backward(cq, ck, cv, cgo, spec.left, spec.right, spec.dilation)
             elif spec is not None and spec.pattern == "index_set":
                 dQ, dK, dV = ext.index_set_backward(cq, ck, cv, cgo, spec.index_set)
             elif spec is not None and spec.pattern in ("block_sparse", "longformer"):
                 # the pattern's key sets as an explicit set (built once, cached)
-                kw = (dict(block_table=spec.block_table, block_size=spec.block_size)
-                      if spec.pattern == "block_sparse" else
-                      dict(left=spec.left, right=spec.right, num_global=spec.num_global))
-                iset = ext.pattern_index_set(spec.pattern, cq.shape[1], cq.device, **kw)
-                dQ, dK, dV = ext.index_set_backward(cq, ck, cv, cgo, iset)
+                dQ, dK, dV = ext.index_set_backward(cq, ck, cv, cgo, _pattern_set(spec, cq.shape[1], cq.device))
             elif spec is not None:
                 dQ, dK, dV = ext.dense_backward(cq, ck, cv, cgo, spec.causal)
             elif ctx.sparse:

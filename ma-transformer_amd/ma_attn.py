@@ -18,7 +18,7 @@ LIB_PATH = os.environ.get("MA_ATTN_LIB", os.path.join(_HERE, "libma_attn.so"))
 
 F32, BF16, F16 = 0, 1, 2
 SLIDING, DENSE, BLOCK_SPARSE, LONGFORMER, INDEX_SET = 0, 1, 2, 3, 4
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 
@@ -110,6 +110,15 @@ def _open():
         [ctypes.c_size_t] + [ctypes.c_void_p] * 3
     lib.ma_attn_backward_timed.restype = ctypes.c_int
     lib.ma_attn_backward_timed.argtypes = [ctypes.POINTER(Desc)] + [ctypes.c_void_p] * 8 + \
+        [ctypes.c_size_t] + [ctypes.c_void_p] * 3
+    lib.ma_attn_forward_lse.restype = ctypes.c_int
+    lib.ma_attn_forward_lse.argtypes = [ctypes.POINTER(Desc)] + [ctypes.c_void_p] * 6 + \
+        [ctypes.c_size_t, ctypes.c_void_p]
+    lib.ma_attn_backward_saved.restype = ctypes.c_int
+    lib.ma_attn_backward_saved.argtypes = [ctypes.POINTER(Desc)] + [ctypes.c_void_p] * 10 + \
+        [ctypes.c_size_t, ctypes.c_void_p]
+    lib.ma_attn_backward_saved_timed.restype = ctypes.c_int
+    lib.ma_attn_backward_saved_timed.argtypes = [ctypes.POINTER(Desc)] + [ctypes.c_void_p] * 10 + \
         [ctypes.c_size_t] + [ctypes.c_void_p] * 3
     lib.ma_attn_block_table.restype = ctypes.c_int
     lib.ma_attn_block_table.argtypes = [ctypes.c_uint64, ctypes.c_int64, ctypes.c_int64,
@@ -206,6 +215,32 @@ def backward_raw(desc: Desc, q_ptr: int, k_ptr: int, v_ptr: int, g_ptr: int, dq_
     else:
         rc = LIB.ma_attn_backward(ctypes.byref(desc), q_ptr, k_ptr, v_ptr, g_ptr, dq_ptr, dk_ptr, dv_ptr,
                                   ws_ptr or None, ws_bytes, stream or None)
+    if rc != 0:
+        raise RuntimeError(last_error())
+
+
+def forward_lse_raw(desc: Desc, q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, lse_ptr: int,
+                    ws_ptr: int = 0, ws_bytes: int = 0, stream: int = 0) -> None:
+    """ma_attn_forward_lse: the forward plus each row's softmax statistic
+    (float32 [B*N*H]) for backward_saved_raw.  Raises RuntimeError on rejection."""
+    rc = LIB.ma_attn_forward_lse(ctypes.byref(desc), q_ptr, k_ptr, v_ptr, o_ptr, lse_ptr, ws_ptr or None,
+                                 ws_bytes, stream or None)
+    if rc != 0:
+        raise RuntimeError(last_error())
+
+
+def backward_saved_raw(desc: Desc, q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, lse_ptr: int, g_ptr: int,
+                       dq_ptr: int, dk_ptr: int, dv_ptr: int, ws_ptr: int, ws_bytes: int, stream: int = 0,
+                       events=None) -> None:
+    """ma_attn_backward_saved: the backward from the forward's O and
+    statistics.  Raises RuntimeError on rejection."""
+    if events:
+        rc = LIB.ma_attn_backward_saved_timed(ctypes.byref(desc), q_ptr, k_ptr, v_ptr, o_ptr, lse_ptr, g_ptr,
+                                              dq_ptr, dk_ptr, dv_ptr, ws_ptr or None, ws_bytes, stream or None,
+                                              events[0] or None, events[1] or None)
+    else:
+        rc = LIB.ma_attn_backward_saved(ctypes.byref(desc), q_ptr, k_ptr, v_ptr, o_ptr, lse_ptr, g_ptr, dq_ptr,
+                                        dk_ptr, dv_ptr, ws_ptr or None, ws_bytes, stream or None)
     if rc != 0:
         raise RuntimeError(last_error())
 

@@ -129,12 +129,18 @@ def _on_device(dev: int, fn):
         return fn(torch.cuda.current_stream(dev).cuda_stream)
 
 
-def _launch(q, k, v, pattern, **kw) -> torch.Tensor:
+def _launch(q, k, v, pattern, return_lse: bool = False, **kw):
     _check(q, k, v)
     B, N, H, D = q.shape
     out = torch.empty_like(q)
     desc, nbytes = _desc_of(B, N, H, D, q.dtype, pattern, kw)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes else None
+    if return_lse:
+        lse = torch.empty((B, N, H), dtype=torch.float32, device=q.device)
+        _on_device(q.get_device(), lambda stream: _ma.forward_lse_raw(
+            desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+            ws.data_ptr() if ws is not None else 0, nbytes, stream))
+        return out, lse
     _on_device(q.get_device(), lambda stream: _ma.forward_raw(
         desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), ws.data_ptr() if ws is not None else 0,
         nbytes, stream, _events))
@@ -219,11 +225,14 @@ class BlockTable:
 
 
 def block_sparse_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
-                         block_table, block_size: int = 64) -> torch.Tensor:
+                         block_table, block_size: int = 64, return_lse: bool = False):
     """Query block r attends the key blocks listed in block_table[r] (ascending, -1 padded).
 
     block_table: an int tensor [ceil(S/block_size), width] (checked at every
     call), or a BlockTable made for this sequence length and block size.
+    return_lse: also return each row's softmax statistic (float32 [B, S, H],
+    ma_attn_forward_lse) for index_set_backward(..., out=, lse=); block size 64,
+    head_dim 64.
     """
     _check(query, key, value)
     B, N, H, D = query.shape
@@ -243,14 +252,15 @@ def block_sparse_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Te
         # memory only for later work on that same stream, i.e. after the
         # kernel read it.
         tab = _validated_table(block_table, nb).to(query.device)
-    return _launch(query, key, value, _ma.BLOCK_SPARSE, block_size=bs,
+    return _launch(query, key, value, _ma.BLOCK_SPARSE, return_lse, block_size=bs,
                    block_table_ptr=tab.data_ptr(), blocks_per_row=tab.shape[1])
 
 
 def longformer_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
-                       left: int, right: int = 0, num_global: int = 16) -> torch.Tensor:
-    """Rows i < G attend all keys; others attend [i-left, i+right] U [0, G)."""
-    return _launch(query, key, value, _ma.LONGFORMER, left=int(left), right=int(right),
+                       left: int, right: int = 0, num_global: int = 16, return_lse: bool = False):
+    """Rows i < G attend all keys; others attend [i-left, i+right] U [0, G).
+    return_lse as for block_sparse_forward (bf16/fp16, 1 <= G <= 16)."""
+    return _launch(query, key, value, _ma.LONGFORMER, return_lse, left=int(left), right=int(right),
                    num_global=int(num_global))
 
 
@@ -389,9 +399,10 @@ def pattern_index_set(pattern: str, seq_len: int, device, **kw) -> IndexSet:
 
 
 def index_set_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
-                      index_set) -> torch.Tensor:
+                      index_set, return_lse: bool = False):
     """Query i attends exactly the keys of row i of index_set (an IndexSet, or
-    an (offsets, keys) pair checked at every call).  Empty rows give zeros."""
+    an (offsets, keys) pair checked at every call).  Empty rows give zeros.
+    return_lse as for block_sparse_forward (a set with a tile plan)."""
     _check(query, key, value)
     B, N, H, D = query.shape
     if not isinstance(index_set, IndexSet):
@@ -401,15 +412,22 @@ def index_set_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tenso
         raise RuntimeError(f"IndexSet was made for S={index_set.seq_len}; called with S={N}")
     if index_set.offsets.device != query.device:
         raise RuntimeError("IndexSet is on another device than the inputs")
-    return _launch(query, key, value, _ma.INDEX_SET, index_offsets_ptr=index_set.offsets.data_ptr(),
+    return _launch(query, key, value, _ma.INDEX_SET, return_lse, index_offsets_ptr=index_set.offsets.data_ptr(),
                    index_keys_ptr=index_set.keys.data_ptr(), num_indices=index_set.num_indices,
                    **index_set._tile_kw())
 
 
-def index_set_backward(query, key, value, grad_out, index_set) -> List[torch.Tensor]:
-    """dQ, dK, dV of index_set_forward (gather kernels at head_dim 64, row
-    kernels otherwise; the reference's generic
-    COO path has no backward).  index_set as for index_set_forward."""
+def index_set_backward(query, key, value, grad_out, index_set, out=None, lse=None) -> List[torch.Tensor]:
+    """dQ, dK, dV of index_set_forward (tiled kernels with a tile plan, gather
+    kernels otherwise at head_dim 64, row kernels at other head_dims; the
+    reference's generic COO path has no backward).  index_set as for
+    index_set_forward.
+
+    out, lse: the forward's output and statistics (a forward with
+    return_lse=True over the same key sets: index_set_forward, or
+    block_sparse_forward / longformer_forward for their pattern_index_set).
+    With both, a set with a tile plan skips recomputing the softmax
+    statistics (ma_attn_backward_saved); without a plan they are ignored."""
     _check(query, key, value, grad_out)
     N = query.shape[1]
     if not isinstance(index_set, IndexSet):
@@ -419,13 +437,31 @@ def index_set_backward(query, key, value, grad_out, index_set) -> List[torch.Ten
         raise RuntimeError(f"IndexSet was made for S={index_set.seq_len}; called with S={N}")
     if index_set.offsets.device != query.device:
         raise RuntimeError("IndexSet is on another device than the inputs")
-    return _backward(query, key, value, grad_out, _ma.INDEX_SET,
-                     index_offsets_ptr=index_set.offsets.data_ptr(), index_keys_ptr=index_set.keys.data_ptr(),
-                     num_indices=index_set.num_indices, index_t_offsets_ptr=index_set.t_offsets.data_ptr(),
-                     index_t_queries_ptr=index_set.t_queries.data_ptr(), **index_set._tile_kw())
+    kw = dict(index_offsets_ptr=index_set.offsets.data_ptr(), index_keys_ptr=index_set.keys.data_ptr(),
+              num_indices=index_set.num_indices, index_t_offsets_ptr=index_set.t_offsets.data_ptr(),
+              index_t_queries_ptr=index_set.t_queries.data_ptr(), **index_set._tile_kw())
+    if out is not None and lse is not None and index_set.tile_plan is not None:
+        _check(query, out)
+        B, N, H, _ = query.shape
+        if not (isinstance(lse, torch.Tensor) and lse.dtype == torch.float32 and lse.is_contiguous()
+                and tuple(lse.shape) == (B, N, H) and lse.device == query.device):
+            raise RuntimeError(f"lse must be a contiguous float32 [{B}, {N}, {H}] tensor on the inputs' device")
+        return _backward_saved(query, key, value, out, lse, grad_out, _ma.INDEX_SET, **kw)
+    return _backward(query, key, value, grad_out, _ma.INDEX_SET, **kw)
 
 
 # ---------------------------------------------------------------- backward (HIP kernels)
+
+def _backward_saved(q, k, v, out, lse, grad_out, pattern, **kw) -> List[torch.Tensor]:
+    B, N, H, D = q.shape
+    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+    desc, nbytes = _desc_of(B, N, H, D, q.dtype, pattern, kw, backward=True)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    _on_device(q.get_device(), lambda stream: _ma.backward_saved_raw(
+        desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(), grad_out.data_ptr(),
+        dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), nbytes, stream, _events))
+    return [dq, dk, dv]
+
 
 def _backward(q, k, v, grad_out, pattern, **kw) -> List[torch.Tensor]:
     _check(q, k, v, grad_out)

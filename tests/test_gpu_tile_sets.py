@@ -137,3 +137,136 @@ def test_tiled_plan_for_another_length_rejected(ext):
     q = torch.randn(1, 3, 1, 64, device="cuda")
     with pytest.raises(RuntimeError, match="S=2"):
         ext.index_set_forward(q, q, q, s)
+
+
+# ---------------------------------------------------------------- saved statistics (ma_attn_forward_lse / _backward_saved)
+
+def _lse_ref(up, off, keys):
+    """float64 log2 of each row's softmax denominator over its key set (in
+    units of the scaled scores), [B, N, H]; 0 for a row with no key."""
+    q, k = (x.astype(np.float64) for x in up[:2])
+    B, N, H, D = q.shape
+    sl2 = np.log2(np.e) / np.sqrt(D)
+    out = np.zeros((B, N, H))
+    for i in range(N):
+        kk = keys[off[i]:off[i + 1]]
+        if kk.size == 0:
+            continue
+        s = np.einsum("bhd,bkhd->bhk", q[:, i], k[:, kk]) * sl2  # [B, H, keys]
+        m = s.max(-1, keepdims=True)
+        out[:, i] = (m[..., 0] + np.log2(np.exp2(s - m).sum(-1)))
+    return out
+
+
+@pytest.mark.parametrize("kind,N,seg", [("random", 300, 0), ("skewed", 700, 2), ("window", 1000, 0),
+                                        ("global", 1200, 0), ("global", 1200, 3)])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_saved_statistics_index_set(ext, oracle, kind, N, seg, dtype):
+    """index_set_forward(return_lse=True) writes each row's log-sum-exp; the
+    backward from the saved O and statistics matches the oracle's gradients
+    and the backward that recomputes them."""
+    rng = np.random.default_rng(N + 7 * len(kind))
+    off, keys = _set(kind, N, rng)
+    shape = (2, N, 2, 64)
+    dev, up = _inputs(shape, 9500 + N, dtype)
+    iset = ext.IndexSet(torch.from_numpy(off), torch.from_numpy(keys), N, tiles=True, tile_seg=seg)
+    out, lse = ext.index_set_forward(*dev[:3], iset, return_lse=True)
+    assert float((out.float() - ext.index_set_forward(*dev[:3], iset).float()).abs().max()) == 0.0
+    err = float(np.abs(lse.cpu().numpy() - _lse_ref(up, off, keys)).max())
+    print(f"  {kind} N={N} {dtype}: max|lse err| = {err:.2e}", flush=True)
+    assert err <= 1e-3, err
+    saved = ext.index_set_backward(*dev, iset, out=out, lse=lse)
+    spec = oracle.Spec(*shape, pattern="index_set", offsets=off, keys=keys)
+    for name, a, b in zip("qkv", saved, oracle.backward(spec, *up)):
+        check_grad("d" + name, a.float().cpu().numpy(), b, dtype == torch.float32)
+    again = ext.index_set_backward(*dev, iset)
+    for a, b in zip(saved, again):
+        assert float((a.float() - b.float()).abs().max()) <= (2e-5 if dtype == torch.float32 else 3e-2)
+
+
+@pytest.mark.parametrize("pattern,N", [("block_sparse", 1536), ("block_sparse", 1500), ("longformer", 1500),
+                                       ("longformer", 700)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_saved_statistics_patterns(ext, oracle, pattern, N, dtype):
+    """block_sparse_forward / longformer_forward with return_lse=True give the
+    statistics of their key sets (block-row and Longformer stream kernels), and
+    the tiled backward of those sets from them matches the oracle."""
+    import ma_attn
+    if pattern == "longformer" and dtype == torch.float32:
+        pytest.skip("fp32 Longformer runs on the row kernels, which write no statistics")
+    shape = (2, N, 2, 64)
+    dev, up = _inputs(shape, 9600 + N, dtype)
+    if pattern == "block_sparse":
+        nb = (N + 63) // 64
+        tab = ext.make_block_table(5, nb, 2)
+        bt = ext.BlockTable(tab, N, 64)
+        out, lse = ext.block_sparse_forward(*dev[:3], bt, 64, return_lse=True)
+        ref_out = ext.block_sparse_forward(*dev[:3], bt, 64)
+        iset = ext.pattern_index_set("block_sparse", N, "cuda", block_table=bt, block_size=64)
+        spec = oracle.Spec(*shape, pattern="block_sparse", block_size=64, table=tab.numpy())
+        pd = ma_attn.make_desc(1, N, 1, 64, ma_attn.F32, ma_attn.BLOCK_SPARSE, block_table_ptr=tab.data_ptr(),
+                               blocks_per_row=int(tab.shape[1]), block_size=64)
+        off, keys = ma_attn.pattern_csr(pd, tab)
+    else:
+        out, lse = ext.longformer_forward(*dev[:3], 127, 0, 16, return_lse=True)
+        ref_out = ext.longformer_forward(*dev[:3], 127, 0, 16)
+        iset = ext.pattern_index_set("longformer", N, "cuda", left=127, right=0, num_global=16)
+        spec = oracle.Spec(*shape, pattern="longformer", left=127, right=0, num_global=16)
+        pd = ma_attn.make_desc(1, N, 1, 64, ma_attn.F32, ma_attn.LONGFORMER, left=127, right=0, num_global=16)
+        off, keys = ma_attn.pattern_csr(pd)
+    assert float((out.float() - ref_out.float()).abs().max()) == 0.0
+    off, keys = np.asarray(off, np.int64), np.asarray(keys, np.int64)
+    err = float(np.abs(lse.cpu().numpy() - _lse_ref(up, off, keys)).max())
+    print(f"  {pattern} N={N} {dtype}: max|lse err| = {err:.2e}", flush=True)
+    assert err <= 1e-3, err
+    saved = ext.index_set_backward(*dev, iset, out=out, lse=lse)
+    for name, a, b in zip("qkv", saved, oracle.backward(spec, *up)):
+        check_grad("d" + name, a.float().cpu().numpy(), b, dtype == torch.float32)
+
+
+def test_saved_statistics_rejected(ext):
+    """Kernels that write no statistics refuse return_lse; a malformed lse is
+    rejected before any launch."""
+    q = torch.randn(1, 256, 2, 64, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="statistics"):
+        ext._launch(q, q, q, __import__("ma_attn").SLIDING, True, left=63, right=0, dilation=1)
+    off = torch.arange(0, 257, dtype=torch.int64)
+    iset = ext.IndexSet(off, torch.arange(256, dtype=torch.int32), 256, tiles=True)
+    out, lse = ext.index_set_forward(q, q, q, iset, return_lse=True)
+    with pytest.raises(RuntimeError, match="lse"):
+        ext.index_set_backward(q, q, q, q, iset, out=out, lse=lse[:, :128])
+
+
+@pytest.mark.parametrize("pattern", ["block_sparse", "longformer"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_layer_trains_from_saved_statistics(ext, oracle, pattern, dtype, monkeypatch):
+    """MACoreAttention training on the device (fallback_training=False) keeps
+    the forward's statistics and runs the backward from them where the
+    forward's kernel writes them (fp32 Longformer's does not: that case
+    recomputes them); gradients match the oracle's either way."""
+    from layers.ma_core_bridge import MACoreAttention
+    N = 1536
+    shape = (2, N, 2, 64)
+    dev, up = _inputs(shape, 9700, dtype)
+    if pattern == "block_sparse":
+        tab = ext.make_block_table(3, N // 64, 2)
+        layer = MACoreAttention(pattern="block_sparse", block_table=tab, block_size=64, fallback_training=False)
+        spec = oracle.Spec(*shape, pattern="block_sparse", block_size=64, table=tab.numpy())
+    else:
+        layer = MACoreAttention(pattern="longformer", window_size=128, causal=True, num_global_tokens=16,
+                                fallback_training=False)
+        spec = oracle.Spec(*shape, pattern="longformer", left=127, right=0, num_global=16)
+    layer.train()
+    calls = []
+    real = ext.index_set_backward
+
+    def spy(*a, **kw):
+        calls.append(kw.get("lse") is not None)
+        return real(*a, **kw)
+
+    monkeypatch.setattr(ext, "index_set_backward", spy)
+    q, k, v = (t.clone().requires_grad_(True) for t in dev[:3])
+    layer(q, k, v).backward(dev[3])
+    assert calls == [not (pattern == "longformer" and dtype == torch.float32)]
+    for name, t, ref in zip("qkv", (q, k, v), oracle.backward(spec, *up)):
+        check_grad("d" + name, t.grad.float().cpu().numpy(), ref, dtype == torch.float32)
