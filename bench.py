@@ -37,8 +37,8 @@ Workload "encoder_layer": the reference model's inference (batch 64, sequence
 against the same weights run as the layer's separate operations; value =
 sequences/s, with per-layer latencies of both forms.
 
-With --pass backward --saved-stats (block-sparse, Longformer and index-set
-workloads), the backward runs from the forward's saved O and per-row
+With --pass backward --saved-stats (dense, block-sparse, Longformer and
+index-set workloads), the backward runs from the forward's saved O and per-row
 statistics (ma_attn_backward_saved), the form the autograd layer trains with;
 the forward runs once per input set before timing, and the algorithmic bytes
 count O and the statistics read as well.
@@ -448,7 +448,7 @@ def main() -> int:
                     help="backward: dQ, dK, dV from (Q, K, V, dO) (block-sparse, Longformer and index "
                          "sets through index_set_backward over their key sets)")
     ap.add_argument("--saved-stats", action="store_true",
-                    help="with --pass backward on block-sparse, Longformer and index sets: the backward from "
+                    help="with --pass backward on dense, block-sparse, Longformer and index sets: the backward from "
                          "the forward's saved O and statistics (the forward runs once per input set, untimed)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -469,9 +469,9 @@ def main() -> int:
     B, H, N, D, dt_name, pk, desc = WORKLOADS[args.workload]
     bwd = args.which == "backward"
     saved = bwd and args.saved_stats
-    if args.saved_stats and (not bwd or pk["pattern"] in ("sliding", "dense")):
-        print("bench.py: --saved-stats applies to --pass backward on block_sparse, longformer and index_set "
-              "workloads", file=sys.stderr)
+    if args.saved_stats and (not bwd or pk["pattern"] == "sliding"):
+        print("bench.py: --saved-stats applies to --pass backward on dense, block_sparse, longformer and "
+              "index_set workloads", file=sys.stderr)
         return 2
     dtype = {"bf16": torch.bfloat16, "fp32": torch.float32}[dt_name]
     elt = 2 if dt_name == "bf16" else 4
@@ -496,7 +496,11 @@ def main() -> int:
         launch = lambda s: ext.sliding_backward(s[0], s[1], s[2], s[3], pk["left"], pk["right"],
                                                 pk.get("dilation", 1))
     elif bwd and pk["pattern"] == "dense":
-        launch = lambda s: ext.dense_backward(s[0], s[1], s[2], s[3], pk["causal"])
+        if saved:  # each input set's forward output and statistics, as the layer's autograd keeps them
+            sets = [s_ + ext.dense_forward(s_[0], s_[1], s_[2], pk["causal"], return_lse=True) for s_ in sets]
+            launch = lambda s: ext.dense_backward(s[0], s[1], s[2], s[3], pk["causal"], out=s[4], lse=s[5])
+        else:
+            launch = lambda s: ext.dense_backward(s[0], s[1], s[2], s[3], pk["causal"])
     elif bwd:
         # block-sparse, Longformer and explicit sets train on index_set_backward
         # over the pattern's key sets as one IndexSet (built once, as the layer does)

@@ -207,9 +207,9 @@ int ma_attn_backward_timed(const ma_attn_desc* desc, const void* q, const void* 
  * ma_attn_backward_saved: the gradients of ma_attn_backward from the
  * forward's o and lse (delta_i = dout_i . o_i), for an INDEX_SET with a tile
  * plan, which may hold the key sets of a BLOCK_SPARSE or LONGFORMER forward
- * (ma_attn_pattern_csr enumerates them).  Workspace:
- * ma_attn_backward_workspace_size(desc).  The _timed form stamps its kernels
- * as ma_attn_backward_timed does.
+ * (ma_attn_pattern_csr enumerates them), and for DENSE (head_dim 64).
+ * Workspace: ma_attn_backward_workspace_size(desc).  The _timed form stamps
+ * its kernels as ma_attn_backward_timed does.
  */
 int ma_attn_forward_lse(const ma_attn_desc* desc, const void* q, const void* k,
                         const void* v, void* o, float* lse, void* workspace,

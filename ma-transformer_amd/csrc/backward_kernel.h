@@ -51,6 +51,8 @@ struct BwdArgs {
   int32_t tok_bytes;         // bytes between consecutive rows of a residue class
   float scale, scale_log2;
   int32_t chunk, chunks;     // stream kernels: tiles per workgroup, workgroups per residue class
+  const float* lse;          // bwd_q_kernel<SAVED>: the forward's row statistics (store_lse), [B*N*H]
+  const void* fo;            // bwd_q_kernel<SAVED>: the forward's O (delta = dO . O)
 };
 
 // LDS of one streamed block in the backward passes: two matrices (K and V
@@ -289,9 +291,42 @@ __device__ __forceinline__ BwdStats bwd_stats_rsrc(const BwdArgs& a, int b, int 
   return st;
 }
 
+// dot(x, y) of one row over the head_dim values this lane holds, both in the
+// Q register layout of P (their sum over the row's four lane groups is the
+// row's dot product).
+template <class P>
+__device__ __forceinline__ float bwd_row_dot(const typename P::Q& x, const typename P::Q& y) {
+  float d = 0.0f;
+  if constexpr (P::kSPB == 1) {
+    using T = typename P::Elt;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t wx[4] = {x.r[h].x, x.r[h].y, x.r[h].z, x.r[h].w};
+      const uint32_t wy[4] = {y.r[h].x, y.r[h].y, y.r[h].z, y.r[h].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        d = fmaf(static_cast<float>(__builtin_bit_cast(T, (uint16_t)(wx[j] & 0xffffu))),
+                 static_cast<float>(__builtin_bit_cast(T, (uint16_t)(wy[j] & 0xffffu))), d);
+        d = fmaf(static_cast<float>(__builtin_bit_cast(T, (uint16_t)(wx[j] >> 16))),
+                 static_cast<float>(__builtin_bit_cast(T, (uint16_t)(wy[j] >> 16))), d);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 xv = __builtin_bit_cast(f32x4, x.r[j]), yv = __builtin_bit_cast(f32x4, y.r[j]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) d = fmaf(xv[r], yv[r], d);
+    }
+  }
+  return d;
+}
+
 // ---------------------------------------------------------------- one tile per workgroup
 
-template <class P>
+// SAVED: from the forward's statistics (lse, and delta = dO . O of the row):
+// pass 2 only.
+template <class P, bool SAVED>
 __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // 2 buffers x PairLds (K, V)
   using Elt = typename P::Elt;
@@ -326,7 +361,7 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
   const int key_lo = max(64 * w.t - L, 0);
   const int key_hi = min(64 * w.t + 63 + R, w.Nr - 1);
   const int nb = (key_hi - key_lo) / 64 + 1;
-  const int items = 2 * nb;  // pass 1, then pass 2 over the same blocks
+  const int items = SAVED ? nb : 2 * nb;  // pass 1, then pass 2 over the same blocks
   // A band of at most two blocks stays resident in the two buffers for pass
   // 2 (block j in buffer j); wider bands stream through them twice.
   const bool resident = nb <= 2;
@@ -334,14 +369,22 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
   auto buf_of = [&](int e) { return resident ? (e < nb ? e : e - nb) : (e & 1); };
   auto off_of = [&](int e) { return e < (resident ? nb : items) ? (uint32_t)row_of(e) * tb : kOob; };
 
+  const int64_t srow = (((int64_t)w.b * a.N + w.rho + (int64_t)a.dil * (q0 + c)) * a.H + w.h);
+  typename P::Q fo_row;
+  float lse2 = 0.0f, dlt = 0.0f;
+  if constexpr (SAVED) {
+    P::load_q(fo_row, make_rsrc(static_cast<const Elt*>(a.fo) + w.base, w.nrec), qrow, g);
+    if (q0 + c < w.Nr) lse2 = a.lse[srow];
+  }
   KvRegs<P> xk;  // V is read only as rows (dP^T = V dO^T)
   kv_load<P>(xk, Kr, Vr, off_of(0), tid, tb);
+  if constexpr (SAVED) dlt = col_sum(bwd_row_dot<P>(gr, fo_row));  // after the first block's loads are issued
   kv_store<P>(xk, ring, tid);
   __syncthreads();
 
   const float sl2 = a.scale_log2;
   const int dl = 4 * g - c + L;  // key - query + L of element 0, minus the sub-tile base
-  float m_run = -INFINITY, l_run = 0.0f, a_run = 0.0f, lse2 = 0.0f, dlt = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f, a_run = 0.0f;
   f32x4 acc[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -351,7 +394,7 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
     const uint8_t* sk = ring + buf_of(e) * kBuf;
     f32x4 s[4], dp[4];
     const int live = bwdq_scores<P>(sk, sk + PL::kRows2, kl, qr, gr, row_of(e), q0, L, R, dl, g, w.Nr, s, dp);
-    if (e < nb) {  // pass 1
+    if (!SAVED && e < nb) {  // pass 1
       bwdq_pass1(s, dp, live, sl2, m_run, l_run, a_run);
       if (e == nb - 1) bwdq_stats(m_run, l_run, a_run, sl2, lse2, dlt);
     } else {  // pass 2
@@ -364,7 +407,6 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
   }
   P::store_o(acc, a.scale, DQr, qrow, g);
   // {lse2, delta} of query q0 + c, one lane per query
-  const int64_t srow = (((int64_t)w.b * a.N + w.rho + (int64_t)a.dil * (q0 + c)) * a.H + w.h);
   if (g == 0 && q0 + c < w.Nr) *reinterpret_cast<float2*>(a.stats + 2 * srow) = make_float2(lse2, dlt);
 }
 

@@ -1547,11 +1547,18 @@ bool bwd_mfma_applies(const ma_attn_desc* d, const void* const* ptrs) {
          d->batch * d->num_heads * dil * tiles <= (int64_t)INT32_MAX;
 }
 
+// fo, lse: the forward's O and statistics (ma_attn_backward_saved), or null.
+// Only the one-tile-per-workgroup dQ kernel (bands wider than two blocks:
+// dense, causal) takes them: the stream and fused kernels keep a tile's
+// scores in registers between their statistics and their dQ.
 template <class P>
-int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* stats, hipStream_t st) {
+int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* stats, hipStream_t st,
+                         const void* fo = nullptr, const float* lse = nullptr) {
   int64_t L, R, dil;
   bwd_band(d, &L, &R, &dil);
   BwdArgs a;
+  a.fo = fo;
+  a.lse = lse;
   a.q = ptrs[0];
   a.k = ptrs[1];
   a.v = ptrs[2];
@@ -1601,7 +1608,7 @@ int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* 
       return 0;
     }
   }
-  auto kq = !chunked     ? &bwd_q_kernel<P>
+  auto kq = !chunked     ? (lse ? &bwd_q_kernel<P, true> : &bwd_q_kernel<P, false>)
             : fixed == 1 ? &bwd_q_stream_kernel<P, 63, 0>
             : fixed == 2 ? &bwd_q_stream_kernel<P, 32, 31>
                          : &bwd_q_stream_kernel<P, -1, -1>;
@@ -2107,17 +2114,27 @@ int ma_attn_backward_saved(const ma_attn_desc* desc, const void* q, const void* 
   if (!q || !k || !v || !o || !lse || !dout || !dq || !dk || !dv)
     return fail("ma_attn_backward_saved: null tensor pointer");
   const void* ptrs[8] = {q, k, v, dout, dq, dk, dv, o};
-  if (!tiles_apply(desc, ptrs, 8))
-    return fail("ma_attn_backward_saved: takes an INDEX_SET with a tile plan, head_dim 64, 16-byte aligned tensors");
-  const size_t need = (size_t)(stats_bytes(desc) + tiles_bwd_part_bytes(desc));
+  const bool tiles = tiles_apply(desc, ptrs, 8);
+  const bool dense =
+      desc->pattern == MA_ATTN_DENSE && !g_opt.force_rows && aligned16(o) && bwd_mfma_applies(desc, ptrs);
+  if (!tiles && !dense)
+    return fail("ma_attn_backward_saved: takes an INDEX_SET with a tile plan or DENSE, head_dim 64, 16-byte "
+                "aligned tensors");
+  const size_t need = tiles ? (size_t)(stats_bytes(desc) + tiles_bwd_part_bytes(desc)) : (size_t)rows * sizeof(RowStat);
   if (!workspace || workspace_bytes < need)
     return fail("ma_attn_backward_saved: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
-  const int rc = desc->dtype == MA_ATTN_BF16 ? launch_tiles_bwd<HalfPath<__bf16>>(desc, ptrs, workspace, st, o, lse)
-                 : desc->dtype == MA_ATTN_F16
-                     ? launch_tiles_bwd<HalfPath<_Float16>>(desc, ptrs, workspace, st, o, lse)
-                     : launch_tiles_bwd<F32BwdPath>(desc, ptrs, workspace, st, o, lse);
+  float* sf = static_cast<float*>(workspace);
+  const int rc =
+      tiles ? (desc->dtype == MA_ATTN_BF16 ? launch_tiles_bwd<HalfPath<__bf16>>(desc, ptrs, workspace, st, o, lse)
+               : desc->dtype == MA_ATTN_F16
+                   ? launch_tiles_bwd<HalfPath<_Float16>>(desc, ptrs, workspace, st, o, lse)
+                   : launch_tiles_bwd<F32BwdPath>(desc, ptrs, workspace, st, o, lse))
+            : (desc->dtype == MA_ATTN_BF16 ? launch_backward_mfma<HalfPath<__bf16>>(desc, ptrs, sf, st, o, lse)
+               : desc->dtype == MA_ATTN_F16
+                   ? launch_backward_mfma<HalfPath<_Float16>>(desc, ptrs, sf, st, o, lse)
+                   : launch_backward_mfma<F32BwdPath>(desc, ptrs, sf, st, o, lse));
   if (rc) return rc;
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail("ma_attn_backward_saved: kernel launch failed: %s", hipGetErrorString(e));

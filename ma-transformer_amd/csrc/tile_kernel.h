@@ -109,37 +109,6 @@ __device__ __forceinline__ int live_subtiles(uint64_t mw, bool full) {
   return live;
 }
 
-// dot(x, y) of one row over the head_dim values this lane holds, both in the
-// Q register layout of P (their sum over the row's four lane groups is the
-// row's dot product).
-template <class P>
-__device__ __forceinline__ float q_dot(const typename P::Q& x, const typename P::Q& y) {
-  float d = 0.0f;
-  if constexpr (P::kSPB == 1) {
-    using T = typename P::Elt;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t wx[4] = {x.r[h].x, x.r[h].y, x.r[h].z, x.r[h].w};
-      const uint32_t wy[4] = {y.r[h].x, y.r[h].y, y.r[h].z, y.r[h].w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        d = fmaf(static_cast<float>(__builtin_bit_cast(T, (uint16_t)(wx[j] & 0xffffu))),
-                 static_cast<float>(__builtin_bit_cast(T, (uint16_t)(wy[j] & 0xffffu))), d);
-        d = fmaf(static_cast<float>(__builtin_bit_cast(T, (uint16_t)(wx[j] >> 16))),
-                 static_cast<float>(__builtin_bit_cast(T, (uint16_t)(wy[j] >> 16))), d);
-      }
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const f32x4 xv = __builtin_bit_cast(f32x4, x.r[j]), yv = __builtin_bit_cast(f32x4, y.r[j]);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) d = fmaf(xv[r], yv[r], d);
-    }
-  }
-  return d;
-}
-
 // Compile-time "every sub-tile live": a full entry's products issue back to
 // back with no per-sub-tile branch.
 template <bool B>
@@ -500,7 +469,7 @@ __global__ __launch_bounds__(256, P::kTrRows ? 3 : 2) void tile_dq_kernel(TileAr
   // split tile writes the same values).
   auto saved_stats = [&]() __attribute__((always_inline)) {
     if constexpr (SAVED) {
-      dlt = col_sum(q_dot<P>(gr, fo_row));
+      dlt = col_sum(bwd_row_dot<P>(gr, fo_row));
       if (g == 0 && i < a.N) *reinterpret_cast<float2*>(srow) = make_float2(lse2, dlt);
     }
   };

@@ -136,11 +136,30 @@ def _saved_statistics_pay(iset) -> bool:
     return h is not None and int(h.num_entries) > 2 * int(h.num_q_items)
 
 
+def _saved_statistics_plan(spec: Optional[PatternSpec], sparse: bool, q: torch.Tensor):
+    """("set", IndexSet) or ("dense", None) when the native backward should
+    start from the forward's saved statistics, else None.  Dense rows longer
+    than two 64-key blocks take the one-tile dQ kernel, whose statistics pass
+    streams every key block once more (bench.py --saved-stats on
+    dense_causal_*); shorter rows keep their scores in registers."""
+    if spec is None or spec.pattern == "dense":
+        if (spec is None and sparse) or q.shape[1] <= 128 or q.shape[3] != 64:
+            return None
+        return ("dense", None)
+    if spec.pattern in ("block_sparse", "longformer", "index_set"):
+        iset = _pattern_set(spec, q.shape[1], q.device)
+        return ("set", iset) if _saved_statistics_pay(iset) else None
+    return None
+
+
 def _native_forward(q, k, v, sparse, window_size, use_causal_mask, spec: Optional[PatternSpec],
                     return_lse: bool = False):
     ext = sparse_attention_cuda
     cq, ck, cv = q.contiguous(), k.contiguous(), v.contiguous()
-    if return_lse:  # block-sparse, Longformer and index sets only
+    if return_lse:  # dense, block-sparse, Longformer and index sets only
+        if spec is None or spec.pattern == "dense":
+            causal = bool(use_causal_mask) if spec is None else spec.causal
+            return ext.dense_forward(cq, ck, cv, causal, return_lse=True)
         if spec.pattern == "block_sparse":
             return ext.block_sparse_forward(cq, ck, cv, spec.block_table, spec.block_size, return_lse=True)
         if spec.pattern == "longformer":
@@ -195,25 +214,23 @@ class MACoreAttentionFunction(torch.autograd.Function):
         ctx.window_size = window_size
         ctx.use_causal_mask = use_causal_mask
         ctx.spec = spec
-        ctx.saved_set = None
+        ctx.saved_plan = None
         on_device = query.is_cuda or key.is_cuda or value.is_cuda
         if on_device:
             if not _HAS_SPARSE_CUDA:
                 raise RuntimeError("device tensors given but the native sparse-attention "
                                    "library (libma_attn.so) is not loaded")
-            if (any(ctx.needs_input_grad[:3]) and spec is not None
-                    and spec.pattern in ("block_sparse", "longformer", "index_set")):
-                iset = _pattern_set(spec, query.shape[1], query.device)
-                if _saved_statistics_pay(iset):
-                    try:
-                        out, lse = _native_forward(query, key, value, sparse, window_size, use_causal_mask, spec,
-                                                   return_lse=True)
-                    except RuntimeError:  # a kernel that writes no statistics takes this shape
-                        pass
-                    else:
-                        ctx.saved_set = iset
-                        ctx.save_for_backward(query, key, value, out, lse)
-                        return out
+            plan = _saved_statistics_plan(spec, sparse, query) if any(ctx.needs_input_grad[:3]) else None
+            if plan is not None:
+                try:
+                    out, lse = _native_forward(query, key, value, sparse, window_size, use_causal_mask, spec,
+                                               return_lse=True)
+                except RuntimeError:  # a kernel that writes no statistics takes this shape
+                    pass
+                else:
+                    ctx.saved_plan = plan
+                    ctx.save_for_backward(query, key, value, out, lse)
+                    return out
             ctx.save_for_backward(query, key, value)
             return _native_forward(query, key, value, sparse, window_size, use_causal_mask, spec)
         ctx.save_for_backward(query, key, value)
@@ -232,9 +249,14 @@ class MACoreAttentionFunction(torch.autograd.Function):
             ext = sparse_attention_cuda
             cq, ck, cv, cgo = (t.contiguous() for t in (query, key, value, grad_output))
             cgo = cgo.to(cq.dtype)
-            if ctx.saved_set is not None:  # from the forward's output and statistics
+            if ctx.saved_plan is not None:  # from the forward's output and statistics
                 out, lse = ctx.saved_tensors[3:]
-                dQ, dK, dV = ext.index_set_backward(cq, ck, cv, cgo, ctx.saved_set, out=out, lse=lse)
+                kind, iset = ctx.saved_plan
+                if kind == "set":
+                    dQ, dK, dV = ext.index_set_backward(cq, ck, cv, cgo, iset, out=out, lse=lse)
+                else:
+                    causal = bool(ctx.use_causal_mask) if spec is None else spec.causal
+                    dQ, dK, dV = ext.dense_backward(cq, ck, cv, cgo, causal, out=out, lse=lse)
             elif spec is not None and spec.pattern == "sliding":
                 dQ, dK, dV = ext.sliding_backward(cq, ck, cv, cgo, spec.left, spec.right, spec.dilation)
             elif spec is not None and spec.pattern == "index_set":

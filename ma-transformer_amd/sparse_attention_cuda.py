@@ -159,9 +159,11 @@ def forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
 
 
 def dense_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
-                  use_causal_mask: bool = False) -> torch.Tensor:
-    """Dense (optionally causal) forward.  Reference: dense_forward_cuda (:348-382)."""
-    return _launch(query, key, value, _ma.DENSE, causal=bool(use_causal_mask))
+                  use_causal_mask: bool = False, return_lse: bool = False):
+    """Dense (optionally causal) forward.  Reference: dense_forward_cuda (:348-382).
+    return_lse: also return each row's softmax statistic (float32 [B, S, H])
+    for dense_backward(..., out=, lse=); head_dim 64."""
+    return _launch(query, key, value, _ma.DENSE, return_lse, causal=bool(use_causal_mask))
 
 
 def sliding_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
@@ -442,15 +444,19 @@ def index_set_backward(query, key, value, grad_out, index_set, out=None, lse=Non
               index_t_queries_ptr=index_set.t_queries.data_ptr(), **index_set._tile_kw())
     if out is not None and lse is not None and index_set.tile_plan is not None:
         _check(query, out)
-        B, N, H, _ = query.shape
-        if not (isinstance(lse, torch.Tensor) and lse.dtype == torch.float32 and lse.is_contiguous()
-                and tuple(lse.shape) == (B, N, H) and lse.device == query.device):
-            raise RuntimeError(f"lse must be a contiguous float32 [{B}, {N}, {H}] tensor on the inputs' device")
+        _check_lse(lse, query)
         return _backward_saved(query, key, value, out, lse, grad_out, _ma.INDEX_SET, **kw)
     return _backward(query, key, value, grad_out, _ma.INDEX_SET, **kw)
 
 
 # ---------------------------------------------------------------- backward (HIP kernels)
+
+def _check_lse(lse, query) -> None:
+    B, N, H, _ = query.shape
+    if not (isinstance(lse, torch.Tensor) and lse.dtype == torch.float32 and lse.is_contiguous()
+            and tuple(lse.shape) == (B, N, H) and lse.device == query.device):
+        raise RuntimeError(f"lse must be a contiguous float32 [{B}, {N}, {H}] tensor on the inputs' device")
+
 
 def _backward_saved(q, k, v, out, lse, grad_out, pattern, **kw) -> List[torch.Tensor]:
     B, N, H, D = q.shape
@@ -481,8 +487,15 @@ def backward(query, key, value, grad_out, window_size: int = 64) -> List[torch.T
     return _backward(query, key, value, grad_out, _ma.SLIDING, left=w, right=w, dilation=1)
 
 
-def dense_backward(query, key, value, grad_out, use_causal_mask: bool = False) -> List[torch.Tensor]:
-    """dQ, dK, dV of dense_forward(); reference dense_backward_cuda (.cu:383-418, kernel :104-175)."""
+def dense_backward(query, key, value, grad_out, use_causal_mask: bool = False, out=None,
+                   lse=None) -> List[torch.Tensor]:
+    """dQ, dK, dV of dense_forward(); reference dense_backward_cuda (.cu:383-418, kernel :104-175).
+    out, lse: the forward's output and statistics (dense_forward(return_lse=True));
+    with both, the dQ pass skips recomputing the statistics (ma_attn_backward_saved)."""
+    if out is not None and lse is not None:
+        _check(query, key, value, grad_out, out)
+        _check_lse(lse, query)
+        return _backward_saved(query, key, value, out, lse, grad_out, _ma.DENSE, causal=bool(use_causal_mask))
     return _backward(query, key, value, grad_out, _ma.DENSE, causal=bool(use_causal_mask))
 
 

@@ -237,7 +237,7 @@ def test_saved_statistics_rejected(ext):
         ext.index_set_backward(q, q, q, q, iset, out=out, lse=lse[:, :128])
 
 
-@pytest.mark.parametrize("pattern", ["block_sparse", "longformer"])
+@pytest.mark.parametrize("pattern", ["block_sparse", "longformer", "dense"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_layer_trains_from_saved_statistics(ext, oracle, pattern, dtype, monkeypatch):
     """MACoreAttention training on the device (fallback_training=False) keeps
@@ -252,21 +252,49 @@ def test_layer_trains_from_saved_statistics(ext, oracle, pattern, dtype, monkeyp
         tab = ext.make_block_table(3, N // 64, 2)
         layer = MACoreAttention(pattern="block_sparse", block_table=tab, block_size=64, fallback_training=False)
         spec = oracle.Spec(*shape, pattern="block_sparse", block_size=64, table=tab.numpy())
-    else:
+    elif pattern == "longformer":
         layer = MACoreAttention(pattern="longformer", window_size=128, causal=True, num_global_tokens=16,
                                 fallback_training=False)
         spec = oracle.Spec(*shape, pattern="longformer", left=127, right=0, num_global=16)
+    else:  # the reference's own dense layer (no pattern keywords)
+        layer = MACoreAttention(sparse=False, use_causal_mask=True, fallback_training=False)
+        spec = oracle.Spec(*shape, pattern="dense", causal=True)
     layer.train()
     calls = []
-    real = ext.index_set_backward
+    fn = "dense_backward" if pattern == "dense" else "index_set_backward"
+    real = getattr(ext, fn)
 
     def spy(*a, **kw):
         calls.append(kw.get("lse") is not None)
         return real(*a, **kw)
 
-    monkeypatch.setattr(ext, "index_set_backward", spy)
+    monkeypatch.setattr(ext, fn, spy)
     q, k, v = (t.clone().requires_grad_(True) for t in dev[:3])
     layer(q, k, v).backward(dev[3])
     assert calls == [not (pattern == "longformer" and dtype == torch.float32)]
     for name, t, ref in zip("qkv", (q, k, v), oracle.backward(spec, *up)):
         check_grad("d" + name, t.grad.float().cpu().numpy(), ref, dtype == torch.float32)
+
+
+@pytest.mark.parametrize("N,causal", [(700, True), (1000, False), (64, True)])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_saved_statistics_dense(ext, oracle, N, causal, dtype):
+    """dense_forward(return_lse=True) (block-row kernel) writes each row's
+    log-sum-exp; dense_backward from the saved O and statistics matches the
+    oracle and the recomputing backward."""
+    shape = (2, N, 2, 64)
+    dev, up = _inputs(shape, 9800 + N, dtype)
+    out, lse = ext.dense_forward(*dev[:3], causal, return_lse=True)
+    assert float((out.float() - ext.dense_forward(*dev[:3], causal).float()).abs().max()) == 0.0
+    off = np.concatenate([[0], np.cumsum(np.arange(1, N + 1) if causal else np.full(N, N))]).astype(np.int64)
+    keys = np.concatenate([np.arange(i + 1 if causal else N) for i in range(N)]).astype(np.int64)
+    err = float(np.abs(lse.cpu().numpy() - _lse_ref(up, off, keys)).max())
+    print(f"  dense N={N} causal={causal} {dtype}: max|lse err| = {err:.2e}", flush=True)
+    assert err <= 1e-3, err
+    saved = ext.dense_backward(*dev, causal, out=out, lse=lse)
+    spec = oracle.Spec(*shape, pattern="dense", causal=causal)
+    for name, a, b in zip("qkv", saved, oracle.backward(spec, *up)):
+        check_grad("d" + name, a.float().cpu().numpy(), b, dtype == torch.float32)
+    again = ext.dense_backward(*dev, causal)
+    for a, b in zip(saved, again):
+        assert float((a.float() - b.float()).abs().max()) <= (2e-5 if dtype == torch.float32 else 3e-2)
