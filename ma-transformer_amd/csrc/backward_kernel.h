@@ -106,10 +106,15 @@ struct BwdTile {
   uint32_t nrec;
 };
 
+// Ids are XCD-contiguous (xcd_row_order): an XCD runs whole heads' tiles,
+// so the head's streamed rows, which every tile of the head reads, meet in
+// its L2.  rev: tiles in descending order, for passes whose work grows with
+// the tile (dQ of a band with a long left side: the longest tiles start
+// first instead of forming the launch's tail).
 template <class P>
-__device__ __forceinline__ bool bwd_tile(const BwdArgs& a, BwdTile& w) {
-  int lin = blockIdx.x;
-  w.t = lin % a.tiles;
+__device__ __forceinline__ bool bwd_tile(const BwdArgs& a, BwdTile& w, bool rev = false) {
+  int lin = xcd_row_order((int)blockIdx.x, (int)gridDim.x);
+  w.t = rev ? a.tiles - 1 - lin % a.tiles : lin % a.tiles;
   lin /= a.tiles;
   w.rho = lin % a.dil;
   lin /= a.dil;
@@ -333,7 +338,7 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdArgs a) {
   using PL = PairLds<P>;
   constexpr int kBuf = PL::kBytes;
   BwdTile w;
-  if (!bwd_tile<P>(a, w)) return;  // uniform, before any barrier
+  if (!bwd_tile<P>(a, w, a.left > a.right)) return;  // uniform, before any barrier
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);

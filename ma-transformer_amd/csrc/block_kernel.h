@@ -38,15 +38,9 @@ struct BlockArgs {
   float* lse;      // optional: each query row's softmax statistic (store_lse), [B*N*H]
 };
 
-// Workgroups are dispatched round-robin over the 8 XCDs, each with its own
-// L2.  Renumbering so that XCD x runs rows [x*G/8, (x+1)*G/8) in order puts
-// row r and row r+1 (which read block r as diagonal and as previous) and a
-// head's random blocks on one L2.  Bijective: the first 8*(G/8) ids are
-// permuted, the rest keep their number.
-__device__ __forceinline__ int xcd_row_order(int bid, int G) {
-  const int per = G >> 3;
-  return bid < (per << 3) ? (bid & 7) * per + (bid >> 3) : bid;
-}
+// Workgroup ids go through xcd_row_order: XCD x runs rows [x*G/8,
+// (x+1)*G/8) in order, which puts row r and row r+1 (which read block r as
+// diagonal and as previous) and a head's random blocks on one L2.
 
 // Online-softmax update of one 64-key block (4 sub-tiles) from an LDS slot.
 // cb < 0: an absent entry, every score masked.  diag: the block is the query

@@ -140,4 +140,14 @@ __device__ __forceinline__ int floordiv32(int a, int d) {
   return (a % d != 0 && a < 0) ? q - 1 : q;
 }
 
+// Workgroups are dispatched round-robin over the 8 XCDs, each with its own
+// L2.  This renumbering gives XCD x the contiguous run of ids [x*G/8,
+// (x+1)*G/8) in order, so work items with neighbouring ids (a head's rows or
+// tiles) share one L2.  Bijective: the first 8*(G/8) ids are permuted, the
+// rest keep their number.
+__device__ __forceinline__ int xcd_row_order(int bid, int G) {
+  const int per = G >> 3;
+  return bid < (per << 3) ? (bid & 7) * per + (bid >> 3) : bid;
+}
+
 }  // namespace ma_dev
