@@ -455,6 +455,11 @@ def main() -> int:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "multi-GPU sharding is a design note, not a measured path.", file=sys.stderr)
         return 2
+    if args.saved_stats and (args.which != "backward" or args.workload not in WORKLOADS
+                             or WORKLOADS[args.workload][5]["pattern"] == "sliding"):
+        print("bench.py: --saved-stats applies to --pass backward on dense, block_sparse, longformer and "
+              "index_set workloads", file=sys.stderr)
+        return 2
     if args.workload == "ticks":
         return bench_ticks(args)
     if args.workload == "encoder_layer":
@@ -469,10 +474,6 @@ def main() -> int:
     B, H, N, D, dt_name, pk, desc = WORKLOADS[args.workload]
     bwd = args.which == "backward"
     saved = bwd and args.saved_stats
-    if args.saved_stats and (not bwd or pk["pattern"] == "sliding"):
-        print("bench.py: --saved-stats applies to --pass backward on dense, block_sparse, longformer and "
-              "index_set workloads", file=sys.stderr)
-        return 2
     dtype = {"bf16": torch.bfloat16, "fp32": torch.float32}[dt_name]
     elt = 2 if dt_name == "bf16" else 4
     dev = torch.device("cuda", 0)

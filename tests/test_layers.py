@@ -147,3 +147,44 @@ def test_pattern_defaults_follow_window():
     assert (s.left, s.right, s.dilation) == (4, 4, 4)
     s = MACoreAttention(sparse=False, use_causal_mask=True, pattern="dense").spec
     assert s.causal
+
+
+def test_saved_statistics_choice():
+    """When the native backward starts from the forward's saved statistics:
+    tiled sets whose query tiles average more than two entries, and dense rows
+    longer than two 64-key blocks at head_dim 64; never for sliding windows
+    (their kernels keep a tile's scores in registers)."""
+    import types
+    from layers import ma_core_bridge as br
+
+    def iset(entries, items):
+        return types.SimpleNamespace(tile_header=types.SimpleNamespace(num_entries=entries, num_q_items=items))
+
+    assert br._saved_statistics_pay(iset(1024, 256))      # block-sparse: 4 entries per tile
+    assert not br._saved_statistics_pay(iset(2048, 1024))  # a causal 64 window: 2 per tile
+    assert not br._saved_statistics_pay(types.SimpleNamespace(tile_header=None))  # no tile plan
+    q = torch.empty(1, 1024, 2, 64)
+    assert br._saved_statistics_plan(None, False, q) == ("dense", None)       # the reference's dense layer
+    assert br._saved_statistics_plan(None, True, q) is None                   # its sliding layer
+    assert br._saved_statistics_plan(None, False, torch.empty(1, 128, 2, 64)) is None  # two blocks
+    assert br._saved_statistics_plan(None, False, torch.empty(1, 1024, 2, 32)) is None  # head_dim 32
+    assert br._saved_statistics_plan(br.PatternSpec(pattern="sliding", left=63, right=0), True, q) is None
+    assert br._saved_statistics_plan(br.PatternSpec(pattern="dense", causal=True), False, q) == ("dense", None)
+    assert br._saved_statistics_plan(br.PatternSpec(pattern="index_set", index_set=iset(900, 300)), False,
+                                     q)[0] == "set"
+    assert br._saved_statistics_plan(br.PatternSpec(pattern="index_set", index_set=iset(600, 300)), False,
+                                     q) is None
+
+
+def test_bench_saved_stats_needs_a_tiled_or_dense_backward():
+    """bench.py refuses --saved-stats outside the backward of dense, block-sparse,
+    Longformer and index-set workloads (before touching any device)."""
+    import subprocess
+    import sys
+    import os
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    for argv in (["--saved-stats"], ["--saved-stats", "--pass", "backward"],
+                 ["--workload", "cfg3", "--saved-stats"]):
+        r = subprocess.run([sys.executable, os.path.join(repo, "bench.py"), *argv], capture_output=True, text=True,
+                           timeout=300, env={**os.environ, "HIP_VISIBLE_DEVICES": ""})
+        assert r.returncode == 2 and "--saved-stats applies" in r.stderr, (argv, r.returncode, r.stderr[-300:])
