@@ -301,3 +301,42 @@ def test_saved_statistics_dense(ext, oracle, N, causal, dtype):
     again = ext.dense_backward(*dev, causal)
     for a, b in zip(saved, again):
         assert float((a.float() - b.float()).abs().max()) <= (2e-5 if dtype == torch.float32 else 3e-2)
+
+
+@pytest.mark.parametrize("workload", ["cfg3", "cfg4"])
+def test_saved_statistics_full_size(ext, workload):
+    """At the BASELINE shapes (cfg3: B2 H8 N16384 block-sparse; cfg4: B2 H12
+    N32768 Longformer; bf16), the backward from saved statistics agrees with
+    the backward that recomputes them on every element, and the statistics
+    satisfy sum_j exp2(s_ij*sl2 - lse_i) = 1 on sampled rows."""
+    torch.manual_seed(11)
+    if workload == "cfg3":
+        B, H, N = 2, 8, 16384
+    else:
+        B, H, N = 2, 12, 32768
+    q, k, v, g = (torch.randn(B, N, H, 64, device="cuda").to(torch.bfloat16) for _ in range(4))
+    if workload == "cfg3":
+        tab = ext.BlockTable(ext.make_block_table(1234, N // 64, 2), N, 64)
+        out, lse = ext.block_sparse_forward(q, k, v, tab, 64, return_lse=True)
+        iset = ext.pattern_index_set("block_sparse", N, "cuda", block_table=tab, block_size=64)
+    else:
+        out, lse = ext.longformer_forward(q, k, v, 127, 0, 16, return_lse=True)
+        iset = ext.pattern_index_set("longformer", N, "cuda", left=127, right=0, num_global=16)
+    saved = ext.index_set_backward(q, k, v, g, iset, out=out, lse=lse)
+    again = ext.index_set_backward(q, k, v, g, iset)
+    for name, a, b in zip(("dq", "dk", "dv"), saved, again):
+        a, b = a.float(), b.float()
+        bound = 1e-2 + 1e-2 * b.abs()
+        worst = float(((a - b).abs() / bound).max())
+        print(f"  {workload} {name}: max |saved - recomputed| / (1e-2 + 1e-2|x|) = {worst:.3f}", flush=True)
+        assert worst <= 1.0
+    # the statistics normalise their rows: a sample of query rows of head 0, batch 0
+    off = iset.offsets.cpu().numpy()
+    keys = iset.keys.cpu().numpy()
+    sl2 = 1.4426950408889634 / 8.0
+    qs, ks = q[0, :, 0].float(), k[0, :, 0].float()
+    for i in list(range(0, 20)) + [N // 2, N - 1]:
+        kk = torch.from_numpy(keys[off[i]:off[i + 1]].astype(np.int64)).cuda()
+        s = (ks[kk] @ qs[i]) * sl2
+        total = float(torch.exp2(s - lse[0, i, 0]).sum())
+        assert abs(total - 1.0) <= 1e-4, (i, total)
