@@ -39,7 +39,7 @@
 namespace ma_dev {
 
 constexpr int kTileFull = 1 << 30;   // entry flag: every pair of the 64x64 block is in the set
-constexpr int kTileSeg = 16;        // default entries per work item
+constexpr int kTileSeg = 32;        // default entries per work item
 constexpr int kTilePart = 68;        // floats per row of a forward partial: 64 O, log2 max, sum, 2 pad
 
 struct TileArgs {

@@ -66,7 +66,7 @@ def test_tile_plan_matches_brute_force(N, density, fr, fc, seg):
     m, off, keys = _csr(rng, N, density, fr, fc)
     hdr, p = _plan(N, off, keys, seg)
     nt = (N + 63) // 64
-    assert hdr.seq_len == N and hdr.num_tiles == nt and hdr.seg == (seg or 16)
+    assert hdr.seq_len == N and hdr.num_tiles == nt and hdr.seg == (seg or 32)
     # entries: exactly the (tile, block) pairs with a key, ordered by tile then block
     pairs = sorted({(i // 64, j // 64) for i, j in zip(*np.nonzero(m))})
     blk = p["blk"] & (FULL - 1)
