@@ -21,7 +21,9 @@ forward pass over that batch.  Prints ONE JSON line:
              host, single thread, bounded sample of the same workload
   pattern_copy  sliding, Longformer and block-sparse forward: the kernel's
              access pattern without its arithmetic (ma_attn_copy_probe), timed
-             the same way -- the copy speed that pattern reaches on the device
+             the same way -- the copy speed that pattern reaches on the device;
+             the 16-bit fixed-window backward: the fused kernel's pattern
+             (ma_attn_backward_copy_probe)
 
 Inputs are resident in HBM before timing; 4+ distinct input sets (>1 GB in
 total) are rotated so the 256 MB MALL cannot serve a repeated set.
@@ -621,6 +623,35 @@ def main() -> int:
         except RuntimeError:
             probe_us = None  # the stream kernel does not take this shape
         del pout
+    elif bwd and pk["pattern"] == "sliding" and dt_name != "fp32":
+        # the fused backward's workgroups, chunks and steps: K, V, Q, dO rows
+        # read and dQ, dK, dV rows written at the kernel's positions
+        import ma_attn as _ma
+        pdesc = _ma.make_desc(B, N, H, D, _ma.DTYPES[dtype], _ma.SLIDING, left=pk["left"], right=pk["right"],
+                              dilation=pk.get("dilation", 1))
+        probe_src = "ma_attn_backward_copy_probe (bwd_fused_kernel's workgroups, chunks and steps, no arithmetic)"
+        pouts = [torch.empty_like(sets[0][0]) for _ in range(3)]
+        raw = stream.cuda_stream
+
+        def bprobe(s_, evs=None):
+            _ma.backward_copy_probe_raw(pdesc, *(t_.data_ptr() for t_ in s_[:4]), *(t_.data_ptr() for t_ in pouts),
+                                        raw, evs)
+        try:
+            for i in range(20):
+                bprobe(sets[i % nsets])
+            pev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                   for _ in range(args.steps)]
+            for a_, b_ in pev:
+                a_.record(stream)
+                b_.record(stream)
+            torch.cuda.synchronize()
+            for i in range(args.steps):
+                bprobe(sets[i % nsets], (pev[i][0].cuda_event, pev[i][1].cuda_event))
+            torch.cuda.synchronize()
+            probe_us = 1e3 * sum(a_.elapsed_time(b_) for a_, b_ in pev) / len(pev)
+        except RuntimeError:
+            probe_us = None  # the fused backward does not take this window
+        del pouts
 
     queries = B * H * N
     alg_bytes = tensors * B * N * H * D * elt + (4 * B * N * H if saved else 0)  # + the statistics read
@@ -691,7 +722,7 @@ def main() -> int:
         # algorithmic bytes over the probe's mean stamped duration, and the
         # kernel's speed as a fraction of it
         out["pattern_copy"] = {"kernel_us_mean": probe_us,
-                               "gbps": (4 * B * N * H * D * elt) / (probe_us * 1e-6) / 1e9,
+                               "gbps": ((7 if bwd else 4) * B * N * H * D * elt) / (probe_us * 1e-6) / 1e9,
                                "kernel_frac_of_pattern_copy": probe_us / (mean_launch_ms * 1e3),
                                "source": probe_src}
     if bwd:

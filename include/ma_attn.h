@@ -326,6 +326,25 @@ int ma_attn_copy_probe_timed(const ma_attn_desc* desc, const void* q, const void
                              const void* v, void* o, void* stream, void* start_event,
                              void* stop_event);
 
+/*
+ * Measurement: the fused backward's memory traffic for desc without its
+ * arithmetic (SLIDING, bf16/fp16, head_dim 64, windows [i-63, i] and
+ * [i-32, i+31] of any dilation: the descriptors ma_attn_backward runs as one
+ * fused launch).  The same workgroups, chunks and steps read the K, V, Q and
+ * dO rows the kernel reads and write dq = q xor dout, dk = k, dv = v
+ * bitwise, each row once, at the kernel's positions.  Gives the copy speed of
+ * that access pattern on the device.  Returns non-zero when the fused kernel
+ * would not take desc.  The _timed form stamps the kernel's start and stop on
+ * two caller-created events.  No reference counterpart.
+ */
+int ma_attn_backward_copy_probe(const ma_attn_desc* desc, const void* q, const void* k,
+                                const void* v, const void* dout, void* dq, void* dk, void* dv,
+                                void* stream);
+int ma_attn_backward_copy_probe_timed(const ma_attn_desc* desc, const void* q, const void* k,
+                                      const void* v, const void* dout, void* dq, void* dk,
+                                      void* dv, void* stream, void* start_event,
+                                      void* stop_event);
+
 /* ABI version of this header (bumped on incompatible change). */
 int ma_attn_abi_version(void);
 

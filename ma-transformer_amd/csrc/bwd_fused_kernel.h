@@ -380,4 +380,80 @@ __global__ __launch_bounds__(256, 2) void bwd_fused_kernel(BwdArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- copy probe
+//
+// bwd_fused_kernel's memory traffic without its arithmetic: the same
+// workgroups, chunks and steps, each step reading the new key block's K, V
+// rows and the query tile's Q, dO rows one step ahead, and writing
+// dQ = Q xor dO for the tiles the chunk owns and dK = K, dV = V for its key
+// blocks, at the kernel's positions.  It measures what this access pattern
+// can move on the device.
+template <int FL, int FR>
+__global__ __launch_bounds__(256) void bwd_probe_kernel(BwdArgs a) {
+  using B = FusedBand<FL, FR>;
+  int lin = a.dil == 1 ? xcd_row_order(blockIdx.x, gridDim.x) : (int)blockIdx.x;
+  const int chunk_id = lin % a.chunks;
+  lin /= a.chunks;
+  const int rho = lin % a.dil;
+  lin /= a.dil;
+  const int h = lin % (int)a.H;
+  const int b = lin / (int)a.H;
+  const int Nr = (int)((a.N - rho + a.dil - 1) / a.dil);
+  const int nblk = (Nr + 63) >> 6;
+  const int nkb = floordiv32(Nr - 1 - B::OB, 64) + 1;
+  const int t0 = chunk_id * a.chunk;
+  const int t1 = min(t0 + a.chunk, nblk);
+  if (t0 >= t1) return;
+  const int k0 = t0, k1 = t1 == nblk ? nkb : t1;
+  const int s0 = max(min(t0, k0 - B::KB0 - 1), 0);
+  const int s1 = max(t1 - 1, k1 - 1 - B::KB0);
+  const uint32_t tb = (uint32_t)a.tok_bytes;
+  const int64_t base = (((int64_t)b * a.N + rho) * a.H + h) * kHeadDim;
+  const uint32_t nrec = (uint32_t)((int64_t)(Nr - 1) * tb + kHeadDim * 2);
+  using E = uint16_t;
+  const __amdgpu_buffer_rsrc_t Qr = make_rsrc(static_cast<const E*>(a.q) + base, nrec);
+  const __amdgpu_buffer_rsrc_t Kr = make_rsrc(static_cast<const E*>(a.k) + base, nrec);
+  const __amdgpu_buffer_rsrc_t Vr = make_rsrc(static_cast<const E*>(a.v) + base, nrec);
+  const __amdgpu_buffer_rsrc_t Gr = make_rsrc(static_cast<const E*>(a.dout) + base, nrec);
+  const __amdgpu_buffer_rsrc_t DQr = make_rsrc(static_cast<E*>(a.dq) + base, nrec);
+  const __amdgpu_buffer_rsrc_t DKr = make_rsrc(static_cast<E*>(a.dk) + base, nrec);
+  const __amdgpu_buffer_rsrc_t DVr = make_rsrc(static_cast<E*>(a.dv) + base, nrec);
+  // thread tid: rows tid>>3 and (tid>>3)+32 of a 64-row block, 16-byte column tid&7
+  const int tid = threadIdx.x;
+  const uint32_t r0 = (uint32_t)(tid >> 3) * tb + 16 * (tid & 7), r1 = r0 + 32 * tb;
+  auto qoff = [&](int x) { return (uint32_t)(64 * x) * tb; };
+  auto koff = [&](int j) { return (uint32_t)(64 * j + B::OB) * tb; };  // rows below 0 fall out of range
+  struct Two {
+    uint4 x, y;
+  };
+  auto ld = [&](__amdgpu_buffer_rsrc_t r, uint32_t o) { return Two{bload16(r, o + r0), bload16(r, o + r1)}; };
+  auto st = [&](__amdgpu_buffer_rsrc_t r, uint32_t o, Two v) {
+    bstore16(r, o + r0, v.x);
+    bstore16(r, o + r1, v.y);
+  };
+  const int kb_first = s0 + B::KB0;
+  Two ka = ld(Kr, koff(kb_first)), va = ld(Vr, koff(kb_first));
+  Two kn = ld(Kr, koff(kb_first + 1)), vn = ld(Vr, koff(kb_first + 1));
+  Two q = ld(Qr, qoff(s0)), g = ld(Gr, qoff(s0));
+  for (int t = s0; t <= s1; ++t) {
+    const int kb = t + B::KB0;
+    const Two kc = kn, vc = vn;  // block kb+1
+    const uint32_t nx = t < s1 ? 0u : kOob;
+    kn = ld(Kr, nx + koff(kb + 2));
+    vn = ld(Vr, nx + koff(kb + 2));
+    const Two qn = ld(Qr, nx + qoff(t + 1)), gn = ld(Gr, nx + qoff(t + 1));
+    if (t >= t0 && t < t1)
+      st(DQr, qoff(t), Two{make_uint4(q.x.x ^ g.x.x, q.x.y ^ g.x.y, q.x.z ^ g.x.z, q.x.w ^ g.x.w),
+                           make_uint4(q.y.x ^ g.y.x, q.y.y ^ g.y.y, q.y.z ^ g.y.z, q.y.w ^ g.y.w)});
+    if (kb >= k0 && kb < k1) {
+      st(DVr, koff(kb), va);
+      st(DKr, koff(kb), ka);
+    }
+    ka = kc;
+    va = vc;
+    q = qn;
+    g = gn;
+  }
+}
+
 }  // namespace ma_dev

@@ -1547,6 +1547,14 @@ bool bwd_mfma_applies(const ma_attn_desc* d, const void* const* ptrs) {
          d->batch * d->num_heads * dil * tiles <= (int64_t)INT32_MAX;
 }
 
+// The fused backward's chunks of a stream's tiles, fitted to one round of the
+// resident workgroups (two per CU).
+void fused_chunks(BwdArgs& a, int64_t streams) {
+  const int64_t per_stream = ma::imax64(1, 256 * 2 / streams);
+  a.chunk = (int32_t)ma::imax64(1, (a.tiles + per_stream - 1) / per_stream);
+  a.chunks = (int32_t)((a.tiles + a.chunk - 1) / a.chunk);
+}
+
 // fo, lse: the forward's O and statistics (ma_attn_backward_saved), or null.
 // Only the one-tile-per-workgroup dQ kernel (bands wider than two blocks:
 // dense, causal) takes them: the stream and fused kernels keep a tile's
@@ -1599,9 +1607,7 @@ int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* 
       // the resident workgroups (measured on the target: one round, chunk 16,
       // 10-15 % faster than two to six rounds)
       const size_t shm = (size_t)FusedLds::kBytes;
-      const int64_t per_stream = ma::imax64(1, 256 * 2 / streams);
-      a.chunk = (int32_t)ma::imax64(1, (a.tiles + per_stream - 1) / per_stream);
-      a.chunks = (int32_t)((a.tiles + a.chunk - 1) / a.chunk);
+      fused_chunks(a, streams);
       auto kf = fixed == 1 ? &bwd_fused_kernel<P, 63, 0> : &bwd_fused_kernel<P, 32, 31>;
       if (reserve_lds(reinterpret_cast<const void*>(kf), shm, st)) return 1;
       launch(true, kf, dim3((unsigned)(streams * a.chunks)), dim3(256), (uint32_t)shm, st, a);
@@ -2375,6 +2381,60 @@ int ma_attn_copy_probe_timed(const ma_attn_desc* desc, const void* q, const void
   g_ev_start = static_cast<hipEvent_t>(start_event);
   g_ev_stop = static_cast<hipEvent_t>(stop_event);
   const int rc = ma_attn_copy_probe(desc, q, k, v, o, stream);
+  g_ev_start = g_ev_stop = nullptr;
+  return rc;
+}
+
+int ma_attn_backward_copy_probe(const ma_attn_desc* desc, const void* q, const void* k, const void* v,
+                                const void* dout, void* dq, void* dk, void* dv, void* stream) {
+  g_last_error.clear();
+  if (validate(desc)) return 1;
+  if (desc->batch * desc->seq_len * desc->num_heads == 0) return 0;
+  if (!q || !k || !v || !dout || !dq || !dk || !dv) return fail("ma_attn: null tensor pointer");
+  const void* ptrs[7] = {q, k, v, dout, dq, dk, dv};
+  const int fixed = desc->pattern != MA_ATTN_SLIDING || desc->dtype == MA_ATTN_F32 || !bwd_mfma_applies(desc, ptrs)
+                        ? 0
+                    : desc->left == 63 && desc->right == 0  ? 1
+                    : desc->left == 32 && desc->right == 31 ? 2
+                                                            : 0;
+  if (fixed == 0)
+    return fail("ma_attn_backward_copy_probe: the fused backward does not take this descriptor (SLIDING, "
+                "16-bit, head_dim 64, windows [i-63, i] or [i-32, i+31] of any dilation, 16-byte aligned "
+                "tensors)");
+  BwdArgs a;
+  memset(&a, 0, sizeof(a));
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.dout = dout;
+  a.dq = dq;
+  a.dk = dk;
+  a.dv = dv;
+  a.N = desc->seq_len;
+  a.H = desc->num_heads;
+  a.left = (int32_t)desc->left;
+  a.right = (int32_t)desc->right;
+  a.dil = (int32_t)desc->dilation;
+  const int64_t nr = (desc->seq_len + desc->dilation - 1) / desc->dilation;
+  a.tiles = (int32_t)((nr + 63) / 64);
+  a.tok_bytes = (int32_t)(desc->dilation * desc->num_heads * kHeadDim * 2);
+  const int64_t streams = desc->batch * desc->num_heads * desc->dilation;
+  fused_chunks(a, streams);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  (void)hipGetLastError();
+  launch(true, fixed == 1 ? bwd_probe_kernel<63, 0> : bwd_probe_kernel<32, 31>, dim3((unsigned)(streams * a.chunks)),
+         dim3(256), 0u, st, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail("ma_attn_backward_copy_probe: kernel launch failed: %s", hipGetErrorString(e));
+  return 0;
+}
+
+int ma_attn_backward_copy_probe_timed(const ma_attn_desc* desc, const void* q, const void* k, const void* v,
+                                      const void* dout, void* dq, void* dk, void* dv, void* stream,
+                                      void* start_event, void* stop_event) {
+  g_ev_start = static_cast<hipEvent_t>(start_event);
+  g_ev_stop = static_cast<hipEvent_t>(stop_event);
+  const int rc = ma_attn_backward_copy_probe(desc, q, k, v, dout, dq, dk, dv, stream);
   g_ev_start = g_ev_stop = nullptr;
   return rc;
 }

@@ -138,6 +138,8 @@ def _open():
                                       ctypes.POINTER(TileHeader), ctypes.c_void_p, ctypes.c_size_t]
     lib.ma_attn_copy_probe_timed.restype = ctypes.c_int
     lib.ma_attn_copy_probe_timed.argtypes = [ctypes.POINTER(Desc)] + [ctypes.c_void_p] * 7
+    lib.ma_attn_backward_copy_probe_timed.restype = ctypes.c_int
+    lib.ma_attn_backward_copy_probe_timed.argtypes = [ctypes.POINTER(Desc)] + [ctypes.c_void_p] * 10
     lib.ma_attn_reload_options.restype = None
     lib.ma_attn_reload_options.argtypes = []
     if lib.ma_attn_abi_version() != ABI_VERSION:
@@ -342,6 +344,16 @@ def copy_probe_raw(desc: Desc, q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, s
         raise RuntimeError(last_error())
 
 
+def backward_copy_probe_raw(desc: Desc, q_ptr: int, k_ptr: int, v_ptr: int, dout_ptr: int, dq_ptr: int,
+                            dk_ptr: int, dv_ptr: int, stream: int = 0, events=None) -> None:
+    """ma_attn_backward_copy_probe(_timed): the fused backward's traffic without
+    its arithmetic (dq = q xor dout, dk = k, dv = v bitwise)."""
+    e0, e1 = events if events else (None, None)
+    if LIB.ma_attn_backward_copy_probe_timed(ctypes.byref(desc), q_ptr, k_ptr, v_ptr, dout_ptr, dq_ptr, dk_ptr,
+                                             dv_ptr, stream or None, e0 or None, e1 or None) != 0:
+        raise RuntimeError(last_error())
+
+
 def reload_options() -> None:
     """Re-read the MA_ATTN_* kernel-selection switches from the environment."""
     LIB.ma_attn_reload_options()
@@ -357,5 +369,5 @@ def default_scale(D: int) -> float:
 
 
 __all__ = ["LIB", "Desc", "make_desc", "forward_raw", "forward_noalloc_raw", "validate", "workspace_size",
-           "block_table", "row_keys", "pattern_csr", "copy_probe_raw", "tile_plan", "tile_header_of", "TileHeader", "reload_options", "last_error", "EncoderLayer", "encoder_layer_forward_raw", "DTYPES", "default_scale",
+           "block_table", "row_keys", "pattern_csr", "copy_probe_raw", "backward_copy_probe_raw", "tile_plan", "tile_header_of", "TileHeader", "reload_options", "last_error", "EncoderLayer", "encoder_layer_forward_raw", "DTYPES", "default_scale",
            "SLIDING", "DENSE", "BLOCK_SPARSE", "LONGFORMER", "INDEX_SET", "F32", "BF16", "F16"]

@@ -2,7 +2,8 @@
 arithmetic, a measurement entry point).  SLIDING: every O element is Q xor K
 xor V of its own position, for the window shapes bench.py measures it on.
 BLOCK_SPARSE: O row i is Q row i xor the K and V rows at the same offset in
-every block its table row lists."""
+every block its table row lists.  ma_attn_backward_copy_probe (the fused
+backward's pattern): dQ = Q xor dO, dK = K, dV = V at every position."""
 import pytest
 import torch
 
@@ -85,3 +86,41 @@ def test_copy_probe_rejects_other_patterns():
     desc = ma_attn.make_desc(1, 64, 1, 64, ma_attn.BF16, ma_attn.DENSE)
     with pytest.raises(RuntimeError, match="SLIDING"):
         ma_attn.copy_probe_raw(desc, q.data_ptr(), q.data_ptr(), q.data_ptr(), q.data_ptr())
+
+
+@pytest.mark.parametrize("shape,left,right,dil,dtype", [
+    ((1, 5000, 8, 64), 63, 0, 1, torch.bfloat16),
+    ((2, 3000, 4, 64), 32, 31, 1, torch.bfloat16),
+    ((1, 4099, 8, 64), 63, 0, 4, torch.bfloat16),
+    ((2, 1000, 3, 64), 32, 31, 2, torch.float16),
+    ((1, 100, 2, 64), 63, 0, 1, torch.float16),
+])
+def test_backward_copy_probe_writes_every_row_once(shape, left, right, dil, dtype):
+    """ma_attn_backward_copy_probe: every dQ row is Q xor dO of its position,
+    every dK / dV row a copy of K / V, so the fused kernel's chunks and steps
+    reach each query tile and key block with one writer."""
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    import ma_attn
+    g = torch.Generator(device="cuda").manual_seed(3)
+    q, k, v, dout = (torch.randn(shape, device="cuda", generator=g).to(dtype) for _ in range(4))
+    dq, dk, dv = (torch.full_like(q, 3.0) for _ in range(3))
+    desc = ma_attn.make_desc(*shape, ma_attn.DTYPES[dtype], ma_attn.SLIDING, left=left, right=right, dilation=dil)
+    ma_attn.backward_copy_probe_raw(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), dout.data_ptr(), dq.data_ptr(),
+                                    dk.data_ptr(), dv.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(dq.view(torch.int16), q.view(torch.int16) ^ dout.view(torch.int16))
+    assert torch.equal(dk.view(torch.int16), k.view(torch.int16))
+    assert torch.equal(dv.view(torch.int16), v.view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype,left,right", [(torch.float32, 63, 0), (torch.bfloat16, 40, 0)])
+def test_backward_copy_probe_rejects_unfused_windows(dtype, left, right):
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    import ma_attn
+    q = torch.zeros(1, 128, 1, 64, device="cuda", dtype=dtype)
+    desc = ma_attn.make_desc(1, 128, 1, 64, ma_attn.DTYPES[dtype], ma_attn.SLIDING, left=left, right=right)
+    p = q.data_ptr()
+    with pytest.raises(RuntimeError, match="fused backward does not take"):
+        ma_attn.backward_copy_probe_raw(desc, p, p, p, p, p, p, p)
