@@ -33,10 +33,11 @@
 // also the blocks past its last tile).  It also runs the query passes of the
 // neighbouring tiles that reach its blocks (tile t1 for the causal window,
 // t0-1 on the shifted grid), without storing their dQ, and reads the key
-// block before its first step.  Chunks are dealt to XCDs in contiguous runs,
-// so those re-reads of a neighbour's rows meet in one L2.  Every other Q, K,
-// V, dO row crosses HBM once; dQ, dK, dV are written once, with one writer
-// per row.
+// block before its first step.  On the shifted grid, chunks are dealt to
+// XCDs in contiguous runs, so those re-reads of a neighbour's rows meet in one
+// L2; the causal window runs its chunks in dispatch order (measured faster).
+// Every other Q, K, V, dO row crosses HBM once; dQ, dK, dV are written once,
+// with one writer per row.
 //
 // Rows outside the residue class read as zero.  Keys outside it are masked;
 // a query row past the end (zero dO) adds nothing to dK, dV, and gets
@@ -262,11 +263,13 @@ __global__ __launch_bounds__(256, 2) void bwd_fused_kernel(BwdArgs a) {
   using B = FusedBand<FL, FR>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // FusedLds
   using Elt = typename P::Elt;
-  // chunks dealt to XCDs in contiguous runs (neighbouring chunks share an
-  // L2); a dilated window's residue classes, which interleave row by row in
-  // memory, run side by side on different XCDs as dispatched (cfg5 bf16
-  // backward 120.3 -> 115.0 us)
-  int lin = a.dil == 1 ? xcd_row_order(blockIdx.x, gridDim.x) : (int)blockIdx.x;
+  // The shifted grid's chunks are dealt to XCDs in contiguous runs
+  // (neighbouring chunks share an L2: [i-32, i+31] at B4 H8 N8192, 53.6 us
+  // against 61.5 us as dispatched).  The causal window runs best as
+  // dispatched: a dilated window's residue classes, which interleave row by
+  // row in memory, side by side on different XCDs (cfg5 bf16 backward 120.3
+  // -> 115.0 us), and at dilation 1 112.4 against 114.5 us at the target.
+  int lin = a.dil == 1 && FR > 0 ? xcd_row_order(blockIdx.x, gridDim.x) : (int)blockIdx.x;
   const int chunk_id = lin % a.chunks;
   lin /= a.chunks;
   const int rho = lin % a.dil;
@@ -391,7 +394,7 @@ __global__ __launch_bounds__(256, 2) void bwd_fused_kernel(BwdArgs a) {
 template <int FL, int FR>
 __global__ __launch_bounds__(256) void bwd_probe_kernel(BwdArgs a) {
   using B = FusedBand<FL, FR>;
-  int lin = a.dil == 1 ? xcd_row_order(blockIdx.x, gridDim.x) : (int)blockIdx.x;
+  int lin = a.dil == 1 && FR > 0 ? xcd_row_order(blockIdx.x, gridDim.x) : (int)blockIdx.x;  // as the kernel
   const int chunk_id = lin % a.chunks;
   lin /= a.chunks;
   const int rho = lin % a.dil;
