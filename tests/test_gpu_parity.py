@@ -132,6 +132,16 @@ def test_narrow_head_geometry(ext, oracle, N, D, left, right, dtype):
     assert _max_err(y, oracle.forward(spec, *up)) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("shape,left,right,dtype", [((2, 16384, 8, 16), 63, 0, torch.float32),
+                                                    ((1, 9000, 64, 24), 40, 20, torch.bfloat16)])
+def test_narrow_head_large_grid(ext, oracle, shape, left, right, dtype):
+    """head_dim <= 32 on large grids (thousands of workgroups), against the oracle."""
+    (q, k, v), up = _inputs(shape, 1700 + shape[1], dtype)
+    y = ext.sliding_forward(q, k, v, left, right)
+    spec = oracle.Spec(*shape, pattern="sliding", left=left, right=right)
+    assert _max_err(y, oracle.forward(spec, *up)) <= TOL[dtype]
+
+
 # ------------------------------------------------------- block-sparse and Longformer kernels
 
 def _random_table(nb, width, seed, rng_extra_pad=True):
