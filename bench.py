@@ -444,6 +444,10 @@ def main() -> int:
     ap.add_argument("--workload", default="target", choices=sorted(WORKLOADS) + ["ticks", "encoder_layer"])
     ap.add_argument("--sets", type=int, default=0, help="input sets rotated (0: enough for >1 GB)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--configs", dest="configs", action="store_true", default=None,
+                    help="also measure every BASELINE config's forward (cfg1, cfg2 fp32/bf16, cfg3, cfg4, "
+                         "cfg5 fp32/bf16) into the line's `configs` object (default: on for the target forward)")
+    ap.add_argument("--no-configs", dest="configs", action="store_false")
     ap.add_argument("--layer-form", choices=["both", "fused", "ops"], default="both",
                     help="encoder_layer workload: time both model forms (default) or only one")
     ap.add_argument("--pass", dest="which", choices=["forward", "backward"], default="forward",
@@ -467,25 +471,28 @@ def main() -> int:
     if args.workload == "encoder_layer":
         return bench_encoder(args)
 
+    return bench_attention(args)
+
+
+def measure(workload: str, which: str = "forward", saved: bool = False, steps: int = 200, warmup=None,
+            nsets_arg: int = 0) -> dict:
+    """One attention workload on cuda:0: the bench line's fields without the
+    CPU baseline and the box copy rate.  Inputs are built here (enough
+    rotated sets for > 1 GB, at least 4) and freed before returning."""
     import torch
     import sparse_attention_cuda as ext
 
-    if not torch.cuda.is_available():
-        print("bench.py: no HIP device visible", file=sys.stderr)
-        return 1
-    B, H, N, D, dt_name, pk, desc = WORKLOADS[args.workload]
-    bwd = args.which == "backward"
-    saved = bwd and args.saved_stats
+    B, H, N, D, dt_name, pk, desc = WORKLOADS[workload]
+    bwd = which == "backward"
     dtype = {"bf16": torch.bfloat16, "fp32": torch.float32}[dt_name]
     elt = 2 if dt_name == "bf16" else 4
     dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
 
     # tensors touched per step: Q, K, V, O (forward); Q, K, V, dO, dQ, dK, dV (backward; and O from
     # saved statistics)
     tensors = 8 if saved else (7 if bwd else 4)
     set_bytes = tensors * B * N * H * D * elt
-    nsets = args.sets or max(4, -(-(1 << 30) // set_bytes))
+    nsets = nsets_arg or max(4, -(-(1 << 30) // set_bytes))
     gen = torch.Generator(device=dev)
     gen.manual_seed(1234)
     sets = []
@@ -548,7 +555,7 @@ def main() -> int:
         launch = lambda s: ext.longformer_forward(s[0], s[1], s[2], pk["left"], pk["right"], pk["num_global"])
 
     # output buffers come from the caching allocator, so steady-state launches allocate nothing new
-    args.warmup = run_warmup(args.warmup, lambda i: launch(sets[i % nsets]))
+    warmup = run_warmup(warmup, lambda i: launch(sets[i % nsets]))
     torch.cuda.synchronize()
 
     # Timed region: K back-to-back launches on the launch stream between two
@@ -558,23 +565,23 @@ def main() -> int:
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_start.record(stream)
-    for i in range(args.steps):
+    for i in range(steps):
         launch(sets[i % nsets])
     t_end.record(stream)
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
-    ms_per_step = total_ms / args.steps
+    ms_per_step = total_ms / steps
     # Kernel durations: K more launches, each stamping its kernels' own start
     # and stop on an event pair (hipExtLaunchKernel through ma_attn_*_timed,
     # stamped on the dispatch packets).  The stamping slows the launch
     # sequence, so it stays out of the region above; the roofline uses these
     # durations.
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     for a, b in ev:  # create the events before they are stamped
         a.record(stream)
         b.record(stream)
     torch.cuda.synchronize()
-    for i in range(args.steps):
+    for i in range(steps):
         with ext.kernel_events(*ev[i]):
             launch(sets[i % nsets])
     torch.cuda.synchronize()
@@ -609,12 +616,12 @@ def main() -> int:
                 s_ = sets[i % nsets]
                 _ma.copy_probe_raw(pdesc, s_[0].data_ptr(), s_[1].data_ptr(), s_[2].data_ptr(), pout.data_ptr(), raw)
             pev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                   for _ in range(args.steps)]
+                   for _ in range(steps)]
             for a_, b_ in pev:
                 a_.record(stream)
                 b_.record(stream)
             torch.cuda.synchronize()
-            for i in range(args.steps):
+            for i in range(steps):
                 s_ = sets[i % nsets]
                 _ma.copy_probe_raw(pdesc, s_[0].data_ptr(), s_[1].data_ptr(), s_[2].data_ptr(), pout.data_ptr(), raw,
                                    (pev[i][0].cuda_event, pev[i][1].cuda_event))
@@ -640,12 +647,12 @@ def main() -> int:
             for i in range(20):
                 bprobe(sets[i % nsets])
             pev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                   for _ in range(args.steps)]
+                   for _ in range(steps)]
             for a_, b_ in pev:
                 a_.record(stream)
                 b_.record(stream)
             torch.cuda.synchronize()
-            for i in range(args.steps):
+            for i in range(steps):
                 bprobe(sets[i % nsets], (pev[i][0].cuda_event, pev[i][1].cuda_event))
             torch.cuda.synchronize()
             probe_us = 1e3 * sum(a_.elapsed_time(b_) for a_, b_ in pev) / len(pev)
@@ -669,10 +676,8 @@ def main() -> int:
     # forward: Q.K^T and P.V; backward: S, dP = dO.V^T, dV, dQ, dK (2 FLOP per MAC)
     flops = (10 if bwd else 4) * D * key_count(N, pk) * B * H
     achieved_gbps = alg_bytes / (mean_launch_ms * 1e-3) / 1e9
-    tkey = args.workload + ("_backward_saved" if saved else ("_backward" if bwd else ""))
+    tkey = workload + ("_backward_saved" if saved else ("_backward" if bwd else ""))
     traffic = load_traffic(tkey)
-
-    copy_gbps = copy_bandwidth(dev, stream)
 
     # the bound is whichever peak the algorithmic work reaches first
     mfma_peak = MFMA_BF16_PEAK_TFLOPS if dt_name == "bf16" else MFMA_F32_PEAK_TFLOPS
@@ -691,8 +696,8 @@ def main() -> int:
         "value": queries / (ms_per_step * 1e-3),
         "unit": "queries/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",
@@ -713,9 +718,8 @@ def main() -> int:
         "tflops": flops / (mean_launch_ms * 1e-3) / 1e12,
         "mfma_bf16_frac_of_peak": (flops / (mean_launch_ms * 1e-3) / 1e12) / MFMA_BF16_PEAK_TFLOPS,
         # rocprofv3 MfmaUtil of the forward kernel (committed summary), not measured in this run
-        "mfma_busy_pct": None if bwd else load_mfma_busy(args.workload),
+        "mfma_busy_pct": None if bwd else load_mfma_busy(workload),
         "mfma_busy_source": None if bwd else "profiles/mfma_busy_by_workload.md (rocprofv3 MfmaUtil, committed)",
-        "copy_kernel_gbps": copy_gbps,
         "device": torch.cuda.get_device_name(dev),
     }
     if probe_us is not None:
@@ -727,7 +731,57 @@ def main() -> int:
                                "source": probe_src}
     if bwd:
         out["pass"] = "backward_saved_statistics" if saved else "backward"
-    if not args.no_cpu_baseline and not bwd:
+    del sets, launch
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
+
+
+# The BASELINE.json configs measured beside the headline in the default run
+# (the forward pass of each; cfg2 and cfg5 in both dtypes).
+CONFIG_LINES = ("cfg1", "cfg2_fp32", "cfg2_bf16", "cfg3", "cfg4", "cfg5_fp32", "cfg5_bf16")
+
+
+def config_entry(r: dict) -> dict:
+    """The per-config summary kept in the headline line's ``configs``."""
+    pc = r.get("pattern_copy")
+    traffic = r["roofline"].get("traffic")
+    return {
+        "workload": r["config"]["workload"], "dtype": r["dtype"],
+        "kernel_us_mean": r["kernel_us_mean"], "kernel_us_median": r["kernel_us_median"],
+        "step_us_mean": r["step_us_mean"], "queries_per_s": r["value"],
+        "hbm_gbps": r["hbm_gbps"], "frac": r["hbm_frac_of_peak"], "tflops": r["tflops"],
+        "pattern_copy": None if pc is None else {"kernel_us_mean": pc["kernel_us_mean"],
+                                                 "kernel_frac_of_pattern_copy": pc["kernel_frac_of_pattern_copy"]},
+        "traffic_ratio": None if traffic is None else traffic / r["algorithmic_bytes_per_launch"],
+        "traffic_source": r["roofline"].get("traffic_source"),
+        "steps": r["steps"], "warmup": r["warmup"],
+    }
+
+
+def bench_attention(args) -> int:
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    saved = args.which == "backward" and args.saved_stats
+    out = measure(args.workload, args.which, saved, args.steps, args.warmup, args.sets)
+    with_configs = args.configs if args.configs is not None else (
+        args.workload == "target" and args.which == "forward")
+    if with_configs:
+        # every BASELINE config's forward under the same clock, after the headline
+        t0 = time.perf_counter()
+        out["configs"] = {}
+        for name in CONFIG_LINES:
+            out["configs"][name] = config_entry(measure(name, "forward", False, args.steps, None, 0))
+        out["configs_wall_s"] = time.perf_counter() - t0
+    out["copy_kernel_gbps"] = copy_bandwidth(dev, torch.cuda.current_stream(dev))
+    if not args.no_cpu_baseline and args.which == "forward":
+        B, H, N, D, dt_name, pk, _ = WORKLOADS[args.workload]
         out["cpu_baseline"] = cpu_baseline(B, H, N, D, dt_name, pk)
     print(json.dumps(out), flush=True)
     return 0

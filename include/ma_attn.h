@@ -275,10 +275,12 @@ int64_t ma_attn_pattern_csr(const ma_attn_desc* desc, const int32_t* host_block_
  * ma_attn_forward for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * No counterpart in the reference.  It takes no workspace and allocates
- * nothing: the only kernel that needs scratch (the Longformer stream kernel's
- * per-chunk partials, ma_attn_workspace_size(desc) bytes) uses a static device
- * array of MA_ATTN_NOALLOC_SCRATCH_BYTES that the library holds on every GPU
- * it runs on until the process ends.  A call needing more is rejected with a
+ * nothing: the two forward kernels that need scratch, the Longformer stream
+ * kernel (its per-chunk partials of the global rows) and the tiled index-set
+ * kernel (the partial results of a tile plan's split rows), take their
+ * ma_attn_workspace_size(desc) bytes from a static device array of
+ * MA_ATTN_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it runs
+ * on until the process ends.  A call needing more is rejected with a
  * message and launches nothing.  Every call on one GPU shares that GPU's
  * array: calls that overlap on one GPU (concurrent streams or threads) race.
  * Outputs are identical to ma_attn_forward's on the same inputs.

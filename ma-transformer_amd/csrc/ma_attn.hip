@@ -28,6 +28,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <algorithm>
+#include <atomic>
 #include <cstring>
 #include <mutex>
 #include <set>
@@ -1696,28 +1697,33 @@ int launch_backward(const ma_attn_desc* d, const void* q, const void* k, const v
 // Device address of `scratch` on the stream's device, looked up once per
 // device with that device current.
 constexpr int kMaxDevices = 64;
-std::once_flag g_scratch_once[kMaxDevices];
-void* g_scratch_ptr[kMaxDevices];
-hipError_t g_scratch_err[kMaxDevices];
+std::mutex g_scratch_mutex;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
 
+// The device address of `scratch` on the stream's device.  Only a successful
+// lookup is kept: after a failure (hipSetDevice, hipGetSymbolAddress) the next
+// call looks it up again.
 int scratch_of_stream(hipStream_t st, void** out) {
   int dev = 0;
   if (stream_device(st, &dev)) return 1;
   if (dev < 0 || dev >= kMaxDevices) return fail("ma_attn: device %d out of range", dev);
-  std::call_once(g_scratch_once[dev], [dev] {
-    int cur = 0;
-    hipError_t e = hipGetDevice(&cur);
-    if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
-    void* ptr = nullptr;
-    if (e == hipSuccess) e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    if (cur != dev) (void)hipSetDevice(cur);
-    g_scratch_err[dev] = e;
-    g_scratch_ptr[dev] = e == hipSuccess ? ptr : nullptr;
-  });
-  if (g_scratch_err[dev] != hipSuccess || !g_scratch_ptr[dev])
-    return fail("ma_attn: cannot locate the static scratch on device %d: %s", dev,
-                hipGetErrorString(g_scratch_err[dev]));
-  *out = g_scratch_ptr[dev];
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!ptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    ptr = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!ptr) {
+      int cur = 0;
+      hipError_t e = hipGetDevice(&cur);
+      if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+      if (e == hipSuccess) e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      if (cur != dev) (void)hipSetDevice(cur);
+      if (e != hipSuccess || !ptr)
+        return fail("ma_attn: cannot locate the static scratch on device %d: %s", dev,
+                    hipGetErrorString(e != hipSuccess ? e : hipErrorInvalidSymbol));
+      g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
   return 0;
 }
 

@@ -33,7 +33,7 @@ from __future__ import annotations
 
 import os
 import sys
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from typing import Optional, Tuple
 
 import torch
@@ -77,6 +77,32 @@ class PatternSpec:
     block_table: Optional[torch.Tensor] = None
     num_global: int = 0
     index_set: Optional[object] = None  # IndexSet or (offsets, keys)
+    # device-side forms built on first use and kept: (device, seq_len) ->
+    # BlockTable (block_sparse) or IndexSet (index_set given as a CSR pair)
+    device_forms: dict = field(default_factory=dict, compare=False, hash=False, repr=False)
+
+    def native_table(self, seq_len: int, device):
+        """The block table as a BlockTable for (seq_len, device): checked and
+        uploaded once; its key sets (pattern_index_set) are then built once too."""
+        key = ("table", int(seq_len), str(device))
+        hit = self.device_forms.get(key)
+        if hit is None:
+            hit = self.device_forms[key] = sparse_attention_cuda.BlockTable(
+                self.block_table, seq_len, self.block_size, device)
+        return hit
+
+    def native_index_set(self, seq_len: int, device):
+        """The index set as an IndexSet on device (a CSR pair is converted once)."""
+        s = self.index_set
+        if not isinstance(s, (tuple, list)):  # an IndexSet already
+            return s
+        key = ("set", int(seq_len), str(device))
+        hit = self.device_forms.get(key)
+        if hit is None:
+            offsets, keys = s
+            hit = self.device_forms[key] = sparse_attention_cuda.IndexSet(
+                torch.as_tensor(offsets), torch.as_tensor(keys), seq_len, device)
+        return hit
 
     def _csr(self, device):
         s = self.index_set
@@ -115,14 +141,17 @@ class PatternSpec:
 
 def _pattern_set(spec: PatternSpec, seq_len: int, device):
     """The explicit key sets the native backward of a block-sparse, Longformer
-    or index-set pattern runs on (pattern_index_set builds and caches them)."""
+    or index-set pattern runs on, built on the first step and kept: on the
+    spec's BlockTable (block-sparse), in pattern_index_set's geometry cache
+    (Longformer), or on the spec (an index set given as a CSR pair)."""
     ext = sparse_attention_cuda
     if spec.pattern == "index_set":
-        return spec.index_set
-    kw = (dict(block_table=spec.block_table, block_size=spec.block_size)
-          if spec.pattern == "block_sparse" else
-          dict(left=spec.left, right=spec.right, num_global=spec.num_global))
-    return ext.pattern_index_set(spec.pattern, seq_len, device, **kw)
+        return spec.native_index_set(seq_len, device)
+    if spec.pattern == "block_sparse":
+        return ext.pattern_index_set("block_sparse", seq_len, device,
+                                     block_table=spec.native_table(seq_len, device), block_size=spec.block_size)
+    return ext.pattern_index_set(spec.pattern, seq_len, device, left=spec.left, right=spec.right,
+                                 num_global=spec.num_global)
 
 
 def _saved_statistics_pay(iset) -> bool:
@@ -161,10 +190,11 @@ def _native_forward(q, k, v, sparse, window_size, use_causal_mask, spec: Optiona
             causal = bool(use_causal_mask) if spec is None else spec.causal
             return ext.dense_forward(cq, ck, cv, causal, return_lse=True)
         if spec.pattern == "block_sparse":
-            return ext.block_sparse_forward(cq, ck, cv, spec.block_table, spec.block_size, return_lse=True)
+            return ext.block_sparse_forward(cq, ck, cv, spec.native_table(cq.shape[1], cq.device), spec.block_size,
+                                            return_lse=True)
         if spec.pattern == "longformer":
             return ext.longformer_forward(cq, ck, cv, spec.left, spec.right, spec.num_global, return_lse=True)
-        return ext.index_set_forward(cq, ck, cv, spec.index_set, return_lse=True)
+        return ext.index_set_forward(cq, ck, cv, spec.native_index_set(cq.shape[1], cq.device), return_lse=True)
     if spec is None:
         if sparse:
             return ext.forward(cq, ck, cv, int(window_size))
@@ -174,11 +204,11 @@ def _native_forward(q, k, v, sparse, window_size, use_causal_mask, spec: Optiona
     if spec.pattern == "dense":
         return ext.dense_forward(cq, ck, cv, spec.causal)
     if spec.pattern == "block_sparse":
-        return ext.block_sparse_forward(cq, ck, cv, spec.block_table, spec.block_size)
+        return ext.block_sparse_forward(cq, ck, cv, spec.native_table(cq.shape[1], cq.device), spec.block_size)
     if spec.pattern == "longformer":
         return ext.longformer_forward(cq, ck, cv, spec.left, spec.right, spec.num_global)
     if spec.pattern == "index_set":
-        return ext.index_set_forward(cq, ck, cv, spec.index_set)
+        return ext.index_set_forward(cq, ck, cv, spec.native_index_set(cq.shape[1], cq.device))
     raise ValueError(f"unknown pattern {spec.pattern}")
 
 
@@ -204,6 +234,9 @@ class MACoreAttentionFunction(torch.autograd.Function):
 
     Reference: src/layers/ma_core_bridge.py:44-154.  The extra trailing
     argument ``spec`` (a PatternSpec or None) selects a non-reference pattern.
+    Device-side pattern data (a block-sparse pattern's BlockTable and the key
+    sets of its backward, an index set given as a CSR pair) is built on the
+    first call and kept on the PatternSpec, so later steps only launch.
     """
 
     @staticmethod
@@ -259,10 +292,8 @@ class MACoreAttentionFunction(torch.autograd.Function):
                     dQ, dK, dV = ext.dense_backward(cq, ck, cv, cgo, causal, out=out, lse=lse)
             elif spec is not None and spec.pattern == "sliding":
                 dQ, dK, dV = ext.sliding_backward(cq, ck, cv, cgo, spec.left, spec.right, spec.dilation)
-            elif spec is not None and spec.pattern == "index_set":
-                dQ, dK, dV = ext.index_set_backward(cq, ck, cv, cgo, spec.index_set)
-            elif spec is not None and spec.pattern in ("block_sparse", "longformer"):
-                # the pattern's key sets as an explicit set (built once, cached)
+            elif spec is not None and spec.pattern in ("index_set", "block_sparse", "longformer"):
+                # the pattern's key sets as an explicit set (built on the first step, kept)
                 dQ, dK, dV = ext.index_set_backward(cq, ck, cv, cgo, _pattern_set(spec, cq.shape[1], cq.device))
             elif spec is not None:
                 dQ, dK, dV = ext.dense_backward(cq, ck, cv, cgo, spec.causal)
@@ -405,7 +436,9 @@ class MACoreAttention(nn.Module):
         if pattern == "block_sparse":
             if table is None:
                 raise ValueError("block_sparse pattern needs block_table")
-            table = torch.as_tensor(table, dtype=torch.int32)
+            if isinstance(table, getattr(sparse_attention_cuda, "BlockTable", ())):
+                table = table.host  # its checked host copy; the device form is rebuilt per device
+            table = torch.as_tensor(table, dtype=torch.int32).cpu()
         if pattern == "index_set" and index_set is None:
             raise ValueError("index_set pattern needs index_set")
         if pattern == "dense":

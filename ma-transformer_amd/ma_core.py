@@ -31,9 +31,14 @@ What runs where:
   closed forms in one C-ABI call (ma_attn_pattern_csr): the entries of
   src/csrc/ma_core.cpp:34-48, in the same (row, col) order.
 
-One difference: the reference accepts a value head_dim different from the
-query's (its output takes the value's, ma_core.cpp:86-90); these kernels take
-Q, K and V of one shape, so a differing value shape raises RuntimeError.
+A value head_dim different from the query's is accepted, as the reference
+does (its output takes the value's, ma_core.cpp:84-90, :178-183): the kernels
+take Q, K and V of one head_dim, so the narrower operands are zero-padded to
+the wider one on the device and the scale is passed as 1/sqrtf(query
+head_dim).  Zero columns add exact zeros to every dot product and give zero
+output columns, which are sliced off.  K and V may carry more batches or heads
+than Q (the reference indexes them with their own shapes and reads only Q's
+range); fewer raise RuntimeError, where the reference would read past them.
 """
 from __future__ import annotations
 
@@ -246,22 +251,42 @@ def _check_qkv(query, key, value):
         raise RuntimeError("Query, key, and value must have same sequence length")
     if qs[3] != ks[3]:
         raise RuntimeError("Query and key must have same head dimension")
-    if not (qs == ks == vs):
-        raise RuntimeError("Query, key, and value must have identical shapes [batch, seq, heads, dim] "
-                           "on the MI355X engine")
+    # the reference reads K and V at Q's (batch, head) range with their own
+    # strides (tensor.cpp:104-114): fewer batches or heads than Q is out of range
+    if min(ks[0], vs[0]) < qs[0] or min(ks[2], vs[2]) < qs[2]:
+        raise RuntimeError("Key and value must have at least the query's batch size and number of heads")
 
 
 def _on_engine(query: Tensor, key: Tensor, value: Tensor, run) -> Tensor:
-    """Stage Q, K, V to the current GPU, run the kernels, copy O back."""
-    if query._data.size == 0:
-        return Tensor(np.zeros(query._data.shape, dtype=np.float32))
+    """Stage Q, K, V to the current GPU, run the kernels, copy O back.
+
+    O is [batch, seq, heads, value head_dim].  run(ext, q, k, v, scale) gets
+    device tensors of one shape and scale None (1/sqrtf(head_dim)) or, when
+    the head_dims were padded, the query head_dim's 1/sqrtf (ma_core.cpp:188)."""
+    B, N, H, D = query._data.shape
+    Dv = value._data.shape[3]
+    if B * N * H * Dv == 0:
+        return Tensor(np.zeros((B, N, H, Dv), dtype=np.float32))
     if not torch.cuda.is_available():
         raise RuntimeError("ma_core: attention runs on the MI355X engine (libma_attn.so); no GPU is visible")
     import sparse_attention_cuda as ext
     dev = torch.device("cuda", torch.cuda.current_device())
-    tq, tk, tv = (torch.from_numpy(t._data).to(dev) for t in (query, key, value))
-    out = run(ext, tq, tk, tv)
-    return Tensor(out.cpu().numpy())
+
+    def staged(t: Tensor, width: int) -> torch.Tensor:
+        x = t._data[:B, :, :H, :]  # Q's (batch, head) range
+        if x.shape[3] == width:
+            return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+        y = torch.zeros((B, N, H, width), dtype=torch.float32, device=dev)
+        y[..., :x.shape[3]] = torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+        return y
+
+    width = max(D, Dv)
+    tq, tk, tv = staged(query, width), staged(key, width), staged(value, width)
+    scale = None if D == width else float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    out = run(ext, tq, tk, tv, scale)
+    if Dv != width:
+        out = out[..., :Dv]
+    return Tensor(np.ascontiguousarray(out.cpu().numpy()))
 
 
 def compute_dense_attention(query: Tensor, key: Tensor, value: Tensor,
@@ -270,7 +295,8 @@ def compute_dense_attention(query: Tensor, key: Tensor, value: Tensor,
     (keys [0, S), or [0, i] with the causal mask)."""
     _check_qkv(query, key, value)
     causal = bool(use_causal_mask)
-    return _on_engine(query, key, value, lambda ext, q, k, v: ext.dense_forward(q, k, v, causal))
+    return _on_engine(query, key, value,
+                      lambda ext, q, k, v, scale: ext.dense_forward(q, k, v, causal, scale=scale))
 
 
 def compute_sparse_attention(query: Tensor, key: Tensor, value: Tensor, window_size: int = 64) -> Tensor:
@@ -278,7 +304,8 @@ def compute_sparse_attention(query: Tensor, key: Tensor, value: Tensor, window_s
     ma_core.cpp:160-246 on the GPU (w = 0 gives O = V, w < 0 an all-zero O)."""
     _check_qkv(query, key, value)
     w = _as_int64(window_size, "compute_sparse_attention")
-    return _on_engine(query, key, value, lambda ext, q, k, v: ext.forward(q, k, v, w))
+    return _on_engine(query, key, value,
+                      lambda ext, q, k, v, scale: ext.sliding_forward(q, k, v, w, w, 1, scale=scale))
 
 
 __all__ = ["add", "create_tensor", "create_random_tensor", "create_sliding_window_pattern",

@@ -47,8 +47,16 @@ class PositionalEncoding(nn.Module):
         return x + self.pe[:x.size(0), :]
 
 
+# model widths the fused layer kernel is instantiated for (d_ff = 4 * d_model)
+_FUSED_WIDTHS = (16, 32, 64, 128)
+
+
 def _fused_applies(layer: nn.Module, src: torch.Tensor) -> bool:
+    """Whether ``layer`` runs as the fused kernel on ``src``; otherwise it runs
+    its separate operations."""
     if not (src.is_cuda and src.dtype == torch.float32) or src.dim() != 3:
+        return False
+    if layer.linear1.in_features not in _FUSED_WIDTHS or layer.linear1.out_features != 4 * layer.linear1.in_features:
         return False
     if layer.training and any(m.p > 0 for m in (layer.dropout, layer.dropout1, layer.dropout2)):
         return False

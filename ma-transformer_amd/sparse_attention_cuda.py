@@ -158,22 +158,34 @@ def forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
     return _launch(query, key, value, _ma.SLIDING, left=w, right=w, dilation=1)
 
 
+def _scale_kw(scale) -> dict:
+    """The descriptor's softmax scale: None keeps 1/sqrtf(head_dim)."""
+    if scale is None:
+        return {}
+    s = float(scale)
+    if not (s > 0.0 and s != float("inf")):
+        raise RuntimeError("scale must be finite and > 0")
+    return {"scale": s}
+
+
 def dense_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
-                  use_causal_mask: bool = False, return_lse: bool = False):
+                  use_causal_mask: bool = False, return_lse: bool = False, scale=None):
     """Dense (optionally causal) forward.  Reference: dense_forward_cuda (:348-382).
     return_lse: also return each row's softmax statistic (float32 [B, S, H])
-    for dense_backward(..., out=, lse=); head_dim 64."""
-    return _launch(query, key, value, _ma.DENSE, return_lse, causal=bool(use_causal_mask))
+    for dense_backward(..., out=, lse=); head_dim 64.
+    scale: softmax scale (None: 1/sqrtf(head_dim), as the reference)."""
+    return _launch(query, key, value, _ma.DENSE, return_lse, causal=bool(use_causal_mask), **_scale_kw(scale))
 
 
 def sliding_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
-                    left: int, right: int, dilation: int = 1) -> torch.Tensor:
+                    left: int, right: int, dilation: int = 1, scale=None) -> torch.Tensor:
     """Keys {i + dilation*t : -left <= t <= right} inside [0, S).
 
     causal window w: left=w-1, right=0; the reference's symmetric w: left=right=w.
+    scale: softmax scale (None: 1/sqrtf(head_dim)).
     """
     return _launch(query, key, value, _ma.SLIDING, left=int(left), right=int(right),
-                   dilation=int(dilation))
+                   dilation=int(dilation), **_scale_kw(scale))
 
 
 def make_block_table(seed: int, num_blocks: int, random_per_row: int = 2) -> torch.Tensor:
@@ -374,7 +386,8 @@ def pattern_index_set(pattern: str, seq_len: int, device, **kw) -> IndexSet:
     backward (index_set_backward) is the exact gradient of that pattern's
     forward.  A BlockTable keeps its set (built on first use, no host transfer
     after that); Longformer sets are cached per geometry and device; a plain
-    tensor table is copied to the host and enumerated at every call."""
+    tensor table is copied to the host at every call (from the device, a
+    synchronising copy) and its set is cached on the table's contents."""
     if pattern == "block_sparse":
         table = kw.pop("block_table")
         bs = int(kw.pop("block_size", 64))
@@ -387,8 +400,14 @@ def pattern_index_set(pattern: str, seq_len: int, device, **kw) -> IndexSet:
                                                          block_size=bs)
             return hit
         nb = (int(seq_len) + bs - 1) // bs
-        return _enumerated_set(_ma.BLOCK_SPARSE, seq_len, device, _validated_table(torch.as_tensor(table), nb),
-                               block_size=bs)
+        host = _validated_table(torch.as_tensor(table), nb)
+        key = ("block_sparse", int(seq_len), bs, str(device), tuple(host.shape), host.numpy().tobytes())
+        hit = _pattern_sets.get(key)
+        if hit is None:
+            if len(_pattern_sets) > 16:
+                _pattern_sets.clear()
+            hit = _pattern_sets[key] = _enumerated_set(_ma.BLOCK_SPARSE, seq_len, device, host, block_size=bs)
+        return hit
     if pattern != "longformer":
         raise ValueError(f"no closed-form index set for pattern {pattern!r}")
     key = (int(seq_len), str(device), tuple(sorted(kw.items())))

@@ -154,6 +154,26 @@ def forward(spec: Spec, q, k, v, heads=None, rows=None) -> np.ndarray:
     return o
 
 
+def forward_value_dim(spec: Spec, q, k, v) -> np.ndarray:
+    """``forward`` for V with a head_dim Dv of its own (q, k [B,N,H,D], v
+    [B,N,H,Dv] -> o [B,N,H,Dv]), as ma_core.cpp:160-246 computes it: scores
+    and scale from D (:188), one weighted sum per value column (:232-239).  V
+    runs through ``forward`` in blocks of D columns (the last one zero-padded);
+    a column's sum does not depend on the other columns, so each block gives
+    its columns' exact values."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    B, N, H, D = q.shape
+    Dv = v.shape[3]
+    o = np.empty((B, N, H, Dv), dtype=np.float32)
+    for c0 in range(0, Dv, max(D, 1)):
+        c1 = min(Dv, c0 + D)
+        vb = np.zeros(q.shape, dtype=np.float32)
+        vb[..., :c1 - c0] = v[..., c0:c1]
+        o[..., c0:c1] = forward(spec, q, k, vb)[..., :c1 - c0]
+    return o
+
+
 def backward(spec: Spec, q, k, v, dout):
     """fp32 oracle backward (restated sparse_attention_kernel.cu:265-346) -> (dq, dk, dv)."""
     lib = _load()
@@ -272,6 +292,10 @@ def _load_ref():
             getattr(lib, name).restype = ctypes.c_int
         lib.ref_sparse_forward.argtypes = [ctypes.c_int64] * 5 + [ctypes.c_void_p] * 4
         lib.ref_dense_forward.argtypes = [ctypes.c_int64] * 4 + [ctypes.c_int] + [ctypes.c_void_p] * 4
+        lib.ref_sparse_forward_v.restype = ctypes.c_int
+        lib.ref_sparse_forward_v.argtypes = [ctypes.c_int64] * 6 + [ctypes.c_void_p] * 4
+        lib.ref_dense_forward_v.restype = ctypes.c_int
+        lib.ref_dense_forward_v.argtypes = [ctypes.c_int64] * 5 + [ctypes.c_int] + [ctypes.c_void_p] * 4
         lib.ref_sliding_pattern.restype = ctypes.c_int64
         lib.ref_sliding_pattern.argtypes = [ctypes.c_int64, ctypes.c_int64,
                                             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
@@ -310,6 +334,26 @@ def ref_dense_forward(q, k, v, causal: bool) -> np.ndarray:
     if lib.ref_dense_forward(B, N, H, D, int(bool(causal)), q.ctypes.data, k.ctypes.data,
                              v.ctypes.data, o.ctypes.data) != 0:
         raise RuntimeError("reference compute_dense_attention raised")
+    return o
+
+
+def ref_forward_v(q, k, v, window=None, causal: bool = False) -> np.ndarray:
+    """The reference's compute_sparse_attention (window given) or
+    compute_dense_attention (window None) with a value head_dim of its own:
+    q, k [B,N,H,D], v [B,N,H,Dv] -> o [B,N,H,Dv] (ma_core.cpp:84-90, :178-183)."""
+    lib = _load_ref()
+    q, k, v = (np.ascontiguousarray(x, dtype=np.float32) for x in (q, k, v))
+    B, N, H, D = q.shape
+    Dv = v.shape[3]
+    o = np.empty((B, N, H, Dv), dtype=np.float32)
+    if window is None:
+        rc = lib.ref_dense_forward_v(B, N, H, D, Dv, int(bool(causal)), q.ctypes.data, k.ctypes.data,
+                                     v.ctypes.data, o.ctypes.data)
+    else:
+        rc = lib.ref_sparse_forward_v(B, N, H, D, Dv, int(window), q.ctypes.data, k.ctypes.data,
+                                      v.ctypes.data, o.ctypes.data)
+    if rc != 0:
+        raise RuntimeError("reference attention raised")
     return o
 
 

@@ -52,6 +52,33 @@ extern "C" int ref_dense_forward(int64_t B, int64_t N, int64_t H, int64_t D, int
   }
 }
 
+// The same two calls with a value head_dim Dv of its own (the reference sizes
+// O by the value's head_dim, ma_core.cpp:84-90, :178-183): q, k are
+// [B, N, H, D], v and o [B, N, H, Dv].
+extern "C" int ref_sparse_forward_v(int64_t B, int64_t N, int64_t H, int64_t D, int64_t Dv, int64_t w,
+                                    const float* q, const float* k, const float* v, float* o) {
+  try {
+    ma_core::Tensor tq = make(B, N, H, D, q), tk = make(B, N, H, D, k), tv = make(B, N, H, Dv, v);
+    ma_core::Tensor out = ma_core::compute_sparse_attention(tq, tk, tv, w);
+    out.copy_to(o, static_cast<size_t>(B * N * H * Dv) * sizeof(float));
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
+extern "C" int ref_dense_forward_v(int64_t B, int64_t N, int64_t H, int64_t D, int64_t Dv, int causal,
+                                   const float* q, const float* k, const float* v, float* o) {
+  try {
+    ma_core::Tensor tq = make(B, N, H, D, q), tk = make(B, N, H, D, k), tv = make(B, N, H, Dv, v);
+    ma_core::Tensor out = ma_core::compute_dense_attention(tq, tk, tv, causal != 0);
+    out.copy_to(o, static_cast<size_t>(B * N * H * Dv) * sizeof(float));
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
 // COO entries of create_sliding_window_pattern(N, w); returns nnz, writes up to cap.
 extern "C" int64_t ref_sliding_pattern(int64_t N, int64_t w, int64_t* rows, int64_t* cols,
                                        int64_t cap) {

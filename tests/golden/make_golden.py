@@ -9,6 +9,10 @@ so the committed numbers are the reference's bits, not this repo's:
   ref_sparse_s256_w64.npz (1,256,4,16) W=64, numpy PCG64 seed 7
   ref_sparse_s33_w0.npz   (2,33,2,16) W=0 (O must equal V)
   ref_dense_s32.npz       (1,32,2,16) causal and non-causal compute_dense_attention
+  ref_value_dim.npz       a value head_dim of its own: q, k (1,40,2,16), v_<Dv> (1,40,2,Dv)
+                          for Dv in 8, 24, 40 (numpy PCG64 seed 10); o_sparse_<Dv> from
+                          compute_sparse_attention(w=5), o_dense_<Dv> / o_causal_<Dv> from
+                          compute_dense_attention
   ref_patterns.npz        nnz of create_sliding_window_pattern for
                           (4,4), (4,10), (16,3), (2,1), (1024,64), and the (row, col)
                           entries for the small (N, w) cases listed in `small`
@@ -58,6 +62,8 @@ def main():
     np.savez(os.path.join(HERE, "ref_dense_s32.npz"), q=q, k=k, v=v,
              o_full=O.ref_dense_forward(q, k, v, False), o_causal=O.ref_dense_forward(q, k, v, True))
 
+    write_value_dim()
+
     cases = np.array([(4, 4), (4, 10), (16, 3), (2, 1), (1024, 64)], dtype=np.int64)
     nnz = np.array([len(O.ref_sliding_pattern(int(n), int(w))[0]) for n, w in cases], dtype=np.int64)
     # the COO entries themselves, in the reference's order, for the small cases
@@ -77,6 +83,20 @@ def main():
     O.block_table(1234, 256, 2).astype("<i4").tofile(
         os.path.join(HERE, "block_table_seed1234_nb256_r2.bin"))
     print("golden vectors written to", HERE)
+
+
+def write_value_dim():
+    """ref_value_dim.npz: the reference's outputs when V's head_dim differs from Q's."""
+    rng = np.random.default_rng(10)
+    q, k = (rng.standard_normal((1, 40, 2, 16), dtype=np.float32) for _ in range(2))
+    out = dict(q=q, k=k, w=np.int64(5))
+    for dv in (8, 24, 40):
+        v = rng.standard_normal((1, 40, 2, dv), dtype=np.float32)
+        out[f"v_{dv}"] = v
+        out[f"o_sparse_{dv}"] = O.ref_forward_v(q, k, v, window=5)
+        out[f"o_dense_{dv}"] = O.ref_forward_v(q, k, v, causal=False)
+        out[f"o_causal_{dv}"] = O.ref_forward_v(q, k, v, causal=True)
+    np.savez(os.path.join(HERE, "ref_value_dim.npz"), **out)
 
 
 if __name__ == "__main__":

@@ -246,6 +246,23 @@ def test_backward_target_shape(ext, oracle):
     _check(got, oracle.backward(spec, *up), torch.bfloat16)
 
 
+@pytest.mark.parametrize("shape,left,right,dil", [((4, 8192, 8, 64), 32, 31, 1), ((1, 65536, 8, 64), 63, 0, 4)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_backward_full_config_shapes_one_head(ext, oracle, shape, left, right, dil, dtype):
+    """cfg 2 (B=4 H=8 N=8192, [i-32, i+31]) and cfg 5 (B=1 H=8 N=65536,
+    dilation 4) at their full shapes, both dtypes: every gradient element of
+    heads 0 and H-1 against the oracle's backward of those heads (heads are
+    independent, so the oracle runs on them alone)."""
+    (q, k, v, g), up = _case(shape, 950 + left + dil, dtype)
+    got = ext.sliding_backward(q, k, v, g, left, right, dil)
+    H = shape[2]
+    for h in (0, H - 1):
+        one = [np.ascontiguousarray(a[:, :, h:h + 1]) for a in up]
+        spec = oracle.Spec(shape[0], shape[1], 1, shape[3], pattern="sliding", left=left, right=right, dilation=dil)
+        print(f"head {h}:", flush=True)
+        _check([t[:, :, h:h + 1] for t in got], oracle.backward(spec, *one), dtype)
+
+
 @pytest.mark.parametrize("left,right,dil", [(63, 0, 1), (32, 31, 1), (63, 0, 4)])
 def test_backward_sum_identities_full_size(ext, left, right, dil):
     """fp32 at B=1 H=8 N=65536 D=64: rows of P sum to 1 and rows of dS to 0,

@@ -168,3 +168,32 @@ def test_fused_layer_rejects(model_mod):
     out = torch.empty_like(src)
     with pytest.raises(RuntimeError, match="d_ff"):
         ma_attn.encoder_layer_forward_raw(L, src.data_ptr(), 0, out.data_ptr())
+
+
+def test_fused_model_other_width_runs_its_operations(model_mod):
+    """fused_layers=True with a model width the fused kernel has no
+    instantiation for (48): the layers run their separate operations, with the
+    unfused model's result."""
+    import sparse_attention_cuda as ext
+    torch.manual_seed(4)
+    fused = model_mod.TransformerModel(input_dim=5, model_dim=48, num_heads=2, num_layers=2,
+                                       fused_layers=True).cuda().eval()
+    plain = copy.deepcopy(fused)
+    for layer in plain.encoder_layers:
+        layer.fused = False
+    src = torch.randn(8, 10, 5, device="cuda")
+    calls = {"n": 0}
+    orig = ext.forward
+
+    def counting(*a, **kw):
+        calls["n"] += 1
+        return orig(*a, **kw)
+    ext.forward = counting
+    try:
+        with torch.no_grad():
+            y_fused = fused(src)
+            y_plain = plain(src)
+    finally:
+        ext.forward = orig
+    assert calls["n"] == 4  # two layers, each through the attention entry point, twice
+    assert torch.equal(y_fused, y_plain)

@@ -215,3 +215,48 @@ def test_layer_pattern_training_native(ext, oracle, monkeypatch, pattern, kw):
     assert calls == [1]
     for t, r in zip((q, k, v), oracle.backward(spec, *up, np.ones(shape, np.float32))):
         assert float(np.abs(t.grad.cpu().numpy() - r).max()) <= 1e-4
+
+
+def test_layer_block_sparse_builds_its_sets_once(ext, oracle, monkeypatch):
+    """The layer's block-sparse training path (MACoreAttention(pattern=
+    "block_sparse", fallback_training=False), bf16, N = 4096) builds its device
+    pattern data on the first step only: the checked BlockTable and the table's
+    key sets with their tile plan and transposed set.  Steps 2 and 3 run with
+    the table check, the set enumerator and the tile-plan builder made to
+    raise, and give the first step's output and gradients bit for bit; the
+    first step is checked against the oracle (one head)."""
+    import ma_attn
+    from layers.ma_core_bridge import MACoreAttention
+    N, shape = 4096, (1, 4096, 2, 64)
+    table = ext.make_block_table(1234, N // 64, 2)
+    dev, up = _inputs(shape, 9100, torch.bfloat16)
+    q, k, v = (t.clone().requires_grad_(True) for t in dev)
+    g = torch.from_numpy(qkv(shape, 9200)[0]).to(torch.bfloat16).cuda()
+    att = MACoreAttention(sparse=True, window_size=64, pattern="block_sparse", block_table=table,
+                          fallback_training=False).train()
+
+    def step():
+        for t in (q, k, v):
+            t.grad = None
+        out = att(q, k, v)
+        out.backward(g)
+        return [out.detach().clone()] + [t.grad.clone() for t in (q, k, v)]
+
+    first = step()
+    spec = oracle.Spec(1, N, 1, 64, pattern="block_sparse", block_size=64, table=table.numpy())
+    one = [np.ascontiguousarray(a[:, :, :1]) for a in up]
+    g1 = np.ascontiguousarray(g.float().cpu().numpy()[:, :, :1])
+    o_ref = oracle.forward(spec, *one)
+    assert float(np.abs(first[0][:, :, :1].float().cpu().numpy() - o_ref).max()) <= 2e-2
+    for name, got, ref in zip(("dq", "dk", "dv"), first[1:], oracle.backward(spec, *one, g1)):
+        check_grad(name, got[:, :, :1].float().cpu().numpy(), ref, False)
+
+    def boom(*a, **kw):
+        raise AssertionError("pattern data rebuilt after the first step")
+    for name in ("pattern_csr", "tile_plan", "tile_header_of"):
+        monkeypatch.setattr(ma_attn, name, boom)
+    monkeypatch.setattr(ext, "_validated_table", boom)
+    for _ in range(2):
+        again = step()
+        for a, b in zip(first, again):
+            assert torch.equal(a, b)

@@ -105,3 +105,50 @@ def test_random_tensors_through_engine(mc):
         assert (s.batch_size, s.sequence_length, s.num_heads, s.head_dim) == (2, 64, 4, 32)
         assert np.isfinite(out.to_numpy()).all()
     assert np.array_equal(before, q.to_numpy())
+
+
+@pytest.mark.parametrize("dv", [8, 24, 40])
+def test_value_head_dim_matches_reference_bits(mc, dv):
+    """V with a head_dim of its own (ma_core.cpp:84-90, :178-183): O takes the
+    value's head_dim; sparse (w=5), dense and causal against the reference's
+    own outputs (tests/golden/ref_value_dim.npz)."""
+    z = np.load(os.path.join(GOLDEN, "ref_value_dim.npz"))
+    q, k, v = _t(mc, z["q"]), _t(mc, z["k"]), _t(mc, z[f"v_{dv}"])
+    for name, out in (("sparse", mc.compute_sparse_attention(q, k, v, int(z["w"]))),
+                      ("dense", mc.compute_dense_attention(q, k, v, False)),
+                      ("causal", mc.compute_dense_attention(q, k, v, use_causal_mask=True))):
+        got = out.to_numpy()
+        ref = z[f"o_{name}_{dv}"]
+        assert got.shape == ref.shape
+        err = float(np.abs(got - ref).max())
+        print(f"Dv={dv} {name}: max|err| vs the reference's ma_core = {err:.3e}", flush=True)
+        assert err <= 1e-5
+
+
+@pytest.mark.parametrize("shape,dv,w", [((2, 300, 3, 16), 40, 16), ((1, 257, 2, 64), 24, 64),
+                                        ((1, 130, 2, 32), 96, 7)])
+def test_value_head_dim_matches_oracle(mc, oracle, shape, dv, w):
+    """Larger shapes against the oracle's column blocks (oracle.forward_value_dim)."""
+    from conftest import qkv, randn
+    q, k, _ = qkv(shape, 5100 + dv, 1.0)
+    v = randn(shape[:3] + (dv,), 5200 + dv)
+    out = mc.compute_sparse_attention(_t(mc, q), _t(mc, k), _t(mc, v), window_size=w).to_numpy()
+    ref = oracle.forward_value_dim(oracle.Spec(*shape, pattern="sliding", left=w, right=w), q, k, v)
+    err = float(np.abs(out - ref).max())
+    print(f"{shape} Dv={dv} w={w}: max|err| vs oracle = {err:.3e}", flush=True)
+    assert out.shape == ref.shape and err <= 1e-5
+
+
+def test_wider_key_value_tensors(mc, oracle):
+    """K and V with more batches and heads than Q: the reference reads Q's
+    (batch, head) range of them with their own strides (tensor.cpp:104-114);
+    fewer raise RuntimeError."""
+    from conftest import randn
+    q = randn((1, 50, 2, 16), 61)
+    k, v = randn((2, 50, 3, 16), 62), randn((2, 50, 3, 16), 63)
+    out = mc.compute_sparse_attention(_t(mc, q), _t(mc, k), _t(mc, v), window_size=4).to_numpy()
+    ks, vs = np.ascontiguousarray(k[:1, :, :2]), np.ascontiguousarray(v[:1, :, :2])
+    ref = oracle.forward(oracle.Spec(1, 50, 2, 16, pattern="sliding", left=4, right=4), q, ks, vs)
+    assert out.shape == q.shape and float(np.abs(out - ref).max()) <= 1e-5
+    with pytest.raises(RuntimeError):
+        mc.compute_sparse_attention(_t(mc, k), _t(mc, q), _t(mc, k), window_size=4)

@@ -165,8 +165,10 @@ def test_attention_shape_errors(mc):
         mc.compute_dense_attention(q, mc.create_random_tensor([1, 6, 2, 8]), q)
     with pytest.raises(RuntimeError, match="head dimension"):
         mc.compute_dense_attention(q, mc.create_random_tensor([1, 4, 2, 16]), q)
-    with pytest.raises(RuntimeError):
-        mc.compute_sparse_attention(q, q, mc.create_random_tensor([1, 4, 2, 16]), 2)
+    # a value head_dim of its own is accepted (ma_core.cpp:84-90); fewer value
+    # heads than the query's would be read out of range and raise
+    with pytest.raises(RuntimeError, match="number of heads"):
+        mc.compute_sparse_attention(q, q, mc.create_random_tensor([1, 4, 1, 16]), 2)
     with pytest.raises(TypeError):
         mc.compute_sparse_attention(q, q, np.zeros((1, 4, 2, 8), np.float32), 2)
 
@@ -174,6 +176,10 @@ def test_attention_shape_errors(mc):
 def test_empty_tensors_need_no_device(mc):
     z = mc.create_tensor([0, 4, 2, 8])
     assert mc.compute_sparse_attention(z, z, z, 3).size() == 0
+    # O takes the value's head_dim, also when empty
+    q, v = mc.create_tensor([1, 4, 2, 8]), mc.create_tensor([1, 4, 2, 0])
+    s = mc.compute_dense_attention(q, q, v).shape()
+    assert (s.batch_size, s.sequence_length, s.num_heads, s.head_dim) == (1, 4, 2, 0)
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the refusal on a host without a GPU")

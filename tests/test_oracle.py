@@ -43,6 +43,20 @@ def test_oracle_matches_reference_golden_dense(oracle):
         assert np.array_equal(o, g[key])
 
 
+@pytest.mark.parametrize("dv", [8, 24, 40])
+def test_oracle_matches_reference_golden_value_dim(oracle, dv):
+    """A value head_dim of its own (ma_core.cpp:84-90): the oracle's column
+    blocks against the reference's bits, sparse (w=5), dense and causal."""
+    g = np.load(os.path.join(GOLDEN, "ref_value_dim.npz"))
+    q, k, v = g["q"], g["k"], g[f"v_{dv}"]
+    w = int(g["w"])
+    for kw, key in ((dict(pattern="sliding", left=w, right=w), "o_sparse"), (dict(pattern="dense"), "o_dense"),
+                    (dict(pattern="dense", causal=True), "o_causal")):
+        o = oracle.forward_value_dim(_spec(oracle, q.shape, **kw), q, k, v)
+        assert o.shape == v.shape
+        assert np.array_equal(o, g[f"{key}_{dv}"]), (key, np.abs(o - g[f"{key}_{dv}"]).max())
+
+
 def test_golden_w0_is_value(oracle):
     g = np.load(os.path.join(GOLDEN, "ref_sparse_s33_w0.npz"))
     assert np.array_equal(g["o"], g["v"])

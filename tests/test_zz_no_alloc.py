@@ -1,13 +1,15 @@
 """ma_attn_forward_noalloc: the allocation-free forward entry point, through
 the C-ABI, against ma_attn_forward on the same inputs.
 
-The Longformer stream kernel is the only forward kernel with scratch (its
-per-chunk partials of the global rows): the no-alloc entry point takes them
-from the library's static device array instead of a caller workspace.  Both
-entry points launch the same kernels, so the outputs must agree bit for bit.
-Two calls in a row, the second smaller (the array keeps the first call's
-contents), then a pattern with no scratch, then a call whose scratch need is
-above the array's size, which must be rejected with nothing launched.
+Two forward kernels use scratch: the Longformer stream kernel (its per-chunk
+partials of the global rows) and the tiled index-set kernel (the partial
+results of a tile plan's split rows).  The no-alloc entry point takes it from
+the library's static device array instead of a caller workspace.  Both entry
+points launch the same kernels, so the outputs must agree bit for bit.  For
+each scratch user: two calls in a row, the second smaller (the array keeps the
+first call's contents); then a pattern with no scratch, then a call whose
+scratch need is above the array's size, which must be rejected with nothing
+launched.
 """
 import ctypes
 
@@ -73,6 +75,33 @@ def test_noalloc_matches_workspace_entry_point(ma, oracle, dtype):
     print(f"call 2 {shape2} {dtype}: scratch {nbytes} B", flush=True)
     assert 0 < nbytes
     assert torch.equal(o_ws, o_na)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_noalloc_tiled_index_set(ma, oracle, dtype):
+    """A tiled index set whose plan splits rows (the Longformer key sets: the
+    global rows' tiles hold every key block): its partials in the static array."""
+    import sparse_attention_cuda as ext
+    calls = [((1, 8192, 4, 64), 127, 16, 21), ((1, 3000, 2, 64), 60, 5, 22)]  # the second smaller
+    for n, (shape, left, G, seed) in enumerate(calls):
+        B, N, H, D = shape
+        iset = ext.pattern_index_set("longformer", N, "cuda:0", left=left, right=0, num_global=G)
+        assert iset.tile_plan is not None and int(iset.tile_header.num_q_split) > 0
+        q, k, v = _inputs(shape, seed, dtype)
+        desc = ma.make_desc(B, N, H, D, ma.DTYPES[dtype], ma.INDEX_SET, index_offsets_ptr=iset.offsets.data_ptr(),
+                            index_keys_ptr=iset.keys.data_ptr(), num_indices=iset.num_indices, **iset._tile_kw())
+        o_ws, o_na, nbytes = _both(ma, desc, q, k, v)
+        print(f"call {n + 1} {shape} {dtype}: tiled set, {int(iset.tile_header.num_q_split)} split rows, "
+              f"scratch {nbytes} B", flush=True)
+        assert 0 < nbytes <= ma.NOALLOC_SCRATCH_BYTES
+        assert torch.equal(o_ws, o_na)
+        # the split (global) rows against the oracle
+        up = [t.float().cpu().numpy() for t in (q, k, v)]
+        spec = oracle.Spec(*shape, pattern="longformer", left=left, right=0, num_global=G)
+        ref = oracle.forward(spec, *up, heads=(0, 1), rows=(0, G + 8))
+        err = float(np.abs(o_na.float().cpu().numpy()[:, :G + 8, :1] - ref[:, :G + 8, :1]).max())
+        print(f"  rows 0-{G + 8} head 0 vs oracle: {err:.3e}", flush=True)
+        assert err <= 2e-2
 
 
 def test_noalloc_without_scratch(ma):
