@@ -260,3 +260,48 @@ def test_layer_block_sparse_builds_its_sets_once(ext, oracle, monkeypatch):
         again = step()
         for a, b in zip(first, again):
             assert torch.equal(a, b)
+
+
+def test_layer_block_sparse_step_time_at_cfg3(ext):
+    """At the block-sparse benchmark shape (bf16, B=2 H=8 N=16384, 2 seeded
+    blocks per row) the layer's training step (forward with statistics, then
+    the backward from them) takes at most 1.3x the time of the same kernels
+    called directly: no host work or transfer holds the step back."""
+    import time
+    from layers.ma_core_bridge import MACoreAttention
+    B, N, H, D = 2, 16384, 8, 64
+    dev = torch.device("cuda", 0)
+    table = ext.make_block_table(1234, N // 64, 2)
+    gen = torch.Generator(device=dev).manual_seed(1)
+    sets = [tuple(torch.randn(B, N, H, D, device=dev, generator=gen).bfloat16() for _ in range(4)) for _ in range(4)]
+    leaves = [tuple(t.clone().requires_grad_(True) for t in s_[:3]) + (s_[3],) for s_ in sets]
+    att = MACoreAttention(sparse=True, window_size=64, pattern="block_sparse", block_table=table,
+                          fallback_training=False).train()
+    bt = ext.BlockTable(table, N, 64, dev)
+    iset = ext.pattern_index_set("block_sparse", N, dev, block_table=bt, block_size=64)
+
+    def layer_step(i):
+        q, k, v, g = leaves[i % 4]
+        for t in (q, k, v):
+            t.grad = None
+        att(q, k, v).backward(g)
+
+    def kernel_step(i):
+        q, k, v, g = sets[i % 4]
+        o, lse = ext.block_sparse_forward(q, k, v, bt, 64, return_lse=True)
+        ext.index_set_backward(q, k, v, g, iset, out=o, lse=lse)
+
+    def timed(step):
+        for i in range(20):
+            step(i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(100):
+            step(i)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / 100 * 1e6
+
+    t_kernels, t_layer = timed(kernel_step), timed(layer_step)
+    print(f"cfg3 training step: layer {t_layer:.1f} us, kernels {t_kernels:.1f} us, "
+          f"ratio {t_layer / t_kernels:.3f}", flush=True)
+    assert t_layer <= 1.3 * t_kernels
