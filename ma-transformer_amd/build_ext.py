@@ -17,9 +17,6 @@ REPO_DIR = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 # one object per translation unit, compiled in parallel, then linked
 SOURCES = [os.path.join(CSRC, f) for f in ("ma_attn.hip", "encoder_layer.hip")]
-HEADERS = [os.path.join(CSRC, h) for h in ("pattern.h", "device_common.h", "stream_kernel.h",
-                                           "block_kernel.h", "backward_kernel.h", "tick_features.h")] + \
-    [os.path.join(REPO_DIR, "include", h) for h in ("ma_attn.h", "ma_features.h", "ma_encoder.h")]
 LIB = os.path.join(PKG_DIR, "libma_attn.so")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 ARCH = os.environ.get("MA_ATTN_ARCH", "gfx950")

@@ -11,9 +11,10 @@
 //   gather_rows_kernel<T>  head_dim 64, any key set (index sets among them)
 //                    the tiled kernels do not take: one wave per query row,
 //                    8 whole K or V rows per load instruction.
-//   rows_kernel<T>   every pattern / dtype / head_dim <= 512: one wave per
-//                    query row, lanes over keys for the scores, lanes over
-//                    head_dim for P.V.  Used where no other kernel applies.
+//   rows_kernel<T>   every pattern / dtype / head_dim: one wave per query
+//                    row, lanes over keys for the scores, lanes over head_dim
+//                    for P.V (above 512, in passes of 512 output columns).
+//                    Used where no other kernel applies.
 //
 // Semantics follow ma_core::compute_sparse_attention
 // (/root/reference src/csrc/ma_core.cpp:160-246): softmax over the row's key
@@ -205,18 +206,21 @@ constexpr int kRowsWaves = 4;
 // STATS (backward): instead of O, writes the row's softmax statistics
 // stats[row] = {lse, delta}: lse = m + log(l) of the scaled scores, delta =
 // dout . O with O kept in fp32.
+// WIDE (head_dim above 64*DPL): the query row is read from memory rather
+// than LDS, and the output columns are done in passes of 64*DPL, each pass
+// recomputing the row's scores over the whole head_dim.
 struct RowStat {
   float lse, delta;
 };
 
-template <typename T, int DPL, bool STATS = false>
+template <typename T, int DPL, bool STATS = false, bool WIDE = false>
 __global__ __launch_bounds__(256) void rows_kernel(const T* __restrict__ q, const T* __restrict__ k,
                                                    const T* __restrict__ v, T* __restrict__ o,
                                                    int64_t B, int64_t H, int64_t D,
                                                    ma::PatternParams pp, float scale,
                                                    const T* __restrict__ dout = nullptr,
                                                    RowStat* __restrict__ stats = nullptr) {
-  extern __shared__ float q_lds[];  // kRowsWaves * D floats
+  extern __shared__ float q_lds[];  // kRowsWaves * D floats (not WIDE)
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const int64_t N = pp.n;
@@ -230,71 +234,84 @@ __global__ __launch_bounds__(256) void rows_kernel(const T* __restrict__ q, cons
   const int64_t rs = H * D;  // elements between consecutive tokens
 
   float* qw = q_lds + wv * D;
-  for (int64_t d = lane; d < D; d += 64) qw[d] = row_ok ? ld_f(q + rr * D + d) : 0.0f;
-  __syncthreads();
+  if constexpr (!WIDE) {
+    for (int64_t d = lane; d < D; d += 64) qw[d] = row_ok ? ld_f(q + rr * D + d) : 0.0f;
+    __syncthreads();
+  }
   if (!row_ok) return;  // no barrier below this point
+  auto qd = [&](int64_t d) -> float {
+    if constexpr (WIDE)
+      return ld_f(q + rr * D + d);
+    else
+      return qw[d];
+  };
 
   const T* kb = k + (b * N * H + h) * D;
   const T* vb = v + (b * N * H + h) * D;
   const ma::RowKeys rk = ma::row_keys(pp, i);
   const int64_t cnt = rk.count;
 
-  float m = -INFINITY, l = 0.0f;
-  float acc[DPL];
+  float m = -INFINITY, l = 0.0f, part = 0.0f;
+  for (int64_t col0 = 0; col0 < (WIDE ? D : 1); col0 += 64 * DPL) {  // one pass unless WIDE
+    m = -INFINITY;
+    l = 0.0f;
+    float acc[DPL];
 #pragma unroll
-  for (int c = 0; c < DPL; ++c) acc[c] = 0.0f;
+    for (int c = 0; c < DPL; ++c) acc[c] = 0.0f;
 
-  for (int64_t c0 = 0; c0 < cnt; c0 += 64) {
-    const int64_t t = c0 + lane;
-    const int64_t jk0 = t < cnt ? ma::key_at(pp, rk, i, t) : -1;
-    // closed-form keys are always in range; an index set's are checked here
-    const bool valid = jk0 >= 0 && jk0 < N;
-    const int64_t j = valid ? jk0 : 0;
-    float s = -INFINITY;
-    if (valid) {
-      const T* kr = kb + j * rs;
-      float dot = 0.0f;
-      for (int64_t d = 0; d < D; ++d) dot = fmaf(qw[d], ld_f(kr + d), dot);
-      s = dot * scale;
-    }
-    // mn is -inf only while every key so far was skipped (index sets)
-    const float mn = fmaxf(m, wave_max(s));
-    const float mu = mn == -INFINITY ? 0.0f : mn;
-    const float corr = expf(m - mu);
-    const float p = valid ? expf(s - mu) : 0.0f;
-    l = l * corr + wave_sum(p);
+    for (int64_t c0 = 0; c0 < cnt; c0 += 64) {
+      const int64_t t = c0 + lane;
+      const int64_t jk0 = t < cnt ? ma::key_at(pp, rk, i, t) : -1;
+      // closed-form keys are always in range; an index set's are checked here
+      const bool valid = jk0 >= 0 && jk0 < N;
+      const int64_t j = valid ? jk0 : 0;
+      float s = -INFINITY;
+      if (valid) {
+        const T* kr = kb + j * rs;
+        float dot = 0.0f;
+        for (int64_t d = 0; d < D; ++d) dot = fmaf(qd(d), ld_f(kr + d), dot);
+        s = dot * scale;
+      }
+      // mn is -inf only while every key so far was skipped (index sets)
+      const float mn = fmaxf(m, wave_max(s));
+      const float mu = mn == -INFINITY ? 0.0f : mn;
+      const float corr = expf(m - mu);
+      const float p = valid ? expf(s - mu) : 0.0f;
+      l = l * corr + wave_sum(p);
 #pragma unroll
-    for (int c = 0; c < DPL; ++c) acc[c] *= corr;
-    const int nk = (int)ma::imin64(64, cnt - c0);
-    for (int kk = 0; kk < nk; ++kk) {
-      const float pk = bcast_f(p, kk);
-      const int64_t jk = (int64_t)bcast_i((int)j, kk);
-      const T* vr = vb + jk * rs;
+      for (int c = 0; c < DPL; ++c) acc[c] *= corr;
+      const int nk = (int)ma::imin64(64, cnt - c0);
+      for (int kk = 0; kk < nk; ++kk) {
+        const float pk = bcast_f(p, kk);
+        const int64_t jk = (int64_t)bcast_i((int)j, kk);
+        const T* vr = vb + jk * rs;
+#pragma unroll
+        for (int c = 0; c < DPL; ++c) {
+          const int64_t d = col0 + lane + 64 * c;
+          if (d < D) acc[c] = fmaf(pk, ld_f(vr + d), acc[c]);
+        }
+      }
+      m = mn;
+    }
+    const float inv = cnt > 0 && l != 0.0f ? 1.0f / l : 0.0f;
+    if constexpr (STATS) {
 #pragma unroll
       for (int c = 0; c < DPL; ++c) {
-        const int64_t d = lane + 64 * c;
-        if (d < D) acc[c] = fmaf(pk, ld_f(vr + d), acc[c]);
+        const int64_t d = col0 + lane + 64 * c;
+        if (d < D) part = fmaf(ld_f(dout + rr * D + d), acc[c] * inv, part);
+      }
+    } else {
+      T* orow = o + rr * D;
+#pragma unroll
+      for (int c = 0; c < DPL; ++c) {
+        const int64_t d = col0 + lane + 64 * c;
+        if (d < D) orow[d] = cvt_out<T>(acc[c] * inv);
       }
     }
-    m = mn;
   }
-  const float inv = cnt > 0 && l != 0.0f ? 1.0f / l : 0.0f;
   if constexpr (STATS) {
-    float part = 0.0f;
-#pragma unroll
-    for (int c = 0; c < DPL; ++c) {
-      const int64_t d = lane + 64 * c;
-      if (d < D) part = fmaf(ld_f(dout + rr * D + d), acc[c] * inv, part);
-    }
     const float delta = wave_sum(part);
     if (lane == 0) stats[rr] = RowStat{cnt > 0 && l > 0.0f ? m + logf(l) : 0.0f, delta};
-  } else {
-    T* orow = o + rr * D;
-#pragma unroll
-    for (int c = 0; c < DPL; ++c) {
-      const int64_t d = lane + 64 * c;
-      if (d < D) orow[d] = cvt_out<T>(acc[c] * inv);
-    }
   }
 }
 
@@ -472,14 +489,16 @@ __global__ __launch_bounds__(256) void narrow_kernel(const T* __restrict__ q, co
 // forms.  Same lane layout as rows_kernel: lanes over the set's entries for
 // the dot products, lanes over head_dim for the accumulations.
 
-// dq: one wave per query row; q_i and dout_i cached in LDS.
-template <typename T, int DPL>
+// dq: one wave per query row; q_i and dout_i cached in LDS (WIDE: read from
+// memory, and dq done in column passes of 64*DPL, each recomputing the
+// row's scores and dP over the whole head_dim).
+template <typename T, int DPL, bool WIDE = false>
 __global__ __launch_bounds__(256) void bwd_dq_kernel(const T* __restrict__ q, const T* __restrict__ k,
                                                      const T* __restrict__ v, const T* __restrict__ dout,
                                                      const RowStat* __restrict__ stats, T* __restrict__ dq,
                                                      int64_t B, int64_t H, int64_t D, ma::PatternParams pp,
                                                      float scale) {
-  extern __shared__ float row_lds[];  // kRowsWaves * 2 * D floats
+  extern __shared__ float row_lds[];  // kRowsWaves * 2 * D floats (not WIDE)
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const int64_t N = pp.n;
@@ -494,12 +513,26 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const T* __restrict__ q, co
 
   float* qw = row_lds + wv * 2 * D;
   float* gw = qw + D;
-  for (int64_t d = lane; d < D; d += 64) {
-    qw[d] = row_ok ? ld_f(q + rr * D + d) : 0.0f;
-    gw[d] = row_ok ? ld_f(dout + rr * D + d) : 0.0f;
+  if constexpr (!WIDE) {
+    for (int64_t d = lane; d < D; d += 64) {
+      qw[d] = row_ok ? ld_f(q + rr * D + d) : 0.0f;
+      gw[d] = row_ok ? ld_f(dout + rr * D + d) : 0.0f;
+    }
+    __syncthreads();
   }
-  __syncthreads();
   if (!row_ok) return;  // no barrier below this point
+  auto qd = [&](int64_t d) -> float {
+    if constexpr (WIDE)
+      return ld_f(q + rr * D + d);
+    else
+      return qw[d];
+  };
+  auto gd = [&](int64_t d) -> float {
+    if constexpr (WIDE)
+      return ld_f(dout + rr * D + d);
+    else
+      return gw[d];
+  };
 
   const T* kb = k + (b * N * H + h) * D;
   const T* vb = v + (b * N * H + h) * D;
@@ -507,54 +540,56 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const T* __restrict__ q, co
   const int64_t cnt = rk.count;
   const RowStat st = stats[rr];
 
-  float acc[DPL];
+  for (int64_t col0 = 0; col0 < (WIDE ? D : 1); col0 += 64 * DPL) {  // one pass unless WIDE
+    float acc[DPL];
 #pragma unroll
-  for (int c = 0; c < DPL; ++c) acc[c] = 0.0f;
-  for (int64_t c0 = 0; c0 < cnt; c0 += 64) {
-    const int64_t t = c0 + lane;
-    const int64_t j0 = t < cnt ? ma::key_at(pp, rk, i, t) : -1;
-    const bool valid = j0 >= 0 && j0 < N;  // an index set's keys are checked here
-    const int64_t j = valid ? j0 : 0;
-    float ds = 0.0f;
-    if (valid) {
-      const T* kr = kb + j * rs;
-      const T* vr = vb + j * rs;
-      float sdot = 0.0f, pdot = 0.0f;
-      for (int64_t d = 0; d < D; ++d) {
-        sdot = fmaf(qw[d], ld_f(kr + d), sdot);
-        pdot = fmaf(gw[d], ld_f(vr + d), pdot);
+    for (int c = 0; c < DPL; ++c) acc[c] = 0.0f;
+    for (int64_t c0 = 0; c0 < cnt; c0 += 64) {
+      const int64_t t = c0 + lane;
+      const int64_t j0 = t < cnt ? ma::key_at(pp, rk, i, t) : -1;
+      const bool valid = j0 >= 0 && j0 < N;  // an index set's keys are checked here
+      const int64_t j = valid ? j0 : 0;
+      float ds = 0.0f;
+      if (valid) {
+        const T* kr = kb + j * rs;
+        const T* vr = vb + j * rs;
+        float sdot = 0.0f, pdot = 0.0f;
+        for (int64_t d = 0; d < D; ++d) {
+          sdot = fmaf(qd(d), ld_f(kr + d), sdot);
+          pdot = fmaf(gd(d), ld_f(vr + d), pdot);
+        }
+        const float p = expf(sdot * scale - st.lse);
+        ds = p * (pdot - st.delta);
       }
-      const float p = expf(sdot * scale - st.lse);
-      ds = p * (pdot - st.delta);
-    }
-    const int nk = (int)ma::imin64(64, cnt - c0);
-    for (int kk = 0; kk < nk; ++kk) {
-      const float dsk = bcast_f(ds, kk);
-      const T* kr = kb + (int64_t)bcast_i((int)j, kk) * rs;
+      const int nk = (int)ma::imin64(64, cnt - c0);
+      for (int kk = 0; kk < nk; ++kk) {
+        const float dsk = bcast_f(ds, kk);
+        const T* kr = kb + (int64_t)bcast_i((int)j, kk) * rs;
 #pragma unroll
-      for (int c = 0; c < DPL; ++c) {
-        const int64_t d = lane + 64 * c;
-        if (d < D) acc[c] = fmaf(dsk, ld_f(kr + d), acc[c]);
+        for (int c = 0; c < DPL; ++c) {
+          const int64_t d = col0 + lane + 64 * c;
+          if (d < D) acc[c] = fmaf(dsk, ld_f(kr + d), acc[c]);
+        }
       }
     }
-  }
-  T* out = dq + rr * D;
+    T* out = dq + rr * D;
 #pragma unroll
-  for (int c = 0; c < DPL; ++c) {
-    const int64_t d = lane + 64 * c;
-    if (d < D) out[d] = cvt_out<T>(acc[c] * scale);
+    for (int c = 0; c < DPL; ++c) {
+      const int64_t d = col0 + lane + 64 * c;
+      if (d < D) out[d] = cvt_out<T>(acc[c] * scale);
+    }
   }
 }
 
 // dk, dv: one wave per key row j over the query set T_j (pt = the transposed
-// pattern); k_j and v_j cached in LDS.
-template <typename T, int DPL>
+// pattern); k_j and v_j cached in LDS (WIDE: as bwd_dq_kernel).
+template <typename T, int DPL, bool WIDE = false>
 __global__ __launch_bounds__(256) void bwd_dkv_kernel(const T* __restrict__ q, const T* __restrict__ k,
                                                       const T* __restrict__ v, const T* __restrict__ dout,
                                                       const RowStat* __restrict__ stats, T* __restrict__ dk,
                                                       T* __restrict__ dv, int64_t B, int64_t H, int64_t D,
                                                       ma::PatternParams pt, float scale) {
-  extern __shared__ float row_lds[];  // kRowsWaves * 2 * D floats
+  extern __shared__ float row_lds[];  // kRowsWaves * 2 * D floats (not WIDE)
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const int64_t N = pt.n;
@@ -569,12 +604,26 @@ __global__ __launch_bounds__(256) void bwd_dkv_kernel(const T* __restrict__ q, c
 
   float* kw = row_lds + wv * 2 * D;
   float* vw = kw + D;
-  for (int64_t d = lane; d < D; d += 64) {
-    kw[d] = row_ok ? ld_f(k + rr * D + d) : 0.0f;
-    vw[d] = row_ok ? ld_f(v + rr * D + d) : 0.0f;
+  if constexpr (!WIDE) {
+    for (int64_t d = lane; d < D; d += 64) {
+      kw[d] = row_ok ? ld_f(k + rr * D + d) : 0.0f;
+      vw[d] = row_ok ? ld_f(v + rr * D + d) : 0.0f;
+    }
+    __syncthreads();
   }
-  __syncthreads();
   if (!row_ok) return;  // no barrier below this point
+  auto kd = [&](int64_t d) -> float {
+    if constexpr (WIDE)
+      return ld_f(k + rr * D + d);
+    else
+      return kw[d];
+  };
+  auto vd = [&](int64_t d) -> float {
+    if constexpr (WIDE)
+      return ld_f(v + rr * D + d);
+    else
+      return vw[d];
+  };
 
   const T* qb = q + (b * N * H + h) * D;
   const T* gb = dout + (b * N * H + h) * D;
@@ -582,52 +631,54 @@ __global__ __launch_bounds__(256) void bwd_dkv_kernel(const T* __restrict__ q, c
   const ma::RowKeys rq = ma::row_keys(pt, j);
   const int64_t cnt = rq.count;
 
-  float acc_k[DPL], acc_v[DPL];
+  for (int64_t col0 = 0; col0 < (WIDE ? D : 1); col0 += 64 * DPL) {  // one pass unless WIDE
+    float acc_k[DPL], acc_v[DPL];
 #pragma unroll
-  for (int c = 0; c < DPL; ++c) acc_k[c] = acc_v[c] = 0.0f;
-  for (int64_t c0 = 0; c0 < cnt; c0 += 64) {
-    const int64_t t = c0 + lane;
-    const int64_t i0 = t < cnt ? ma::key_at(pt, rq, j, t) : -1;
-    const bool valid = i0 >= 0 && i0 < N;  // a transposed index set's queries are checked here
-    const int64_t i = valid ? i0 : 0;
-    float p = 0.0f, ds = 0.0f;
-    if (valid) {
-      const T* qr = qb + i * rs;
-      const T* gr = gb + i * rs;
-      float sdot = 0.0f, pdot = 0.0f;
-      for (int64_t d = 0; d < D; ++d) {
-        sdot = fmaf(ld_f(qr + d), kw[d], sdot);
-        pdot = fmaf(ld_f(gr + d), vw[d], pdot);
+    for (int c = 0; c < DPL; ++c) acc_k[c] = acc_v[c] = 0.0f;
+    for (int64_t c0 = 0; c0 < cnt; c0 += 64) {
+      const int64_t t = c0 + lane;
+      const int64_t i0 = t < cnt ? ma::key_at(pt, rq, j, t) : -1;
+      const bool valid = i0 >= 0 && i0 < N;  // a transposed index set's queries are checked here
+      const int64_t i = valid ? i0 : 0;
+      float p = 0.0f, ds = 0.0f;
+      if (valid) {
+        const T* qr = qb + i * rs;
+        const T* gr = gb + i * rs;
+        float sdot = 0.0f, pdot = 0.0f;
+        for (int64_t d = 0; d < D; ++d) {
+          sdot = fmaf(ld_f(qr + d), kd(d), sdot);
+          pdot = fmaf(ld_f(gr + d), vd(d), pdot);
+        }
+        const RowStat st = sb[i * H];
+        p = expf(sdot * scale - st.lse);
+        ds = p * (pdot - st.delta);
       }
-      const RowStat st = sb[i * H];
-      p = expf(sdot * scale - st.lse);
-      ds = p * (pdot - st.delta);
-    }
-    const int nk = (int)ma::imin64(64, cnt - c0);
-    for (int kk = 0; kk < nk; ++kk) {
-      const float pk = bcast_f(p, kk);
-      const float dsk = bcast_f(ds, kk);
-      const int64_t ik = (int64_t)bcast_i((int)i, kk);
-      const T* qr = qb + ik * rs;
-      const T* gr = gb + ik * rs;
+      const int nk = (int)ma::imin64(64, cnt - c0);
+      for (int kk = 0; kk < nk; ++kk) {
+        const float pk = bcast_f(p, kk);
+        const float dsk = bcast_f(ds, kk);
+        const int64_t ik = (int64_t)bcast_i((int)i, kk);
+        const T* qr = qb + ik * rs;
+        const T* gr = gb + ik * rs;
 #pragma unroll
-      for (int c = 0; c < DPL; ++c) {
-        const int64_t d = lane + 64 * c;
-        if (d < D) {
-          acc_v[c] = fmaf(pk, ld_f(gr + d), acc_v[c]);
-          acc_k[c] = fmaf(dsk, ld_f(qr + d), acc_k[c]);
+        for (int c = 0; c < DPL; ++c) {
+          const int64_t d = col0 + lane + 64 * c;
+          if (d < D) {
+            acc_v[c] = fmaf(pk, ld_f(gr + d), acc_v[c]);
+            acc_k[c] = fmaf(dsk, ld_f(qr + d), acc_k[c]);
+          }
         }
       }
     }
-  }
-  T* ok = dk + rr * D;
-  T* ov = dv + rr * D;
+    T* ok = dk + rr * D;
+    T* ov = dv + rr * D;
 #pragma unroll
-  for (int c = 0; c < DPL; ++c) {
-    const int64_t d = lane + 64 * c;
-    if (d < D) {
-      ok[d] = cvt_out<T>(acc_k[c] * scale);
-      ov[d] = cvt_out<T>(acc_v[c]);
+    for (int c = 0; c < DPL; ++c) {
+      const int64_t d = col0 + lane + 64 * c;
+      if (d < D) {
+        ok[d] = cvt_out<T>(acc_k[c] * scale);
+        ov[d] = cvt_out<T>(acc_v[c]);
+      }
     }
   }
 }
@@ -854,7 +905,7 @@ int validate(const ma_attn_desc* d) {
                 (long long)d->seq_len, (long long)d->num_heads, (long long)d->head_dim);
   if (d->dtype != MA_ATTN_F32 && d->dtype != MA_ATTN_BF16 && d->dtype != MA_ATTN_F16)
     return fail("ma_attn: unsupported dtype %d (float32, bfloat16, float16 only)", d->dtype);
-  if (d->head_dim > 512) return fail("ma_attn: head_dim %lld > 512 unsupported", (long long)d->head_dim);
+  if (d->head_dim > (1LL << 24)) return fail("ma_attn: head_dim %lld above 2^24", (long long)d->head_dim);
   if (d->seq_len > (int64_t)INT32_MAX) return fail("ma_attn: seq_len exceeds int32 range");
   switch (d->pattern) {
     case MA_ATTN_SLIDING:
@@ -921,8 +972,11 @@ int launch_rows(const ma_attn_desc* d, const void* q, const void* k, const void*
     MA_ROWS(2);
   else if (dpl <= 4)
     MA_ROWS(4);
-  else
+  else if (dpl <= 8)
     MA_ROWS(8);
+  else  // head_dim above 512: the query row from memory, output columns in passes of 512
+    launch(true, rows_kernel<T, 8, false, true>, dim3((unsigned)blocks), dim3(256), 0u, st, tq, tk, tv, to, d->batch,
+           d->num_heads, d->head_dim, pp, scale, (const T*)nullptr, (RowStat*)nullptr);
 #undef MA_ROWS
   return 0;
 }
@@ -1688,8 +1742,16 @@ int launch_backward(const ma_attn_desc* d, const void* q, const void* k, const v
     MA_BWD(2);
   else if (dpl <= 4)
     MA_BWD(4);
-  else
+  else if (dpl <= 8)
     MA_BWD(8);
+  else {  // head_dim above 512: rows from memory, columns in passes of 512
+    launch(false, rows_kernel<T, 8, true, true>, grid, blk, 0u, st, tq, tk, tv, (T*)nullptr, B, H, D, pp, scale, tg,
+           stats);
+    launch(false, bwd_dq_kernel<T, 8, true>, grid, blk, 0u, st, tq, tk, tv, tg, (const RowStat*)stats,
+           static_cast<T*>(dq), B, H, D, pp, scale);
+    launch(true, bwd_dkv_kernel<T, 8, true>, grid, blk, 0u, st, tq, tk, tv, tg, (const RowStat*)stats,
+           static_cast<T*>(dk), static_cast<T*>(dv), B, H, D, pt, scale);
+  }
 #undef MA_BWD
   return 0;
 }

@@ -52,7 +52,7 @@ def test_desc_layout_matches_header(tmp_path):
     (dict(dtype_code=7), "dtype"),
     (dict(pattern=9), "pattern"),
     (dict(dilation=0), "dilation"),
-    (dict(D=1000), "head_dim"),
+    (dict(D=(1 << 24) + 1), "head_dim"),
     (dict(N=-1), "negative"),
 ])
 def test_validate_rejects(kw, msg):
@@ -62,6 +62,13 @@ def test_validate_rejects(kw, msg):
     d = ma_attn.make_desc(**args)
     with pytest.raises(RuntimeError, match=msg):
         ma_attn.validate(d)
+
+
+def test_validate_accepts_wide_heads():
+    """Any head_dim up to the 2^24 sanity bound (the reference loops over any)."""
+    import ma_attn
+    for D in (513, 1000, 4096, 1 << 24):
+        ma_attn.validate(ma_attn.make_desc(1, 8, 1, D, ma_attn.F32, ma_attn.SLIDING, left=2, right=2))
 
 
 def test_forward_rejects_before_launch():
