@@ -773,11 +773,11 @@ def bench_attention(args) -> int:
     with_configs = args.configs if args.configs is not None else (
         args.workload == "target" and args.which == "forward")
     if with_configs:
-        # every BASELINE config's forward under the same clock, after the headline
+        # every BASELINE config's forward under the same clock, after the
+        # headline, each with its own ~0.1 s warmup and K stamped launches
         t0 = time.perf_counter()
-        out["configs"] = {}
-        for name in CONFIG_LINES:
-            out["configs"][name] = config_entry(measure(name, "forward", False, args.steps, None, 0))
+        out["configs"] = {name: config_entry(measure(name, "forward", False, args.steps, None, 0))
+                          for name in CONFIG_LINES}
         out["configs_wall_s"] = time.perf_counter() - t0
     out["copy_kernel_gbps"] = copy_bandwidth(dev, torch.cuda.current_stream(dev))
     if not args.no_cpu_baseline and args.which == "forward":
