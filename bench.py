@@ -524,7 +524,16 @@ def measure(workload: str, which: str = "forward", saved: bool = False, steps: i
         else:
             iset = ext.pattern_index_set("longformer", N, dev, left=pk["left"], right=pk["right"],
                                          num_global=pk["num_global"])
-        if saved:
+        if saved and pk["pattern"] == "longformer":
+            # the layer's path: the one-pass Longformer backward from the forward's
+            # output and statistics (no key-set description read)
+            for n_, s_ in enumerate(sets):
+                sets[n_] = s_ + ext.longformer_forward(s_[0], s_[1], s_[2], pk["left"], pk["right"],
+                                                       pk["num_global"], return_lse=True)
+            iset = None
+            launch = lambda s: ext.longformer_backward(s[0], s[1], s[2], s[3], pk["left"], pk["right"],
+                                                       pk["num_global"], out=s[4], lse=s[5])
+        elif saved:
             # each input set's forward output and statistics, as the layer's autograd keeps them
             for n_, s_ in enumerate(sets):
                 if pk["pattern"] == "index_set":
@@ -663,7 +672,7 @@ def measure(workload: str, which: str = "forward", saved: bool = False, steps: i
     queries = B * H * N
     alg_bytes = tensors * B * N * H * D * elt + (4 * B * N * H if saved else 0)  # + the statistics read
     set_source = None
-    if pk["pattern"] == "index_set" or (bwd and pk["pattern"] not in ("sliding", "dense")):
+    if iset is not None:
         # plus the set's description, read once per pass: the tile plan the
         # kernels read when the set has one (built once on the host), else the
         # key lists (the backward: the set and its transpose)

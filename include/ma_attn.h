@@ -207,7 +207,10 @@ int ma_attn_backward_timed(const ma_attn_desc* desc, const void* q, const void* 
  * ma_attn_backward_saved: the gradients of ma_attn_backward from the
  * forward's o and lse (delta_i = dout_i . o_i), for an INDEX_SET with a tile
  * plan, which may hold the key sets of a BLOCK_SPARSE or LONGFORMER forward
- * (ma_attn_pattern_csr enumerates them), and for DENSE (head_dim 64).
+ * (ma_attn_pattern_csr enumerates them), for DENSE (head_dim 64), and for
+ * LONGFORMER itself in 16 bits at head_dim 64 with right = 0, 0 <= left < 128
+ * and 1 to 16 global tokens (one pass over the sequence; per-chunk sums of the
+ * global rows' and keys' gradients in the workspace).
  * Workspace: ma_attn_backward_workspace_size(desc).  The _timed form stamps
  * its kernels as ma_attn_backward_timed does.
  */

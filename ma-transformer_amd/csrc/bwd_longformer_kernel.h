@@ -1,0 +1,571 @@
+// bwd_longformer_kernel.h -- one-pass backward of the Longformer key sets
+// from the forward's saved statistics: bf16/fp16, head_dim 64, dilation 1.
+// Rows i >= G attend [max(0, i-L), i] U [0, G) with L <= 127 (the union, no
+// key twice); rows i < G (the global rows) attend every key.
+//
+// Gradients from the saved row statistics lse2_i (log2 units of the scaled
+// scores, store_lse) and delta_i = dO_i . O_i (O the forward's output):
+//   P_ij = 2^(s_ij sl2 - lse2_i),  dS_ij = P_ij (dO_i . V_j - delta_i)
+//   dQ_i = scale sum_j dS_ij K_j,  dK_j = scale sum_i dS_ij Q_i,
+//   dV_j = sum_i P_ij dO_i.
+// With the statistics given, every (i, j) pair contributes independently,
+// so the set splits into three parts:
+//   band pairs       i >= G, j in [max(G, i-L), i]
+//   global keys      i >= G, j < G
+//   global rows      i < G, every j.
+//
+// Rows and keys come in 128-row tiles / blocks, so query tile t meets key
+// blocks t-1 and t, and key block j is seen by query tiles j and j+1.  One
+// workgroup (8 waves) streams a chunk [t0, t1) of query tiles of one
+// (batch, head) and owns key blocks [t0, t1); LDS holds the K, V rows of
+// blocks t-1 and t (a two-slot ring), tile t's Q and dO rows and statistics,
+// and the 16 global keys' K, V rows and global rows' Q, dO rows.  Step t:
+//   query pass   wave w: queries 128t + 16w + c against their 9 window key
+//                sub-tiles and the global keys (P^T, dS^T with the query as
+//                the MFMA column), dQ^T += K^T dS^T, dQ stored;
+//   global keys  wave w: the same queries against the global keys with the
+//                key as the MFMA column, the global keys' dK^T, dV^T summed
+//                over the chunk;
+//   key pass     wave w owns keys 16w.. of blocks t-1 and t: the tile's
+//                query sub-tiles that see them, P, dS recomputed with the key
+//                as the MFMA column (no exchange area), dV^T += dO^T P,
+//                dK^T += Q^T dS; block t-1 is then complete: the global
+//                rows' contributions are added (and their dQ summed over the
+//                chunk) and its dK, dV stored.  Block t's sums carry.
+// A chunk also runs the key pass of tile t1 (no dQ) for its block t1-1, and
+// reads block t0-1 for tile t0's queries.  The global rows' dQ and the
+// global keys' dK, dV are per-chunk sums in the workspace; bwd_lf_combine
+// adds them up and writes rows 0..G-1 of dQ, dK, dV.  Every other row of
+// dQ, dK, dV has one writer; no atomics.  Rows past the end read as zero and
+// their stores are dropped by the buffer range check; rows below 0 (block
+// -1) wrap past the range the same way.
+#pragma once
+
+#include "bwd_fused_kernel.h"
+
+namespace ma_dev {
+
+struct LfArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* dout;
+  const void* o;     // the forward's output (delta = dO . O)
+  const float* lse;  // the forward's row statistics (store_lse), [B*N*H]
+  void* dq;
+  void* dk;
+  void* dv;
+  float* part;  // [B*H][chunks][3][16][64]: global rows' dQ, global keys' dK, dV (unscaled sums)
+  int32_t N, H, L, G;
+  int32_t chunk, chunks;
+  int32_t tok_bytes;
+  float scale, scale_log2;
+};
+
+constexpr int kLfRows = 128;  // rows per query tile and key block
+constexpr int kLfWaves = 8;
+
+struct LfLds {
+  static constexpr int kRow = FusedLds::kRow;     // 144 B rows (128 + 16 pad)
+  static constexpr int kMat = kLfRows * kRow;     // one 128-row matrix
+  static constexpr int kSlot = 2 * kMat;          // a key block: K rows, then V rows
+  static constexpr int kQ = 2 * kSlot;            // tile t's Q rows
+  static constexpr int kG = kQ + kMat;            // tile t's dO rows
+  static constexpr int kGM = 16 * kRow;           // one 16-row global matrix
+  static constexpr int kGK = kG + kMat;           // global keys' K rows
+  static constexpr int kGV = kGK + kGM;           // global keys' V rows
+  static constexpr int kGQ = kGV + kGM;           // global rows' Q rows
+  static constexpr int kGG = kGQ + kGM;           // global rows' dO rows
+  static constexpr int kSt = kGG + kGM;           // tile t: lse2[128], then delta[128]
+  static constexpr int kStG = kSt + 8 * kLfRows;  // global rows: lse2[16], then delta[16]
+  static constexpr int kBytes = kStG + 128;       // 120960
+};
+static_assert(LfLds::kBytes <= 160 * 1024, "one workgroup per CU");
+// the chunk-end reduction of the 8 waves' sums reuses the ring: 4 waves x 12 KB
+static_assert(4 * 64 * 48 * 4 <= LfLds::kQ, "reduction area");
+
+// 16-bit dot product of two 8-element pieces, in fp32.
+template <typename T>
+__device__ __forceinline__ float dot8(uint4 x, uint4 y) {
+  const uint32_t a[4] = {x.x, x.y, x.z, x.w}, b[4] = {y.x, y.y, y.z, y.w};
+  float d = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    d = fmaf(static_cast<float>(__builtin_bit_cast(T, (uint16_t)(a[j] & 0xffffu))),
+             static_cast<float>(__builtin_bit_cast(T, (uint16_t)(b[j] & 0xffffu))), d);
+    d = fmaf(static_cast<float>(__builtin_bit_cast(T, (uint16_t)(a[j] >> 16))),
+             static_cast<float>(__builtin_bit_cast(T, (uint16_t)(b[j] >> 16))), d);
+  }
+  return d;
+}
+
+// Sum over the 8 consecutive lanes that hold one row's 16-byte pieces.
+__device__ __forceinline__ float sum8(float x) {
+  x += __shfl_xor(x, 1);
+  x += __shfl_xor(x, 2);
+  return x + __shfl_xor(x, 4);
+}
+
+// A 128-row matrix in flight: thread tid carries rows tid>>3 and (tid>>3)+64
+// at 16-byte column tid&7.
+struct Rows128 {
+  uint4 r[2];
+};
+__device__ __forceinline__ void lf_load(Rows128& x, __amdgpu_buffer_rsrc_t R, uint32_t off, int tid, uint32_t tb) {
+  const uint32_t o = off + (uint32_t)(tid >> 3) * tb + 16 * (tid & 7);
+  x.r[0] = bload16(R, o);
+  x.r[1] = bload16(R, o + 64 * tb);
+}
+__device__ __forceinline__ void lf_store(const Rows128& x, uint8_t* mat, int tid) {
+  uint8_t* p = mat + (tid >> 3) * LfLds::kRow + 16 * (tid & 7);
+  *reinterpret_cast<uint4*>(p) = x.r[0];
+  *reinterpret_cast<uint4*>(p + 64 * LfLds::kRow) = x.r[1];
+}
+
+// A query tile in flight: Q, dO and O rows and the statistic of row tid (tid < 128).
+struct LfTile {
+  Rows128 q, g, o;
+  float lse2;
+};
+
+// Tile t's rows into LDS: Q and dO rows, each row's lse2 and delta = dO . O.
+template <typename T>
+__device__ __forceinline__ void lf_stage_tile(const LfTile& x, uint8_t* lds, int tid) {
+  lf_store(x.q, lds + LfLds::kQ, tid);
+  lf_store(x.g, lds + LfLds::kG, tid);
+  float* st = reinterpret_cast<float*>(lds + LfLds::kSt);
+  if (tid < kLfRows) st[tid] = x.lse2;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float d = sum8(dot8<T>(x.g.r[h], x.o.r[h]));
+    if ((tid & 7) == 0) st[kLfRows + (tid >> 3) + 64 * h] = d;
+  }
+}
+
+// P (or P^T) and dS of one 16x16 sub-tile: elements where keep[r] holds.
+__device__ __forceinline__ void lf_probs(const f32x4& s, const f32x4& dp, const float (&lse2)[4],
+                                         const float (&dlt)[4], const bool (&keep)[4], float sl2, float (&p)[4],
+                                         float (&ds)[4]) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    p[r] = keep[r] ? __builtin_amdgcn_exp2f(fmaf(s[r], sl2, -lse2[r])) : 0.0f;
+    ds[r] = p[r] * (dp[r] - dlt[r]);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ uint2 pack4(const float (&x)[4]) {
+  return make_uint2(Mma<T>::pack2(x[0], x[1]), Mma<T>::pack2(x[2], x[3]));
+}
+
+// acc += M^T X^T over one sub-tile with X split into a 16-bit value and its
+// 16-bit remainder (two MFMAs): for the global rows' and global keys' sums,
+// which run over every row or key of the sequence, so that the operand's
+// rounding (2^-9 relative in bf16) does not accumulate over thousands of
+// terms.
+template <typename T>
+__device__ __forceinline__ void pv_tr_split(const uint8_t* m0, const float (&x)[4], f32x4 (&acc)[4]) {
+  const uint2 hi = pack4<T>(x);
+  const uint32_t w[4] = {hi.x & 0xffffu, hi.x >> 16, hi.y & 0xffffu, hi.y >> 16};
+  float lo[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) lo[r] = x[r] - static_cast<float>(__builtin_bit_cast(T, (uint16_t)w[r]));
+  pv_tr<T>(m0, hi, acc);
+  pv_tr<T>(m0, pack4<T>(lo), acc);
+}
+
+// Key pass of one key sub-tile (16 keys, lane c = key k0 + c) against query
+// sub-tiles jq in [jlo, jhi] of the tile at row q0, whose Q / dO rows and
+// statistics are in LDS (band pairs only: 0 <= i - k <= L, i >= G, k >= G,
+// i < N).  K, V of the keys as register operands.
+template <class P>
+__device__ __forceinline__ void lf_kpass(const uint8_t* lds, const typename P::Q& kr, const typename P::Q& vr,
+                                         int k0, int q0, int jlo, int jhi, int L, int G, int N, int c, int g,
+                                         uint32_t kl, uint32_t trl, float sl2, f32x4 (&ak)[4], f32x4 (&av)[4]) {
+  using T = typename P::Elt;
+  const float* st = reinterpret_cast<const float*>(lds + LfLds::kSt);
+  const int key = k0 + c;
+  const bool key_ok = key >= G;
+  // packed P and dS of query sub-tile jq (key as the MFMA column)
+  auto probs = [&](int jq, uint2& pp, uint2& dd) __attribute__((always_inline)) {
+    const f32x4 s = P::qk(lds + LfLds::kQ + 16 * jq * LfLds::kRow + kl, kr);   // S[query 16jq + 4g + r][key c]
+    const f32x4 dp = P::qk(lds + LfLds::kG + 16 * jq * LfLds::kRow + kl, vr);  // dP[query][key c]
+    const int qi0 = q0 + 16 * jq + 4 * g;
+    const f32x4 l4 = *reinterpret_cast<const f32x4*>(st + 16 * jq + 4 * g);
+    const f32x4 d4 = *reinterpret_cast<const f32x4*>(st + kLfRows + 16 * jq + 4 * g);
+    float lse2[4], dlt[4], p[4], ds[4];
+    bool keep[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int qi = qi0 + r;
+      const int dq = qi - key;
+      keep[r] = key_ok && qi >= G && qi < N && dq >= 0 && dq <= L;
+      lse2[r] = l4[r];
+      dlt[r] = d4[r];
+    }
+    lf_probs(s, dp, lse2, dlt, keep, sl2, p, ds);
+    pp = pack4<T>(p);
+    dd = pack4<T>(ds);
+  };
+  int jq = jlo;
+  for (; jq < jhi; jq += 2) {  // uniform: two query sub-tiles per 16x16x32 MFMA
+    uint2 p0, d0, p1, d1;
+    probs(jq, p0, d0);
+    probs(jq + 1, p1, d1);
+    const uint32_t o0 = 16 * jq * LfLds::kRow + trl, o1 = o0 + 16 * LfLds::kRow;
+    pv2_tr<T>(lds + LfLds::kG + o0, lds + LfLds::kG + o1, make_uint4(p0.x, p0.y, p1.x, p1.y), av);
+    pv2_tr<T>(lds + LfLds::kQ + o0, lds + LfLds::kQ + o1, make_uint4(d0.x, d0.y, d1.x, d1.y), ak);
+  }
+  if (jq == jhi) {  // uniform: an odd count's last sub-tile
+    uint2 p0, d0;
+    probs(jq, p0, d0);
+    const uint32_t o0 = 16 * jq * LfLds::kRow + trl;
+    pv_tr<T>(lds + LfLds::kG + o0, p0, av);
+    pv_tr<T>(lds + LfLds::kQ + o0, d0, ak);
+  }
+}
+
+// The global rows' contributions to one key sub-tile (lane c = key k0 + c,
+// K / V rows at krows / vrows, their register operands kr / vr): dK^T, dV^T
+// of the keys (key as the MFMA column) and the global rows' dQ^T (global
+// query as the column).
+template <class P>
+__device__ __forceinline__ void lf_global_rows(const uint8_t* lds, const uint8_t* krows, const uint8_t* vrows,
+                                               const typename P::Q& kr, const typename P::Q& vr, int k0, int G,
+                                               int N, int c, int g, uint32_t kl, uint32_t trl, float sl2,
+                                               f32x4 (&ak)[4], f32x4 (&av)[4], f32x4 (&agq)[4]) {
+  using T = typename P::Elt;
+  const float* sg = reinterpret_cast<const float*>(lds + LfLds::kStG);
+  {
+    const f32x4 s = P::qk(lds + LfLds::kGQ + kl, kr);   // S[global query 4g + r][key c]
+    const f32x4 dp = P::qk(lds + LfLds::kGG + kl, vr);
+    const f32x4 l4 = *reinterpret_cast<const f32x4*>(sg + 4 * g);
+    const f32x4 d4 = *reinterpret_cast<const f32x4*>(sg + 16 + 4 * g);
+    float lse2[4], dlt[4], p[4], ds[4];
+    bool keep[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      keep[r] = 4 * g + r < G && k0 + c < N;
+      lse2[r] = l4[r];
+      dlt[r] = d4[r];
+    }
+    lf_probs(s, dp, lse2, dlt, keep, sl2, p, ds);
+    pv_tr<T>(lds + LfLds::kGG + trl, pack4<T>(p), av);
+    pv_tr<T>(lds + LfLds::kGQ + trl, pack4<T>(ds), ak);
+  }
+  {
+    typename P::Q qg, gg;
+    lds_q<P>(qg, lds + LfLds::kGQ, c, g);
+    lds_q<P>(gg, lds + LfLds::kGG, c, g);
+    const f32x4 s = P::qk(krows + kl, qg);  // S^T[key 4g + r][global query c]
+    const f32x4 dp = P::qk(vrows + kl, gg);
+    const float lse2c = sg[c], dltc = sg[16 + c];
+    float lse2[4], dlt[4], p[4], ds[4];
+    bool keep[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      keep[r] = c < G && k0 + 4 * g + r < N;
+      lse2[r] = lse2c;
+      dlt[r] = dltc;
+    }
+    lf_probs(s, dp, lse2, dlt, keep, sl2, p, ds);
+    pv_tr_split<T>(krows + trl, ds, agq);
+  }
+}
+
+template <class P>
+__global__ __launch_bounds__(512, 1) void bwd_lf_kernel(LfArgs a) {
+  static_assert(P::kKRow == LfLds::kRow, "LDS rows are the 16-bit path's");
+  using T = typename P::Elt;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // LfLds
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15;
+  const int g = lane >> 4;
+
+  const int chunk_id = blockIdx.x % a.chunks;
+  const int bh = blockIdx.x / a.chunks;
+  const int h = bh % a.H;
+  const int b = bh / a.H;
+  const int N = a.N, L = a.L, G = a.G;
+  const int nt = (N + kLfRows - 1) / kLfRows;
+  const int t0 = chunk_id * a.chunk;
+  const int t1 = min(t0 + a.chunk, nt);
+  if (t0 >= t1) return;  // uniform, before any barrier
+  const int s1 = t1 < nt ? t1 : t1 - 1;  // the last step: tile t1's key pass for block t1-1
+  const uint32_t tb = (uint32_t)a.tok_bytes;
+  const int64_t base = ((int64_t)b * N * a.H + h) * kHeadDim;
+  const uint32_t nrec = (uint32_t)((int64_t)(N - 1) * tb + kHeadDim * sizeof(T));
+  const __amdgpu_buffer_rsrc_t Qr = make_rsrc(static_cast<const T*>(a.q) + base, nrec);
+  const __amdgpu_buffer_rsrc_t Kr = make_rsrc(static_cast<const T*>(a.k) + base, nrec);
+  const __amdgpu_buffer_rsrc_t Vr = make_rsrc(static_cast<const T*>(a.v) + base, nrec);
+  const __amdgpu_buffer_rsrc_t Gr = make_rsrc(static_cast<const T*>(a.dout) + base, nrec);
+  const __amdgpu_buffer_rsrc_t Or = make_rsrc(static_cast<const T*>(a.o) + base, nrec);
+  const __amdgpu_buffer_rsrc_t DQr = make_rsrc(static_cast<T*>(a.dq) + base, nrec);
+  const __amdgpu_buffer_rsrc_t DKr = make_rsrc(static_cast<T*>(a.dk) + base, nrec);
+  const __amdgpu_buffer_rsrc_t DVr = make_rsrc(static_cast<T*>(a.dv) + base, nrec);
+  const float* lse = a.lse + (int64_t)b * N * a.H + h;  // row i at i * H
+  // byte offset of row r (r >= -128); rows below 0 wrap past the range
+  auto roff = [&](int r) { return (uint32_t)r * tb; };
+  auto slot = [&](int j) { return lds + (j & 1) * LfLds::kSlot; };
+  auto load_tile = [&](LfTile& x, int t) {
+    const uint32_t o = roff(kLfRows * t);
+    lf_load(x.q, Qr, o, tid, tb);
+    lf_load(x.g, Gr, o, tid, tb);
+    lf_load(x.o, Or, o, tid, tb);
+    const int i = kLfRows * t + tid;
+    x.lse2 = tid < kLfRows && i < N ? lse[(int64_t)i * a.H] : 0.0f;
+  };
+  const float sl2 = a.scale_log2;
+  const uint32_t kl = c * LfLds::kRow + 16 * g;
+  const uint32_t trl = tr_lane(lane);
+
+  // prologue: the global keys' K, V rows and the global rows' Q, dO rows
+  // and statistics (waves 0 and 1: one 16-byte piece per thread), the key
+  // blocks t0-1 and t0, and tile t0
+  if (tid < 128) {  // uniform per wave
+    const uint32_t o = (uint32_t)(tid >> 3) * tb + 16 * (tid & 7);
+    const uint4 kx = bload16(Kr, o), vx = bload16(Vr, o), qx = bload16(Qr, o), gx = bload16(Gr, o);
+    const uint4 ox = bload16(Or, o);
+    const int r = tid >> 3;
+    uint8_t* p = lds + r * LfLds::kRow + 16 * (tid & 7);
+    *reinterpret_cast<uint4*>(p + LfLds::kGK) = kx;
+    *reinterpret_cast<uint4*>(p + LfLds::kGV) = vx;
+    *reinterpret_cast<uint4*>(p + LfLds::kGQ) = qx;
+    *reinterpret_cast<uint4*>(p + LfLds::kGG) = gx;
+    const float d = sum8(dot8<T>(gx, ox));
+    float* sg = reinterpret_cast<float*>(lds + LfLds::kStG);
+    if ((tid & 7) == 0) {
+      sg[r] = r < G && r < N ? lse[(int64_t)r * a.H] : 0.0f;
+      sg[16 + r] = d;
+    }
+  }
+  {
+    Rows128 xk, xv;
+    lf_load(xk, Kr, roff(kLfRows * (t0 - 1)), tid, tb);
+    lf_load(xv, Vr, roff(kLfRows * (t0 - 1)), tid, tb);
+    lf_store(xk, slot(t0 - 1), tid);
+    lf_store(xv, slot(t0 - 1) + LfLds::kMat, tid);
+    lf_load(xk, Kr, roff(kLfRows * t0), tid, tb);
+    lf_load(xv, Vr, roff(kLfRows * t0), tid, tb);
+    LfTile x;
+    load_tile(x, t0);
+    lf_store(xk, slot(t0), tid);
+    lf_store(xv, slot(t0) + LfLds::kMat, tid);
+    lf_stage_tile<T>(x, lds, tid);
+  }
+  __syncthreads();
+
+  // sums of this wave's keys 16wv.. of the carried block (t-1 at step t,
+  // then t); the global rows' dQ and the global keys' dK, dV over the chunk
+  f32x4 ak0[4], av0[4], agq[4], agk[4], agv[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    ak0[dt] = av0[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    agq[dt] = agk[dt] = agv[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+
+  // block j complete (its sums in ak, av): the global rows' part, then dK,
+  // dV of keys 16wv.. stored (rows 0..G-1 are rewritten by the combine, so
+  // block 0's global keys also go to the chunk's global-key sums)
+  auto finish_block = [&](int j, f32x4(&ak)[4], f32x4(&av)[4]) __attribute__((always_inline)) {
+    const uint8_t* krows = slot(j) + 16 * wv * LfLds::kRow;
+    const uint8_t* vrows = krows + LfLds::kMat;
+    typename P::Q kr, vr;
+    lds_q<P>(kr, slot(j), 16 * wv + c, g);
+    lds_q<P>(vr, slot(j) + LfLds::kMat, 16 * wv + c, g);
+    lf_global_rows<P>(lds, krows, vrows, kr, vr, kLfRows * j + 16 * wv, G, N, c, g, kl, trl, sl2, ak, av, agq);
+    if (j == 0 && wv == 0 && c < G) {  // the global keys: their totals come from the combine
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        agk[dt] += ak[dt];
+        agv[dt] += av[dt];
+      }
+    }
+    const uint32_t row = roff(kLfRows * j + 16 * wv + c);
+    store_nat<T>(av, 1.0f, DVr, row, g);
+    store_nat<T>(ak, a.scale, DKr, row, g);
+  };
+
+  for (int t = t0; t <= s1; ++t) {
+    const bool more = t < s1;
+    const bool own = t < t1;  // tile t's queries are this chunk's
+    Rows128 nk, nv;
+    LfTile nx;
+    if (more) {  // step t+1's key block and query tile in flight
+      lf_load(nk, Kr, roff(kLfRows * (t + 1)), tid, tb);
+      lf_load(nv, Vr, roff(kLfRows * (t + 1)), tid, tb);
+      load_tile(nx, t + 1);
+    }
+    const float* st = reinterpret_cast<const float*>(lds + LfLds::kSt);
+
+    if (own) {
+      // ---- query pass: queries i = 128t + 16wv + c, keys 4g + r of each sub-tile
+      const int i = kLfRows * t + 16 * wv + c;
+      const bool row_ok = i >= G && i < N;
+      typename P::Q qb, gb;
+      lds_q<P>(qb, lds + LfLds::kQ, 16 * wv + c, g);
+      lds_q<P>(gb, lds + LfLds::kG, 16 * wv + c, g);
+      const float lse2c = st[16 * wv + c], dltc = st[kLfRows + 16 * wv + c];
+      float lse2[4], dlt[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        lse2[r] = lse2c;
+        dlt[r] = dltc;
+      }
+      f32x4 acc[4];
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      {  // the global keys 0..G-1
+        const f32x4 s = P::qk(lds + LfLds::kGK + kl, qb);
+        const f32x4 dp = P::qk(lds + LfLds::kGV + kl, gb);
+        bool keep[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) keep[r] = row_ok && 4 * g + r < G;
+        float p[4], ds[4];
+        lf_probs(s, dp, lse2, dlt, keep, sl2, p, ds);
+        pv_tr<T>(lds + LfLds::kGK + trl, pack4<T>(ds), acc);
+      }
+      // window sub-tiles s = 8t + wv - 8 + jj (keys 16s..16s+15), jj = 0..8, in
+      // blocks t-1 and t; one 16x16x16 MFMA per sub-tile and head_dim tile.
+      // (Pairing sub-tiles on 16x16x32 MFMA here, with each pair's products
+      // issued between the next sub-tile's scores, gave intermittently wrong
+      // dQ for whole waves on the device; the one-sub-tile form, the same
+      // MFMA work, did not in any of the repeated runs.)
+#pragma unroll
+      for (int jj = 0; jj < 9; ++jj) {
+        const int s = 8 * t + wv - 8 + jj;
+        const uint32_t sub = (uint32_t)((s >> 3) & 1) * LfLds::kSlot + 16 * (s & 7) * LfLds::kRow;
+        const f32x4 sc = P::qk(lds + sub + kl, qb);
+        const f32x4 dp = P::qk(lds + sub + LfLds::kMat + kl, gb);
+        bool keep[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = 16 * s + 4 * g + r;
+          const int dq = i - key;
+          keep[r] = row_ok && key >= G && dq >= 0 && dq <= L;
+        }
+        float p[4], ds[4];
+        lf_probs(sc, dp, lse2, dlt, keep, sl2, p, ds);
+        pv_tr<T>(lds + sub + trl, pack4<T>(ds), acc);
+      }
+      store_nat<T>(acc, a.scale, DQr, row_ok ? roff(i) : kOob, g);
+
+      // ---- the global keys' dK, dV from this wave's queries (key as the column)
+      {
+        typename P::Q kg, vg;
+        lds_q<P>(kg, lds + LfLds::kGK, c, g);
+        lds_q<P>(vg, lds + LfLds::kGV, c, g);
+        const uint8_t* qrows = lds + LfLds::kQ + 16 * wv * LfLds::kRow;
+        const uint8_t* grows = lds + LfLds::kG + 16 * wv * LfLds::kRow;
+        const f32x4 s = P::qk(qrows + kl, kg);  // S[query 4g + r][global key c]
+        const f32x4 dp = P::qk(grows + kl, vg);
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(st + 16 * wv + 4 * g);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(st + kLfRows + 16 * wv + 4 * g);
+        float lq[4], dq4[4], p[4], ds[4];
+        bool keep[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int qi = kLfRows * t + 16 * wv + 4 * g + r;
+          keep[r] = c < G && qi >= G && qi < N;
+          lq[r] = l4[r];
+          dq4[r] = d4[r];
+        }
+        lf_probs(s, dp, lq, dq4, keep, sl2, p, ds);
+        pv_tr_split<T>(grows + trl, p, agv);
+        pv_tr_split<T>(qrows + trl, ds, agk);
+      }
+    }
+
+    // ---- key pass: tile t's queries into keys 16wv.. of blocks t-1 and t
+    const int q0 = kLfRows * t;
+    if (t > t0) {  // block t-1 is this chunk's: query sub-tiles 0..wv reach its keys
+      typename P::Q kr, vr;
+      lds_q<P>(kr, slot(t - 1), 16 * wv + c, g);
+      lds_q<P>(vr, slot(t - 1) + LfLds::kMat, 16 * wv + c, g);
+      lf_kpass<P>(lds, kr, vr, kLfRows * (t - 1) + 16 * wv, q0, 0, wv, L, G, N, c, g, kl, trl, sl2, ak0, av0);
+      finish_block(t - 1, ak0, av0);
+    }
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) ak0[dt] = av0[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (own) {  // block t: query sub-tiles wv..7
+      typename P::Q kr, vr;
+      lds_q<P>(kr, slot(t), 16 * wv + c, g);
+      lds_q<P>(vr, slot(t) + LfLds::kMat, 16 * wv + c, g);
+      lf_kpass<P>(lds, kr, vr, kLfRows * t + 16 * wv, q0, wv, kLfWaves - 1, L, G, N, c, g, kl, trl, sl2, ak0, av0);
+      if (t == nt - 1) {  // no tile t+1: block t is complete too
+        finish_block(t, ak0, av0);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) ak0[dt] = av0[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+    }
+
+    // step t+1's rows replace block t-1 and tile t, which every pass has read
+    __syncthreads();
+    if (more) {
+      lf_store(nk, slot(t + 1), tid);
+      lf_store(nv, slot(t + 1) + LfLds::kMat, tid);
+      lf_stage_tile<T>(nx, lds, tid);
+      __syncthreads();
+    }
+  }
+
+  // ---- the chunk's global sums: the 8 waves' sums added pairwise in LDS
+  // (the ring is free: the loop ended on a barrier), then written by wave 0
+  // as natural-order rows: [3][16][64], row c, head_dim 16dt + 4g + r
+  f32x4* red = reinterpret_cast<f32x4*>(lds);
+  for (int half = kLfWaves / 2; half >= 1; half >>= 1) {  // uniform
+    if (wv >= half && wv < 2 * half) {
+      f32x4* w = red + (wv - half) * 12 * 64 + lane;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        w[(0 + dt) * 64] = agq[dt];
+        w[(4 + dt) * 64] = agk[dt];
+        w[(8 + dt) * 64] = agv[dt];
+      }
+    }
+    __syncthreads();
+    if (wv < half) {
+      const f32x4* w = red + wv * 12 * 64 + lane;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        agq[dt] += w[(0 + dt) * 64];
+        agk[dt] += w[(4 + dt) * 64];
+        agv[dt] += w[(8 + dt) * 64];
+      }
+    }
+    __syncthreads();
+  }
+  if (wv == 0) {
+    float* dst = a.part + ((int64_t)bh * a.chunks + chunk_id) * 3 * 16 * kHeadDim + c * kHeadDim + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      *reinterpret_cast<f32x4*>(dst + 16 * dt) = agq[dt];
+      *reinterpret_cast<f32x4*>(dst + 16 * kHeadDim + 16 * dt) = agk[dt];
+      *reinterpret_cast<f32x4*>(dst + 2 * 16 * kHeadDim + 16 * dt) = agv[dt];
+    }
+  }
+}
+
+// Rows 0..G-1 of dQ, dK, dV of one (batch, head): the sums of its chunks'
+// global parts (in chunk order), dQ and dK times the scale.
+template <typename T>
+__global__ __launch_bounds__(256) void bwd_lf_combine(LfArgs a) {
+  const int bh = blockIdx.x;
+  const int h = bh % a.H;
+  const int b = bh / a.H;
+  const int64_t base = ((int64_t)b * a.N * a.H + h) * kHeadDim;
+  const int rows = min(a.G, a.N);
+  for (int e = threadIdx.x; e < 3 * 16 * kHeadDim; e += 256) {
+    const int m = e / (16 * kHeadDim), r = (e / kHeadDim) % 16, d = e % kHeadDim;
+    if (r >= rows) continue;
+    const float* p = a.part + (int64_t)bh * a.chunks * 3 * 16 * kHeadDim + e;
+    float s = 0.0f;
+    for (int ch = 0; ch < a.chunks; ++ch) s += p[(int64_t)ch * 3 * 16 * kHeadDim];
+    T* out = static_cast<T*>(m == 0 ? a.dq : m == 1 ? a.dk : a.dv);
+    out[base + (int64_t)r * a.H * kHeadDim + d] = static_cast<T>(m == 2 ? s : s * a.scale);
+  }
+}
+
+}  // namespace ma_dev

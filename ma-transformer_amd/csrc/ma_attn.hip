@@ -45,6 +45,7 @@
 #include "block_kernel.h"
 #include "backward_kernel.h"
 #include "bwd_fused_kernel.h"
+#include "bwd_longformer_kernel.h"
 #include "tile_kernel.h"
 #include "tick_features.h"
 
@@ -1792,6 +1793,73 @@ int scratch_of_stream(hipStream_t st, void** out) {
 int forward_launch(const ma_attn_desc* desc, const void* q, const void* k, const void* v, void* o, float* lse,
                    void* workspace, size_t workspace_bytes, hipStream_t st);
 
+// ------------------------------------------------------------------ Longformer backward from saved statistics
+//
+// bwd_longformer_kernel.h: one pass over Q, K, V, dO and O for Longformer
+// sets with a causal window of at most 128 keys ([i-L, i], L <= 127) and 1 to
+// 16 global tokens, 16-bit, head_dim 64.  Workspace: per (batch, head) and
+// chunk, the global rows' dQ and the global keys' dK, dV sums (3 x 16 x 64
+// floats).
+struct LfPlan {
+  int64_t chunk, chunks, part_bytes;
+};
+
+LfPlan lf_plan(const ma_attn_desc* d) {
+  LfPlan p;
+  const int64_t nt = (d->seq_len + kLfRows - 1) / kLfRows;
+  const int64_t streams = ma::imax64(d->batch * d->num_heads, 1);
+  // one workgroup per CU (121 KB of LDS): chunks fitted to one round of 256
+  const int64_t per_stream = ma::imax64(1, 256 / streams);
+  p.chunk = ma::imax64(1, (nt + per_stream - 1) / per_stream);
+  p.chunks = ma::imax64(1, (nt + p.chunk - 1) / p.chunk);
+  p.part_bytes = streams * p.chunks * 3 * 16 * kHeadDim * (int64_t)sizeof(float);
+  return p;
+}
+
+bool lf_applies(const ma_attn_desc* d, const void* const* ptrs, int n) {
+  if (d->pattern != MA_ATTN_LONGFORMER || d->dtype == MA_ATTN_F32 || d->head_dim != kHeadDim) return false;
+  if (g_opt.force_rows || d->right != 0 || d->left < 0 || d->left >= kLfRows || d->num_global < 1 ||
+      d->num_global > 16)
+    return false;
+  for (int i = 0; i < n; ++i)
+    if (!aligned16(ptrs[i])) return false;
+  const int64_t tb = d->num_heads * kHeadDim * 2;
+  return (d->seq_len + 2 * kLfRows) * tb < (1LL << 31) &&
+         d->batch * d->num_heads * lf_plan(d).chunks <= (int64_t)INT32_MAX;
+}
+
+template <typename T>
+int launch_lf_bwd(const ma_attn_desc* d, const void* const* ptrs, const void* o, const float* lse, void* ws,
+                  hipStream_t st) {
+  const LfPlan p = lf_plan(d);
+  LfArgs a;
+  a.q = ptrs[0];
+  a.k = ptrs[1];
+  a.v = ptrs[2];
+  a.dout = ptrs[3];
+  a.dq = const_cast<void*>(ptrs[4]);
+  a.dk = const_cast<void*>(ptrs[5]);
+  a.dv = const_cast<void*>(ptrs[6]);
+  a.o = o;
+  a.lse = lse;
+  a.part = static_cast<float*>(ws);
+  a.N = (int32_t)d->seq_len;
+  a.H = (int32_t)d->num_heads;
+  a.L = (int32_t)d->left;
+  a.G = (int32_t)ma::imin64(d->num_global, d->seq_len);
+  a.chunk = (int32_t)p.chunk;
+  a.chunks = (int32_t)p.chunks;
+  a.tok_bytes = (int32_t)(d->num_heads * kHeadDim * sizeof(T));
+  a.scale = scale_of(d);
+  a.scale_log2 = a.scale * 1.4426950408889634f;
+  auto kf = &bwd_lf_kernel<HalfPath<T>>;
+  if (reserve_lds(reinterpret_cast<const void*>(kf), (size_t)LfLds::kBytes, st)) return 1;
+  const int64_t streams = d->batch * d->num_heads;
+  launch(false, kf, dim3((unsigned)(streams * p.chunks)), dim3(kLfWaves * 64), (uint32_t)LfLds::kBytes, st, a);
+  launch(true, bwd_lf_combine<T>, dim3((unsigned)streams), dim3(256), 0u, st, a);
+  return 0;
+}
+
 // ------------------------------------------------------------------ tiled index sets
 //
 // INDEX_SET with a tile plan (ma_attn_tile_plan), head_dim 64, 16-byte
@@ -2104,6 +2172,8 @@ size_t ma_attn_backward_workspace_size(const ma_attn_desc* desc) {
   const void* const ptrs[7] = {dummy, dummy, dummy, dummy, dummy, dummy, dummy};
   if (desc->batch * desc->seq_len * desc->num_heads > 0 && tiles_apply(desc, ptrs, 7))
     return (size_t)(stats_bytes(desc) + tiles_bwd_part_bytes(desc));
+  if (desc->batch * desc->seq_len * desc->num_heads > 0 && lf_applies(desc, ptrs, 7))
+    return (size_t)lf_plan(desc).part_bytes;  // the Longformer backward from saved statistics
   return (size_t)(desc->batch * desc->seq_len * desc->num_heads) * sizeof(RowStat);
 }
 
@@ -2191,17 +2261,22 @@ int ma_attn_backward_saved(const ma_attn_desc* desc, const void* q, const void* 
   const bool tiles = tiles_apply(desc, ptrs, 8);
   const bool dense =
       desc->pattern == MA_ATTN_DENSE && !g_opt.force_rows && aligned16(o) && bwd_mfma_applies(desc, ptrs);
-  if (!tiles && !dense)
-    return fail("ma_attn_backward_saved: takes an INDEX_SET with a tile plan or DENSE, head_dim 64, 16-byte "
-                "aligned tensors");
-  const size_t need = tiles ? (size_t)(stats_bytes(desc) + tiles_bwd_part_bytes(desc)) : (size_t)rows * sizeof(RowStat);
+  const bool lf = lf_applies(desc, ptrs, 8);
+  if (!tiles && !dense && !lf)
+    return fail("ma_attn_backward_saved: takes an INDEX_SET with a tile plan, DENSE, or LONGFORMER (16-bit, "
+                "window [i-L, i] with L <= 127, 1 to 16 global tokens), head_dim 64, 16-byte aligned tensors");
+  const size_t need = tiles ? (size_t)(stats_bytes(desc) + tiles_bwd_part_bytes(desc))
+                      : lf  ? (size_t)lf_plan(desc).part_bytes
+                            : (size_t)rows * sizeof(RowStat);
   if (!workspace || workspace_bytes < need)
     return fail("ma_attn_backward_saved: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
   float* sf = static_cast<float*>(workspace);
   const int rc =
-      tiles ? (desc->dtype == MA_ATTN_BF16 ? launch_tiles_bwd<HalfPath<__bf16>>(desc, ptrs, workspace, st, o, lse)
+      lf ? (desc->dtype == MA_ATTN_BF16 ? launch_lf_bwd<__bf16>(desc, ptrs, o, lse, workspace, st)
+                                        : launch_lf_bwd<_Float16>(desc, ptrs, o, lse, workspace, st))
+      : tiles ? (desc->dtype == MA_ATTN_BF16 ? launch_tiles_bwd<HalfPath<__bf16>>(desc, ptrs, workspace, st, o, lse)
                : desc->dtype == MA_ATTN_F16
                    ? launch_tiles_bwd<HalfPath<_Float16>>(desc, ptrs, workspace, st, o, lse)
                    : launch_tiles_bwd<F32BwdPath>(desc, ptrs, workspace, st, o, lse))

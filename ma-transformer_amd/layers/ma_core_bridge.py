@@ -166,8 +166,10 @@ def _saved_statistics_pay(iset) -> bool:
 
 
 def _saved_statistics_plan(spec: Optional[PatternSpec], sparse: bool, q: torch.Tensor):
-    """("set", IndexSet) or ("dense", None) when the native backward should
-    start from the forward's saved statistics, else None.  Dense rows longer
+    """("set", IndexSet), ("longformer", None) or ("dense", None) when the
+    native backward should start from the forward's saved statistics, else
+    None.  Longformer windows of at most 128 keys with 1 to 16 global tokens
+    (16-bit, head_dim 64) take the one-pass kernel.  Dense rows longer
     than two 64-key blocks take the one-tile dQ kernel, whose statistics pass
     streams every key block once more (bench.py --saved-stats on
     dense_causal_*); shorter rows keep their scores in registers."""
@@ -175,6 +177,9 @@ def _saved_statistics_plan(spec: Optional[PatternSpec], sparse: bool, q: torch.T
         if (spec is None and sparse) or q.shape[1] <= 128 or q.shape[3] != 64:
             return None
         return ("dense", None)
+    if spec.pattern == "longformer" and sparse_attention_cuda.longformer_fused_applies(
+            q, spec.left, spec.right, spec.num_global):
+        return ("longformer", None)  # one pass from the statistics (bwd_lf_kernel)
     if spec.pattern in ("block_sparse", "longformer", "index_set"):
         iset = _pattern_set(spec, q.shape[1], q.device)
         return ("set", iset) if _saved_statistics_pay(iset) else None
@@ -285,7 +290,10 @@ class MACoreAttentionFunction(torch.autograd.Function):
             if ctx.saved_plan is not None:  # from the forward's output and statistics
                 out, lse = ctx.saved_tensors[3:]
                 kind, iset = ctx.saved_plan
-                if kind == "set":
+                if kind == "longformer":
+                    dQ, dK, dV = ext.longformer_backward(cq, ck, cv, cgo, spec.left, spec.right, spec.num_global,
+                                                         out=out, lse=lse)
+                elif kind == "set":
                     dQ, dK, dV = ext.index_set_backward(cq, ck, cv, cgo, iset, out=out, lse=lse)
                 else:
                     causal = bool(ctx.use_causal_mask) if spec is None else spec.causal

@@ -20,6 +20,7 @@ New pattern entry points (not in the reference; the benchmark patterns):
     block_sparse_forward(q, k, v, block_table, block_size=64)
     BlockTable(block_table, seq_len, block_size=64)   (checked once, on the device)
     longformer_forward(q, k, v, left, right=0, num_global=16)
+    longformer_backward(q, k, v, grad_out, left, right=0, num_global=16, out=, lse=)
     make_block_table(seed, num_blocks, random_per_row=2)
     index_set_forward(q, k, v, index_set)              (explicit key set per query row)
     IndexSet(offsets, keys, seq_len), IndexSet.from_coo(rows, cols, seq_len)
@@ -40,8 +41,9 @@ import torch
 import ma_attn as _ma
 
 __all__ = ["forward", "dense_forward", "backward", "dense_backward", "sliding_forward",
-           "sliding_backward", "block_sparse_forward", "longformer_forward", "make_block_table",
-           "BlockTable", "IndexSet", "index_set_forward", "index_set_backward", "pattern_index_set"]
+           "sliding_backward", "block_sparse_forward", "longformer_forward", "longformer_backward",
+           "make_block_table", "BlockTable", "IndexSet", "index_set_forward", "index_set_backward",
+           "pattern_index_set"]
 
 
 def _check(*ts: torch.Tensor) -> None:
@@ -498,6 +500,35 @@ def _backward(q, k, v, grad_out, pattern, **kw) -> List[torch.Tensor]:
         desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), grad_out.data_ptr(), dq.data_ptr(), dk.data_ptr(),
         dv.data_ptr(), ws.data_ptr(), nbytes, stream, _events))
     return [dq, dk, dv]
+
+
+def longformer_fused_applies(query, left: int, right: int, num_global: int) -> bool:
+    """Whether longformer_backward's one-pass kernel (ma_attn_backward_saved on
+    a LONGFORMER descriptor) takes this call: bf16/fp16, head_dim 64, window
+    [i-left, i] with left <= 127, 1 to 16 global tokens, 16-byte aligned tensors."""
+    return (query.dtype in (torch.bfloat16, torch.float16) and query.dim() == 4 and query.shape[3] == 64
+            and int(right) == 0 and 0 <= int(left) < 128 and 1 <= int(num_global) <= 16)
+
+
+def longformer_backward(query, key, value, grad_out, left: int, right: int = 0, num_global: int = 16,
+                        out=None, lse=None) -> List[torch.Tensor]:
+    """dQ, dK, dV of longformer_forward.
+
+    With the forward's output and statistics (longformer_forward(...,
+    return_lse=True)) and a window [i-left, i] (left <= 127, 1 to 16 global
+    tokens, 16-bit, head_dim 64), one pass over Q, K, V, dO and O
+    (ma_attn_backward_saved, bwd_lf_kernel).  Otherwise the tiled kernels over
+    the pattern's key sets (index_set_backward on pattern_index_set)."""
+    _check(query, key, value, grad_out)
+    N = query.shape[1]
+    kw = dict(left=int(left), right=int(right), num_global=int(num_global))
+    if out is not None and lse is not None and longformer_fused_applies(query, left, right, num_global) and all(
+            t.data_ptr() % 16 == 0 for t in (query, key, value, grad_out, out)):
+        _check(query, out)
+        _check_lse(lse, query)
+        return _backward_saved(query, key, value, out, lse, grad_out, _ma.LONGFORMER, **kw)
+    iset = pattern_index_set("longformer", N, query.device, **kw)
+    return index_set_backward(query, key, value, grad_out, iset, out=out, lse=lse)
 
 
 def backward(query, key, value, grad_out, window_size: int = 64) -> List[torch.Tensor]:
