@@ -10,9 +10,14 @@
 //   dV_j = sum_i P_ij dO_i.
 // With the statistics given, every (i, j) pair contributes independently,
 // so the set splits into three parts:
-//   band pairs       i >= G, j in [max(G, i-L), i]
-//   global keys      i >= G, j < G
+//   band pairs       i >= G, j in [max(0, i-L), i]
+//   global keys      i >= G, j < G, i - j > L
 //   global rows      i < G, every j.
+// Band pairs are selected by i - j alone (0 <= i - j <= L): a row outside
+// [G, N) carries lse2 = +inf in the tile's statistics, so its P and dS are 0
+// in every pass; a key sub-tile below row 0 has +inf added to the rows'
+// lse2.  For L = 127 (the kernel's FIXED127 form) only the diagonal
+// sub-tiles at both ends of a window need a mask, one fixed per lane.
 //
 // Rows and keys come in 128-row tiles / blocks, so query tile t meets key
 // blocks t-1 and t, and key block j is seen by query tiles j and j+1.  One
@@ -153,6 +158,40 @@ __device__ __forceinline__ void lf_probs(const f32x4& s, const f32x4& dp, const 
   }
 }
 
+// Which pairs of a band sub-tile (MFMA column c, rows 4g + r) are kept:
+//   kLfBand       those with 0 <= i - j <= L (dq[r] = i - j);
+//   kLfAll        all of them;
+//   kLfColBefore  those with c <  4g + r,   kLfColFrom  those with c >= 4g + r;
+//   kLfColAfter   those with c >  4g + r,   kLfColUpTo  those with c <= 4g + r.
+// The last five are the sub-tiles of a window of L = 127 on the 16-row grid:
+// whole sub-tiles between the two diagonal ones at its ends.
+enum LfMask { kLfBand, kLfAll, kLfColBefore, kLfColFrom, kLfColAfter, kLfColUpTo };
+
+template <int M>
+__device__ __forceinline__ void lf_probs_m(const f32x4& s, const f32x4& dp, const float (&lse2)[4],
+                                           const float (&dlt)[4], const int (&dq)[4], int L, int c, int g,
+                                           float sl2, float (&p)[4], float (&ds)[4]) {
+  if (M == kLfAll) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[r] = __builtin_amdgcn_exp2f(fmaf(s[r], sl2, -lse2[r]));
+      ds[r] = p[r] * (dp[r] - dlt[r]);
+    }
+  } else {
+    bool keep[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 4 * g + r;
+      keep[r] = M == kLfBand       ? (uint32_t)dq[r] <= (uint32_t)L
+                : M == kLfColBefore ? c < row
+                : M == kLfColFrom   ? c >= row
+                : M == kLfColAfter  ? c > row
+                                    : c <= row;
+    }
+    lf_probs(s, dp, lse2, dlt, keep, sl2, p, ds);
+  }
+}
+
 template <typename T>
 __device__ __forceinline__ uint2 pack4(const float (&x)[4]) {
   return make_uint2(Mma<T>::pack2(x[0], x[1]), Mma<T>::pack2(x[2], x[3]));
@@ -174,36 +213,33 @@ __device__ __forceinline__ void pv_tr_split(const uint8_t* m0, const float (&x)[
   pv_tr<T>(m0, pack4<T>(lo), acc);
 }
 
-// Key pass of one key sub-tile (16 keys, lane c = key k0 + c) against query
-// sub-tiles jq in [jlo, jhi] of the tile at row q0, whose Q / dO rows and
-// statistics are in LDS (band pairs only: 0 <= i - k <= L, i >= G, k >= G,
-// i < N).  K, V of the keys as register operands.
-template <class P>
+// Key pass of one key sub-tile (16 keys k0.., lane c = key k0 + c, k0 >= 0)
+// against query sub-tiles jq in [jlo, jhi] of the tile at row q0, whose Q /
+// dO rows and statistics are in LDS: the band pairs, selected as M says
+// (rows outside [G, N) have P = 0 through their statistics).  K, V of the
+// keys as register operands.
+template <class P, int M>
 __device__ __forceinline__ void lf_kpass(const uint8_t* lds, const typename P::Q& kr, const typename P::Q& vr,
-                                         int k0, int q0, int jlo, int jhi, int L, int G, int N, int c, int g,
-                                         uint32_t kl, uint32_t trl, float sl2, f32x4 (&ak)[4], f32x4 (&av)[4]) {
+                                         int k0, int q0, int jlo, int jhi, int L, int c, int g, uint32_t kl,
+                                         uint32_t trl, float sl2, f32x4 (&ak)[4], f32x4 (&av)[4]) {
   using T = typename P::Elt;
   const float* st = reinterpret_cast<const float*>(lds + LfLds::kSt);
-  const int key = k0 + c;
-  const bool key_ok = key >= G;
   // packed P and dS of query sub-tile jq (key as the MFMA column)
   auto probs = [&](int jq, uint2& pp, uint2& dd) __attribute__((always_inline)) {
     const f32x4 s = P::qk(lds + LfLds::kQ + 16 * jq * LfLds::kRow + kl, kr);   // S[query 16jq + 4g + r][key c]
     const f32x4 dp = P::qk(lds + LfLds::kG + 16 * jq * LfLds::kRow + kl, vr);  // dP[query][key c]
-    const int qi0 = q0 + 16 * jq + 4 * g;
+    const int dq0 = q0 + 16 * jq + 4 * g - (k0 + c);
     const f32x4 l4 = *reinterpret_cast<const f32x4*>(st + 16 * jq + 4 * g);
     const f32x4 d4 = *reinterpret_cast<const f32x4*>(st + kLfRows + 16 * jq + 4 * g);
     float lse2[4], dlt[4], p[4], ds[4];
-    bool keep[4];
+    int dq[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int qi = qi0 + r;
-      const int dq = qi - key;
-      keep[r] = key_ok && qi >= G && qi < N && dq >= 0 && dq <= L;
       lse2[r] = l4[r];
       dlt[r] = d4[r];
+      dq[r] = dq0 + r;
     }
-    lf_probs(s, dp, lse2, dlt, keep, sl2, p, ds);
+    lf_probs_m<M>(s, dp, lse2, dlt, dq, L, c, g, sl2, p, ds);
     pp = pack4<T>(p);
     dd = pack4<T>(ds);
   };
@@ -273,7 +309,8 @@ __device__ __forceinline__ void lf_global_rows(const uint8_t* lds, const uint8_t
   }
 }
 
-template <class P>
+// FIXED127: L = 127, the band's sub-tiles selected by the fixed masks.
+template <class P, bool FIXED127>
 __global__ __launch_bounds__(512, 1) void bwd_lf_kernel(LfArgs a) {
   static_assert(P::kKRow == LfLds::kRow, "LDS rows are the 16-bit path's");
   using T = typename P::Elt;
@@ -288,7 +325,7 @@ __global__ __launch_bounds__(512, 1) void bwd_lf_kernel(LfArgs a) {
   const int bh = blockIdx.x / a.chunks;
   const int h = bh % a.H;
   const int b = bh / a.H;
-  const int N = a.N, L = a.L, G = a.G;
+  const int N = a.N, L = FIXED127 ? kLfRows - 1 : a.L, G = a.G;
   const int nt = (N + kLfRows - 1) / kLfRows;
   const int t0 = chunk_id * a.chunk;
   const int t1 = min(t0 + a.chunk, nt);
@@ -314,8 +351,8 @@ __global__ __launch_bounds__(512, 1) void bwd_lf_kernel(LfArgs a) {
     lf_load(x.q, Qr, o, tid, tb);
     lf_load(x.g, Gr, o, tid, tb);
     lf_load(x.o, Or, o, tid, tb);
-    const int i = kLfRows * t + tid;
-    x.lse2 = tid < kLfRows && i < N ? lse[(int64_t)i * a.H] : 0.0f;
+    const int i = kLfRows * t + tid;  // no band pair for a row outside [G, N): P = 0
+    x.lse2 = tid < kLfRows && i >= G && i < N ? lse[(int64_t)i * a.H] : __builtin_inff();
   };
   const float sl2 = a.scale_log2;
   const uint32_t kl = c * LfLds::kRow + 16 * g;
@@ -403,7 +440,6 @@ __global__ __launch_bounds__(512, 1) void bwd_lf_kernel(LfArgs a) {
     if (own) {
       // ---- query pass: queries i = 128t + 16wv + c, keys 4g + r of each sub-tile
       const int i = kLfRows * t + 16 * wv + c;
-      const bool row_ok = i >= G && i < N;
       typename P::Q qb, gb;
       lds_q<P>(qb, lds + LfLds::kQ, 16 * wv + c, g);
       lds_q<P>(gb, lds + LfLds::kG, 16 * wv + c, g);
@@ -417,42 +453,51 @@ __global__ __launch_bounds__(512, 1) void bwd_lf_kernel(LfArgs a) {
       f32x4 acc[4];
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      {  // the global keys 0..G-1
+      {  // the global keys 0..G-1 outside the row's band
         const f32x4 s = P::qk(lds + LfLds::kGK + kl, qb);
         const f32x4 dp = P::qk(lds + LfLds::kGV + kl, gb);
         bool keep[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) keep[r] = row_ok && 4 * g + r < G;
+        for (int r = 0; r < 4; ++r) keep[r] = 4 * g + r < G && i - (4 * g + r) > L;
         float p[4], ds[4];
         lf_probs(s, dp, lse2, dlt, keep, sl2, p, ds);
         pv_tr<T>(lds + LfLds::kGK + trl, pack4<T>(ds), acc);
       }
       // window sub-tiles s = 8t + wv - 8 + jj (keys 16s..16s+15), jj = 0..8, in
-      // blocks t-1 and t; one 16x16x16 MFMA per sub-tile and head_dim tile.
-      // (Pairing sub-tiles on 16x16x32 MFMA here, with each pair's products
-      // issued between the next sub-tile's scores, gave intermittently wrong
-      // dQ for whole waves on the device; the one-sub-tile form, the same
-      // MFMA work, did not in any of the repeated runs.)
+      // blocks t-1 and t, i - key = 16(8 - jj) + c - (4g + r); one 16x16x16
+      // MFMA per sub-tile and head_dim tile.  (Pairing sub-tiles on 16x16x32
+      // MFMA here, with each pair's products issued between the next
+      // sub-tile's scores, gave intermittently wrong dQ for whole waves on the
+      // device; the one-sub-tile form, the same MFMA work, did not in any of
+      // the repeated runs.)
 #pragma unroll
       for (int jj = 0; jj < 9; ++jj) {
         const int s = 8 * t + wv - 8 + jj;
         const uint32_t sub = (uint32_t)((s >> 3) & 1) * LfLds::kSlot + 16 * (s & 7) * LfLds::kRow;
         const f32x4 sc = P::qk(lds + sub + kl, qb);
         const f32x4 dp = P::qk(lds + sub + LfLds::kMat + kl, gb);
-        bool keep[4];
+        const float l2 = s < 0 ? __builtin_inff() : lse2c;  // keys below row 0 (tile 0): no pair
+        float ls[4], p[4], ds[4];
+        int dq[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int key = 16 * s + 4 * g + r;
-          const int dq = i - key;
-          keep[r] = row_ok && key >= G && dq >= 0 && dq <= L;
+          ls[r] = l2;
+          dq[r] = 16 * (8 - jj) + c - (4 * g + r);
         }
-        float p[4], ds[4];
-        lf_probs(sc, dp, lse2, dlt, keep, sl2, p, ds);
+        if (!FIXED127)
+          lf_probs_m<kLfBand>(sc, dp, ls, dlt, dq, L, c, g, sl2, p, ds);
+        else if (jj == 0)
+          lf_probs_m<kLfColBefore>(sc, dp, ls, dlt, dq, L, c, g, sl2, p, ds);
+        else if (jj == 8)
+          lf_probs_m<kLfColFrom>(sc, dp, ls, dlt, dq, L, c, g, sl2, p, ds);
+        else
+          lf_probs_m<kLfAll>(sc, dp, ls, dlt, dq, L, c, g, sl2, p, ds);
         pv_tr<T>(lds + sub + trl, pack4<T>(ds), acc);
       }
-      store_nat<T>(acc, a.scale, DQr, row_ok ? roff(i) : kOob, g);
+      store_nat<T>(acc, a.scale, DQr, i >= G && i < N ? roff(i) : kOob, g);
 
-      // ---- the global keys' dK, dV from this wave's queries (key as the column)
+      // ---- the global keys' dK, dV from this wave's queries (key as the
+      // column), pairs outside the band
       {
         typename P::Q kg, vg;
         lds_q<P>(kg, lds + LfLds::kGK, c, g);
@@ -467,8 +512,7 @@ __global__ __launch_bounds__(512, 1) void bwd_lf_kernel(LfArgs a) {
         bool keep[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int qi = kLfRows * t + 16 * wv + 4 * g + r;
-          keep[r] = c < G && qi >= G && qi < N;
+          keep[r] = c < G && kLfRows * t + 16 * wv + 4 * g + r - c > L;
           lq[r] = l4[r];
           dq4[r] = d4[r];
         }
@@ -484,7 +528,13 @@ __global__ __launch_bounds__(512, 1) void bwd_lf_kernel(LfArgs a) {
       typename P::Q kr, vr;
       lds_q<P>(kr, slot(t - 1), 16 * wv + c, g);
       lds_q<P>(vr, slot(t - 1) + LfLds::kMat, 16 * wv + c, g);
-      lf_kpass<P>(lds, kr, vr, kLfRows * (t - 1) + 16 * wv, q0, 0, wv, L, G, N, c, g, kl, trl, sl2, ak0, av0);
+      const int k0 = kLfRows * (t - 1) + 16 * wv;
+      if (FIXED127) {  // i - key = 128 + 16(jq - wv) + (4g + r) - c
+        lf_kpass<P, kLfAll>(lds, kr, vr, k0, q0, 0, wv - 1, L, c, g, kl, trl, sl2, ak0, av0);
+        lf_kpass<P, kLfColAfter>(lds, kr, vr, k0, q0, wv, wv, L, c, g, kl, trl, sl2, ak0, av0);
+      } else {
+        lf_kpass<P, kLfBand>(lds, kr, vr, k0, q0, 0, wv, L, c, g, kl, trl, sl2, ak0, av0);
+      }
       finish_block(t - 1, ak0, av0);
     }
 #pragma unroll
@@ -493,7 +543,13 @@ __global__ __launch_bounds__(512, 1) void bwd_lf_kernel(LfArgs a) {
       typename P::Q kr, vr;
       lds_q<P>(kr, slot(t), 16 * wv + c, g);
       lds_q<P>(vr, slot(t) + LfLds::kMat, 16 * wv + c, g);
-      lf_kpass<P>(lds, kr, vr, kLfRows * t + 16 * wv, q0, wv, kLfWaves - 1, L, G, N, c, g, kl, trl, sl2, ak0, av0);
+      const int k0 = kLfRows * t + 16 * wv;
+      if (FIXED127) {  // i - key = 16(jq - wv) + (4g + r) - c
+        lf_kpass<P, kLfColUpTo>(lds, kr, vr, k0, q0, wv, wv, L, c, g, kl, trl, sl2, ak0, av0);
+        lf_kpass<P, kLfAll>(lds, kr, vr, k0, q0, wv + 1, kLfWaves - 1, L, c, g, kl, trl, sl2, ak0, av0);
+      } else {
+        lf_kpass<P, kLfBand>(lds, kr, vr, k0, q0, wv, kLfWaves - 1, L, c, g, kl, trl, sl2, ak0, av0);
+      }
       if (t == nt - 1) {  // no tile t+1: block t is complete too
         finish_block(t, ak0, av0);
 #pragma unroll

@@ -1852,7 +1852,7 @@ int launch_lf_bwd(const ma_attn_desc* d, const void* const* ptrs, const void* o,
   a.tok_bytes = (int32_t)(d->num_heads * kHeadDim * sizeof(T));
   a.scale = scale_of(d);
   a.scale_log2 = a.scale * 1.4426950408889634f;
-  auto kf = &bwd_lf_kernel<HalfPath<T>>;
+  auto kf = d->left == kLfRows - 1 ? &bwd_lf_kernel<HalfPath<T>, true> : &bwd_lf_kernel<HalfPath<T>, false>;
   if (reserve_lds(reinterpret_cast<const void*>(kf), (size_t)LfLds::kBytes, st)) return 1;
   const int64_t streams = d->batch * d->num_heads;
   launch(false, kf, dim3((unsigned)(streams * p.chunks)), dim3(kLfWaves * 64), (uint32_t)LfLds::kBytes, st, a);
