@@ -69,6 +69,7 @@ struct LfArgs {
 
 constexpr int kLfRows = 128;  // rows per query tile and key block
 constexpr int kLfWaves = 8;
+constexpr int kLfPart = 3 * 16 * kHeadDim;  // one chunk's partials: dQ, dK, dV of 16 rows
 
 struct LfLds {
   static constexpr int kRow = FusedLds::kRow;     // 144 B rows (128 + 16 pad)
@@ -604,24 +605,26 @@ __global__ __launch_bounds__(512, 1) void bwd_lf_kernel(LfArgs a) {
   }
 }
 
-// Rows 0..G-1 of dQ, dK, dV of one (batch, head): the sums of its chunks'
-// global parts (in chunk order), dQ and dK times the scale.
+// Rows 0..G-1 of dQ, dK, dV: the sums of a (batch, head)'s chunk partials
+// (in chunk order), dQ and dK times the scale.  One thread per element of
+// the [3][16][64] part: kLfCombineBlocks workgroups of 256 per (batch, head),
+// so the chunk loads of many elements are in flight together.
+constexpr int kLfCombineBlocks = 3 * 16 * kHeadDim / 256;
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_lf_combine(LfArgs a) {
-  const int bh = blockIdx.x;
+  const int bh = blockIdx.x / kLfCombineBlocks;
+  const int e = (blockIdx.x % kLfCombineBlocks) * 256 + threadIdx.x;
+  const int m = e / (16 * kHeadDim), r = (e / kHeadDim) % 16, d = e % kHeadDim;
+  if (r >= min(a.G, a.N)) return;
   const int h = bh % a.H;
   const int b = bh / a.H;
-  const int64_t base = ((int64_t)b * a.N * a.H + h) * kHeadDim;
-  const int rows = min(a.G, a.N);
-  for (int e = threadIdx.x; e < 3 * 16 * kHeadDim; e += 256) {
-    const int m = e / (16 * kHeadDim), r = (e / kHeadDim) % 16, d = e % kHeadDim;
-    if (r >= rows) continue;
-    const float* p = a.part + (int64_t)bh * a.chunks * 3 * 16 * kHeadDim + e;
-    float s = 0.0f;
-    for (int ch = 0; ch < a.chunks; ++ch) s += p[(int64_t)ch * 3 * 16 * kHeadDim];
-    T* out = static_cast<T*>(m == 0 ? a.dq : m == 1 ? a.dk : a.dv);
-    out[base + (int64_t)r * a.H * kHeadDim + d] = static_cast<T>(m == 2 ? s : s * a.scale);
-  }
+  const float* p = a.part + (int64_t)bh * a.chunks * kLfPart + e;
+  float s = 0.0f;
+#pragma unroll 8
+  for (int ch = 0; ch < a.chunks; ++ch) s += p[(int64_t)ch * kLfPart];
+  T* out = static_cast<T*>(m == 0 ? a.dq : m == 1 ? a.dk : a.dv);
+  out[((int64_t)b * a.N * a.H + h) * kHeadDim + (int64_t)r * a.H * kHeadDim + d] =
+      static_cast<T>(m == 2 ? s : s * a.scale);
 }
 
 }  // namespace ma_dev

@@ -1856,7 +1856,7 @@ int launch_lf_bwd(const ma_attn_desc* d, const void* const* ptrs, const void* o,
   if (reserve_lds(reinterpret_cast<const void*>(kf), (size_t)LfLds::kBytes, st)) return 1;
   const int64_t streams = d->batch * d->num_heads;
   launch(false, kf, dim3((unsigned)(streams * p.chunks)), dim3(kLfWaves * 64), (uint32_t)LfLds::kBytes, st, a);
-  launch(true, bwd_lf_combine<T>, dim3((unsigned)streams), dim3(256), 0u, st, a);
+  launch(true, bwd_lf_combine<T>, dim3((unsigned)(streams * kLfCombineBlocks)), dim3(256), 0u, st, a);
   return 0;
 }
 
