@@ -246,7 +246,8 @@ def test_layer_trains_from_saved_statistics(ext, oracle, pattern, dtype, monkeyp
     """MACoreAttention training on the device (fallback_training=False) keeps
     the forward's statistics and runs the backward from them where the
     forward's kernel writes them (fp32 Longformer's does not: that case
-    recomputes them); gradients match the oracle's either way."""
+    recomputes them; 16-bit Longformer runs the one-pass longformer_backward);
+    gradients match the oracle's either way."""
     from layers.ma_core_bridge import MACoreAttention
     N = 1536
     shape = (2, N, 2, 64)
@@ -264,7 +265,12 @@ def test_layer_trains_from_saved_statistics(ext, oracle, pattern, dtype, monkeyp
         spec = oracle.Spec(*shape, pattern="dense", causal=True)
     layer.train()
     calls = []
-    fn = "dense_backward" if pattern == "dense" else "index_set_backward"
+    if pattern == "dense":
+        fn = "dense_backward"
+    elif pattern == "longformer" and dtype != torch.float32:
+        fn = "longformer_backward"
+    else:
+        fn = "index_set_backward"
     real = getattr(ext, fn)
 
     def spy(*a, **kw):
