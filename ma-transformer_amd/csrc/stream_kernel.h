@@ -74,13 +74,20 @@ __device__ __forceinline__ void store_lse(float* lse, int64_t row, bool valid, f
 // O[c][32+8g..32+8g+7] in acc[2..3]: two 16 B stores per lane.  For that
 // order lane l of a transpose read addresses V row l>>2 at head_dim
 // 32*(dt>>1) + 8*(l&3) + 4*(dt&1): v_lane + v_tr(dt).
-template <typename T>
+//
+// KROW: bytes per K or V row in LDS (128 + pad).  160 puts the four rows of a
+// transpose read's 16-lane group on disjoint LDS banks; 144 keeps the 16-byte
+// row reads conflict-free instead.  160 measured faster for the forward and
+// tiled kernels (target 54.0 -> 53.5 us, cfg3 backward from saved statistics
+// 132 -> 124 us, A/B on one box); the fused backward keeps 144, which fits
+// two of its workgroups per CU.
+template <typename T, int KROW = 160>
 struct HalfPath {
   using Elt = T;
   static constexpr int kRows = 64;                 // keys per ring slot
-  static constexpr int kKRow = 144;                // bytes per K or V row in LDS (128 + 16 pad)
-  static constexpr int kSlotK = kRows * kKRow;     // 9216
-  static constexpr int kSlot = 2 * kSlotK;         // 18432: K rows, then V rows
+  static constexpr int kKRow = KROW;               // bytes per K or V row in LDS
+  static constexpr int kSlotK = kRows * kKRow;     // 10240 at 160 B rows
+  static constexpr int kSlot = 2 * kSlotK;         // K rows, then V rows
   static constexpr int kMinBlocks = 4;             // launch bound (workgroups per CU)
   static constexpr bool kTrRows = true;            // transposed operands read from rows (tr_read)
   struct Q {
