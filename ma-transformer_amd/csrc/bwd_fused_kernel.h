@@ -25,7 +25,7 @@
 //     all through gfx950's LDS transpose read (ds_read_b64_tr_b16), which
 //     turns row-major [query][key] into the MFMA operand layout.  Block kb is
 //     then complete and stored; block kb+1's partial sums carry to step t+1.
-// No slot holds a transposed copy and no statistics leave registers: 76 KB
+// No slot holds a transposed copy and no statistics leave registers: 80 KB
 // of LDS, two workgroups per CU.  While step t computes, step t+1's key
 // block and query tile are in flight into registers.
 //
@@ -50,19 +50,22 @@
 
 namespace ma_dev {
 
-// Rows of 144 B, the 16-bit path's padded rows (136 B rows, read as 8-byte
-// pairs, halved the bank-conflict counter and left the time unchanged).
+// Rows of 160 B, the 16-bit path's padded rows (HalfPath's KROW: transpose
+// reads on disjoint banks); exchange rows unpadded, so that two workgroups
+// still fit a CU.  (At 144 B rows and 176 B exchange rows, 76 KB, the kernel
+// took 0.2-0.9 % longer; 136 B rows read as 8-byte pairs halved the
+// bank-conflict counter and left the time unchanged.)
 struct FusedLds {
-  static constexpr int kRow = 144;                // bytes per K/V/Q/dO row (128 + 16 pad)
+  static constexpr int kRow = 160;                // bytes per K/V/Q/dO row (128 + 32 pad)
   static constexpr int kMat = 64 * kRow;          // one 64-row matrix
   static constexpr int kRing = 2 * kMat;          // one ring slot: K rows, V rows
   static constexpr int kQ = 2 * kRing;            // tile t's Q rows
   static constexpr int kG = kQ + kMat;            // tile t's dO rows
-  static constexpr int kXRow = 176;               // exchange row: 80 keys (160 B) + 16 pad
+  static constexpr int kXRow = 160;               // exchange row: 80 keys (160 B), unpadded
   static constexpr int kXW = 16 * kXRow;          // one wave's 16 query rows
   static constexpr int kXP = kG + kMat;           // P, 4 waves
   static constexpr int kXD = kXP + 4 * kXW;       // dS, 4 waves
-  static constexpr int kBytes = kXD + 4 * kXW;    // 77824
+  static constexpr int kBytes = kXD + 4 * kXW;    // 81920: two workgroups fill a CU's 160 KB
 };
 
 // A operand of M^T for head_dim tile dt from a 16-row sub-tile of a

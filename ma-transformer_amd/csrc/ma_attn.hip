@@ -1659,13 +1659,12 @@ int launch_backward_mfma(const ma_attn_desc* d, const void* const* ptrs, float* 
   if constexpr (P::kSPB == 1) {
     if (fixed != 0 && !g_opt.bwd_unfused) {
       // the fixed windows in 16 bits: one fused launch (bwd_fused_kernel.h),
-      // 76 KB of LDS, two workgroups per CU; chunks fitted to one round of
+      // 80 KB of LDS, two workgroups per CU; chunks fitted to one round of
       // the resident workgroups (measured on the target: one round, chunk 16,
       // 10-15 % faster than two to six rounds)
       const size_t shm = (size_t)FusedLds::kBytes;
       fused_chunks(a, streams);
-      using FP = HalfPath<typename P::Elt, FusedLds::kRow>;  // the fused kernel's 144 B rows
-      auto kf = fixed == 1 ? &bwd_fused_kernel<FP, 63, 0> : &bwd_fused_kernel<FP, 32, 31>;
+      auto kf = fixed == 1 ? &bwd_fused_kernel<P, 63, 0> : &bwd_fused_kernel<P, 32, 31>;
       if (reserve_lds(reinterpret_cast<const void*>(kf), shm, st)) return 1;
       launch(true, kf, dim3((unsigned)(streams * a.chunks)), dim3(256), (uint32_t)shm, st, a);
       return 0;

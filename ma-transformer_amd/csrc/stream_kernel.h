@@ -77,10 +77,9 @@ __device__ __forceinline__ void store_lse(float* lse, int64_t row, bool valid, f
 //
 // KROW: bytes per K or V row in LDS (128 + pad).  160 puts the four rows of a
 // transpose read's 16-lane group on disjoint LDS banks; 144 keeps the 16-byte
-// row reads conflict-free instead.  160 measured faster for the forward and
-// tiled kernels (target 54.0 -> 53.5 us, cfg3 backward from saved statistics
-// 132 -> 124 us, A/B on one box); the fused backward keeps 144, which fits
-// two of its workgroups per CU.
+// row reads conflict-free instead.  160 measured faster (A/B on one box:
+// dense causal bf16 forward 417 -> 388 us, backward 1783 -> 1645 us, cfg3
+// backward from saved statistics 130 -> 125 us, the fused backward 0.2-0.9 %).
 template <typename T, int KROW = 160>
 struct HalfPath {
   using Elt = T;
