@@ -21,29 +21,34 @@
 //
 // Rows and keys come in 128-row tiles / blocks, so query tile t meets key
 // blocks t-1 and t, and key block j is seen by query tiles j and j+1.  One
-// workgroup (8 waves) streams a chunk [t0, t1) of query tiles of one
-// (batch, head) and owns key blocks [t0, t1); LDS holds the K, V rows of
-// blocks t-1 and t (a two-slot ring), tile t's Q and dO rows and statistics,
-// and the 16 global keys' K, V rows and global rows' Q, dO rows.  Step t:
-//   query pass   wave w: queries 128t + 16w + c against their 9 window key
-//                sub-tiles and the global keys (P^T, dS^T with the query as
-//                the MFMA column), dQ^T += K^T dS^T, dQ stored;
-//   global keys  wave w: the same queries against the global keys with the
-//                key as the MFMA column, the global keys' dK^T, dV^T summed
-//                over the chunk;
-//   key pass     wave w owns keys 16w.. of blocks t-1 and t: the tile's
+// workgroup (12 waves, one per CU, 3 per SIMD) streams a chunk [t0, t1) of
+// query tiles of one (batch, head) and owns key blocks [t0, t1); LDS holds
+// the K, V rows of blocks t-1 and t (a two-slot ring), tile t's Q and dO rows
+// and statistics, and the 16 global keys' K, V rows and global rows' Q, dO
+// rows.  Step t:
+//   query pass   main wave w (0-7): queries 128t + 16w + c against their 9
+//                window key sub-tiles and the global keys (P^T, dS^T with the
+//                query as the MFMA column), dQ^T += K^T dS^T, dQ stored;
+//   key pass     main wave w owns keys 16w.. of blocks t-1 and t: the tile's
 //                query sub-tiles that see them, P, dS recomputed with the key
 //                as the MFMA column (no exchange area), dV^T += dO^T P,
 //                dK^T += Q^T dS; block t-1 is then complete: the global
-//                rows' contributions are added (and their dQ summed over the
-//                chunk) and its dK, dV stored.  Block t's sums carry.
-// A chunk also runs the key pass of tile t1 (no dQ) for its block t1-1, and
-// reads block t0-1 for tile t0's queries.  The global rows' dQ and the
-// global keys' dK, dV are per-chunk sums in the workspace; bwd_lf_combine
-// adds them up and writes rows 0..G-1 of dQ, dK, dV.  Every other row of
-// dQ, dK, dV has one writer; no atomics.  Rows past the end read as zero and
-// their stores are dropped by the buffer range check; rows below 0 (block
-// -1) wrap past the range the same way.
+//                rows' contributions are added and its dK, dV stored.
+//                Block t's sums carry;
+//   global sums  helper wave w (0-3): query sub-tiles 2w, 2w+1 against the
+//                global keys with the key as the MFMA column (the global
+//                keys' dK^T, dV^T) and the global rows against key sub-tiles
+//                2w, 2w+1 of each completed block (the global rows' dQ^T),
+//                summed over the chunk.
+// The main waves load the next key block and the helpers the next query
+// tile.  A chunk also runs the key pass of tile t1 (no dQ) for its block
+// t1-1, and reads block t0-1 for tile t0's queries.  The global rows' dQ and
+// the global keys' dK, dV are per-chunk sums in the workspace (with one more
+// slot for block 0's sums of keys 0..G-1); bwd_lf_combine adds them up and
+// writes rows 0..G-1 of dQ, dK, dV.  Every other row of dQ, dK, dV has one
+// writer; no atomics.  Rows past the end read as zero and their stores are
+// dropped by the buffer range check; rows below 0 (block -1) wrap past the
+// range the same way.
 #pragma once
 
 #include "bwd_fused_kernel.h"
@@ -60,7 +65,7 @@ struct LfArgs {
   void* dq;
   void* dk;
   void* dv;
-  float* part;  // [B*H][chunks][3][16][64]: global rows' dQ, global keys' dK, dV (unscaled sums)
+  float* part;  // [B*H][chunks + 1][3][16][64]: global rows' dQ, global keys' dK, dV (unscaled sums)
   int32_t N, H, L, G;
   int32_t chunk, chunks;
   int32_t tok_bytes;
@@ -68,7 +73,9 @@ struct LfArgs {
 };
 
 constexpr int kLfRows = 128;  // rows per query tile and key block
-constexpr int kLfWaves = 8;
+constexpr int kLfWaves = 8;    // main waves: the query and key passes
+constexpr int kLfHelpers = 4;  // helper waves: tile loads and the global sums
+constexpr int kLfThreads = 64 * (kLfWaves + kLfHelpers);  // 768
 constexpr int kLfPart = 3 * 16 * kHeadDim;  // one chunk's partials: dQ, dK, dV of 16 rows
 
 struct LfLds {
@@ -98,7 +105,7 @@ __device__ __forceinline__ void lf_lds_q(typename P::Q& x, const uint8_t* mat, i
   x.r[0] = *reinterpret_cast<const uint4*>(mat + r * LfLds::kRow + 16 * g);
   x.r[1] = *reinterpret_cast<const uint4*>(mat + r * LfLds::kRow + 16 * g + 64);
 }
-// the chunk-end reduction of the 8 waves' sums reuses the ring: 4 waves x 12 KB
+// the chunk-end reduction of the helpers' sums reuses the ring: 2 waves x 12 KB
 static_assert(4 * 64 * 48 * 4 <= LfLds::kQ, "reduction area");
 
 // 16-bit dot product of two 8-element pieces, in fp32.
@@ -123,8 +130,8 @@ __device__ __forceinline__ float sum8(float x) {
   return x + __shfl_xor(x, 4);
 }
 
-// A 128-row matrix in flight: thread tid carries rows tid>>3 and (tid>>3)+64
-// at 16-byte column tid&7.
+// A 128-row matrix in flight over the 512 threads of the main waves: thread
+// tid carries rows tid>>3 and (tid>>3)+64 at 16-byte column tid&7.
 struct Rows128 {
   uint4 r[2];
 };
@@ -139,23 +146,40 @@ __device__ __forceinline__ void lf_store(const Rows128& x, uint8_t* mat, int tid
   *reinterpret_cast<uint4*>(p + 64 * LfLds::kRow) = x.r[1];
 }
 
-// A query tile in flight: Q, dO and O rows and the statistic of row tid (tid < 128).
+// The same over the 256 threads of the helper waves (ht = tid - 512): rows
+// (ht>>3) + 32k, k = 0..3, at 16-byte column ht&7.
+struct Rows128x4 {
+  uint4 r[4];
+};
+__device__ __forceinline__ void lf_load4(Rows128x4& x, __amdgpu_buffer_rsrc_t R, uint32_t off, int ht, uint32_t tb) {
+  const uint32_t o = off + (uint32_t)(ht >> 3) * tb + 16 * (ht & 7);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) x.r[k] = bload16(R, o + 32 * k * tb);
+}
+__device__ __forceinline__ void lf_store4(const Rows128x4& x, uint8_t* mat, int ht) {
+  uint8_t* p = mat + (ht >> 3) * LfLds::kRow + 16 * (ht & 7);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) *reinterpret_cast<uint4*>(p + 32 * k * LfLds::kRow) = x.r[k];
+}
+
+// A query tile in flight (helper waves): Q, dO and O rows and the statistic
+// of row ht (ht < 128).
 struct LfTile {
-  Rows128 q, g, o;
+  Rows128x4 q, g, o;
   float lse2;
 };
 
 // Tile t's rows into LDS: Q and dO rows, each row's lse2 and delta = dO . O.
 template <typename T>
-__device__ __forceinline__ void lf_stage_tile(const LfTile& x, uint8_t* lds, int tid) {
-  lf_store(x.q, lds + LfLds::kQ, tid);
-  lf_store(x.g, lds + LfLds::kG, tid);
+__device__ __forceinline__ void lf_stage_tile(const LfTile& x, uint8_t* lds, int ht) {
+  lf_store4(x.q, lds + LfLds::kQ, ht);
+  lf_store4(x.g, lds + LfLds::kG, ht);
   float* st = reinterpret_cast<float*>(lds + LfLds::kSt);
-  if (tid < kLfRows) st[tid] = x.lse2;
+  if (ht < kLfRows) st[ht] = x.lse2;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const float d = sum8(dot8<T>(x.g.r[h], x.o.r[h]));
-    if ((tid & 7) == 0) st[kLfRows + (tid >> 3) + 64 * h] = d;
+  for (int k = 0; k < 4; ++k) {
+    const float d = sum8(dot8<T>(x.g.r[k], x.o.r[k]));
+    if ((ht & 7) == 0) st[kLfRows + (ht >> 3) + 32 * k] = d;
   }
 }
 
@@ -273,62 +297,70 @@ __device__ __forceinline__ void lf_kpass(const uint8_t* lds, const typename P::Q
   }
 }
 
-// The global rows' contributions to one key sub-tile (lane c = key k0 + c,
-// K / V rows at krows / vrows, their register operands kr / vr): dK^T, dV^T
-// of the keys (key as the MFMA column) and the global rows' dQ^T (global
-// query as the column).
+// The global rows' contributions to the dK^T, dV^T of one key sub-tile (lane
+// c = key k0 + c, key as the MFMA column; K, V of the keys as the register
+// operands kr / vr).
 template <class P>
-__device__ __forceinline__ void lf_global_rows(const uint8_t* lds, const uint8_t* krows, const uint8_t* vrows,
-                                               const typename P::Q& kr, const typename P::Q& vr, int k0, int G,
-                                               int N, int c, int g, uint32_t kl, uint32_t trl, float sl2,
-                                               f32x4 (&ak)[4], f32x4 (&av)[4], f32x4 (&agq)[4]) {
+__device__ __forceinline__ void lf_global_rows_kv(const uint8_t* lds, const typename P::Q& kr,
+                                                  const typename P::Q& vr, int k0, int G, int N, int c, int g,
+                                                  uint32_t kl, uint32_t trl, float sl2, f32x4 (&ak)[4],
+                                                  f32x4 (&av)[4]) {
   using T = typename P::Elt;
   const float* sg = reinterpret_cast<const float*>(lds + LfLds::kStG);
-  {
-    const f32x4 s = P::qk(lds + LfLds::kGQ + kl, kr);   // S[global query 4g + r][key c]
-    const f32x4 dp = P::qk(lds + LfLds::kGG + kl, vr);
-    const f32x4 l4 = *reinterpret_cast<const f32x4*>(sg + 4 * g);
-    const f32x4 d4 = *reinterpret_cast<const f32x4*>(sg + 16 + 4 * g);
-    float lse2[4], dlt[4], p[4], ds[4];
-    bool keep[4];
+  const f32x4 s = P::qk(lds + LfLds::kGQ + kl, kr);  // S[global query 4g + r][key c]
+  const f32x4 dp = P::qk(lds + LfLds::kGG + kl, vr);
+  const f32x4 l4 = *reinterpret_cast<const f32x4*>(sg + 4 * g);
+  const f32x4 d4 = *reinterpret_cast<const f32x4*>(sg + 16 + 4 * g);
+  float lse2[4], dlt[4], p[4], ds[4];
+  bool keep[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      keep[r] = 4 * g + r < G && k0 + c < N;
-      lse2[r] = l4[r];
-      dlt[r] = d4[r];
-    }
-    lf_probs(s, dp, lse2, dlt, keep, sl2, p, ds);
-    pv_tr<T>(lds + LfLds::kGG + trl, pack4<T>(p), av);
-    pv_tr<T>(lds + LfLds::kGQ + trl, pack4<T>(ds), ak);
+  for (int r = 0; r < 4; ++r) {
+    keep[r] = 4 * g + r < G && k0 + c < N;
+    lse2[r] = l4[r];
+    dlt[r] = d4[r];
   }
-  {
-    typename P::Q qg, gg;
-    lf_lds_q<P>(qg, lds + LfLds::kGQ, c, g);
-    lf_lds_q<P>(gg, lds + LfLds::kGG, c, g);
-    const f32x4 s = P::qk(krows + kl, qg);  // S^T[key 4g + r][global query c]
-    const f32x4 dp = P::qk(vrows + kl, gg);
-    const float lse2c = sg[c], dltc = sg[16 + c];
-    float lse2[4], dlt[4], p[4], ds[4];
-    bool keep[4];
+  lf_probs(s, dp, lse2, dlt, keep, sl2, p, ds);
+  pv_tr<T>(lds + LfLds::kGG + trl, pack4<T>(p), av);
+  pv_tr<T>(lds + LfLds::kGQ + trl, pack4<T>(ds), ak);
+}
+
+// The global rows' dQ^T from one key sub-tile (keys k0.., K / V rows at
+// krows / vrows; global query as the MFMA column).
+template <class P>
+__device__ __forceinline__ void lf_global_rows_dq(const uint8_t* lds, const uint8_t* krows, const uint8_t* vrows,
+                                                  int k0, int G, int N, int c, int g, uint32_t kl, uint32_t trl,
+                                                  float sl2, f32x4 (&agq)[4]) {
+  using T = typename P::Elt;
+  const float* sg = reinterpret_cast<const float*>(lds + LfLds::kStG);
+  typename P::Q qg, gg;
+  lds_q<P>(qg, lds + LfLds::kGQ, c, g);
+  lds_q<P>(gg, lds + LfLds::kGG, c, g);
+  const f32x4 s = P::qk(krows + kl, qg);  // S^T[key 4g + r][global query c]
+  const f32x4 dp = P::qk(vrows + kl, gg);
+  const float lse2c = sg[c], dltc = sg[16 + c];
+  float lse2[4], dlt[4], p[4], ds[4];
+  bool keep[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      keep[r] = c < G && k0 + 4 * g + r < N;
-      lse2[r] = lse2c;
-      dlt[r] = dltc;
-    }
-    lf_probs(s, dp, lse2, dlt, keep, sl2, p, ds);
-    pv_tr_split<T>(krows + trl, ds, agq);
+  for (int r = 0; r < 4; ++r) {
+    keep[r] = c < G && k0 + 4 * g + r < N;
+    lse2[r] = lse2c;
+    dlt[r] = dltc;
   }
+  lf_probs(s, dp, lse2, dlt, keep, sl2, p, ds);
+  pv_tr_split<T>(krows + trl, ds, agq);
 }
 
 // FIXED127: L = 127, the band's sub-tiles selected by the fixed masks.
 template <class P, bool FIXED127>
-__global__ __launch_bounds__(512, 1) void bwd_lf_kernel(LfArgs a) {
+__global__ __launch_bounds__(kLfThreads, 1) void bwd_lf_kernel(LfArgs a) {
   using T = typename P::Elt;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // LfLds
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wq = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool main_wave = wq < kLfWaves;
+  const int wv = main_wave ? wq : wq - kLfWaves;  // main: 0..7, helper: 0..3
+  const int ht = tid - 64 * kLfWaves;             // a helper's thread index (0..255)
   const int c = lane & 15;
   const int g = lane >> 4;
 
@@ -354,24 +386,31 @@ __global__ __launch_bounds__(512, 1) void bwd_lf_kernel(LfArgs a) {
   const __amdgpu_buffer_rsrc_t DKr = make_rsrc(static_cast<T*>(a.dk) + base, nrec);
   const __amdgpu_buffer_rsrc_t DVr = make_rsrc(static_cast<T*>(a.dv) + base, nrec);
   const float* lse = a.lse + (int64_t)b * N * a.H + h;  // row i at i * H
+  float* part = a.part + (int64_t)bh * (a.chunks + 1) * kLfPart;
   // byte offset of row r (r >= -128); rows below 0 wrap past the range
   auto roff = [&](int r) { return (uint32_t)r * tb; };
   auto slot = [&](int j) { return lds + (j & 1) * LfLds::kSlot; };
-  auto load_tile = [&](LfTile& x, int t) {
+  auto load_tile = [&](LfTile& x, int t) {  // helper waves
     const uint32_t o = roff(kLfRows * t);
-    lf_load(x.q, Qr, o, tid, tb);
-    lf_load(x.g, Gr, o, tid, tb);
-    lf_load(x.o, Or, o, tid, tb);
-    const int i = kLfRows * t + tid;  // no band pair for a row outside [G, N): P = 0
-    x.lse2 = tid < kLfRows && i >= G && i < N ? lse[(int64_t)i * a.H] : __builtin_inff();
+    lf_load4(x.q, Qr, o, ht, tb);
+    lf_load4(x.g, Gr, o, ht, tb);
+    lf_load4(x.o, Or, o, ht, tb);
+    const int i = kLfRows * t + ht;  // no band pair for a row outside [G, N): P = 0
+    x.lse2 = ht < kLfRows && i >= G && i < N ? lse[(int64_t)i * a.H] : __builtin_inff();
+  };
+  // row c, head_dim 16dt + 4g + r of matrix m (0 dQ, 1 dK, 2 dV) of a slot of partials
+  auto store_part = [&](int slot_id, int m, const f32x4(&v)[4]) __attribute__((always_inline)) {
+    float* dst = part + (int64_t)slot_id * kLfPart + m * 16 * kHeadDim + c * kHeadDim + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) *reinterpret_cast<f32x4*>(dst + 16 * dt) = v[dt];
   };
   const float sl2 = a.scale_log2;
   const uint32_t kl = c * LfLds::kRow + 16 * g;
   const uint32_t trl = lf_tr_lane(lane);
 
   // prologue: the global keys' K, V rows and the global rows' Q, dO rows
-  // and statistics (waves 0 and 1: one 16-byte piece per thread), the key
-  // blocks t0-1 and t0, and tile t0
+  // and statistics (main waves 0 and 1: one 16-byte piece per thread), the
+  // key blocks t0-1 and t0 (main waves) and tile t0 (helpers)
   if (tid < 128) {  // uniform per wave
     const uint32_t o = (uint32_t)(tid >> 3) * tb + 16 * (tid & 7);
     const uint4 kx = bload16(Kr, o), vx = bload16(Vr, o), qx = bload16(Qr, o), gx = bload16(Gr, o);
@@ -389,7 +428,7 @@ __global__ __launch_bounds__(512, 1) void bwd_lf_kernel(LfArgs a) {
       sg[16 + r] = d;
     }
   }
-  {
+  if (main_wave) {
     Rows128 xk, xv;
     lf_load(xk, Kr, roff(kLfRows * (t0 - 1)), tid, tb);
     lf_load(xv, Vr, roff(kLfRows * (t0 - 1)), tid, tb);
@@ -397,229 +436,246 @@ __global__ __launch_bounds__(512, 1) void bwd_lf_kernel(LfArgs a) {
     lf_store(xv, slot(t0 - 1) + LfLds::kMat, tid);
     lf_load(xk, Kr, roff(kLfRows * t0), tid, tb);
     lf_load(xv, Vr, roff(kLfRows * t0), tid, tb);
-    LfTile x;
-    load_tile(x, t0);
     lf_store(xk, slot(t0), tid);
     lf_store(xv, slot(t0) + LfLds::kMat, tid);
-    lf_stage_tile<T>(x, lds, tid);
+  } else {
+    LfTile x;
+    load_tile(x, t0);
+    lf_stage_tile<T>(x, lds, ht);
   }
   __syncthreads();
 
-  // sums of this wave's keys 16wv.. of the carried block (t-1 at step t,
-  // then t); the global rows' dQ and the global keys' dK, dV over the chunk
-  f32x4 ak0[4], av0[4], agq[4], agk[4], agv[4];
+  if (main_wave) {
+    // ---- main waves: query pass, key pass and the completed blocks' dK, dV
+    f32x4 ak0[4], av0[4];  // sums of keys 16wv.. of the carried block (t-1 at step t, then t)
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt) {
-    ak0[dt] = av0[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    agq[dt] = agk[dt] = agv[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  }
-
-  // block j complete (its sums in ak, av): the global rows' part, then dK,
-  // dV of keys 16wv.. stored (rows 0..G-1 are rewritten by the combine, so
-  // block 0's global keys also go to the chunk's global-key sums)
-  auto finish_block = [&](int j, f32x4(&ak)[4], f32x4(&av)[4]) __attribute__((always_inline)) {
-    const uint8_t* krows = slot(j) + 16 * wv * LfLds::kRow;
-    const uint8_t* vrows = krows + LfLds::kMat;
-    typename P::Q kr, vr;
-    lf_lds_q<P>(kr, slot(j), 16 * wv + c, g);
-    lf_lds_q<P>(vr, slot(j) + LfLds::kMat, 16 * wv + c, g);
-    lf_global_rows<P>(lds, krows, vrows, kr, vr, kLfRows * j + 16 * wv, G, N, c, g, kl, trl, sl2, ak, av, agq);
-    if (j == 0 && wv == 0 && c < G) {  // the global keys: their totals come from the combine
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        agk[dt] += ak[dt];
-        agv[dt] += av[dt];
+    for (int dt = 0; dt < 4; ++dt) ak0[dt] = av0[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // block j complete (its sums in ak0, av0): the global rows' part, then
+    // dK, dV of keys 16wv.. stored.  Rows 0..G-1 are rewritten by the
+    // combine: block 0's sums for them go to the extra slot of partials.
+    auto finish_block = [&](int j, const typename P::Q& kr, const typename P::Q& vr) __attribute__((always_inline)) {
+      const int k0 = kLfRows * j + 16 * wv;
+      lf_global_rows_kv<P>(lds, kr, vr, k0, G, N, c, g, kl, trl, sl2, ak0, av0);
+      if (j == 0 && wv == 0 && c < G) {
+        store_part(a.chunks, 1, ak0);
+        store_part(a.chunks, 2, av0);
       }
-    }
-    const uint32_t row = roff(kLfRows * j + 16 * wv + c);
-    store_nat<T>(av, 1.0f, DVr, row, g);
-    store_nat<T>(ak, a.scale, DKr, row, g);
-  };
+      const uint32_t row = roff(k0 + c);
+      store_nat<T>(av0, 1.0f, DVr, row, g);
+      store_nat<T>(ak0, a.scale, DKr, row, g);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) ak0[dt] = av0[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    };
 
-  for (int t = t0; t <= s1; ++t) {
-    const bool more = t < s1;
-    const bool own = t < t1;  // tile t's queries are this chunk's
-    Rows128 nk, nv;
-    LfTile nx;
-    if (more) {  // step t+1's key block and query tile in flight
-      lf_load(nk, Kr, roff(kLfRows * (t + 1)), tid, tb);
-      lf_load(nv, Vr, roff(kLfRows * (t + 1)), tid, tb);
-      load_tile(nx, t + 1);
-    }
-    const float* st = reinterpret_cast<const float*>(lds + LfLds::kSt);
+    for (int t = t0; t <= s1; ++t) {
+      const bool more = t < s1;
+      const bool own = t < t1;  // tile t's queries are this chunk's
+      Rows128 nk, nv;
+      if (more) {  // step t+1's key block in flight
+        lf_load(nk, Kr, roff(kLfRows * (t + 1)), tid, tb);
+        lf_load(nv, Vr, roff(kLfRows * (t + 1)), tid, tb);
+      }
+      const float* st = reinterpret_cast<const float*>(lds + LfLds::kSt);
 
-    if (own) {
-      // ---- query pass: queries i = 128t + 16wv + c, keys 4g + r of each sub-tile
-      const int i = kLfRows * t + 16 * wv + c;
-      typename P::Q qb, gb;
-      lf_lds_q<P>(qb, lds + LfLds::kQ, 16 * wv + c, g);
-      lf_lds_q<P>(gb, lds + LfLds::kG, 16 * wv + c, g);
-      const float lse2c = st[16 * wv + c], dltc = st[kLfRows + 16 * wv + c];
-      float lse2[4], dlt[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        lse2[r] = lse2c;
-        dlt[r] = dltc;
-      }
-      f32x4 acc[4];
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      {  // the global keys 0..G-1 outside the row's band
-        const f32x4 s = P::qk(lds + LfLds::kGK + kl, qb);
-        const f32x4 dp = P::qk(lds + LfLds::kGV + kl, gb);
-        bool keep[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) keep[r] = 4 * g + r < G && i - (4 * g + r) > L;
-        float p[4], ds[4];
-        lf_probs(s, dp, lse2, dlt, keep, sl2, p, ds);
-        pv_tr<T>(lds + LfLds::kGK + trl, pack4<T>(ds), acc);
-      }
-      // window sub-tiles s = 8t + wv - 8 + jj (keys 16s..16s+15), jj = 0..8, in
-      // blocks t-1 and t, i - key = 16(8 - jj) + c - (4g + r); one 16x16x16
-      // MFMA per sub-tile and head_dim tile.  (Pairing sub-tiles on 16x16x32
-      // MFMA here, with each pair's products issued between the next
-      // sub-tile's scores, gave intermittently wrong dQ for whole waves on the
-      // device; the one-sub-tile form, the same MFMA work, did not in any of
-      // the repeated runs.)
-#pragma unroll
-      for (int jj = 0; jj < 9; ++jj) {
-        const int s = 8 * t + wv - 8 + jj;
-        const uint32_t sub = (uint32_t)((s >> 3) & 1) * LfLds::kSlot + 16 * (s & 7) * LfLds::kRow;
-        const f32x4 sc = P::qk(lds + sub + kl, qb);
-        const f32x4 dp = P::qk(lds + sub + LfLds::kMat + kl, gb);
-        const float l2 = s < 0 ? __builtin_inff() : lse2c;  // keys below row 0 (tile 0): no pair
-        float ls[4], p[4], ds[4];
-        int dq[4];
+      if (own) {
+        // ---- query pass: queries i = 128t + 16wv + c, keys 4g + r of each sub-tile
+        const int i = kLfRows * t + 16 * wv + c;
+        typename P::Q qb, gb;
+        lf_lds_q<P>(qb, lds + LfLds::kQ, 16 * wv + c, g);
+        lf_lds_q<P>(gb, lds + LfLds::kG, 16 * wv + c, g);
+        const float lse2c = st[16 * wv + c], dltc = st[kLfRows + 16 * wv + c];
+        float lse2[4], dlt[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          ls[r] = l2;
-          dq[r] = 16 * (8 - jj) + c - (4 * g + r);
+          lse2[r] = lse2c;
+          dlt[r] = dltc;
         }
-        if (!FIXED127)
-          lf_probs_m<kLfBand>(sc, dp, ls, dlt, dq, L, c, g, sl2, p, ds);
-        else if (jj == 0)
-          lf_probs_m<kLfColBefore>(sc, dp, ls, dlt, dq, L, c, g, sl2, p, ds);
-        else if (jj == 8)
-          lf_probs_m<kLfColFrom>(sc, dp, ls, dlt, dq, L, c, g, sl2, p, ds);
-        else
-          lf_probs_m<kLfAll>(sc, dp, ls, dlt, dq, L, c, g, sl2, p, ds);
-        pv_tr<T>(lds + sub + trl, pack4<T>(ds), acc);
+        f32x4 acc[4];
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        {  // the global keys 0..G-1 outside the row's band
+          const f32x4 s = P::qk(lds + LfLds::kGK + kl, qb);
+          const f32x4 dp = P::qk(lds + LfLds::kGV + kl, gb);
+          bool keep[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) keep[r] = 4 * g + r < G && i - (4 * g + r) > L;
+          float p[4], ds[4];
+          lf_probs(s, dp, lse2, dlt, keep, sl2, p, ds);
+          pv_tr<T>(lds + LfLds::kGK + trl, pack4<T>(ds), acc);
+        }
+        // window sub-tiles s = 8t + wv - 8 + jj (keys 16s..16s+15), jj = 0..8,
+        // in blocks t-1 and t, i - key = 16(8 - jj) + c - (4g + r); one
+        // 16x16x16 MFMA per sub-tile and head_dim tile.  (Pairing sub-tiles on
+        // 16x16x32 MFMA here, with each pair's products issued between the
+        // next sub-tile's scores, gave intermittently wrong dQ for whole waves
+        // on the device; the one-sub-tile form, the same MFMA work, did not
+        // in any of the repeated runs.)
+#pragma unroll
+        for (int jj = 0; jj < 9; ++jj) {
+          const int s = 8 * t + wv - 8 + jj;
+          const uint32_t sub = (uint32_t)((s >> 3) & 1) * LfLds::kSlot + 16 * (s & 7) * LfLds::kRow;
+          const f32x4 sc = P::qk(lds + sub + kl, qb);
+          const f32x4 dp = P::qk(lds + sub + LfLds::kMat + kl, gb);
+          const float l2 = s < 0 ? __builtin_inff() : lse2c;  // keys below row 0 (tile 0): no pair
+          float ls[4], p[4], ds[4];
+          int dq[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            ls[r] = l2;
+            dq[r] = 16 * (8 - jj) + c - (4 * g + r);
+          }
+          if (!FIXED127)
+            lf_probs_m<kLfBand>(sc, dp, ls, dlt, dq, L, c, g, sl2, p, ds);
+          else if (jj == 0)
+            lf_probs_m<kLfColBefore>(sc, dp, ls, dlt, dq, L, c, g, sl2, p, ds);
+          else if (jj == 8)
+            lf_probs_m<kLfColFrom>(sc, dp, ls, dlt, dq, L, c, g, sl2, p, ds);
+          else
+            lf_probs_m<kLfAll>(sc, dp, ls, dlt, dq, L, c, g, sl2, p, ds);
+          pv_tr<T>(lds + sub + trl, pack4<T>(ds), acc);
+        }
+        store_nat<T>(acc, a.scale, DQr, i >= G && i < N ? roff(i) : kOob, g);
       }
-      store_nat<T>(acc, a.scale, DQr, i >= G && i < N ? roff(i) : kOob, g);
 
-      // ---- the global keys' dK, dV from this wave's queries (key as the
-      // column), pairs outside the band
-      {
+      // ---- key pass: tile t's queries into keys 16wv.. of blocks t-1 and t
+      const int q0 = kLfRows * t;
+      if (t > t0) {  // block t-1 is this chunk's: query sub-tiles 0..wv reach its keys
+        typename P::Q kr, vr;
+        lf_lds_q<P>(kr, slot(t - 1), 16 * wv + c, g);
+        lf_lds_q<P>(vr, slot(t - 1) + LfLds::kMat, 16 * wv + c, g);
+        const int k0 = kLfRows * (t - 1) + 16 * wv;
+        if (FIXED127) {  // i - key = 128 + 16(jq - wv) + (4g + r) - c
+          lf_kpass<P, kLfAll>(lds, kr, vr, k0, q0, 0, wv - 1, L, c, g, kl, trl, sl2, ak0, av0);
+          lf_kpass<P, kLfColAfter>(lds, kr, vr, k0, q0, wv, wv, L, c, g, kl, trl, sl2, ak0, av0);
+        } else {
+          lf_kpass<P, kLfBand>(lds, kr, vr, k0, q0, 0, wv, L, c, g, kl, trl, sl2, ak0, av0);
+        }
+        finish_block(t - 1, kr, vr);
+      }
+      if (own) {  // block t: query sub-tiles wv..7
+        typename P::Q kr, vr;
+        lf_lds_q<P>(kr, slot(t), 16 * wv + c, g);
+        lf_lds_q<P>(vr, slot(t) + LfLds::kMat, 16 * wv + c, g);
+        const int k0 = kLfRows * t + 16 * wv;
+        if (FIXED127) {  // i - key = 16(jq - wv) + (4g + r) - c
+          lf_kpass<P, kLfColUpTo>(lds, kr, vr, k0, q0, wv, wv, L, c, g, kl, trl, sl2, ak0, av0);
+          lf_kpass<P, kLfAll>(lds, kr, vr, k0, q0, wv + 1, kLfWaves - 1, L, c, g, kl, trl, sl2, ak0, av0);
+        } else {
+          lf_kpass<P, kLfBand>(lds, kr, vr, k0, q0, wv, kLfWaves - 1, L, c, g, kl, trl, sl2, ak0, av0);
+        }
+        if (t == nt - 1) finish_block(t, kr, vr);  // no tile t+1: block t is complete too
+      }
+
+      // step t+1's rows replace block t-1 and tile t, which every pass has read
+      __syncthreads();
+      if (more) {
+        lf_store(nk, slot(t + 1), tid);
+        lf_store(nv, slot(t + 1) + LfLds::kMat, tid);
+        __syncthreads();
+      }
+    }
+    // the helpers' chunk-end reduction: the same barriers
+    for (int half = kLfHelpers / 2; half >= 1; half >>= 1) {  // uniform
+      __syncthreads();
+      __syncthreads();
+    }
+  } else {
+    // ---- helper waves: the next tile's loads; the global keys' dK, dV from
+    // query sub-tiles 2wv, 2wv+1 (key as the MFMA column, pairs outside the
+    // band) and the global rows' dQ from key sub-tiles 2wv, 2wv+1 of each
+    // completed block, summed over the chunk
+    f32x4 agq[4], agk[4], agv[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) agq[dt] = agk[dt] = agv[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    auto global_rows_dq = [&](int j) __attribute__((always_inline)) {
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int ks = 2 * wv + e;
+        const uint8_t* krows = slot(j) + 16 * ks * LfLds::kRow;
+        lf_global_rows_dq<P>(lds, krows, krows + LfLds::kMat, kLfRows * j + 16 * ks, G, N, c, g, kl, trl, sl2,
+                             agq);
+      }
+    };
+    for (int t = t0; t <= s1; ++t) {
+      const bool more = t < s1;
+      const bool own = t < t1;
+      LfTile nx;
+      if (more) load_tile(nx, t + 1);  // step t+1's query tile in flight
+      const float* st = reinterpret_cast<const float*>(lds + LfLds::kSt);
+      if (own) {
         typename P::Q kg, vg;
         lf_lds_q<P>(kg, lds + LfLds::kGK, c, g);
         lf_lds_q<P>(vg, lds + LfLds::kGV, c, g);
-        const uint8_t* qrows = lds + LfLds::kQ + 16 * wv * LfLds::kRow;
-        const uint8_t* grows = lds + LfLds::kG + 16 * wv * LfLds::kRow;
-        const f32x4 s = P::qk(qrows + kl, kg);  // S[query 4g + r][global key c]
-        const f32x4 dp = P::qk(grows + kl, vg);
-        const f32x4 l4 = *reinterpret_cast<const f32x4*>(st + 16 * wv + 4 * g);
-        const f32x4 d4 = *reinterpret_cast<const f32x4*>(st + kLfRows + 16 * wv + 4 * g);
-        float lq[4], dq4[4], p[4], ds[4];
-        bool keep[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          keep[r] = c < G && kLfRows * t + 16 * wv + 4 * g + r - c > L;
-          lq[r] = l4[r];
-          dq4[r] = d4[r];
+        for (int e = 0; e < 2; ++e) {
+          const int qs = 2 * wv + e;  // query sub-tile
+          const uint8_t* qrows = lds + LfLds::kQ + 16 * qs * LfLds::kRow;
+          const uint8_t* grows = lds + LfLds::kG + 16 * qs * LfLds::kRow;
+          const f32x4 s = P::qk(qrows + kl, kg);  // S[query 4g + r][global key c]
+          const f32x4 dp = P::qk(grows + kl, vg);
+          const f32x4 l4 = *reinterpret_cast<const f32x4*>(st + 16 * qs + 4 * g);
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(st + kLfRows + 16 * qs + 4 * g);
+          float lq[4], dq4[4], p[4], ds[4];
+          bool keep[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            keep[r] = c < G && kLfRows * t + 16 * qs + 4 * g + r - c > L;
+            lq[r] = l4[r];
+            dq4[r] = d4[r];
+          }
+          lf_probs(s, dp, lq, dq4, keep, sl2, p, ds);
+          pv_tr_split<T>(grows + trl, p, agv);
+          pv_tr_split<T>(qrows + trl, ds, agk);
         }
-        lf_probs(s, dp, lq, dq4, keep, sl2, p, ds);
-        pv_tr_split<T>(grows + trl, p, agv);
-        pv_tr_split<T>(qrows + trl, ds, agk);
+      }
+      if (t > t0) global_rows_dq(t - 1);
+      if (own && t == nt - 1) global_rows_dq(t);
+      __syncthreads();
+      if (more) {
+        lf_stage_tile<T>(nx, lds, ht);
+        __syncthreads();
       }
     }
-
-    // ---- key pass: tile t's queries into keys 16wv.. of blocks t-1 and t
-    const int q0 = kLfRows * t;
-    if (t > t0) {  // block t-1 is this chunk's: query sub-tiles 0..wv reach its keys
-      typename P::Q kr, vr;
-      lf_lds_q<P>(kr, slot(t - 1), 16 * wv + c, g);
-      lf_lds_q<P>(vr, slot(t - 1) + LfLds::kMat, 16 * wv + c, g);
-      const int k0 = kLfRows * (t - 1) + 16 * wv;
-      if (FIXED127) {  // i - key = 128 + 16(jq - wv) + (4g + r) - c
-        lf_kpass<P, kLfAll>(lds, kr, vr, k0, q0, 0, wv - 1, L, c, g, kl, trl, sl2, ak0, av0);
-        lf_kpass<P, kLfColAfter>(lds, kr, vr, k0, q0, wv, wv, L, c, g, kl, trl, sl2, ak0, av0);
-      } else {
-        lf_kpass<P, kLfBand>(lds, kr, vr, k0, q0, 0, wv, L, c, g, kl, trl, sl2, ak0, av0);
-      }
-      finish_block(t - 1, ak0, av0);
-    }
+    // ---- the chunk's global sums: the 4 helpers' sums added pairwise in LDS
+    // (the ring is free: the loop ended on a barrier), then written by helper
+    // 0 as natural-order rows: [3][16][64], row c, head_dim 16dt + 4g + r
+    f32x4* red = reinterpret_cast<f32x4*>(lds);
+    for (int half = kLfHelpers / 2; half >= 1; half >>= 1) {  // uniform
+      if (wv >= half && wv < 2 * half) {
+        f32x4* w = red + (wv - half) * 12 * 64 + lane;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) ak0[dt] = av0[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    if (own) {  // block t: query sub-tiles wv..7
-      typename P::Q kr, vr;
-      lf_lds_q<P>(kr, slot(t), 16 * wv + c, g);
-      lf_lds_q<P>(vr, slot(t) + LfLds::kMat, 16 * wv + c, g);
-      const int k0 = kLfRows * t + 16 * wv;
-      if (FIXED127) {  // i - key = 16(jq - wv) + (4g + r) - c
-        lf_kpass<P, kLfColUpTo>(lds, kr, vr, k0, q0, wv, wv, L, c, g, kl, trl, sl2, ak0, av0);
-        lf_kpass<P, kLfAll>(lds, kr, vr, k0, q0, wv + 1, kLfWaves - 1, L, c, g, kl, trl, sl2, ak0, av0);
-      } else {
-        lf_kpass<P, kLfBand>(lds, kr, vr, k0, q0, wv, kLfWaves - 1, L, c, g, kl, trl, sl2, ak0, av0);
+        for (int dt = 0; dt < 4; ++dt) {
+          w[(0 + dt) * 64] = agq[dt];
+          w[(4 + dt) * 64] = agk[dt];
+          w[(8 + dt) * 64] = agv[dt];
+        }
       }
-      if (t == nt - 1) {  // no tile t+1: block t is complete too
-        finish_block(t, ak0, av0);
+      __syncthreads();
+      if (wv < half) {
+        const f32x4* w = red + wv * 12 * 64 + lane;
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) ak0[dt] = av0[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int dt = 0; dt < 4; ++dt) {
+          agq[dt] += w[(0 + dt) * 64];
+          agk[dt] += w[(4 + dt) * 64];
+          agv[dt] += w[(8 + dt) * 64];
+        }
       }
-    }
-
-    // step t+1's rows replace block t-1 and tile t, which every pass has read
-    __syncthreads();
-    if (more) {
-      lf_store(nk, slot(t + 1), tid);
-      lf_store(nv, slot(t + 1) + LfLds::kMat, tid);
-      lf_stage_tile<T>(nx, lds, tid);
       __syncthreads();
     }
-  }
-
-  // ---- the chunk's global sums: the 8 waves' sums added pairwise in LDS
-  // (the ring is free: the loop ended on a barrier), then written by wave 0
-  // as natural-order rows: [3][16][64], row c, head_dim 16dt + 4g + r
-  f32x4* red = reinterpret_cast<f32x4*>(lds);
-  for (int half = kLfWaves / 2; half >= 1; half >>= 1) {  // uniform
-    if (wv >= half && wv < 2 * half) {
-      f32x4* w = red + (wv - half) * 12 * 64 + lane;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        w[(0 + dt) * 64] = agq[dt];
-        w[(4 + dt) * 64] = agk[dt];
-        w[(8 + dt) * 64] = agv[dt];
-      }
-    }
-    __syncthreads();
-    if (wv < half) {
-      const f32x4* w = red + wv * 12 * 64 + lane;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        agq[dt] += w[(0 + dt) * 64];
-        agk[dt] += w[(4 + dt) * 64];
-        agv[dt] += w[(8 + dt) * 64];
-      }
-    }
-    __syncthreads();
-  }
-  if (wv == 0) {
-    float* dst = a.part + ((int64_t)bh * a.chunks + chunk_id) * 3 * 16 * kHeadDim + c * kHeadDim + 4 * g;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      *reinterpret_cast<f32x4*>(dst + 16 * dt) = agq[dt];
-      *reinterpret_cast<f32x4*>(dst + 16 * kHeadDim + 16 * dt) = agk[dt];
-      *reinterpret_cast<f32x4*>(dst + 2 * 16 * kHeadDim + 16 * dt) = agv[dt];
+    if (wv == 0) {
+      store_part(chunk_id, 0, agq);
+      store_part(chunk_id, 1, agk);
+      store_part(chunk_id, 2, agv);
     }
   }
 }
 
 // Rows 0..G-1 of dQ, dK, dV: the sums of a (batch, head)'s chunk partials
-// (in chunk order), dQ and dK times the scale.  One thread per element of
-// the [3][16][64] part: kLfCombineBlocks workgroups of 256 per (batch, head),
-// so the chunk loads of many elements are in flight together.
-constexpr int kLfCombineBlocks = 3 * 16 * kHeadDim / 256;
+// (in chunk order; for dK and dV also the extra slot of block 0's sums), dQ
+// and dK times the scale.  One thread per element of the [3][16][64] part:
+// kLfCombineBlocks workgroups of 256 per (batch, head), so the chunk loads of
+// many elements are in flight together.
+constexpr int kLfCombineBlocks = kLfPart / 256;
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_lf_combine(LfArgs a) {
   const int bh = blockIdx.x / kLfCombineBlocks;
@@ -628,10 +684,11 @@ __global__ __launch_bounds__(256) void bwd_lf_combine(LfArgs a) {
   if (r >= min(a.G, a.N)) return;
   const int h = bh % a.H;
   const int b = bh / a.H;
-  const float* p = a.part + (int64_t)bh * a.chunks * kLfPart + e;
+  const float* p = a.part + (int64_t)bh * (a.chunks + 1) * kLfPart + e;
+  const int slots = m == 0 ? a.chunks : a.chunks + 1;
   float s = 0.0f;
 #pragma unroll 8
-  for (int ch = 0; ch < a.chunks; ++ch) s += p[(int64_t)ch * kLfPart];
+  for (int ch = 0; ch < slots; ++ch) s += p[(int64_t)ch * kLfPart];
   T* out = static_cast<T*>(m == 0 ? a.dq : m == 1 ? a.dk : a.dv);
   out[((int64_t)b * a.N * a.H + h) * kHeadDim + (int64_t)r * a.H * kHeadDim + d] =
       static_cast<T>(m == 2 ? s : s * a.scale);

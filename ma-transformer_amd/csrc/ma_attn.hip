@@ -1797,9 +1797,9 @@ int forward_launch(const ma_attn_desc* desc, const void* q, const void* k, const
 //
 // bwd_longformer_kernel.h: one pass over Q, K, V, dO and O for Longformer
 // sets with a causal window of at most 128 keys ([i-L, i], L <= 127) and 1 to
-// 16 global tokens, 16-bit, head_dim 64.  Workspace: per (batch, head) and
-// chunk, the global rows' dQ and the global keys' dK, dV sums (3 x 16 x 64
-// floats).
+// 16 global tokens, 16-bit, head_dim 64.  Workspace: per (batch, head), for
+// each chunk and one more slot (block 0's sums of keys 0..G-1), the global
+// rows' dQ and the global keys' dK, dV sums (3 x 16 x 64 floats).
 struct LfPlan {
   int64_t chunk, chunks, part_bytes;
 };
@@ -1812,7 +1812,7 @@ LfPlan lf_plan(const ma_attn_desc* d) {
   const int64_t per_stream = ma::imax64(1, 256 / streams);
   p.chunk = ma::imax64(1, (nt + per_stream - 1) / per_stream);
   p.chunks = ma::imax64(1, (nt + p.chunk - 1) / p.chunk);
-  p.part_bytes = streams * p.chunks * 3 * 16 * kHeadDim * (int64_t)sizeof(float);
+  p.part_bytes = streams * (p.chunks + 1) * kLfPart * (int64_t)sizeof(float);
   return p;
 }
 
@@ -1855,7 +1855,7 @@ int launch_lf_bwd(const ma_attn_desc* d, const void* const* ptrs, const void* o,
   auto kf = d->left == kLfRows - 1 ? &bwd_lf_kernel<HalfPath<T>, true> : &bwd_lf_kernel<HalfPath<T>, false>;
   if (reserve_lds(reinterpret_cast<const void*>(kf), (size_t)LfLds::kBytes, st)) return 1;
   const int64_t streams = d->batch * d->num_heads;
-  launch(false, kf, dim3((unsigned)(streams * p.chunks)), dim3(kLfWaves * 64), (uint32_t)LfLds::kBytes, st, a);
+  launch(false, kf, dim3((unsigned)(streams * p.chunks)), dim3(kLfThreads), (uint32_t)LfLds::kBytes, st, a);
   launch(true, bwd_lf_combine<T>, dim3((unsigned)(streams * kLfCombineBlocks)), dim3(256), 0u, st, a);
   return 0;
 }
