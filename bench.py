@@ -43,7 +43,10 @@ With --pass backward --saved-stats (dense, block-sparse, Longformer and
 index-set workloads), the backward runs from the forward's saved O and per-row
 statistics (ma_attn_backward_saved), the form the autograd layer trains with;
 the forward runs once per input set before timing, and the algorithmic bytes
-count O and the statistics read as well.
+count O and the statistics read as well.  Without --saved-stats the Longformer
+backward (longformer_backward) runs the forward keeping the statistics and
+then the one-pass backward, both timed; its algorithmic bytes stay the 7
+tensors of a backward.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
                        [--pass forward|backward] [--saved-stats]
@@ -512,8 +515,9 @@ def measure(workload: str, which: str = "forward", saved: bool = False, steps: i
         else:
             launch = lambda s: ext.dense_backward(s[0], s[1], s[2], s[3], pk["causal"])
     elif bwd:
-        # block-sparse, Longformer and explicit sets train on index_set_backward
-        # over the pattern's key sets as one IndexSet (built once, as the layer does)
+        # block-sparse and explicit sets train on index_set_backward over the
+        # pattern's key sets as one IndexSet (built once, as the layer does);
+        # Longformer on longformer_backward
         if pk["pattern"] == "index_set":
             offsets, keys = window_csr(N, pk["left"], pk["right"])
             iset = ext.IndexSet(torch.from_numpy(offsets), torch.from_numpy(keys), N, dev)
@@ -545,6 +549,13 @@ def measure(workload: str, which: str = "forward", saved: bool = False, steps: i
                                                     return_lse=True)
                 sets[n_] = s_ + (o_, l_)
             launch = lambda s: ext.index_set_backward(s[0], s[1], s[2], s[3], iset, out=s[4], lse=s[5])
+        elif pk["pattern"] == "longformer":
+            # longformer_backward without saved statistics: the forward keeping
+            # them, then the one-pass backward (the tiled kernels where the
+            # one-pass kernel does not apply); both calls' kernels in one span
+            iset = None
+            launch = lambda s: ext.longformer_backward(s[0], s[1], s[2], s[3], pk["left"], pk["right"],
+                                                       pk["num_global"])
         else:
             launch = lambda s: ext.index_set_backward(s[0], s[1], s[2], s[3], iset)
     elif pk["pattern"] == "sliding":

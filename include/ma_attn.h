@@ -211,12 +211,18 @@ int ma_attn_backward_timed(const ma_attn_desc* desc, const void* q, const void* 
  * LONGFORMER itself in 16 bits at head_dim 64 with right = 0, 0 <= left < 128
  * and 1 to 16 global tokens (one pass over the sequence; per-chunk sums of the
  * global rows' and keys' gradients in the workspace).
- * Workspace: ma_attn_backward_workspace_size(desc).  The _timed form stamps
- * its kernels as ma_attn_backward_timed does.
+ * Workspace: ma_attn_backward_workspace_size(desc).  The _timed forms stamp
+ * their kernels as ma_attn_forward_timed / ma_attn_backward_timed do (either
+ * event may be NULL, so a forward_lse + backward_saved pair can be stamped
+ * as one span).
  */
 int ma_attn_forward_lse(const ma_attn_desc* desc, const void* q, const void* k,
                         const void* v, void* o, float* lse, void* workspace,
                         size_t workspace_bytes, void* stream);
+int ma_attn_forward_lse_timed(const ma_attn_desc* desc, const void* q, const void* k,
+                              const void* v, void* o, float* lse, void* workspace,
+                              size_t workspace_bytes, void* stream, void* start_event,
+                              void* stop_event);
 int ma_attn_backward_saved(const ma_attn_desc* desc, const void* q, const void* k,
                            const void* v, const void* o, const float* lse,
                            const void* dout, void* dq, void* dk, void* dv,

@@ -2248,6 +2248,16 @@ int ma_attn_forward_timed(const ma_attn_desc* desc, const void* q, const void* k
   return rc;
 }
 
+int ma_attn_forward_lse_timed(const ma_attn_desc* desc, const void* q, const void* k, const void* v, void* o,
+                              float* lse, void* workspace, size_t workspace_bytes, void* stream, void* start_event,
+                              void* stop_event) {
+  g_ev_start = static_cast<hipEvent_t>(start_event);
+  g_ev_stop = static_cast<hipEvent_t>(stop_event);
+  const int rc = ma_attn_forward_lse(desc, q, k, v, o, lse, workspace, workspace_bytes, stream);
+  g_ev_start = g_ev_stop = nullptr;
+  return rc;
+}
+
 int ma_attn_backward_saved(const ma_attn_desc* desc, const void* q, const void* k, const void* v, const void* o,
                            const float* lse, const void* dout, void* dq, void* dk, void* dv, void* workspace,
                            size_t workspace_bytes, void* stream) {

@@ -114,6 +114,9 @@ def _open():
     lib.ma_attn_forward_lse.restype = ctypes.c_int
     lib.ma_attn_forward_lse.argtypes = [ctypes.POINTER(Desc)] + [ctypes.c_void_p] * 6 + \
         [ctypes.c_size_t, ctypes.c_void_p]
+    lib.ma_attn_forward_lse_timed.restype = ctypes.c_int
+    lib.ma_attn_forward_lse_timed.argtypes = [ctypes.POINTER(Desc)] + [ctypes.c_void_p] * 6 + \
+        [ctypes.c_size_t] + [ctypes.c_void_p] * 3
     lib.ma_attn_backward_saved.restype = ctypes.c_int
     lib.ma_attn_backward_saved.argtypes = [ctypes.POINTER(Desc)] + [ctypes.c_void_p] * 10 + \
         [ctypes.c_size_t, ctypes.c_void_p]
@@ -222,11 +225,17 @@ def backward_raw(desc: Desc, q_ptr: int, k_ptr: int, v_ptr: int, g_ptr: int, dq_
 
 
 def forward_lse_raw(desc: Desc, q_ptr: int, k_ptr: int, v_ptr: int, o_ptr: int, lse_ptr: int,
-                    ws_ptr: int = 0, ws_bytes: int = 0, stream: int = 0) -> None:
+                    ws_ptr: int = 0, ws_bytes: int = 0, stream: int = 0, events=None) -> None:
     """ma_attn_forward_lse: the forward plus each row's softmax statistic
-    (float32 [B*N*H]) for backward_saved_raw.  Raises RuntimeError on rejection."""
-    rc = LIB.ma_attn_forward_lse(ctypes.byref(desc), q_ptr, k_ptr, v_ptr, o_ptr, lse_ptr, ws_ptr or None,
-                                 ws_bytes, stream or None)
+    (float32 [B*N*H]) for backward_saved_raw; events as for forward_raw.
+    Raises RuntimeError on rejection."""
+    if events:
+        rc = LIB.ma_attn_forward_lse_timed(ctypes.byref(desc), q_ptr, k_ptr, v_ptr, o_ptr, lse_ptr,
+                                           ws_ptr or None, ws_bytes, stream or None, events[0] or None,
+                                           events[1] or None)
+    else:
+        rc = LIB.ma_attn_forward_lse(ctypes.byref(desc), q_ptr, k_ptr, v_ptr, o_ptr, lse_ptr, ws_ptr or None,
+                                     ws_bytes, stream or None)
     if rc != 0:
         raise RuntimeError(last_error())
 

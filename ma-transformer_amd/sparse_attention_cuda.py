@@ -141,7 +141,7 @@ def _launch(q, k, v, pattern, return_lse: bool = False, **kw):
         lse = torch.empty((B, N, H), dtype=torch.float32, device=q.device)
         _on_device(q.get_device(), lambda stream: _ma.forward_lse_raw(
             desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
-            ws.data_ptr() if ws is not None else 0, nbytes, stream))
+            ws.data_ptr() if ws is not None else 0, nbytes, stream, _events))
         return out, lse
     _on_device(q.get_device(), lambda stream: _ma.forward_raw(
         desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), ws.data_ptr() if ws is not None else 0,
@@ -514,19 +514,33 @@ def longformer_backward(query, key, value, grad_out, left: int, right: int = 0, 
                         out=None, lse=None) -> List[torch.Tensor]:
     """dQ, dK, dV of longformer_forward.
 
-    With the forward's output and statistics (longformer_forward(...,
-    return_lse=True)) and a window [i-left, i] (left <= 127, 1 to 16 global
-    tokens, 16-bit, head_dim 64), one pass over Q, K, V, dO and O
-    (ma_attn_backward_saved, bwd_lf_kernel).  Otherwise the tiled kernels over
-    the pattern's key sets (index_set_backward on pattern_index_set)."""
+    For a window [i-left, i] (left <= 127, 1 to 16 global tokens, 16-bit,
+    head_dim 64, 16-byte aligned tensors): one pass over Q, K, V, dO and O
+    (ma_attn_backward_saved, bwd_lf_kernel) from the forward's output and
+    statistics, taken from out and lse (longformer_forward(...,
+    return_lse=True)) or, without them, from one longformer_forward run here
+    first (the two calls' kernels stamped as one span under kernel_events).
+    Otherwise the tiled kernels over the pattern's key sets (index_set_backward
+    on pattern_index_set)."""
+    global _events
     _check(query, key, value, grad_out)
     N = query.shape[1]
     kw = dict(left=int(left), right=int(right), num_global=int(num_global))
-    if out is not None and lse is not None and longformer_fused_applies(query, left, right, num_global) and all(
-            t.data_ptr() % 16 == 0 for t in (query, key, value, grad_out, out)):
-        _check(query, out)
-        _check_lse(lse, query)
-        return _backward_saved(query, key, value, out, lse, grad_out, _ma.LONGFORMER, **kw)
+    if longformer_fused_applies(query, left, right, num_global) and all(
+            t.data_ptr() % 16 == 0 for t in (query, key, value, grad_out)):
+        if out is None or lse is None:
+            ev = _events
+            try:
+                _events = (ev[0], None) if ev else None  # the forward's kernels start the span
+                out, lse = longformer_forward(query, key, value, left, right, num_global, return_lse=True)
+                _events = (None, ev[1]) if ev else None  # the backward's end it
+                return _backward_saved(query, key, value, out, lse, grad_out, _ma.LONGFORMER, **kw)
+            finally:
+                _events = ev
+        if out.data_ptr() % 16 == 0:
+            _check(query, out)
+            _check_lse(lse, query)
+            return _backward_saved(query, key, value, out, lse, grad_out, _ma.LONGFORMER, **kw)
     iset = pattern_index_set("longformer", N, query.device, **kw)
     return index_set_backward(query, key, value, grad_out, iset, out=out, lse=lse)
 

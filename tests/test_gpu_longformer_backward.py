@@ -188,3 +188,25 @@ def test_layer_longformer_training_uses_the_one_pass_kernel(ext, oracle, monkeyp
     ref = oracle.backward(oracle.Spec(*shape, pattern="longformer", left=127, right=0, num_global=16), *up)
     for name, t, r in zip(("dq", "dk", "dv"), dev, ref):
         check_grad(name, t.grad.float().cpu().numpy(), r, False)
+
+
+@pytest.mark.parametrize("shape,L,G", [((1, 700, 2, 64), 127, 16), ((2, 300, 1, 64), 40, 5)])
+def test_longformer_backward_without_statistics(ext, oracle, shape, L, G):
+    """longformer_backward without out / lse: the forward keeping the
+    statistics, then the one-pass kernel; the same bits as calling the two
+    in sequence, and the oracle's gradients; under kernel_events the two
+    calls' kernels are stamped as one span."""
+    dev, out, lse, up = _case(ext, shape, 6700 + shape[1] + L, torch.bfloat16, L, G)
+    got = ext.longformer_backward(*dev, L, 0, G)
+    saved = ext.longformer_backward(*dev, L, 0, G, out=out, lse=lse)
+    for a, b in zip(got, saved):
+        assert torch.equal(a, b)
+    _check_heads(oracle, got, up, shape, L, G, range(shape[2]))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    e1.record()
+    torch.cuda.synchronize()
+    with ext.kernel_events(e0, e1):
+        ext.longformer_backward(*dev, L, 0, G)
+    torch.cuda.synchronize()
+    assert e0.elapsed_time(e1) > 0.0
