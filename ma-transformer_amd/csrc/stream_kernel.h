@@ -898,11 +898,12 @@ __global__ __launch_bounds__(256, LG ? 2 : P::kMinBlocks) void stream_kernel(Str
 // Global query rows of Longformer: merge the per-wave partials of every chunk
 // (log-sum-exp combine) into O rows 0..G-1.  One workgroup of 4 waves per
 // (batch, head, global row), over one partial per chunk; thread (wave w,
-// lane d) owns head_dim element d of the partials p = w, w+4, ...  Each wave takes its partials' maximum
-// first, so the weighted sums that follow have no dependence between
-// iterations (their loads overlap), then the 4 wave results merge in LDS.
-// (A single wave folding the partials one by one in an online merge waited
-// out one load round trip per partial: 42 us at cfg 4.)
+// lane d) owns head_dim element d of the partials p = w, w+4, ...  A wave
+// loads 8 of its partials (maximum, denominator, element d) at once, then
+// merges them, so a row of up to 32 partials costs one load round trip; the 4
+// wave results merge in LDS.  (A single wave folding the partials one by one
+// waited out one round trip per partial: 42 us at cfg 4; a maximum pass
+// before the weighted sums, two round trips: 5.2 us.)
 template <typename Elt>
 __global__ __launch_bounds__(256) void longformer_combine(const float* __restrict__ partials, Elt* __restrict__ o,
                                                           int nparts, int G, int H, int64_t N, float* lse) {
@@ -916,17 +917,34 @@ __global__ __launch_bounds__(256) void longformer_combine(const float* __restric
   // partial p of this global row: base + p * 16 * kPartial
   const float* base = partials + ((int64_t)bh * nparts * 16 + gq) * kPartial;
   constexpr int64_t kStride = 16 * kPartial;
-  float m = -INFINITY;
-#pragma unroll 8
-  for (int p = wv; p < nparts; p += 4) m = fmaxf(m, base[p * kStride + kHeadDim]);
-  float l = 0.0f, acc = 0.0f;
-  if (m != -INFINITY) {
-#pragma unroll 8
-    for (int p = wv; p < nparts; p += 4) {
-      const float* src = base + p * kStride;
-      const float w = __builtin_amdgcn_exp2f(src[kHeadDim] - m);  // 0 for a partial that saw no key
-      l = fmaf(src[kHeadDim + 1], w, l);
-      acc = fmaf(src[d], w, acc);
+  // Batches of 8 partials per wave, all 24 loads of a batch issued together:
+  // one load round trip per 32 partials of the row.
+  float m = -INFINITY, l = 0.0f, acc = 0.0f;
+  for (int p0 = wv; p0 < nparts; p0 += 32) {
+    float mk[8], lk[8], ak[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int p = p0 + 4 * k;
+      const float* src = base + (int64_t)min(p, nparts - 1) * kStride;
+      mk[k] = src[kHeadDim];
+      lk[k] = src[kHeadDim + 1];
+      ak[k] = src[d];
+      if (p >= nparts) mk[k] = -INFINITY;
+    }
+    float mb = m;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) mb = fmaxf(mb, mk[k]);
+    if (mb != -INFINITY) {
+      const float c = __builtin_amdgcn_exp2f(m - mb);  // 0 while m is -inf
+      l *= c;
+      acc *= c;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float w = __builtin_amdgcn_exp2f(mk[k] - mb);  // 0 for a partial that saw no key
+        l = fmaf(lk[k], w, l);
+        acc = fmaf(ak[k], w, acc);
+      }
+      m = mb;
     }
   }
   sh[wv][d] = acc;
