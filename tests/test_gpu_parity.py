@@ -180,6 +180,23 @@ def test_longformer_geometry(ext, oracle, N, G, left, right, dtype):
     assert _max_err(y, oracle.forward(spec, *up)) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("shape,G,left,dtype", [
+    ((1, 8192, 1, 64), 16, 127, torch.bfloat16),  # one stream: 128 chunks of one tile
+    ((1, 3000, 2, 64), 5, 40, torch.float16),     # 47 chunks: a second batch of 15
+])
+def test_longformer_many_chunks(ext, oracle, shape, G, left, dtype):
+    """Few (batch, head) streams over a long sequence: the grid splits each
+    stream into more than 32 chunks, so longformer_combine merges each global
+    row's partials in several batches of 32 (the last one ragged).  Whole
+    output against the oracle, global rows included."""
+    (q, k, v), up = _inputs(shape, 950 + shape[1] + G, dtype)
+    y = ext.longformer_forward(q, k, v, left, 0, G)
+    spec = oracle.Spec(*shape, pattern="longformer", left=left, right=0, num_global=G)
+    ref = oracle.forward(spec, *up)
+    assert _max_err(y, ref, rows=(0, G)) <= TOL[dtype]
+    assert _max_err(y, ref) <= TOL[dtype]
+
+
 @pytest.mark.parametrize("N", [1, 63, 64, 65, 200, 1000])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
