@@ -1808,7 +1808,7 @@ LfPlan lf_plan(const ma_attn_desc* d) {
   LfPlan p;
   const int64_t nt = (d->seq_len + kLfRows - 1) / kLfRows;
   const int64_t streams = ma::imax64(d->batch * d->num_heads, 1);
-  // one workgroup per CU (121 KB of LDS): chunks fitted to one round of 256
+  // one workgroup per CU (131 KB of LDS): chunks fitted to one round of 256
   const int64_t per_stream = ma::imax64(1, 256 / streams);
   p.chunk = ma::imax64(1, (nt + per_stream - 1) / per_stream);
   p.chunks = ma::imax64(1, (nt + p.chunk - 1) / p.chunk);

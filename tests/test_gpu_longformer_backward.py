@@ -59,6 +59,7 @@ def _check_heads(oracle, got, up, shape, L, G, heads):
     ((1, 700, 2, 64), 0, 16),      # window of the key itself
     ((1, 10, 2, 64), 127, 16),     # fewer rows than global tokens
     ((2, 2000, 2, 64), 127, 16),
+    ((1, 8192, 1, 64), 127, 16),   # one stream: 64 chunks, each global sum merged over all of them
 ])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_longformer_backward_vs_oracle(ext, oracle, shape, L, G, dtype):
