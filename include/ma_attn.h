@@ -209,8 +209,8 @@ int ma_attn_backward_timed(const ma_attn_desc* desc, const void* q, const void* 
  * plan, which may hold the key sets of a BLOCK_SPARSE or LONGFORMER forward
  * (ma_attn_pattern_csr enumerates them), for DENSE (head_dim 64), and for
  * LONGFORMER itself in 16 bits at head_dim 64 with right = 0, 0 <= left < 128
- * and 1 to 16 global tokens (one pass over the sequence; per-chunk sums of the
- * global rows' and keys' gradients in the workspace).
+ * and 1 to 16 global tokens (one pass over the sequence; per-segment sums of
+ * the global rows' and keys' gradients in the workspace).
  * Workspace: ma_attn_backward_workspace_size(desc).  The _timed forms stamp
  * their kernels as ma_attn_forward_timed / ma_attn_backward_timed do (either
  * event may be NULL, so a forward_lse + backward_saved pair can be stamped

@@ -21,8 +21,9 @@
 //
 // Rows and keys come in 128-row tiles / blocks, so query tile t meets key
 // blocks t-1 and t, and key block j is seen by query tiles j and j+1.  One
-// workgroup (12 waves, one per CU, 3 per SIMD) streams a chunk [t0, t1) of
-// query tiles of one (batch, head) and owns key blocks [t0, t1); LDS holds
+// workgroup (12 waves, one per CU, 3 per SIMD) streams a segment [t0, t1) of
+// query tiles of one (batch, head) and owns key blocks [t0, t1) (a run of
+// tiles that crosses into the next (batch, head) is two segments); LDS holds
 // the K, V rows of blocks t-1 and t (a two-slot ring), tile t's Q and dO rows
 // and statistics, and the 16 global keys' K, V rows and global rows' Q, dO
 // rows.  Step t:
@@ -39,11 +40,11 @@
 //                global keys with the key as the MFMA column (the global
 //                keys' dK^T, dV^T) and the global rows against key sub-tiles
 //                2w, 2w+1 of each completed block (the global rows' dQ^T),
-//                summed over the chunk.
+//                summed over the segment.
 // The main waves load the next key block and the helpers the next query
-// tile.  A chunk also runs the key pass of tile t1 (no dQ) for its block
+// tile.  A segment also runs the key pass of tile t1 (no dQ) for its block
 // t1-1, and reads block t0-1 for tile t0's queries.  The global rows' dQ and
-// the global keys' dK, dV are per-chunk sums in the workspace (with one more
+// the global keys' dK, dV are per-segment sums in the workspace (with one more
 // slot for block 0's sums of keys 0..G-1); bwd_lf_combine adds them up and
 // writes rows 0..G-1 of dQ, dK, dV.  Every other row of dQ, dK, dV has one
 // writer; no atomics.  Rows past the end read as zero and their stores are
@@ -65,9 +66,11 @@ struct LfArgs {
   void* dq;
   void* dk;
   void* dv;
-  float* part;  // [B*H][chunks + 1][3][16][64]: global rows' dQ, global keys' dK, dV (unscaled sums)
+  float* part;  // [B*H][nslot + 1][3][16][64]: global rows' dQ, global keys' dK, dV (unscaled sums)
   int32_t N, H, L, G;
-  int32_t chunk, chunks;
+  int32_t streams;  // B*H
+  int32_t per_wg;   // query tiles per workgroup: its run of the streams' tiles, in order
+  int32_t nslot;    // partial slots per (batch, head) before the extra one: workgroups meeting it, at most
   int32_t tok_bytes;
   float scale, scale_log2;
 };
@@ -76,7 +79,7 @@ constexpr int kLfRows = 128;  // rows per query tile and key block
 constexpr int kLfWaves = 8;    // main waves: the query and key passes
 constexpr int kLfHelpers = 4;  // helper waves: tile loads and the global sums
 constexpr int kLfThreads = 64 * (kLfWaves + kLfHelpers);  // 768
-constexpr int kLfPart = 3 * 16 * kHeadDim;  // one chunk's partials: dQ, dK, dV of 16 rows
+constexpr int kLfPart = 3 * 16 * kHeadDim;  // one segment's partials: dQ, dK, dV of 16 rows
 
 struct LfLds {
   // 160 B rows (128 + 32 pad): the four rows of a transpose read's 16-lane
@@ -105,7 +108,7 @@ __device__ __forceinline__ void lf_lds_q(typename P::Q& x, const uint8_t* mat, i
   x.r[0] = *reinterpret_cast<const uint4*>(mat + r * LfLds::kRow + 16 * g);
   x.r[1] = *reinterpret_cast<const uint4*>(mat + r * LfLds::kRow + 16 * g + 64);
 }
-// the chunk-end reduction of the helpers' sums reuses the ring: 2 waves x 12 KB
+// the segment-end reduction of the helpers' sums reuses the ring: 2 waves x 12 KB
 static_assert(4 * 64 * 48 * 4 <= LfLds::kQ, "reduction area");
 
 // 16-bit dot product of two 8-element pieces, in fp32.
@@ -350,11 +353,12 @@ __device__ __forceinline__ void lf_global_rows_dq(const uint8_t* lds, const uint
   pv_tr_split<T>(krows + trl, ds, agq);
 }
 
-// FIXED127: L = 127, the band's sub-tiles selected by the fixed masks.
+// One segment: query tiles [t0, t1) of (batch, head) bh and key blocks
+// [t0, t1), its global sums into partial slot slot_id.  FIXED127: L = 127,
+// the band's sub-tiles selected by the fixed masks.
 template <class P, bool FIXED127>
-__global__ __launch_bounds__(kLfThreads, 1) void bwd_lf_kernel(LfArgs a) {
+__device__ __forceinline__ void lf_segment(const LfArgs& a, uint8_t* lds, int bh, int t0, int t1, int slot_id) {
   using T = typename P::Elt;
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // LfLds
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wq = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -364,14 +368,10 @@ __global__ __launch_bounds__(kLfThreads, 1) void bwd_lf_kernel(LfArgs a) {
   const int c = lane & 15;
   const int g = lane >> 4;
 
-  const int chunk_id = blockIdx.x % a.chunks;
-  const int bh = blockIdx.x / a.chunks;
   const int h = bh % a.H;
   const int b = bh / a.H;
   const int N = a.N, L = FIXED127 ? kLfRows - 1 : a.L, G = a.G;
   const int nt = (N + kLfRows - 1) / kLfRows;
-  const int t0 = chunk_id * a.chunk;
-  const int t1 = min(t0 + a.chunk, nt);
   if (t0 >= t1) return;  // uniform, before any barrier
   const int s1 = t1 < nt ? t1 : t1 - 1;  // the last step: tile t1's key pass for block t1-1
   const uint32_t tb = (uint32_t)a.tok_bytes;
@@ -386,7 +386,7 @@ __global__ __launch_bounds__(kLfThreads, 1) void bwd_lf_kernel(LfArgs a) {
   const __amdgpu_buffer_rsrc_t DKr = make_rsrc(static_cast<T*>(a.dk) + base, nrec);
   const __amdgpu_buffer_rsrc_t DVr = make_rsrc(static_cast<T*>(a.dv) + base, nrec);
   const float* lse = a.lse + (int64_t)b * N * a.H + h;  // row i at i * H
-  float* part = a.part + (int64_t)bh * (a.chunks + 1) * kLfPart;
+  float* part = a.part + (int64_t)bh * (a.nslot + 1) * kLfPart;
   // byte offset of row r (r >= -128); rows below 0 wrap past the range
   auto roff = [&](int r) { return (uint32_t)r * tb; };
   auto slot = [&](int j) { return lds + (j & 1) * LfLds::kSlot; };
@@ -457,8 +457,8 @@ __global__ __launch_bounds__(kLfThreads, 1) void bwd_lf_kernel(LfArgs a) {
       const int k0 = kLfRows * j + 16 * wv;
       lf_global_rows_kv<P>(lds, kr, vr, k0, G, N, c, g, kl, trl, sl2, ak0, av0);
       if (j == 0 && wv == 0 && c < G) {
-        store_part(a.chunks, 1, ak0);
-        store_part(a.chunks, 2, av0);
+        store_part(a.nslot, 1, ak0);
+        store_part(a.nslot, 2, av0);
       }
       const uint32_t row = roff(k0 + c);
       store_nat<T>(av0, 1.0f, DVr, row, g);
@@ -469,7 +469,7 @@ __global__ __launch_bounds__(kLfThreads, 1) void bwd_lf_kernel(LfArgs a) {
 
     for (int t = t0; t <= s1; ++t) {
       const bool more = t < s1;
-      const bool own = t < t1;  // tile t's queries are this chunk's
+      const bool own = t < t1;  // tile t's queries are this segment's
       Rows128 nk, nv;
       if (more) {  // step t+1's key block in flight
         lf_load(nk, Kr, roff(kLfRows * (t + 1)), tid, tb);
@@ -539,7 +539,7 @@ __global__ __launch_bounds__(kLfThreads, 1) void bwd_lf_kernel(LfArgs a) {
 
       // ---- key pass: tile t's queries into keys 16wv.. of blocks t-1 and t
       const int q0 = kLfRows * t;
-      if (t > t0) {  // block t-1 is this chunk's: query sub-tiles 0..wv reach its keys
+      if (t > t0) {  // block t-1 is this segment's: query sub-tiles 0..wv reach its keys
         typename P::Q kr, vr;
         lf_lds_q<P>(kr, slot(t - 1), 16 * wv + c, g);
         lf_lds_q<P>(vr, slot(t - 1) + LfLds::kMat, 16 * wv + c, g);
@@ -574,7 +574,7 @@ __global__ __launch_bounds__(kLfThreads, 1) void bwd_lf_kernel(LfArgs a) {
         __syncthreads();
       }
     }
-    // the helpers' chunk-end reduction: the same barriers
+    // the helpers' segment-end reduction: the same barriers
     for (int half = kLfHelpers / 2; half >= 1; half >>= 1) {  // uniform
       __syncthreads();
       __syncthreads();
@@ -583,7 +583,7 @@ __global__ __launch_bounds__(kLfThreads, 1) void bwd_lf_kernel(LfArgs a) {
     // ---- helper waves: the next tile's loads; the global keys' dK, dV from
     // query sub-tiles 2wv, 2wv+1 (key as the MFMA column, pairs outside the
     // band) and the global rows' dQ from key sub-tiles 2wv, 2wv+1 of each
-    // completed block, summed over the chunk
+    // completed block, summed over the segment
     f32x4 agq[4], agk[4], agv[4];
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) agq[dt] = agk[dt] = agv[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -636,7 +636,7 @@ __global__ __launch_bounds__(kLfThreads, 1) void bwd_lf_kernel(LfArgs a) {
         __syncthreads();
       }
     }
-    // ---- the chunk's global sums: the 4 helpers' sums added pairwise in LDS
+    // ---- the segment's global sums: the 4 helpers' sums added pairwise in LDS
     // (the ring is free: the loop ended on a barrier), then written by helper
     // 0 as natural-order rows: [3][16][64], row c, head_dim 16dt + 4g + r
     f32x4* red = reinterpret_cast<f32x4*>(lds);
@@ -663,17 +663,44 @@ __global__ __launch_bounds__(kLfThreads, 1) void bwd_lf_kernel(LfArgs a) {
       __syncthreads();
     }
     if (wv == 0) {
-      store_part(chunk_id, 0, agq);
-      store_part(chunk_id, 1, agk);
-      store_part(chunk_id, 2, agv);
+      store_part(slot_id, 0, agq);
+      store_part(slot_id, 1, agk);
+      store_part(slot_id, 2, agv);
     }
   }
 }
 
-// Rows 0..G-1 of dQ, dK, dV: the sums of a (batch, head)'s chunk partials
-// (in chunk order; for dK and dV also the extra slot of block 0's sums), dQ
+// The streams' query tiles in order, (batch, head) after (batch, head), are
+// dealt to the workgroups in equal runs of per_wg tiles (per_wg at most one
+// stream's tiles), so that one round of one workgroup per CU has no idle CU
+// and no run longer than the average (cfg4: 24 tiles each on 256 CUs,
+// against 26 on 240 with whole chunks per stream).  A run that crosses the
+// end of a stream continues at the next stream's start: a second segment,
+// with its own prologue and partial slot (the workgroup's index among those
+// whose runs meet that stream).
+template <class P, bool FIXED127>
+__global__ __launch_bounds__(kLfThreads, 1) void bwd_lf_kernel(LfArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // LfLds
+  const int nt = (a.N + kLfRows - 1) / kLfRows;
+  const int64_t g0 = (int64_t)blockIdx.x * a.per_wg;
+  const int64_t g1 = min(g0 + a.per_wg, (int64_t)a.streams * nt);
+  const int bh = (int)(g0 / nt);
+  const int64_t s0 = (int64_t)bh * nt;
+  const int t0 = (int)(g0 - s0);
+  const int t1 = (int)min(g1 - s0, (int64_t)nt);
+  const int t1b = (int)(g1 - s0 - nt);  // > 0: tiles [0, t1b) of stream bh + 1
+  const int slot2 = (int)(blockIdx.x - (s0 + nt) / a.per_wg);
+  lf_segment<P, FIXED127>(a, lds, bh, t0, t1, (int)(blockIdx.x - s0 / a.per_wg));
+  if (t1b > 0) {  // uniform
+    __syncthreads();  // the first segment's LDS reads are done
+    lf_segment<P, FIXED127>(a, lds, bh + 1, 0, t1b, slot2);
+  }
+}
+
+// Rows 0..G-1 of dQ, dK, dV: the sums of a (batch, head)'s segment partials
+// (in tile order; for dK and dV also the extra slot of block 0's sums), dQ
 // and dK times the scale.  One thread per element of the [3][16][64] part:
-// kLfCombineBlocks workgroups of 256 per (batch, head), so the chunk loads of
+// kLfCombineBlocks workgroups of 256 per (batch, head), so the partial loads of
 // many elements are in flight together.
 constexpr int kLfCombineBlocks = kLfPart / 256;
 template <typename T>
@@ -684,11 +711,13 @@ __global__ __launch_bounds__(256) void bwd_lf_combine(LfArgs a) {
   if (r >= min(a.G, a.N)) return;
   const int h = bh % a.H;
   const int b = bh / a.H;
-  const float* p = a.part + (int64_t)bh * (a.chunks + 1) * kLfPart + e;
-  const int slots = m == 0 ? a.chunks : a.chunks + 1;
-  // 16 chunk loads in flight at once (indices clamped, so unconditional),
-  // then the adds in chunk order: one load round trip per 16 chunks (a
-  // rolled remainder loop waited out one per chunk: 5.1 us at cfg4)
+  const float* p = a.part + (int64_t)bh * (a.nslot + 1) * kLfPart + e;
+  const int nt = (a.N + kLfRows - 1) / kLfRows;
+  // the workgroups whose runs meet this stream, in tile order
+  const int slots = (int)(((int64_t)(bh + 1) * nt - 1) / a.per_wg - (int64_t)bh * nt / a.per_wg + 1);
+  // 16 partial loads in flight at once (indices clamped, so unconditional),
+  // then the adds in tile order: one load round trip per 16 partials (a
+  // rolled remainder loop waited out one per partial: 5.1 us at cfg4)
   float s = 0.0f;
   for (int c0 = 0; c0 < slots; c0 += 16) {
     float v[16];
@@ -698,6 +727,7 @@ __global__ __launch_bounds__(256) void bwd_lf_combine(LfArgs a) {
     for (int k = 0; k < 16; ++k)
       if (c0 + k < slots) s += v[k];
   }
+  if (m != 0) s += p[(int64_t)a.nslot * kLfPart];  // block 0's sums of keys 0..G-1
   T* out = static_cast<T*>(m == 0 ? a.dq : m == 1 ? a.dk : a.dv);
   out[((int64_t)b * a.N * a.H + h) * kHeadDim + (int64_t)r * a.H * kHeadDim + d] =
       static_cast<T>(m == 2 ? s : s * a.scale);

@@ -1801,18 +1801,22 @@ int forward_launch(const ma_attn_desc* desc, const void* q, const void* k, const
 // each chunk and one more slot (block 0's sums of keys 0..G-1), the global
 // rows' dQ and the global keys' dK, dV sums (3 x 16 x 64 floats).
 struct LfPlan {
-  int64_t chunk, chunks, part_bytes;
+  int64_t per_wg, wgs, nslot, part_bytes;
 };
 
 LfPlan lf_plan(const ma_attn_desc* d) {
   LfPlan p;
   const int64_t nt = (d->seq_len + kLfRows - 1) / kLfRows;
   const int64_t streams = ma::imax64(d->batch * d->num_heads, 1);
-  // one workgroup per CU (131 KB of LDS): chunks fitted to one round of 256
-  const int64_t per_stream = ma::imax64(1, 256 / streams);
-  p.chunk = ma::imax64(1, (nt + per_stream - 1) / per_stream);
-  p.chunks = ma::imax64(1, (nt + p.chunk - 1) / p.chunk);
-  p.part_bytes = streams * (p.chunks + 1) * kLfPart * (int64_t)sizeof(float);
+  // one workgroup per CU (131 KB of LDS): the streams' tiles in equal runs
+  // over one round of 256 workgroups, a run at most one stream long (so it
+  // meets at most two streams); from 256 streams on, one stream per
+  // workgroup
+  const int64_t tiles = streams * nt;
+  p.per_wg = streams >= 256 ? nt : ma::imax64(1, (tiles + 255) / 256);
+  p.wgs = (tiles + p.per_wg - 1) / p.per_wg;
+  p.nslot = (nt + p.per_wg - 1) / p.per_wg + 1;  // workgroups whose runs meet one stream, at most
+  p.part_bytes = streams * (p.nslot + 1) * kLfPart * (int64_t)sizeof(float);
   return p;
 }
 
@@ -1825,7 +1829,7 @@ bool lf_applies(const ma_attn_desc* d, const void* const* ptrs, int n) {
     if (!aligned16(ptrs[i])) return false;
   const int64_t tb = d->num_heads * kHeadDim * 2;
   return (d->seq_len + 2 * kLfRows) * tb < (1LL << 31) &&
-         d->batch * d->num_heads * lf_plan(d).chunks <= (int64_t)INT32_MAX;
+         lf_plan(d).wgs <= (int64_t)INT32_MAX && d->batch * d->num_heads <= (int64_t)INT32_MAX;
 }
 
 template <typename T>
@@ -1847,15 +1851,16 @@ int launch_lf_bwd(const ma_attn_desc* d, const void* const* ptrs, const void* o,
   a.H = (int32_t)d->num_heads;
   a.L = (int32_t)d->left;
   a.G = (int32_t)ma::imin64(d->num_global, d->seq_len);
-  a.chunk = (int32_t)p.chunk;
-  a.chunks = (int32_t)p.chunks;
+  a.streams = (int32_t)(d->batch * d->num_heads);
+  a.per_wg = (int32_t)p.per_wg;
+  a.nslot = (int32_t)p.nslot;
   a.tok_bytes = (int32_t)(d->num_heads * kHeadDim * sizeof(T));
   a.scale = scale_of(d);
   a.scale_log2 = a.scale * 1.4426950408889634f;
   auto kf = d->left == kLfRows - 1 ? &bwd_lf_kernel<HalfPath<T>, true> : &bwd_lf_kernel<HalfPath<T>, false>;
   if (reserve_lds(reinterpret_cast<const void*>(kf), (size_t)LfLds::kBytes, st)) return 1;
   const int64_t streams = d->batch * d->num_heads;
-  launch(false, kf, dim3((unsigned)(streams * p.chunks)), dim3(kLfThreads), (uint32_t)LfLds::kBytes, st, a);
+  launch(false, kf, dim3((unsigned)p.wgs), dim3(kLfThreads), (uint32_t)LfLds::kBytes, st, a);
   launch(true, bwd_lf_combine<T>, dim3((unsigned)(streams * kLfCombineBlocks)), dim3(256), 0u, st, a);
   return 0;
 }
