@@ -60,6 +60,8 @@ def _check_heads(oracle, got, up, shape, L, G, heads):
     ((1, 10, 2, 64), 127, 16),     # fewer rows than global tokens
     ((2, 2000, 2, 64), 127, 16),
     ((1, 8192, 1, 64), 127, 16),   # one stream: 64 chunks, each global sum merged over all of them
+    ((1, 12928, 3, 64), 127, 16),  # 3 x 101 tiles in runs of 2: runs cross the heads' ends
+    ((1, 12928, 3, 64), 40, 5),
 ])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_longformer_backward_vs_oracle(ext, oracle, shape, L, G, dtype):
