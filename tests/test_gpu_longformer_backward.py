@@ -6,9 +6,10 @@ Longformer key sets).
 
 Cases: windows [i-L, i] with L in {0, 40, 100, 127}, 1 to 16 global tokens,
 sequence lengths around the 128-row tile (ragged last tiles, a single tile,
-fewer rows than global tokens), one and several tiles per workgroup chunk, and
-the full cfg4 shape (B=2 H=12 N=32768) on three heads against the oracle and
-on all heads against the tiled backward.  Tolerance: check_grad's 16-bit
+fewer rows than global tokens), one and several tiles per workgroup,
+workgroup runs of tiles that cross a head's end, 12 seeded random geometries,
+and the full cfg4 shape (B=2 H=12 N=32768) on three heads against the oracle
+and on all heads against the tiled backward.  Tolerance: check_grad's 16-bit
 bound, per element |got - ref| <= 1e-2 + 1e-2 |ref|; against float64 from the
 same saved statistics, twice the worst case of the 16-bit roundings.
 """
@@ -71,6 +72,44 @@ def test_longformer_backward_vs_oracle(ext, oracle, shape, L, G, dtype):
     _check_heads(oracle, got, up, shape, L, G, range(shape[2]))
 
 
+@pytest.mark.parametrize("i", range(12))
+def test_random_longformer_backward(ext, oracle, i):
+    """Seeded random geometries in the one-pass kernel's domain (16-bit,
+    L <= 127, 1 to 16 globals): sequence lengths from one row to 15 000, 1 to
+    12 (batch, head) streams.  The odd cases have more than 256 tiles and an
+    odd tile count per stream, so the workgroups' equal runs (2 to 5 tiles)
+    start and end at varied places and cross the streams' ends.  Every head
+    against the oracle.  In bf16, windows narrower than 63 keys are drawn
+    only up to N = 2000: over longer sequences the global keys' dK gather a
+    systematic term from delta = dO . O with the forward's bf16 O.  When the
+    global keys carry much of every row's softmax, every row's O is nearly the
+    same vector, so its roundings add up over the rows instead of averaging
+    out; against the float32 oracle that exceeded check_grad's bound at
+    N = 12316, G = 11 (2.3x at L = 0, 1.2x at L = 17), while bf16 at L >= 63
+    and fp16 at any L stayed within it.  test_longformer_backward_long_key_only_window
+    holds the kernel to float64 from the same statistics in that regime."""
+    rng = np.random.default_rng(41000 + i)
+    if i % 2:  # more than 256 tiles, an odd count per stream: runs of 2+ tiles cross the heads' ends
+        B, H = 1 + (i % 4 == 1), int(rng.integers(3, 7))
+        nt = int(rng.integers(256 // (B * H) + 2, 121)) | 1
+        N = 128 * (nt - 1) + int(rng.integers(1, 129))
+    else:
+        N = int(rng.choice([int(rng.integers(1, 700)), int(rng.integers(2000, 9000))]))
+        B, H = int(rng.integers(1, 3)), int(rng.integers(1, 7))
+    G = int(rng.integers(1, 17))
+    dtype = [torch.bfloat16, torch.float16][int(rng.integers(0, 2))]
+    narrow = N <= 2000 or dtype == torch.float16
+    L = int(rng.choice([0, 17, 63, 64, 100, 127] if narrow else [63, 64, 100, 127]))
+    tiles = B * H * ((N + 127) // 128)
+    print(f"  case {i}: B={B} N={N} H={H} L={L} G={G} {dtype}, {tiles} tiles in runs of "
+          f"{max(1, (tiles + 255) // 256)}", flush=True)
+    shape = (B, N, H, 64)
+    dev, out, lse, up = _case(ext, shape, 42000 + i, dtype, L, G)
+    assert ext.longformer_fused_applies(dev[0], L, 0, G)
+    got = ext.longformer_backward(*dev, L, 0, G, out=out, lse=lse)
+    _check_heads(oracle, got, up, shape, L, G, range(H))
+
+
 def _same_statistics_grads(dev, out, lse, L, G):
     """float64 dQ, dK, dV of every (batch, head) from the forward's saved
     statistics (lse2, and delta = dO . O with the forward's 16-bit O): the
@@ -115,6 +154,46 @@ def test_longformer_backward_vs_same_statistics(ext, shape, L, G):
     refs, mags = _same_statistics_grads(dev, out, lse, L, G)
     for name, a, r, m in zip(("dq", "dk", "dv"), got, refs, mags):
         a = a.double().cpu().numpy()
+        err = np.abs(a - r)
+        bound = 2e-3 + 2.0 ** -8 * (m + np.abs(r))
+        print(f"  {name}: max|err| = {err.max():.3e}, worst err/bound = {(err / bound).max():.3f}", flush=True)
+        assert (err <= bound).all(), name
+
+
+def test_longformer_backward_long_key_only_window(ext):
+    """L = 0 over a long sequence in bf16 (B=1 N=12316 H=1, G=11, runs of
+    tiles crossing nothing but the chunking of one stream): every element of
+    dQ, dK, dV against float64 from the same saved statistics (lse2, and delta
+    from the forward's bf16 O), within twice the worst case of the kernel's
+    16-bit roundings, as test_longformer_backward_vs_same_statistics.  Against
+    the float32 oracle this geometry exceeds check_grad's bound on the global
+    keys (delta's rounding, see test_random_longformer_backward); here the
+    kernel's own arithmetic is held to its bound."""
+    shape, L, G = (1, 12316, 1, 64), 0, 11
+    dev, out, lse, _ = _case(ext, shape, 42001, torch.bfloat16, L, G)
+    got = ext.longformer_backward(*dev, L, 0, G, out=out, lse=lse)
+    Q, K, V, dO = (t.double().cpu().numpy()[0, :, 0] for t in dev)
+    Ob, l2 = out.double().cpu().numpy()[0, :, 0], lse.double().cpu().numpy()[0, :, 0]
+    N = shape[1]
+    scale = 1.0 / np.sqrt(np.float32(64)).astype(np.float64)
+    refs = [np.zeros((N, 64)) for _ in range(3)]
+    mags = [np.zeros((N, 64)) for _ in range(3)]
+    j = np.arange(N)[None, :]
+    for lo in range(0, N, 2048):  # row blocks: the float64 matrices stay at 2048 x N
+        hi = min(N, lo + 2048)
+        i = np.arange(lo, hi)[:, None]
+        member = (i < G) | (j < G) | ((j <= i) & (j >= i - L))
+        p = np.where(member, 2.0 ** ((Q[lo:hi] @ K.T) * scale * np.log2(np.e) - l2[lo:hi, None]), 0.0)
+        delta = (dO[lo:hi] * Ob[lo:hi]).sum(-1, keepdims=True)
+        ds = p * (dO[lo:hi] @ V.T - delta)
+        refs[0][lo:hi] = scale * ds @ K
+        refs[1] += scale * ds.T @ Q[lo:hi]
+        refs[2] += p.T @ dO[lo:hi]
+        mags[0][lo:hi] = scale * np.abs(ds) @ np.abs(K)
+        mags[1] += scale * np.abs(ds).T @ np.abs(Q[lo:hi])
+        mags[2] += p.T @ np.abs(dO[lo:hi])
+    for name, a, r, m in zip(("dq", "dk", "dv"), got, refs, mags):
+        a = a.double().cpu().numpy()[0, :, 0]
         err = np.abs(a - r)
         bound = 2e-3 + 2.0 ** -8 * (m + np.abs(r))
         print(f"  {name}: max|err| = {err.max():.3e}, worst err/bound = {(err / bound).max():.3f}", flush=True)
