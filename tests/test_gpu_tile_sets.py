@@ -285,7 +285,7 @@ def test_layer_trains_from_saved_statistics(ext, oracle, pattern, dtype, monkeyp
         check_grad("d" + name, t.grad.float().cpu().numpy(), ref, dtype == torch.float32)
 
 
-@pytest.mark.parametrize("N,causal", [(700, True), (1000, False), (64, True)])
+@pytest.mark.parametrize("N,causal", [(700, True), (1000, False), (64, True), (4096, True)])
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_saved_statistics_dense(ext, oracle, N, causal, dtype):
     """dense_forward(return_lse=True) (block-row kernel) writes each row's
