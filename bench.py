@@ -44,9 +44,9 @@ index-set workloads), the backward runs from the forward's saved O and per-row
 statistics (ma_attn_backward_saved), the form the autograd layer trains with;
 the forward runs once per input set before timing, and the algorithmic bytes
 count O and the statistics read as well.  Without --saved-stats the Longformer
-backward (longformer_backward) runs the forward keeping the statistics and
-then the one-pass backward, both timed; its algorithmic bytes stay the 7
-tensors of a backward.
+backward (longformer_backward) runs a forward that writes each row's lse and
+delta = sum_j P dP (no O) and then the one-pass backward, both timed; its
+algorithmic bytes stay the 7 tensors of a backward.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
                        [--pass forward|backward] [--saved-stats]
@@ -550,9 +550,9 @@ def measure(workload: str, which: str = "forward", saved: bool = False, steps: i
                 sets[n_] = s_ + (o_, l_)
             launch = lambda s: ext.index_set_backward(s[0], s[1], s[2], s[3], iset, out=s[4], lse=s[5])
         elif pk["pattern"] == "longformer":
-            # longformer_backward without saved statistics: the forward keeping
-            # them, then the one-pass backward (the tiled kernels where the
-            # one-pass kernel does not apply); both calls' kernels in one span
+            # longformer_backward without saved statistics: a forward writing
+            # lse and delta, then the one-pass backward (the tiled kernels
+            # where the one-pass kernel does not apply), in one span
             iset = None
             launch = lambda s: ext.longformer_backward(s[0], s[1], s[2], s[3], pk["left"], pk["right"],
                                                        pk["num_global"])

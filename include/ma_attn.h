@@ -158,17 +158,23 @@ size_t ma_attn_workspace_size(const ma_attn_desc* desc);
  *                         kernel :265-346)
  *   dense_backward_cuda   src/cuda/sparse_attention_kernel.cu:383-418 (DENSE; kernel :104-175)
  * generalised to any left/right/dilation and to bf16/fp16 (fp32 arithmetic),
- * and for INDEX_SET, which also needs the transposed set (index_t_offsets,
- * index_t_queries: for each key, the queries that list it).  Other patterns
+ * for INDEX_SET, which also needs the transposed set (index_t_offsets,
+ * index_t_queries: for each key, the queries that list it), and for
+ * LONGFORMER in 16 bits at head_dim 64 with right = 0, 0 <= left < 128 and 1
+ * to 16 global tokens (a forward that writes each row's lse and
+ * delta_i = sum_j P_ij dP_ij, dP_ij = dout_i . v_j, in fp32, then the
+ * one-pass backward of ma_attn_backward_saved from them).  Other patterns
  * return non-zero.  workspace: device memory of
- * ma_attn_backward_workspace_size(desc) bytes (per-row softmax statistics).
+ * ma_attn_backward_workspace_size(desc) bytes (per-row softmax statistics;
+ * LONGFORMER also the per-segment partial sums of the global rows and keys).
  */
 int ma_attn_backward(const ma_attn_desc* desc, const void* q, const void* k,
                      const void* v, const void* dout, void* dq, void* dk,
                      void* dv, void* workspace, size_t workspace_bytes,
                      void* stream);
 
-/* Bytes of device workspace ma_attn_backward needs (8 per (b, i, h) row).
+/* Bytes of device workspace ma_attn_backward needs (8 per (b, i, h) row;
+ * LONGFORMER adds the forward's and the backward's partial sums).
  * No reference counterpart: the reference keeps no statistics (it recomputes
  * them per gradient pass, sparse_attention_kernel.cu:285-304). */
 size_t ma_attn_backward_workspace_size(const ma_attn_desc* desc);

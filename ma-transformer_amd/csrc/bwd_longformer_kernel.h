@@ -63,6 +63,7 @@ struct LfArgs {
   const void* dout;
   const void* o;     // the forward's output (delta = dO . O)
   const float* lse;  // the forward's row statistics (store_lse), [B*N*H]
+  const float* delta;  // DLT kernels: each row's sum_j P_ij dP_ij from a delta-mode forward, [B*N*H] (o unused)
   void* dq;
   void* dk;
   void* dv;
@@ -169,20 +170,25 @@ __device__ __forceinline__ void lf_store4(const Rows128x4& x, uint8_t* mat, int 
 // of row ht (ht < 128).
 struct LfTile {
   Rows128x4 q, g, o;
-  float lse2;
+  float lse2, dlt;  // dlt: DLT kernels, row ht's delta
 };
 
-// Tile t's rows into LDS: Q and dO rows, each row's lse2 and delta = dO . O.
-template <typename T>
+// Tile t's rows into LDS: Q and dO rows, each row's lse2 and delta = dO . O
+// (DLT: as given).
+template <typename T, bool DLT>
 __device__ __forceinline__ void lf_stage_tile(const LfTile& x, uint8_t* lds, int ht) {
   lf_store4(x.q, lds + LfLds::kQ, ht);
   lf_store4(x.g, lds + LfLds::kG, ht);
   float* st = reinterpret_cast<float*>(lds + LfLds::kSt);
   if (ht < kLfRows) st[ht] = x.lse2;
+  if constexpr (DLT) {
+    if (ht < kLfRows) st[kLfRows + ht] = x.dlt;
+  } else {
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const float d = sum8(dot8<T>(x.g.r[k], x.o.r[k]));
-    if ((ht & 7) == 0) st[kLfRows + (ht >> 3) + 32 * k] = d;
+    for (int k = 0; k < 4; ++k) {
+      const float d = sum8(dot8<T>(x.g.r[k], x.o.r[k]));
+      if ((ht & 7) == 0) st[kLfRows + (ht >> 3) + 32 * k] = d;
+    }
   }
 }
 
@@ -356,7 +362,7 @@ __device__ __forceinline__ void lf_global_rows_dq(const uint8_t* lds, const uint
 // One segment: query tiles [t0, t1) of (batch, head) bh and key blocks
 // [t0, t1), its global sums into partial slot slot_id.  FIXED127: L = 127,
 // the band's sub-tiles selected by the fixed masks.
-template <class P, bool FIXED127>
+template <class P, bool FIXED127, bool DLT>
 __device__ __forceinline__ void lf_segment(const LfArgs& a, uint8_t* lds, int bh, int t0, int t1, int slot_id) {
   using T = typename P::Elt;
   const int tid = threadIdx.x;
@@ -386,6 +392,7 @@ __device__ __forceinline__ void lf_segment(const LfArgs& a, uint8_t* lds, int bh
   const __amdgpu_buffer_rsrc_t DKr = make_rsrc(static_cast<T*>(a.dk) + base, nrec);
   const __amdgpu_buffer_rsrc_t DVr = make_rsrc(static_cast<T*>(a.dv) + base, nrec);
   const float* lse = a.lse + (int64_t)b * N * a.H + h;  // row i at i * H
+  const float* dlt = DLT ? a.delta + (int64_t)b * N * a.H + h : nullptr;
   float* part = a.part + (int64_t)bh * (a.nslot + 1) * kLfPart;
   // byte offset of row r (r >= -128); rows below 0 wrap past the range
   auto roff = [&](int r) { return (uint32_t)r * tb; };
@@ -394,9 +401,11 @@ __device__ __forceinline__ void lf_segment(const LfArgs& a, uint8_t* lds, int bh
     const uint32_t o = roff(kLfRows * t);
     lf_load4(x.q, Qr, o, ht, tb);
     lf_load4(x.g, Gr, o, ht, tb);
-    lf_load4(x.o, Or, o, ht, tb);
+    if constexpr (!DLT) lf_load4(x.o, Or, o, ht, tb);
     const int i = kLfRows * t + ht;  // no band pair for a row outside [G, N): P = 0
-    x.lse2 = ht < kLfRows && i >= G && i < N ? lse[(int64_t)i * a.H] : __builtin_inff();
+    const bool in = ht < kLfRows && i >= G && i < N;
+    x.lse2 = in ? lse[(int64_t)i * a.H] : __builtin_inff();
+    if constexpr (DLT) x.dlt = in ? dlt[(int64_t)i * a.H] : 0.0f;
   };
   // row c, head_dim 16dt + 4g + r of matrix m (0 dQ, 1 dK, 2 dV) of a slot of partials
   auto store_part = [&](int slot_id, int m, const f32x4(&v)[4]) __attribute__((always_inline)) {
@@ -414,14 +423,19 @@ __device__ __forceinline__ void lf_segment(const LfArgs& a, uint8_t* lds, int bh
   if (tid < 128) {  // uniform per wave
     const uint32_t o = (uint32_t)(tid >> 3) * tb + 16 * (tid & 7);
     const uint4 kx = bload16(Kr, o), vx = bload16(Vr, o), qx = bload16(Qr, o), gx = bload16(Gr, o);
-    const uint4 ox = bload16(Or, o);
     const int r = tid >> 3;
     uint8_t* p = lds + r * LfLds::kRow + 16 * (tid & 7);
     *reinterpret_cast<uint4*>(p + LfLds::kGK) = kx;
     *reinterpret_cast<uint4*>(p + LfLds::kGV) = vx;
     *reinterpret_cast<uint4*>(p + LfLds::kGQ) = qx;
     *reinterpret_cast<uint4*>(p + LfLds::kGG) = gx;
-    const float d = sum8(dot8<T>(gx, ox));
+    float d;
+    if constexpr (DLT) {
+      d = r < G && r < N ? dlt[(int64_t)r * a.H] : 0.0f;
+    } else {
+      const uint4 ox = bload16(Or, o);
+      d = sum8(dot8<T>(gx, ox));
+    }
     float* sg = reinterpret_cast<float*>(lds + LfLds::kStG);
     if ((tid & 7) == 0) {
       sg[r] = r < G && r < N ? lse[(int64_t)r * a.H] : 0.0f;
@@ -441,7 +455,7 @@ __device__ __forceinline__ void lf_segment(const LfArgs& a, uint8_t* lds, int bh
   } else {
     LfTile x;
     load_tile(x, t0);
-    lf_stage_tile<T>(x, lds, ht);
+    lf_stage_tile<T, DLT>(x, lds, ht);
   }
   __syncthreads();
 
@@ -632,7 +646,7 @@ __device__ __forceinline__ void lf_segment(const LfArgs& a, uint8_t* lds, int bh
       if (own && t == nt - 1) global_rows_dq(t);
       __syncthreads();
       if (more) {
-        lf_stage_tile<T>(nx, lds, ht);
+        lf_stage_tile<T, DLT>(nx, lds, ht);
         __syncthreads();
       }
     }
@@ -678,7 +692,7 @@ __device__ __forceinline__ void lf_segment(const LfArgs& a, uint8_t* lds, int bh
 // end of a stream continues at the next stream's start: a second segment,
 // with its own prologue and partial slot (the workgroup's index among those
 // whose runs meet that stream).
-template <class P, bool FIXED127>
+template <class P, bool FIXED127, bool DLT>
 __global__ __launch_bounds__(kLfThreads, 1) void bwd_lf_kernel(LfArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // LfLds
   const int nt = (a.N + kLfRows - 1) / kLfRows;
@@ -690,10 +704,10 @@ __global__ __launch_bounds__(kLfThreads, 1) void bwd_lf_kernel(LfArgs a) {
   const int t1 = (int)min(g1 - s0, (int64_t)nt);
   const int t1b = (int)(g1 - s0 - nt);  // > 0: tiles [0, t1b) of stream bh + 1
   const int slot2 = (int)(blockIdx.x - (s0 + nt) / a.per_wg);
-  lf_segment<P, FIXED127>(a, lds, bh, t0, t1, (int)(blockIdx.x - s0 / a.per_wg));
+  lf_segment<P, FIXED127, DLT>(a, lds, bh, t0, t1, (int)(blockIdx.x - s0 / a.per_wg));
   if (t1b > 0) {  // uniform
     __syncthreads();  // the first segment's LDS reads are done
-    lf_segment<P, FIXED127>(a, lds, bh + 1, 0, t1b, slot2);
+    lf_segment<P, FIXED127, DLT>(a, lds, bh + 1, 0, t1b, slot2);
   }
 }
 

@@ -1419,10 +1419,10 @@ bool stream_applies(const ma_attn_desc* d, const void* q, const void* k, const v
   return p.tok_bytes < (1LL << 24) && rows * p.tok_bytes + 256 < (1LL << 31);
 }
 
-template <class P, int NSLOT, int FL, int FR, bool LG>
+template <class P, int NSLOT, int FL, int FR, bool LG, bool DM>
 int launch_stream_t(const StreamArgs& a, int64_t wgs, hipStream_t st) {
   const size_t shm = (size_t)(NSLOT + (LG ? 1 : 0)) * P::kSlot;
-  auto kern = &stream_kernel<P, NSLOT, kStreamSG, FL, FR, LG>;
+  auto kern = &stream_kernel<P, NSLOT, kStreamSG, FL, FR, LG, DM>;
   if (reserve_lds(reinterpret_cast<const void*>(kern), shm, st)) return 1;
   launch(!LG, kern, dim3((unsigned)wgs), dim3(256), (uint32_t)shm, st, a);  // Longformer: combine is last
   return 0;
@@ -1431,48 +1431,57 @@ int launch_stream_t(const StreamArgs& a, int64_t wgs, hipStream_t st) {
 // Fixed-window instantiations (the benchmark windows: causal 64, [i-32, i+31],
 // Longformer causal 128); other windows run the
 // generic kernel with `slots` ring slots.
-template <class P, bool LG>
+template <class P, bool LG, bool DM>
 int launch_stream_any(const StreamArgs& a, int64_t slots, int64_t wgs, hipStream_t st) {
   constexpr int RS = P::kRows;
   if (!g_opt.no_fixed) {
     if constexpr (!LG) {
-      if (a.left == 63 && a.right == 0) return launch_stream_t<P, WinGeom<63, 0, RS>::NSLOT, 63, 0, LG>(a, wgs, st);
+      if (a.left == 63 && a.right == 0) return launch_stream_t<P, WinGeom<63, 0, RS>::NSLOT, 63, 0, LG, DM>(a, wgs, st);
       if (a.left == 32 && a.right == 31)
-        return launch_stream_t<P, WinGeom<32, 31, RS>::NSLOT, 32, 31, LG>(a, wgs, st);
+        return launch_stream_t<P, WinGeom<32, 31, RS>::NSLOT, 32, 31, LG, DM>(a, wgs, st);
     } else {
       if (a.left == 127 && a.right == 0)
-        return launch_stream_t<P, WinGeom<127, 0, RS>::NSLOT, 127, 0, LG>(a, wgs, st);
+        return launch_stream_t<P, WinGeom<127, 0, RS>::NSLOT, 127, 0, LG, DM>(a, wgs, st);
     }
   }
   switch (slots) {
-    case 1: return launch_stream_t<P, 1, -1, -1, LG>(a, wgs, st);
-    case 2: return launch_stream_t<P, 2, -1, -1, LG>(a, wgs, st);
-    case 3: return launch_stream_t<P, 3, -1, -1, LG>(a, wgs, st);
-    case 4: return launch_stream_t<P, 4, -1, -1, LG>(a, wgs, st);
-    case 5: return launch_stream_t<P, 5, -1, -1, LG>(a, wgs, st);
-    default: return launch_stream_t<P, 6, -1, -1, LG>(a, wgs, st);
+    case 1: return launch_stream_t<P, 1, -1, -1, LG, DM>(a, wgs, st);
+    case 2: return launch_stream_t<P, 2, -1, -1, LG, DM>(a, wgs, st);
+    case 3: return launch_stream_t<P, 3, -1, -1, LG, DM>(a, wgs, st);
+    case 4: return launch_stream_t<P, 4, -1, -1, LG, DM>(a, wgs, st);
+    case 5: return launch_stream_t<P, 5, -1, -1, LG, DM>(a, wgs, st);
+    default: return launch_stream_t<P, 6, -1, -1, LG, DM>(a, wgs, st);
   }
 }
 
 template <typename T>
 int launch_stream_half(const ma_attn_desc* d, const StreamArgs& a, const StreamPlan& p, hipStream_t st) {
   using P = HalfPath<T>;
-  if (p.geom.G == 0) return launch_stream_any<P, false>(a, p.slots, p.wgs, st);
-  const int rc = launch_stream_any<P, true>(a, p.slots, p.wgs, st);
+  if (p.geom.G == 0) return launch_stream_any<P, false, false>(a, p.slots, p.wgs, st);
+  // delta mode is its own instantiation: as a runtime flag its dO loads and
+  // sums cost the plain forward registers (177 -> 203 VGPRs, SGPR spills)
+  // and ~3 % time
+  const int rc = a.delta ? launch_stream_any<P, true, true>(a, p.slots, p.wgs, st)
+                         : launch_stream_any<P, true, false>(a, p.slots, p.wgs, st);
   if (rc) return rc;
   launch(true, longformer_combine<T>, dim3((unsigned)(d->batch * d->num_heads * p.geom.G)), dim3(256), 0, st,
                      a.partials, static_cast<T*>(a.o), (int)p.chunks, (int)p.geom.G, (int)d->num_heads,
-                     d->seq_len, a.lse);
+                     d->seq_len, a.lse, a.delta);
   return 0;
 }
 
+// dout, delta (Longformer only): delta mode, each row's
+// delta = sum_j P_ij dP_ij (dP_ij = dO_i . V_j, fp32) into delta alongside
+// lse, and O not written.
 int launch_stream(const ma_attn_desc* d, const void* q, const void* k, const void* v, void* o, float* lse,
-                  void* ws, size_t ws_bytes, hipStream_t st) {
+                  void* ws, size_t ws_bytes, hipStream_t st, const void* dout = nullptr, float* delta = nullptr) {
   const StreamPlan p = stream_plan(d);
   if ((int64_t)ws_bytes < p.partial_bytes || (p.partial_bytes > 0 && !ws))
     return fail("ma_attn: workspace of %lld bytes required (ma_attn_workspace_size), got %zu",
                 (long long)p.partial_bytes, ws_bytes);
-  StreamArgs a;
+  StreamArgs a{};
+  a.dout = dout;
+  a.delta = delta;
   a.q = q;
   a.k = k;
   a.v = v;
@@ -1499,7 +1508,7 @@ int launch_stream(const ma_attn_desc* d, const void* q, const void* k, const voi
   switch (d->dtype) {
     case MA_ATTN_BF16: return launch_stream_half<__bf16>(d, a, p, st);
     case MA_ATTN_F16: return launch_stream_half<_Float16>(d, a, p, st);
-    default: return launch_stream_any<F32Path, false>(a, p.slots, p.wgs, st);
+    default: return launch_stream_any<F32Path, false, false>(a, p.slots, p.wgs, st);
   }
 }
 
@@ -1547,7 +1556,8 @@ int launch_block(const ma_attn_desc* d, const void* q, const void* k, const void
 // Backward: SLIDING and DENSE key sets (the reference's backward entry
 // points), any dtype, head_dim <= 512.
 bool backward_supported(const ma_attn_desc* d) {
-  return d->pattern == MA_ATTN_SLIDING || d->pattern == MA_ATTN_DENSE || d->pattern == MA_ATTN_INDEX_SET;
+  return d->pattern == MA_ATTN_SLIDING || d->pattern == MA_ATTN_DENSE || d->pattern == MA_ATTN_INDEX_SET ||
+         d->pattern == MA_ATTN_LONGFORMER;
 }
 
 // The query sets T_j = {i : j in S_i}: a SLIDING pattern for the banded
@@ -1832,9 +1842,32 @@ bool lf_applies(const ma_attn_desc* d, const void* const* ptrs, int n) {
          lf_plan(d).wgs <= (int64_t)INT32_MAX && d->batch * d->num_heads <= (int64_t)INT32_MAX;
 }
 
+// ma_attn_backward on LONGFORMER (the one-pass domain): the forward in delta
+// mode (lse and sum_j P_ij dP_ij per row; no O written), then the one-pass
+// backward reading them.  Workspace: lse, delta, the forward's
+// global-row partials, the backward's partials.
+struct LfBwdWs {
+  int64_t off_dlt, off_fp, fp_bytes, off_bp, bp_bytes, total;
+};
+
+LfBwdWs lf_bwd_ws(const ma_attn_desc* d) {
+  auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
+  const int64_t rows = d->batch * d->seq_len * d->num_heads;
+  LfBwdWs w;
+  w.off_dlt = up(rows * (int64_t)sizeof(float));
+  w.off_fp = w.off_dlt + up(rows * (int64_t)sizeof(float));
+  w.fp_bytes = stream_plan(d).partial_bytes;
+  w.off_bp = w.off_fp + up(w.fp_bytes);
+  w.bp_bytes = lf_plan(d).part_bytes;
+  w.total = w.off_bp + w.bp_bytes;
+  return w;
+}
+
+// delta (optional): each row's delta from a delta-mode forward; the DLT
+// kernels read it and not o.
 template <typename T>
 int launch_lf_bwd(const ma_attn_desc* d, const void* const* ptrs, const void* o, const float* lse, void* ws,
-                  hipStream_t st) {
+                  hipStream_t st, const float* delta = nullptr) {
   const LfPlan p = lf_plan(d);
   LfArgs a;
   a.q = ptrs[0];
@@ -1846,6 +1879,7 @@ int launch_lf_bwd(const ma_attn_desc* d, const void* const* ptrs, const void* o,
   a.dv = const_cast<void*>(ptrs[6]);
   a.o = o;
   a.lse = lse;
+  a.delta = delta;
   a.part = static_cast<float*>(ws);
   a.N = (int32_t)d->seq_len;
   a.H = (int32_t)d->num_heads;
@@ -1857,7 +1891,9 @@ int launch_lf_bwd(const ma_attn_desc* d, const void* const* ptrs, const void* o,
   a.tok_bytes = (int32_t)(d->num_heads * kHeadDim * sizeof(T));
   a.scale = scale_of(d);
   a.scale_log2 = a.scale * 1.4426950408889634f;
-  auto kf = d->left == kLfRows - 1 ? &bwd_lf_kernel<HalfPath<T>, true> : &bwd_lf_kernel<HalfPath<T>, false>;
+  const bool fixed = d->left == kLfRows - 1;
+  auto kf = delta ? (fixed ? &bwd_lf_kernel<HalfPath<T>, true, true> : &bwd_lf_kernel<HalfPath<T>, false, true>)
+                  : (fixed ? &bwd_lf_kernel<HalfPath<T>, true, false> : &bwd_lf_kernel<HalfPath<T>, false, false>);
   if (reserve_lds(reinterpret_cast<const void*>(kf), (size_t)LfLds::kBytes, st)) return 1;
   const int64_t streams = d->batch * d->num_heads;
   launch(false, kf, dim3((unsigned)p.wgs), dim3(kLfThreads), (uint32_t)LfLds::kBytes, st, a);
@@ -2178,7 +2214,7 @@ size_t ma_attn_backward_workspace_size(const ma_attn_desc* desc) {
   if (desc->batch * desc->seq_len * desc->num_heads > 0 && tiles_apply(desc, ptrs, 7))
     return (size_t)(stats_bytes(desc) + tiles_bwd_part_bytes(desc));
   if (desc->batch * desc->seq_len * desc->num_heads > 0 && lf_applies(desc, ptrs, 7))
-    return (size_t)lf_plan(desc).part_bytes;  // the Longformer backward from saved statistics
+    return (size_t)lf_bwd_ws(desc).total;  // ma_attn_backward's (ma_attn_backward_saved needs part of it)
   return (size_t)(desc->batch * desc->seq_len * desc->num_heads) * sizeof(RowStat);
 }
 
@@ -2187,7 +2223,7 @@ int ma_attn_backward(const ma_attn_desc* desc, const void* q, const void* k, con
   g_last_error.clear();
   if (validate(desc)) return 1;
   if (!backward_supported(desc))
-    return fail("ma_attn_backward: pattern %d has no backward (SLIDING, DENSE and INDEX_SET only)",
+    return fail("ma_attn_backward: pattern %d has no backward (SLIDING, DENSE, INDEX_SET and LONGFORMER only)",
                 desc->pattern);
   if (desc->pattern == MA_ATTN_INDEX_SET && desc->seq_len > 0 &&
       (!desc->index_t_offsets || (desc->num_indices > 0 && !desc->index_t_queries)))
@@ -2195,6 +2231,35 @@ int ma_attn_backward(const ma_attn_desc* desc, const void* q, const void* k, con
   const int64_t rows = desc->batch * desc->seq_len * desc->num_heads;
   if (rows == 0 || desc->head_dim == 0) return 0;
   if (!q || !k || !v || !dout || !dq || !dk || !dv) return fail("ma_attn_backward: null tensor pointer");
+  if (desc->pattern == MA_ATTN_LONGFORMER) {
+    const void* ptrs[7] = {q, k, v, dout, dq, dk, dv};
+    if (!lf_applies(desc, ptrs, 7) || !stream_applies(desc, q, k, v, dout))
+      return fail("ma_attn_backward: LONGFORMER takes 16-bit tensors, head_dim 64, right = 0, left < 128, 1 to 16 "
+                  "global tokens, 16-byte aligned tensors (index_set_backward over the pattern's key sets "
+                  "serves the rest)");
+    const LfBwdWs w = lf_bwd_ws(desc);
+    if (!workspace || workspace_bytes < (size_t)w.total)
+      return fail("ma_attn_backward: workspace of %lld bytes needed, %zu given", (long long)w.total,
+                  workspace_bytes);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    (void)hipGetLastError();
+    uint8_t* wb = static_cast<uint8_t*>(workspace);
+    float* lse = reinterpret_cast<float*>(wb);
+    float* dlt = reinterpret_cast<float*>(wb + w.off_dlt);
+    // The forward's kernels leave a timed call's stop event to the backward's last.
+    hipEvent_t stop = g_ev_stop;
+    g_ev_stop = nullptr;
+    int rc = launch_stream(desc, q, k, v, nullptr, lse, wb + w.off_fp, (size_t)w.fp_bytes, st, dout, dlt);
+    g_ev_stop = stop;
+    if (!rc)
+      rc = desc->dtype == MA_ATTN_BF16
+               ? launch_lf_bwd<__bf16>(desc, ptrs, nullptr, lse, wb + w.off_bp, st, dlt)
+               : launch_lf_bwd<_Float16>(desc, ptrs, nullptr, lse, wb + w.off_bp, st, dlt);
+    if (rc) return rc;
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail("ma_attn_backward: kernel launch failed: %s", hipGetErrorString(e));
+    return 0;
+  }
   const size_t need = (size_t)rows * sizeof(RowStat);
   if (!workspace || workspace_bytes < need)
     return fail("ma_attn_backward: workspace of %zu bytes needed, %zu given", need, workspace_bytes);

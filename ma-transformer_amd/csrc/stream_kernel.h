@@ -47,11 +47,14 @@ struct StreamArgs {
   float* partials;     // Longformer: [B*H][chunks][16][kPartial] per-chunk softmax partials of the global rows
   float* lse;          // Longformer, optional: each query row's softmax statistic (store_lse), [B*N*H]
   int32_t pairs;       // 1: chunks 2p and 2p+1 share an XCD (grid a multiple of 16, chunks even)
+  const void* dout;    // Longformer delta mode (delta != null): the output gradient dO
+  float* delta;        // Longformer delta mode: each row's sum_j P_ij dP_ij (= dO . O) in fp32, [B*N*H]; O not written
 };
 
 // One partial of a global query row: unnormalised O (64), running max of the
-// log2-scaled scores, and the softmax denominator.
-constexpr int kPartial = kHeadDim + 2;
+// log2-scaled scores, the softmax denominator, and (delta mode) the
+// unnormalised sum of p dP, padded to 16 bytes.
+constexpr int kPartial = kHeadDim + 4;
 
 // A query row's softmax statistic for a backward from saved statistics:
 // log2 of its softmax denominator sum_j 2^(s_j * sl2) over the raw scores
@@ -430,6 +433,14 @@ __device__ __forceinline__ uint32_t ring_slot_bytes(int s) {
   return (uint32_t)(((s / kSubs) % NSLOT) * P::kSlot);
 }
 
+// Longformer delta mode: d + sum_r p[r] dp[r] (probabilities before their
+// 16-bit rounding, dP = dO . V in fp32 from exact 16-bit products).
+__device__ __forceinline__ float p_dp(const float (&p)[4], const f32x4& dp, float d) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) d = fmaf(p[r], dp[r], d);
+  return d;
+}
+
 // One wave's 16 queries qa..qa+15 (qa wave-uniform) against the ring, any
 // window (runtime left/right): scores on MFMA, softmax in registers (online
 // across groups of SG sub-tiles), P.V on MFMA, one store per O row.  Used for
@@ -441,12 +452,13 @@ __device__ __forceinline__ uint32_t ring_slot_bytes(int s) {
 template <class P, int NSLOT, int SG, bool LG>
 __device__ __forceinline__ float stream_tile(const uint8_t* ring, uint32_t kl, uint32_t vl, const typename P::Q& q,
                                             int qa, int Nr, int L, int R, float sl2, __amdgpu_buffer_rsrc_t Or,
-                                            uint32_t orow, int g, int dl, int G) {
+                                            uint32_t orow, int g, int dl, int G, const typename P::Q& gq, bool dm,
+                                            float& dlt) {
   constexpr int kSubs = P::kRows / 16;
   int sub_lo = max(floordiv32(qa - L, 16), 0);
   const int sub_hi = min(floordiv32(qa + 15 + R, 16), (Nr - 1) >> 4);
   const uint32_t span = (uint32_t)(L + R);
-  float m_run = -INFINITY, l_run = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f, d_run = 0.0f;  // d_run: delta mode, sum of p dP
   f32x4 acc[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -463,6 +475,7 @@ __device__ __forceinline__ float stream_tile(const uint8_t* ring, uint32_t kl, u
       p[r] = __builtin_amdgcn_exp2f(fmaf(z[r], sl2, -m_use));
       l_run += p[r];
     }
+    if (dm) d_run = p_dp(p, P::qk(ring + NSLOT * P::kSlot + P::kSlotK + kl, gq), d_run);
     P::pv(ring + NSLOT * P::kSlot + vl, p, acc);
   }
   for (int s0 = sub_lo; s0 <= sub_hi; s0 += SG) {
@@ -500,6 +513,7 @@ __device__ __forceinline__ float stream_tile(const uint8_t* ring, uint32_t kl, u
     if (LG || s0 != sub_lo) {  // rescale what earlier groups accumulated
       const float corr = __builtin_amdgcn_exp2f(m_run * sl2 - m_use);
       l_run *= corr;
+      d_run *= corr;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) acc[dt] *= corr;
     }
@@ -514,11 +528,22 @@ __device__ __forceinline__ float stream_tile(const uint8_t* ring, uint32_t kl, u
         p[r] = __builtin_amdgcn_exp2f(fmaf(sc[j][r], sl2, -m_use));
         l_run += p[r];
       }
+      if (LG && dm)
+        d_run = p_dp(p, P::qk(ring + ring_slot_bytes<P, NSLOT>(s) + P::kSlotK + P::v_sub(s % kSubs) + kl, gq),
+                     d_run);
       P::pv(ring + ring_slot_bytes<P, NSLOT>(s) + P::v_sub(s % kSubs) + vl, p, acc);
     }
   }
   const float l_tot = col_sum(l_run);
-  P::store_o(acc, l_tot > 0.0f ? __builtin_amdgcn_rcpf(l_tot) : 0.0f, Or, orow, g);
+  const float inv = l_tot > 0.0f ? __builtin_amdgcn_rcpf(l_tot) : 0.0f;
+  if constexpr (LG) {  // delta mode: sum_j P_ij dP_ij instead of O
+    if (dm)
+      dlt = l_tot > 0.0f ? col_sum(d_run) / l_tot : 0.0f;
+    else
+      P::store_o(acc, inv, Or, orow, g);
+  } else {
+    P::store_o(acc, inv, Or, orow, g);
+  }
   return l_tot > 0.0f ? m_run * sl2 + __log2f(l_tot) : 0.0f;
 }
 
@@ -540,7 +565,7 @@ struct WinGeom {
 template <class P, int L, int R, bool LG>
 __device__ __forceinline__ float window_tile(const uint8_t* ring, uint32_t kl, uint32_t vl, const typename P::Q& q,
                                             int t, int wv, float sl2, __amdgpu_buffer_rsrc_t Or, uint32_t orow,
-                                            int g, int dl, int ng) {
+                                            int g, int dl, int ng, const typename P::Q& gq, bool dm, float& dlt) {
   using G = WinGeom<L, R, P::kRows>;
   constexpr int kSubs = P::kRows / 16;
   f32x4 sc[G::NSUB];
@@ -632,6 +657,9 @@ __device__ __forceinline__ float window_tile(const uint8_t* ring, uint32_t kl, u
   constexpr int kN = G::NSUB + (LG ? 1 : 0);
   auto score = [&](int j) -> const f32x4& { return LG ? (j == 0 ? zg : sc[j - 1]) : sc[j]; };
   auto vaddr_of = [&](int j) { return LG ? (j == 0 ? (uint32_t)(G::NSLOT * P::kSlot) + vl : vaddr[j - 1]) : vaddr[j]; };
+  // delta mode: the V rows of sub-tile j as the row operand (dP = dO V^T)
+  auto vrow_of = [&](int j) { return vaddr_of(j) - vl + (uint32_t)P::kSlotK + kl; };
+  float d_run = 0.0f;
 #pragma unroll
   for (int j = 0; j < kN; j += 2) {
     float p0[4], p1[4];
@@ -640,19 +668,28 @@ __device__ __forceinline__ float window_tile(const uint8_t* ring, uint32_t kl, u
       p0[r] = __builtin_amdgcn_exp2f(fmaf(score(j)[r], sl2, -m_use));
       l_run += p0[r];
     }
+    if (LG && dm) d_run = p_dp(p0, P::qk(ring + vrow_of(j), gq), d_run);
     if (j + 1 < kN) {  // resolved at compile time
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         p1[r] = __builtin_amdgcn_exp2f(fmaf(score(j + 1)[r], sl2, -m_use));
         l_run += p1[r];
       }
+      if (LG && dm) d_run = p_dp(p1, P::qk(ring + vrow_of(j + 1), gq), d_run);
       P::pv2(ring + vaddr_of(j), ring + vaddr_of(j + 1), p0, p1, acc);
     } else {
       P::pv(ring + vaddr_of(j), p0, acc);
     }
   }
   const float l_tot = col_sum(l_run);
-  P::store_o(acc, __builtin_amdgcn_rcpf(l_tot), Or, orow, g);
+  if constexpr (LG) {  // delta mode: sum_j P_ij dP_ij instead of O
+    if (dm)
+      dlt = col_sum(d_run) / l_tot;  // l_tot > 0: every query sees its own key
+    else
+      P::store_o(acc, __builtin_amdgcn_rcpf(l_tot), Or, orow, g);
+  } else {
+    P::store_o(acc, __builtin_amdgcn_rcpf(l_tot), Or, orow, g);
+  }
   return m_use + __log2f(l_tot);
 }
 
@@ -667,7 +704,7 @@ __device__ __forceinline__ float window_tile(const uint8_t* ring, uint32_t kl, u
 // masked so no key counts twice), and each wave folds one 16-key sub-tile of
 // every tile into an online softmax for the global query rows 0..G-1, written
 // as one partial per wave for longformer_combine.
-template <class P, int NSLOT, int SG, int FL, int FR, bool LG>
+template <class P, int NSLOT, int SG, int FL, int FR, bool LG, bool DM>
 __global__ __launch_bounds__(256, LG ? 2 : P::kMinBlocks) void stream_kernel(StreamArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // (NSLOT + LG) * P::kSlot bytes
   using Elt = typename P::Elt;
@@ -724,6 +761,9 @@ __global__ __launch_bounds__(256, LG ? 2 : P::kMinBlocks) void stream_kernel(Str
   const __amdgpu_buffer_rsrc_t Kr = make_rsrc(static_cast<const Elt*>(a.k) + base, nrec);
   const __amdgpu_buffer_rsrc_t Vr = make_rsrc(static_cast<const Elt*>(a.v) + base, nrec);
   const __amdgpu_buffer_rsrc_t Or = make_rsrc(static_cast<const Elt*>(a.o) + base, nrec);
+  // Longformer delta mode: dO rows read where O rows would be written
+  constexpr bool dm = LG && DM;
+  const __amdgpu_buffer_rsrc_t Gr = make_rsrc(static_cast<const Elt*>(dm ? a.dout : a.o) + base, nrec);
 
   auto row_off = [&](int row) { return (uint32_t)(row - base_row) * tb; };
   const uint32_t q_lane = (16 * wv + c) * tb;  // this lane's query row within a tile
@@ -757,6 +797,8 @@ __global__ __launch_bounds__(256, LG ? 2 : P::kMinBlocks) void stream_kernel(Str
   // second tile's new rows
   typename P::Q qc;
   P::load_q(qc, Qr, row_off(tfirst * 64) + q_lane, g);
+  typename P::Q gc{};  // delta mode: the tile's dO rows
+  if (LG && dm) P::load_q(gc, Gr, row_off(tfirst * 64) + q_lane, g);
   const int blo_f = max(blo_of(tfirst), 0);
   const int top_f = min(bhi_of(tfirst), nblk - 1);
   typename P::Slot X[SPS], Y[SPS];
@@ -775,16 +817,17 @@ __global__ __launch_bounds__(256, LG ? 2 : P::kMinBlocks) void stream_kernel(Str
     for (int s = 0; s < NSLOT; ++s)
       if (blo_f + s <= top_f) P::store_slot(pre[s], ring + ((blo_f + s) % NSLOT) * P::kSlot, tid);
   }
-  typename P::Q qg;  // Longformer: Q rows of the global queries (query c of every wave)
+  typename P::Q qg, gqg{};  // Longformer: Q (and, delta mode, dO) rows of the global queries (query c of every wave)
   if (LG) {
     typename P::Slot gs;
     P::load_slot(gs, Kr, Vr, row_off(0), tid, tb);
     P::store_slot(gs, ring + NSLOT * P::kSlot, tid);
     P::load_q(qg, Qr, row_off(0) + c * tb, g);
+    if (dm) P::load_q(gqg, Gr, row_off(0) + c * tb, g);
   }
   __syncthreads();
   const int G = LG ? a.num_global : 0;
-  float mg = -INFINITY, lg = 0.0f;  // Longformer global rows: this wave's softmax partial
+  float mg = -INFINITY, lg = 0.0f, dg = 0.0f;  // Longformer global rows: this wave's softmax partial
   f32x4 accg[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) accg[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -795,8 +838,9 @@ __global__ __launch_bounds__(256, LG ? 2 : P::kMinBlocks) void stream_kernel(Str
   // was the last to read.
   auto step = [&](int t, typename P::Slot(&cur)[SPS], typename P::Slot(&nxt)[SPS]) {
     const int tn = t + dir, tnn = t + 2 * dir;
-    typename P::Q qn;
+    typename P::Q qn, gn{};
     P::load_q(qn, Qr, (tile_ok(tn) ? row_off(tn * 64) : kOob) + q_lane, g);
+    if (LG && dm) P::load_q(gn, Gr, (tile_ok(tn) ? row_off(tn * 64) : kOob) + q_lane, g);
 #pragma unroll
     for (int i = 0; i < SPS; ++i) {
       const int blk = new_of(tnn) + i;
@@ -804,15 +848,17 @@ __global__ __launch_bounds__(256, LG ? 2 : P::kMinBlocks) void stream_kernel(Str
     }
 
     const uint32_t orow = row_off(t * 64) + q_lane;
-    float lse2;
+    float lse2, dlt = 0.0f;
     if (kFixed && t >= t_int_lo && t < t_int_hi)
-      lse2 = window_tile<P, FLc, FRc, LG>(ring, kl, vl, qc, t, wv, a.scale_log2, Or, orow, g, dl, G);
+      lse2 = window_tile<P, FLc, FRc, LG>(ring, kl, vl, qc, t, wv, a.scale_log2, Or, orow, g, dl, G, gc, dm, dlt);
     else
       lse2 = stream_tile<P, NSLOT, SG, LG>(ring, kl, vl, qc, t * 64 + 16 * wv, Nr, L, R, a.scale_log2, Or, orow,
-                                           g, dl, G);
+                                           g, dl, G, gc, dm, dlt);
     if constexpr (LG) {  // dilation 1: query m is token m (rows 0..G-1 are rewritten by the combine)
       const int m = t * 64 + 16 * wv + c;
-      if (a.lse && g == 0 && m < Nr) a.lse[((int64_t)b * a.N + m) * a.H + h] = lse2;
+      const int64_t row = ((int64_t)b * a.N + m) * a.H + h;
+      if (a.lse && g == 0 && m < Nr) a.lse[row] = lse2;
+      if (dm && g == 0 && m < Nr) a.delta[row] = dlt;
     }
     if (LG) {  // global query rows against keys 64t + 16wv .. +15 (in the ring at tile t)
       const int key0 = t * 64 + 16 * wv;
@@ -826,6 +872,7 @@ __global__ __launch_bounds__(256, LG ? 2 : P::kMinBlocks) void stream_kernel(Str
       const float m_use = m_new == -INFINITY ? 0.0f : m_new * a.scale_log2;
       const float corr = __builtin_amdgcn_exp2f(mg * a.scale_log2 - m_use);
       lg *= corr;
+      dg *= corr;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) accg[dt] *= corr;
       mg = m_new;
@@ -835,7 +882,9 @@ __global__ __launch_bounds__(256, LG ? 2 : P::kMinBlocks) void stream_kernel(Str
         p[r] = __builtin_amdgcn_exp2f(fmaf(z[r], a.scale_log2, -m_use));
         lg += p[r];
       }
-      P::pv(ring + ring_slot_bytes<P, NSLOT>(key0 / 16) + P::v_sub((key0 / 16) % kSubs) + vl, p, accg);
+      const uint32_t vsub = ring_slot_bytes<P, NSLOT>(key0 / 16) + P::v_sub((key0 / 16) % kSubs);
+      if (dm) dg = p_dp(p, P::qk(ring + vsub + P::kSlotK + kl, gqg), dg);
+      P::pv(ring + vsub + vl, p, accg);
     }
 
     __syncthreads();
@@ -846,6 +895,7 @@ __global__ __launch_bounds__(256, LG ? 2 : P::kMinBlocks) void stream_kernel(Str
     }
     __syncthreads();
     qc = qn;
+    gc = gn;
   };
 
   const int cnt = t1 - t0;
@@ -857,17 +907,19 @@ __global__ __launch_bounds__(256, LG ? 2 : P::kMinBlocks) void stream_kernel(Str
 
   if (LG) {
     // Each wave's partial for global query c ([64 unnormalised O][log2-scaled
-    // max][denominator]) goes to LDS (the ring is free after the last tile's
-    // barrier; rows of 68 floats keep the 16 B stores aligned); the 4 waves'
-    // partials of a query then merge (log-sum-exp) into one per chunk, so the
-    // combine reads a quarter as many.
+    // max][denominator][delta mode: sum of p dP]) goes to LDS (the ring is
+    // free after the last tile's barrier; rows of 68 floats keep the 16 B
+    // stores aligned); the 4 waves' partials of a query then merge
+    // (log-sum-exp) into one per chunk, so the combine reads a quarter as many.
     constexpr int kRowF = 68;
     const float l_tot = col_sum(lg);
+    const float d_tot = dm ? col_sum(dg) : 0.0f;
     float* shp = reinterpret_cast<float*>(ring) + (wv * 16 + c) * kRowF;
     P::store_acc(accg, shp, g);
     if (g == 0) {
       shp[kHeadDim] = mg == -INFINITY ? -INFINITY : mg * a.scale_log2;
       shp[kHeadDim + 1] = l_tot;
+      shp[kHeadDim + 2] = d_tot;
     }
     __syncthreads();
     const int qq = tid >> 4, d0 = 4 * (tid & 15);  // global query qq, head_dim d0..d0+3
@@ -878,20 +930,20 @@ __global__ __launch_bounds__(256, LG ? 2 : P::kMinBlocks) void stream_kernel(Str
       mw[w] = sp[w * 16 * kRowF + kHeadDim];
       mt = fmaxf(mt, mw[w]);
     }
-    float lt = 0.0f;
+    float lt = 0.0f, dtt = 0.0f;
     f32x4 at = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     if (mt != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         const float cw = __builtin_amdgcn_exp2f(mw[w] - mt);  // 0 for a wave that saw no key
         lt = fmaf(sp[w * 16 * kRowF + kHeadDim + 1], cw, lt);
+        dtt = fmaf(sp[w * 16 * kRowF + kHeadDim + 2], cw, dtt);
         at += *reinterpret_cast<const f32x4*>(sp + w * 16 * kRowF + d0) * cw;
       }
     }
     float* dst = a.partials + ((((int64_t)b * a.H + h) * a.chunks + chunk_id) * 16 + qq) * kPartial;
-    *reinterpret_cast<float2*>(dst + d0) = make_float2(at[0], at[1]);  // rows of 66 floats: 8 B aligned
-    *reinterpret_cast<float2*>(dst + d0 + 2) = make_float2(at[2], at[3]);
-    if ((tid & 15) == 0) *reinterpret_cast<float2*>(dst + kHeadDim) = make_float2(mt, lt);
+    *reinterpret_cast<f32x4*>(dst + d0) = at;  // rows of 68 floats: 16 B aligned
+    if ((tid & 15) == 0) *reinterpret_cast<f32x4*>(dst + kHeadDim) = f32x4{mt, lt, dtt, 0.0f};
   }
 }
 
@@ -906,7 +958,8 @@ __global__ __launch_bounds__(256, LG ? 2 : P::kMinBlocks) void stream_kernel(Str
 // before the weighted sums, two round trips: 5.2 us.)
 template <typename Elt>
 __global__ __launch_bounds__(256) void longformer_combine(const float* __restrict__ partials, Elt* __restrict__ o,
-                                                          int nparts, int G, int H, int64_t N, float* lse) {
+                                                          int nparts, int G, int H, int64_t N, float* lse,
+                                                          float* delta) {
   __shared__ float sh[4][kPartial];
   const int d = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
@@ -917,17 +970,20 @@ __global__ __launch_bounds__(256) void longformer_combine(const float* __restric
   // partial p of this global row: base + p * 16 * kPartial
   const float* base = partials + ((int64_t)bh * nparts * 16 + gq) * kPartial;
   constexpr int64_t kStride = 16 * kPartial;
-  // Batches of 8 partials per wave, all 24 loads of a batch issued together:
-  // one load round trip per 32 partials of the row.
-  float m = -INFINITY, l = 0.0f, acc = 0.0f;
+  // Batches of 8 partials per wave, all loads of a batch issued together:
+  // one load round trip per 32 partials of the row.  Delta mode also merges
+  // the partials' sums of p dP, with the denominators' weights.
+  const bool dm = delta != nullptr;
+  float m = -INFINITY, l = 0.0f, acc = 0.0f, dsum = 0.0f;
   for (int p0 = wv; p0 < nparts; p0 += 32) {
-    float mk[8], lk[8], ak[8];
+    float mk[8], lk[8], ak[8], dk[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int p = p0 + 4 * k;
       const float* src = base + (int64_t)min(p, nparts - 1) * kStride;
       mk[k] = src[kHeadDim];
       lk[k] = src[kHeadDim + 1];
+      dk[k] = dm ? src[kHeadDim + 2] : 0.0f;
       ak[k] = src[d];
       if (p >= nparts) mk[k] = -INFINITY;
     }
@@ -938,11 +994,13 @@ __global__ __launch_bounds__(256) void longformer_combine(const float* __restric
       const float c = __builtin_amdgcn_exp2f(m - mb);  // 0 while m is -inf
       l *= c;
       acc *= c;
+      dsum *= c;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const float w = __builtin_amdgcn_exp2f(mk[k] - mb);  // 0 for a partial that saw no key
         l = fmaf(lk[k], w, l);
         acc = fmaf(ak[k], w, acc);
+        dsum = fmaf(dk[k], w, dsum);
       }
       m = mb;
     }
@@ -951,24 +1009,31 @@ __global__ __launch_bounds__(256) void longformer_combine(const float* __restric
   if (d == 0) {
     sh[wv][kHeadDim] = m;
     sh[wv][kHeadDim + 1] = l;
+    sh[wv][kHeadDim + 2] = dsum;
   }
   __syncthreads();
   if (wv == 0) {
     float mt = -INFINITY;
 #pragma unroll
     for (int w = 0; w < 4; ++w) mt = fmaxf(mt, sh[w][kHeadDim]);
-    float lt = 0.0f, at = 0.0f;
+    float lt = 0.0f, at = 0.0f, dt = 0.0f;
     if (mt != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         const float c = __builtin_amdgcn_exp2f(sh[w][kHeadDim] - mt);
         lt = fmaf(sh[w][kHeadDim + 1], c, lt);
         at = fmaf(sh[w][d], c, at);
+        dt = fmaf(sh[w][kHeadDim + 2], c, dt);
       }
     }
-    o[(((int64_t)b * N + gq) * H + h) * kHeadDim + d] = static_cast<Elt>(lt > 0.0f ? at / lt : 0.0f);
+    const int64_t row = ((int64_t)b * N + gq) * H + h;
+    if (dm) {  // delta mode: the row's sum_j P_ij dP_ij; O not written
+      if (d == 0) delta[row] = lt > 0.0f ? dt / lt : 0.0f;
+    } else {
+      o[row * kHeadDim + d] = static_cast<Elt>(lt > 0.0f ? at / lt : 0.0f);
+    }
     // the global row's statistic (mt is in log2 units of the scaled scores)
-    if (lse && d == 0) lse[((int64_t)b * N + gq) * H + h] = lt > 0.0f ? mt + __log2f(lt) : 0.0f;
+    if (lse && d == 0) lse[row] = lt > 0.0f ? mt + __log2f(lt) : 0.0f;
   }
 }
 

@@ -515,28 +515,23 @@ def longformer_backward(query, key, value, grad_out, left: int, right: int = 0, 
     """dQ, dK, dV of longformer_forward.
 
     For a window [i-left, i] (left <= 127, 1 to 16 global tokens, 16-bit,
-    head_dim 64, 16-byte aligned tensors): one pass over Q, K, V, dO and O
-    (ma_attn_backward_saved, bwd_lf_kernel) from the forward's output and
-    statistics, taken from out and lse (longformer_forward(...,
-    return_lse=True)) or, without them, from one longformer_forward run here
-    first (the two calls' kernels stamped as one span under kernel_events).
+    head_dim 64, 16-byte aligned tensors) one pass over the sequence
+    (bwd_lf_kernel):
+    - with out and lse (longformer_forward(..., return_lse=True)): from the
+      forward's output and statistics, delta = dO . O with the 16-bit O
+      (ma_attn_backward_saved);
+    - without them: ma_attn_backward on the LONGFORMER descriptor, which runs
+      the forward first for each row's statistic and delta = dO . O from its
+      fp32 O (no O written), then the same pass.
     Otherwise the tiled kernels over the pattern's key sets (index_set_backward
     on pattern_index_set)."""
-    global _events
     _check(query, key, value, grad_out)
     N = query.shape[1]
     kw = dict(left=int(left), right=int(right), num_global=int(num_global))
     if longformer_fused_applies(query, left, right, num_global) and all(
             t.data_ptr() % 16 == 0 for t in (query, key, value, grad_out)):
         if out is None or lse is None:
-            ev = _events
-            try:
-                _events = (ev[0], None) if ev else None  # the forward's kernels start the span
-                out, lse = longformer_forward(query, key, value, left, right, num_global, return_lse=True)
-                _events = (None, ev[1]) if ev else None  # the backward's end it
-                return _backward_saved(query, key, value, out, lse, grad_out, _ma.LONGFORMER, **kw)
-            finally:
-                _events = ev
+            return _backward(query, key, value, grad_out, _ma.LONGFORMER, **kw)
         if out.data_ptr() % 16 == 0:
             _check(query, out)
             _check_lse(lse, query)

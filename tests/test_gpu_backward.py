@@ -279,8 +279,12 @@ def test_backward_sum_identities_full_size(ext, left, right, dil):
 def test_backward_rejects_unsupported(ext):
     q = torch.randn(1, 64, 1, 64, device="cuda", dtype=torch.bfloat16)
     from ma_attn import BLOCK_SPARSE, LONGFORMER
-    for pat in (BLOCK_SPARSE, LONGFORMER):
-        with pytest.raises(RuntimeError):
-            ext._backward(q, q, q, q, pat, num_global=4)
+    with pytest.raises(RuntimeError):
+        ext._backward(q, q, q, q, BLOCK_SPARSE)
+    # LONGFORMER only in the one-pass kernel's domain (16-bit, left < 128, right = 0)
+    for t, kw in ((q.float(), dict(num_global=4)), (q, dict(left=200, num_global=4)),
+                  (q, dict(left=3, right=2, num_global=4))):
+        with pytest.raises(RuntimeError, match="LONGFORMER"):
+            ext._backward(t, t, t, t, LONGFORMER, **kw)
     with pytest.raises(RuntimeError):
         ext.backward(q, q, q, q.float())  # mixed dtypes

@@ -200,6 +200,18 @@ def test_longformer_backward_long_key_only_window(ext):
         assert (err <= bound).all(), name
 
 
+@pytest.mark.parametrize("L,G", [(0, 11), (17, 11)])
+def test_longformer_backward_long_narrow_window_without_statistics(ext, oracle, L, G):
+    """The regime where delta from the forward's bf16 O exceeds the bound
+    (B=2 N=12316 H=2, bf16): without saved statistics delta comes from the
+    forward's fp32 O, and every gradient element of both heads is within
+    check_grad's bound of the oracle's."""
+    shape = (2, 12316, 2, 64)
+    dev, _, _, up = _case(ext, shape, 42001, torch.bfloat16, L, G)
+    got = ext.longformer_backward(*dev, L, 0, G)
+    _check_heads(oracle, got, up, shape, L, G, range(shape[2]))
+
+
 def test_longformer_backward_several_tiles_per_chunk(ext, oracle):
     """64 (batch, head) streams: 4 chunks of 8 tiles each (the chunk's carried
     key block and its extra key pass for the next chunk's first tile)."""
@@ -274,14 +286,18 @@ def test_layer_longformer_training_uses_the_one_pass_kernel(ext, oracle, monkeyp
 
 @pytest.mark.parametrize("shape,L,G", [((1, 700, 2, 64), 127, 16), ((2, 300, 1, 64), 40, 5)])
 def test_longformer_backward_without_statistics(ext, oracle, shape, L, G):
-    """longformer_backward without out / lse: the forward keeping the
-    statistics, then the one-pass kernel; the same bits as calling the two
-    in sequence, and the oracle's gradients; under kernel_events the two
-    calls' kernels are stamped as one span."""
+    """longformer_backward without out / lse (ma_attn_backward on the
+    LONGFORMER descriptor: the forward writing each row's statistic and
+    delta = dO . O from its fp32 O, then the one-pass kernel): the oracle's
+    gradients, the saved-statistics call's within the 16-bit bound (the two
+    differ only in delta's rounding), bit-identical repeats; under
+    kernel_events both launches' kernels are stamped as one span."""
     dev, out, lse, up = _case(ext, shape, 6700 + shape[1] + L, torch.bfloat16, L, G)
     got = ext.longformer_backward(*dev, L, 0, G)
     saved = ext.longformer_backward(*dev, L, 0, G, out=out, lse=lse)
-    for a, b in zip(got, saved):
+    for name, a, b in zip(("dq", "dk", "dv"), got, saved):
+        check_grad(name, a.float().cpu().numpy(), b.float().cpu().numpy(), False)
+    for a, b in zip(got, ext.longformer_backward(*dev, L, 0, G)):
         assert torch.equal(a, b)
     _check_heads(oracle, got, up, shape, L, G, range(shape[2]))
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
