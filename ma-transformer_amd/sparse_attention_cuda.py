@@ -521,8 +521,9 @@ def longformer_backward(query, key, value, grad_out, left: int, right: int = 0, 
       forward's output and statistics, delta = dO . O with the 16-bit O
       (ma_attn_backward_saved);
     - without them: ma_attn_backward on the LONGFORMER descriptor, which runs
-      the forward first for each row's statistic and delta = dO . O from its
-      fp32 O (no O written), then the same pass.
+      the forward first for each row's statistic and
+      delta = sum_j P_ij dP_ij (dP_ij = dO_i . V_j, fp32; no O written), then
+      the same pass.
     Otherwise the tiled kernels over the pattern's key sets (index_set_backward
     on pattern_index_set)."""
     _check(query, key, value, grad_out)

@@ -288,3 +288,31 @@ def test_backward_rejects_unsupported(ext):
             ext._backward(t, t, t, t, LONGFORMER, **kw)
     with pytest.raises(RuntimeError):
         ext.backward(q, q, q, q.float())  # mixed dtypes
+
+
+def test_longformer_backward_workspace_through_the_c_abi(ext):
+    """ma_attn_backward on a LONGFORMER descriptor through the C-ABI: the
+    workspace ma_attn_backward_workspace_size names (statistics, delta and
+    both passes' partials) is taken, one byte less or none is refused with a
+    message naming the size, and nothing is written then."""
+    import ma_attn as _ma
+    B, N, H, D = 1, 1000, 2, 64
+    q, k, v, g = (torch.randn(B, N, H, D, device="cuda", dtype=torch.bfloat16) for _ in range(4))
+    desc = _ma.make_desc(B, N, H, D, _ma.BF16, _ma.LONGFORMER, left=127, right=0, num_global=16)
+    need = _ma.backward_workspace_size(desc)
+    saved_need = 2 * 4 * B * N * H  # at least the statistics and delta, 4 B each per row
+    assert need > saved_need
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    ptrs = [t.data_ptr() for t in (q, k, v, g)]
+    for nbytes, wsp in ((need - 1, ws.data_ptr()), (need, 0)):
+        outs = [torch.full_like(q, 7.0) for _ in range(3)]
+        with pytest.raises(RuntimeError, match=f"workspace of {need} bytes"):
+            _ma.backward_raw(desc, *ptrs, *(t.data_ptr() for t in outs), wsp, nbytes)
+        torch.cuda.synchronize()
+        assert all(bool((t == 7.0).all()) for t in outs)
+    outs = [torch.empty_like(q) for _ in range(3)]
+    _ma.backward_raw(desc, *ptrs, *(t.data_ptr() for t in outs), ws.data_ptr(), need)
+    ref = ext.longformer_backward(q, k, v, g, 127, 0, 16)
+    torch.cuda.synchronize()
+    for a, b in zip(outs, ref):
+        assert torch.equal(a, b)

@@ -65,15 +65,19 @@ def _check_heads(oracle, got, up, shape, L, G, heads):
     ((1, 12928, 3, 64), 40, 5),
 ])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_longformer_backward_vs_oracle(ext, oracle, shape, L, G, dtype):
+@pytest.mark.parametrize("saved", [True, False], ids=["saved", "nostats"])
+def test_longformer_backward_vs_oracle(ext, oracle, shape, L, G, dtype, saved):
+    """saved: from the forward's O and statistics (ma_attn_backward_saved);
+    nostats: ma_attn_backward (the forward in delta mode, then the same pass)."""
     dev, out, lse, up = _case(ext, shape, 6100 + shape[1] + L, dtype, L, G)
     assert ext.longformer_fused_applies(dev[0], L, 0, G)
-    got = ext.longformer_backward(*dev, L, 0, G, out=out, lse=lse)
+    got = ext.longformer_backward(*dev, L, 0, G, **(dict(out=out, lse=lse) if saved else {}))
     _check_heads(oracle, got, up, shape, L, G, range(shape[2]))
 
 
+@pytest.mark.parametrize("saved", [True, False], ids=["saved", "nostats"])
 @pytest.mark.parametrize("i", range(12))
-def test_random_longformer_backward(ext, oracle, i):
+def test_random_longformer_backward(ext, oracle, i, saved):
     """Seeded random geometries in the one-pass kernel's domain (16-bit,
     L <= 127, 1 to 16 globals): sequence lengths from one row to 15 000, 1 to
     12 (batch, head) streams.  The odd cases have more than 256 tiles and an
@@ -87,7 +91,9 @@ def test_random_longformer_backward(ext, oracle, i):
     out; against the float32 oracle that exceeded check_grad's bound at
     N = 12316, G = 11 (2.3x at L = 0, 1.2x at L = 17), while bf16 at L >= 63
     and fp16 at any L stayed within it.  test_longformer_backward_long_key_only_window
-    holds the kernel to float64 from the same statistics in that regime."""
+    holds the kernel to float64 from the same statistics in that regime.
+    Without saved statistics (nostats: delta = sum_j P_ij dP_ij from the
+    forward in fp32) every window is drawn at every length."""
     rng = np.random.default_rng(41000 + i)
     if i % 2:  # more than 256 tiles, an odd count per stream: runs of 2+ tiles cross the heads' ends
         B, H = 1 + (i % 4 == 1), int(rng.integers(3, 7))
@@ -98,7 +104,7 @@ def test_random_longformer_backward(ext, oracle, i):
         B, H = int(rng.integers(1, 3)), int(rng.integers(1, 7))
     G = int(rng.integers(1, 17))
     dtype = [torch.bfloat16, torch.float16][int(rng.integers(0, 2))]
-    narrow = N <= 2000 or dtype == torch.float16
+    narrow = N <= 2000 or dtype == torch.float16 or not saved
     L = int(rng.choice([0, 17, 63, 64, 100, 127] if narrow else [63, 64, 100, 127]))
     tiles = B * H * ((N + 127) // 128)
     print(f"  case {i}: B={B} N={N} H={H} L={L} G={G} {dtype}, {tiles} tiles in runs of "
@@ -106,7 +112,7 @@ def test_random_longformer_backward(ext, oracle, i):
     shape = (B, N, H, 64)
     dev, out, lse, up = _case(ext, shape, 42000 + i, dtype, L, G)
     assert ext.longformer_fused_applies(dev[0], L, 0, G)
-    got = ext.longformer_backward(*dev, L, 0, G, out=out, lse=lse)
+    got = ext.longformer_backward(*dev, L, 0, G, **(dict(out=out, lse=lse) if saved else {}))
     _check_heads(oracle, got, up, shape, L, G, range(H))
 
 
@@ -203,9 +209,9 @@ def test_longformer_backward_long_key_only_window(ext):
 @pytest.mark.parametrize("L,G", [(0, 11), (17, 11)])
 def test_longformer_backward_long_narrow_window_without_statistics(ext, oracle, L, G):
     """The regime where delta from the forward's bf16 O exceeds the bound
-    (B=2 N=12316 H=2, bf16): without saved statistics delta comes from the
-    forward's fp32 O, and every gradient element of both heads is within
-    check_grad's bound of the oracle's."""
+    (B=2 N=12316 H=2, bf16): without saved statistics the forward sums
+    delta = sum_j P_ij dP_ij in fp32, and every gradient element of both
+    heads is within check_grad's bound of the oracle's."""
     shape = (2, 12316, 2, 64)
     dev, _, _, up = _case(ext, shape, 42001, torch.bfloat16, L, G)
     got = ext.longformer_backward(*dev, L, 0, G)
@@ -288,7 +294,7 @@ def test_layer_longformer_training_uses_the_one_pass_kernel(ext, oracle, monkeyp
 def test_longformer_backward_without_statistics(ext, oracle, shape, L, G):
     """longformer_backward without out / lse (ma_attn_backward on the
     LONGFORMER descriptor: the forward writing each row's statistic and
-    delta = dO . O from its fp32 O, then the one-pass kernel): the oracle's
+    delta = sum_j P_ij dP_ij, then the one-pass kernel): the oracle's
     gradients, the saved-statistics call's within the 16-bit bound (the two
     differ only in delta's rounding), bit-identical repeats; under
     kernel_events both launches' kernels are stamped as one span."""
