@@ -166,15 +166,18 @@ __device__ __forceinline__ void lf_store4(const Rows128x4& x, uint8_t* mat, int 
   for (int k = 0; k < 4; ++k) *reinterpret_cast<uint4*>(p + 32 * k * LfLds::kRow) = x.r[k];
 }
 
-// A query tile in flight (helper waves): Q, dO and O rows and the statistic
-// of row ht (ht < 128).
+// A query tile in flight (helper waves): Q and dO rows, the statistic of row
+// ht (ht < 128) and the rows' delta.  From saved statistics delta = dO . O is
+// taken as soon as the O rows arrive, so they hold no registers through the
+// helpers' sums (with O in flight to the staging point, 14 VGPRs spilled; cfg4
+// 243-245 -> 229-231 us).
 struct LfTile {
-  Rows128x4 q, g, o;
+  Rows128x4 q, g;
   float lse2, dlt;  // dlt: DLT kernels, row ht's delta
+  float od[4];      // otherwise: rows (ht>>3) + 32k's delta, summed over their 8 threads
 };
 
-// Tile t's rows into LDS: Q and dO rows, each row's lse2 and delta = dO . O
-// (DLT: as given).
+// Tile t's rows into LDS: Q and dO rows, each row's lse2 and delta.
 template <typename T, bool DLT>
 __device__ __forceinline__ void lf_stage_tile(const LfTile& x, uint8_t* lds, int ht) {
   lf_store4(x.q, lds + LfLds::kQ, ht);
@@ -185,10 +188,8 @@ __device__ __forceinline__ void lf_stage_tile(const LfTile& x, uint8_t* lds, int
     if (ht < kLfRows) st[kLfRows + ht] = x.dlt;
   } else {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float d = sum8(dot8<T>(x.g.r[k], x.o.r[k]));
-      if ((ht & 7) == 0) st[kLfRows + (ht >> 3) + 32 * k] = d;
-    }
+    for (int k = 0; k < 4; ++k)
+      if ((ht & 7) == 0) st[kLfRows + (ht >> 3) + 32 * k] = x.od[k];
   }
 }
 
@@ -401,7 +402,12 @@ __device__ __forceinline__ void lf_segment(const LfArgs& a, uint8_t* lds, int bh
     const uint32_t o = roff(kLfRows * t);
     lf_load4(x.q, Qr, o, ht, tb);
     lf_load4(x.g, Gr, o, ht, tb);
-    if constexpr (!DLT) lf_load4(x.o, Or, o, ht, tb);
+    if constexpr (!DLT) {  // delta = dO . O at once: O's registers free before the sums
+      Rows128x4 xo;
+      lf_load4(xo, Or, o, ht, tb);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) x.od[k] = sum8(dot8<T>(x.g.r[k], xo.r[k]));
+    }
     const int i = kLfRows * t + ht;  // no band pair for a row outside [G, N): P = 0
     const bool in = ht < kLfRows && i >= G && i < N;
     x.lse2 = in ? lse[(int64_t)i * a.H] : __builtin_inff();
