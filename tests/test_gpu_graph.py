@@ -29,6 +29,7 @@ def test_graph_capture_replays(ext):
     iset = ext.IndexSet.from_coo(rows, (rows * 7 + torch.arange(3).repeat(4096) * 13) % 4096, 4096)
 
     def work():
+        lo, llse = ext.longformer_forward(q, k, v, 127, 0, 16, return_lse=True)
         return [ext.sliding_forward(q, k, v, 63, 0),
                 ext.sliding_forward(q, k, v, 32, 31, 2),
                 ext.block_sparse_forward(q, k, v, table, 64),
@@ -36,7 +37,11 @@ def test_graph_capture_replays(ext):
                 ext.dense_forward(qf, kf, vf, True),
                 ext.index_set_forward(q, k, v, iset),  # gather kernel over a device-resident set
                 *ext.sliding_backward(q, k, v, g, 63, 0, 1),  # statistics workspace, two launches
-                *ext.sliding_backward(qf, kf, vf, gf, 63, 0, 1)]
+                *ext.sliding_backward(qf, kf, vf, gf, 63, 0, 1),
+                # one-pass Longformer backward: from the saved statistics, and without them (the
+                # delta-mode forward, then the same pass); per-segment partials + combines
+                lo, llse, *ext.longformer_backward(q, k, v, g, 127, 0, 16, out=lo, lse=llse),
+                *ext.longformer_backward(q, k, v, g, 127, 0, 16)]
 
     eager = work()  # the first calls also reserve the kernels' dynamic LDS
     torch.cuda.synchronize()
