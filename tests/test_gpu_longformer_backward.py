@@ -9,7 +9,9 @@ sequence lengths around the 128-row tile (ragged last tiles, a single tile,
 fewer rows than global tokens), one and several tiles per workgroup,
 workgroup runs of tiles that cross a head's end, 12 seeded random geometries,
 and the full cfg4 shape (B=2 H=12 N=32768) on three heads against the oracle
-and on all heads against the tiled backward.  Tolerance: check_grad's 16-bit
+and on all heads against the tiled backward (fp16 without saved statistics:
+two heads against the oracle).  The oracle cases and the random geometries
+run both routes: from saved statistics and without them.  Tolerance: check_grad's 16-bit
 bound, per element |got - ref| <= 1e-2 + 1e-2 |ref|; against float64 from the
 same saved statistics, twice the worst case of the 16-bit roundings.
 """
@@ -314,3 +316,14 @@ def test_longformer_backward_without_statistics(ext, oracle, shape, L, G):
         ext.longformer_backward(*dev, L, 0, G)
     torch.cuda.synchronize()
     assert e0.elapsed_time(e1) > 0.0
+
+
+def test_longformer_backward_cfg4_shape_fp16_without_statistics(ext, oracle):
+    """cfg4's shape (B=2 H=12 N=32768, w=128, 16 globals) in fp16 without
+    saved statistics (the delta-mode forward, then the one-pass kernel):
+    heads 0 and 11 against the oracle, every element within check_grad's
+    16-bit bound."""
+    shape = (2, 32768, 12, 64)
+    dev, _, _, up = _case(ext, shape, 6350, torch.float16, 127, 16)
+    got = ext.longformer_backward(*dev, 127, 0, 16)
+    _check_heads(oracle, got, up, shape, 127, 16, (0, 11))

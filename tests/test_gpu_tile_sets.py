@@ -346,3 +346,29 @@ def test_saved_statistics_full_size(ext, workload):
         s = (ks[kk] @ qs[i]) * sl2
         total = float(torch.exp2(s - lse[0, i, 0]).sum())
         assert abs(total - 1.0) <= 1e-4, (i, total)
+
+
+def test_block_sparse_backward_cfg3_shape_vs_oracle(ext, oracle):
+    """cfg3 at full size (B=2 H=8 N=16384, block 64, diagonal + previous + 2
+    seeded blocks, bf16): the tiled backward over the table's key sets,
+    recomputing and from the forward's saved statistics, on heads 0 and 7
+    against the oracle's backward of those heads (heads are independent),
+    every element within check_grad's 16-bit bound."""
+    B, N, H, D = 2, 16384, 8, 64
+    q, k, v = qkv((B, N, H, D), 7100)
+    g = randn((B, N, H, D), 7101)
+    dev = [torch.from_numpy(a).bfloat16().cuda() for a in (q, k, v, g)]
+    up = [t.float().cpu().numpy() for t in dev]
+    host = ext.make_block_table(1234, N // 64, 2)
+    tab = ext.BlockTable(host, N, 64)
+    out, lse = ext.block_sparse_forward(dev[0], dev[1], dev[2], tab, 64, return_lse=True)
+    iset = ext.pattern_index_set("block_sparse", N, "cuda", block_table=tab, block_size=64)
+    routes = {"recomputed": ext.index_set_backward(*dev, iset),
+              "saved": ext.index_set_backward(*dev, iset, out=out, lse=lse)}
+    spec = oracle.Spec(B, N, 1, D, pattern="block_sparse", block_size=64, table=host.numpy())
+    for h in (0, H - 1):
+        ref = oracle.backward(spec, *(np.ascontiguousarray(a[:, :, h:h + 1]) for a in up))
+        for route, got in routes.items():
+            print(f"head {h}, {route}:", flush=True)
+            for name, a, r in zip(("dq", "dk", "dv"), got, ref):
+                check_grad(name, a[:, :, h:h + 1].float().cpu().numpy(), r, False)
