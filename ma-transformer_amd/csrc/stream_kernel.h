@@ -704,6 +704,12 @@ __device__ __forceinline__ float window_tile(const uint8_t* ring, uint32_t kl, u
 // masked so no key counts twice), and each wave folds one 16-key sub-tile of
 // every tile into an online softmax for the global query rows 0..G-1, written
 // as one partial per wave for longformer_combine.
+//
+// DM (with LG, delta mode: the first half of a Longformer backward without
+// saved statistics): also reads each tile's dO rows, sums p dP beside the
+// softmax (dP = dO V^T on the same MFMA form as the scores) and writes each
+// row's delta = sum_j P_ij dP_ij with its statistic instead of O.  Its own
+// instantiation, so the plain forward keeps its registers.
 template <class P, int NSLOT, int SG, int FL, int FR, bool LG, bool DM>
 __global__ __launch_bounds__(256, LG ? 2 : P::kMinBlocks) void stream_kernel(StreamArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];  // (NSLOT + LG) * P::kSlot bytes
