@@ -311,23 +311,27 @@ def test_target_causal_bf16(ext, oracle):
     _check_sampled(oracle, spec, up, y, torch.bfloat16, (3, 4), [(0, 65536)])
 
 
-def test_cfg3_block_sparse(ext, oracle):
-    """B=2 H=8 N=16384 D=64, block 64, diag + previous + 2 seeded blocks; inputs N(0,1)*0.5."""
-    (q, k, v), up = _inputs((2, 16384, 8, 64), 1237, torch.bfloat16, scale=0.5)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_cfg3_block_sparse(ext, oracle, dtype):
+    """B=2 H=8 N=16384 D=64, block 64, diag + previous + 2 seeded blocks; inputs N(0,1)*0.5
+    (BASELINE's bf16, and fp16 on the same kernel)."""
+    (q, k, v), up = _inputs((2, 16384, 8, 64), 1237, dtype, scale=0.5)
     table = ext.make_block_table(1234, 256, 2)
     y = ext.block_sparse_forward(q, k, v, table, 64)
     spec = oracle.Spec(2, 16384, 8, 64, pattern="block_sparse", block_size=64, table=table.numpy())
-    _check_sampled(oracle, spec, up, y, torch.bfloat16, (0, 2), [(0, 256), (8000, 8256), (16128, 16384)])
-    _check_sampled(oracle, spec, up, y, torch.bfloat16, (6, 7), [(0, 16384)])  # one whole head
+    _check_sampled(oracle, spec, up, y, dtype, (0, 2), [(0, 256), (8000, 8256), (16128, 16384)])
+    _check_sampled(oracle, spec, up, y, dtype, (6, 7), [(0, 16384)])  # one whole head
 
 
-def test_cfg4_longformer(ext, oracle):
-    """B=2 H=12 N=32768 D=64, causal w=128 plus 16 global tokens."""
-    (q, k, v), up = _inputs((2, 32768, 12, 64), 1238, torch.bfloat16)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_cfg4_longformer(ext, oracle, dtype):
+    """B=2 H=12 N=32768 D=64, causal w=128 plus 16 global tokens (BASELINE's bf16, and fp16
+    on the same kernel)."""
+    (q, k, v), up = _inputs((2, 32768, 12, 64), 1238, dtype)
     y = ext.longformer_forward(q, k, v, 127, 0, 16)
     spec = oracle.Spec(2, 32768, 12, 64, pattern="longformer", left=127, right=0, num_global=16)
-    _check_sampled(oracle, spec, up, y, torch.bfloat16, (0, 2), [(0, 300), (16000, 16100), (32700, 32768)])
-    _check_sampled(oracle, spec, up, y, torch.bfloat16, (9, 10), [(0, 32768)])  # one whole head, globals included
+    _check_sampled(oracle, spec, up, y, dtype, (0, 2), [(0, 300), (16000, 16100), (32700, 32768)])
+    _check_sampled(oracle, spec, up, y, dtype, (9, 10), [(0, 32768)])  # one whole head, globals included
 
 
 # ------------------------------------------------------- properties at full size
