@@ -235,7 +235,9 @@ class MACoreAttentionFunction(torch.autograd.Function):
     index sets, block-sparse and Longformer on the tiled index-set kernels
     (the latter two as their explicit key sets).  When those sets' tiles
     average more than two entries, the forward also keeps each row's softmax
-    statistic and the backward starts from it and the saved output.
+    statistic and the backward starts from it and the saved output; the
+    16-bit Longformer with a causal window of at most 128 keys and 1 to 16
+    global tokens then runs the one-pass kernel (longformer_backward).
 
     Reference: src/layers/ma_core_bridge.py:44-154.  The extra trailing
     argument ``spec`` (a PatternSpec or None) selects a non-reference pattern.

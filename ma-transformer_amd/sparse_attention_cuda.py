@@ -27,7 +27,9 @@ New pattern entry points (not in the reference; the benchmark patterns):
 
 Forward and backward are hand-written HIP kernels (libma_attn.so).  The
 backward recomputes the softmax from q, k, v as the reference's does, for the
-sliding and dense patterns, in the input dtype:
+sliding and dense patterns, in the input dtype (index sets, block-sparse and
+Longformer have backward entry points of their own: index_set_backward,
+longformer_backward):
 
     sliding_backward(q, k, v, grad_out, left, right, dilation=1) -> [dQ, dK, dV]
 """
