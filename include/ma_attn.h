@@ -362,10 +362,12 @@ int ma_attn_backward_copy_probe_timed(const ma_attn_desc* desc, const void* q, c
                                       void* dv, void* stream, void* start_event,
                                       void* stop_event);
 
-/* ABI version of this header (bumped on incompatible change). */
+/* ABI version of this header (bumped on incompatible change, and when an
+ * entry point takes descriptors it refused before: 10, ma_attn_backward on
+ * LONGFORMER). */
 int ma_attn_abi_version(void);
 
-#define MA_ATTN_ABI_VERSION 9
+#define MA_ATTN_ABI_VERSION 10
 
 #ifdef __cplusplus
 }

@@ -18,7 +18,7 @@ LIB_PATH = os.environ.get("MA_ATTN_LIB", os.path.join(_HERE, "libma_attn.so"))
 
 F32, BF16, F16 = 0, 1, 2
 SLIDING, DENSE, BLOCK_SPARSE, LONGFORMER, INDEX_SET = 0, 1, 2, 3, 4
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 
