@@ -1406,7 +1406,7 @@ constexpr int kMaxGlobal = 16;  // Longformer global tokens handled by the strea
 bool stream_applies(const ma_attn_desc* d, const void* q, const void* k, const void* v, const void* o) {
   StreamGeom g;
   if (!stream_geom(d, &g) || d->head_dim != kHeadDim || g.left < 0 || g.right < 0) return false;
-  if (g.G > 0 && (g.G > kMaxGlobal || d->dtype == MA_ATTN_F32)) return false;
+  if (g.G > kMaxGlobal) return false;
   if (!(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o))) return false;
   if (g.left > (1 << 20) || g.right > (1 << 20)) return false;
   const StreamPlan p = stream_plan(d);
@@ -1470,6 +1470,19 @@ int launch_stream_half(const ma_attn_desc* d, const StreamArgs& a, const StreamP
   return 0;
 }
 
+// fp32: the sliding windows, and Longformer (no delta mode: the one-pass
+// backward is 16-bit) with its combine.
+int launch_stream_f32(const ma_attn_desc* d, const StreamArgs& a, const StreamPlan& p, hipStream_t st) {
+  if (p.geom.G == 0) return launch_stream_any<F32Path, false, false>(a, p.slots, p.wgs, st);
+  if (a.delta) return fail("ma_attn: the Longformer delta-mode forward is 16-bit only");
+  const int rc = launch_stream_any<F32Path, true, false>(a, p.slots, p.wgs, st);
+  if (rc) return rc;
+  launch(true, longformer_combine<float>, dim3((unsigned)(d->batch * d->num_heads * p.geom.G)), dim3(256), 0, st,
+         a.partials, static_cast<float*>(a.o), (int)p.chunks, (int)p.geom.G, (int)d->num_heads, d->seq_len,
+         a.lse, a.delta);
+  return 0;
+}
+
 // dout, delta (Longformer only): delta mode, each row's
 // delta = sum_j P_ij dP_ij (dP_ij = dO_i . V_j, fp32) into delta alongside
 // lse, and O not written.
@@ -1508,7 +1521,7 @@ int launch_stream(const ma_attn_desc* d, const void* q, const void* k, const voi
   switch (d->dtype) {
     case MA_ATTN_BF16: return launch_stream_half<__bf16>(d, a, p, st);
     case MA_ATTN_F16: return launch_stream_half<_Float16>(d, a, p, st);
-    default: return launch_stream_any<F32Path, false, false>(a, p.slots, p.wgs, st);
+    default: return launch_stream_f32(d, a, p, st);
   }
 }
 
@@ -2072,7 +2085,7 @@ size_t ma_attn_workspace_size(const ma_attn_desc* desc) {
   static const char dummy[16] __attribute__((aligned(16))) = {0};
   const void* const ptrs[4] = {dummy, dummy, dummy, dummy};
   if (tiles_apply(desc, ptrs, 4)) return (size_t)tiles_fwd_part_bytes(desc);
-  if (desc->pattern != MA_ATTN_LONGFORMER || desc->dtype == MA_ATTN_F32) return 0;
+  if (desc->pattern != MA_ATTN_LONGFORMER) return 0;
   if (!stream_applies(desc, dummy, dummy, dummy, dummy)) return 0;
   return (size_t)stream_plan(desc).partial_bytes;
 }
@@ -2138,7 +2151,7 @@ int forward_launch(const ma_attn_desc* desc, const void* q, const void* k, const
   const bool stream = !want_rows && !want_band && stream_applies(desc, q, k, v, o);
   const bool block = !stream && !want_rows && block_applies(desc, q, k, v, o);
   if (lse && !block && !tiles_apply(desc, qkvo, 4) &&
-      !(stream && desc->pattern == MA_ATTN_LONGFORMER && desc->num_global > 0))
+      !(stream && desc->pattern == MA_ATTN_LONGFORMER && desc->num_global > 0 && desc->dtype != MA_ATTN_F32))
     return fail("ma_attn_forward_lse: these kernels write no statistics (block-sparse, dense, Longformer in "
                 "16 bits and index sets with a tile plan do, at head_dim 64)");
   if (stream) {

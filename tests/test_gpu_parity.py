@@ -171,7 +171,7 @@ def test_block_sparse_geometry(ext, oracle, N, dtype):
     (16, 16, 127, 0), (17, 16, 127, 0), (100, 5, 127, 0), (300, 16, 127, 0), (1000, 16, 127, 0),
     (257, 1, 3, 0), (300, 7, 20, 9), (130, 16, 200, 0), (500, 3, 64, 64), (10, 4, 2, 1),
 ])
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_longformer_geometry(ext, oracle, N, G, left, right, dtype):
     shape = (2, N, 3, 64)
     (q, k, v), up = _inputs(shape, 900 + N + G, dtype)
@@ -183,6 +183,7 @@ def test_longformer_geometry(ext, oracle, N, G, left, right, dtype):
 @pytest.mark.parametrize("shape,G,left,dtype", [
     ((1, 8192, 1, 64), 16, 127, torch.bfloat16),  # one stream: 128 chunks of one tile
     ((1, 3000, 2, 64), 5, 40, torch.float16),     # 47 chunks: a second batch of 15
+    ((1, 8192, 2, 64), 16, 127, torch.float32),   # fp32 (one workgroup per CU): 128 chunks of one tile
 ])
 def test_longformer_many_chunks(ext, oracle, shape, G, left, dtype):
     """Few (batch, head) streams over a long sequence: the grid splits each
@@ -323,10 +324,10 @@ def test_cfg3_block_sparse(ext, oracle, dtype):
     _check_sampled(oracle, spec, up, y, dtype, (6, 7), [(0, 16384)])  # one whole head
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_cfg4_longformer(ext, oracle, dtype):
-    """B=2 H=12 N=32768 D=64, causal w=128 plus 16 global tokens (BASELINE's bf16, and fp16
-    on the same kernel)."""
+    """B=2 H=12 N=32768 D=64, causal w=128 plus 16 global tokens (BASELINE's bf16, fp16 on
+    the same kernel, and fp32 on its fp32 instantiation at 1e-5)."""
     (q, k, v), up = _inputs((2, 32768, 12, 64), 1238, dtype)
     y = ext.longformer_forward(q, k, v, 127, 0, 16)
     spec = oracle.Spec(2, 32768, 12, 64, pattern="longformer", left=127, right=0, num_global=16)

@@ -195,7 +195,8 @@ def test_saved_statistics_patterns(ext, oracle, pattern, N, dtype):
     shape = (2, N, 2, 64)
     dev, up = _inputs(shape, 9600 + N, dtype)
     if pattern == "longformer" and dtype == torch.float32:
-        # fp32 Longformer runs on the row kernels, which write no statistics: refused before any launch
+        # no statistics from the fp32 Longformer forward (the one-pass backward that takes them is
+        # 16-bit): refused before any launch
         with pytest.raises(RuntimeError, match="statistics"):
             ext.longformer_forward(*dev[:3], 127, 0, 16, return_lse=True)
         return
