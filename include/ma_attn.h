@@ -207,8 +207,9 @@ int ma_attn_backward_timed(const ma_attn_desc* desc, const void* q, const void* 
  * writes lse[(b*N + i)*H + h] (float32, B*N*H entries): log2 of row i's
  * softmax denominator sum_j 2^(scale*log2(e)*q_i.k_j) (0 for a row with no
  * key).  Taken by the kernels that produce it at head_dim 64: BLOCK_SPARSE
- * (block size 64) and DENSE on the block-row kernel, LONGFORMER in 16 bits,
- * INDEX_SET with a tile plan; otherwise non-zero with an error.
+ * (block size 64) and DENSE on the block-row kernel, LONGFORMER with 1 to
+ * 16 global tokens on the stream kernel (any dtype), INDEX_SET with a tile
+ * plan; otherwise non-zero with an error.
  *
  * ma_attn_backward_saved: the gradients of ma_attn_backward from the
  * forward's o and lse (delta_i = dout_i . o_i), for an INDEX_SET with a tile

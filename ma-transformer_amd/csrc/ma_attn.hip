@@ -2139,8 +2139,8 @@ int ma_attn_forward_noalloc(const ma_attn_desc* desc, const void* q, const void*
 namespace {
 
 // lse: optional per-row softmax statistics (ma_attn_forward_lse), written by
-// the block-row, tiled and 16-bit Longformer stream kernels; other kernels
-// refuse it.
+// the block-row, tiled and Longformer stream kernels; other kernels refuse
+// it.
 int forward_launch(const ma_attn_desc* desc, const void* q, const void* k, const void* v, void* o, float* lse,
                    void* workspace, size_t workspace_bytes, hipStream_t st) {
   (void)hipGetLastError();  // launch errors below must be ours
@@ -2151,9 +2151,9 @@ int forward_launch(const ma_attn_desc* desc, const void* q, const void* k, const
   const bool stream = !want_rows && !want_band && stream_applies(desc, q, k, v, o);
   const bool block = !stream && !want_rows && block_applies(desc, q, k, v, o);
   if (lse && !block && !tiles_apply(desc, qkvo, 4) &&
-      !(stream && desc->pattern == MA_ATTN_LONGFORMER && desc->num_global > 0 && desc->dtype != MA_ATTN_F32))
-    return fail("ma_attn_forward_lse: these kernels write no statistics (block-sparse, dense, Longformer in "
-                "16 bits and index sets with a tile plan do, at head_dim 64)");
+      !(stream && desc->pattern == MA_ATTN_LONGFORMER && desc->num_global > 0))
+    return fail("ma_attn_forward_lse: these kernels write no statistics (block-sparse, dense, Longformer "
+                "with 1 to 16 global tokens and index sets with a tile plan do, at head_dim 64)");
   if (stream) {
     rc = launch_stream(desc, q, k, v, o, lse, workspace, workspace_bytes, st);
   } else if (block) {

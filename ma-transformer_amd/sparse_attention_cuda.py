@@ -277,7 +277,7 @@ def block_sparse_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Te
 def longformer_forward(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                        left: int, right: int = 0, num_global: int = 16, return_lse: bool = False):
     """Rows i < G attend all keys; others attend [i-left, i+right] U [0, G).
-    return_lse as for block_sparse_forward (bf16/fp16, 1 <= G <= 16)."""
+    return_lse as for block_sparse_forward (1 <= G <= 16, head_dim 64)."""
     return _launch(query, key, value, _ma.LONGFORMER, return_lse, left=int(left), right=int(right),
                    num_global=int(num_global))
 

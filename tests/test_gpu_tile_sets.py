@@ -194,12 +194,6 @@ def test_saved_statistics_patterns(ext, oracle, pattern, N, dtype):
     import ma_attn
     shape = (2, N, 2, 64)
     dev, up = _inputs(shape, 9600 + N, dtype)
-    if pattern == "longformer" and dtype == torch.float32:
-        # no statistics from the fp32 Longformer forward (the one-pass backward that takes them is
-        # 16-bit): refused before any launch
-        with pytest.raises(RuntimeError, match="statistics"):
-            ext.longformer_forward(*dev[:3], 127, 0, 16, return_lse=True)
-        return
     if pattern == "block_sparse":
         nb = (N + 63) // 64
         tab = ext.make_block_table(5, nb, 2)
@@ -245,10 +239,9 @@ def test_saved_statistics_rejected(ext):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_layer_trains_from_saved_statistics(ext, oracle, pattern, dtype, monkeypatch):
     """MACoreAttention training on the device (fallback_training=False) keeps
-    the forward's statistics and runs the backward from them where the
-    forward's kernel writes them (fp32 Longformer's does not: that case
-    recomputes them; 16-bit Longformer runs the one-pass longformer_backward);
-    gradients match the oracle's either way."""
+    the forward's statistics and runs the backward from them (16-bit
+    Longformer on the one-pass longformer_backward, fp32 Longformer on the
+    tiled index-set kernels); gradients match the oracle's."""
     from layers.ma_core_bridge import MACoreAttention
     N = 1536
     shape = (2, N, 2, 64)
@@ -281,7 +274,7 @@ def test_layer_trains_from_saved_statistics(ext, oracle, pattern, dtype, monkeyp
     monkeypatch.setattr(ext, fn, spy)
     q, k, v = (t.clone().requires_grad_(True) for t in dev[:3])
     layer(q, k, v).backward(dev[3])
-    assert calls == [not (pattern == "longformer" and dtype == torch.float32)]
+    assert calls == [True]
     for name, t, ref in zip("qkv", (q, k, v), oracle.backward(spec, *up)):
         check_grad("d" + name, t.grad.float().cpu().numpy(), ref, dtype == torch.float32)
 
